@@ -1,0 +1,236 @@
+/*
+ * q35.h — C ABI of the MI355X (gfx950) decode hot path for the Qwen3.5-2B-shaped hybrid
+ * decoder (Gated DeltaNet + gated GQA attention, Q8F weights).
+ *
+ * Every entry point replaces one function of the reference engine (inventwithdean/Qwen-3.5);
+ * the citation beside each declaration names the file:line it replaces.  The reference reaches
+ * these through `#[backend_extension(Cube, Fusion)] trait CustomKernels` (src/kernels.rs:373-433)
+ * and the `seq_len == 1` branches of src/text_modules.rs; here they are plain C functions.
+ *
+ * Conventions
+ *   - All tensor arguments are DEVICE pointers (hipMalloc'd) unless the name ends in `_host`.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Calls are
+ *     stream-ordered and asynchronous; no entry point synchronises the device.
+ *   - The caller owns every buffer.  Entry points that need scratch take `ws`/`ws_bytes`; the
+ *     required size comes from the matching *_ws_bytes() query.  A workspace must be zero-filled
+ *     once before its first use; every call leaves it zero-filled again on completion, so it can
+ *     be reused by later calls on the same stream (calls running concurrently need distinct
+ *     workspaces).
+ *   - Return value: Q35_OK or a Q35_E_* code; q35_last_error() gives a message.  Nothing aborts.
+ *   - Q8F: int8 two's complement values plus one f32 scale per block of 64 consecutive elements
+ *     along the stored matrix's contiguous axis; dequant = f32(q) * scale (kernels.rs:34-43,84-88).
+ */
+#ifndef Q35_H
+#define Q35_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  Q35_OK = 0,
+  Q35_E_SHAPE = 1,   /* a dimension violates the kernel contract (multiple of 64, limits) */
+  Q35_E_ALIGN = 2,   /* a pointer is not 16-byte aligned */
+  Q35_E_HIP = 3,     /* a HIP runtime call failed */
+  Q35_E_ARG = 4,     /* NULL pointer or invalid enum */
+  Q35_E_WS = 5,      /* workspace smaller than the *_ws_bytes() requirement */
+  Q35_E_NOMEM = 6,   /* device or host allocation failed (model creation only) */
+};
+
+/* Storage layouts of a Q8F matrix.
+ *   Q35_KN: q is [rows=K(in)][cols=N(out)], scale is [K][N/64]  — Burn Linear weight of the
+ *           reference projections, blocks along N (kernels.rs:56-57,75-76,87).
+ *   Q35_NK: q is [rows=N(out)][cols=K(in)], scale is [N][K/64]  — the tied embedding table
+ *           used as lm_head, blocks along K (kernels.rs:253-255,283). */
+enum { Q35_KN = 0, Q35_NK = 1 };
+
+typedef struct {
+  const int8_t* q;
+  const float* scale;
+  int32_t rows;
+  int32_t cols;
+  int32_t layout; /* Q35_KN or Q35_NK */
+} q35_q8f;
+
+/* Shape constants of the decoder; mirrors the fields of TextConfig that the decode path
+ * reads (src/text_config.rs:56-126).  q35_dims_qwen35_2b() returns the 2B values. */
+typedef struct {
+  int32_t hidden, ffn, vocab, n_layers, full_interval;
+  int32_t lin_heads, lin_dk, lin_dv, conv_k;
+  int32_t attn_heads, kv_heads, head_dim, rot_dim;
+  float eps, theta;
+} q35_dims;
+
+const char* q35_last_error(void);
+q35_dims q35_dims_qwen35_2b(void);
+
+/* ---------------------------------------------------------------- tensor level (kernels.rs) */
+
+/* y[M][N] = x[M][K] @ dequant(W).  W.layout selects KN (reference projections) or NK.
+ * Full-K semantics (every input row is summed).  M in [1, 64]; K, N multiples of 64.
+ * Replaces q8_gemv (src/kernels.rs:681-688, kernel :53-92). */
+int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream);
+
+/* Same contract; replaces q8_gemv_partial_sum (src/kernels.rs:690-700, impl :495-537, kernels
+ * :103-165) whose split-K reduction is done here deterministically inside one launch. */
+int q35_q8_gemv_partial_sum(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream);
+size_t q35_q8_gemv_ws_bytes(int32_t M, q35_q8f W);
+
+/* logits[M][V] = h[M][D] @ dequant(E)^T with E the NK [V][D] embedding table.
+ * Replaces q8_lm_head (src/kernels.rs:724-731, kernel :251-291). */
+int q35_q8_lm_head(const float* h, int32_t M, q35_q8f E, float* logits, void* stream);
+
+/* out[n][D] = dequant(table[ids[i]]).  Replaces q8_embedding_lookup (src/kernels.rs:669-679,
+ * kernel :15-45).  ids must lie in [0, V). */
+int q35_q8_embedding_lookup(q35_q8f table, const int32_t* ids, int32_t n, float* out, void* stream);
+
+/* out[b] = [beta(n_heads) | g(n_heads)] with beta = sigmoid(x.W_b), g = -exp(A_log) *
+ * softplus(x.W_a + dt_bias) (softplus branch x when ln(1+e^x) > 20).  x [B][in_dim];
+ * W_b, W_a f32 [in_dim][n_heads].  Replaces gate_proj (src/kernels.rs:702-722, kernel :174-247). */
+int q35_gate_proj(const float* x, int32_t B, int32_t in_dim, const float* w_b, const float* w_a,
+                  const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream);
+
+/* out[0] = index of the largest logit (ties: lowest index).  Replaces argmax
+ * (src/kernels.rs:733-739, kernels :298-371). */
+int q35_argmax(const float* logits, int64_t n, int32_t* out, void* ws, size_t ws_bytes, void* stream);
+size_t q35_argmax_ws_bytes(int64_t n);
+
+/* ---------------------------------------------------------------- layer level (text_modules.rs) */
+
+typedef struct {
+  q35_q8f in_proj_qkv; /* KN [hidden][2*key_dim+value_dim] */
+  q35_q8f in_proj_z;   /* KN [hidden][value_dim] */
+  q35_q8f out_proj;    /* KN [value_dim][hidden] */
+  const float* in_proj_b; /* f32 [hidden][lin_heads] */
+  const float* in_proj_a; /* f32 [hidden][lin_heads] */
+  const float* a_log;     /* [lin_heads] */
+  const float* dt_bias;   /* [lin_heads] */
+  const float* conv_w;    /* [conv_dim][conv_k] */
+  const float* norm_w;    /* [lin_dv] */
+} q35_gdn_weights;
+
+typedef struct {
+  q35_q8f q_proj; /* KN [hidden][attn_heads*head_dim*2], per head [query | gate] */
+  q35_q8f k_proj; /* KN [hidden][kv_heads*head_dim] */
+  q35_q8f v_proj; /* KN [hidden][kv_heads*head_dim] */
+  q35_q8f o_proj; /* KN [attn_heads*head_dim][hidden] */
+  const float* q_norm; /* [head_dim], applied as (1 + w) */
+  const float* k_norm; /* [head_dim] */
+} q35_attn_weights;
+
+typedef struct {
+  q35_q8f gate_proj, up_proj, down_proj; /* KN */
+} q35_mlp_weights;
+
+/* One decode token through GatedDeltaNet for B rows.  x: [B][hidden] (already input-normed);
+ * conv_state: [B][conv_dim][conv_k-1]; rec_state: [B][lin_heads][lin_dk][lin_dv] (both updated
+ * in place); out: [B][hidden].  Replaces GatedDeltaNet::forward's seq_len==1 branch with cached
+ * states (src/text_modules.rs:484-667). */
+int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const float* x, int32_t B,
+                              float* conv_state, float* rec_state, float* out,
+                              void* ws, size_t ws_bytes, void* stream);
+
+/* One decode token through gated GQA attention for B rows.  k_cache/v_cache:
+ * [B][kv_heads][tmax][head_dim]; d_pos[b] = tokens already cached for row b (the new K/V are
+ * written at that index, then attention runs over d_pos[b]+1 tokens); rope_cos/rope_sin:
+ * [tmax][rot_dim] from q35_rope_tables.  Replaces Attention::forward's seq_len==1 branch
+ * (src/text_modules.rs:842-944). */
+int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const float* x, int32_t B,
+                         float* k_cache, float* v_cache, int32_t tmax, const int32_t* d_pos,
+                         const float* rope_cos, const float* rope_sin, float* out,
+                         void* ws, size_t ws_bytes, void* stream);
+
+/* down(up(x) * silu(gate(x))) for B rows.  Replaces MLP::forward (src/text_modules.rs:1000-1011). */
+int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, int32_t B, float* out,
+                   void* ws, size_t ws_bytes, void* stream);
+
+/* The recurrent core of GatedDeltaNet for one token, B rows: causal conv update + SiLU on the
+ * mixed q|k|v channels, l2norm(q)*dk^-1/2, l2norm(k), S = e^g S; S += k (x) (v - S^T k) beta;
+ * out = S^T q.  mixed_qkv: [B][2*key_dim+value_dim] (pre-conv projection output); beta_g:
+ * [B][2*lin_heads] = [beta | g] as q35_gate_proj produces; conv_state [B][conv_dim][3] and
+ * rec_state [B][lin_heads][128][lin_dv] updated in place; core_out: [B][lin_heads*lin_dv] (before
+ * the gated norm).  Replaces causal_conv1d_update + burn_recurrent_gated_delta_rule
+ * (src/text_modules.rs:134-162, :365-443) as called at :515-530, :627-652. */
+int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* beta_g, float* conv_state,
+                                const float* conv_w, float* rec_state, float* core_out, int32_t lin_heads,
+                                int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes, void* stream);
+
+/* The attention core for one token, B rows: q_norm/k_norm (1+w), RoPE, K/V append at d_pos[b],
+ * softmax(q K^T/sqrt(256)) V with GQA, times sigmoid(gate).  q_gate: [B][attn_heads*2*head_dim]
+ * (q_proj output, per head [query | gate]); k_new, v_new: [B][kv_heads*head_dim] (k_proj / v_proj
+ * outputs, ld = kv_ld floats between rows); out: [B][attn_heads*head_dim].  Replaces the part of
+ * Attention::forward between the projections (src/text_modules.rs:860-936). */
+int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const float* k_new, const float* v_new,
+                              int32_t kv_ld, int32_t B, const float* q_norm, const float* k_norm, float* k_cache,
+                              float* v_cache, int32_t tmax, const int32_t* d_pos, const float* rope_cos,
+                              const float* rope_sin, float* out, void* ws, size_t ws_bytes, void* stream);
+
+/* Workspace large enough for any of the layer calls above with these B / tmax. */
+size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax);
+
+/* Host: cos/sin tables [tmax][rot_dim] of TextRotaryEmbedding::forward for positions 0..tmax-1
+ * (src/text_modules.rs:30-43,73-81; the mRoPE recomposition :45-58 is the identity for text). */
+int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin_host);
+
+/* ---------------------------------------------------------------- model level (model.rs, main.rs) */
+
+typedef struct q35_model q35_model;
+
+/* Builds the decoder with seeded random-init weights, the reference's init rules
+ * (LinearConfig::init / EmbeddingConfig::init drawn N(0, 0.02) here, RMSNorm w=0, gated-norm
+ * w=1, dt_bias=1, A_log=ln U(0.01,16), text_modules.rs:698-700,820,111) and Q8F quantisation of
+ * the tensors main.rs:159-222 quantises.  Allocates weights, caches for tmax tokens and the step
+ * workspace.  Replaces TextForCausalLMConfig::init + load_file (main.rs:29-37). */
+int q35_model_create_synthetic(const q35_dims* d, uint64_t seed, int32_t tmax, q35_model** out);
+int q35_model_destroy(q35_model* m);
+
+/* Zero every cache and set the position to 0 (the chat loop's /reset, main.rs:65-71). */
+int q35_model_reset(q35_model* m, void* stream);
+
+/* Write the next input token (host value) into the model's device token slot. */
+int q35_model_set_token(q35_model* m, int32_t token, void* stream);
+
+/* One decode step: reads the device token slot, runs embedding -> layers -> norm -> lm_head ->
+ * argmax, writes the argmax back into the token slot and advances the device position.
+ * Replaces TextForCausalLM::forward (model.rs:113-129) + kernels::argmax (main.rs:131).
+ * use_graph=1 replays a hipGraph captured on first use on this stream. */
+int q35_model_step(q35_model* m, int32_t use_graph, void* stream);
+
+/* Greedy generation (main.rs:100-132 without tokenizer or stop tokens): feeds the n_prompt
+ * prompt ids one decode step at a time, then runs n_new decode steps.  out_tokens_host receives
+ * n_new+1 ids: the argmax after the last prompt token, then the argmax after each decode step.
+ * readback_each=1 copies each token to the host and synchronises per step as main.rs:107
+ * does.  decode_seconds_host (optional) receives the wall time of the n_new decode steps. */
+int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t n_new,
+                       int32_t* out_tokens_host, int32_t use_graph, int32_t readback_each,
+                       double* decode_seconds_host, void* stream);
+
+/* Device pointer and byte size of a named model tensor, named as the reference's module
+ * paths: "embed_tokens", "norm", "layers.{i}.input_layernorm", "layers.{i}.linear_attn.in_proj_qkv"
+ * (".q" / ".scale" suffix for the Q8F parts), "...conv_state", "...recurrent_state",
+ * "layers.{i}.self_attn.k_cache", "logits", "token", "pos", ...  Used by tests and tools. */
+int q35_model_tensor(q35_model* m, const char* name, void** dptr, size_t* bytes);
+
+/* ---------------------------------------------------------------- host utilities */
+
+/* Seeded N(0, sigma) f32 values: counter-based splitmix64 + Box-Muller in double; element i of
+ * stream `stream` is independent of how the range is split, so any slice can be regenerated. */
+int q35_synth_normal(uint64_t seed, uint64_t stream, int64_t offset, int64_t n, float sigma, float* out_host);
+/* Seeded U(lo, hi) f32 values from the same generator. */
+int q35_synth_uniform(uint64_t seed, uint64_t stream, int64_t offset, int64_t n, float lo, float hi, float* out_host);
+/* Stream id the model builder uses for a named tensor (FNV-1a of the name). */
+uint64_t q35_synth_stream_id(const char* name);
+/* Q8F quantiser, blocks of 64 along cols: scale = max|w|/127 (f32), q = round-half-away(w/scale)
+ * clamped to [-127,127]; all-zero block -> scale 0.  Replaces the Quantizer of main.rs:175-179. */
+int q35_quantize_q8f(const float* w_host, int64_t rows, int64_t cols, int8_t* q_host, float* scale_host);
+/* Host copy of the f32 values the model builder draws for a named tensor (before
+ * quantisation), so a host-side checker can rebuild the same model. */
+int q35_synth_model_tensor(const q35_dims* d, uint64_t seed, const char* name, float* out_host, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q35_H */

@@ -1,0 +1,387 @@
+// extern "C" entry points for the tensor-level (kernels.rs) and layer-level (text_modules.rs)
+// surface.  Argument checking lives here; kernels assume validated shapes.
+#include "q35_host.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace q35 {
+
+namespace {
+thread_local std::string g_err;
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+int check_q8f(const q35_q8f& W, const char* what) {
+  if (!W.q || !W.scale) return fail(Q35_E_ARG, std::string(what) + ": null Q8F pointer");
+  if (W.rows < 1 || W.cols < 64 || (W.cols % 64) != 0)
+    return fail(Q35_E_SHAPE, std::string(what) + ": Q8F cols must be a positive multiple of 64");
+  if (W.layout != Q35_KN && W.layout != Q35_NK) return fail(Q35_E_ARG, std::string(what) + ": bad layout");
+  if ((reinterpret_cast<uintptr_t>(W.q) & 15) != 0) return fail(Q35_E_ALIGN, std::string(what) + ": q not 16-byte aligned");
+  return Q35_OK;
+}
+
+// NK rows of x handled per launch: LDS holds MR*K floats.
+int nk_group(int K) {
+  int g = 8;
+  while (g > 1 && g * K > 12288) g /= 2;
+  return g;
+}
+
+MvSeg seg_of(const q35_q8f& W, float* y, int ldy) { return MvSeg{W.q, W.scale, y, W.cols, ldy}; }
+
+// Bump allocator over the caller's layer workspace (after the kernel scratch).
+struct Carver {
+  char* p;
+  size_t left;
+  float* f(size_t n) {
+    const size_t b = align256(n * sizeof(float));
+    if (b > left) return nullptr;
+    float* r = reinterpret_cast<float*>(p);
+    p += b; left -= b;
+    return r;
+  }
+};
+
+struct LayerDims {
+  int H, F, nh, dk, dv, key_dim, vdim, conv_dim, ah, kvh, hd;
+};
+LayerDims ldims(const q35_dims& d) {
+  LayerDims L;
+  L.H = d.hidden; L.F = d.ffn; L.nh = d.lin_heads; L.dk = d.lin_dk; L.dv = d.lin_dv;
+  L.key_dim = L.nh * L.dk; L.vdim = L.nh * L.dv; L.conv_dim = 2 * L.key_dim + L.vdim;
+  L.ah = d.attn_heads; L.kvh = d.kv_heads; L.hd = d.head_dim;
+  return L;
+}
+
+size_t layer_scratch_bytes(const q35_dims& d, int B, int tmax) {
+  const LayerDims L = ldims(d);
+  const int M = std::min(B, 8);
+  size_t m = gdn_step_ws_bytes(B, L.nh);
+  auto mv = [&](int K, std::initializer_list<int> Ns, int aux) {
+    MvCall c;
+    c.K = K; c.M = M; c.nseg = 0;
+    for (int N : Ns) { c.seg[c.nseg].N = N; ++c.nseg; }
+    c.aux_nh = aux;
+    m = std::max(m, mv_kn_ws_bytes(c));
+  };
+  mv(L.H, {L.conv_dim, L.vdim}, L.nh);
+  mv(L.vdim, {L.H}, 0);
+  mv(L.H, {L.ah * L.hd * 2, L.kvh * L.hd, L.kvh * L.hd}, 0);
+  mv(L.ah * L.hd, {L.H}, 0);
+  mv(L.H, {L.F, L.F}, 0);
+  mv(L.F, {L.H}, 0);
+  m = std::max(m, attn_ws_bytes(B, L.ah, L.kvh, L.hd, tmax));
+  return align256(m);
+}
+
+size_t layer_act_floats(const q35_dims& d, int B) {
+  const LayerDims L = ldims(d);
+  size_t gdn = (size_t)B * (L.conv_dim + L.vdim) + 256 + (size_t)B * 2 * L.nh + 256 + (size_t)B * L.vdim + 256;
+  size_t att = (size_t)B * L.ah * L.hd * 2 + 256 + (size_t)B * 2 * L.kvh * L.hd + 256 + (size_t)B * L.ah * L.hd + 256;
+  size_t mlp = (size_t)B * 2 * L.F + 256;
+  return std::max(gdn, std::max(att, mlp)) + 1024;
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { g_err = msg; }
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int validate_dims(const q35_dims& d) {
+  if (d.hidden < 64 || d.hidden % 64 || d.ffn < 64 || d.ffn % 64 || d.vocab < 1 || d.n_layers < 1 || d.full_interval < 1)
+    return fail(Q35_E_SHAPE, "dims: hidden/ffn must be multiples of 64, vocab/n_layers/full_interval >= 1");
+  if (d.lin_dk != 128 || d.lin_dv % 32 || d.conv_k != 4 || d.lin_heads < 1 || (256 % (2 * d.lin_heads)) != 0)
+    return fail(Q35_E_SHAPE, "dims: linear heads need dk=128, dv%32==0, conv_k=4, 2*heads | 256");
+  if (d.head_dim != 256 || d.kv_heads < 1 || d.attn_heads % d.kv_heads || d.attn_heads / d.kv_heads > 4 ||
+      d.rot_dim < 2 || d.rot_dim > d.head_dim || d.rot_dim % 2)
+    return fail(Q35_E_SHAPE, "dims: attention needs head_dim=256, heads/kv_heads in 1..4, even rot_dim");
+  if ((d.lin_heads * d.lin_dv) % 64 || (d.attn_heads * d.head_dim) % 64) return fail(Q35_E_SHAPE, "dims: widths % 64");
+  return Q35_OK;
+}
+
+}  // namespace q35
+
+using namespace q35;
+
+extern "C" {
+
+const char* q35_last_error(void) { return g_err.c_str(); }
+
+q35_dims q35_dims_qwen35_2b(void) {
+  q35_dims d;
+  d.hidden = 2048; d.ffn = 6144; d.vocab = 248320; d.n_layers = 24; d.full_interval = 4;
+  d.lin_heads = 16; d.lin_dk = 128; d.lin_dv = 128; d.conv_k = 4;
+  d.attn_heads = 8; d.kv_heads = 2; d.head_dim = 256; d.rot_dim = 64;
+  d.eps = 1e-6f; d.theta = 1e7f;
+  return d;
+}
+
+size_t q35_q8_gemv_ws_bytes(int32_t M, q35_q8f W) {
+  if (W.layout == Q35_NK) return kCounterBytes;
+  MvCall c;
+  c.K = W.rows; c.M = std::max(1, std::min<int>(M, 8)); c.nseg = 1;
+  c.seg[0].N = W.cols;
+  return mv_kn_ws_bytes(c);
+}
+
+int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_q8f(W, "q8_gemv");
+  if (rc) return rc;
+  if (!x || !y) return fail(Q35_E_ARG, "q8_gemv: null x or y");
+  if (M < 1 || M > 64) return fail(Q35_E_SHAPE, "q8_gemv: M must be in [1, 64]");
+  if (W.layout == Q35_KN) {
+    const int K = W.rows, N = W.cols;
+    for (int m0 = 0; m0 < M; m0 += 8) {
+      MvCall c;
+      c.K = K; c.M = std::min(8, M - m0); c.nseg = 1;
+      c.seg[0] = seg_of(W, y + (size_t)m0 * N, N);
+      c.pro = PRO_PLAIN; c.x = x + (size_t)m0 * K; c.ldx = K;
+      rc = mv_kn_launch(c, ws, ws_bytes, S(stream));
+      if (rc) return rc;
+    }
+    return Q35_OK;
+  }
+  const int N = W.rows, K = W.cols;
+  const int g = nk_group(K);
+  for (int m0 = 0; m0 < M; m0 += g) {
+    NkCall c;
+    c.q = W.q; c.s = W.scale; c.N = N; c.K = K; c.M = std::min(g, M - m0);
+    c.x = x + (size_t)m0 * K; c.ldx = K; c.y = y + (size_t)m0 * N; c.ldy = N;
+    rc = nk_launch(c, ws, ws_bytes, S(stream));
+    if (rc) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_q8_gemv_partial_sum(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream) {
+  return q35_q8_gemv(x, M, W, y, ws, ws_bytes, stream);
+}
+
+int q35_q8_lm_head(const float* h, int32_t M, q35_q8f E, float* logits, void* stream) {
+  int rc = check_q8f(E, "q8_lm_head");
+  if (rc) return rc;
+  if (E.layout != Q35_NK) return fail(Q35_E_ARG, "q8_lm_head: embedding table must be Q35_NK");
+  if (!h || !logits) return fail(Q35_E_ARG, "q8_lm_head: null pointer");
+  if (M < 1 || M > 64) return fail(Q35_E_SHAPE, "q8_lm_head: M must be in [1, 64]");
+  const int N = E.rows, K = E.cols;
+  const int g = nk_group(K);
+  for (int m0 = 0; m0 < M; m0 += g) {
+    NkCall c;
+    c.q = E.q; c.s = E.scale; c.N = N; c.K = K; c.M = std::min(g, M - m0);
+    c.x = h + (size_t)m0 * K; c.ldx = K; c.y = logits + (size_t)m0 * N; c.ldy = N;
+    rc = nk_launch(c, nullptr, 0, S(stream));
+    if (rc) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_q8_embedding_lookup(q35_q8f table, const int32_t* ids, int32_t n, float* out, void* stream) {
+  int rc = check_q8f(table, "q8_embedding_lookup");
+  if (rc) return rc;
+  if (table.layout != Q35_NK) return fail(Q35_E_ARG, "q8_embedding_lookup: table must be Q35_NK ([V][D])");
+  return embed_launch(table.q, table.scale, table.rows, table.cols, ids, n, out, S(stream));
+}
+
+int q35_gate_proj(const float* x, int32_t B, int32_t in_dim, const float* w_b, const float* w_a,
+                  const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream) {
+  return gate_proj_simple_launch(x, B, in_dim, w_b, w_a, a_log, dt_bias, n_heads, out, S(stream));
+}
+
+size_t q35_argmax_ws_bytes(int64_t n) { return argmax_ws_bytes(n); }
+
+int q35_argmax(const float* logits, int64_t n, int32_t* out, void* ws, size_t ws_bytes, void* stream) {
+  return argmax_launch(logits, n, out, ws, ws_bytes, S(stream));
+}
+
+size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax) {
+  if (!d || B < 1) return 0;
+  return layer_scratch_bytes(*d, B, std::max(1, tmax)) + layer_act_floats(*d, B) * sizeof(float);
+}
+
+int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const float* x, int32_t B,
+                              float* conv_state, float* rec_state, float* out, void* ws, size_t ws_bytes,
+                              void* stream) {
+  if (!d || !w || !x || !conv_state || !rec_state || !out) return fail(Q35_E_ARG, "gated_deltanet_decode: null pointer");
+  int rc = validate_dims(*d);
+  if (rc) return rc;
+  if (B < 1) return fail(Q35_E_SHAPE, "gated_deltanet_decode: B must be >= 1");
+  const LayerDims L = ldims(*d);
+  if ((rc = check_q8f(w->in_proj_qkv, "in_proj_qkv")) || (rc = check_q8f(w->in_proj_z, "in_proj_z")) ||
+      (rc = check_q8f(w->out_proj, "out_proj")))
+    return rc;
+  if (w->in_proj_qkv.rows != L.H || w->in_proj_qkv.cols != L.conv_dim || w->in_proj_z.rows != L.H ||
+      w->in_proj_z.cols != L.vdim || w->out_proj.rows != L.vdim || w->out_proj.cols != L.H)
+    return fail(Q35_E_SHAPE, "gated_deltanet_decode: projection shapes do not match dims");
+  if (!w->in_proj_b || !w->in_proj_a || !w->a_log || !w->dt_bias || !w->conv_w || !w->norm_w)
+    return fail(Q35_E_ARG, "gated_deltanet_decode: null f32 weight");
+  const size_t scratch = layer_scratch_bytes(*d, B, 1);
+  if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, 1)) return fail(Q35_E_WS, "gated_deltanet_decode: workspace too small");
+  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
+  const int ldq = L.conv_dim + L.vdim;
+  float* qkvz = cv.f((size_t)B * ldq);
+  float* bg = cv.f((size_t)B * 2 * L.nh);
+  float* o = cv.f((size_t)B * L.vdim);
+  hipStream_t st = S(stream);
+  for (int b0 = 0; b0 < B; b0 += 8) {  // in_proj_qkv + in_proj_z + gate projection (text_modules.rs:497-508,569-576)
+    MvCall c;
+    c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
+    c.seg[0] = seg_of(w->in_proj_qkv, qkvz + (size_t)b0 * ldq, ldq);
+    c.seg[1] = seg_of(w->in_proj_z, qkvz + (size_t)b0 * ldq + L.conv_dim, ldq);
+    c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
+    c.aux_wb = w->in_proj_b; c.aux_wa = w->in_proj_a; c.aux_alog = w->a_log; c.aux_dtb = w->dt_bias;
+    c.aux_nh = L.nh; c.aux_out = bg + (size_t)b0 * 2 * L.nh; c.aux_ldo = 2 * L.nh;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  GdnCall g;  // conv update, l2norm, recurrent delta rule (:515-530, :627-652)
+  g.qkv = qkvz; g.ld_qkv = ldq; g.bg = bg; g.ld_bg = 2 * L.nh; g.conv_state = conv_state; g.conv_w = w->conv_w;
+  g.S = rec_state; g.o = o; g.ld_o = L.vdim; g.B = B; g.nh = L.nh; g.dk = L.dk; g.dv = L.dv; g.conv_k = d->conv_k;
+  if ((rc = gdn_step_launch(g, ws, scratch, st))) return rc;
+  for (int b0 = 0; b0 < B; b0 += 8) {  // gated RMSNorm + out_proj (:654-663)
+    MvCall c;
+    c.K = L.vdim; c.M = std::min(8, B - b0); c.nseg = 1;
+    c.seg[0] = seg_of(w->out_proj, out + (size_t)b0 * L.H, L.H);
+    c.pro = PRO_GATED; c.x = o + (size_t)b0 * L.vdim; c.ldx = L.vdim;
+    c.x2 = qkvz + (size_t)b0 * ldq + L.conv_dim; c.ldx2 = ldq;
+    c.pw = w->norm_w; c.group = L.dv; c.eps = d->eps;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const float* x, int32_t B, float* k_cache,
+                         float* v_cache, int32_t tmax, const int32_t* d_pos, const float* rope_cos,
+                         const float* rope_sin, float* out, void* ws, size_t ws_bytes, void* stream) {
+  if (!d || !w || !x || !k_cache || !v_cache || !d_pos || !rope_cos || !rope_sin || !out)
+    return fail(Q35_E_ARG, "attention_decode: null pointer");
+  int rc = validate_dims(*d);
+  if (rc) return rc;
+  if (B < 1 || tmax < 1) return fail(Q35_E_SHAPE, "attention_decode: B and tmax must be >= 1");
+  const LayerDims L = ldims(*d);
+  if ((rc = check_q8f(w->q_proj, "q_proj")) || (rc = check_q8f(w->k_proj, "k_proj")) ||
+      (rc = check_q8f(w->v_proj, "v_proj")) || (rc = check_q8f(w->o_proj, "o_proj")))
+    return rc;
+  if (w->q_proj.rows != L.H || w->q_proj.cols != L.ah * L.hd * 2 || w->k_proj.rows != L.H ||
+      w->k_proj.cols != L.kvh * L.hd || w->v_proj.rows != L.H || w->v_proj.cols != L.kvh * L.hd ||
+      w->o_proj.rows != L.ah * L.hd || w->o_proj.cols != L.H)
+    return fail(Q35_E_SHAPE, "attention_decode: projection shapes do not match dims");
+  if (!w->q_norm || !w->k_norm) return fail(Q35_E_ARG, "attention_decode: null norm weight");
+  const size_t scratch = layer_scratch_bytes(*d, B, tmax);
+  if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, tmax)) return fail(Q35_E_WS, "attention_decode: workspace too small");
+  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
+  const int ldqg = L.ah * L.hd * 2, ldkv = 2 * L.kvh * L.hd, ldo = L.ah * L.hd;
+  float* qg = cv.f((size_t)B * ldqg);
+  float* kv = cv.f((size_t)B * ldkv);
+  float* att = cv.f((size_t)B * ldo);
+  hipStream_t st = S(stream);
+  for (int b0 = 0; b0 < B; b0 += 8) {  // q_proj, k_proj, v_proj (text_modules.rs:855-893)
+    MvCall c;
+    c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 3;
+    c.seg[0] = seg_of(w->q_proj, qg + (size_t)b0 * ldqg, ldqg);
+    c.seg[1] = seg_of(w->k_proj, kv + (size_t)b0 * ldkv, ldkv);
+    c.seg[2] = seg_of(w->v_proj, kv + (size_t)b0 * ldkv + L.kvh * L.hd, ldkv);
+    c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  AttnCall a;  // norms, RoPE, KV append, attention, gate (:860-936)
+  a.qg = qg; a.ld_qg = ldqg; a.k = kv; a.v = kv + L.kvh * L.hd; a.ld_kv = ldkv; a.qnw = w->q_norm; a.knw = w->k_norm; a.eps = d->eps;
+  a.rcos = rope_cos; a.rsin = rope_sin; a.rot = d->rot_dim; a.kc = k_cache; a.vc = v_cache; a.tmax = tmax;
+  a.pos = d_pos; a.out = att; a.ld_out = ldo; a.B = B; a.nh = L.ah; a.nkv = L.kvh; a.hd = L.hd;
+  if ((rc = attn_launch(a, ws, scratch, st))) return rc;
+  for (int b0 = 0; b0 < B; b0 += 8) {  // o_proj (:938-942)
+    MvCall c;
+    c.K = ldo; c.M = std::min(8, B - b0); c.nseg = 1;
+    c.seg[0] = seg_of(w->o_proj, out + (size_t)b0 * L.H, L.H);
+    c.pro = PRO_PLAIN; c.x = att + (size_t)b0 * ldo; c.ldx = ldo;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, int32_t B, float* out, void* ws,
+                   size_t ws_bytes, void* stream) {
+  if (!d || !w || !x || !out) return fail(Q35_E_ARG, "mlp_decode: null pointer");
+  int rc = validate_dims(*d);
+  if (rc) return rc;
+  if (B < 1) return fail(Q35_E_SHAPE, "mlp_decode: B must be >= 1");
+  const LayerDims L = ldims(*d);
+  if ((rc = check_q8f(w->gate_proj, "gate_proj")) || (rc = check_q8f(w->up_proj, "up_proj")) ||
+      (rc = check_q8f(w->down_proj, "down_proj")))
+    return rc;
+  if (w->gate_proj.rows != L.H || w->gate_proj.cols != L.F || w->up_proj.rows != L.H || w->up_proj.cols != L.F ||
+      w->down_proj.rows != L.F || w->down_proj.cols != L.H)
+    return fail(Q35_E_SHAPE, "mlp_decode: projection shapes do not match dims");
+  const size_t scratch = layer_scratch_bytes(*d, B, 1);
+  if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, 1)) return fail(Q35_E_WS, "mlp_decode: workspace too small");
+  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
+  float* gu = cv.f((size_t)B * 2 * L.F);
+  hipStream_t st = S(stream);
+  for (int b0 = 0; b0 < B; b0 += 8) {  // gate_proj + up_proj (text_modules.rs:1003-1004)
+    MvCall c;
+    c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
+    c.seg[0] = seg_of(w->gate_proj, gu + (size_t)b0 * 2 * L.F, 2 * L.F);
+    c.seg[1] = seg_of(w->up_proj, gu + (size_t)b0 * 2 * L.F + L.F, 2 * L.F);
+    c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  for (int b0 = 0; b0 < B; b0 += 8) {  // up * silu(gate) -> down_proj (:1005)
+    MvCall c;
+    c.K = L.F; c.M = std::min(8, B - b0); c.nseg = 1;
+    c.seg[0] = seg_of(w->down_proj, out + (size_t)b0 * L.H, L.H);
+    c.pro = PRO_SWIGLU; c.x = gu + (size_t)b0 * 2 * L.F; c.ldx = 2 * L.F; c.swiglu_off = L.F;
+    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* beta_g, float* conv_state,
+                                const float* conv_w, float* rec_state, float* core_out, int32_t lin_heads,
+                                int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes, void* stream) {
+  if (!mixed_qkv || !beta_g || !conv_state || !conv_w || !rec_state || !core_out)
+    return fail(Q35_E_ARG, "gated_delta_rule_decode: null pointer");
+  if (B < 1 || lin_heads < 1) return fail(Q35_E_SHAPE, "gated_delta_rule_decode: B and heads must be >= 1");
+  GdnCall g;
+  const int conv_dim = 2 * lin_heads * lin_dk + lin_heads * lin_dv;
+  g.qkv = mixed_qkv; g.ld_qkv = conv_dim; g.bg = beta_g; g.ld_bg = 2 * lin_heads; g.conv_state = conv_state;
+  g.conv_w = conv_w; g.S = rec_state; g.o = core_out; g.ld_o = lin_heads * lin_dv; g.B = B; g.nh = lin_heads;
+  g.dk = lin_dk; g.dv = lin_dv; g.conv_k = 4;
+  return gdn_step_launch(g, ws, ws_bytes, S(stream));
+}
+
+int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const float* k_new, const float* v_new,
+                              int32_t kv_ld, int32_t B, const float* q_norm, const float* k_norm, float* k_cache,
+                              float* v_cache, int32_t tmax, const int32_t* d_pos, const float* rope_cos,
+                              const float* rope_sin, float* out, void* ws, size_t ws_bytes, void* stream) {
+  if (!d) return fail(Q35_E_ARG, "attention_core_decode: null dims");
+  int rc = validate_dims(*d);
+  if (rc) return rc;
+  if (kv_ld < d->kv_heads * d->head_dim) return fail(Q35_E_SHAPE, "attention_core_decode: kv_ld too small");
+  AttnCall a;
+  a.qg = q_gate; a.ld_qg = d->attn_heads * d->head_dim * 2; a.k = k_new; a.v = v_new; a.ld_kv = kv_ld;
+  a.qnw = q_norm; a.knw = k_norm; a.eps = d->eps; a.rcos = rope_cos; a.rsin = rope_sin; a.rot = d->rot_dim;
+  a.kc = k_cache; a.vc = v_cache; a.tmax = tmax; a.pos = d_pos; a.out = out; a.ld_out = d->attn_heads * d->head_dim;
+  a.B = B; a.nh = d->attn_heads; a.nkv = d->kv_heads; a.hd = d->head_dim;
+  return attn_launch(a, ws, ws_bytes, S(stream));
+}
+
+int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin_host) {
+  if (!d || !cos_host || !sin_host || tmax < 1) return fail(Q35_E_ARG, "rope_tables: bad argument");
+  const int rot = d->rot_dim, half = rot / 2;
+  const float sf = -std::log(d->theta) / (float)rot;
+  for (int i = 0; i < half; ++i) {
+    const float inv = std::exp((float)(2 * i) * sf);
+    for (int t = 0; t < tmax; ++t) {
+      const float ang = (float)t * inv;
+      const float c = std::cos(ang), s = std::sin(ang);
+      cos_host[(size_t)t * rot + i] = c; cos_host[(size_t)t * rot + i + half] = c;
+      sin_host[(size_t)t * rot + i] = s; sin_host[(size_t)t * rot + i + half] = s;
+    }
+  }
+  return Q35_OK;
+}
+
+}  // extern "C"

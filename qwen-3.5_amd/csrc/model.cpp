@@ -1,0 +1,410 @@
+// The decoder model: weight upload, per-layer caches, the decode step as a fixed sequence of
+// fused kernels, hipGraph capture of that sequence, and greedy generation.
+//
+// One decode step (TextForCausalLM::forward at seq_len 1, model.rs:27-84,113-129, plus the
+// greedy argmax of main.rs:131) is 5 launches per layer + 1:
+//   linear-attention layer: [input RMSNorm -> in_proj_qkv|in_proj_z|gate-proj]  -> DeltaNet step
+//                           -> [gated RMSNorm -> out_proj -> +residual]
+//   full-attention layer:   [input RMSNorm -> q|k|v proj] -> attention -> [o_proj -> +residual]
+//   MLP:                    [post RMSNorm -> gate|up] -> [SwiGLU -> down -> +residual]
+//   head:                   [final RMSNorm -> lm_head -> argmax -> token, pos += 1]
+// The token, the position, the prompt and the token history live in device memory, so the
+// captured graph is replayed unchanged for every prompt token and every generated token.
+#include "q35_host.h"
+
+#include <chrono>
+#include <cstring>
+#include <map>
+#include <vector>
+
+struct q35_model {
+  q35_dims d;
+  uint64_t seed = 0;
+  int32_t tmax = 0;
+  int32_t host_pos = 0;  // host mirror of the device position
+  struct Buf { void* p; size_t bytes; };
+  std::map<std::string, Buf> tensors;
+  std::vector<void*> allocs;
+  struct Q8 { const int8_t* q; const float* s; int rows, cols; };
+  struct Layer {
+    bool full = false;
+    const float *in_norm = nullptr, *post_norm = nullptr;
+    Q8 qkv{}, z{}, out{}, q{}, k{}, v{}, o{}, gate{}, up{}, down{};
+    const float *w_b = nullptr, *w_a = nullptr, *a_log = nullptr, *dt_bias = nullptr, *conv_w = nullptr, *norm_w = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    float *conv_state = nullptr, *rec = nullptr, *kc = nullptr, *vc = nullptr;
+  };
+  std::vector<Layer> layers;
+  Q8 embed{};
+  const float* final_norm = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float *h = nullptr, *qkvz = nullptr, *bg = nullptr, *o_raw = nullptr, *gu = nullptr;
+  float *qg = nullptr, *kvb = nullptr, *attn = nullptr, *logits = nullptr;
+  int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr;
+  int32_t* pinned = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipStream_t own_stream = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+};
+
+namespace q35 {
+namespace {
+
+int dev_alloc(q35_model* m, const std::string& name, size_t bytes, void** out) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes < 256 ? 256 : bytes);
+  if (e != hipSuccess) return fail(Q35_E_NOMEM, "hipMalloc(" + name + "): " + hipGetErrorString(e));
+  m->allocs.push_back(p);
+  m->tensors[name] = {p, bytes};
+  *out = p;
+  return Q35_OK;
+}
+
+template <class T>
+int dev_alloc_t(q35_model* m, const std::string& name, size_t n, T** out) {
+  void* p = nullptr;
+  int rc = dev_alloc(m, name, n * sizeof(T), &p);
+  *out = static_cast<T*>(p);
+  return rc;
+}
+
+hipStream_t pick(q35_model* m, void* s) { return s ? static_cast<hipStream_t>(s) : m->own_stream; }
+
+int launch_step(q35_model* m, hipStream_t st) {
+  const q35_dims& d = m->d;
+  const int H = d.hidden, F = d.ffn;
+  const int nh = d.lin_heads, dk = d.lin_dk, dv = d.lin_dv;
+  const int key_dim = nh * dk, vdim = nh * dv, conv_dim = 2 * key_dim + vdim, ldq = conv_dim + vdim;
+  const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  int rc;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    MvCall c;
+    c.K = H; c.M = 1; c.x = m->h; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps;
+    if (l == 0) {
+      c.pro = PRO_EMBED_RMS;
+      c.emb_q = m->embed.q; c.emb_s = m->embed.s; c.token = m->token; c.h_out = m->h;
+      c.prompt = m->prompt; c.plen = m->plen; c.pos = m->pos;
+    } else {
+      c.pro = PRO_RMS;
+    }
+    if (!L.full) {
+      c.nseg = 2;
+      c.seg[0] = MvSeg{L.qkv.q, L.qkv.s, m->qkvz, conv_dim, ldq};
+      c.seg[1] = MvSeg{L.z.q, L.z.s, m->qkvz + conv_dim, vdim, ldq};
+      c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_alog = L.a_log; c.aux_dtb = L.dt_bias;
+      c.aux_nh = nh; c.aux_out = m->bg; c.aux_ldo = 2 * nh;
+      if ((rc = mv_kn_launch(c, m->ws, m->ws_bytes, st))) return rc;
+      GdnCall g;
+      g.qkv = m->qkvz; g.ld_qkv = ldq; g.bg = m->bg; g.ld_bg = 2 * nh; g.conv_state = L.conv_state;
+      g.conv_w = L.conv_w; g.S = L.rec; g.o = m->o_raw; g.ld_o = vdim; g.B = 1; g.nh = nh; g.dk = dk; g.dv = dv;
+      g.conv_k = d.conv_k;
+      if ((rc = gdn_step_launch(g, m->ws, m->ws_bytes, st))) return rc;
+      MvCall c2;
+      c2.K = vdim; c2.M = 1; c2.nseg = 1;
+      c2.seg[0] = MvSeg{L.out.q, L.out.s, m->h, H, H};
+      c2.pro = PRO_GATED; c2.x = m->o_raw; c2.ldx = vdim; c2.x2 = m->qkvz + conv_dim; c2.ldx2 = ldq;
+      c2.pw = L.norm_w; c2.group = dv; c2.eps = d.eps; c2.epi = EPI_RESID;
+      if ((rc = mv_kn_launch(c2, m->ws, m->ws_bytes, st))) return rc;
+    } else {
+      c.nseg = 3;
+      c.seg[0] = MvSeg{L.q.q, L.q.s, m->qg, ah * hd * 2, ah * hd * 2};
+      c.seg[1] = MvSeg{L.k.q, L.k.s, m->kvb, kvh * hd, 2 * kvh * hd};
+      c.seg[2] = MvSeg{L.v.q, L.v.s, m->kvb + kvh * hd, kvh * hd, 2 * kvh * hd};
+      if ((rc = mv_kn_launch(c, m->ws, m->ws_bytes, st))) return rc;
+      AttnCall a;
+      a.qg = m->qg; a.ld_qg = ah * hd * 2; a.k = m->kvb; a.v = m->kvb + kvh * hd; a.ld_kv = 2 * kvh * hd;
+      a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
+      a.rcos = m->rope_cos; a.rsin = m->rope_sin; a.rot = d.rot_dim;
+      a.kc = L.kc; a.vc = L.vc; a.tmax = m->tmax; a.pos = m->pos;
+      a.out = m->attn; a.ld_out = ah * hd; a.B = 1; a.nh = ah; a.nkv = kvh; a.hd = hd;
+      if ((rc = attn_launch(a, m->ws, m->ws_bytes, st))) return rc;
+      MvCall c2;
+      c2.K = ah * hd; c2.M = 1; c2.nseg = 1;
+      c2.seg[0] = MvSeg{L.o.q, L.o.s, m->h, H, H};
+      c2.pro = PRO_PLAIN; c2.x = m->attn; c2.ldx = ah * hd; c2.epi = EPI_RESID;
+      if ((rc = mv_kn_launch(c2, m->ws, m->ws_bytes, st))) return rc;
+    }
+    MvCall c3;
+    c3.K = H; c3.M = 1; c3.nseg = 2;
+    c3.seg[0] = MvSeg{L.gate.q, L.gate.s, m->gu, F, 2 * F};
+    c3.seg[1] = MvSeg{L.up.q, L.up.s, m->gu + F, F, 2 * F};
+    c3.pro = PRO_RMS; c3.x = m->h; c3.ldx = H; c3.pw = L.post_norm; c3.eps = d.eps;
+    if ((rc = mv_kn_launch(c3, m->ws, m->ws_bytes, st))) return rc;
+    MvCall c4;
+    c4.K = F; c4.M = 1; c4.nseg = 1;
+    c4.seg[0] = MvSeg{L.down.q, L.down.s, m->h, H, H};
+    c4.pro = PRO_SWIGLU; c4.x = m->gu; c4.ldx = 2 * F; c4.swiglu_off = F; c4.epi = EPI_RESID;
+    if ((rc = mv_kn_launch(c4, m->ws, m->ws_bytes, st))) return rc;
+  }
+  NkCall n;
+  n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = 1;
+  n.x = m->h; n.ldx = H; n.y = m->logits; n.ldy = d.vocab; n.pro = PRO_RMS; n.pw = m->final_norm; n.eps = d.eps;
+  n.argmax_out = m->token; n.pos_inc = m->pos; n.hist = m->hist;
+  return nk_launch(n, m->ws, m->ws_bytes, st);
+}
+
+size_t model_ws_bytes(const q35_dims& d, int tmax) {
+  const int H = d.hidden, F = d.ffn;
+  const int nh = d.lin_heads, vdim = nh * d.lin_dv, conv_dim = 2 * nh * d.lin_dk + vdim;
+  const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  size_t m = gdn_step_ws_bytes(1, nh);
+  auto mv = [&](int K, std::initializer_list<int> Ns, int aux) {
+    MvCall c;
+    c.K = K; c.M = 1; c.nseg = 0;
+    for (int N : Ns) { c.seg[c.nseg].N = N; ++c.nseg; }
+    c.aux_nh = aux;
+    m = std::max(m, mv_kn_ws_bytes(c));
+  };
+  mv(H, {conv_dim, vdim}, nh);
+  mv(vdim, {H}, 0);
+  mv(H, {ah * hd * 2, kvh * hd, kvh * hd}, 0);
+  mv(ah * hd, {H}, 0);
+  mv(H, {F, F}, 0);
+  mv(F, {H}, 0);
+  m = std::max(m, attn_ws_bytes(1, ah, kvh, hd, tmax));
+  NkCall n;
+  n.N = d.vocab; n.K = H;
+  m = std::max(m, nk_ws_bytes(n));
+  return align256(m);
+}
+
+void destroy(q35_model* m) {
+  if (!m) return;
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (void* p : m->allocs) (void)hipFree(p);
+  if (m->pinned) (void)hipHostFree(m->pinned);
+  if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
+  delete m;
+}
+
+int capture(q35_model* m, hipStream_t st) {
+  if (m->exec) return Q35_OK;
+  Q35_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  int rc = launch_step(m, st);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(st, &g);
+  if (rc != Q35_OK) { if (g) (void)hipGraphDestroy(g); return rc; }
+  if (e != hipSuccess) return fail(Q35_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+  e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) { (void)hipGraphDestroy(g); return fail(Q35_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e)); }
+  m->graph = g;
+  return Q35_OK;
+}
+
+int step(q35_model* m, int use_graph, hipStream_t st) {
+  if (m->host_pos >= m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
+  if (use_graph) {
+    int rc = capture(m, st);
+    if (rc) return rc;
+    Q35_HIP_TRY(hipGraphLaunch(m->exec, st));
+  } else {
+    int rc = launch_step(m, st);
+    if (rc) return rc;
+  }
+  m->host_pos += 1;
+  return Q35_OK;
+}
+
+}  // namespace
+}  // namespace q35
+
+using namespace q35;
+
+extern "C" {
+
+int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, q35_model** out) {
+  if (!dp || !out) return fail(Q35_E_ARG, "model_create: null pointer");
+  *out = nullptr;
+  int rc = validate_dims(*dp);
+  if (rc) return rc;
+  if (tmax < 1) return fail(Q35_E_SHAPE, "model_create: tmax must be >= 1");
+  q35_model* m = new q35_model();
+  m->d = *dp; m->seed = seed; m->tmax = tmax;
+  const q35_dims& d = m->d;
+  auto bail = [&](int code) { destroy(m); return code; };
+  if (hipStreamCreateWithFlags(&m->own_stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(Q35_E_HIP, "hipStreamCreate failed"));
+
+  // weights
+  std::vector<float> host;
+  std::vector<int8_t> hq;
+  std::vector<float> hs;
+  for (const TensorSpec& t : model_specs(d)) {
+    const size_t n = (size_t)t.rows * t.cols;
+    host.resize(n);
+    synth_values(t, seed, host.data());
+    if (t.kind == kF32) {
+      float* p;
+      if ((rc = dev_alloc_t(m, t.name, n, &p))) return bail(rc);
+      if (hipMemcpy(p, host.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) return bail(fail(Q35_E_HIP, "upload " + t.name));
+    } else {
+      hq.resize(n);
+      hs.resize(n / 64);
+      quantize_q8f(host.data(), t.rows, t.cols, hq.data(), hs.data());
+      int8_t* pq; float* ps;
+      if ((rc = dev_alloc_t(m, t.name + ".q", n, &pq))) return bail(rc);
+      if ((rc = dev_alloc_t(m, t.name + ".scale", n / 64, &ps))) return bail(rc);
+      if (hipMemcpy(pq, hq.data(), n, hipMemcpyHostToDevice) != hipSuccess ||
+          hipMemcpy(ps, hs.data(), n / 64 * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(Q35_E_HIP, "upload " + t.name));
+    }
+  }
+  std::vector<float>().swap(host);
+  std::vector<int8_t>().swap(hq);
+  std::vector<float>().swap(hs);
+  auto f32 = [&](const std::string& n) { return static_cast<const float*>(m->tensors.at(n).p); };
+  auto q8 = [&](const std::string& n, int rows, int cols) {
+    return q35_model::Q8{static_cast<const int8_t*>(m->tensors.at(n + ".q").p), f32(n + ".scale"), rows, cols};
+  };
+  const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
+  const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  m->embed = q8("embed_tokens", d.vocab, H);
+  m->final_norm = f32("norm");
+  m->layers.resize(d.n_layers);
+  for (int l = 0; l < d.n_layers; ++l) {
+    q35_model::Layer& L = m->layers[l];
+    const std::string p = "layers." + std::to_string(l) + ".";
+    L.full = is_full_layer(d, l);
+    L.in_norm = f32(p + "input_layernorm");
+    L.post_norm = f32(p + "post_attention_layernorm");
+    if (!L.full) {
+      const std::string a = p + "linear_attn.";
+      L.qkv = q8(a + "in_proj_qkv", H, conv_dim);
+      L.z = q8(a + "in_proj_z", H, vdim);
+      L.out = q8(a + "out_proj", vdim, H);
+      L.w_b = f32(a + "in_proj_b"); L.w_a = f32(a + "in_proj_a");
+      L.a_log = f32(a + "a_log"); L.dt_bias = f32(a + "dt_bias");
+      L.conv_w = f32(a + "conv1d"); L.norm_w = f32(a + "norm");
+      if ((rc = dev_alloc_t(m, a + "conv_state", (size_t)conv_dim * (d.conv_k - 1), &L.conv_state))) return bail(rc);
+      if ((rc = dev_alloc_t(m, a + "recurrent_state", (size_t)nh * d.lin_dk * d.lin_dv, &L.rec))) return bail(rc);
+    } else {
+      const std::string a = p + "self_attn.";
+      L.q = q8(a + "q_proj", H, ah * hd * 2);
+      L.k = q8(a + "k_proj", H, kvh * hd);
+      L.v = q8(a + "v_proj", H, kvh * hd);
+      L.o = q8(a + "o_proj", ah * hd, H);
+      L.q_norm = f32(a + "q_norm"); L.k_norm = f32(a + "k_norm");
+      if ((rc = dev_alloc_t(m, a + "k_cache", (size_t)kvh * tmax * hd, &L.kc))) return bail(rc);
+      if ((rc = dev_alloc_t(m, a + "v_cache", (size_t)kvh * tmax * hd, &L.vc))) return bail(rc);
+    }
+    const std::string mp = p + "mlp.";
+    L.gate = q8(mp + "gate_proj", H, F);
+    L.up = q8(mp + "up_proj", H, F);
+    L.down = q8(mp + "down_proj", F, H);
+  }
+  // rotary tables
+  {
+    std::vector<float> cs((size_t)tmax * d.rot_dim), sn((size_t)tmax * d.rot_dim);
+    q35_rope_tables(&d, tmax, cs.data(), sn.data());
+    if ((rc = dev_alloc_t(m, "rope_cos", cs.size(), &m->rope_cos))) return bail(rc);
+    if ((rc = dev_alloc_t(m, "rope_sin", sn.size(), &m->rope_sin))) return bail(rc);
+    if (hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bail(fail(Q35_E_HIP, "upload rope tables"));
+  }
+  // activations, control scalars, workspace
+  if ((rc = dev_alloc_t(m, "h", H, &m->h)) || (rc = dev_alloc_t(m, "qkvz", conv_dim + vdim, &m->qkvz)) ||
+      (rc = dev_alloc_t(m, "bg", 2 * nh, &m->bg)) || (rc = dev_alloc_t(m, "o_raw", vdim, &m->o_raw)) ||
+      (rc = dev_alloc_t(m, "gu", 2 * F, &m->gu)) || (rc = dev_alloc_t(m, "qg", ah * hd * 2, &m->qg)) ||
+      (rc = dev_alloc_t(m, "kv", 2 * kvh * hd, &m->kvb)) || (rc = dev_alloc_t(m, "attn", ah * hd, &m->attn)) ||
+      (rc = dev_alloc_t(m, "logits", d.vocab, &m->logits)) || (rc = dev_alloc_t(m, "token", 1, &m->token)) ||
+      (rc = dev_alloc_t(m, "pos", 1, &m->pos)) || (rc = dev_alloc_t(m, "prompt", tmax, &m->prompt)) ||
+      (rc = dev_alloc_t(m, "plen", 1, &m->plen)) || (rc = dev_alloc_t(m, "hist", tmax, &m->hist)))
+    return bail(rc);
+  m->ws_bytes = model_ws_bytes(d, tmax);
+  if ((rc = dev_alloc(m, "workspace", m->ws_bytes, &m->ws))) return bail(rc);
+  if (hipHostMalloc(reinterpret_cast<void**>(&m->pinned), 64 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
+    return bail(fail(Q35_E_NOMEM, "hipHostMalloc failed"));
+  if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(fail(Q35_E_HIP, "workspace clear"));
+  if ((rc = q35_model_reset(m, nullptr))) return bail(rc);
+  if (hipStreamSynchronize(m->own_stream) != hipSuccess) return bail(fail(Q35_E_HIP, "sync"));
+  *out = m;
+  return Q35_OK;
+}
+
+int q35_model_destroy(q35_model* m) {
+  if (!m) return Q35_OK;
+  (void)hipDeviceSynchronize();
+  destroy(m);
+  return Q35_OK;
+}
+
+int q35_model_reset(q35_model* m, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_reset: null model");
+  hipStream_t st = pick(m, stream);
+  for (auto& kv : m->tensors) {
+    const std::string& n = kv.first;
+    const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
+                       n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
+                       n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt";
+    if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
+  }
+  m->host_pos = 0;
+  return Q35_OK;
+}
+
+int q35_model_set_token(q35_model* m, int32_t token, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_set_token: null model");
+  if (token < 0 || token >= m->d.vocab) return fail(Q35_E_ARG, "model_set_token: token out of range");
+  hipStream_t st = pick(m, stream);
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  m->pinned[0] = token;
+  Q35_HIP_TRY(hipMemcpyAsync(m->token, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  return Q35_OK;
+}
+
+int q35_model_step(q35_model* m, int32_t use_graph, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_step: null model");
+  return step(m, use_graph, pick(m, stream));
+}
+
+int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t n_new,
+                       int32_t* out_tokens_host, int32_t use_graph, int32_t readback_each,
+                       double* decode_seconds_host, void* stream) {
+  if (!m || !prompt_host || !out_tokens_host) return fail(Q35_E_ARG, "model_generate: null pointer");
+  if (n_prompt < 1 || n_new < 0) return fail(Q35_E_SHAPE, "model_generate: need n_prompt >= 1, n_new >= 0");
+  const int32_t p0 = m->host_pos;
+  if ((int64_t)p0 + n_prompt + n_new > m->tmax) return fail(Q35_E_SHAPE, "model_generate: tmax too small");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt_host[i] < 0 || prompt_host[i] >= m->d.vocab) return fail(Q35_E_ARG, "model_generate: prompt id out of range");
+  hipStream_t st = pick(m, stream);
+  Q35_HIP_TRY(hipMemcpyAsync(m->prompt + p0, prompt_host, sizeof(int32_t) * n_prompt, hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  m->pinned[0] = p0 + n_prompt;
+  Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  int rc;
+  if (use_graph && (rc = capture(m, st))) return rc;
+  for (int i = 0; i < n_prompt; ++i)
+    if ((rc = step(m, use_graph, st))) return rc;
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < n_new; ++i) {
+    if ((rc = step(m, use_graph, st))) return rc;
+    if (readback_each) {  // main.rs:107: the token goes to the host every step
+      Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+      Q35_HIP_TRY(hipStreamSynchronize(st));
+    }
+  }
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const auto t1 = std::chrono::steady_clock::now();
+  if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
+  Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + p0 + n_prompt - 1, sizeof(int32_t) * (n_new + 1), hipMemcpyDeviceToHost));
+  return Q35_OK;
+}
+
+int q35_model_tensor(q35_model* m, const char* name, void** dptr, size_t* bytes) {
+  if (!m || !name || !dptr) return fail(Q35_E_ARG, "model_tensor: null pointer");
+  auto it = m->tensors.find(name);
+  if (it == m->tensors.end()) return fail(Q35_E_ARG, std::string("model_tensor: unknown tensor ") + name);
+  *dptr = it->second.p;
+  if (bytes) *bytes = it->second.bytes;
+  return Q35_OK;
+}
+
+}  // extern "C"

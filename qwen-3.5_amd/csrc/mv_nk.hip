@@ -1,0 +1,300 @@
+// Q8F matvec with rows contiguous along K (NK: W[N][K] int8, scale[N][K/64]) — the tied
+// embedding table used as lm_head (kernels.rs:251-291) — plus the greedy argmax
+// (kernels.rs:298-371) fused into its epilogue, the standalone argmax and the embedding
+// lookup (kernels.rs:15-45).
+//
+// lm_head decomposition: each wave owns 4 rows per step; lane l reads 16-byte chunks
+// k = 16*(l + 64c) of every row, so a wave reads 1 KB contiguous per row per chunk.  x (after
+// the optional final RMSNorm) is staged once per block in LDS.  The 4 row partials of a lane
+// are folded with a transposed butterfly (xor 32, xor 16 exchange halves of the row set,
+// xor 8..1 finish the sum), 7 lane exchanges per 4 rows.  Blocks stride over row groups.
+// The argmax keeps (max, lowest index) per lane -> wave -> block; the last block to finish
+// reduces the block results; (max, lowest index) is a total order so the result does not
+// depend on the reduction order.
+#include "q35_internal.h"
+#include <climits>
+
+namespace q35 {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerWave = 4;
+constexpr int kRowsPerBlock = 16;
+constexpr int kMaxCpw = 8;        // 16-byte chunks per lane per row: K <= 8192
+constexpr int kMaxGrid = 2048;
+constexpr int kLdsFloats = 12288; // MR*K staged floats (48 KB)
+
+struct NkArgs {
+  const int8_t* q; const float* s;
+  int32_t N, K, M;
+  const float* x; int32_t ldx;
+  float* y; int32_t ldy;
+  int32_t pro; const float* pw; float eps;
+  int32_t* argmax_out; int32_t* pos_inc; int32_t* hist;
+  float* part_v; int32_t* part_i; uint32_t* counter;
+};
+
+Q35_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+Q35_DEV void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int oi = __shfl_xor(i, o, 64);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// Block-wide (max, lowest index) reduction; result valid in all threads.
+Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
+  wave_argmax(v, i);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) { shv[wid] = v; shi[wid] = i; }
+  __syncthreads();
+  v = shv[0]; i = shi[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w)
+    if (better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
+}
+
+template <int MR>
+__global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
+  extern __shared__ __align__(16) float xs[];  // [MR][K]
+  __shared__ float sh[4];
+  __shared__ float shv[4];
+  __shared__ int shi[4];
+  __shared__ int flag;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int K = a.K, nbK = K >> 6;
+
+  // prologue: x (optionally RMS-normalised with (1+w)) into LDS
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= a.M) break;
+    float r = 1.0f;
+    if (a.pro == PRO_RMS) {
+      float ss = 0.f;
+      for (int k = tid; k < K; k += kThreads) { float v = a.x[(size_t)m * a.ldx + k]; ss += v * v; }
+      ss = block_sum256(ss, sh);
+      r = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    for (int k = tid; k < K; k += kThreads) {
+      float v = a.x[(size_t)m * a.ldx + k];
+      if (a.pro == PRO_RMS) v = (v * r) * (1.0f + a.pw[k]);
+      xs[m * K + k] = v;
+    }
+  }
+  __syncthreads();
+
+  const int cpw = (K + 1023) >> 10;
+  float best_v = -INFINITY;
+  int best_i = INT_MAX;
+  const int nrb = (a.N + kRowsPerBlock - 1) / kRowsPerBlock;
+  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+    const int row0 = rb * kRowsPerBlock + wid * kRowsPerWave;
+    uint4 wv[kRowsPerWave][kMaxCpw];
+    float sv[kRowsPerWave][kMaxCpw];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+      const int row = row0 + r;
+#pragma unroll
+      for (int c = 0; c < kMaxCpw; ++c) {
+        if (c >= cpw) break;
+        const int k = 16 * (lane + 64 * c);
+        const bool ok = row < a.N && k < K;
+        wv[r][c] = ok ? *reinterpret_cast<const uint4*>(a.q + (size_t)row * K + k) : make_uint4(0, 0, 0, 0);
+        sv[r][c] = ok ? a.s[(size_t)row * nbK + (k >> 6)] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= a.M) break;
+      float p[kRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kMaxCpw; ++c) {
+        if (c >= cpw) break;
+        const int k = 16 * (lane + 64 * c);
+        if (k >= K) continue;
+        float xv[16];
+        const float4* xp = reinterpret_cast<const float4*>(&xs[m * K + k]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float4 t = xp[q];
+          xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+        }
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+          float f[16];
+          unpack16(wv[r][c], f);
+          float d = 0.f;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) d += f[j] * xv[j];
+          p[r] += d * sv[r][c];
+        }
+      }
+      // transposed butterfly: lane l ends with row (l >> 4) summed over its 16-lane group
+      const bool hi32 = (lane & 32) != 0;
+      float s0 = hi32 ? p[0] : p[2], s1 = hi32 ? p[1] : p[3];
+      float k0 = hi32 ? p[2] : p[0], k1 = hi32 ? p[3] : p[1];
+      k0 += __shfl_xor(s0, 32, 64);
+      k1 += __shfl_xor(s1, 32, 64);
+      const bool hi16 = (lane & 16) != 0;
+      float snd = hi16 ? k0 : k1;
+      float v = hi16 ? k1 : k0;
+      v += __shfl_xor(snd, 16, 64);
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 1, 64);
+      const int row = row0 + (lane >> 4);
+      if ((lane & 15) == 0 && row < a.N) {
+        if (a.y) a.y[(size_t)m * a.ldy + row] = v;
+        if (m == 0 && v > best_v) { best_v = v; best_i = row; }
+      }
+    }
+  }
+
+  if (!a.argmax_out) return;
+  block_argmax(best_v, best_i, shv, shi);
+  if (tid == 0) { a.part_v[blockIdx.x] = best_v; a.part_i[blockIdx.x] = best_i; }
+  if (!arrive_last(a.counter, gridDim.x, &flag)) return;
+  float v = -INFINITY;
+  int i = INT_MAX;
+  for (int b = tid; b < (int)gridDim.x; b += kThreads)
+    if (better(a.part_v[b], a.part_i[b], v, i)) { v = a.part_v[b]; i = a.part_i[b]; }
+  block_argmax(v, i, shv, shi);
+  if (tid == 0) {
+    const int32_t tok = (i == INT_MAX) ? 0 : i;
+    *a.argmax_out = tok;
+    if (a.pos_inc) {
+      const int32_t p = *a.pos_inc;
+      if (a.hist) a.hist[p] = tok;
+      *a.pos_inc = p + 1;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* v, int64_t n, float* part_v, int32_t* part_i,
+                                                         uint32_t* counter, int32_t* out) {
+  __shared__ float shv[4];
+  __shared__ int shi[4];
+  __shared__ int flag;
+  const int tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + tid; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const float x = v[i];
+    if (x > bv) { bv = x; bi = (int)i; }
+  }
+  block_argmax(bv, bi, shv, shi);
+  if (tid == 0) { part_v[blockIdx.x] = bv; part_i[blockIdx.x] = bi; }
+  if (!arrive_last(counter, gridDim.x, &flag)) return;
+  float rv = -INFINITY;
+  int ri = INT_MAX;
+  for (int b = tid; b < (int)gridDim.x; b += kThreads)
+    if (better(part_v[b], part_i[b], rv, ri)) { rv = part_v[b]; ri = part_i[b]; }
+  block_argmax(rv, ri, shv, shi);
+  if (tid == 0) *out = (ri == INT_MAX) ? 0 : ri;
+}
+
+__global__ __launch_bounds__(kThreads) void embed_kernel(const int8_t* q, const float* s, int32_t D, const int32_t* ids,
+                                                        int32_t n, float* out) {
+  const int64_t total = (int64_t)n * (D / 16);
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += (int64_t)gridDim.x * kThreads) {
+    const int i = (int)(e / (D / 16));
+    const int d = (int)(e % (D / 16)) * 16;
+    const int64_t id = ids[i];
+    const uint4 w = *reinterpret_cast<const uint4*>(q + id * D + d);
+    const float sc = s[id * (D / 64) + d / 64];
+    float f[16];
+    unpack16(w, f);
+    float4* o = reinterpret_cast<float4*>(out + (size_t)i * D + d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = make_float4(f[4 * j] * sc, f[4 * j + 1] * sc, f[4 * j + 2] * sc, f[4 * j + 3] * sc);
+  }
+}
+
+int nk_grid(int N) {
+  const int nrb = (N + kRowsPerBlock - 1) / kRowsPerBlock;
+  return nrb < kMaxGrid ? nrb : kMaxGrid;
+}
+
+}  // namespace
+
+size_t nk_ws_bytes(const NkCall& c) {
+  const size_t g = (size_t)nk_grid(c.N);
+  return kCounterBytes + align256(g * 4) * 2;
+}
+
+int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (!c.q || !c.s || !c.x) return fail(Q35_E_ARG, "nk: null pointer");
+  if (c.N <= 0 || c.K <= 0 || (c.K % 64) != 0) return fail(Q35_E_SHAPE, "nk: K must be a positive multiple of 64");
+  if (c.K > 1024 * kMaxCpw) return fail(Q35_E_SHAPE, "nk: K > 8192");
+  if (c.M < 1 || c.M > 8) return fail(Q35_E_SHAPE, "nk: M in [1,8]");
+  int MR = c.M == 1 ? 1 : (c.M == 2 ? 2 : (c.M <= 4 ? 4 : 8));
+  if ((size_t)MR * c.K > (size_t)kLdsFloats) return fail(Q35_E_SHAPE, "nk: M*K too large for LDS staging");
+  if ((reinterpret_cast<uintptr_t>(c.q) & 15) != 0) return fail(Q35_E_ALIGN, "nk: weights not 16-byte aligned");
+  if (c.pro == PRO_RMS && !c.pw) return fail(Q35_E_ARG, "nk: RMSNorm needs weight");
+  if (c.argmax_out && c.M != 1) return fail(Q35_E_SHAPE, "nk: fused argmax needs M == 1");
+  if (!c.y && !c.argmax_out) return fail(Q35_E_ARG, "nk: no output");
+  NkArgs a;
+  a.q = c.q; a.s = c.s; a.N = c.N; a.K = c.K; a.M = c.M;
+  a.x = c.x; a.ldx = c.ldx; a.y = c.y; a.ldy = c.ldy;
+  a.pro = c.pro; a.pw = c.pw; a.eps = c.eps;
+  a.argmax_out = c.argmax_out; a.pos_inc = c.pos_inc; a.hist = c.hist;
+  const int grid = nk_grid(c.N);
+  a.counter = nullptr; a.part_v = nullptr; a.part_i = nullptr;
+  if (c.argmax_out) {
+    if (!ws || ws_bytes < nk_ws_bytes(c)) return fail(Q35_E_WS, "nk: workspace too small");
+    char* base = ws_scratch(ws);
+    const size_t pb = align256((size_t)grid * 4);
+    a.counter = ws_counters(ws);
+    a.part_v = reinterpret_cast<float*>(base);
+    a.part_i = reinterpret_cast<int32_t*>(base + pb);
+  }
+  const size_t lds = (size_t)MR * c.K * sizeof(float);
+  if (MR == 1) hipLaunchKernelGGL(nk_kernel<1>, dim3(grid), dim3(kThreads), lds, st, a);
+  else if (MR == 2) hipLaunchKernelGGL(nk_kernel<2>, dim3(grid), dim3(kThreads), lds, st, a);
+  else if (MR == 4) hipLaunchKernelGGL(nk_kernel<4>, dim3(grid), dim3(kThreads), lds, st, a);
+  else hipLaunchKernelGGL(nk_kernel<8>, dim3(grid), dim3(kThreads), lds, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+size_t argmax_ws_bytes(int64_t n) {
+  (void)n;
+  return kCounterBytes + 2 * 1024 * 4;
+}
+
+int argmax_launch(const float* v, int64_t n, int32_t* out, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (!v || !out) return fail(Q35_E_ARG, "argmax: null pointer");
+  if (n <= 0 || n > INT_MAX) return fail(Q35_E_SHAPE, "argmax: n out of range");
+  if (!ws || ws_bytes < argmax_ws_bytes(n)) return fail(Q35_E_WS, "argmax: workspace too small");
+  int64_t g = (n + kThreads * 8 - 1) / (kThreads * 8);
+  if (g > 1024) g = 1024;
+  if (g < 1) g = 1;
+  char* base = ws_scratch(ws);
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, v, n,
+                     reinterpret_cast<float*>(base), reinterpret_cast<int32_t*>(base + 4096),
+                     ws_counters(ws), out);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int embed_launch(const int8_t* q, const float* s, int32_t V, int32_t D, const int32_t* ids, int32_t n,
+                 float* out, hipStream_t st) {
+  (void)V;
+  if (!q || !s || !ids || !out) return fail(Q35_E_ARG, "embedding: null pointer");
+  if (D <= 0 || (D % 64) != 0 || n < 0) return fail(Q35_E_SHAPE, "embedding: D must be a multiple of 64");
+  if (n == 0) return Q35_OK;
+  const int64_t total = (int64_t)n * (D / 16);
+  int64_t g = (total + kThreads - 1) / kThreads;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, q, s, D, ids, n, out);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+}  // namespace q35

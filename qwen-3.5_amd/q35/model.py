@@ -1,0 +1,98 @@
+"""Whole-model decode driver (model.rs TextForCausalLM + the greedy loop of main.rs:100-132).
+
+The model, its caches and the captured decode-step graph live in libq35.so; this class only
+owns the handle.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib as L
+
+
+class TextForCausalLM:
+    def __init__(self, dims=None, seed=0, tmax=2048):
+        self.dims = dims if dims is not None else L.dims_2b()
+        self.seed, self.tmax = seed, tmax
+        h = ctypes.c_void_p()
+        L.check(L.lib().q35_model_create_synthetic(ctypes.byref(self.dims), seed, tmax, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            L.lib().q35_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        L.check(L.lib().q35_model_reset(self.h, None))
+
+    def set_token(self, token):
+        L.check(L.lib().q35_model_set_token(self.h, int(token), None))
+
+    def step(self, use_graph=True):
+        L.check(L.lib().q35_model_step(self.h, 1 if use_graph else 0, None))
+
+    def generate(self, prompt, n_new, use_graph=True, readback_each=False):
+        """Returns (tokens[n_new+1], decode_seconds): the argmax after the last prompt token,
+        then the argmax after each of n_new decode steps."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.zeros(n_new + 1, np.int32)
+        secs = ctypes.c_double(0.0)
+        L.check(L.lib().q35_model_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data,
+                                           1 if use_graph else 0, 1 if readback_each else 0, ctypes.byref(secs), None))
+        return out, secs.value
+
+    def tensor_ptr(self, name):
+        ptr = ctypes.c_void_p()
+        nbytes = ctypes.c_size_t()
+        L.check(L.lib().q35_model_tensor(self.h, name.encode(), ctypes.byref(ptr), ctypes.byref(nbytes)))
+        return ptr.value, nbytes.value
+
+    def tensor(self, name, dtype, shape=None):
+        """Copy of a model tensor as a numpy array (synchronises the device)."""
+        import torch
+        ptr, nbytes = self.tensor_ptr(name)
+        torch.cuda.synchronize()
+        n = nbytes // np.dtype(dtype).itemsize
+        out = np.empty(n, dtype)
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        rc = hip.hipMemcpy(out.ctypes.data, ctypes.c_void_p(ptr), nbytes, 2)  # hipMemcpyDeviceToHost
+        if rc != 0:
+            raise RuntimeError(f"hipMemcpy failed: {rc}")
+        return out.reshape(shape) if shape is not None else out
+
+
+def synth_model_tensor(dims, seed, name, n):
+    """f32 values the model builder draws for tensor `name` (before Q8F quantisation)."""
+    out = np.empty(n, np.float32)
+    L.check(L.lib().q35_synth_model_tensor(ctypes.byref(dims), seed, name.encode(), out.ctypes.data, n))
+    return out
+
+
+def quantize_q8f(w):
+    """Q8F quantiser of the library (blocks of 64 along the last axis)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty((rows, cols // 64), np.float32)
+    L.check(L.lib().q35_quantize_q8f(w.ctypes.data, rows, cols, q.ctypes.data, s.ctypes.data))
+    return q, s
+
+
+def synth_normal(seed, stream, n, sigma=1.0, offset=0):
+    out = np.empty(n, np.float32)
+    L.check(L.lib().q35_synth_normal(seed, stream, offset, n, sigma, out.ctypes.data))
+    return out
+
+
+def synth_uniform(seed, stream, n, lo, hi, offset=0):
+    out = np.empty(n, np.float32)
+    L.check(L.lib().q35_synth_uniform(seed, stream, offset, n, lo, hi, out.ctypes.data))
+    return out
