@@ -13,9 +13,11 @@
  *     stream-ordered and asynchronous; no entry point synchronises the device.
  *   - The caller owns every buffer.  Entry points that need scratch take `ws`/`ws_bytes`; the
  *     required size comes from the matching *_ws_bytes() query.  A workspace must be zero-filled
- *     once before its first use; every call leaves it zero-filled again on completion, so it can
- *     be reused by later calls on the same stream (calls running concurrently need distinct
- *     workspaces).
+ *     once before its first use and then serve one entry point with one set of sizes (B, tmax):
+ *     every call leaves the parts that must start at zero (completion counters, fixed-point
+ *     split-K accumulators) zero again, so later such calls on the same stream can reuse it.
+ *     The layout depends on the entry point and its sizes (use one workspace per combination,
+ *     or re-zero it), and calls running concurrently need distinct workspaces.
  *   - Return value: Q35_OK or a Q35_E_* code; q35_last_error() gives a message.  Nothing aborts.
  *   - Q8F: int8 two's complement values plus one f32 scale per block of 64 consecutive elements
  *     along the stored matrix's contiguous axis; dequant = f32(q) * scale (kernels.rs:34-43,84-88).
@@ -44,8 +46,13 @@ enum {
  *   Q35_KN: q is [rows=K(in)][cols=N(out)], scale is [K][N/64]  — Burn Linear weight of the
  *           reference projections, blocks along N (kernels.rs:56-57,75-76,87).
  *   Q35_NK: q is [rows=N(out)][cols=K(in)], scale is [N][K/64]  — the tied embedding table
- *           used as lm_head, blocks along K (kernels.rs:253-255,283). */
-enum { Q35_KN = 0, Q35_NK = 1 };
+ *           used as lm_head, blocks along K (kernels.rs:253-255,283).
+ *   Q35_KN_TILED: the Q35_KN matrix (rows=K, cols=N) re-laid out by q35_q8f_pack_kn_tiled into
+ *           256-column tiles stored one after another: q[t][K][256], scale[t][K][4] for
+ *           t < ceil(N/256) (columns past N zero).  Same values, so results are identical to
+ *           Q35_KN; every K-chunk of a tile is one contiguous run of HBM, which is how the
+ *           matvec streams it. */
+enum { Q35_KN = 0, Q35_NK = 1, Q35_KN_TILED = 2 };
 
 typedef struct {
   const int8_t* q;
@@ -210,7 +217,8 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
 
 /* Device pointer and byte size of a named model tensor, named as the reference's module
  * paths: "embed_tokens", "norm", "layers.{i}.input_layernorm", "layers.{i}.linear_attn.in_proj_qkv"
- * (".q" / ".scale" suffix for the Q8F parts), "...conv_state", "...recurrent_state",
+ * (".q" / ".scale" suffix for the Q8F parts; projections are held in the Q35_KN_TILED layout,
+ * the embedding table in Q35_NK), "...conv_state", "...recurrent_state",
  * "layers.{i}.self_attn.k_cache", "logits", "token", "pos", ...  Used by tests and tools. */
 int q35_model_tensor(q35_model* m, const char* name, void** dptr, size_t* bytes);
 
@@ -226,6 +234,12 @@ uint64_t q35_synth_stream_id(const char* name);
 /* Q8F quantiser, blocks of 64 along cols: scale = max|w|/127 (f32), q = round-half-away(w/scale)
  * clamped to [-127,127]; all-zero block -> scale 0.  Replaces the Quantizer of main.rs:175-179. */
 int q35_quantize_q8f(const float* w_host, int64_t rows, int64_t cols, int8_t* q_host, float* scale_host);
+/* Host: element counts of the Q35_KN_TILED form of a K x N Q8F matrix (int8 values, f32 scales). */
+int64_t q35_q8f_tiled_q_count(int32_t K, int32_t N);
+int64_t q35_q8f_tiled_scale_count(int32_t K, int32_t N);
+/* Host: re-lay a Q35_KN matrix (q [K][N], scale [K][N/64]) out as Q35_KN_TILED. */
+int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_tiled_host,
+                          float* scale_tiled_host);
 /* Host copy of the f32 values the model builder draws for a named tensor (before
  * quantisation), so a host-side checker can rebuild the same model. */
 int q35_synth_model_tensor(const q35_dims* d, uint64_t seed, const char* name, float* out_host, int64_t n);

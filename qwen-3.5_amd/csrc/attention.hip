@@ -19,7 +19,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kHd = 256;
 constexpr int kMaxRep = 4;
-constexpr int kMaxChunk = 256;
+constexpr int kMaxChunk = 256;     // tokens per block
+constexpr int kMaxChunks = 1024;   // chunks per (b, kv head): the merge weights live in LDS
 
 struct AttnArgs {
   AttnCall c;
@@ -29,6 +30,12 @@ struct AttnArgs {
   float* part_ml;      // [B*nkv][nchunk][2][kMaxRep]
   float* part_o;       // [B*nkv][nchunk][kMaxRep][hd]
 };
+
+Q35_DEV float4 ld4(const float* f, const fx_t* x, size_t i) {
+  if (x) return make_float4(from_fx(x[i]), from_fx(x[i + 1]), from_fx(x[i + 2]), from_fx(x[i + 3]));
+  return *reinterpret_cast<const float4*>(f + i);
+}
+Q35_DEV float ld1(const float* f, const fx_t* x, size_t i) { return x ? from_fx(x[i]) : f[i]; }
 
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A) {
   const AttnCall& a = A.c;
@@ -58,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
   for (int w = wid; w < rep + (has_new ? 2 : 0); w += 4) {
     if (w < rep) {
       const int hq = g * rep + w;
-      const float4 v = *reinterpret_cast<const float4*>(a.qg + (size_t)b * a.ld_qg + (size_t)hq * 2 * kHd + 4 * lane);
+      const float4 v = ld4(a.qg, a.qg_f, (size_t)b * a.ld_qg + (size_t)hq * 2 * kHd + 4 * lane);
       const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
       const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
       const int d = 4 * lane;
@@ -67,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
       qn[w][d + 2] = (v.z * r) * (1.0f + a.qnw[d + 2]);
       qn[w][d + 3] = (v.w * r) * (1.0f + a.qnw[d + 3]);
     } else if (w == rep) {
-      const float4 v = *reinterpret_cast<const float4*>(a.k + (size_t)b * a.ld_kv + (size_t)g * kHd + 4 * lane);
+      const float4 v = ld4(a.k, a.k_f, (size_t)b * a.ld_kv + (size_t)g * kHd + 4 * lane);
       const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
       const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
       const int d = 4 * lane;
@@ -76,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
       kn[d + 2] = (v.z * r) * (1.0f + a.knw[d + 2]);
       kn[d + 3] = (v.w * r) * (1.0f + a.knw[d + 3]);
     } else {
-      const float4 v = *reinterpret_cast<const float4*>(a.v + (size_t)b * a.ld_kv + (size_t)g * kHd + 4 * lane);
+      const float4 v = ld4(a.v, a.v_f, (size_t)b * a.ld_kv + (size_t)g * kHd + 4 * lane);
       *reinterpret_cast<float4*>(&vn[4 * lane]) = v;
     }
   }
@@ -168,13 +175,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
   for (int h = 0; h < kMaxRep; ++h) o[h] = (ored[0][h][tid] + ored[1][h][tid]) + (ored[2][h][tid] + ored[3][h][tid]);
 
   const int grpi = b * a.nkv + g;
-  const float* gate = a.qg + (size_t)b * a.ld_qg;
+  const size_t gate0 = (size_t)b * a.ld_qg;
   if (nact == 1) {
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h) {
       if (h >= rep) break;
       const int hq = g * rep + h;
-      const float gv = gate[(size_t)hq * 2 * kHd + kHd + tid];
+      const float gv = ld1(a.qg, a.qg_f, gate0 + (size_t)hq * 2 * kHd + kHd + tid);
       a.out[(size_t)b * a.ld_out + (size_t)hq * kHd + tid] = (o[h] / hl[h]) * sigmoid_f(gv);
     }
     return;
@@ -182,22 +189,50 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
   float* pml = A.part_ml + ((size_t)grpi * A.nchunk + c) * 2 * kMaxRep;
   float* po = A.part_o + ((size_t)grpi * A.nchunk + c) * kMaxRep * kHd;
 #pragma unroll
-  for (int h = 0; h < kMaxRep; ++h) if (h < rep) po[h * kHd + tid] = o[h];
-  if (tid < rep) { pml[tid] = hm[tid]; pml[kMaxRep + tid] = hl[tid]; }
+  for (int h = 0; h < kMaxRep; ++h) if (h < rep) st_agent(&po[h * kHd + tid], o[h]);
+  if (tid < rep) { st_agent(&pml[tid], hm[tid]); st_agent(&pml[kMaxRep + tid], hl[tid]); }
   if (!arrive_last(&A.counters[grpi], (uint32_t)nact, &flag)) return;
-  for (int h = 0; h < rep; ++h) {
+  const float* mlg = A.part_ml + (size_t)grpi * A.nchunk * 2 * kMaxRep;
+  const float* og = A.part_o + (size_t)grpi * A.nchunk * kMaxRep * kHd;
+  // Merge: wave h turns the chunk maxima / sums of head h into weights w_c = exp(m_c - M)
+  // (kept in LDS, reusing ored) and the total L; then every thread merges dim `tid` of all heads
+  // in chunk order, 16 chunks of loads in flight.
+  float* wts = &ored[0][0][0];  // [kMaxRep][kMaxChunks]
+  for (int h = wid; h < rep; h += 4) {
     float M = -INFINITY;
-    for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, A.part_ml[((size_t)grpi * A.nchunk + cc) * 2 * kMaxRep + h]);
-    float L = 0.f, O = 0.f;
-    for (int cc = 0; cc < nact; ++cc) {
-      const float* ml = A.part_ml + ((size_t)grpi * A.nchunk + cc) * 2 * kMaxRep;
-      const float w = expf(ml[h] - M);
-      L += ml[kMaxRep + h] * w;
-      O += A.part_o[(((size_t)grpi * A.nchunk + cc) * kMaxRep + h) * kHd + tid] * w;
+    for (int cc = lane; cc < nact; cc += 64) M = fmaxf(M, ld_agent(&mlg[(size_t)cc * 2 * kMaxRep + h]));
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, __shfl_xor(M, o2, 64));
+    float L = 0.f;
+    for (int cc = lane; cc < nact; cc += 64) {
+      const float w = expf(ld_agent(&mlg[(size_t)cc * 2 * kMaxRep + h]) - M);
+      wts[h * kMaxChunks + cc] = w;
+      L += ld_agent(&mlg[(size_t)cc * 2 * kMaxRep + kMaxRep + h]) * w;
     }
+    L = wave_sum(L);
+    if (lane == 0) hl[h] = L;
+  }
+  __syncthreads();
+  float O[kMaxRep] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nact; c0 += 16) {
+    float ov[kMaxRep][16];
+#pragma unroll
+    for (int h = 0; h < kMaxRep; ++h)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        ov[h][j] = (h < rep && c0 + j < nact) ? ld_agent(&og[((size_t)(c0 + j) * kMaxRep + h) * kHd + tid]) : 0.f;
+#pragma unroll
+    for (int h = 0; h < kMaxRep; ++h)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (h < rep && c0 + j < nact) O[h] += ov[h][j] * wts[h * kMaxChunks + c0 + j];
+  }
+#pragma unroll
+  for (int h = 0; h < kMaxRep; ++h) {
+    if (h >= rep) break;
     const int hq = g * rep + h;
-    const float gv = gate[(size_t)hq * 2 * kHd + kHd + tid];
-    a.out[(size_t)b * a.ld_out + (size_t)hq * kHd + tid] = (O / L) * sigmoid_f(gv);
+    const float gv = ld1(a.qg, a.qg_f, gate0 + (size_t)hq * 2 * kHd + kHd + tid);
+    a.out[(size_t)b * a.ld_out + (size_t)hq * kHd + tid] = (O[h] / hl[h]) * sigmoid_f(gv);
   }
 }
 
@@ -233,7 +268,12 @@ size_t attn_ws_bytes(int32_t B, int32_t nh, int32_t nkv, int32_t hd, int32_t tma
 }
 
 int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (!c.qg || !c.k || !c.v || !c.qnw || !c.knw || !c.rcos || !c.rsin || !c.kc || !c.vc || !c.pos || !c.out)
+  if (!ws || ws_bytes < kCounterBytes) return fail(Q35_E_WS, "attention: workspace too small");
+  return attn_launch_split(c, ws_counters(ws), ws_scratch(ws), ws_bytes - kCounterBytes, st);
+}
+
+int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size_t scratch_bytes, hipStream_t st) {
+  if ((!c.qg && !c.qg_f) || (!c.k && !c.k_f) || (!c.v && !c.v_f) || !c.qnw || !c.knw || !c.rcos || !c.rsin || !c.kc || !c.vc || !c.pos || !c.out)
     return fail(Q35_E_ARG, "attention: null pointer");
   if (c.hd != kHd) return fail(Q35_E_SHAPE, "attention: head_dim must be 256");
   if (c.nkv < 1 || c.nh % c.nkv != 0 || c.nh / c.nkv > kMaxRep)
@@ -242,15 +282,15 @@ int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
   if (c.B < 1 || c.tmax < 1) return fail(Q35_E_SHAPE, "attention: B and tmax must be >= 1");
   if (c.B * c.nkv > kMaxCounters) return fail(Q35_E_SHAPE, "attention: B*kv_heads too large");
   AttnLayout L = attn_layout(c.B, c.nkv, c.hd, c.tmax);
-  if (!ws || ws_bytes < L.cnt_bytes + L.ml_bytes + L.o_bytes) return fail(Q35_E_WS, "attention: workspace too small");
+  if (!counters || !scratch || scratch_bytes < L.ml_bytes + L.o_bytes) return fail(Q35_E_WS, "attention: workspace too small");
+  if (L.nchunk > kMaxChunks) return fail(Q35_E_SHAPE, "attention: tmax too large for one merge");
   AttnArgs A;
   A.c = c;
   A.scale = (float)(1.0 / sqrt((double)c.hd));
   A.chunk = L.chunk; A.nchunk = L.nchunk;
-  char* base = static_cast<char*>(ws);
-  A.counters = reinterpret_cast<uint32_t*>(base);
-  A.part_ml = reinterpret_cast<float*>(base + L.cnt_bytes);
-  A.part_o = reinterpret_cast<float*>(base + L.cnt_bytes + L.ml_bytes);
+  A.counters = counters;
+  A.part_ml = reinterpret_cast<float*>(scratch);
+  A.part_o = reinterpret_cast<float*>(scratch + L.ml_bytes);
   const int grid = c.B * c.nkv * L.nchunk;
   hipLaunchKernelGGL(attn_decode_kernel, dim3(grid), dim3(kThreads), 0, st, A);
   Q35_HIP_TRY(hipGetLastError());

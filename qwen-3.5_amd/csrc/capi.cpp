@@ -1,5 +1,10 @@
 // extern "C" entry points for the tensor-level (kernels.rs) and layer-level (text_modules.rs)
 // surface.  Argument checking lives here; kernels assume validated shapes.
+//
+// Workspace layout of every entry point: [completion counters (kCounterBytes)]
+// [fixed-point accumulators][f32 scratch].  Counters and accumulators must be zero when a call
+// starts and are zero again when it completes, so a workspace can be reused by later calls of
+// the same entry point on the same stream.
 #include "q35_host.h"
 
 #include <algorithm>
@@ -17,8 +22,17 @@ int check_q8f(const q35_q8f& W, const char* what) {
   if (!W.q || !W.scale) return fail(Q35_E_ARG, std::string(what) + ": null Q8F pointer");
   if (W.rows < 1 || W.cols < 64 || (W.cols % 64) != 0)
     return fail(Q35_E_SHAPE, std::string(what) + ": Q8F cols must be a positive multiple of 64");
-  if (W.layout != Q35_KN && W.layout != Q35_NK) return fail(Q35_E_ARG, std::string(what) + ": bad layout");
+  if (W.layout != Q35_KN && W.layout != Q35_NK && W.layout != Q35_KN_TILED)
+    return fail(Q35_E_ARG, std::string(what) + ": bad layout");
   if ((reinterpret_cast<uintptr_t>(W.q) & 15) != 0) return fail(Q35_E_ALIGN, std::string(what) + ": q not 16-byte aligned");
+  return Q35_OK;
+}
+
+// Projection weights of the layer entry points: [K][N] storage, row-major or tiled.
+int check_kn(const q35_q8f& W, const char* what) {
+  const int rc = check_q8f(W, what);
+  if (rc) return rc;
+  if (W.layout == Q35_NK) return fail(Q35_E_ARG, std::string(what) + ": projection must be Q35_KN or Q35_KN_TILED");
   return Q35_OK;
 }
 
@@ -29,16 +43,19 @@ int nk_group(int K) {
   return g;
 }
 
-MvSeg seg_of(const q35_q8f& W, float* y, int ldy) { return MvSeg{W.q, W.scale, y, W.cols, ldy}; }
+MvSeg seg_of(const q35_q8f& W, fx_t* acc, int ldacc) {
+  return MvSeg{W.q, W.scale, acc, W.cols, ldacc, W.layout == Q35_KN_TILED ? 1 : 0};
+}
 
-// Bump allocator over the caller's layer workspace (after the kernel scratch).
+// Bump allocator over a workspace region.
 struct Carver {
   char* p;
   size_t left;
-  float* f(size_t n) {
-    const size_t b = align256(n * sizeof(float));
+  template <class T>
+  T* take(size_t n) {
+    const size_t b = align256(n * sizeof(T));
     if (b > left) return nullptr;
-    float* r = reinterpret_cast<float*>(p);
+    T* r = reinterpret_cast<T*>(p);
     p += b; left -= b;
     return r;
   }
@@ -55,33 +72,21 @@ LayerDims ldims(const q35_dims& d) {
   return L;
 }
 
-size_t layer_scratch_bytes(const q35_dims& d, int B, int tmax) {
+// accumulator bytes of the three layer calls (each region 256-byte aligned)
+size_t acc_bytes(const q35_dims& d, int B) {
   const LayerDims L = ldims(d);
-  const int M = std::min(B, 8);
-  size_t m = gdn_step_ws_bytes(B, L.nh);
-  auto mv = [&](int K, std::initializer_list<int> Ns, int aux) {
-    MvCall c;
-    c.K = K; c.M = M; c.nseg = 0;
-    for (int N : Ns) { c.seg[c.nseg].N = N; ++c.nseg; }
-    c.aux_nh = aux;
-    m = std::max(m, mv_kn_ws_bytes(c));
-  };
-  mv(L.H, {L.conv_dim, L.vdim}, L.nh);
-  mv(L.vdim, {L.H}, 0);
-  mv(L.H, {L.ah * L.hd * 2, L.kvh * L.hd, L.kvh * L.hd}, 0);
-  mv(L.ah * L.hd, {L.H}, 0);
-  mv(L.H, {L.F, L.F}, 0);
-  mv(L.F, {L.H}, 0);
-  m = std::max(m, attn_ws_bytes(B, L.ah, L.kvh, L.hd, tmax));
-  return align256(m);
+  auto a = [](size_t n) { return align256(n * sizeof(fx_t)); };
+  const size_t gdn = a((size_t)B * (L.conv_dim + L.vdim)) + a((size_t)B * 2 * L.nh) + a((size_t)B * L.H);
+  const size_t att = a((size_t)B * (L.ah * L.hd * 2 + 2 * L.kvh * L.hd)) + a((size_t)B * L.H);
+  const size_t mlp = a((size_t)B * 2 * L.F) + a((size_t)B * L.H);
+  return std::max(gdn, std::max(att, mlp));
 }
 
-size_t layer_act_floats(const q35_dims& d, int B) {
+size_t scratch_bytes(const q35_dims& d, int B, int tmax) {
   const LayerDims L = ldims(d);
-  size_t gdn = (size_t)B * (L.conv_dim + L.vdim) + 256 + (size_t)B * 2 * L.nh + 256 + (size_t)B * L.vdim + 256;
-  size_t att = (size_t)B * L.ah * L.hd * 2 + 256 + (size_t)B * 2 * L.kvh * L.hd + 256 + (size_t)B * L.ah * L.hd + 256;
-  size_t mlp = (size_t)B * 2 * L.F + 256;
-  return std::max(gdn, std::max(att, mlp)) + 1024;
+  const size_t gdn = align256((size_t)B * L.vdim * 4);
+  const size_t att = (attn_ws_bytes(B, L.ah, L.kvh, L.hd, tmax) - kCounterBytes) + align256((size_t)B * L.ah * L.hd * 4);
+  return std::max(gdn, att);
 }
 
 }  // namespace
@@ -123,10 +128,8 @@ q35_dims q35_dims_qwen35_2b(void) {
 
 size_t q35_q8_gemv_ws_bytes(int32_t M, q35_q8f W) {
   if (W.layout == Q35_NK) return kCounterBytes;
-  MvCall c;
-  c.K = W.rows; c.M = std::max(1, std::min<int>(M, 8)); c.nseg = 1;
-  c.seg[0].N = W.cols;
-  return mv_kn_ws_bytes(c);
+  const int m = std::max(1, std::min<int>(M, 8));
+  return kCounterBytes + align256((size_t)m * W.cols * sizeof(fx_t));
 }
 
 int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream) {
@@ -134,15 +137,17 @@ int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t
   if (rc) return rc;
   if (!x || !y) return fail(Q35_E_ARG, "q8_gemv: null x or y");
   if (M < 1 || M > 64) return fail(Q35_E_SHAPE, "q8_gemv: M must be in [1, 64]");
-  if (W.layout == Q35_KN) {
+  if (W.layout != Q35_NK) {
     const int K = W.rows, N = W.cols;
+    if (!ws || ws_bytes < q35_q8_gemv_ws_bytes(M, W)) return fail(Q35_E_WS, "q8_gemv: workspace too small");
+    fx_t* acc = reinterpret_cast<fx_t*>(ws_scratch(ws));
     for (int m0 = 0; m0 < M; m0 += 8) {
       MvCall c;
       c.K = K; c.M = std::min(8, M - m0); c.nseg = 1;
-      c.seg[0] = seg_of(W, y + (size_t)m0 * N, N);
+      c.seg[0] = seg_of(W, acc, N);
       c.pro = PRO_PLAIN; c.x = x + (size_t)m0 * K; c.ldx = K;
-      rc = mv_kn_launch(c, ws, ws_bytes, S(stream));
-      if (rc) return rc;
+      if ((rc = mv_kn_launch(c, S(stream)))) return rc;
+      if ((rc = fx_to_f32_launch(acc, (int64_t)c.M * N, y + (size_t)m0 * N, true, S(stream)))) return rc;
     }
     return Q35_OK;
   }
@@ -200,7 +205,7 @@ int q35_argmax(const float* logits, int64_t n, int32_t* out, void* ws, size_t ws
 
 size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax) {
   if (!d || B < 1) return 0;
-  return layer_scratch_bytes(*d, B, std::max(1, tmax)) + layer_act_floats(*d, B) * sizeof(float);
+  return kCounterBytes + acc_bytes(*d, B) + scratch_bytes(*d, B, std::max(1, tmax));
 }
 
 int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const float* x, int32_t B,
@@ -211,46 +216,52 @@ int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const
   if (rc) return rc;
   if (B < 1) return fail(Q35_E_SHAPE, "gated_deltanet_decode: B must be >= 1");
   const LayerDims L = ldims(*d);
-  if ((rc = check_q8f(w->in_proj_qkv, "in_proj_qkv")) || (rc = check_q8f(w->in_proj_z, "in_proj_z")) ||
-      (rc = check_q8f(w->out_proj, "out_proj")))
+  if ((rc = check_kn(w->in_proj_qkv, "in_proj_qkv")) || (rc = check_kn(w->in_proj_z, "in_proj_z")) ||
+      (rc = check_kn(w->out_proj, "out_proj")))
     return rc;
   if (w->in_proj_qkv.rows != L.H || w->in_proj_qkv.cols != L.conv_dim || w->in_proj_z.rows != L.H ||
       w->in_proj_z.cols != L.vdim || w->out_proj.rows != L.vdim || w->out_proj.cols != L.H)
     return fail(Q35_E_SHAPE, "gated_deltanet_decode: projection shapes do not match dims");
   if (!w->in_proj_b || !w->in_proj_a || !w->a_log || !w->dt_bias || !w->conv_w || !w->norm_w)
     return fail(Q35_E_ARG, "gated_deltanet_decode: null f32 weight");
-  const size_t scratch = layer_scratch_bytes(*d, B, 1);
   if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, 1)) return fail(Q35_E_WS, "gated_deltanet_decode: workspace too small");
-  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
+  Carver ac{ws_scratch(ws), acc_bytes(*d, B)};
+  Carver sc{ws_scratch(ws) + acc_bytes(*d, B), ws_bytes - kCounterBytes - acc_bytes(*d, B)};
   const int ldq = L.conv_dim + L.vdim;
-  float* qkvz = cv.f((size_t)B * ldq);
-  float* bg = cv.f((size_t)B * 2 * L.nh);
-  float* o = cv.f((size_t)B * L.vdim);
+  fx_t* qkvz = ac.take<fx_t>((size_t)B * ldq);
+  fx_t* ba = ac.take<fx_t>((size_t)B * 2 * L.nh);
+  fx_t* y = ac.take<fx_t>((size_t)B * L.H);
+  float* o = sc.take<float>((size_t)B * L.vdim);
   hipStream_t st = S(stream);
-  for (int b0 = 0; b0 < B; b0 += 8) {  // in_proj_qkv + in_proj_z + gate projection (text_modules.rs:497-508,569-576)
+  for (int b0 = 0; b0 < B; b0 += 8) {  // in_proj_qkv | in_proj_z | in_proj_b,a (text_modules.rs:497-508,569-576)
     MvCall c;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
     c.seg[0] = seg_of(w->in_proj_qkv, qkvz + (size_t)b0 * ldq, ldq);
     c.seg[1] = seg_of(w->in_proj_z, qkvz + (size_t)b0 * ldq + L.conv_dim, ldq);
     c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
-    c.aux_wb = w->in_proj_b; c.aux_wa = w->in_proj_a; c.aux_alog = w->a_log; c.aux_dtb = w->dt_bias;
-    c.aux_nh = L.nh; c.aux_out = bg + (size_t)b0 * 2 * L.nh; c.aux_ldo = 2 * L.nh;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    c.aux_wb = w->in_proj_b; c.aux_wa = w->in_proj_a; c.aux_nh = L.nh;
+    c.aux_acc = ba + (size_t)b0 * 2 * L.nh; c.aux_ldo = 2 * L.nh;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
   GdnCall g;  // conv update, l2norm, recurrent delta rule (:515-530, :627-652)
-  g.qkv = qkvz; g.ld_qkv = ldq; g.bg = bg; g.ld_bg = 2 * L.nh; g.conv_state = conv_state; g.conv_w = w->conv_w;
-  g.S = rec_state; g.o = o; g.ld_o = L.vdim; g.B = B; g.nh = L.nh; g.dk = L.dk; g.dv = L.dv; g.conv_k = d->conv_k;
-  if ((rc = gdn_step_launch(g, ws, scratch, st))) return rc;
-  for (int b0 = 0; b0 < B; b0 += 8) {  // gated RMSNorm + out_proj (:654-663)
+  g.qkv_f = qkvz; g.ld_qkv = ldq; g.ba_f = ba; g.ld_bg = 2 * L.nh; g.a_log = w->a_log; g.dt_bias = w->dt_bias;
+  g.conv_state = conv_state; g.conv_w = w->conv_w; g.S = rec_state; g.o = o; g.ld_o = L.vdim;
+  g.B = B; g.nh = L.nh; g.dk = L.dk; g.dv = L.dv; g.conv_k = d->conv_k;
+  if ((rc = gdn_step_launch(g, st))) return rc;
+  for (int b0 = 0; b0 < B; b0 += 8) {  // gated RMSNorm + out_proj (:654-663); conv state advance
     MvCall c;
     c.K = L.vdim; c.M = std::min(8, B - b0); c.nseg = 1;
-    c.seg[0] = seg_of(w->out_proj, out + (size_t)b0 * L.H, L.H);
+    c.seg[0] = seg_of(w->out_proj, y + (size_t)b0 * L.H, L.H);
     c.pro = PRO_GATED; c.x = o + (size_t)b0 * L.vdim; c.ldx = L.vdim;
-    c.x2 = qkvz + (size_t)b0 * ldq + L.conv_dim; c.ldx2 = ldq;
+    c.x2f = qkvz + (size_t)b0 * ldq + L.conv_dim; c.ldx2 = ldq;
     c.pw = w->norm_w; c.group = L.dv; c.eps = d->eps;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    c.cs_state = conv_state + (size_t)b0 * L.conv_dim * 3; c.cs_x = qkvz + (size_t)b0 * ldq;
+    c.cs_ch = L.conv_dim; c.cs_ldx = ldq; c.cs_B = c.M;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
-  return Q35_OK;
+  if ((rc = fx_to_f32_launch(y, (int64_t)B * L.H, out, true, st))) return rc;
+  if ((rc = fx_zero_launch(qkvz, (int64_t)B * ldq, st))) return rc;
+  return fx_zero_launch(ba, (int64_t)B * 2 * L.nh, st);
 }
 
 int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const float* x, int32_t B, float* k_cache,
@@ -262,44 +273,50 @@ int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const flo
   if (rc) return rc;
   if (B < 1 || tmax < 1) return fail(Q35_E_SHAPE, "attention_decode: B and tmax must be >= 1");
   const LayerDims L = ldims(*d);
-  if ((rc = check_q8f(w->q_proj, "q_proj")) || (rc = check_q8f(w->k_proj, "k_proj")) ||
-      (rc = check_q8f(w->v_proj, "v_proj")) || (rc = check_q8f(w->o_proj, "o_proj")))
+  if ((rc = check_kn(w->q_proj, "q_proj")) || (rc = check_kn(w->k_proj, "k_proj")) ||
+      (rc = check_kn(w->v_proj, "v_proj")) || (rc = check_kn(w->o_proj, "o_proj")))
     return rc;
   if (w->q_proj.rows != L.H || w->q_proj.cols != L.ah * L.hd * 2 || w->k_proj.rows != L.H ||
       w->k_proj.cols != L.kvh * L.hd || w->v_proj.rows != L.H || w->v_proj.cols != L.kvh * L.hd ||
       w->o_proj.rows != L.ah * L.hd || w->o_proj.cols != L.H)
     return fail(Q35_E_SHAPE, "attention_decode: projection shapes do not match dims");
   if (!w->q_norm || !w->k_norm) return fail(Q35_E_ARG, "attention_decode: null norm weight");
-  const size_t scratch = layer_scratch_bytes(*d, B, tmax);
   if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, tmax)) return fail(Q35_E_WS, "attention_decode: workspace too small");
-  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
-  const int ldqg = L.ah * L.hd * 2, ldkv = 2 * L.kvh * L.hd, ldo = L.ah * L.hd;
-  float* qg = cv.f((size_t)B * ldqg);
-  float* kv = cv.f((size_t)B * ldkv);
-  float* att = cv.f((size_t)B * ldo);
+  const size_t abytes = acc_bytes(*d, B);
+  Carver ac{ws_scratch(ws), abytes};
+  const int ldqg = L.ah * L.hd * 2, ldo = L.ah * L.hd, LD = ldqg + 2 * L.kvh * L.hd;
+  fx_t* qkv = ac.take<fx_t>((size_t)B * LD);
+  fx_t* y = ac.take<fx_t>((size_t)B * L.H);
+  // scratch after the accumulators: the attention kernel's chunk partials, then its output
+  const size_t att_ws = attn_ws_bytes(B, L.ah, L.kvh, L.hd, tmax);
+  Carver sc{ws_scratch(ws) + abytes + (att_ws - kCounterBytes), ws_bytes - kCounterBytes - abytes - (att_ws - kCounterBytes)};
+  float* att = sc.take<float>((size_t)B * ldo);
   hipStream_t st = S(stream);
-  for (int b0 = 0; b0 < B; b0 += 8) {  // q_proj, k_proj, v_proj (text_modules.rs:855-893)
+  for (int b0 = 0; b0 < B; b0 += 8) {  // q_proj | k_proj | v_proj (text_modules.rs:855-893)
     MvCall c;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 3;
-    c.seg[0] = seg_of(w->q_proj, qg + (size_t)b0 * ldqg, ldqg);
-    c.seg[1] = seg_of(w->k_proj, kv + (size_t)b0 * ldkv, ldkv);
-    c.seg[2] = seg_of(w->v_proj, kv + (size_t)b0 * ldkv + L.kvh * L.hd, ldkv);
+    c.seg[0] = seg_of(w->q_proj, qkv + (size_t)b0 * LD, LD);
+    c.seg[1] = seg_of(w->k_proj, qkv + (size_t)b0 * LD + ldqg, LD);
+    c.seg[2] = seg_of(w->v_proj, qkv + (size_t)b0 * LD + ldqg + L.kvh * L.hd, LD);
     c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
   AttnCall a;  // norms, RoPE, KV append, attention, gate (:860-936)
-  a.qg = qg; a.ld_qg = ldqg; a.k = kv; a.v = kv + L.kvh * L.hd; a.ld_kv = ldkv; a.qnw = w->q_norm; a.knw = w->k_norm; a.eps = d->eps;
+  a.qg_f = qkv; a.ld_qg = LD; a.k_f = qkv + ldqg; a.v_f = qkv + ldqg + L.kvh * L.hd; a.ld_kv = LD;
+  a.qnw = w->q_norm; a.knw = w->k_norm; a.eps = d->eps;
   a.rcos = rope_cos; a.rsin = rope_sin; a.rot = d->rot_dim; a.kc = k_cache; a.vc = v_cache; a.tmax = tmax;
   a.pos = d_pos; a.out = att; a.ld_out = ldo; a.B = B; a.nh = L.ah; a.nkv = L.kvh; a.hd = L.hd;
-  if ((rc = attn_launch(a, ws, scratch, st))) return rc;
+  // the attention kernel takes [counters | partials]; its partials start right after the accumulators
+  if ((rc = attn_launch_split(a, ws_counters(ws), ws_scratch(ws) + abytes, att_ws - kCounterBytes, st))) return rc;
   for (int b0 = 0; b0 < B; b0 += 8) {  // o_proj (:938-942)
     MvCall c;
     c.K = ldo; c.M = std::min(8, B - b0); c.nseg = 1;
-    c.seg[0] = seg_of(w->o_proj, out + (size_t)b0 * L.H, L.H);
+    c.seg[0] = seg_of(w->o_proj, y + (size_t)b0 * L.H, L.H);
     c.pro = PRO_PLAIN; c.x = att + (size_t)b0 * ldo; c.ldx = ldo;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
-  return Q35_OK;
+  if ((rc = fx_to_f32_launch(y, (int64_t)B * L.H, out, true, st))) return rc;
+  return fx_zero_launch(qkv, (int64_t)B * LD, st);
 }
 
 int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, int32_t B, float* out, void* ws,
@@ -309,38 +326,40 @@ int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, 
   if (rc) return rc;
   if (B < 1) return fail(Q35_E_SHAPE, "mlp_decode: B must be >= 1");
   const LayerDims L = ldims(*d);
-  if ((rc = check_q8f(w->gate_proj, "gate_proj")) || (rc = check_q8f(w->up_proj, "up_proj")) ||
-      (rc = check_q8f(w->down_proj, "down_proj")))
+  if ((rc = check_kn(w->gate_proj, "gate_proj")) || (rc = check_kn(w->up_proj, "up_proj")) ||
+      (rc = check_kn(w->down_proj, "down_proj")))
     return rc;
   if (w->gate_proj.rows != L.H || w->gate_proj.cols != L.F || w->up_proj.rows != L.H || w->up_proj.cols != L.F ||
       w->down_proj.rows != L.F || w->down_proj.cols != L.H)
     return fail(Q35_E_SHAPE, "mlp_decode: projection shapes do not match dims");
-  const size_t scratch = layer_scratch_bytes(*d, B, 1);
   if (!ws || ws_bytes < q35_layer_ws_bytes(d, B, 1)) return fail(Q35_E_WS, "mlp_decode: workspace too small");
-  Carver cv{static_cast<char*>(ws) + scratch, ws_bytes - scratch};
-  float* gu = cv.f((size_t)B * 2 * L.F);
+  Carver ac{ws_scratch(ws), acc_bytes(*d, B)};
+  fx_t* gu = ac.take<fx_t>((size_t)B * 2 * L.F);
+  fx_t* y = ac.take<fx_t>((size_t)B * L.H);
   hipStream_t st = S(stream);
-  for (int b0 = 0; b0 < B; b0 += 8) {  // gate_proj + up_proj (text_modules.rs:1003-1004)
+  for (int b0 = 0; b0 < B; b0 += 8) {  // gate_proj | up_proj (text_modules.rs:1003-1004)
     MvCall c;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
     c.seg[0] = seg_of(w->gate_proj, gu + (size_t)b0 * 2 * L.F, 2 * L.F);
     c.seg[1] = seg_of(w->up_proj, gu + (size_t)b0 * 2 * L.F + L.F, 2 * L.F);
     c.pro = PRO_PLAIN; c.x = x + (size_t)b0 * L.H; c.ldx = L.H;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
   for (int b0 = 0; b0 < B; b0 += 8) {  // up * silu(gate) -> down_proj (:1005)
     MvCall c;
     c.K = L.F; c.M = std::min(8, B - b0); c.nseg = 1;
-    c.seg[0] = seg_of(w->down_proj, out + (size_t)b0 * L.H, L.H);
-    c.pro = PRO_SWIGLU; c.x = gu + (size_t)b0 * 2 * L.F; c.ldx = 2 * L.F; c.swiglu_off = L.F;
-    if ((rc = mv_kn_launch(c, ws, scratch, st))) return rc;
+    c.seg[0] = seg_of(w->down_proj, y + (size_t)b0 * L.H, L.H);
+    c.pro = PRO_SWIGLU; c.xf = gu + (size_t)b0 * 2 * L.F; c.ldx = 2 * L.F; c.swiglu_off = L.F;
+    if ((rc = mv_kn_launch(c, st))) return rc;
   }
-  return Q35_OK;
+  if ((rc = fx_to_f32_launch(y, (int64_t)B * L.H, out, true, st))) return rc;
+  return fx_zero_launch(gu, (int64_t)B * 2 * L.F, st);
 }
 
 int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* beta_g, float* conv_state,
                                 const float* conv_w, float* rec_state, float* core_out, int32_t lin_heads,
                                 int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes, void* stream) {
+  (void)ws; (void)ws_bytes;
   if (!mixed_qkv || !beta_g || !conv_state || !conv_w || !rec_state || !core_out)
     return fail(Q35_E_ARG, "gated_delta_rule_decode: null pointer");
   if (B < 1 || lin_heads < 1) return fail(Q35_E_SHAPE, "gated_delta_rule_decode: B and heads must be >= 1");
@@ -349,7 +368,9 @@ int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* 
   g.qkv = mixed_qkv; g.ld_qkv = conv_dim; g.bg = beta_g; g.ld_bg = 2 * lin_heads; g.conv_state = conv_state;
   g.conv_w = conv_w; g.S = rec_state; g.o = core_out; g.ld_o = lin_heads * lin_dv; g.B = B; g.nh = lin_heads;
   g.dk = lin_dk; g.dv = lin_dv; g.conv_k = 4;
-  return gdn_step_launch(g, ws, ws_bytes, S(stream));
+  int rc = gdn_step_launch(g, S(stream));
+  if (rc) return rc;
+  return conv_shift_launch(conv_state, mixed_qkv, B, conv_dim, S(stream));
 }
 
 int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const float* k_new, const float* v_new,

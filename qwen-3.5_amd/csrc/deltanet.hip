@@ -1,14 +1,16 @@
 // Gated DeltaNet single-token step (text_modules.rs:134-162 causal_conv1d_update,
-// :184-187 l2norm, :365-443 burn_recurrent_gated_delta_rule), one kernel.
+// :184-187 l2norm, :365-443 burn_recurrent_gated_delta_rule), plus the standalone gate
+// projection (kernels.rs:174-247) and the causal-conv state shift.
 //
-// Block (b, head h, 32-column slice of the value dim): 256 threads.  Threads 0..255 run the
-// 4-tap depthwise conv + SiLU for the head's 128 q and 128 k channels, threads 0..31 for the
-// slice's v channels; q and k are L2-normalised in LDS.  Every slice of a head reads the same
-// q/k conv state, so the last slice to finish (per-head counter) advances it; v channels
-// belong to one slice and are advanced directly.  The state slice S[h][0:128][j0:j0+32] (16 KB) is held in registers, 16 rows per
-// thread: decay, S^T k (8-way LDS reduction), delta = (v - S^T k) * beta, rank-1 update,
-// S^T q, write back.  Every value column is independent, so slices need no cross-block
-// reduction; the per-head gated RMSNorm is applied by the out_proj matvec prologue.
+// Step block (b, head h, 32-column slice of the value dim): 256 threads.  Threads 0..255 run
+// the 4-tap depthwise conv + SiLU for the head's 128 q and 128 k channels, threads 0..31 for
+// the slice's v channels; q and k are L2-normalised in LDS.  The state slice
+// S[h][0:128][j0:j0+32] (16 KB) is held in registers, 16 rows per thread: decay, S^T k (8-way
+// LDS reduction), delta = (v - S^T k) * beta, rank-1 update, S^T q, write back.  Every value
+// column is independent, so slices need no cross-block reduction; the per-head gated RMSNorm
+// is applied by the out_proj matvec prologue.  The conv state is only read here (all slices of
+// a head read the same q/k channels); it is advanced afterwards by conv_shift or by a side task
+// of the next matvec launch.
 #include "q35_internal.h"
 
 namespace q35 {
@@ -22,48 +24,51 @@ constexpr int kRowGroups = kThreads / kCS;  // 8
 constexpr int kRowsPerThread = kDk / kRowGroups;  // 16
 
 struct GdnArgs {
-  const float* qkv; int32_t ld_qkv;
-  const float* bg; int32_t ld_bg;
-  float* conv_state; const float* conv_w;
-  float* S;
-  float* o; int32_t ld_o;
-  uint32_t* counters;  // [B*nh], zero between launches
-  int32_t nh, dv, conv_dim, key_dim, nslice;
+  GdnCall c;
+  int32_t conv_dim, key_dim, nslice;
   float qscale;
 };
 
-Q35_DEV float conv4_silu(const float* x, int c, float* st, const float* w, bool advance) {
-  const float xin = x[c];
-  const float s0 = st[0], s1 = st[1], s2 = st[2];
-  const float acc = ((w[0] * s0 + w[1] * s1) + w[2] * s2) + w[3] * xin;
-  if (advance) { st[0] = s1; st[1] = s2; st[2] = xin; }
+Q35_DEV float qkv_at(const GdnCall& c, int b, int ch) {
+  const size_t i = (size_t)b * c.ld_qkv + ch;
+  return c.qkv_f ? from_fx(c.qkv_f[i]) : c.qkv[i];
+}
+
+Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
+  const float acc = ((w[0] * st[0] + w[1] * st[1]) + w[2] * st[2]) + w[3] * xin;
   return silu_f(acc);
 }
 
-__global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs a) {
+__global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
+  const GdnCall& a = A.c;
   __shared__ float qk[2 * kDk];
   __shared__ float qh[kDk];
   __shared__ float kh[kDk];
   __shared__ float vv[kCS];
   __shared__ float wsum[4];
   __shared__ float red[kRowGroups * kCS];
-  __shared__ int flag;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int slice = blockIdx.x % a.nslice;
-  const int h = (blockIdx.x / a.nslice) % a.nh;
-  const int b = blockIdx.x / (a.nslice * a.nh);
-  const float* x = a.qkv + (size_t)b * a.ld_qkv;
-  float* cs = a.conv_state + (size_t)b * a.conv_dim * 3;
+  const int slice = blockIdx.x % A.nslice;
+  const int h = (blockIdx.x / A.nslice) % a.nh;
+  const int b = blockIdx.x / (A.nslice * a.nh);
+  const float* cs = a.conv_state + (size_t)b * A.conv_dim * 3;
 
-  // q (tid < 128) and k (tid >= 128) channels of head h; state advanced at the end
-  const int cqk = (tid < kDk) ? h * kDk + tid : a.key_dim + h * kDk + (tid - kDk);
-  float* stqk = cs + (size_t)cqk * 3;
-  const float xq = x[cqk], q1 = stqk[1], q2 = stqk[2];
-  qk[tid] = conv4_silu(x, cqk, stqk, a.conv_w + (size_t)cqk * 4, false);
+  // state slice loads first: their latency overlaps the conv / norm work
+  const int j = tid % kCS, ig = tid / kCS;
+  const int i0 = ig * kRowsPerThread;
+  float* Sp = a.S + (((size_t)b * a.nh + h) * kDk) * a.dv + slice * kCS + j;
+  float sr[kRowsPerThread];
+#pragma unroll
+  for (int r = 0; r < kRowsPerThread; ++r) sr[r] = Sp[(size_t)(i0 + r) * a.dv];
+
+  {  // q (tid < 128) and k (tid >= 128) channels of head h
+    const int c = (tid < kDk) ? h * kDk + tid : A.key_dim + h * kDk + (tid - kDk);
+    qk[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
+  }
   if (tid < kCS) {
-    const int c = 2 * a.key_dim + h * a.dv + slice * kCS + tid;
-    vv[tid] = conv4_silu(x, c, cs + (size_t)c * 3, a.conv_w + (size_t)c * 4, true);
+    const int c = 2 * A.key_dim + h * a.dv + slice * kCS + tid;
+    vv[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
   }
   __syncthreads();
   {
@@ -74,18 +79,26 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs a) {
   __syncthreads();
   const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
   const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
-  if (tid < kDk) qh[tid] = (qk[tid] * rq) * a.qscale;
+  if (tid < kDk) qh[tid] = (qk[tid] * rq) * A.qscale;
   else kh[tid - kDk] = qk[tid] * rk;
+
+  float beta, g;
+  if (a.ba_f) {  // raw projections: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias)
+    const float bs = from_fx(a.ba_f[(size_t)b * a.ld_bg + h]);
+    const float as = from_fx(a.ba_f[(size_t)b * a.ld_bg + a.nh + h]);
+    beta = 1.0f / (1.0f + expf(-bs));
+    const float xg = as + a.dt_bias[h];
+    const float pre = logf(expf(xg) + 1.0f);
+    g = -expf(a.a_log[h]) * (pre > 20.0f ? xg : pre);
+  } else {
+    beta = a.bg[(size_t)b * a.ld_bg + h];
+    g = a.bg[(size_t)b * a.ld_bg + a.nh + h];
+  }
+  const float decay = expf(g);
   __syncthreads();
 
-  const float beta = a.bg[(size_t)b * a.ld_bg + h];
-  const float decay = expf(a.bg[(size_t)b * a.ld_bg + a.nh + h]);
-  const int j = tid % kCS, ig = tid / kCS;
-  const int i0 = ig * kRowsPerThread;
-  float* Sp = a.S + (((size_t)b * a.nh + h) * kDk) * a.dv + slice * kCS + j;
-  float sr[kRowsPerThread];
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) sr[r] = Sp[(size_t)(i0 + r) * a.dv] * decay;
+  for (int r = 0; r < kRowsPerThread; ++r) sr[r] = sr[r] * decay;
   float mp = 0.f;
 #pragma unroll
   for (int r = 0; r < kRowsPerThread; ++r) mp += sr[r] * kh[i0 + r];
@@ -111,14 +124,19 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs a) {
     for (int i = 0; i < kRowGroups; ++i) o += red[i * kCS + j];
     a.o[(size_t)b * a.ld_o + h * a.dv + slice * kCS + j] = o;
   }
-  if (a.nslice == 1 || arrive_last(&a.counters[b * a.nh + h], (uint32_t)a.nslice, &flag)) {
-    stqk[0] = q1; stqk[1] = q2; stqk[2] = xq;
+}
+
+__global__ __launch_bounds__(kThreads) void conv_shift_kernel(float* state, const float* x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    float* st = state + i * 3;
+    const float s1 = st[1], s2 = st[2];
+    st[0] = s1; st[1] = s2; st[2] = x[i];
   }
 }
 
-// Standalone gate projection (kernels.rs:174-247): one block per batch row; thread t owns
-// output t % (2*nh) and a strided subset of the input rows, partial sums are reduced in LDS in
-// a fixed order, then sigmoid / -exp(A_log)*softplus are applied.
+// Standalone gate projection: one block per batch row; thread t owns output t % (2*nh) and a
+// strided subset of the input rows, partial sums are reduced in LDS in a fixed order, then
+// sigmoid / -exp(A_log)*softplus are applied.
 __global__ __launch_bounds__(kThreads) void gate_proj_kernel(const float* x, int32_t in_dim, const float* wb,
                                                             const float* wa, const float* alog, const float* dtb,
                                                             int32_t nh, float* out) {
@@ -159,25 +177,32 @@ int gate_proj_simple_launch(const float* x, int32_t B, int32_t in_dim, const flo
   return Q35_OK;
 }
 
-size_t gdn_step_ws_bytes(int32_t B, int32_t nh) { (void)B; (void)nh; return kCounterBytes; }
-
-int gdn_step_launch(const GdnCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (!c.qkv || !c.bg || !c.conv_state || !c.conv_w || !c.S || !c.o) return fail(Q35_E_ARG, "gdn_step: null pointer");
-  if (!ws || ws_bytes < gdn_step_ws_bytes(c.B, c.nh)) return fail(Q35_E_WS, "gdn_step: workspace too small");
+int gdn_step_launch(const GdnCall& c, hipStream_t st) {
+  if ((!c.qkv && !c.qkv_f) || !c.conv_state || !c.conv_w || !c.S || !c.o) return fail(Q35_E_ARG, "gdn_step: null pointer");
+  if (!c.bg && !(c.ba_f && c.a_log && c.dt_bias)) return fail(Q35_E_ARG, "gdn_step: need bg, or ba_f with a_log and dt_bias");
   if (c.dk != kDk) return fail(Q35_E_SHAPE, "gdn_step: key head dim must be 128");
   if (c.dv <= 0 || (c.dv % kCS) != 0) return fail(Q35_E_SHAPE, "gdn_step: value head dim must be a multiple of 32");
   if (c.conv_k != 4) return fail(Q35_E_SHAPE, "gdn_step: conv kernel must be 4");
   if (c.B < 1 || c.nh < 1) return fail(Q35_E_SHAPE, "gdn_step: B and heads must be >= 1");
-  if (c.B * c.nh > kMaxCounters) return fail(Q35_E_SHAPE, "gdn_step: B*heads too large");
   GdnArgs a;
-  a.qkv = c.qkv; a.ld_qkv = c.ld_qkv; a.bg = c.bg; a.ld_bg = c.ld_bg;
-  a.conv_state = c.conv_state; a.conv_w = c.conv_w; a.S = c.S; a.o = c.o; a.ld_o = c.ld_o;
-  a.counters = ws_counters(ws);
-  a.nh = c.nh; a.dv = c.dv; a.key_dim = c.nh * c.dk; a.conv_dim = 2 * a.key_dim + c.nh * c.dv;
+  a.c = c;
+  a.key_dim = c.nh * c.dk;
+  a.conv_dim = 2 * a.key_dim + c.nh * c.dv;
   a.nslice = c.dv / kCS;
   a.qscale = powf((float)c.dk, -0.5f);
   const int grid = c.B * c.nh * a.nslice;
   hipLaunchKernelGGL(gdn_step_kernel, dim3(grid), dim3(kThreads), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int conv_shift_launch(float* state, const float* x, int32_t B, int32_t ch, hipStream_t st) {
+  if (!state || !x) return fail(Q35_E_ARG, "conv_shift: null pointer");
+  const int64_t n = (int64_t)B * ch;
+  if (n <= 0) return Q35_OK;
+  int64_t g = (n + kThreads - 1) / kThreads;
+  if (g > 1024) g = 1024;
+  hipLaunchKernelGGL(conv_shift_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, state, x, n);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

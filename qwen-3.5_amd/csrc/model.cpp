@@ -3,11 +3,16 @@
 //
 // One decode step (TextForCausalLM::forward at seq_len 1, model.rs:27-84,113-129, plus the
 // greedy argmax of main.rs:131) is 5 launches per layer + 1:
-//   linear-attention layer: [input RMSNorm -> in_proj_qkv|in_proj_z|gate-proj]  -> DeltaNet step
-//                           -> [gated RMSNorm -> out_proj -> +residual]
+//   linear-attention layer: [input RMSNorm -> in_proj_qkv|in_proj_z|in_proj_b,a] -> DeltaNet step
+//                           -> [gated RMSNorm -> out_proj -> +residual; conv-state shift]
 //   full-attention layer:   [input RMSNorm -> q|k|v proj] -> attention -> [o_proj -> +residual]
 //   MLP:                    [post RMSNorm -> gate|up] -> [SwiGLU -> down -> +residual]
 //   head:                   [final RMSNorm -> lm_head -> argmax -> token, pos += 1]
+// Matvec outputs are fixed-point accumulators (see fx_add); the residual stream h is one too, so
+// residual adds are the projections' own atomics.  Accumulator hygiene: the q|k|v(|z) and gate
+// accumulators are zero when a step starts; the gate|up launch clears the projection
+// accumulators (read for the last time by the launch before it) and the next layer's first
+// launch clears the gate|up accumulator (last read by down_proj).
 // The token, the position, the prompt and the token history live in device memory, so the
 // captured graph is replayed unchanged for every prompt token and every generated token.
 #include "q35_host.h"
@@ -38,8 +43,12 @@ struct q35_model {
   Q8 embed{};
   const float* final_norm = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
-  float *h = nullptr, *qkvz = nullptr, *bg = nullptr, *o_raw = nullptr, *gu = nullptr;
-  float *qg = nullptr, *kvb = nullptr, *attn = nullptr, *logits = nullptr;
+  q35::fx_t* h = nullptr;         // residual stream [hidden]
+  q35::fx_t* acc_proj = nullptr;  // q|k|v|z (linear) or q|k|v (full) projection outputs
+  q35::fx_t* acc_ba = nullptr;    // raw in_proj_b | in_proj_a sums [2*lin_heads]
+  q35::fx_t* acc_gu = nullptr;    // gate | up [2*ffn]
+  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr;
+  int64_t acc_proj_n = 0;
   int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr;
   int32_t* pinned = nullptr;
   void* ws = nullptr;
@@ -78,11 +87,13 @@ int launch_step(q35_model* m, hipStream_t st) {
   const int nh = d.lin_heads, dk = d.lin_dk, dv = d.lin_dv;
   const int key_dim = nh * dk, vdim = nh * dv, conv_dim = 2 * key_dim + vdim, ldq = conv_dim + vdim;
   const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  const int ldqg = ah * hd * 2, LDa = ldqg + 2 * kvh * hd;
   int rc;
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
     MvCall c;
-    c.K = H; c.M = 1; c.x = m->h; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps;
+    c.K = H; c.M = 1; c.xf = m->h; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps;
+    c.zero_ptr = m->acc_gu; c.zero_n = 2 * (int64_t)F;
     if (l == 0) {
       c.pro = PRO_EMBED_RMS;
       c.emb_q = m->embed.q; c.emb_s = m->embed.s; c.token = m->token; c.h_out = m->h;
@@ -92,81 +103,65 @@ int launch_step(q35_model* m, hipStream_t st) {
     }
     if (!L.full) {
       c.nseg = 2;
-      c.seg[0] = MvSeg{L.qkv.q, L.qkv.s, m->qkvz, conv_dim, ldq};
-      c.seg[1] = MvSeg{L.z.q, L.z.s, m->qkvz + conv_dim, vdim, ldq};
-      c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_alog = L.a_log; c.aux_dtb = L.dt_bias;
-      c.aux_nh = nh; c.aux_out = m->bg; c.aux_ldo = 2 * nh;
-      if ((rc = mv_kn_launch(c, m->ws, m->ws_bytes, st))) return rc;
+      c.seg[0] = MvSeg{L.qkv.q, L.qkv.s, m->acc_proj, conv_dim, ldq, 1};
+      c.seg[1] = MvSeg{L.z.q, L.z.s, m->acc_proj + conv_dim, vdim, ldq, 1};
+      c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = m->acc_ba; c.aux_ldo = 2 * nh;
+      if ((rc = mv_kn_launch(c, st))) return rc;
       GdnCall g;
-      g.qkv = m->qkvz; g.ld_qkv = ldq; g.bg = m->bg; g.ld_bg = 2 * nh; g.conv_state = L.conv_state;
-      g.conv_w = L.conv_w; g.S = L.rec; g.o = m->o_raw; g.ld_o = vdim; g.B = 1; g.nh = nh; g.dk = dk; g.dv = dv;
-      g.conv_k = d.conv_k;
-      if ((rc = gdn_step_launch(g, m->ws, m->ws_bytes, st))) return rc;
+      g.qkv_f = m->acc_proj; g.ld_qkv = ldq; g.ba_f = m->acc_ba; g.ld_bg = 2 * nh; g.a_log = L.a_log;
+      g.dt_bias = L.dt_bias; g.conv_state = L.conv_state; g.conv_w = L.conv_w; g.S = L.rec; g.o = m->o_raw;
+      g.ld_o = vdim; g.B = 1; g.nh = nh; g.dk = dk; g.dv = dv; g.conv_k = d.conv_k;
+      if ((rc = gdn_step_launch(g, st))) return rc;
       MvCall c2;
       c2.K = vdim; c2.M = 1; c2.nseg = 1;
-      c2.seg[0] = MvSeg{L.out.q, L.out.s, m->h, H, H};
-      c2.pro = PRO_GATED; c2.x = m->o_raw; c2.ldx = vdim; c2.x2 = m->qkvz + conv_dim; c2.ldx2 = ldq;
-      c2.pw = L.norm_w; c2.group = dv; c2.eps = d.eps; c2.epi = EPI_RESID;
-      if ((rc = mv_kn_launch(c2, m->ws, m->ws_bytes, st))) return rc;
+      c2.seg[0] = MvSeg{L.out.q, L.out.s, m->h, H, H, 1};
+      c2.pro = PRO_GATED; c2.x = m->o_raw; c2.ldx = vdim; c2.x2f = m->acc_proj + conv_dim; c2.ldx2 = ldq;
+      c2.pw = L.norm_w; c2.group = dv; c2.eps = d.eps;
+      c2.cs_state = L.conv_state; c2.cs_x = m->acc_proj; c2.cs_ch = conv_dim; c2.cs_ldx = ldq; c2.cs_B = 1;
+      if ((rc = mv_kn_launch(c2, st))) return rc;
     } else {
       c.nseg = 3;
-      c.seg[0] = MvSeg{L.q.q, L.q.s, m->qg, ah * hd * 2, ah * hd * 2};
-      c.seg[1] = MvSeg{L.k.q, L.k.s, m->kvb, kvh * hd, 2 * kvh * hd};
-      c.seg[2] = MvSeg{L.v.q, L.v.s, m->kvb + kvh * hd, kvh * hd, 2 * kvh * hd};
-      if ((rc = mv_kn_launch(c, m->ws, m->ws_bytes, st))) return rc;
+      c.seg[0] = MvSeg{L.q.q, L.q.s, m->acc_proj, ldqg, LDa, 1};
+      c.seg[1] = MvSeg{L.k.q, L.k.s, m->acc_proj + ldqg, kvh * hd, LDa, 1};
+      c.seg[2] = MvSeg{L.v.q, L.v.s, m->acc_proj + ldqg + kvh * hd, kvh * hd, LDa, 1};
+      if ((rc = mv_kn_launch(c, st))) return rc;
       AttnCall a;
-      a.qg = m->qg; a.ld_qg = ah * hd * 2; a.k = m->kvb; a.v = m->kvb + kvh * hd; a.ld_kv = 2 * kvh * hd;
-      a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
+      a.qg_f = m->acc_proj; a.ld_qg = LDa; a.k_f = m->acc_proj + ldqg; a.v_f = m->acc_proj + ldqg + kvh * hd;
+      a.ld_kv = LDa; a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
       a.rcos = m->rope_cos; a.rsin = m->rope_sin; a.rot = d.rot_dim;
       a.kc = L.kc; a.vc = L.vc; a.tmax = m->tmax; a.pos = m->pos;
       a.out = m->attn; a.ld_out = ah * hd; a.B = 1; a.nh = ah; a.nkv = kvh; a.hd = hd;
       if ((rc = attn_launch(a, m->ws, m->ws_bytes, st))) return rc;
       MvCall c2;
       c2.K = ah * hd; c2.M = 1; c2.nseg = 1;
-      c2.seg[0] = MvSeg{L.o.q, L.o.s, m->h, H, H};
-      c2.pro = PRO_PLAIN; c2.x = m->attn; c2.ldx = ah * hd; c2.epi = EPI_RESID;
-      if ((rc = mv_kn_launch(c2, m->ws, m->ws_bytes, st))) return rc;
+      c2.seg[0] = MvSeg{L.o.q, L.o.s, m->h, H, H, 1};
+      c2.pro = PRO_PLAIN; c2.x = m->attn; c2.ldx = ah * hd;
+      if ((rc = mv_kn_launch(c2, st))) return rc;
     }
     MvCall c3;
     c3.K = H; c3.M = 1; c3.nseg = 2;
-    c3.seg[0] = MvSeg{L.gate.q, L.gate.s, m->gu, F, 2 * F};
-    c3.seg[1] = MvSeg{L.up.q, L.up.s, m->gu + F, F, 2 * F};
-    c3.pro = PRO_RMS; c3.x = m->h; c3.ldx = H; c3.pw = L.post_norm; c3.eps = d.eps;
-    if ((rc = mv_kn_launch(c3, m->ws, m->ws_bytes, st))) return rc;
+    c3.seg[0] = MvSeg{L.gate.q, L.gate.s, m->acc_gu, F, 2 * F, 1};
+    c3.seg[1] = MvSeg{L.up.q, L.up.s, m->acc_gu + F, F, 2 * F, 1};
+    c3.pro = PRO_RMS; c3.xf = m->h; c3.ldx = H; c3.pw = L.post_norm; c3.eps = d.eps;
+    c3.zero_ptr = m->acc_proj; c3.zero_n = m->acc_proj_n + 2 * nh;  // acc_ba follows acc_proj
+    if ((rc = mv_kn_launch(c3, st))) return rc;
     MvCall c4;
     c4.K = F; c4.M = 1; c4.nseg = 1;
-    c4.seg[0] = MvSeg{L.down.q, L.down.s, m->h, H, H};
-    c4.pro = PRO_SWIGLU; c4.x = m->gu; c4.ldx = 2 * F; c4.swiglu_off = F; c4.epi = EPI_RESID;
-    if ((rc = mv_kn_launch(c4, m->ws, m->ws_bytes, st))) return rc;
+    c4.seg[0] = MvSeg{L.down.q, L.down.s, m->h, H, H, 1};
+    c4.pro = PRO_SWIGLU; c4.xf = m->acc_gu; c4.ldx = 2 * F; c4.swiglu_off = F;
+    if ((rc = mv_kn_launch(c4, st))) return rc;
   }
   NkCall n;
   n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = 1;
-  n.x = m->h; n.ldx = H; n.y = m->logits; n.ldy = d.vocab; n.pro = PRO_RMS; n.pw = m->final_norm; n.eps = d.eps;
+  n.xf = m->h; n.ldx = H; n.y = m->logits; n.ldy = d.vocab; n.pro = PRO_RMS; n.pw = m->final_norm; n.eps = d.eps;
   n.argmax_out = m->token; n.pos_inc = m->pos; n.hist = m->hist;
   return nk_launch(n, m->ws, m->ws_bytes, st);
 }
 
 size_t model_ws_bytes(const q35_dims& d, int tmax) {
-  const int H = d.hidden, F = d.ffn;
-  const int nh = d.lin_heads, vdim = nh * d.lin_dv, conv_dim = 2 * nh * d.lin_dk + vdim;
-  const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
-  size_t m = gdn_step_ws_bytes(1, nh);
-  auto mv = [&](int K, std::initializer_list<int> Ns, int aux) {
-    MvCall c;
-    c.K = K; c.M = 1; c.nseg = 0;
-    for (int N : Ns) { c.seg[c.nseg].N = N; ++c.nseg; }
-    c.aux_nh = aux;
-    m = std::max(m, mv_kn_ws_bytes(c));
-  };
-  mv(H, {conv_dim, vdim}, nh);
-  mv(vdim, {H}, 0);
-  mv(H, {ah * hd * 2, kvh * hd, kvh * hd}, 0);
-  mv(ah * hd, {H}, 0);
-  mv(H, {F, F}, 0);
-  mv(F, {H}, 0);
-  m = std::max(m, attn_ws_bytes(1, ah, kvh, hd, tmax));
+  size_t m = attn_ws_bytes(1, d.attn_heads, d.kv_heads, d.head_dim, tmax);
   NkCall n;
-  n.N = d.vocab; n.K = H;
+  n.N = d.vocab; n.K = d.hidden;
   m = std::max(m, nk_ws_bytes(n));
   return align256(m);
 }
@@ -233,6 +228,8 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
   std::vector<float> host;
   std::vector<int8_t> hq;
   std::vector<float> hs;
+  std::vector<int8_t> tq;
+  std::vector<float> ts;
   for (const TensorSpec& t : model_specs(d)) {
     const size_t n = (size_t)t.rows * t.cols;
     host.resize(n);
@@ -245,17 +242,31 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
       hq.resize(n);
       hs.resize(n / 64);
       quantize_q8f(host.data(), t.rows, t.cols, hq.data(), hs.data());
+      size_t nq = n, ns = n / 64;
+      if (t.kind == kQ8KN) {
+        // projections are stored tile-major (Q35_KN_TILED) so that each split-K block of the
+        // matvec streams one contiguous run of HBM
+        nq = (size_t)q35_q8f_tiled_q_count((int32_t)t.rows, (int32_t)t.cols);
+        ns = (size_t)q35_q8f_tiled_scale_count((int32_t)t.rows, (int32_t)t.cols);
+        tq.resize(nq);
+        ts.resize(ns);
+        pack_kn_tiled(hq.data(), hs.data(), t.rows, t.cols, tq.data(), ts.data());
+      }
+      const int8_t* srcq = t.kind == kQ8KN ? tq.data() : hq.data();
+      const float* srcs = t.kind == kQ8KN ? ts.data() : hs.data();
       int8_t* pq; float* ps;
-      if ((rc = dev_alloc_t(m, t.name + ".q", n, &pq))) return bail(rc);
-      if ((rc = dev_alloc_t(m, t.name + ".scale", n / 64, &ps))) return bail(rc);
-      if (hipMemcpy(pq, hq.data(), n, hipMemcpyHostToDevice) != hipSuccess ||
-          hipMemcpy(ps, hs.data(), n / 64 * 4, hipMemcpyHostToDevice) != hipSuccess)
+      if ((rc = dev_alloc_t(m, t.name + ".q", nq, &pq))) return bail(rc);
+      if ((rc = dev_alloc_t(m, t.name + ".scale", ns, &ps))) return bail(rc);
+      if (hipMemcpy(pq, srcq, nq, hipMemcpyHostToDevice) != hipSuccess ||
+          hipMemcpy(ps, srcs, ns * 4, hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(Q35_E_HIP, "upload " + t.name));
     }
   }
   std::vector<float>().swap(host);
   std::vector<int8_t>().swap(hq);
   std::vector<float>().swap(hs);
+  std::vector<int8_t>().swap(tq);
+  std::vector<float>().swap(ts);
   auto f32 = [&](const std::string& n) { return static_cast<const float*>(m->tensors.at(n).p); };
   auto q8 = [&](const std::string& n, int rows, int cols) {
     return q35_model::Q8{static_cast<const int8_t*>(m->tensors.at(n + ".q").p), f32(n + ".scale"), rows, cols};
@@ -307,10 +318,16 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
       return bail(fail(Q35_E_HIP, "upload rope tables"));
   }
   // activations, control scalars, workspace
-  if ((rc = dev_alloc_t(m, "h", H, &m->h)) || (rc = dev_alloc_t(m, "qkvz", conv_dim + vdim, &m->qkvz)) ||
-      (rc = dev_alloc_t(m, "bg", 2 * nh, &m->bg)) || (rc = dev_alloc_t(m, "o_raw", vdim, &m->o_raw)) ||
-      (rc = dev_alloc_t(m, "gu", 2 * F, &m->gu)) || (rc = dev_alloc_t(m, "qg", ah * hd * 2, &m->qg)) ||
-      (rc = dev_alloc_t(m, "kv", 2 * kvh * hd, &m->kvb)) || (rc = dev_alloc_t(m, "attn", ah * hd, &m->attn)) ||
+  const int64_t proj_n = std::max<int64_t>(conv_dim + vdim, (int64_t)ah * hd * 2 + 2 * kvh * hd);
+  m->acc_proj_n = proj_n;
+  {  // acc_ba directly follows acc_proj so one side task clears both
+    fx_t* both = nullptr;
+    if ((rc = dev_alloc_t(m, "acc_proj", (size_t)(proj_n + 2 * nh), &both))) return bail(rc);
+    m->acc_proj = both;
+    m->acc_ba = both + proj_n;
+  }
+  if ((rc = dev_alloc_t(m, "h", H, &m->h)) || (rc = dev_alloc_t(m, "acc_gu", 2 * F, &m->acc_gu)) ||
+      (rc = dev_alloc_t(m, "o_raw", vdim, &m->o_raw)) || (rc = dev_alloc_t(m, "attn", ah * hd, &m->attn)) ||
       (rc = dev_alloc_t(m, "logits", d.vocab, &m->logits)) || (rc = dev_alloc_t(m, "token", 1, &m->token)) ||
       (rc = dev_alloc_t(m, "pos", 1, &m->pos)) || (rc = dev_alloc_t(m, "prompt", tmax, &m->prompt)) ||
       (rc = dev_alloc_t(m, "plen", 1, &m->plen)) || (rc = dev_alloc_t(m, "hist", tmax, &m->hist)))
@@ -340,7 +357,8 @@ int q35_model_reset(q35_model* m, void* stream) {
     const std::string& n = kv.first;
     const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
                        n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
-                       n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt";
+                       n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt" ||
+                       n == "h" || n == "acc_proj" || n == "acc_gu";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
   m->host_pos = 0;

@@ -3,14 +3,15 @@
 // (kernels.rs:298-371) fused into its epilogue, the standalone argmax and the embedding
 // lookup (kernels.rs:15-45).
 //
-// lm_head decomposition: each wave owns 4 rows per step; lane l reads 16-byte chunks
-// k = 16*(l + 64c) of every row, so a wave reads 1 KB contiguous per row per chunk.  x (after
-// the optional final RMSNorm) is staged once per block in LDS.  The 4 row partials of a lane
-// are folded with a transposed butterfly (xor 32, xor 16 exchange halves of the row set,
-// xor 8..1 finish the sum), 7 lane exchanges per 4 rows.  Blocks stride over row groups.
-// The argmax keeps (max, lowest index) per lane -> wave -> block; the last block to finish
-// reduces the block results; (max, lowest index) is a total order so the result does not
-// depend on the reduction order.
+// lm_head decomposition: each wave owns R rows per step; lane l reads the 16-byte chunks
+// k = 16*(l + 64c), c < CPW = K/1024, of every row, so a wave reads 1 KB contiguous per row per
+// chunk and keeps R*CPW loads (16 for K = 2048) in flight per lane.  x (after the optional final
+// RMSNorm) is staged once per block in LDS.  The R row partials of a lane are folded with a
+// transposed butterfly (each xor stage exchanges half of the remaining rows, then the lanes
+// sharing a row finish the sum): log2(R) + log2(64/R) exchanges for R rows.  Blocks stride over
+// row groups.  The argmax keeps (max, lowest index) per lane -> wave -> block; the last block
+// to finish reduces the block results; (max, lowest index) is a total order, so the result
+// does not depend on the reduction order.
 #include "q35_internal.h"
 #include <climits>
 
@@ -19,23 +20,48 @@ namespace q35 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 4;
-constexpr int kRowsPerBlock = 16;
 constexpr int kMaxCpw = 8;        // 16-byte chunks per lane per row: K <= 8192
 constexpr int kMaxGrid = 2048;
 constexpr int kLdsFloats = 12288; // MR*K staged floats (48 KB)
 
+// rows per wave per step: 16 loads in flight per lane
+template <int CPW> constexpr int kRowsPerWave = CPW >= 8 ? 2 : (CPW >= 4 ? 4 : 8);
+
 struct NkArgs {
   const int8_t* q; const float* s;
   int32_t N, K, M;
-  const float* x; int32_t ldx;
+  const float* x; const fx_t* xf; int32_t ldx;
   float* y; int32_t ldy;
   int32_t pro; const float* pw; float eps;
   int32_t* argmax_out; int32_t* pos_inc; int32_t* hist;
   float* part_v; int32_t* part_i; uint32_t* counter;
 };
 
+Q35_DEV float nk_in(const NkArgs& a, int m, int k) {
+  const size_t i = (size_t)m * a.ldx + k;
+  return a.xf ? from_fx(a.xf[i]) : a.x[i];
+}
+
 Q35_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+// (max, lowest index) over the n published block results, 8 loads in flight per thread.
+Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& v, int& i) {
+  v = -INFINITY;
+  i = INT_MAX;
+  for (int b0 = threadIdx.x; b0 < n; b0 += 8 * kThreads) {
+    float vv[8];
+    int ii[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int b = b0 + j * kThreads;
+      vv[j] = (b < n) ? ld_agent(&pv[b]) : -INFINITY;
+      ii[j] = (b < n) ? ld_agent(&pi[b]) : INT_MAX;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (better(vv[j], ii[j], v, i)) { v = vv[j]; i = ii[j]; }
+  }
+}
 
 Q35_DEV void wave_argmax(float& v, int& i) {
 #pragma unroll
@@ -59,8 +85,34 @@ Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
     if (better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
 }
 
-template <int MR>
+// Transposed butterfly over R per-lane row partials: on return every lane holds the full sum of
+// row (lane / (64 / R)).
+template <int R>
+Q35_DEV float fold_rows(float (&p)[R], int lane) {
+  int cnt = R;
+#pragma unroll
+  for (int s = 32; s >= 64 / R; s >>= 1) {
+    const int half = cnt / 2;
+    const bool hi = (lane & s) != 0;
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+      if (i >= half) break;
+      const float snd = hi ? p[i] : p[i + half];
+      const float keep = hi ? p[i + half] : p[i];
+      p[i] = keep + __shfl_xor(snd, s, 64);
+    }
+    cnt = half;
+  }
+  float v = p[0];
+#pragma unroll
+  for (int s = 32 / R; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+  return v;
+}
+
+template <int MR, int CPW>
 __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
+  constexpr int R = kRowsPerWave<CPW>;
+  constexpr int kRowsPerBlock = 4 * R;
   extern __shared__ __align__(16) float xs[];  // [MR][K]
   __shared__ float sh[4];
   __shared__ float shv[4];
@@ -69,39 +121,44 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int K = a.K, nbK = K >> 6;
 
-  // prologue: x (optionally RMS-normalised with (1+w)) into LDS
+  // prologue: thread t loads x[t + 256 j] for all j at once (one round trip), normalises, stages
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m >= a.M) break;
+    float v[CPW * 4];
+#pragma unroll
+    for (int j = 0; j < CPW * 4; ++j) {
+      const int k = tid + kThreads * j;
+      v[j] = (k < K) ? nk_in(a, m, k) : 0.f;
+    }
     float r = 1.0f;
     if (a.pro == PRO_RMS) {
       float ss = 0.f;
-      for (int k = tid; k < K; k += kThreads) { float v = a.x[(size_t)m * a.ldx + k]; ss += v * v; }
+#pragma unroll
+      for (int j = 0; j < CPW * 4; ++j) ss += v[j] * v[j];
       ss = block_sum256(ss, sh);
       r = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    for (int k = tid; k < K; k += kThreads) {
-      float v = a.x[(size_t)m * a.ldx + k];
-      if (a.pro == PRO_RMS) v = (v * r) * (1.0f + a.pw[k]);
-      xs[m * K + k] = v;
+#pragma unroll
+    for (int j = 0; j < CPW * 4; ++j) {
+      const int k = tid + kThreads * j;
+      if (k < K) xs[m * K + k] = (a.pro == PRO_RMS) ? (v[j] * r) * (1.0f + a.pw[k]) : v[j];
     }
   }
   __syncthreads();
 
-  const int cpw = (K + 1023) >> 10;
   float best_v = -INFINITY;
   int best_i = INT_MAX;
   const int nrb = (a.N + kRowsPerBlock - 1) / kRowsPerBlock;
   for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-    const int row0 = rb * kRowsPerBlock + wid * kRowsPerWave;
-    uint4 wv[kRowsPerWave][kMaxCpw];
-    float sv[kRowsPerWave][kMaxCpw];
+    const int row0 = rb * kRowsPerBlock + wid * R;
+    uint4 wv[R][CPW];
+    float sv[R][CPW];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
+    for (int r = 0; r < R; ++r) {
       const int row = row0 + r;
 #pragma unroll
-      for (int c = 0; c < kMaxCpw; ++c) {
-        if (c >= cpw) break;
+      for (int c = 0; c < CPW; ++c) {
         const int k = 16 * (lane + 64 * c);
         const bool ok = row < a.N && k < K;
         wv[r][c] = ok ? *reinterpret_cast<const uint4*>(a.q + (size_t)row * K + k) : make_uint4(0, 0, 0, 0);
@@ -111,21 +168,22 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       if (m >= a.M) break;
-      float p[kRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
+      float p[R];
 #pragma unroll
-      for (int c = 0; c < kMaxCpw; ++c) {
-        if (c >= cpw) break;
+      for (int r = 0; r < R; ++r) p[r] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) {
         const int k = 16 * (lane + 64 * c);
         if (k >= K) continue;
         float xv[16];
         const float4* xp = reinterpret_cast<const float4*>(&xs[m * K + k]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          float4 t = xp[q];
+          const float4 t = xp[q];
           xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
         }
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < R; ++r) {
           float f[16];
           unpack16(wv[r][c], f);
           float d = 0.f;
@@ -134,22 +192,9 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
           p[r] += d * sv[r][c];
         }
       }
-      // transposed butterfly: lane l ends with row (l >> 4) summed over its 16-lane group
-      const bool hi32 = (lane & 32) != 0;
-      float s0 = hi32 ? p[0] : p[2], s1 = hi32 ? p[1] : p[3];
-      float k0 = hi32 ? p[2] : p[0], k1 = hi32 ? p[3] : p[1];
-      k0 += __shfl_xor(s0, 32, 64);
-      k1 += __shfl_xor(s1, 32, 64);
-      const bool hi16 = (lane & 16) != 0;
-      float snd = hi16 ? k0 : k1;
-      float v = hi16 ? k1 : k0;
-      v += __shfl_xor(snd, 16, 64);
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 4, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 1, 64);
-      const int row = row0 + (lane >> 4);
-      if ((lane & 15) == 0 && row < a.N) {
+      const float v = fold_rows<R>(p, lane);
+      const int row = row0 + lane / (64 / R);
+      if ((lane % (64 / R)) == 0 && row < a.N) {
         if (a.y) a.y[(size_t)m * a.ldy + row] = v;
         if (m == 0 && v > best_v) { best_v = v; best_i = row; }
       }
@@ -158,12 +203,11 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
 
   if (!a.argmax_out) return;
   block_argmax(best_v, best_i, shv, shi);
-  if (tid == 0) { a.part_v[blockIdx.x] = best_v; a.part_i[blockIdx.x] = best_i; }
-  if (!arrive_last(a.counter, gridDim.x, &flag)) return;
-  float v = -INFINITY;
-  int i = INT_MAX;
-  for (int b = tid; b < (int)gridDim.x; b += kThreads)
-    if (better(a.part_v[b], a.part_i[b], v, i)) { v = a.part_v[b]; i = a.part_i[b]; }
+  if (tid == 0) { st_agent(&a.part_v[blockIdx.x], best_v); st_agent(&a.part_i[blockIdx.x], best_i); }
+  if (!arrive_last_grid(a.counter, &flag)) return;
+  float v;
+  int i;
+  reduce_published(a.part_v, a.part_i, gridDim.x, v, i);
   block_argmax(v, i, shv, shi);
   if (tid == 0) {
     const int32_t tok = (i == INT_MAX) ? 0 : i;
@@ -189,12 +233,11 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* v, int64_
     if (x > bv) { bv = x; bi = (int)i; }
   }
   block_argmax(bv, bi, shv, shi);
-  if (tid == 0) { part_v[blockIdx.x] = bv; part_i[blockIdx.x] = bi; }
-  if (!arrive_last(counter, gridDim.x, &flag)) return;
-  float rv = -INFINITY;
-  int ri = INT_MAX;
-  for (int b = tid; b < (int)gridDim.x; b += kThreads)
-    if (better(part_v[b], part_i[b], rv, ri)) { rv = part_v[b]; ri = part_i[b]; }
+  if (tid == 0) { st_agent(&part_v[blockIdx.x], bv); st_agent(&part_i[blockIdx.x], bi); }
+  if (!arrive_last_grid(counter, &flag)) return;
+  float rv;
+  int ri;
+  reduce_published(part_v, part_i, gridDim.x, rv, ri);
   block_argmax(rv, ri, shv, shi);
   if (tid == 0) *out = (ri == INT_MAX) ? 0 : ri;
 }
@@ -216,24 +259,38 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const int8_t* q, const 
   }
 }
 
-int nk_grid(int N) {
-  const int nrb = (N + kRowsPerBlock - 1) / kRowsPerBlock;
+int cpw_of(int K) {
+  const int need = (K + 1023) / 1024;
+  return need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+}
+
+int nk_grid(int N, int K) {
+  const int rows_per_block = 4 * (cpw_of(K) >= 8 ? 2 : (cpw_of(K) >= 4 ? 4 : 8));
+  const int nrb = (N + rows_per_block - 1) / rows_per_block;
   return nrb < kMaxGrid ? nrb : kMaxGrid;
+}
+
+template <int MR>
+void launch_mr(int cpw, dim3 g, size_t lds, hipStream_t st, const NkArgs& a) {
+  if (cpw == 1) hipLaunchKernelGGL((nk_kernel<MR, 1>), g, dim3(kThreads), lds, st, a);
+  else if (cpw == 2) hipLaunchKernelGGL((nk_kernel<MR, 2>), g, dim3(kThreads), lds, st, a);
+  else if (cpw == 4) hipLaunchKernelGGL((nk_kernel<MR, 4>), g, dim3(kThreads), lds, st, a);
+  else hipLaunchKernelGGL((nk_kernel<MR, 8>), g, dim3(kThreads), lds, st, a);
 }
 
 }  // namespace
 
 size_t nk_ws_bytes(const NkCall& c) {
-  const size_t g = (size_t)nk_grid(c.N);
+  const size_t g = (size_t)nk_grid(c.N, c.K);
   return kCounterBytes + align256(g * 4) * 2;
 }
 
 int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (!c.q || !c.s || !c.x) return fail(Q35_E_ARG, "nk: null pointer");
+  if (!c.q || !c.s || (!c.x && !c.xf)) return fail(Q35_E_ARG, "nk: null pointer");
   if (c.N <= 0 || c.K <= 0 || (c.K % 64) != 0) return fail(Q35_E_SHAPE, "nk: K must be a positive multiple of 64");
   if (c.K > 1024 * kMaxCpw) return fail(Q35_E_SHAPE, "nk: K > 8192");
   if (c.M < 1 || c.M > 8) return fail(Q35_E_SHAPE, "nk: M in [1,8]");
-  int MR = c.M == 1 ? 1 : (c.M == 2 ? 2 : (c.M <= 4 ? 4 : 8));
+  const int MR = c.M == 1 ? 1 : (c.M == 2 ? 2 : (c.M <= 4 ? 4 : 8));
   if ((size_t)MR * c.K > (size_t)kLdsFloats) return fail(Q35_E_SHAPE, "nk: M*K too large for LDS staging");
   if ((reinterpret_cast<uintptr_t>(c.q) & 15) != 0) return fail(Q35_E_ALIGN, "nk: weights not 16-byte aligned");
   if (c.pro == PRO_RMS && !c.pw) return fail(Q35_E_ARG, "nk: RMSNorm needs weight");
@@ -241,10 +298,10 @@ int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
   if (!c.y && !c.argmax_out) return fail(Q35_E_ARG, "nk: no output");
   NkArgs a;
   a.q = c.q; a.s = c.s; a.N = c.N; a.K = c.K; a.M = c.M;
-  a.x = c.x; a.ldx = c.ldx; a.y = c.y; a.ldy = c.ldy;
+  a.x = c.x; a.xf = c.xf; a.ldx = c.ldx; a.y = c.y; a.ldy = c.ldy;
   a.pro = c.pro; a.pw = c.pw; a.eps = c.eps;
   a.argmax_out = c.argmax_out; a.pos_inc = c.pos_inc; a.hist = c.hist;
-  const int grid = nk_grid(c.N);
+  const int grid = nk_grid(c.N, c.K);
   a.counter = nullptr; a.part_v = nullptr; a.part_i = nullptr;
   if (c.argmax_out) {
     if (!ws || ws_bytes < nk_ws_bytes(c)) return fail(Q35_E_WS, "nk: workspace too small");
@@ -255,10 +312,11 @@ int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
     a.part_i = reinterpret_cast<int32_t*>(base + pb);
   }
   const size_t lds = (size_t)MR * c.K * sizeof(float);
-  if (MR == 1) hipLaunchKernelGGL(nk_kernel<1>, dim3(grid), dim3(kThreads), lds, st, a);
-  else if (MR == 2) hipLaunchKernelGGL(nk_kernel<2>, dim3(grid), dim3(kThreads), lds, st, a);
-  else if (MR == 4) hipLaunchKernelGGL(nk_kernel<4>, dim3(grid), dim3(kThreads), lds, st, a);
-  else hipLaunchKernelGGL(nk_kernel<8>, dim3(grid), dim3(kThreads), lds, st, a);
+  const int cpw = cpw_of(c.K);
+  if (MR == 1) launch_mr<1>(cpw, dim3(grid), lds, st, a);
+  else if (MR == 2) launch_mr<2>(cpw, dim3(grid), lds, st, a);
+  else if (MR == 4) launch_mr<4>(cpw, dim3(grid), lds, st, a);
+  else launch_mr<8>(cpw, dim3(grid), lds, st, a);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

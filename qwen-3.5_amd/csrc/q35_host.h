@@ -26,6 +26,8 @@ void fill_normal(uint64_t seed, uint64_t stream, int64_t offset, int64_t n, floa
 void fill_uniform(uint64_t seed, uint64_t stream, int64_t offset, int64_t n, float lo, float hi, float* out);
 uint64_t fnv1a(const char* s);
 void quantize_q8f(const float* w, int64_t rows, int64_t cols, int8_t* q, float* s);
+// Q35_KN -> Q35_KN_TILED: q[t][K][256], s[t][K][4], columns past N zero
+void pack_kn_tiled(const int8_t* q, const float* s, int64_t K, int64_t N, int8_t* qt, float* st);
 std::vector<TensorSpec> model_specs(const q35_dims& d);
 void synth_values(const TensorSpec& t, uint64_t seed, float* out);
 int validate_dims(const q35_dims& d);

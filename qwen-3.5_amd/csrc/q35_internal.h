@@ -51,23 +51,68 @@ Q35_DEV void unpack16(const uint4 w, float* f) {
   }
 }
 
+// Split-K accumulation in 64-bit fixed point (value * 2^32, two's complement).  Every block
+// adds its partial sums with a fire-and-forget atomic; integer addition is associative, so the
+// total is identical whatever order the blocks arrive in (bit-reproducible), and the only
+// rounding is one f32 -> 2^-32 grid step per partial (|error| <= 2^-33 each).  The consumer
+// (a later kernel) converts the total back to f32.  Valid for |value| < 2^31.
+typedef long long fx_t;
+Q35_DEV fx_t to_fx(float v) { return __float2ll_rn(v * 4294967296.0f); }
+Q35_DEV float from_fx(fx_t a) { return (float)((double)a * (1.0 / 4294967296.0)); }
+Q35_DEV void fx_add(fx_t* p, float v) {
+  __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(p), (unsigned long long)to_fx(v), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cross-block partial results are written and read with agent-scope relaxed atomics: on
+// gfx950 these are `global_store ... sc1` / `global_load ... sc1`, i.e. coherent at the device
+// level (write-through / miss in the per-XCD L2) without the whole-L2 writeback and
+// invalidate (`buffer_wbl2` / `buffer_inv`) that a device-scope fence costs on every block.
+Q35_DEV void st_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+Q35_DEV int32_t ld_agent(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// sum_{i<n} p[i*stride] in index order.  Loads are issued kSumBatch at a time so their latency
+// overlaps (a loop that adds each value as it arrives would wait for every load in turn).
+#ifndef Q35_SUM_BATCH
+#define Q35_SUM_BATCH 32
+#endif
+constexpr int kSumBatch = Q35_SUM_BATCH;
+Q35_DEV float sum_agent(const float* p, int n, size_t stride) {
+  float t = 0.f;
+  for (int i = 0; i < n; i += kSumBatch) {
+    float v[kSumBatch];
+#pragma unroll
+    for (int j = 0; j < kSumBatch; ++j) v[j] = (i + j < n) ? ld_agent(p + (size_t)(i + j) * stride) : 0.f;
+#pragma unroll
+    for (int j = 0; j < kSumBatch; ++j) t += v[j];
+  }
+  return t;
+}
+
 // Split-K / split-T "last block finishes" protocol.  Every block of a group publishes its
-// partial, then increments the group's counter; the block that brings it to `expected`
-// reads all partials (in a fixed order, so results are deterministic) and resets the counter
-// to zero so the next launch (or graph replay) starts clean.  Returns true in that block.
+// partial with st_agent, then increments the group's counter; the block that brings it to
+// `expected` reads all partials with ld_agent (in a fixed order, so results are
+// deterministic) and resets the counter to zero so the next launch (or graph replay) starts
+// clean.  Ordering: s_waitcnt 0 makes every wave's earlier memory operations (the sc1 partial
+// stores included) complete before the barrier, and the counter RMW is issued after it; the
+// reader's sc1 loads are issued after the RMW result is known.  Returns true in that block.
 Q35_DEV bool arrive_last(uint32_t* counter, uint32_t expected, int* sh_flag) {
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t prev = atomicAdd(counter, 1u);
+    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = (prev + 1u == expected);
-    if (last) *counter = 0u;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *sh_flag = last ? 1 : 0;
   }
   __syncthreads();
-  const bool last = *sh_flag != 0;
-  if (last) __threadfence();
-  return last;
+  return *sh_flag != 0;
 }
 
 // Workspace layout shared by every kernel: the first kCounterBytes hold completion
@@ -79,26 +124,56 @@ inline uint32_t* ws_counters(void* ws) { return static_cast<uint32_t*>(ws); }
 inline char* ws_scratch(void* ws) { return static_cast<char*>(ws) + kCounterBytes; }
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// arrive_last for a whole grid of many blocks: blocks arrive on a counter per group of 64
+// (counters[1 + blockIdx/64]); the last block of each group arrives on counters[0].  Keeps
+// the same-address atomic chain at <= 64 instead of gridDim.x.  Uses 1 + ceil(grid/64)
+// counters.
+Q35_DEV bool arrive_last_grid(uint32_t* counters, int* sh_flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t G = 64;
+    const uint32_t grp = blockIdx.x / G;
+    const uint32_t ngrp = (gridDim.x + G - 1) / G;
+    const uint32_t in_grp = (gridDim.x - grp * G) < G ? (gridDim.x - grp * G) : G;
+    bool last = false;
+    const uint32_t p1 = __hip_atomic_fetch_add(&counters[1 + grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (p1 + 1u == in_grp) {
+      __hip_atomic_store(&counters[1 + grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t p0 = __hip_atomic_fetch_add(&counters[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p0 + 1u == ngrp) {
+        __hip_atomic_store(&counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = true;
+      }
+    }
+    *sh_flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  return *sh_flag != 0;
+}
+
 // ------------------------------------------------------------------ Q8F KN matvec (split-K)
 enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_SWIGLU = 3, PRO_EMBED_RMS = 4 };
-enum { EPI_STORE = 0, EPI_RESID = 1 };
-
 struct MvSeg {
   const int8_t* w;  // [K][N]
   const float* s;   // [K][N/64]
-  float* y;         // y[m*ldy + n]; for EPI_RESID the residual stream updated in place
+  fx_t* acc;        // acc[m*ldacc + n] += y: a zeroed accumulator, or the residual stream
   int32_t N;
-  int32_t ldy;
+  int32_t ldacc;
+  int32_t tiled = 0;  // 1: w, s in the Q35_KN_TILED layout (w[t][K][256], s[t][K][4])
 };
 
 struct MvCall {
   MvSeg seg[4];
   int32_t nseg = 0;
   int32_t K = 0, M = 1;
-  int32_t pro = PRO_PLAIN, epi = EPI_STORE;
-  const float* x = nullptr;   // prologue input x[m*ldx + k]
+  int32_t pro = PRO_PLAIN;
+  // prologue input in[m][k]: f32 x[m*ldx + k], or the fixed-point accumulator xf when set
+  const float* x = nullptr;
+  const fx_t* xf = nullptr;
   int32_t ldx = 0;
-  const float* x2 = nullptr;  // PRO_GATED: z[m*ldx2 + k]
+  const float* x2 = nullptr;  // PRO_GATED: z (f32 or fixed point x2f), row stride ldx2
+  const fx_t* x2f = nullptr;
   int32_t ldx2 = 0;
   const float* pw = nullptr;  // PRO_RMS: norm weight (applied as 1+w); PRO_GATED: weight [group]
   int32_t group = 0;          // PRO_GATED group size
@@ -112,19 +187,27 @@ struct MvCall {
   const int32_t* prompt = nullptr;
   const int32_t* plen = nullptr;
   const int32_t* pos = nullptr;
-  float* h_out = nullptr;
-  // optional f32 gate projection riding in the same launch (GatedDeltaNet in_proj_b/in_proj_a)
+  fx_t* h_out = nullptr;
+  // optional f32 gate projection on extra blocks (GatedDeltaNet in_proj_b / in_proj_a): raw
+  // sums [x.W_b | x.W_a] added to aux_acc[m*aux_ldo + 0 .. 2*aux_nh)
   const float* aux_wb = nullptr;
   const float* aux_wa = nullptr;
-  const float* aux_alog = nullptr;
-  const float* aux_dtb = nullptr;
   int32_t aux_nh = 0;
-  float* aux_out = nullptr;  // [M][2*aux_nh] = [beta | g]
+  fx_t* aux_acc = nullptr;
   int32_t aux_ldo = 0;
+  // side task: zero zero_ptr[0 .. zero_n) for a later kernel
+  fx_t* zero_ptr = nullptr;
+  int64_t zero_n = 0;
+  // side task: causal-conv state shift, state[b][c] <- [s1, s2, x[b*cs_ldx + c]] for c < cs_ch
+  float* cs_state = nullptr;
+  const fx_t* cs_x = nullptr;
+  int32_t cs_ch = 0, cs_ldx = 0, cs_B = 0;
 };
 
-size_t mv_kn_ws_bytes(const MvCall& c);
-int mv_kn_launch(const MvCall& c, void* ws, size_t ws_bytes, hipStream_t st);
+int mv_kn_launch(const MvCall& c, hipStream_t st);
+// y[i] = f32(acc[i]) (optionally re-zeroing acc); acc[i] = 0
+int fx_to_f32_launch(fx_t* acc, int64_t n, float* y, bool zero_after, hipStream_t st);
+int fx_zero_launch(fx_t* acc, int64_t n, hipStream_t st);
 
 // ------------------------------------------------------------------ Q8F NK matvec / lm_head
 struct NkCall {
@@ -132,6 +215,7 @@ struct NkCall {
   const float* s;   // [N][K/64]
   int32_t N = 0, K = 0, M = 1;
   const float* x = nullptr;
+  const fx_t* xf = nullptr;  // fixed-point input (the residual stream) instead of x
   int32_t ldx = 0;
   float* y = nullptr;  // y[m*ldy + n] (may be null when only the argmax is wanted)
   int32_t ldy = 0;
@@ -154,23 +238,26 @@ int embed_launch(const int8_t* q, const float* s, int32_t V, int32_t D, const in
                  float* out, hipStream_t st);
 
 // ------------------------------------------------------------------ Gated DeltaNet step
+// The step reads the conv state but does not advance it (every value-column slice of a head
+// reads the same q/k channels); the caller advances it afterwards (conv_shift_launch, or the
+// cs_* side task of the next matvec).
 struct GdnCall {
-  const float* qkv; int32_t ld_qkv;  // pre-conv mixed qkv [B][conv_dim]
-  const float* bg;  int32_t ld_bg;   // [B][2*nh] = [beta | g]
-  float* conv_state;                 // [B][conv_dim][conv_k-1]
-  const float* conv_w;               // [conv_dim][conv_k]
-  float* S;                          // [B][nh][dk][dv]
-  float* o;         int32_t ld_o;    // [B][nh*dv] raw core output (before the gated norm)
-  int32_t B, nh, dk, dv, conv_k;
+  // pre-conv mixed qkv [B][conv_dim]: f32 qkv, or the fixed-point accumulator qkv_f
+  const float* qkv = nullptr; const fx_t* qkv_f = nullptr; int32_t ld_qkv = 0;
+  // gates: activated [beta | g] bg (f32), or raw [x.W_b | x.W_a] ba_f (fixed point) plus
+  // a_log / dt_bias, activated here as kernels.rs:228-244 does
+  const float* bg = nullptr; const fx_t* ba_f = nullptr; int32_t ld_bg = 0;
+  const float* a_log = nullptr; const float* dt_bias = nullptr;
+  const float* conv_state = nullptr;  // [B][conv_dim][conv_k-1]
+  const float* conv_w = nullptr;      // [conv_dim][conv_k]
+  float* S = nullptr;                 // [B][nh][dk][dv]
+  float* o = nullptr; int32_t ld_o = 0;  // [B][nh*dv] raw core output (before the gated norm)
+  int32_t B = 1, nh = 0, dk = 0, dv = 0, conv_k = 0;
 };
-size_t gdn_step_ws_bytes(int32_t B, int32_t nh);
-int gdn_step_launch(const GdnCall& c, void* ws, size_t ws_bytes, hipStream_t st);
+int gdn_step_launch(const GdnCall& c, hipStream_t st);
+// state[b][c] <- [s1, s2, x[b][c]] for all conv_dim channels (f32 x)
+int conv_shift_launch(float* state, const float* x, int32_t B, int32_t ch, hipStream_t st);
 
-// Gate projection alone (kernels.rs gate_proj): uses the matvec kernel's aux path.
-int gate_proj_launch(const float* x, int32_t B, int32_t in_dim, const float* wb, const float* wa,
-                     const float* alog, const float* dtb, int32_t nh, float* out, void* ws,
-                     size_t ws_bytes, hipStream_t st);
-size_t gate_proj_ws_bytes(int32_t B, int32_t in_dim, int32_t nh);
 // Gate projection without workspace: one block per batch row.
 int gate_proj_simple_launch(const float* x, int32_t B, int32_t in_dim, const float* wb, const float* wa,
                             const float* alog, const float* dtb, int32_t nh, float* out, hipStream_t st);
@@ -178,10 +265,13 @@ int gate_proj_simple_launch(const float* x, int32_t B, int32_t in_dim, const flo
 // Gated-RMSNorm alone is folded into the out_proj prologue (PRO_GATED).
 
 // ------------------------------------------------------------------ attention decode
+// Inputs are f32, or (the *_f pointers, when set) the fixed-point accumulator of the q|k|v
+// projection launch.
 struct AttnCall {
-  const float* qg; int32_t ld_qg;   // [B][nh*2*hd], per head [query | gate]
-  const float* k; const float* v;   // new token's k / v rows: k[b*ld_kv + g*hd + i]
-  int32_t ld_kv;
+  const float* qg = nullptr; const fx_t* qg_f = nullptr; int32_t ld_qg = 0;  // [B][nh*2*hd], per head [q | gate]
+  const float* k = nullptr; const float* v = nullptr;   // new token's k / v rows: k[b*ld_kv + g*hd + i]
+  const fx_t* k_f = nullptr; const fx_t* v_f = nullptr;
+  int32_t ld_kv = 0;
   const float* qnw; const float* knw; float eps;
   const float* rcos; const float* rsin; int32_t rot;
   float* kc; float* vc; int32_t tmax;  // [B][nkv][tmax][hd]
@@ -191,5 +281,7 @@ struct AttnCall {
 };
 size_t attn_ws_bytes(int32_t B, int32_t nh, int32_t nkv, int32_t hd, int32_t tmax);
 int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st);
+// same, with the completion counters and the chunk-partial scratch given separately
+int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size_t scratch_bytes, hipStream_t st);
 
 }  // namespace q35

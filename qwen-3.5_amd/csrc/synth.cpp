@@ -95,6 +95,23 @@ void quantize_q8f(const float* w, int64_t rows, int64_t cols, int8_t* q, float* 
   });
 }
 
+void pack_kn_tiled(const int8_t* q, const float* s, int64_t K, int64_t N, int8_t* qt, float* st) {
+  const int64_t ntile = (N + 255) / 256, nb = N / 64;
+  parallel_for(ntile * K, [&](int64_t i0, int64_t i1) {
+    for (int64_t i = i0; i < i1; ++i) {
+      const int64_t t = i / K, k = i % K;
+      for (int64_t c = 0; c < 256; ++c) {
+        const int64_t n = t * 256 + c;
+        qt[i * 256 + c] = n < N ? q[k * N + n] : 0;
+      }
+      for (int64_t j = 0; j < 4; ++j) {
+        const int64_t b = t * 4 + j;
+        st[i * 4 + j] = b < nb ? s[k * nb + b] : 0.0f;
+      }
+    }
+  });
+}
+
 std::vector<TensorSpec> model_specs(const q35_dims& d) {
   std::vector<TensorSpec> v;
   const int64_t H = d.hidden, F = d.ffn, V = d.vocab;
@@ -172,6 +189,17 @@ int q35_quantize_q8f(const float* w_host, int64_t rows, int64_t cols, int8_t* q_
   if (!w_host || !q_host || !scale_host) return fail(Q35_E_ARG, "quantize: null pointer");
   if (rows < 1 || cols < 64 || (cols % 64) != 0) return fail(Q35_E_SHAPE, "quantize: cols must be a positive multiple of 64");
   quantize_q8f(w_host, rows, cols, q_host, scale_host);
+  return Q35_OK;
+}
+
+int64_t q35_q8f_tiled_q_count(int32_t K, int32_t N) { return (int64_t)((N + 255) / 256) * K * 256; }
+int64_t q35_q8f_tiled_scale_count(int32_t K, int32_t N) { return (int64_t)((N + 255) / 256) * K * 4; }
+
+int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_tiled_host,
+                          float* scale_tiled_host) {
+  if (!q_host || !scale_host || !q_tiled_host || !scale_tiled_host) return fail(Q35_E_ARG, "pack_kn_tiled: null pointer");
+  if (K < 1 || N < 64 || (N % 64) != 0) return fail(Q35_E_SHAPE, "pack_kn_tiled: N must be a positive multiple of 64");
+  pack_kn_tiled(q_host, scale_host, K, N, q_tiled_host, scale_tiled_host);
   return Q35_OK;
 }
 

@@ -9,6 +9,7 @@ Differences from the reference, by design: batches of M rows are accepted (the r
 squeezes [1,1,K] and panics otherwise) and q8_gemv_partial_sum sums every input row (the
 reference kernel skips rows when K / splits is not a multiple of 8, kernels.rs:119-133,504).
 """
+import numpy as np
 import torch
 
 from . import _lib as L
@@ -24,15 +25,17 @@ def ctypes_stream(s):
     return s.cuda_stream
 
 
-def workspace(nbytes, device=None):
-    """Zero-filled scratch shared by calls on the current stream (every call leaves its
-    completion counters zero again, so one buffer serves all calls in stream order)."""
+def workspace(nbytes, device=None, key="default"):
+    """Zero-filled scratch for one kind of entry point on the current stream.  Each call leaves
+    its completion counters and fixed-point accumulators zero again, so a buffer serves every
+    later call of the same entry point in stream order; different entry points lay out their
+    workspace differently and get separate buffers (`key`)."""
     device = torch.device(device or "cuda")
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
-    buf = _workspaces.get(key)
+    k = (key, device.type, device.index if device.index is not None else torch.cuda.current_device())
+    buf = _workspaces.get(k)
     if buf is None or buf.numel() < nbytes:
         buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = buf
+        _workspaces[k] = buf
     return buf
 
 
@@ -41,27 +44,48 @@ class Q8FTensor:
 
     layout Q35_KN: q [K(in)][N(out)], scale [K][N/64]  (Burn Linear weight, kernels.rs:56-57)
     layout Q35_NK: q [N][K],          scale [N][K/64]  (embedding table, kernels.rs:253-255)
+    layout Q35_KN_TILED: the Q35_KN matrix cut into 256-column tiles, tile-major:
+        q [ceil(N/256)][K][256], scale [ceil(N/256)][K][4], columns past N zero
     """
 
-    def __init__(self, q, scale, layout=L.Q35_KN):
-        assert q.dtype == torch.int8 and scale.dtype == torch.float32 and q.dim() == 2
-        assert scale.shape == (q.shape[0], q.shape[1] // 64), (scale.shape, q.shape)
+    def __init__(self, q, scale, layout=L.Q35_KN, shape=None):
+        assert q.dtype == torch.int8 and scale.dtype == torch.float32
+        if layout == L.Q35_KN_TILED:
+            assert shape is not None and q.dim() == 3 and q.shape[2] == 256 and scale.shape == q.shape[:2] + (4,)
+            self.rows, self.cols = shape
+            assert q.shape[:2] == ((self.cols + 255) // 256, self.rows), (q.shape, shape)
+        else:
+            assert q.dim() == 2 and scale.shape == (q.shape[0], q.shape[1] // 64), (scale.shape, q.shape)
+            self.rows, self.cols = q.shape
         self.q, self.scale, self.layout = q.contiguous(), scale.contiguous(), layout
 
     @property
     def shape(self):
-        return tuple(self.q.shape)
+        return (self.rows, self.cols)
 
     @property
     def in_dim(self):
-        return self.q.shape[0] if self.layout == L.Q35_KN else self.q.shape[1]
+        return self.cols if self.layout == L.Q35_NK else self.rows
 
     @property
     def out_dim(self):
-        return self.q.shape[1] if self.layout == L.Q35_KN else self.q.shape[0]
+        return self.rows if self.layout == L.Q35_NK else self.cols
 
     def desc(self):
-        return L.Q8F(self.q.data_ptr(), self.scale.data_ptr(), self.q.shape[0], self.q.shape[1], self.layout)
+        return L.Q8F(self.q.data_ptr(), self.scale.data_ptr(), self.rows, self.cols, self.layout)
+
+    def tiled(self):
+        """Q35_KN -> Q35_KN_TILED copy, packed on the host through q35_q8f_pack_kn_tiled."""
+        assert self.layout == L.Q35_KN
+        K, N = self.rows, self.cols
+        q = self.q.cpu().numpy()
+        s = self.scale.cpu().numpy()
+        qt = np.empty(L.lib().q35_q8f_tiled_q_count(K, N), dtype=np.int8)
+        st = np.empty(L.lib().q35_q8f_tiled_scale_count(K, N), dtype=np.float32)
+        L.check(L.lib().q35_q8f_pack_kn_tiled(q.ctypes.data, s.ctypes.data, K, N, qt.ctypes.data, st.ctypes.data))
+        nt = (N + 255) // 256
+        return Q8FTensor(torch.from_numpy(qt.reshape(nt, K, 256)).to(self.q.device),
+                         torch.from_numpy(st.reshape(nt, K, 4)).to(self.q.device), L.Q35_KN_TILED, (K, N))
 
 
 def _rows(x, k):
@@ -76,8 +100,7 @@ def q8_gemv(hidden_states, weights: Q8FTensor):
     x = _rows(hidden_states, K)
     y = torch.empty((x.shape[0], N), dtype=torch.float32, device=x.device)
     W = weights.desc()
-    nbytes = L.lib().q35_q8_gemv_ws_bytes(x.shape[0], W)
-    ws = workspace(nbytes, x.device)
+    ws = workspace(L.lib().q35_q8_gemv_ws_bytes(x.shape[0], W), x.device, "gemv")
     L.check(L.lib().q35_q8_gemv(x.data_ptr(), x.shape[0], W, y.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
     return y.reshape(*hidden_states.shape[:-1], N)
 
@@ -87,7 +110,7 @@ def q8_gemv_partial_sum(hidden_states, weights: Q8FTensor):
     x = _rows(hidden_states, K)
     y = torch.empty((x.shape[0], N), dtype=torch.float32, device=x.device)
     W = weights.desc()
-    ws = workspace(L.lib().q35_q8_gemv_ws_bytes(x.shape[0], W), x.device)
+    ws = workspace(L.lib().q35_q8_gemv_ws_bytes(x.shape[0], W), x.device, "gemv")
     L.check(L.lib().q35_q8_gemv_partial_sum(x.data_ptr(), x.shape[0], W, y.data_ptr(), ws.data_ptr(), ws.numel(),
                                             _stream()))
     return y.reshape(*hidden_states.shape[:-1], N)
@@ -126,6 +149,6 @@ def gate_proj(hidden_states, w_b, w_a, a_log, dt_bias):
 def argmax(logits):
     v = logits.reshape(-1).contiguous()
     out = torch.empty(1, dtype=torch.int32, device=v.device)
-    ws = workspace(L.lib().q35_argmax_ws_bytes(v.numel()), v.device)
+    ws = workspace(L.lib().q35_argmax_ws_bytes(v.numel()), v.device, "argmax")
     L.check(L.lib().q35_argmax(v.data_ptr(), v.numel(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
     return out

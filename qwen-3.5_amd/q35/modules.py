@@ -36,7 +36,7 @@ class GatedDeltaNet:
         x = hidden_states.reshape(-1, d.hidden).contiguous()
         B = x.shape[0]
         out = torch.empty_like(x)
-        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, 1), x.device)
+        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, 1), x.device, ("gated_deltanet", B))
         L.check(L.lib().q35_gated_deltanet_decode(ctypes.byref(d), ctypes.byref(self.w), x.data_ptr(), B,
                                                   conv_state.data_ptr(), recurrent_state.data_ptr(), out.data_ptr(),
                                                   ws.data_ptr(), ws.numel(), _stream()))
@@ -60,7 +60,7 @@ class Attention:
         B = x.shape[0]
         tmax = k_cache.shape[2]
         out = torch.empty_like(x)
-        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, tmax), x.device)
+        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, tmax), x.device, ("attention", B, tmax))
         L.check(L.lib().q35_attention_decode(ctypes.byref(d), ctypes.byref(self.w), x.data_ptr(), B, k_cache.data_ptr(),
                                              v_cache.data_ptr(), tmax, pos.data_ptr(), rope_cos.data_ptr(),
                                              rope_sin.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream()))
@@ -78,7 +78,7 @@ class MLP:
         x2 = x.reshape(-1, d.hidden).contiguous()
         B = x2.shape[0]
         out = torch.empty_like(x2)
-        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, 1), x2.device)
+        ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, 1), x2.device, ("mlp", B))
         L.check(L.lib().q35_mlp_decode(ctypes.byref(d), ctypes.byref(self.w), x2.data_ptr(), B, out.data_ptr(),
                                        ws.data_ptr(), ws.numel(), _stream()))
         return out
@@ -90,7 +90,7 @@ def gated_delta_rule_decode(mixed_qkv, beta_g, conv_state, conv_w, recurrent_sta
     returns the core output [B, heads*dv] (before the gated norm)."""
     B = mixed_qkv.shape[0]
     out = torch.empty((B, heads * dv), dtype=torch.float32, device=mixed_qkv.device)
-    ws = workspace(1 << 16, mixed_qkv.device)
+    ws = workspace(1 << 16, mixed_qkv.device, "delta_rule")
     L.check(L.lib().q35_gated_delta_rule_decode(_p(mixed_qkv), B, _p(beta_g), conv_state.data_ptr(), _p(conv_w),
                                                 recurrent_state.data_ptr(), out.data_ptr(), heads, dk, dv,
                                                 ws.data_ptr(), ws.numel(), _stream()))
@@ -103,7 +103,7 @@ def attention_core_decode(dims, q_gate, k_new, v_new, q_norm, k_norm, k_cache, v
     B = q_gate.shape[0]
     tmax = k_cache.shape[2]
     out = torch.empty((B, dims.attn_heads * dims.head_dim), dtype=torch.float32, device=q_gate.device)
-    ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(dims), B, tmax), q_gate.device)
+    ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(dims), B, tmax), q_gate.device, ("attention_core", B, tmax))
     L.check(L.lib().q35_attention_core_decode(ctypes.byref(dims), _p(q_gate), _p(k_new), _p(v_new), k_new.shape[1], B,
                                               _p(q_norm), _p(k_norm), k_cache.data_ptr(), v_cache.data_ptr(), tmax,
                                               pos.data_ptr(), _p(rope_cos), _p(rope_sin), out.data_ptr(), ws.data_ptr(),

@@ -48,6 +48,27 @@ def test_q8_gemv_kn_odd_shapes(N, K, M):
     assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
 
 
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("N,K", C1_SHAPES)
+def test_q8_gemv_kn_tiled_projection_shapes(N, K, M):
+    print(f"[gemv_kn tiled] N={N} K={K} M={M}", flush=True)
+    W = q8(1000 + N + K, K, N)
+    x = normal(7, (M, K))
+    y = host(q35.q8_gemv(dev(x), q8_dev(W, q35.Q35_KN).tiled()))
+    assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
+
+
+@pytest.mark.parametrize("N,K,M", [(64, 64, 1), (192, 100, 3), (320, 48, 2), (1024, 16, 8), (6400, 2048, 1)])
+def test_q8_gemv_kn_tiled_odd_shapes(N, K, M):
+    """N not a multiple of the 256-column tile: the padded columns must not reach the output."""
+    print(f"[gemv_kn tiled odd] N={N} K={K} M={M}", flush=True)
+    W = q8(3000 + N + K, K, N, sigma=1.0)
+    x = normal(9, (M, K))
+    y = host(q35.q8_gemv(dev(x), q8_dev(W, q35.Q35_KN).tiled()))
+    assert y.shape == (M, N)
+    assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
+
+
 @pytest.mark.parametrize("N,K,M", [(1, 64, 1), (17, 128, 2), (33, 1088, 3), (100, 8192, 1), (4097, 6144, 8)])
 def test_q8_gemv_nk_odd_shapes(N, K, M):
     print(f"[gemv_nk odd] N={N} K={K} M={M}", flush=True)

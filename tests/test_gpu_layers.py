@@ -153,3 +153,16 @@ def test_mlp_module(B):
     out = host(gpu.forward(dev(x)))
     exp = O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), x)
     assert rel_l2(out, exp) <= 1e-5
+
+
+@pytest.mark.parametrize("B", [1, 11])
+def test_mlp_module_tiled_weights(B):
+    """The layer entry points take Q35_KN_TILED projections, as the model holds them."""
+    d = q35.dims_2b()
+    cfg = O.cfg_from_dims(d)
+    Wg, Wu, Wd = q8(100, d.hidden, d.ffn), q8(101, d.hidden, d.ffn), q8(102, d.ffn, d.hidden)
+    gpu = q35.MLP(d, *(q8_dev(W, q35.Q35_KN).tiled() for W in (Wg, Wu, Wd)))
+    x = normal(103, (B, d.hidden))
+    out = host(gpu.forward(dev(x)))
+    exp = O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), x)
+    assert rel_l2(out, exp) <= 1e-5

@@ -7,6 +7,7 @@ import re
 
 import numpy as np
 import pytest
+import torch
 
 import oracle as O
 import q35
@@ -113,3 +114,23 @@ def test_argument_validation_without_gpu():
     h = ctypes.c_void_p()
     assert lib.q35_model_create_synthetic(ctypes.byref(d), 0, 16, ctypes.byref(h)) == L.Q35_E_SHAPE
     assert lib.q35_gate_proj(x, 1, 64, x, x, x, x, 48, x, None) == L.Q35_E_SHAPE  # 2*48 does not divide 256
+
+
+@pytest.mark.parametrize("K,N", [(3, 64), (5, 256), (2, 320), (7, 704)])
+def test_pack_kn_tiled_layout(K, N):
+    """Q35_KN -> Q35_KN_TILED: element (k, n) lands at [n // 256][k][n % 256], scale block b at
+    [b // 4][k][b % 4]; the tile's columns past N are zero."""
+    rng = np.random.default_rng(K * 1000 + N)
+    q = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+    s = rng.random((K, N // 64), dtype=np.float32) + 0.5
+    t = q35.Q8FTensor(torch.from_numpy(q), torch.from_numpy(s), q35.Q35_KN).tiled()
+    assert t.layout == q35.Q35_KN_TILED and t.shape == (K, N) and t.in_dim == K and t.out_dim == N
+    qt, st = t.q.numpy(), t.scale.numpy()
+    nt = (N + 255) // 256
+    assert qt.shape == (nt, K, 256) and st.shape == (nt, K, 4)
+    for n in range(N):
+        np.testing.assert_array_equal(qt[n // 256, :, n % 256], q[:, n])
+    for b in range(N // 64):
+        np.testing.assert_array_equal(st[b // 4, :, b % 4], s[:, b])
+    assert not qt[nt - 1, :, N - (nt - 1) * 256:].any()
+    assert not st[nt - 1, :, N // 64 - (nt - 1) * 4:].any()
