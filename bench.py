@@ -4,9 +4,10 @@ seeded random init), plus the Q8F matvec bandwidth against the 8 TB/s HBM roofli
 
 Workload: 24 layers (18 Gated DeltaNet + 6 gated GQA), hidden 2048, FFN 6144, vocab 248320,
 tied embeddings, random-init weights N(0, 0.02) quantised to Q8F, seed 0; a 512-token uniform
-random prompt is fed through the decode step (captured hipGraph), then W untimed and K timed
-greedy decode steps.  A "step" is one token through the whole model (embedding -> 24 layers ->
-final norm -> lm_head -> argmax), graph-replayed with inputs and weights resident in HBM.
+random prompt is fed through the decode step, then W untimed and K timed greedy decode steps.  A
+"step" is one token through the whole model (embedding -> 24 layers -> final norm -> lm_head ->
+argmax) with weights and caches resident in HBM, run by the persistent step kernel (--chunk steps
+per launch; each step's argmax feeds the next step on the device).
 
 Prints one JSON line.  Only one GPU is used; --gpus N > 1 exits with a message.
 """
@@ -148,6 +149,9 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape matvec sweep")
+    ap.add_argument("--chunk", type=int, default=64, help="decode steps per persistent-kernel launch")
+    ap.add_argument("--readback", action="store_true",
+                    help="also time one launch per token with a host readback each step (main.rs loop)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the decode path is single-GPU; multi-GPU is "
@@ -160,39 +164,63 @@ def main():
 
     torch.cuda.set_device(0)
     d = q35.dims_2b()
-    tmax = args.prompt + args.warmup + args.steps + 8
+    chunk = args.chunk
+    n_pre = -(-args.prompt // chunk) * chunk
+    n_warm = -(-args.warmup // chunk) * chunk
+    n_timed = -(-args.steps // chunk) * chunk
+    tmax = n_pre + n_warm + n_timed + 8
     t0 = time.time()
     m = q35.TextForCausalLM(d, seed=args.seed, tmax=tmax)
     create_s = time.time() - t0
-    prompt = np.random.default_rng(args.seed).integers(0, d.vocab, args.prompt).astype(np.int32)
+    grid = m.persistent_grid()
+    prompt = np.random.default_rng(args.seed).integers(0, d.vocab, n_pre).astype(np.int32)
+    st = torch.cuda.Stream()  # a stream of its own (the null stream's handle would mean "model stream")
+    torch.cuda.set_stream(st)
+    sh = st.cuda_stream
 
-    # prompt through the captured decode step, then warmup, then K timed steps
+    # The prompt goes through the decode step; every persistent launch below is `chunk` steps, so
+    # the kernel's average launch duration in a profile of this command is the timed one.
     t0 = time.time()
-    m.generate(prompt, 0, use_graph=True)
-    torch.cuda.synchronize()
+    m.generate(prompt[:chunk], 0, mode="persistent", stream=sh)
+    for c0 in range(chunk, n_pre, chunk):
+        m.generate(prompt[c0:c0 + chunk], 0, mode="persistent", stream=sh)
+    m.check(stream=sh)
     prefill_s = time.time() - t0
-    for _ in range(args.warmup):
-        m.step(use_graph=True)
+    for _ in range(n_warm // chunk):
+        m.decode(chunk, mode="persistent", stream=sh)
+    m.check(stream=sh)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_timed // chunk)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        m.step(use_graph=True)
+    for e0, e1 in ev:
+        e0.record(st)
+        m.decode(chunk, mode="persistent", stream=sh)
+        e1.record(st)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    toks = args.steps / el
-    ms = el * 1e3 / args.steps
+    m.check(stream=sh)
+    launch_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
+    kern_s = sum(launch_ms) * 1e-3
+    toks = n_timed / el
+    ms = el * 1e3 / n_timed
+    ctx0 = n_pre + n_warm
+    bytes_timed = sum(step_bytes(d, ctx0 + i + 1) for i in range(n_timed))
+    bytes_per_launch = bytes_timed / len(ev)
+    avg_launch_us = kern_s * 1e6 / len(ev)
+    achieved = bytes_per_launch / (avg_launch_us * 1e-6) / 1e9
+    hist = m.tensor("hist", np.int32)[:ctx0 + n_timed]
 
-    # main.rs semantics: per-token device->host readback and sync inside the timed loop
-    m.reset()
-    _, dec_s = m.generate(prompt, 64, use_graph=True, readback_each=True)
-    toks_readback = 64 / dec_s
+    toks_readback = None
+    if args.readback:  # main.rs semantics: one launch per token, token read back and synced each step
+        m.reset()
+        m.generate(prompt[:chunk], 0, mode="persistent", stream=sh)
+        _, dec_s = m.generate(prompt[chunk:chunk + 1], 64, mode="persistent", readback_each=True, stream=sh)
+        toks_readback = 64 / dec_s
 
     lm_us = time_lm_head(torch, q35, m, d, reps=50)
     lm_bytes = q8_bytes(d.vocab, d.hidden, 1)
     lm_gbs = lm_bytes / lm_us / 1e3
     sweep = None if args.no_sweep else matvec_sweep(torch, q35, m, d)
-    ctx_mid = args.prompt + args.warmup + args.steps // 2
-    sb = step_bytes(d, ctx_mid)
     m.close()
 
     cpu = None
@@ -214,16 +242,18 @@ def main():
         "data": "synthetic (random-init weights N(0,0.02) quantised to Q8F, seed 0; uniform random prompt)",
         "config": {"workload": "greedy decode bs=1, Qwen3.5-2B-shaped hybrid decoder (18 Gated DeltaNet + 6 gated "
                                "GQA layers, hidden 2048, FFN 6144, vocab 248320, tied Q8F embeddings)",
-                   "batch": 1, "prompt_len": args.prompt, "ctx_range": [args.prompt + args.warmup,
-                                                                       args.prompt + args.warmup + args.steps],
-                   "weights": "int8 Q8F per-64 f32 scales", "graph": "hipGraph per decode step"},
-        "roofline": {"kernel": "nk_kernel<1>: Q8F lm_head matvec 248320x2048 (kernels.rs q8_lm_head)",
-                     "bound": "hbm", "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)},
-        "step_roofline": {"bytes_per_step": sb, "achieved_GBs": round(sb / (ms * 1e-3) / 1e9, 1),
-                          "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
-        "tok_s_with_readback": round(toks_readback, 2),
+                   "batch": 1, "prompt_len": n_pre, "ctx_range": [ctx0, ctx0 + n_timed],
+                   "weights": "int8 Q8F per-64 f32 scales",
+                   "launch": f"persistent step kernel, {chunk} steps per launch, grid {grid}x512"},
+        "roofline": {"kernel": f"step_kernel<2>: persistent decode step, {chunk} tokens per launch",
+                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_us, 1)},
+        "lm_head_kernel": {"kernel": "nk_kernel<1,2>: standalone Q8F lm_head 248320x2048 (kernels.rs q8_lm_head)",
+                           "achieved_GBs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+                           "avg_launch_us": round(lm_us, 2)},
+        "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
+        "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
         "prefill_tok_s_via_decode_step": round(args.prompt / prefill_s, 1),
         "model_build_s": round(create_s, 1),
         "matvec_kn_sweep": sweep,

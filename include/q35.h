@@ -200,17 +200,41 @@ int q35_model_reset(q35_model* m, void* stream);
 /* Write the next input token (host value) into the model's device token slot. */
 int q35_model_set_token(q35_model* m, int32_t token, void* stream);
 
+/* How a decode step is launched (the `use_graph` / `mode` arguments below):
+ *   Q35_LAUNCH_STREAM      the step's ~120 fused kernels launched one by one on the stream;
+ *   Q35_LAUNCH_GRAPH       the same kernels as a hipGraph captured on first use on this stream;
+ *   Q35_LAUNCH_PERSISTENT  one cooperative launch of the persistent step kernel (one block per
+ *                          CU, grid barriers between stages) that runs any number of
+ *                          consecutive steps; fastest.  Needs hidden <= 4096 and the device to
+ *                          co-schedule the grid (q35_model_persistent_info). */
+enum { Q35_LAUNCH_STREAM = 0, Q35_LAUNCH_GRAPH = 1, Q35_LAUNCH_PERSISTENT = 2 };
+
 /* One decode step: reads the device token slot, runs embedding -> layers -> norm -> lm_head ->
  * argmax, writes the argmax back into the token slot and advances the device position.
  * Replaces TextForCausalLM::forward (model.rs:113-129) + kernels::argmax (main.rs:131).
- * use_graph=1 replays a hipGraph captured on first use on this stream. */
+ * use_graph: a Q35_LAUNCH_* mode. */
 int q35_model_step(q35_model* m, int32_t use_graph, void* stream);
+
+/* n_steps consecutive decode steps (each one's argmax feeds the next, or the prompt id while the
+ * position is inside the prompt given to q35_model_generate); asynchronous on the stream.  In
+ * Q35_LAUNCH_PERSISTENT mode all steps are one kernel launch. */
+int q35_model_decode(q35_model* m, int32_t n_steps, int32_t mode, void* stream);
+
+/* Synchronises the stream and reports a persistent-kernel failure (a grid barrier that timed
+ * out; the kernel then exits early and its results are invalid).  Q35_OK otherwise. */
+int q35_model_check(q35_model* m, void* stream);
+
+/* Grid of the persistent step kernel (blocks, one per CU); returns an error code and message
+ * when the persistent mode is unavailable for this model or device. */
+int q35_model_persistent_info(q35_model* m, int32_t* grid_out);
 
 /* Greedy generation (main.rs:100-132 without tokenizer or stop tokens): feeds the n_prompt
  * prompt ids one decode step at a time, then runs n_new decode steps.  out_tokens_host receives
  * n_new+1 ids: the argmax after the last prompt token, then the argmax after each decode step.
  * readback_each=1 copies each token to the host and synchronises per step as main.rs:107
- * does.  decode_seconds_host (optional) receives the wall time of the n_new decode steps. */
+ * does (in persistent mode: one launch per decode step; otherwise the prompt and the n_new
+ * steps are one launch each).  decode_seconds_host (optional) receives the wall time of the
+ * n_new decode steps.  use_graph: a Q35_LAUNCH_* mode. */
 int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t n_new,
                        int32_t* out_tokens_host, int32_t use_graph, int32_t readback_each,
                        double* decode_seconds_host, void* stream);

@@ -18,6 +18,7 @@
 #include "q35_host.h"
 
 #include <chrono>
+#include <cmath>
 #include <cstring>
 #include <map>
 #include <vector>
@@ -56,6 +57,11 @@ struct q35_model {
   hipStream_t own_stream = nullptr;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  // persistent decode-step kernel (launch mode 2)
+  int step_grid = 0;
+  int step_rc = Q35_OK;  // why the persistent kernel cannot run here, if it cannot
+  std::string step_msg;
+  q35::StepArgs step_args{};
 };
 
 namespace q35 {
@@ -166,6 +172,67 @@ size_t model_ws_bytes(const q35_dims& d, int tmax) {
   return align256(m);
 }
 
+// Device tables and scratch of the persistent step kernel.  A model whose shapes the kernel does
+// not support still builds; launch mode 2 then reports why.
+int setup_persistent(q35_model* m) {
+  const q35_dims& d = m->d;
+  m->step_grid = step_grid(d.hidden);
+  m->step_rc = step_validate(d, m->tmax, m->step_grid);
+  if (m->step_rc != Q35_OK) {
+    m->step_msg = "persistent step unavailable: " + std::string(q35_last_error());
+    return Q35_OK;
+  }
+  const int grid = m->step_grid, nh = d.lin_heads, kvh = d.kv_heads;
+  const int nmax = step_att_nmax(grid, kvh);
+  std::vector<StepLayer> hl(d.n_layers);
+  for (int l = 0; l < d.n_layers; ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    StepLayer& s = hl[l];
+    s = StepLayer{};
+    s.full = L.full ? 1 : 0;
+    s.in_norm = L.in_norm; s.post_norm = L.post_norm;
+    s.qkv_q = L.qkv.q; s.qkv_s = L.qkv.s; s.z_q = L.z.q; s.z_s = L.z.s; s.out_q = L.out.q; s.out_s = L.out.s;
+    s.w_b = L.w_b; s.w_a = L.w_a; s.a_log = L.a_log; s.dt_bias = L.dt_bias; s.conv_w = L.conv_w; s.norm_w = L.norm_w;
+    s.conv_state = L.conv_state; s.rec = L.rec;
+    s.q_q = L.q.q; s.q_s = L.q.s; s.k_q = L.k.q; s.k_s = L.k.s; s.v_q = L.v.q; s.v_s = L.v.s; s.o_q = L.o.q; s.o_s = L.o.s;
+    s.q_norm = L.q_norm; s.k_norm = L.k_norm; s.kc = L.kc; s.vc = L.vc;
+    s.gate_q = L.gate.q; s.gate_s = L.gate.s; s.up_q = L.up.q; s.up_s = L.up.s; s.down_q = L.down.q; s.down_s = L.down.s;
+  }
+  StepLayer* dl = nullptr;
+  uint32_t* bar = nullptr;
+  float *att_ml = nullptr, *att_o = nullptr, *arg_v = nullptr;
+  int32_t* arg_i = nullptr;
+  int rc;
+  if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
+      (rc = dev_alloc_t(m, "step_barrier", kStepBarBytes / 4, &bar)) ||
+      (rc = dev_alloc_t(m, "attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
+      (rc = dev_alloc_t(m, "attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
+      (rc = dev_alloc_t(m, "argmax_partial_v", (size_t)grid, &arg_v)) ||
+      (rc = dev_alloc_t(m, "argmax_partial_i", (size_t)grid, &arg_i)))
+    return rc;
+  Q35_HIP_TRY(hipMemcpy(dl, hl.data(), hl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+  Q35_HIP_TRY(hipMemset(bar, 0, kStepBarBytes));
+  StepArgs& a = m->step_args;
+  a.layers = dl; a.n_layers = d.n_layers;
+  a.H = d.hidden; a.F = d.ffn; a.V = d.vocab; a.nh = nh; a.dk = d.lin_dk; a.dv = d.lin_dv;
+  a.key_dim = nh * d.lin_dk; a.vdim = nh * d.lin_dv; a.conv_dim = 2 * a.key_dim + a.vdim;
+  a.ah = d.attn_heads; a.kvh = kvh; a.hd = d.head_dim; a.rot = d.rot_dim; a.tmax = m->tmax;
+  a.eps = d.eps;
+  a.qscale = powf((float)d.lin_dk, -0.5f);
+  a.ascale = (float)(1.0 / sqrt((double)d.head_dim));
+  step_plan(d, grid, a.mv);
+  a.emb_q = m->embed.q; a.emb_s = m->embed.s; a.final_norm = m->final_norm;
+  a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
+  a.h = m->h; a.acc_proj = m->acc_proj; a.acc_ba = m->acc_ba; a.acc_gu = m->acc_gu;
+  a.acc_zero_n = m->acc_proj_n + 2 * nh;
+  a.o_raw = m->o_raw; a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
+  a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
+  a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
+  a.bar = bar;
+  a.ntok = 0;
+  return Q35_OK;
+}
+
 void destroy(q35_model* m) {
   if (!m) return;
   if (m->exec) (void)hipGraphExecDestroy(m->exec);
@@ -190,8 +257,30 @@ int capture(q35_model* m, hipStream_t st) {
   return Q35_OK;
 }
 
+// n consecutive steps in one launch of the persistent kernel
+int persistent(q35_model* m, int n, hipStream_t st) {
+  if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
+  if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
+  StepArgs a = m->step_args;
+  a.ntok = n;
+  int rc = step_launch(a, m->step_grid, st);
+  if (rc) return rc;
+  m->host_pos += n;
+  return Q35_OK;
+}
+
+// Reads the persistent kernel's error word (synchronises the stream).
+int check_persistent(q35_model* m, hipStream_t st) {
+  if (m->step_rc != Q35_OK) return Q35_OK;
+  Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 8, m->step_args.bar + kStepErrWord, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  if (m->pinned[8] != 0) return fail(Q35_E_HIP, "persistent step: a grid barrier timed out; results are invalid");
+  return Q35_OK;
+}
+
 int step(q35_model* m, int use_graph, hipStream_t st) {
   if (m->host_pos >= m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
+  if (use_graph == Q35_LAUNCH_PERSISTENT) return persistent(m, 1, st);
   if (use_graph) {
     int rc = capture(m, st);
     if (rc) return rc;
@@ -337,6 +426,7 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
   if (hipHostMalloc(reinterpret_cast<void**>(&m->pinned), 64 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
     return bail(fail(Q35_E_NOMEM, "hipHostMalloc failed"));
   if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(fail(Q35_E_HIP, "workspace clear"));
+  if ((rc = setup_persistent(m))) return bail(rc);
   if ((rc = q35_model_reset(m, nullptr))) return bail(rc);
   if (hipStreamSynchronize(m->own_stream) != hipSuccess) return bail(fail(Q35_E_HIP, "sync"));
   *out = m;
@@ -378,7 +468,34 @@ int q35_model_set_token(q35_model* m, int32_t token, void* stream) {
 
 int q35_model_step(q35_model* m, int32_t use_graph, void* stream) {
   if (!m) return fail(Q35_E_ARG, "model_step: null model");
+  if (use_graph < Q35_LAUNCH_STREAM || use_graph > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_step: bad launch mode");
   return step(m, use_graph, pick(m, stream));
+}
+
+int q35_model_decode(q35_model* m, int32_t n_steps, int32_t mode, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_decode: null model");
+  if (mode < Q35_LAUNCH_STREAM || mode > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_decode: bad launch mode");
+  if (n_steps < 0) return fail(Q35_E_SHAPE, "model_decode: n_steps must be >= 0");
+  if ((int64_t)m->host_pos + n_steps > m->tmax) return fail(Q35_E_SHAPE, "model_decode: tmax too small");
+  hipStream_t st = pick(m, stream);
+  if (mode == Q35_LAUNCH_PERSISTENT) return n_steps ? persistent(m, n_steps, st) : Q35_OK;
+  for (int i = 0; i < n_steps; ++i) {
+    const int rc = step(m, mode, st);
+    if (rc) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_model_check(q35_model* m, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_check: null model");
+  return check_persistent(m, pick(m, stream));
+}
+
+int q35_model_persistent_info(q35_model* m, int32_t* grid_out) {
+  if (!m) return fail(Q35_E_ARG, "model_persistent_info: null model");
+  if (grid_out) *grid_out = m->step_grid;
+  if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
+  return Q35_OK;
 }
 
 int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t n_new,
@@ -397,20 +514,30 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
   Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
   Q35_HIP_TRY(hipStreamSynchronize(st));
   int rc;
-  if (use_graph && (rc = capture(m, st))) return rc;
-  for (int i = 0; i < n_prompt; ++i)
-    if ((rc = step(m, use_graph, st))) return rc;
+  const bool pers = (use_graph == Q35_LAUNCH_PERSISTENT);
+  if (use_graph == Q35_LAUNCH_GRAPH && (rc = capture(m, st))) return rc;
+  if (pers) {
+    if ((rc = persistent(m, n_prompt, st))) return rc;
+  } else {
+    for (int i = 0; i < n_prompt; ++i)
+      if ((rc = step(m, use_graph, st))) return rc;
+  }
   Q35_HIP_TRY(hipStreamSynchronize(st));
   const auto t0 = std::chrono::steady_clock::now();
-  for (int i = 0; i < n_new; ++i) {
-    if ((rc = step(m, use_graph, st))) return rc;
-    if (readback_each) {  // main.rs:107: the token goes to the host every step
-      Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
-      Q35_HIP_TRY(hipStreamSynchronize(st));
+  if (pers && !readback_each) {
+    if ((rc = persistent(m, n_new, st))) return rc;
+  } else {
+    for (int i = 0; i < n_new; ++i) {
+      if ((rc = step(m, use_graph, st))) return rc;
+      if (readback_each) {  // main.rs:107: the token goes to the host every step
+        Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        Q35_HIP_TRY(hipStreamSynchronize(st));
+      }
     }
   }
   Q35_HIP_TRY(hipStreamSynchronize(st));
   const auto t1 = std::chrono::steady_clock::now();
+  if (pers && (rc = check_persistent(m, st))) return rc;
   if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
   Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + p0 + n_prompt - 1, sizeof(int32_t) * (n_new + 1), hipMemcpyDeviceToHost));
   return Q35_OK;

@@ -42,8 +42,6 @@ Q35_DEV float nk_in(const NkArgs& a, int m, int k) {
   return a.xf ? from_fx(a.xf[i]) : a.x[i];
 }
 
-Q35_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
-
 // (max, lowest index) over the n published block results, 8 loads in flight per thread.
 Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& v, int& i) {
   v = -INFINITY;
@@ -59,16 +57,7 @@ Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& 
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (better(vv[j], ii[j], v, i)) { v = vv[j]; i = ii[j]; }
-  }
-}
-
-Q35_DEV void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    int oi = __shfl_xor(i, o, 64);
-    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+      if (argmax_better(vv[j], ii[j], v, i)) { v = vv[j]; i = ii[j]; }
   }
 }
 
@@ -82,31 +71,7 @@ Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
   v = shv[0]; i = shi[0];
 #pragma unroll
   for (int w = 1; w < 4; ++w)
-    if (better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
-}
-
-// Transposed butterfly over R per-lane row partials: on return every lane holds the full sum of
-// row (lane / (64 / R)).
-template <int R>
-Q35_DEV float fold_rows(float (&p)[R], int lane) {
-  int cnt = R;
-#pragma unroll
-  for (int s = 32; s >= 64 / R; s >>= 1) {
-    const int half = cnt / 2;
-    const bool hi = (lane & s) != 0;
-#pragma unroll
-    for (int i = 0; i < R / 2; ++i) {
-      if (i >= half) break;
-      const float snd = hi ? p[i] : p[i + half];
-      const float keep = hi ? p[i + half] : p[i];
-      p[i] = keep + __shfl_xor(snd, s, 64);
-    }
-    cnt = half;
-  }
-  float v = p[0];
-#pragma unroll
-  for (int s = 32 / R; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
-  return v;
+    if (argmax_better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
 }
 
 template <int MR, int CPW>

@@ -77,6 +77,55 @@ Q35_DEV int32_t ld_agent(const int32_t* p) {
   return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+Q35_DEV fx_t ld_agent(const fx_t* p) {
+  return __hip_atomic_load(const_cast<fx_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+Q35_DEV void st_agent(fx_t* p, fx_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (max, lowest index) order used by every argmax: a total order, so any reduction tree gives
+// the same winner.
+Q35_DEV bool argmax_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+Q35_DEV void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (argmax_better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// Transposed butterfly over R per-lane row partials: on return every lane holds the full sum of
+// row (lane / (64 / R)).  Stage S (32, 16, ...) halves the rows a lane keeps: lanes with bit S
+// set keep the upper half and receive their partner's copy of it, the others the lower half;
+// then the 64/R lanes sharing a row finish the sum: log2(R) + log2(64/R) exchanges for R rows.
+// Written as compile-time recursion so every index into p is a constant (no private memory).
+template <int R, int CNT, int S>
+Q35_DEV void fold_stage(float (&p)[R], int lane) {
+  if constexpr (CNT > 1) {
+    constexpr int half = CNT / 2;
+    const bool hi = (lane & S) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float snd = hi ? p[i] : p[i + half];
+      const float keep = hi ? p[i + half] : p[i];
+      p[i] = keep + __shfl_xor(snd, S, 64);
+    }
+    fold_stage<R, half, S / 2>(p, lane);
+  }
+}
+template <int R>
+Q35_DEV float fold_rows(float (&p)[R], int lane) {
+  static_assert(R >= 1 && R <= 64 && (R & (R - 1)) == 0, "R must be a power of two <= 64");
+  fold_stage<R, R, 32>(p, lane);
+  float v = p[0];
+#pragma unroll
+  for (int s = 32 / R; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+  return v;
+}
+
 // sum_{i<n} p[i*stride] in index order.  Loads are issued kSumBatch at a time so their latency
 // overlaps (a loop that adds each value as it arrives would wait for every load in turn).
 #ifndef Q35_SUM_BATCH
@@ -153,7 +202,7 @@ Q35_DEV bool arrive_last_grid(uint32_t* counters, int* sh_flag) {
 }
 
 // ------------------------------------------------------------------ Q8F KN matvec (split-K)
-enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_SWIGLU = 3, PRO_EMBED_RMS = 4 };
+enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_SWIGLU = 3, PRO_EMBED_RMS = 4, PRO_ATTN = 5 };
 struct MvSeg {
   const int8_t* w;  // [K][N]
   const float* s;   // [K][N/64]
@@ -283,5 +332,55 @@ size_t attn_ws_bytes(int32_t B, int32_t nh, int32_t nkv, int32_t hd, int32_t tma
 int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st);
 // same, with the completion counters and the chunk-partial scratch given separately
 int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size_t scratch_bytes, hipStream_t st);
+
+// ------------------------------------------------------------------ persistent decode step
+// Per-layer pointers of the persistent decode-step kernel (Q8F projections in Q35_KN_TILED).
+struct StepLayer {
+  int32_t full;
+  const float *in_norm, *post_norm;
+  const int8_t *qkv_q, *z_q, *out_q;
+  const float *qkv_s, *z_s, *out_s;
+  const float *w_b, *w_a, *a_log, *dt_bias, *conv_w, *norm_w;
+  float *conv_state, *rec;
+  const int8_t *q_q, *k_q, *v_q, *o_q;
+  const float *q_s, *k_s, *v_s, *o_s;
+  const float *q_norm, *k_norm;
+  float *kc, *vc;
+  const int8_t *gate_q, *up_q, *down_q;
+  const float *gate_s, *up_s, *down_s;
+};
+// split-K plan of one matvec stage: item = (256-column tile, chunk of kch rows)
+struct StepMv { int32_t kch, nchunk; };
+enum { SMV_QKVZ = 0, SMV_OUT, SMV_QKV, SMV_O, SMV_GU, SMV_DOWN, SMV_COUNT };
+struct StepArgs {
+  const StepLayer* layers;
+  int32_t n_layers;
+  int32_t H, F, V, nh, dk, dv, conv_dim, key_dim, vdim, ah, kvh, hd, rot, tmax;
+  float eps, qscale, ascale;
+  StepMv mv[SMV_COUNT];
+  const int8_t* emb_q; const float* emb_s; const float* final_norm;
+  const float *rope_cos, *rope_sin;
+  fx_t *h, *acc_proj, *acc_ba, *acc_gu;
+  int64_t acc_zero_n;  // acc_proj + acc_ba entries cleared by the gate|up stage
+  float *o_raw, *att_ml, *att_o;
+  int32_t att_nmax;    // attention chunks per kv head
+  float* logits;       // may be null
+  float* arg_v; int32_t* arg_i;  // per-block argmax partials [grid]
+  int32_t *token, *pos, *prompt, *plen, *hist;
+  uint32_t* bar;       // barrier counters (kStepBarBytes, zero at launch); bar[kStepErrWord] = error flag
+  int32_t ntok;
+};
+constexpr size_t kStepBarBytes = 16384;
+constexpr int kStepErrWord = 3072;
+constexpr int kStepThreads = 512;
+// Blocks of the persistent kernel that fit co-resident (one per CU); 0 if the kernel cannot run.
+int step_grid(int hidden);
+// Attention chunks per kv head for a grid (the merge keeps their weights in LDS).
+int step_att_nmax(int grid, int kvh);
+// Checks dims / tmax against the kernel's limits.
+int step_validate(const q35_dims& d, int tmax, int grid);
+// Plans the split-K of every matvec stage for `grid` blocks.
+void step_plan(const q35_dims& d, int grid, StepMv* mv);
+int step_launch(const StepArgs& a, int grid, hipStream_t st);
 
 }  // namespace q35

@@ -1,0 +1,962 @@
+// Persistent decode step: the whole TextForCausalLM forward at seq_len 1 (model.rs:27-84,
+// 113-129) plus the greedy argmax (main.rs:131), for `ntok` consecutive tokens, in ONE launch.
+//
+// Why: a decode step streams ~2 GB of Q8F weights through ~120 dependent stages.  As separate
+// kernels every stage boundary costs a launch gap plus a ramp-up/drain with HBM idle; here the
+// grid is one co-resident block per CU (cooperative launch) and stages are separated by a grid
+// barrier.  Each block issues the weight loads of its next stage *between* arriving at the
+// barrier and polling it, so the weight stream of stage s+1 overlaps the barrier latency and
+// the tail of stage s.
+//
+// Stages per token (each ends with a grid barrier):
+//   linear-attention layer: qkvz  [RMSNorm(h) or embedding -> in_proj_qkv|in_proj_z; in_proj_b|a]
+//                           gdn   [conv1d + SiLU, l2norm, gated delta rule step]
+//                           out   [gated RMSNorm(o, z) -> out_proj -> +h; conv-state shift]
+//   full-attention layer:   qkv   [RMSNorm(h) or embedding -> q|gate, k, v]
+//                           attn  [q/k RMSNorm, RoPE, KV append, split-T softmax partials]
+//                           o     [merge attention partials * sigmoid(gate) -> o_proj -> +h]
+//   MLP:                    gu    [RMSNorm(h) -> gate|up]
+//                           down  [SwiGLU -> down_proj -> +h]
+//   head:                   lm    [final RMSNorm -> tied lm_head -> logits, block argmax]
+// The next token's first stage reduces the block argmaxes (or takes the prompt id).
+//
+// Matvec stages use the split-K decomposition of the standalone KN kernel on the tile-major
+// layout: an item is (256-column tile, kch rows); 512 threads = 16 column groups x 32 row
+// groups, every lane holds up to 16 rows (16-byte loads) of its item in registers; partial
+// sums go through LDS and then 64-bit fixed-point atomics (fx_add) into the output.  Every
+// value exchanged between blocks inside the launch is written with agent-scope atomics or
+// sc1 stores and read with sc1 loads (no stale per-CU / per-XCD cache lines).
+//
+// Barrier: blocks arrive on one of 32 group counters (blockIdx % 32) with a non-returning
+// atomic after their stores have completed; the waiting wave reads all group counters with one
+// load per lane.  Counters only grow within a launch (zeroed by the host before it), so the
+// target of the n-th barrier is (blocks in group) * n.  Every wait is bounded: on time-out the
+// block sets the error word and returns, and the other blocks see the word and return too, so
+// the grid always drains.
+#include "q35_internal.h"
+
+#include <algorithm>
+#include <climits>
+
+namespace q35 {
+
+namespace {
+
+constexpr int kT = kStepThreads;  // 512
+constexpr int kNW = kT / 64;      // waves per block
+constexpr int kTile = 256;
+constexpr int kRG = kT / 16;      // matvec row groups (16 lanes cover a 256-byte tile row)
+constexpr int kU = 16;            // rows per lane per item
+constexpr int kKch = kRG * kU;    // rows per item, at most 512
+constexpr int kRmsRegs = 8;       // RMSNorm prologue: K <= 8 * 512
+constexpr int kGroups = 32;       // barrier counters
+constexpr int kCtrStride = 64;    // uint32 words between counters (own 256-byte line each)
+constexpr uint32_t kSpin = 1u << 20;
+constexpr int kHd = 256;          // attention head dim
+constexpr int kMaxRep = 4;        // query heads per kv head
+constexpr int kMaxChunk = 256;    // cached tokens per attention item
+constexpr int kMinChunk = 8;
+constexpr int kMaxNmax = 256;     // attention chunks per kv head
+constexpr int kMaxTouch = 8;      // norm groups / heads one matvec item's rows can span
+constexpr int kDk = 128;          // DeltaNet key head dim
+constexpr int kCS = 8;            // DeltaNet value columns per item
+constexpr int kSmem = 12288;      // floats of LDS shared by all stages (48 KB)
+
+// LDS carve-up (float offsets)
+constexpr int kXs = 0;                  // matvec x chunk [kKch]
+constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
+constexpr int kGrp = kRed + kRG * kTile;  // gated-norm factors [kMaxTouch]
+static_assert(kGrp + kMaxTouch <= kSmem, "LDS");
+static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
+
+// threadIdx.x / blockIdx.x read through an empty asm: every use is then loop-variant, so each
+// stage recomputes its per-thread address arithmetic instead of the compiler hoisting it out of
+// the token / layer loops and keeping it live (spilled to scratch) across the whole kernel.
+Q35_DEV int tix() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+Q35_DEV int bix() {
+  int b = blockIdx.x;
+  asm volatile("" : "+s"(b));
+  return b;
+}
+
+struct Shared {
+  float* smem;
+  float* shs;  // [kNW] block sums
+  float* shv;  // [kNW] argmax values
+  int* shi;    // [kNW] argmax indices
+  int* ok;
+};
+
+// ------------------------------------------------------------------ block reductions
+Q35_DEV float block_sum(float v, float* shs) {
+  v = wave_sum(v);
+  const int lane = tix() & 63, wid = tix() >> 6;
+  __syncthreads();
+  if (lane == 0) shs[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNW; ++w) t += shs[w];
+  return t;
+}
+
+Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
+  wave_argmax(v, i);
+  const int lane = tix() & 63, wid = tix() >> 6;
+  __syncthreads();
+  if (lane == 0) { shv[wid] = v; shi[wid] = i; }
+  __syncthreads();
+  v = shv[0];
+  i = shi[0];
+#pragma unroll
+  for (int w = 1; w < kNW; ++w)
+    if (argmax_better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
+}
+
+Q35_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+Q35_DEV float4 ld4_agent(const float* p) {
+  return make_float4(ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3));
+}
+Q35_DEV float4 ld4_fx(const fx_t* p) {
+  return make_float4(from_fx(ld_agent(p)), from_fx(ld_agent(p + 1)), from_fx(ld_agent(p + 2)), from_fx(ld_agent(p + 3)));
+}
+
+// ------------------------------------------------------------------ grid barrier
+struct Bar {
+  uint32_t* ctr;
+  uint32_t* err;
+  uint32_t epoch;  // barriers passed so far by this block
+};
+
+// Publishes this block's completion of the current stage: all of its memory operations are
+// complete (s_waitcnt 0 in every wave, then the workgroup barrier) before the counter add.
+Q35_DEV void bar_arrive(Bar& b) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tix() == 0)
+    __hip_atomic_fetch_add(&b.ctr[(bix() % kGroups) * kCtrStride], 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  b.epoch += 1;
+}
+
+// Waits until every block has arrived `epoch` times.  Wave 0 polls: lane g < 32 reads group
+// counter g.  Returns false (in every thread of the block) on time-out or when another block
+// has raised the error word.
+Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
+  if (tix() < 64) {
+    const int g = tix();
+    const uint32_t nb = gridDim.x;
+    const uint32_t per = g < kGroups ? (nb + kGroups - 1 - (uint32_t)g) / kGroups : 0u;
+    const uint32_t target = per * b.epoch;
+    uint32_t spin = 0;
+    bool ok = true;
+    while (true) {
+      const uint32_t v = g < kGroups ? ld_agent(&b.ctr[g * kCtrStride]) : 0xffffffffu;
+      const uint32_t e = ld_agent(b.err);
+      if (__all(v >= target)) break;
+      if (e != 0u || ++spin > kSpin) { ok = false; break; }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (tix() == 0) {
+      if (!ok) __hip_atomic_fetch_or(b.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *sh_ok = ok ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  return *sh_ok != 0;
+}
+
+// ------------------------------------------------------------------ matvec stages
+struct Mv {
+  const int8_t *w0, *w1, *w2;
+  const float *s0, *s1, *s2;
+  fx_t *a0, *a1, *a2;
+  int n0, n1, n2;
+  int t1, t2, t3;  // first tile of segments 1 and 2, total tiles
+  int K, kch, nchunk;
+};
+
+Q35_DEV int tiles_of(int n) { return (n + kTile - 1) / kTile; }
+
+Q35_DEV Mv make_mv(const StepArgs& a, const StepLayer& L, int kind) {
+  Mv d{};
+  const StepMv pl = a.mv[kind];
+  d.kch = pl.kch;
+  d.nchunk = pl.nchunk;
+  switch (kind) {
+    case SMV_QKVZ:
+      d.K = a.H;
+      d.w0 = L.qkv_q; d.s0 = L.qkv_s; d.a0 = a.acc_proj; d.n0 = a.conv_dim;
+      d.w1 = L.z_q; d.s1 = L.z_s; d.a1 = a.acc_proj + a.conv_dim; d.n1 = a.vdim;
+      d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2;
+      break;
+    case SMV_OUT:
+      d.K = a.vdim;
+      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = a.h; d.n0 = a.H;
+      d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
+      break;
+    case SMV_QKV: {
+      const int ldqg = a.ah * a.hd * 2, nkv = a.kvh * a.hd;
+      d.K = a.H;
+      d.w0 = L.q_q; d.s0 = L.q_s; d.a0 = a.acc_proj; d.n0 = ldqg;
+      d.w1 = L.k_q; d.s1 = L.k_s; d.a1 = a.acc_proj + ldqg; d.n1 = nkv;
+      d.w2 = L.v_q; d.s2 = L.v_s; d.a2 = a.acc_proj + ldqg + nkv; d.n2 = nkv;
+      d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2 + tiles_of(d.n2);
+    } break;
+    case SMV_O:
+      d.K = a.ah * a.hd;
+      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = a.h; d.n0 = a.H;
+      d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
+      break;
+    case SMV_GU:
+      d.K = a.H;
+      d.w0 = L.gate_q; d.s0 = L.gate_s; d.a0 = a.acc_gu; d.n0 = a.F;
+      d.w1 = L.up_q; d.s1 = L.up_s; d.a1 = a.acc_gu + a.F; d.n1 = a.F;
+      d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2;
+      break;
+    default:  // SMV_DOWN
+      d.K = a.F;
+      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = a.h; d.n0 = a.H;
+      d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
+      break;
+  }
+  return d;
+}
+
+struct MvItem {
+  const int8_t* w;
+  const float* s;
+  fx_t* acc;
+  int N, tile, tl, k0, klen;
+};
+
+Q35_DEV MvItem mv_item(const Mv& d, int item) {
+  MvItem it;
+  const int tile = item / d.nchunk, ch = item - tile * d.nchunk;
+  it.tile = tile;
+  if (tile < d.t1) { it.w = d.w0; it.s = d.s0; it.acc = d.a0; it.N = d.n0; it.tl = tile; }
+  else if (tile < d.t2) { it.w = d.w1; it.s = d.s1; it.acc = d.a1; it.N = d.n1; it.tl = tile - d.t1; }
+  else { it.w = d.w2; it.s = d.s2; it.acc = d.a2; it.N = d.n2; it.tl = tile - d.t2; }
+  it.k0 = ch * d.kch;
+  it.klen = min(d.kch, d.K - it.k0);
+  return it;
+}
+
+struct MvPf {
+  uint4 w[kU];
+  float s[kU];
+};
+
+// Lane (cg, rr) loads 16 columns [cg*16, cg*16+16) of rows rr, rr+32, ... of the item.
+Q35_DEV void mv_load(const MvItem& it, int K, MvPf& pf) {
+  // 32-bit offsets from the matrix base (every tiled matrix is < 4 GB) keep the addresses in
+  // one VGPR each
+  const int cg = tix() & 15, rr = tix() >> 4;
+  const bool colok = it.tl * kTile + cg * 16 < it.N;
+  const uint32_t row0 = (uint32_t)it.tl * (uint32_t)K + (uint32_t)it.k0 + (uint32_t)rr;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int r = rr + kRG * u;
+    const bool ok = colok && r < it.klen;
+    const uint32_t row = row0 + (uint32_t)(kRG * u);
+    pf.w[u] = ok ? *reinterpret_cast<const uint4*>(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16))) : make_uint4(0, 0, 0, 0);
+    pf.s[u] = ok ? it.s[row * (uint32_t)(kTile / 64) + (uint32_t)(cg >> 2)] : 0.f;
+  }
+}
+
+// y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.
+Q35_DEV void mv_compute(const MvItem& it, const MvPf& pf, const float* xs, float* red) {
+  const int tid = tix(), cg = tid & 15, rr = tid >> 4;
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    if (kRG * u >= it.klen) break;
+    const int r = rr + kRG * u;
+    const float c = (r < it.klen) ? xs[r] * pf.s[u] : 0.f;
+    float f[16];
+    unpack16(pf.w[u], f);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] += f[j] * c;
+  }
+  float4* dst = reinterpret_cast<float4*>(&red[rr * kTile + cg * 16]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dst[q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+  __syncthreads();
+  if (tid < kTile) {
+    float v = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < kRG; ++i) v += red[i * kTile + tid];
+    const int n = it.tl * kTile + tid;
+    if (n < it.N) fx_add(&it.acc[n], v);
+  }
+  __syncthreads();
+}
+
+// xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j].
+template <class Src>
+Q35_DEV void pro_rms(Src src, int K, const float* w, float eps, int k0, int klen, float* xs, float* shs) {
+  const int tid = tix();
+  float v[kRmsRegs];
+#pragma unroll
+  for (int j = 0; j < kRmsRegs; ++j) {
+    const int k = tid + kT * j;
+    v[j] = (k < K) ? src(k) : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRmsRegs; ++j) ss += v[j] * v[j];
+  ss = block_sum(ss, shs);
+  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+  for (int j = 0; j < kRmsRegs; ++j) {
+    const int k = tid + kT * j;
+    if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + w[k]);
+  }
+}
+
+// Token of step i at position p: the prompt id while p < plen, else the argmax of the previous
+// step (reduced here from the per-block partials), or *token for the launch's first step.
+// Block 0 records the previous step's argmax in hist.
+Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
+  int tok;
+  if (i == 0) {
+    tok = ld_agent(a.token);
+  } else {
+    float v = -INFINITY;
+    int ix = INT_MAX;
+    if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
+    block_argmax(v, ix, sh.shv, sh.shi);
+    tok = (ix == INT_MAX) ? 0 : ix;
+    if (bix() == 0 && tix() == 0) st_agent(&a.hist[p - 1], tok);
+  }
+  if (p < *a.plen) tok = a.prompt[p];
+  return tok;
+}
+
+// Gated RMSNorm per group of G = dv (text_modules.rs RMSNormGated): x = w[k%G] * (o * r_g) * silu(z)
+Q35_DEV void pro_gated(const StepArgs& a, const StepLayer& L, int k0, int klen, float* xs, float* grp) {
+  const int G = a.dv, lane = tix() & 63, wid = tix() >> 6;
+  const int g0 = k0 / G, g1 = (k0 + klen - 1) / G;
+  for (int gi = g0 + wid; gi <= g1; gi += kNW) {
+    float ss = 0.f;
+    for (int i = lane; i < G; i += 64) {
+      const float v = ld_agent(&a.o_raw[gi * G + i]);
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) grp[gi - g0] = 1.0f / sqrtf(ss / (float)G + a.eps);
+  }
+  __syncthreads();
+  for (int i = tix(); i < klen; i += kT) {
+    const int k = k0 + i;
+    const float r = grp[k / G - g0];
+    const float z = from_fx(ld_agent(&a.acc_proj[a.conv_dim + k]));
+    xs[i] = (L.norm_w[k % G] * (ld_agent(&a.o_raw[k]) * r)) * silu_f(z);
+  }
+}
+
+Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
+  chunk = max(kMinChunk, (T + a.att_nmax - 1) / a.att_nmax);
+  nact = (T + chunk - 1) / chunk;
+}
+
+// o_proj input: merge the split-T partials of each touched query head (flash-decoding merge,
+// chunks in order) and apply the sigmoid output gate (text_modules.rs:936).
+Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, float* scratch) {
+  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int rep = a.ah / a.kvh;
+  int chunk, nact;
+  attn_chunking(a, T, chunk, nact);
+  float* wts = scratch;                         // [kMaxTouch][kMaxNmax] exp(m_c - M)
+  float* pbuf = scratch + kMaxTouch * kMaxNmax; // [kT] per-part sums
+  float* wl = pbuf + kT;                        // [kMaxTouch] L
+  const int h0 = k0 / kHd, h1 = (k0 + klen - 1) / kHd;
+  for (int hh = h0 + wid; hh <= h1; hh += kNW) {
+    const int g = hh / rep, hr = hh % rep;
+    const float* ml = a.att_ml + (size_t)g * a.att_nmax * 2 * kMaxRep;
+    float M = -INFINITY;
+    for (int c = lane; c < nact; c += 64) M = fmaxf(M, ld_agent(&ml[c * 2 * kMaxRep + hr]));
+    M = wave_max(M);
+    float Ls = 0.f;
+    for (int c = lane; c < nact; c += 64) {
+      const float w = expf(ld_agent(&ml[c * 2 * kMaxRep + hr]) - M);
+      wts[(hh - h0) * kMaxNmax + c] = w;
+      Ls += ld_agent(&ml[c * 2 * kMaxRep + kMaxRep + hr]) * w;
+    }
+    Ls = wave_sum(Ls);
+    if (lane == 0) wl[hh - h0] = Ls;
+  }
+  __syncthreads();
+  const int parts = klen <= 64 ? 8 : (klen <= 128 ? 4 : (klen <= 256 ? 2 : 1));
+  const int span = kT / parts;
+  const int i = tid % span, part = tid / span;
+  float o = 0.f;
+  if (i < klen) {
+    const int k = k0 + i, hh = k / kHd, d = k % kHd, g = hh / rep, hr = hh % rep;
+    const float* og = a.att_o + ((size_t)g * a.att_nmax * kMaxRep + hr) * kHd + d;  // + c*kMaxRep*kHd
+    const float* w = wts + (hh - h0) * kMaxNmax;
+    for (int c0 = part; c0 < nact; c0 += 8 * parts) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = c0 + j * parts;
+        v[j] = (c < nact) ? ld_agent(&og[(size_t)c * kMaxRep * kHd]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = c0 + j * parts;
+        if (c < nact) o += v[j] * w[c];
+      }
+    }
+  }
+  pbuf[part * span + i] = o;
+  __syncthreads();
+  if (tid < klen) {
+    float s = 0.f;
+    for (int q = 0; q < parts; ++q) s += pbuf[q * span + tid];
+    const int k = k0 + tid, hh = k / kHd, d = k % kHd;
+    const float gv = from_fx(ld_agent(&a.acc_proj[(size_t)hh * 2 * kHd + kHd + d]));
+    xs[tid] = (s / wl[hh - h0]) * sigmoid_f(gv);
+  }
+}
+
+// Side tasks that run right after a stage's barrier (their inputs are final, their outputs are
+// not read before the next barrier), spread over every thread of the grid.
+Q35_DEV void side_tasks(const StepArgs& a, const StepLayer& L, int kind) {
+  const int64_t gt = (int64_t)bix() * kT + tix(), gs = (int64_t)gridDim.x * kT;
+  if (kind == SMV_QKVZ || kind == SMV_QKV) {  // gate|up accumulator: last read by the previous down stage
+    for (int64_t i = gt; i < 2 * (int64_t)a.F; i += gs) st_agent(&a.acc_gu[i], (fx_t)0);
+  } else if (kind == SMV_GU) {  // projection + gate accumulators: last read by the out / o stage
+    for (int64_t i = gt; i < a.acc_zero_n; i += gs) st_agent(&a.acc_proj[i], (fx_t)0);
+  } else if (kind == SMV_OUT) {  // causal-conv state [c][3] <- [s1, s2, x_c] (text_modules.rs:134-162)
+    for (int64_t c = gt; c < a.conv_dim; c += gs) {
+      float* st = L.conv_state + c * 3;
+      const float s1 = ld_agent(&st[1]), s2 = ld_agent(&st[2]);
+      const float x = from_fx(ld_agent(&a.acc_proj[c]));
+      st_agent(&st[0], s1);
+      st_agent(&st[1], s2);
+      st_agent(&st[2], x);
+    }
+  }
+}
+
+// One matvec stage.  The in_proj_b / in_proj_a gate projection (f32, [H][nh] each,
+// kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
+// dot product of its rows with column t of [W_b | W_a].
+Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, int i, int p, Bar& bar,
+                      const Shared& sh) {
+  const Mv d = make_mv(a, L, kind);
+  const int nitems = d.t3 * d.nchunk;
+  int item = bix();
+  MvPf pf;
+  MvItem it{};
+  float auxw = 0.f;
+  const int naux = 2 * a.nh;
+  if (item < nitems) {
+    it = mv_item(d, item);
+    mv_load(it, d.K, pf);
+    if (kind == SMV_QKVZ && it.tile < naux && tix() < it.klen) {
+      const float* W = it.tile < a.nh ? L.w_b : L.w_a;
+      auxw = W[(size_t)(it.k0 + tix()) * a.nh + (it.tile % a.nh)];
+    }
+  }
+  if (!bar_wait(bar, sh.ok)) return false;
+  side_tasks(a, L, kind);
+  int tok = 0;
+  if (pro == PRO_EMBED_RMS && item < nitems) tok = select_token(a, i, p, sh);
+  float* xs = sh.smem + kXs;
+  float* red = sh.smem + kRed;
+  for (bool first = true; item < nitems; item += gridDim.x, first = false) {
+    if (!first) it = mv_item(d, item), mv_load(it, d.K, pf);
+    switch (pro) {
+      case PRO_EMBED_RMS: {
+        const int K = d.K, nbK = K >> 6;
+        const int8_t* eq = a.emb_q + (size_t)tok * K;
+        const float* es = a.emb_s + (size_t)tok * nbK;
+        auto src = [&](int k) { return (float)eq[k] * es[k >> 6]; };
+        pro_rms(src, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
+        if (bix() == 0 && first)  // the residual stream starts as the embedding row
+          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k], to_fx(src(k)));
+      } break;
+      case PRO_RMS: {
+        auto src = [&](int k) { return from_fx(ld_agent(&a.h[k])); };
+        pro_rms(src, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
+      } break;
+      case PRO_GATED:
+        pro_gated(a, L, it.k0, it.klen, xs, sh.smem + kGrp);
+        break;
+      case PRO_SWIGLU:
+        for (int r = tix(); r < it.klen; r += kT) {
+          const int k = it.k0 + r;
+          xs[r] = from_fx(ld_agent(&a.acc_gu[a.F + k])) * silu_f(from_fx(ld_agent(&a.acc_gu[k])));
+        }
+        break;
+      default:  // PRO_ATTN: merged attention output
+        pro_attn(a, p + 1, it.k0, it.klen, xs, red);
+        break;
+    }
+    __syncthreads();
+    if (kind == SMV_QKVZ) {
+      for (int o = it.tile; o < naux; o += d.t3) {
+        float w = auxw;
+        if (o != it.tile || !first) {
+          const float* W = o < a.nh ? L.w_b : L.w_a;
+          w = (tix() < it.klen) ? W[(size_t)(it.k0 + tix()) * a.nh + (o % a.nh)] : 0.f;
+        }
+        const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
+        const float s = block_sum(v, sh.shs);
+        if (tix() == 0) fx_add(&a.acc_ba[o], s);
+      }
+    }
+    mv_compute(it, pf, xs, red);
+  }
+  bar_arrive(bar);
+  return true;
+}
+
+// ------------------------------------------------------------------ Gated DeltaNet step
+Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
+  const float acc = ((w[0] * ld_agent(&st[0]) + w[1] * ld_agent(&st[1])) + w[2] * ld_agent(&st[2])) + w[3] * xin;
+  return silu_f(acc);
+}
+
+// Item (head h, 8 value columns): lane (row group ig = tid/8, column j = tid%8) holds
+// S[h][2ig, 2ig+1][col0 + j].  text_modules.rs:134-162 (conv), :184-187 (l2norm),
+// :365-443 (recurrent gated delta rule).
+Q35_DEV bool gdn_stage(const StepArgs& a, const StepLayer& L, Bar& bar, const Shared& sh) {
+  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int nsl = a.dv / kCS, nitems = a.nh * nsl;
+  const int j = tid % kCS, ig = tid / kCS, i0 = 2 * ig;
+  float* qk = sh.smem;            // [256] q | k after conv
+  float* vv = sh.smem + 256;      // [kCS]
+  float* red = sh.smem + 264;     // [kNW][kCS]
+  float* wsum = sh.smem + 264 + kNW * kCS;  // [4]
+  int item = bix();
+  float sr[2] = {0.f, 0.f};
+  auto sptr = [&](int it) {
+    const int h = it / nsl, sl = it % nsl;
+    return L.rec + ((size_t)h * kDk) * a.dv + sl * kCS + j;
+  };
+  if (item < nitems) {
+    float* Sp = sptr(item);
+    sr[0] = ld_agent(&Sp[(size_t)i0 * a.dv]);
+    sr[1] = ld_agent(&Sp[(size_t)(i0 + 1) * a.dv]);
+  }
+  if (!bar_wait(bar, sh.ok)) return false;
+  for (bool first = true; item < nitems; item += gridDim.x, first = false) {
+    const int h = item / nsl, sl = item % nsl, col0 = sl * kCS;
+    float* Sp = sptr(item);
+    if (!first) {
+      sr[0] = ld_agent(&Sp[(size_t)i0 * a.dv]);
+      sr[1] = ld_agent(&Sp[(size_t)(i0 + 1) * a.dv]);
+    }
+    if (tid < 2 * kDk) {  // q (tid < 128) and k channels of head h
+      const int c = (tid < kDk) ? h * kDk + tid : a.key_dim + h * kDk + (tid - kDk);
+      qk[tid] = conv4_silu(from_fx(ld_agent(&a.acc_proj[c])), L.conv_state + (size_t)c * 3, L.conv_w + (size_t)c * 4);
+    } else if (tid < 2 * kDk + kCS) {
+      const int c = 2 * a.key_dim + h * a.dv + col0 + (tid - 2 * kDk);
+      vv[tid - 2 * kDk] = conv4_silu(from_fx(ld_agent(&a.acc_proj[c])), L.conv_state + (size_t)c * 3, L.conv_w + (size_t)c * 4);
+    }
+    // gates: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias) (kernels.rs:228-244)
+    const float bs = from_fx(ld_agent(&a.acc_ba[h]));
+    const float as = from_fx(ld_agent(&a.acc_ba[a.nh + h]));
+    const float beta = 1.0f / (1.0f + expf(-bs));
+    const float xg = as + L.dt_bias[h];
+    const float pre = logf(expf(xg) + 1.0f);
+    const float g = -expf(L.a_log[h]) * (pre > 20.0f ? xg : pre);
+    __syncthreads();
+    if (wid < 4) {  // waves 0,1: q; waves 2,3: k
+      const float v = qk[tid];
+      const float ss = wave_sum(v * v);
+      if (lane == 0) wsum[wid] = ss;
+    }
+    __syncthreads();
+    const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
+    const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
+    const float q0 = (qk[i0] * rq) * a.qscale, q1 = (qk[i0 + 1] * rq) * a.qscale;
+    const float k0 = qk[kDk + i0] * rk, k1 = qk[kDk + i0 + 1] * rk;
+    const float decay = expf(g);
+    sr[0] *= decay;
+    sr[1] *= decay;
+    // S^T k for column j: lanes of a wave hold row groups 8w'..8w'+7 (lane = 8*(ig%8) + j)
+    float mp = sr[0] * k0 + sr[1] * k1;
+    mp += __shfl_xor(mp, 8, 64);
+    mp += __shfl_xor(mp, 16, 64);
+    mp += __shfl_xor(mp, 32, 64);
+    if (lane < kCS) red[wid * kCS + lane] = mp;
+    __syncthreads();
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) m += red[w * kCS + j];
+    const float delta = (vv[j] - m) * beta;
+    sr[0] += k0 * delta;
+    sr[1] += k1 * delta;
+    st_agent(&Sp[(size_t)i0 * a.dv], sr[0]);
+    st_agent(&Sp[(size_t)(i0 + 1) * a.dv], sr[1]);
+    float op = sr[0] * q0 + sr[1] * q1;
+    op += __shfl_xor(op, 8, 64);
+    op += __shfl_xor(op, 16, 64);
+    op += __shfl_xor(op, 32, 64);
+    __syncthreads();  // every lane has read red (m) before it is overwritten
+    if (lane < kCS) red[wid * kCS + lane] = op;
+    __syncthreads();
+    if (tid < kCS) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) o += red[w * kCS + tid];
+      st_agent(&a.o_raw[h * a.dv + col0 + tid], o);
+    }
+    __syncthreads();
+  }
+  bar_arrive(bar);
+  return true;
+}
+
+// ------------------------------------------------------------------ attention partials
+// Item (kv head g, chunk c of `chunk` cached tokens) for the rep query heads of g
+// (text_modules.rs:842-944): q/k RMSNorm (1+w), partial RoPE (:739-774), KV append at p
+// (the item holding p), scores, chunk softmax statistics and P.V.
+Q35_DEV bool attn_stage(const StepArgs& a, const StepLayer& L, int p, Bar& bar, const Shared& sh) {
+  if (!bar_wait(bar, sh.ok)) return false;
+  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int T = p + 1, rep = a.ah / a.kvh;
+  int chunk, nact;
+  attn_chunking(a, T, chunk, nact);
+  float* qn = sh.smem;               // [kMaxRep][kHd]
+  float* kn = qn + kMaxRep * kHd;    // [kHd]
+  float* vn = kn + kHd;              // [kHd]
+  float* rtmp = vn + kHd;            // [kMaxRep + 1][kHd]
+  float* sc = rtmp + (kMaxRep + 1) * kHd;  // [kMaxRep][kMaxChunk]
+  float* ored = sc + kMaxRep * kMaxChunk;  // [kNW][kMaxRep][kHd]
+  float* hm = ored + kNW * kMaxRep * kHd;  // [kMaxRep]
+  float* hl = hm + kMaxRep;                // [kMaxRep]
+  const int ldqg = a.ah * kHd * 2;
+  for (int item = bix(); item < a.kvh * nact; item += gridDim.x) {
+    const int g = item / nact, c = item % nact;
+    const int t0 = c * chunk, len = min(chunk, T - t0);
+    const bool has_new = (c == nact - 1);
+    for (int w = wid; w < rep + (has_new ? 2 : 0); w += kNW) {
+      const int d = 4 * lane;
+      if (w < rep) {
+        const float4 v = ld4_fx(&a.acc_proj[(size_t)(g * rep + w) * 2 * kHd + d]);
+        const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+        const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+        qn[w * kHd + d + 0] = (v.x * r) * (1.0f + L.q_norm[d + 0]);
+        qn[w * kHd + d + 1] = (v.y * r) * (1.0f + L.q_norm[d + 1]);
+        qn[w * kHd + d + 2] = (v.z * r) * (1.0f + L.q_norm[d + 2]);
+        qn[w * kHd + d + 3] = (v.w * r) * (1.0f + L.q_norm[d + 3]);
+      } else if (w == rep) {
+        const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)g * kHd + d]);
+        const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+        const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+        kn[d + 0] = (v.x * r) * (1.0f + L.k_norm[d + 0]);
+        kn[d + 1] = (v.y * r) * (1.0f + L.k_norm[d + 1]);
+        kn[d + 2] = (v.z * r) * (1.0f + L.k_norm[d + 2]);
+        kn[d + 3] = (v.w * r) * (1.0f + L.k_norm[d + 3]);
+      } else {
+        const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)(a.kvh + g) * kHd + d]);
+        *reinterpret_cast<float4*>(&vn[d]) = v;
+      }
+    }
+    __syncthreads();
+    // RoPE on dims [0, rot): x' = x*cos + rotate_half(x)*sin
+    const int half = a.rot / 2;
+    const float* cs = a.rope_cos + (size_t)p * a.rot;
+    const float* sn = a.rope_sin + (size_t)p * a.rot;
+    const int nrot = rep + (has_new ? 1 : 0);
+    for (int e = tid; e < nrot * a.rot; e += kT) {
+      const int hh = e / a.rot, ii = e % a.rot;
+      const float* src = (hh < rep) ? qn + hh * kHd : kn;
+      const float rh = (ii < half) ? -src[ii + half] : src[ii - half];
+      rtmp[hh * kHd + ii] = src[ii] * cs[ii] + rh * sn[ii];
+    }
+    __syncthreads();
+    for (int e = tid; e < nrot * a.rot; e += kT) {
+      const int hh = e / a.rot, ii = e % a.rot;
+      if (hh < rep) qn[hh * kHd + ii] = rtmp[hh * kHd + ii];
+      else kn[ii] = rtmp[hh * kHd + ii];
+    }
+    __syncthreads();
+    float* Kc = L.kc + (size_t)g * a.tmax * kHd;
+    float* Vc = L.vc + (size_t)g * a.tmax * kHd;
+    if (has_new) {  // append post-RoPE k and raw v at row p
+      if (tid < kHd) st_agent(&Kc[(size_t)p * kHd + tid], kn[tid]);
+      else st_agent(&Vc[(size_t)p * kHd + tid - kHd], vn[tid - kHd]);
+    }
+    float q4[kMaxRep][4];
+#pragma unroll
+    for (int h = 0; h < kMaxRep; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q4[h][e] = (h < rep) ? qn[h * kHd + 4 * lane + e] : 0.f;
+    for (int tt = wid; tt < len; tt += kNW) {
+      const int t = t0 + tt;
+      const float4 kv = (t == p) ? *reinterpret_cast<const float4*>(&kn[4 * lane]) : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]);
+#pragma unroll
+      for (int h = 0; h < kMaxRep; ++h) {
+        if (h >= rep) break;
+        float dd = q4[h][0] * kv.x + q4[h][1] * kv.y + q4[h][2] * kv.z + q4[h][3] * kv.w;
+        dd = wave_sum(dd);
+        if (lane == 0) sc[h * kMaxChunk + tt] = dd * a.ascale;
+      }
+    }
+    __syncthreads();
+    for (int h = wid; h < rep; h += kNW) {
+      float mx = -INFINITY;
+      for (int tt = lane; tt < len; tt += 64) mx = fmaxf(mx, sc[h * kMaxChunk + tt]);
+      mx = wave_max(mx);
+      float l = 0.f;
+      for (int tt = lane; tt < len; tt += 64) {
+        const float pe = expf(sc[h * kMaxChunk + tt] - mx);
+        sc[h * kMaxChunk + tt] = pe;
+        l += pe;
+      }
+      l = wave_sum(l);
+      if (lane == 0) { hm[h] = mx; hl[h] = l; }
+    }
+    __syncthreads();
+    float acc[kMaxRep][4];
+#pragma unroll
+    for (int h = 0; h < kMaxRep; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+    for (int tt = wid; tt < len; tt += kNW) {
+      const int t = t0 + tt;
+      const float4 vv = (t == p) ? *reinterpret_cast<const float4*>(&vn[4 * lane]) : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]);
+#pragma unroll
+      for (int h = 0; h < kMaxRep; ++h) {
+        if (h >= rep) break;
+        const float pe = sc[h * kMaxChunk + tt];
+        acc[h][0] += pe * vv.x; acc[h][1] += pe * vv.y; acc[h][2] += pe * vv.z; acc[h][3] += pe * vv.w;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxRep; ++h)
+      *reinterpret_cast<float4*>(&ored[(wid * kMaxRep + h) * kHd + 4 * lane]) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    __syncthreads();
+    const size_t pc = (size_t)g * a.att_nmax + c;
+    for (int e = tid; e < rep * kHd; e += kT) {
+      const int h = e / kHd, d = e % kHd;
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) o += ored[(w * kMaxRep + h) * kHd + d];
+      st_agent(&a.att_o[(pc * kMaxRep + h) * kHd + d], o);
+    }
+    if (tid < rep) {
+      st_agent(&a.att_ml[pc * 2 * kMaxRep + tid], hm[tid]);
+      st_agent(&a.att_ml[pc * 2 * kMaxRep + kMaxRep + tid], hl[tid]);
+    }
+    __syncthreads();
+  }
+  bar_arrive(bar);
+  return true;
+}
+
+// ------------------------------------------------------------------ lm_head + argmax
+// Tied embedding [V][H] as lm_head (kernels.rs:251-291): wave w owns R rows per block step,
+// lane l reads the 16-byte chunks 16*(l + 64c), c < CPW, of each row; two steps of loads
+// (2 x 8 per lane, 128 KB per block) are kept in flight.  Block (max, lowest index) -> arg_v /
+// arg_i.
+template <int CPW>
+Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
+  constexpr int R = 8 / CPW;
+  constexpr int RPB = kNW * R;
+  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int K = a.H, nbK = K >> 6;
+  const int nrb = (a.V + RPB - 1) / RPB;
+  uint4 wa[R][CPW], wb[R][CPW];
+  float sa[R][CPW], sb[R][CPW];
+  auto load = [&](int rb, uint4 (&wv)[R][CPW], float (&sv)[R][CPW]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rb * RPB + wid * R + r;
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) {
+        const int k = 16 * (lane + 64 * c);
+        const bool ok = row < a.V && k < K;
+        wv[r][c] = ok ? *reinterpret_cast<const uint4*>(a.emb_q + ((uint32_t)row * (uint32_t)K + (uint32_t)k)) : make_uint4(0, 0, 0, 0);
+        sv[r][c] = ok ? a.emb_s[(uint32_t)row * (uint32_t)nbK + (uint32_t)(k >> 6)] : 0.f;
+      }
+    }
+  };
+  float* xs = sh.smem;
+  float best_v = -INFINITY;
+  int best_i = INT_MAX;
+  auto compute = [&](int rb, const uint4 (&wv)[R][CPW], const float (&sv)[R][CPW]) {
+    float pr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) pr[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int k = 16 * (lane + 64 * c);
+      if (k >= K) continue;
+      float xv[16];
+      const float4* xp = reinterpret_cast<const float4*>(&xs[k]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 t = xp[q];
+        xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float f[16];
+        unpack16(wv[r][c], f);
+        float dd = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dd += f[e] * xv[e];
+        pr[r] += dd * sv[r][c];
+      }
+    }
+    const float v = fold_rows<R>(pr, lane);
+    const int row = rb * RPB + wid * R + lane / (64 / R);
+    if ((lane % (64 / R)) == 0 && row < a.V) {
+      if (a.logits) a.logits[row] = v;
+      if (v > best_v) { best_v = v; best_i = row; }
+    }
+  };
+  const int rb0 = bix(), gs = gridDim.x;
+  if (rb0 < nrb) load(rb0, wa, sa);
+  if (!bar_wait(bar, sh.ok)) return false;
+  {
+    auto src = [&](int k) { return from_fx(ld_agent(&a.h[k])); };
+    pro_rms(src, K, a.final_norm, a.eps, 0, K, xs, sh.shs);
+  }
+  __syncthreads();
+  for (int rb = rb0; rb < nrb; rb += 2 * gs) {
+    if (rb + gs < nrb) load(rb + gs, wb, sb);
+    compute(rb, wa, sa);
+    if (rb + gs >= nrb) break;
+    if (rb + 2 * gs < nrb) load(rb + 2 * gs, wa, sa);
+    compute(rb + gs, wb, sb);
+  }
+  block_argmax(best_v, best_i, sh.shv, sh.shi);
+  if (tid == 0) { st_agent(&a.arg_v[bix()], best_v); st_agent(&a.arg_i[bix()], best_i); }
+  bar_arrive(bar);
+  return true;
+}
+
+// ------------------------------------------------------------------ the kernel
+template <int CPW>
+__global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
+  __shared__ __align__(16) float smem[kSmem];
+  __shared__ float shs[kNW];
+  __shared__ float shv[kNW];
+  __shared__ int shi[kNW];
+  __shared__ int ok;
+  const Shared sh{smem, shs, shv, shi, &ok};
+  Bar bar{a.bar, a.bar + kStepErrWord, 0u};
+  const int p0 = *a.pos;
+  for (int i = 0; i < a.ntok; ++i) {
+    const int p = p0 + i;
+    for (int l = 0; l < a.n_layers; ++l) {
+      const StepLayer& L = a.layers[l];
+      const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
+      if (!L.full) {
+        if (!mv_stage(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
+        if (!gdn_stage(a, L, bar, sh)) return;
+        if (!mv_stage(a, L, SMV_OUT, PRO_GATED, i, p, bar, sh)) return;
+      } else {
+        if (!mv_stage(a, L, SMV_QKV, pro0, i, p, bar, sh)) return;
+        if (!attn_stage(a, L, p, bar, sh)) return;
+        if (!mv_stage(a, L, SMV_O, PRO_ATTN, i, p, bar, sh)) return;
+      }
+      if (!mv_stage(a, L, SMV_GU, PRO_RMS, i, p, bar, sh)) return;
+      if (!mv_stage(a, L, SMV_DOWN, PRO_SWIGLU, i, p, bar, sh)) return;
+    }
+    if (!lm_stage<CPW>(a, bar, sh)) return;
+  }
+  // tail: block 0 turns the last step's block argmaxes into the token
+  if (bix() != 0) return;
+  if (!bar_wait(bar, sh.ok)) return;
+  float v = -INFINITY;
+  int ix = INT_MAX;
+  if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
+  block_argmax(v, ix, sh.shv, sh.shi);
+  if (tix() == 0) {
+    const int tok = (ix == INT_MAX) ? 0 : ix;
+    const int pl = p0 + a.ntok - 1;
+    a.hist[pl] = tok;
+    *a.token = tok;
+    *a.pos = pl + 1;
+  }
+}
+
+const void* kernel_for(int hidden) {
+  if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1>);
+  if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2>);
+  return reinterpret_cast<const void*>(step_kernel<4>);
+}
+
+}  // namespace
+
+int step_grid(int hidden) {
+  if (hidden < 64 || hidden > 4096) return 0;
+  int dev = 0, ncu = 0, coop = 0, nb = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(hidden), kT, 0) != hipSuccess || nb < 1) return 0;
+  return std::min(ncu, kT);  // one block per CU; the argmax reduction reads one partial per thread
+}
+
+int step_att_nmax(int grid, int kvh) { return std::max(1, std::min(kMaxNmax, grid / std::max(1, kvh))); }
+
+int step_validate(const q35_dims& d, int tmax, int grid) {
+  if (grid < 1) return fail(Q35_E_HIP, "persistent step: device cannot co-schedule the step kernel");
+  if (d.hidden > 4096 || d.hidden > kRmsRegs * kT) return fail(Q35_E_SHAPE, "persistent step: hidden must be <= 4096");
+  if (d.hidden % 64 != 0) return fail(Q35_E_SHAPE, "persistent step: hidden must be a multiple of 64");
+  if (d.ffn > kRmsRegs * kT * 4) return fail(Q35_E_SHAPE, "persistent step: ffn too large");
+  if (d.lin_dk != kDk || (d.lin_dv % kCS) != 0 || d.conv_k != 4)
+    return fail(Q35_E_SHAPE, "persistent step: DeltaNet needs dk 128, dv % 8 == 0, conv 4");
+  if (d.head_dim != kHd || d.kv_heads < 1 || d.attn_heads % d.kv_heads != 0 || d.attn_heads / d.kv_heads > kMaxRep)
+    return fail(Q35_E_SHAPE, "persistent step: attention needs head_dim 256 and <= 4 query heads per kv head");
+  if ((long long)tmax > (long long)kMaxChunk * step_att_nmax(grid, d.kv_heads))
+    return fail(Q35_E_SHAPE, "persistent step: tmax too large for the attention split");
+  if (d.lin_dv > kMaxTouch * 64 || (d.lin_dv % 64) != 0) return fail(Q35_E_SHAPE, "persistent step: bad value head dim");
+  return Q35_OK;
+}
+
+// Items per stage: nchunk chunks of each tile, nchunk = floor(grid / tiles) (at least 1), chunk
+// rows rounded up to 16 and at most 512 (more chunks, i.e. a second round, only beyond that).
+void step_plan(const q35_dims& d, int grid, StepMv* mv) {
+  auto tiles = [](long long n) { return (int)((n + kTile - 1) / kTile); };
+  const int nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk, conv_dim = 2 * key_dim + vdim;
+  const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  struct S { int kind, tiles, K; } st[SMV_COUNT] = {
+      {SMV_QKVZ, tiles(conv_dim) + tiles(vdim), d.hidden},
+      {SMV_OUT, tiles(d.hidden), vdim},
+      {SMV_QKV, tiles((long long)ah * hd * 2) + 2 * tiles((long long)kvh * hd), d.hidden},
+      {SMV_O, tiles(d.hidden), ah * hd},
+      {SMV_GU, 2 * tiles(d.ffn), d.hidden},
+      {SMV_DOWN, tiles(d.hidden), d.ffn},
+  };
+  for (const S& s : st) {
+    int nchunk = std::max(1, grid / s.tiles);
+    int kch = (s.K + nchunk - 1) / nchunk;
+    kch = (kch + 15) & ~15;
+    if (kch > kKch) kch = kKch;
+    nchunk = (s.K + kch - 1) / kch;
+    mv[s.kind] = StepMv{kch, nchunk};
+  }
+}
+
+int step_launch(const StepArgs& a, int grid, hipStream_t st) {
+  if (a.ntok < 1) return Q35_OK;
+  Q35_HIP_TRY(hipMemsetAsync(a.bar, 0, kStepBarBytes, st));
+  StepArgs args = a;
+  void* params[] = {&args};
+  Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H), dim3(grid), dim3(kT), params, 0, st));
+  return Q35_OK;
+}
+
+}  // namespace q35

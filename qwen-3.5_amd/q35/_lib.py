@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "libq35.so")
 
 Q35_OK, Q35_E_SHAPE, Q35_E_ALIGN, Q35_E_HIP, Q35_E_ARG, Q35_E_WS, Q35_E_NOMEM = range(7)
 Q35_KN, Q35_NK, Q35_KN_TILED = 0, 1, 2
+Q35_LAUNCH_STREAM, Q35_LAUNCH_GRAPH, Q35_LAUNCH_PERSISTENT = 0, 1, 2
 ERROR_NAMES = {1: "Q35_E_SHAPE", 2: "Q35_E_ALIGN", 3: "Q35_E_HIP", 4: "Q35_E_ARG", 5: "Q35_E_WS", 6: "Q35_E_NOMEM"}
 
 c_i32, c_i64, c_u64, c_f32, c_sz, c_vp = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float,
@@ -73,6 +74,9 @@ PROTOTYPES = {
     "q35_model_reset": (ctypes.c_int, [c_vp, c_vp]),
     "q35_model_set_token": (ctypes.c_int, [c_vp, c_i32, c_vp]),
     "q35_model_step": (ctypes.c_int, [c_vp, c_i32, c_vp]),
+    "q35_model_decode": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp]),
+    "q35_model_check": (ctypes.c_int, [c_vp, c_vp]),
+    "q35_model_persistent_info": (ctypes.c_int, [c_vp, ctypes.POINTER(c_i32)]),
     "q35_model_generate": (ctypes.c_int, [c_vp, c_vp, c_i32, c_i32, c_vp, c_i32, c_i32,
                                           ctypes.POINTER(ctypes.c_double), c_vp]),
     "q35_model_tensor": (ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_vp), ctypes.POINTER(c_sz)]),

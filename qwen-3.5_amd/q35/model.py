@@ -35,17 +35,44 @@ class TextForCausalLM:
     def set_token(self, token):
         L.check(L.lib().q35_model_set_token(self.h, int(token), None))
 
-    def step(self, use_graph=True):
-        L.check(L.lib().q35_model_step(self.h, 1 if use_graph else 0, None))
+    MODES = {"stream": L.Q35_LAUNCH_STREAM, "graph": L.Q35_LAUNCH_GRAPH, "persistent": L.Q35_LAUNCH_PERSISTENT}
 
-    def generate(self, prompt, n_new, use_graph=True, readback_each=False):
+    def _mode(self, mode, use_graph):
+        """Launch mode: `mode` ("stream" | "graph" | "persistent"), else the legacy use_graph
+        flag (True -> graph, False -> stream), else the persistent kernel."""
+        if mode is not None:
+            return self.MODES[mode] if isinstance(mode, str) else int(mode)
+        if use_graph is not None:
+            return L.Q35_LAUNCH_GRAPH if use_graph else L.Q35_LAUNCH_STREAM
+        return L.Q35_LAUNCH_PERSISTENT
+
+    def persistent_grid(self):
+        """Blocks of the persistent step kernel; raises Q35Error if it cannot run here."""
+        g = ctypes.c_int32(0)
+        L.check(L.lib().q35_model_persistent_info(self.h, ctypes.byref(g)))
+        return g.value
+
+    def step(self, use_graph=None, mode=None, stream=None):
+        L.check(L.lib().q35_model_step(self.h, self._mode(mode, use_graph), stream))
+
+    def decode(self, n_steps, mode=None, stream=None):
+        """n_steps decode steps, asynchronous on `stream` (a hipStream_t value; None = the model's
+        own stream); one launch in persistent mode."""
+        L.check(L.lib().q35_model_decode(self.h, int(n_steps), self._mode(mode, None), stream))
+
+    def check(self, stream=None):
+        """Synchronise and raise if a persistent launch failed."""
+        L.check(L.lib().q35_model_check(self.h, stream))
+
+    def generate(self, prompt, n_new, use_graph=None, readback_each=False, mode=None, stream=None):
         """Returns (tokens[n_new+1], decode_seconds): the argmax after the last prompt token,
         then the argmax after each of n_new decode steps."""
         p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
         out = np.zeros(n_new + 1, np.int32)
         secs = ctypes.c_double(0.0)
         L.check(L.lib().q35_model_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data,
-                                           1 if use_graph else 0, 1 if readback_each else 0, ctypes.byref(secs), None))
+                                           self._mode(mode, use_graph), 1 if readback_each else 0,
+                                           ctypes.byref(secs), stream))
         return out, secs.value
 
     def tensor_ptr(self, name):

@@ -1,5 +1,6 @@
-"""End-to-end decode on the GPU (captured hipGraph and eager launches) against the oracle: greedy
-token ids must be identical; the final logits agree to rel-L2 <= 1e-5."""
+"""End-to-end decode on the GPU in every launch mode (persistent step kernel, captured hipGraph,
+eager launches) against the oracle: greedy token ids must be identical; the final logits agree
+to rel-L2 <= 1e-5."""
 import numpy as np
 import pytest
 
@@ -18,13 +19,18 @@ def oracle_model(d, seed, tmax):
     return O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, seed, name, n), tmax)
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_tiny_model_generate_matches_oracle(use_graph):
+MODES = ["persistent", "graph", "stream"]
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_tiny_model_generate_matches_oracle(mode):
+    print(f"[model tiny] mode={mode}", flush=True)
     d = tiny_dims()
     seed, tmax = 5, 128
     prompt = np.random.default_rng(0).integers(0, d.vocab, 16).astype(np.int32)
     m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
-    toks, _ = m.generate(prompt, 48, use_graph=use_graph)
+    toks, _ = m.generate(prompt, 48, mode=mode)
+    m.check()
     logits = m.tensor("logits", np.float32)
     ref = oracle_model(d, seed, tmax)
     rt, margins = ref.generate(prompt, 48)
@@ -33,27 +39,61 @@ def test_tiny_model_generate_matches_oracle(use_graph):
     # logits of the last decode step
     _, _, last = ref.step(rt[-1], want_logits=True)  # one more step on both sides
     m.set_token(int(rt[-1]))
-    m.step(use_graph=use_graph)
+    m.step(mode=mode)
+    m.check()
     assert rel_l2(m.tensor("logits", np.float32), last) <= 1e-5
     m.close()
 
 
-def test_graph_replays_match_eager_and_reset():
+def test_launch_modes_agree_and_reset():
+    print("[model modes]", flush=True)
     d = tiny_dims()
     prompt = np.arange(10, dtype=np.int32) * 37 % d.vocab
     a = q35.TextForCausalLM(d, seed=9, tmax=96)
-    t1, _ = a.generate(prompt, 30, use_graph=True)
+    t1, _ = a.generate(prompt, 30, mode="graph")
+    runs = {}
+    for mode in MODES:
+        for rb in (False, True):
+            a.reset()
+            runs[(mode, rb)], _ = a.generate(prompt, 30, mode=mode, readback_each=rb)
+            a.check()
+    for k, t in runs.items():
+        np.testing.assert_array_equal(t, t1, err_msg=str(k))
+    # continuing a conversation (cache kept) equals one long prompt, in every mode
+    for mode in MODES:
+        a.reset()
+        first, _ = a.generate(prompt[:4], 0, mode=mode)
+        rest, _ = a.generate(prompt[4:], 30, mode=mode)
+        a.check()
+        np.testing.assert_array_equal(rest, t1, err_msg=mode)
+    # mixing modes mid-stream: the persistent kernel and the per-op kernels share all state
     a.reset()
-    t2, _ = a.generate(prompt, 30, use_graph=False)
+    first, _ = a.generate(prompt, 10, mode="persistent")
+    a.decode(12, mode="graph")
+    a.decode(8, mode="persistent")
+    a.check()
+    hist = a.tensor("hist", np.int32)
+    np.testing.assert_array_equal(hist[len(prompt) - 1:len(prompt) + 30], t1)
+    a.close()
+
+
+def test_persistent_multi_step_launch_equals_single_steps():
+    """decode(n) as one launch vs n launches of one step: identical history."""
+    print("[model persistent multi]", flush=True)
+    d = tiny_dims()
+    prompt = np.arange(7, dtype=np.int32) * 11 % d.vocab
+    a = q35.TextForCausalLM(d, seed=4, tmax=64)
+    a.generate(prompt, 0, mode="persistent")
+    a.decode(40, mode="persistent")
+    a.check()
+    h1 = a.tensor("hist", np.int32)[:47].copy()
     a.reset()
-    t3, _ = a.generate(prompt, 30, use_graph=True, readback_each=True)
-    np.testing.assert_array_equal(t1, t2)
-    np.testing.assert_array_equal(t1, t3)
-    # continuing a conversation (cache kept) equals one long prompt
-    a.reset()
-    first, _ = a.generate(prompt[:4], 0)
-    rest, _ = a.generate(prompt[4:], 30)
-    np.testing.assert_array_equal(rest, t1)
+    a.generate(prompt, 0, mode="persistent")
+    for _ in range(40):
+        a.step(mode="persistent")
+    a.check()
+    h2 = a.tensor("hist", np.int32)[:47]
+    np.testing.assert_array_equal(h1, h2)
     a.close()
 
 
@@ -64,4 +104,39 @@ def test_model_rejects_overflow():
         m.generate(np.zeros(4, np.int32), 5)
     with pytest.raises(q35.Q35Error):
         m.set_token(d.vocab)
+    m.close()
+
+
+def test_2b_persistent_matches_oracle_short():
+    """Full Qwen3.5-2B shapes: 12-token prompt + 12 greedy steps, persistent kernel vs oracle."""
+    print("[model 2b persistent vs oracle]", flush=True)
+    d = q35.dims_2b()
+    seed, tmax = 0, 64
+    prompt = np.random.default_rng(3).integers(0, d.vocab, 12).astype(np.int32)
+    m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    toks, _ = m.generate(prompt, 12, mode="persistent")
+    m.check()
+    ref = oracle_model(d, seed, tmax)
+    rt, margins = ref.generate(prompt, 12)
+    print("tokens", toks, "min margin", margins.min(), flush=True)
+    np.testing.assert_array_equal(toks, rt)
+    m.close()
+
+
+def test_2b_persistent_matches_graph_long_context():
+    """Full shapes over a 600-token context (many attention chunks per kv head): the persistent
+    kernel and the per-op graph give the same greedy ids and near-identical final logits."""
+    print("[model 2b persistent vs graph]", flush=True)
+    d = q35.dims_2b()
+    tmax = 700
+    prompt = np.random.default_rng(5).integers(0, d.vocab, 600).astype(np.int32)
+    m = q35.TextForCausalLM(d, seed=1, tmax=tmax)
+    tp, _ = m.generate(prompt, 40, mode="persistent")
+    m.check()
+    lp = m.tensor("logits", np.float32).copy()
+    m.reset()
+    tg, _ = m.generate(prompt, 40, mode="graph")
+    lg = m.tensor("logits", np.float32)
+    np.testing.assert_array_equal(tp, tg)
+    assert rel_l2(lp, lg) <= 1e-4
     m.close()
