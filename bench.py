@@ -117,6 +117,28 @@ def matvec_sweep(torch, q35, m, d, reps=4):
     return out
 
 
+def copy_calibration():
+    """Three device-to-device copies of exactly 1 GiB: what FETCH_SIZE / WRITE_SIZE report for a
+    known byte count, the scale factor for the step kernel's counters."""
+    import torch
+    torch.cuda.set_device(0)
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("copied 3 x 1 GiB", flush=True)
+
+
+# HBM traffic of one step_kernel<2> launch of 64 steps in this workload: FETCH_SIZE + WRITE_SIZE
+# per dispatch from two rocprofv3 --pmc passes over `bench.py --no-cpu --no-sweep`, scaled by the
+# counters' reading for a 1 GiB copy (`bench.py --copy-calibration`): x2.0 and x1.0.  Measured for
+# the kernel at the commit that recorded it; profiles/step_kernel_decode_2b_traffic.md has the
+# commands and the per-dispatch values.
+STEP_TRAFFIC_PER_LAUNCH = 142.35e9
+
+
 def cpu_baseline(q35, d, prompt, budget_s=20.0):
     """Oracle (CPU restatement) decode tok/s on the host cores, bounded sample."""
     import oracle as O
@@ -152,7 +174,12 @@ def main():
     ap.add_argument("--chunk", type=int, default=64, help="decode steps per persistent-kernel launch")
     ap.add_argument("--readback", action="store_true",
                     help="also time one launch per token with a host readback each step (main.rs loop)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three 1 GiB device copies (reference point for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the decode path is single-GPU; multi-GPU is "
               "design-only), so --gpus must be 1", file=sys.stderr)
@@ -247,7 +274,8 @@ def main():
                    "launch": f"persistent step kernel, {chunk} steps per launch, grid {grid}x512"},
         "roofline": {"kernel": f"step_kernel<2>: persistent decode step, {chunk} tokens per launch",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": STEP_TRAFFIC_PER_LAUNCH if chunk == 64 else None,
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_us, 1)},
         "lm_head_kernel": {"kernel": "nk_kernel<1,2>: standalone Q8F lm_head 248320x2048 (kernels.rs q8_lm_head)",
                            "achieved_GBs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4),

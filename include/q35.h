@@ -59,7 +59,7 @@ typedef struct {
   const float* scale;
   int32_t rows;
   int32_t cols;
-  int32_t layout; /* Q35_KN or Q35_NK */
+  int32_t layout; /* Q35_KN, Q35_NK or Q35_KN_TILED */
 } q35_q8f;
 
 /* Shape constants of the decoder; mirrors the fields of TextConfig that the decode path
@@ -107,6 +107,7 @@ size_t q35_argmax_ws_bytes(int64_t n);
 
 /* ---------------------------------------------------------------- layer level (text_modules.rs) */
 
+/* Projection weights of the layer entry points: Q35_KN or Q35_KN_TILED (rows = in, cols = out). */
 typedef struct {
   q35_q8f in_proj_qkv; /* KN [hidden][2*key_dim+value_dim] */
   q35_q8f in_proj_z;   /* KN [hidden][value_dim] */

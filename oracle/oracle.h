@@ -15,7 +15,21 @@
  *     formulas are evaluated in f32 in the order the reference writes them.
  *
  * Pinning (tests/test_oracle_*.py): every function is checked against numpy float64
- * brute force on small shapes, plus known-answer cases and invariants listed next to it.
+ * brute force on small shapes, plus known-answer cases and invariants listed next to it;
+ * orc_gdn_decode / orc_attn_decode / orc_model_step are checked against the pinned pieces
+ * composed in the reference's order.  The reference ships no golden vectors and cannot be
+ * built here (Rust, no toolchain), so nothing is compared with a reference run.
+ *
+ * Parity unpinned (no check can fix these without running the reference's dependencies):
+ *   - orc_quantize_q8f vs Burn 0.22.1's Quantizer (main.rs:175-179): the rule implemented is
+ *     the stated one (scale = max|w|/127, q = round-half-away(w/scale) clamped to +-127, an
+ *     all-zero block gives scale 0); Burn's exact rounding and clamp are not pinned.
+ *   - orc_attention_core: the 1/sqrt(head_dim) score scale assumes Burn attention()'s default
+ *     options (text_modules.rs:921-928); no softcap.
+ *   - orc_conv_update: Burn conv1d orientation assumed to be cross-correlation with the oldest
+ *     tap first (text_modules.rs:153).
+ *   - f32 transcendentals (exp/log/sqrt/sin/cos) of Rust/ndarray to the last ulp: covered only
+ *     by the tolerances of the parity tests.
  */
 #ifndef Q35_ORACLE_H
 #define Q35_ORACLE_H

@@ -1,6 +1,8 @@
 """Pinning of the oracle's module-level functions (text_modules.rs restatements) on the CPU:
 closed forms in numpy float64, special cases that reduce to a textbook result, and
 cross-algorithm identities (chunked delta rule == sequential recurrent steps)."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -235,3 +237,72 @@ def test_attn_layer_wiring(rng):
     np.testing.assert_allclose(out[0], ref, rtol=1e-5, atol=1e-6)
     np.testing.assert_array_equal(kc[0], kc0)
     np.testing.assert_array_equal(vc[0], vc0)
+
+
+def test_model_step_wiring():
+    """orc_model_step == the pinned layer forwards composed as model.rs:27-84,113-129 and
+    text_modules.rs:1053-1085 write it: h = embed(token); per layer h += mixer(RMSNorm(h)),
+    h += MLP(RMSNorm(h)); logits = tied lm_head(RMSNorm(h)); token = argmax.  Two linear layers
+    and one full-attention layer (full_interval 3), three consecutive tokens."""
+    H, F, V, nh, dk, dv = 256, 512, 640, 2, 128, 128
+    cfg = O.Cfg(hidden=H, ffn=F, vocab=V, n_layers=3, full_interval=3, lin_heads=nh, lin_dk=dk, lin_dv=dv,
+                conv_k=4, attn_heads=4, kv_heads=2, head_dim=256, rot_dim=64, eps=1e-6, theta=1e7)
+    tmax = 8
+    vals = {}
+
+    def get(name, n):
+        if name not in vals:
+            g = np.random.default_rng(zlib.crc32(name.encode()))
+            if name.endswith("norm") and "linear_attn" not in name:
+                v = g.standard_normal(n) * 0.1          # RMSNorm weights (applied as 1 + w)
+            elif name.endswith("linear_attn.norm"):
+                v = g.uniform(0.5, 1.5, n)
+            elif name.endswith("a_log"):
+                v = np.log(g.uniform(0.01, 16, n))
+            elif name.endswith("dt_bias"):
+                v = np.ones(n)
+            else:
+                v = g.standard_normal(n) * 0.05
+            vals[name] = v.astype(np.float32)
+        return vals[name]
+
+    m = O.Model(cfg, get, tmax)
+    conv_dim = 2 * nh * dk + nh * dv
+    q8 = lambda name, r, c: O.quantize(get(name, r * c).reshape(r, c))
+    E = q8("embed_tokens", V, H)
+    layers, states = [], []
+    for l in range(3):
+        p = f"layers.{l}."
+        if (l + 1) % 3:
+            a = p + "linear_attn."
+            layers.append(O.GdnLayer(q8(a + "in_proj_qkv", H, conv_dim), q8(a + "in_proj_z", H, nh * dv),
+                                     q8(a + "out_proj", nh * dv, H), get(a + "in_proj_b", H * nh).reshape(H, nh),
+                                     get(a + "in_proj_a", H * nh).reshape(H, nh), get(a + "a_log", nh),
+                                     get(a + "dt_bias", nh), get(a + "conv1d", conv_dim * 4).reshape(conv_dim, 4),
+                                     get(a + "norm", dv)))
+            states.append([np.zeros((1, conv_dim, 3), np.float32), np.zeros((1, nh, dk, dv), np.float32)])
+        else:
+            a = p + "self_attn."
+            layers.append(O.AttnLayer(q8(a + "q_proj", H, 4 * 256 * 2), q8(a + "k_proj", H, 2 * 256),
+                                      q8(a + "v_proj", H, 2 * 256), q8(a + "o_proj", 4 * 256, H),
+                                      get(a + "q_norm", 256), get(a + "k_norm", 256)))
+            states.append([np.zeros((1, 2, tmax, 256), np.float32), np.zeros((1, 2, tmax, 256), np.float32)])
+    mlps = [O.MlpLayer(q8(f"layers.{l}.mlp.gate_proj", H, F), q8(f"layers.{l}.mlp.up_proj", H, F),
+                       q8(f"layers.{l}.mlp.down_proj", F, H)) for l in range(3)]
+    tok = 17
+    for pos in range(3):
+        got, _, logits = m.step(tok, want_logits=True)
+        h = O.embedding(E, [tok])[0].astype(np.float32)
+        for l in range(3):
+            x = O.rmsnorm(h, get(f"layers.{l}.input_layernorm", H))[None]
+            if (l + 1) % 3:
+                mix = O.gdn_decode(cfg, layers[l], x, states[l][0], states[l][1])[0]
+            else:
+                mix = O.attn_decode(cfg, layers[l], x, states[l][0], states[l][1], [pos])[0]
+            h = (h + mix).astype(np.float32)
+            x2 = O.rmsnorm(h, get(f"layers.{l}.post_attention_layernorm", H))[None]
+            h = (h + O.mlp_decode(cfg, mlps[l], x2)[0]).astype(np.float32)
+        ref, _ = O.gemv_nk(O.rmsnorm(h, get("norm", H))[None], E)
+        np.testing.assert_allclose(logits, ref[0], rtol=1e-5, atol=1e-6)
+        assert got == O.argmax(ref[0])
+        tok = got
