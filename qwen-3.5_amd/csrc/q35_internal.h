@@ -59,8 +59,26 @@ Q35_DEV void unpack16(const uint4 w, float* f) {
 typedef long long fx_t;
 Q35_DEV fx_t to_fx(float v) { return __float2ll_rn(v * 4294967296.0f); }
 Q35_DEV float from_fx(fx_t a) { return (float)((double)a * (1.0 / 4294967296.0)); }
+
+// Every buffer the kernels touch through these helpers is device memory (global address
+// space).  Pointers that reach a kernel through a table in memory are generic to the compiler,
+// and generic accesses become FLAT instructions, which count against the LDS counter too: a
+// workgroup barrier (which waits for LDS) would then also wait for every weight load in flight.
+// The casts keep them `global_*`.
+#define Q35_GLOBAL __attribute__((address_space(1)))
+template <class T>
+Q35_DEV T ldg(const T* p) { return *(const Q35_GLOBAL T*)p; }
+template <class T>
+Q35_DEV void stg(T* p, T v) { *(Q35_GLOBAL T*)p = v; }
+// 16-byte global load (p 16-byte aligned)
+typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
+Q35_DEV uint4 ldg16(const void* p) {
+  const q35_u32x4 v = *(const Q35_GLOBAL q35_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 Q35_DEV void fx_add(fx_t* p, float v) {
-  __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(p), (unsigned long long)to_fx(v), __ATOMIC_RELAXED,
+  __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -68,21 +86,23 @@ Q35_DEV void fx_add(fx_t* p, float v) {
 // gfx950 these are `global_store ... sc1` / `global_load ... sc1`, i.e. coherent at the device
 // level (write-through / miss in the per-XCD L2) without the whole-L2 writeback and
 // invalidate (`buffer_wbl2` / `buffer_inv`) that a device-scope fence costs on every block.
-Q35_DEV void st_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-Q35_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV void st_agent(float* p, float v) { __hip_atomic_store((Q35_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV void st_agent(int32_t* p, int32_t v) {
+  __hip_atomic_store((Q35_GLOBAL int32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 Q35_DEV float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((Q35_GLOBAL float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 Q35_DEV int32_t ld_agent(const int32_t* p) {
-  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((Q35_GLOBAL int32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 Q35_DEV fx_t ld_agent(const fx_t* p) {
-  return __hip_atomic_load(const_cast<fx_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((Q35_GLOBAL fx_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-Q35_DEV void st_agent(fx_t* p, fx_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+Q35_DEV void st_agent(fx_t* p, fx_t v) { __hip_atomic_store((Q35_GLOBAL fx_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 Q35_DEV uint32_t ld_agent(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((Q35_GLOBAL uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // (max, lowest index) order used by every argmax: a total order, so any reduction tree gives
@@ -155,9 +175,9 @@ Q35_DEV bool arrive_last(uint32_t* counter, uint32_t expected, int* sh_flag) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = (prev + 1u == expected);
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) __hip_atomic_store((Q35_GLOBAL uint32_t*)counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *sh_flag = last ? 1 : 0;
   }
   __syncthreads();
@@ -186,12 +206,12 @@ Q35_DEV bool arrive_last_grid(uint32_t* counters, int* sh_flag) {
     const uint32_t ngrp = (gridDim.x + G - 1) / G;
     const uint32_t in_grp = (gridDim.x - grp * G) < G ? (gridDim.x - grp * G) : G;
     bool last = false;
-    const uint32_t p1 = __hip_atomic_fetch_add(&counters[1 + grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t p1 = __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&counters[1 + grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (p1 + 1u == in_grp) {
-      __hip_atomic_store(&counters[1 + grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t p0 = __hip_atomic_fetch_add(&counters[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store((Q35_GLOBAL uint32_t*)&counters[1 + grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t p0 = __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&counters[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (p0 + 1u == ngrp) {
-        __hip_atomic_store(&counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store((Q35_GLOBAL uint32_t*)&counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = true;
       }
     }

@@ -127,7 +127,8 @@ Q35_DEV float4 ld4_agent(const float* p) {
   return make_float4(ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3));
 }
 Q35_DEV float4 ld4_fx(const fx_t* p) {
-  return make_float4(from_fx(ld_agent(p)), from_fx(ld_agent(p + 1)), from_fx(ld_agent(p + 2)), from_fx(ld_agent(p + 3)));
+  const fx_t a = ld_agent(p), b = ld_agent(p + 1), c = ld_agent(p + 2), d = ld_agent(p + 3);
+  return make_float4(from_fx(a), from_fx(b), from_fx(c), from_fx(d));
 }
 
 // ------------------------------------------------------------------ grid barrier
@@ -143,7 +144,7 @@ Q35_DEV void bar_arrive(Bar& b) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tix() == 0)
-    __hip_atomic_fetch_add(&b.ctr[(bix() % kGroups) * kCtrStride], 1u, __ATOMIC_RELAXED,
+    __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&b.ctr[(bix() % kGroups) * kCtrStride], 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   b.epoch += 1;
 }
@@ -167,7 +168,7 @@ Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
       __builtin_amdgcn_s_sleep(2);
     }
     if (tix() == 0) {
-      if (!ok) __hip_atomic_fetch_or(b.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!ok) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)b.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       *sh_ok = ok ? 1 : 0;
     }
   }
@@ -257,19 +258,19 @@ struct MvPf {
 };
 
 // Lane (cg, rr) loads 16 columns [cg*16, cg*16+16) of rows rr, rr+32, ... of the item.
+// Loads are unconditional and branch-free so that all of them are in flight at once: a row past
+// the item is clamped to its last row (mv_compute zeroes its contribution), and the columns past
+// N of the last tile are the zero padding of the tiled layout.  32-bit offsets from the matrix
+// base (every tiled matrix is < 4 GB) keep one VGPR per address.
 Q35_DEV void mv_load(const MvItem& it, int K, MvPf& pf) {
-  // 32-bit offsets from the matrix base (every tiled matrix is < 4 GB) keep the addresses in
-  // one VGPR each
   const int cg = tix() & 15, rr = tix() >> 4;
-  const bool colok = it.tl * kTile + cg * 16 < it.N;
-  const uint32_t row0 = (uint32_t)it.tl * (uint32_t)K + (uint32_t)it.k0 + (uint32_t)rr;
+  const uint32_t row0 = (uint32_t)it.tl * (uint32_t)K + (uint32_t)it.k0;
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    const int r = rr + kRG * u;
-    const bool ok = colok && r < it.klen;
-    const uint32_t row = row0 + (uint32_t)(kRG * u);
-    pf.w[u] = ok ? *reinterpret_cast<const uint4*>(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16))) : make_uint4(0, 0, 0, 0);
-    pf.s[u] = ok ? it.s[row * (uint32_t)(kTile / 64) + (uint32_t)(cg >> 2)] : 0.f;
+    if (kRG * u >= it.klen) break;  // uniform
+    const uint32_t row = row0 + (uint32_t)min(rr + kRG * u, it.klen - 1);
+    pf.w[u] = ldg16(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16)));
+    pf.s[u] = ldg(it.s + (row * (uint32_t)(kTile / 64) + (uint32_t)(cg >> 2)));
   }
 }
 
@@ -303,27 +304,45 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf& pf, const float* xs, float
   __syncthreads();
 }
 
-// xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j].
-template <class Src>
-Q35_DEV void pro_rms(Src src, int K, const float* w, float eps, int k0, int klen, float* xs, float* shs) {
+// xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j].  All
+// loads are issued before any value is used (indices clamped, masked afterwards), so the
+// prologue costs one round trip: `load(k)` returns the raw element, `conv` turns it into f32.
+template <class Raw, class Load, class Conv>
+Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int k0, int klen, float* xs,
+                     float* shs) {
   const int tid = tix();
-  float v[kRmsRegs];
+  Raw raw[kRmsRegs];
 #pragma unroll
   for (int j = 0; j < kRmsRegs; ++j) {
-    const int k = tid + kT * j;
-    v[j] = (k < K) ? src(k) : 0.f;
+    if (kT * j >= K) break;  // uniform
+    raw[j] = load(min(tid + kT * j, K - 1));
   }
+  float v[kRmsRegs];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRmsRegs; ++j) ss += v[j] * v[j];
+  for (int j = 0; j < kRmsRegs; ++j) {
+    if (kT * j >= K) break;
+    v[j] = (tid + kT * j < K) ? conv(raw[j]) : 0.f;
+    ss += v[j] * v[j];
+  }
   ss = block_sum(ss, shs);
   const float r = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
   for (int j = 0; j < kRmsRegs; ++j) {
+    if (kT * j >= K) break;
     const int k = tid + kT * j;
-    if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + w[k]);
+    if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + ldg(w + k));
   }
 }
+
+// the residual stream h (fixed point) as pro_rms input
+struct HLoad {
+  const fx_t* h;
+  Q35_DEV fx_t operator()(int k) const { return ld_agent(h + k); }
+};
+struct HConv {
+  Q35_DEV float operator()(fx_t x) const { return from_fx(x); }
+};
 
 // Token of step i at position p: the prompt id while p < plen, else the argmax of the previous
 // step (reduced here from the per-block partials), or *token for the launch's first step.
@@ -340,7 +359,7 @@ Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
     tok = (ix == INT_MAX) ? 0 : ix;
     if (bix() == 0 && tix() == 0) st_agent(&a.hist[p - 1], tok);
   }
-  if (p < *a.plen) tok = a.prompt[p];
+  if (p < ldg(a.plen)) tok = ldg(a.prompt + p);
   return tok;
 }
 
@@ -362,7 +381,7 @@ Q35_DEV void pro_gated(const StepArgs& a, const StepLayer& L, int k0, int klen, 
     const int k = k0 + i;
     const float r = grp[k / G - g0];
     const float z = from_fx(ld_agent(&a.acc_proj[a.conv_dim + k]));
-    xs[i] = (L.norm_w[k % G] * (ld_agent(&a.o_raw[k]) * r)) * silu_f(z);
+    xs[i] = (ldg(L.norm_w + k % G) * (ld_agent(&a.o_raw[k]) * r)) * silu_f(z);
   }
 }
 
@@ -466,9 +485,9 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
   if (item < nitems) {
     it = mv_item(d, item);
     mv_load(it, d.K, pf);
-    if (kind == SMV_QKVZ && it.tile < naux && tix() < it.klen) {
+    if (kind == SMV_QKVZ && it.tile < naux) {  // row clamped; masked where it is used
       const float* W = it.tile < a.nh ? L.w_b : L.w_a;
-      auxw = W[(size_t)(it.k0 + tix()) * a.nh + (it.tile % a.nh)];
+      auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
     }
   }
   if (!bar_wait(bar, sh.ok)) return false;
@@ -484,22 +503,24 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
         const int K = d.K, nbK = K >> 6;
         const int8_t* eq = a.emb_q + (size_t)tok * K;
         const float* es = a.emb_s + (size_t)tok * nbK;
-        auto src = [&](int k) { return (float)eq[k] * es[k >> 6]; };
-        pro_rms(src, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
+        auto src = [&](int k) { return (float)ldg(eq + k) * ldg(es + (k >> 6)); };
+        auto same = [](float x) { return x; };
+        pro_rms<float>(src, same, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row
           for (int k = tix(); k < K; k += kT) st_agent(&a.h[k], to_fx(src(k)));
       } break;
-      case PRO_RMS: {
-        auto src = [&](int k) { return from_fx(ld_agent(&a.h[k])); };
-        pro_rms(src, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
-      } break;
+      case PRO_RMS:
+        pro_rms<fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen, xs,
+                      sh.shs);
+        break;
       case PRO_GATED:
         pro_gated(a, L, it.k0, it.klen, xs, sh.smem + kGrp);
         break;
       case PRO_SWIGLU:
         for (int r = tix(); r < it.klen; r += kT) {
           const int k = it.k0 + r;
-          xs[r] = from_fx(ld_agent(&a.acc_gu[a.F + k])) * silu_f(from_fx(ld_agent(&a.acc_gu[k])));
+          const fx_t up = ld_agent(&a.acc_gu[a.F + k]), gate = ld_agent(&a.acc_gu[k]);
+          xs[r] = from_fx(up) * silu_f(from_fx(gate));
         }
         break;
       default:  // PRO_ATTN: merged attention output
@@ -512,7 +533,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
         float w = auxw;
         if (o != it.tile || !first) {
           const float* W = o < a.nh ? L.w_b : L.w_a;
-          w = (tix() < it.klen) ? W[(size_t)(it.k0 + tix()) * a.nh + (o % a.nh)] : 0.f;
+          w = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (o % a.nh)));
         }
         const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
         const float s = block_sum(v, sh.shs);
@@ -527,7 +548,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
 
 // ------------------------------------------------------------------ Gated DeltaNet step
 Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
-  const float acc = ((w[0] * ld_agent(&st[0]) + w[1] * ld_agent(&st[1])) + w[2] * ld_agent(&st[2])) + w[3] * xin;
+  const float acc = ((ldg(w) * ld_agent(&st[0]) + ldg(w + 1) * ld_agent(&st[1])) + ldg(w + 2) * ld_agent(&st[2])) + ldg(w + 3) * xin;
   return silu_f(acc);
 }
 
@@ -572,9 +593,9 @@ Q35_DEV bool gdn_stage(const StepArgs& a, const StepLayer& L, Bar& bar, const Sh
     const float bs = from_fx(ld_agent(&a.acc_ba[h]));
     const float as = from_fx(ld_agent(&a.acc_ba[a.nh + h]));
     const float beta = 1.0f / (1.0f + expf(-bs));
-    const float xg = as + L.dt_bias[h];
+    const float xg = as + ldg(L.dt_bias + h);
     const float pre = logf(expf(xg) + 1.0f);
-    const float g = -expf(L.a_log[h]) * (pre > 20.0f ? xg : pre);
+    const float g = -expf(ldg(L.a_log + h)) * (pre > 20.0f ? xg : pre);
     __syncthreads();
     if (wid < 4) {  // waves 0,1: q; waves 2,3: k
       const float v = qk[tid];
@@ -652,18 +673,18 @@ Q35_DEV bool attn_stage(const StepArgs& a, const StepLayer& L, int p, Bar& bar, 
         const float4 v = ld4_fx(&a.acc_proj[(size_t)(g * rep + w) * 2 * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
-        qn[w * kHd + d + 0] = (v.x * r) * (1.0f + L.q_norm[d + 0]);
-        qn[w * kHd + d + 1] = (v.y * r) * (1.0f + L.q_norm[d + 1]);
-        qn[w * kHd + d + 2] = (v.z * r) * (1.0f + L.q_norm[d + 2]);
-        qn[w * kHd + d + 3] = (v.w * r) * (1.0f + L.q_norm[d + 3]);
+        qn[w * kHd + d + 0] = (v.x * r) * (1.0f + ldg(L.q_norm + d + 0));
+        qn[w * kHd + d + 1] = (v.y * r) * (1.0f + ldg(L.q_norm + d + 1));
+        qn[w * kHd + d + 2] = (v.z * r) * (1.0f + ldg(L.q_norm + d + 2));
+        qn[w * kHd + d + 3] = (v.w * r) * (1.0f + ldg(L.q_norm + d + 3));
       } else if (w == rep) {
         const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)g * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
-        kn[d + 0] = (v.x * r) * (1.0f + L.k_norm[d + 0]);
-        kn[d + 1] = (v.y * r) * (1.0f + L.k_norm[d + 1]);
-        kn[d + 2] = (v.z * r) * (1.0f + L.k_norm[d + 2]);
-        kn[d + 3] = (v.w * r) * (1.0f + L.k_norm[d + 3]);
+        kn[d + 0] = (v.x * r) * (1.0f + ldg(L.k_norm + d + 0));
+        kn[d + 1] = (v.y * r) * (1.0f + ldg(L.k_norm + d + 1));
+        kn[d + 2] = (v.z * r) * (1.0f + ldg(L.k_norm + d + 2));
+        kn[d + 3] = (v.w * r) * (1.0f + ldg(L.k_norm + d + 3));
       } else {
         const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)(a.kvh + g) * kHd + d]);
         *reinterpret_cast<float4*>(&vn[d]) = v;
@@ -679,7 +700,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, const StepLayer& L, int p, Bar& bar, 
       const int hh = e / a.rot, ii = e % a.rot;
       const float* src = (hh < rep) ? qn + hh * kHd : kn;
       const float rh = (ii < half) ? -src[ii + half] : src[ii - half];
-      rtmp[hh * kHd + ii] = src[ii] * cs[ii] + rh * sn[ii];
+      rtmp[hh * kHd + ii] = src[ii] * ldg(cs + ii) + rh * ldg(sn + ii);
     }
     __syncthreads();
     for (int e = tid; e < nrot * a.rot; e += kT) {
@@ -782,10 +803,10 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
       const int row = rb * RPB + wid * R + r;
 #pragma unroll
       for (int c = 0; c < CPW; ++c) {
-        const int k = 16 * (lane + 64 * c);
-        const bool ok = row < a.V && k < K;
-        wv[r][c] = ok ? *reinterpret_cast<const uint4*>(a.emb_q + ((uint32_t)row * (uint32_t)K + (uint32_t)k)) : make_uint4(0, 0, 0, 0);
-        sv[r][c] = ok ? a.emb_s[(uint32_t)row * (uint32_t)nbK + (uint32_t)(k >> 6)] : 0.f;
+        // branch-free: clamped into the table; compute() drops rows past V and chunks past K
+        const uint32_t rw = (uint32_t)min(row, a.V - 1), k = (uint32_t)min(16 * (lane + 64 * c), K - 16);
+        wv[r][c] = ldg16(a.emb_q + (rw * (uint32_t)K + k));
+        sv[r][c] = ldg(a.emb_s + (rw * (uint32_t)nbK + (k >> 6)));
       }
     }
   };
@@ -820,17 +841,14 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
     const float v = fold_rows<R>(pr, lane);
     const int row = rb * RPB + wid * R + lane / (64 / R);
     if ((lane % (64 / R)) == 0 && row < a.V) {
-      if (a.logits) a.logits[row] = v;
+      if (a.logits) stg(a.logits + row, v);
       if (v > best_v) { best_v = v; best_i = row; }
     }
   };
   const int rb0 = bix(), gs = gridDim.x;
   if (rb0 < nrb) load(rb0, wa, sa);
   if (!bar_wait(bar, sh.ok)) return false;
-  {
-    auto src = [&](int k) { return from_fx(ld_agent(&a.h[k])); };
-    pro_rms(src, K, a.final_norm, a.eps, 0, K, xs, sh.shs);
-  }
+  pro_rms<fx_t>(HLoad{a.h}, HConv{}, K, a.final_norm, a.eps, 0, K, xs, sh.shs);
   __syncthreads();
   for (int rb = rb0; rb < nrb; rb += 2 * gs) {
     if (rb + gs < nrb) load(rb + gs, wb, sb);
@@ -855,7 +873,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   __shared__ int ok;
   const Shared sh{smem, shs, shv, shi, &ok};
   Bar bar{a.bar, a.bar + kStepErrWord, 0u};
-  const int p0 = *a.pos;
+  const int p0 = ldg(a.pos);
   for (int i = 0; i < a.ntok; ++i) {
     const int p = p0 + i;
     for (int l = 0; l < a.n_layers; ++l) {
@@ -885,9 +903,9 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   if (tix() == 0) {
     const int tok = (ix == INT_MAX) ? 0 : ix;
     const int pl = p0 + a.ntok - 1;
-    a.hist[pl] = tok;
-    *a.token = tok;
-    *a.pos = pl + 1;
+    stg(a.hist + pl, (int32_t)tok);
+    stg(a.token, (int32_t)tok);
+    stg(a.pos, (int32_t)(pl + 1));
   }
 }
 
