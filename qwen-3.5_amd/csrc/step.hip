@@ -61,12 +61,14 @@ constexpr int kMaxTouch = 8;      // norm groups / heads one matvec item's rows 
 constexpr int kDk = 128;          // DeltaNet key head dim
 constexpr int kCS = 8;            // DeltaNet value columns per item
 constexpr int kSmem = 12288;      // floats of LDS shared by all stages (48 KB)
+constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
 
 // LDS carve-up (float offsets)
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
 constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
 constexpr int kGrp = kRed + kRG * kTile;  // gated-norm factors [kMaxTouch]
 static_assert(kGrp + kMaxTouch <= kSmem, "LDS");
+static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
 static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
 
 // threadIdx.x / blockIdx.x read through an empty asm: every use is then loop-variant, so each
@@ -305,17 +307,21 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf& pf, const float* xs, float
 }
 
 // xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j].  All
-// loads are issued before any value is used (indices clamped, masked afterwards), so the
-// prologue costs one round trip: `load(k)` returns the raw element, `conv` turns it into f32.
+// loads (x and the thread's norm weights) are issued before any value is used (indices clamped,
+// masked afterwards), so the prologue costs one round trip: `load(k)` returns the raw element,
+// `conv` turns it into f32.
 template <class Raw, class Load, class Conv>
 Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int k0, int klen, float* xs,
                      float* shs) {
   const int tid = tix();
   Raw raw[kRmsRegs];
+  float wn[kRmsRegs];
 #pragma unroll
   for (int j = 0; j < kRmsRegs; ++j) {
     if (kT * j >= K) break;  // uniform
-    raw[j] = load(min(tid + kT * j, K - 1));
+    const int k = tid + kT * j;
+    raw[j] = load(min(k, K - 1));
+    wn[j] = ldg(w + min(max(k, k0), k0 + klen - 1));
   }
   float v[kRmsRegs];
   float ss = 0.f;
@@ -331,7 +337,7 @@ Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int
   for (int j = 0; j < kRmsRegs; ++j) {
     if (kT * j >= K) break;
     const int k = tid + kT * j;
-    if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + ldg(w + k));
+    if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + wn[j]);
   }
 }
 
@@ -365,8 +371,13 @@ Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
 
 // Gated RMSNorm per group of G = dv (text_modules.rs RMSNormGated): x = w[k%G] * (o * r_g) * silu(z)
 Q35_DEV void pro_gated(const StepArgs& a, const StepLayer& L, int k0, int klen, float* xs, float* grp) {
-  const int G = a.dv, lane = tix() & 63, wid = tix() >> 6;
+  const int G = a.dv, tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int g0 = k0 / G, g1 = (k0 + klen - 1) / G;
+  // the thread's own element (klen <= 512 = threads): z, o and w, loaded with the group sums
+  const int ki = k0 + min(tid, klen - 1);
+  const fx_t zr = ld_agent(&a.acc_proj[a.conv_dim + ki]);
+  const float ov = ld_agent(&a.o_raw[ki]);
+  const float wv = ldg(L.norm_w + ki % G);
   for (int gi = g0 + wid; gi <= g1; gi += kNW) {
     float ss = 0.f;
     for (int i = lane; i < G; i += 64) {
@@ -377,12 +388,7 @@ Q35_DEV void pro_gated(const StepArgs& a, const StepLayer& L, int k0, int klen, 
     if (lane == 0) grp[gi - g0] = 1.0f / sqrtf(ss / (float)G + a.eps);
   }
   __syncthreads();
-  for (int i = tix(); i < klen; i += kT) {
-    const int k = k0 + i;
-    const float r = grp[k / G - g0];
-    const float z = from_fx(ld_agent(&a.acc_proj[a.conv_dim + k]));
-    xs[i] = (ldg(L.norm_w + k % G) * (ld_agent(&a.o_raw[k]) * r)) * silu_f(z);
-  }
+  if (tid < klen) xs[tid] = (wv * (ov * grp[ki / G - g0])) * silu_f(from_fx(zr));
 }
 
 Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
@@ -401,17 +407,32 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   float* pbuf = scratch + kMaxTouch * kMaxNmax; // [kT] per-part sums
   float* wl = pbuf + kT;                        // [kMaxTouch] L
   const int h0 = k0 / kHd, h1 = (k0 + klen - 1) / kHd;
+  // the thread's output gate (klen <= 512 = threads), loaded with the chunk statistics
+  const int kg = k0 + min(tid, klen - 1);
+  const fx_t graw = ld_agent(&a.acc_proj[(size_t)(kg / kHd) * 2 * kHd + kHd + kg % kHd]);
   for (int hh = h0 + wid; hh <= h1; hh += kNW) {
     const int g = hh / rep, hr = hh % rep;
     const float* ml = a.att_ml + (size_t)g * a.att_nmax * 2 * kMaxRep;
+    float mv[kMaxNmax / 64], lv[kMaxNmax / 64];  // chunk c = lane + 64q (clamped; masked below)
+#pragma unroll
+    for (int q = 0; q < kMaxNmax / 64; ++q) {
+      const int c = min(lane + 64 * q, nact - 1);
+      mv[q] = ld_agent(&ml[c * 2 * kMaxRep + hr]);
+      lv[q] = ld_agent(&ml[c * 2 * kMaxRep + kMaxRep + hr]);
+    }
     float M = -INFINITY;
-    for (int c = lane; c < nact; c += 64) M = fmaxf(M, ld_agent(&ml[c * 2 * kMaxRep + hr]));
+#pragma unroll
+    for (int q = 0; q < kMaxNmax / 64; ++q) M = fmaxf(M, (lane + 64 * q < nact) ? mv[q] : -INFINITY);
     M = wave_max(M);
     float Ls = 0.f;
-    for (int c = lane; c < nact; c += 64) {
-      const float w = expf(ld_agent(&ml[c * 2 * kMaxRep + hr]) - M);
-      wts[(hh - h0) * kMaxNmax + c] = w;
-      Ls += ld_agent(&ml[c * 2 * kMaxRep + kMaxRep + hr]) * w;
+#pragma unroll
+    for (int q = 0; q < kMaxNmax / 64; ++q) {
+      const int c = lane + 64 * q;
+      const float w = expf(mv[q] - M);
+      if (c < nact) {
+        wts[(hh - h0) * kMaxNmax + c] = w;
+        Ls += lv[q] * w;
+      }
     }
     Ls = wave_sum(Ls);
     if (lane == 0) wl[hh - h0] = Ls;
@@ -425,15 +446,12 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
     const int k = k0 + i, hh = k / kHd, d = k % kHd, g = hh / rep, hr = hh % rep;
     const float* og = a.att_o + ((size_t)g * a.att_nmax * kMaxRep + hr) * kHd + d;  // + c*kMaxRep*kHd
     const float* w = wts + (hh - h0) * kMaxNmax;
-    for (int c0 = part; c0 < nact; c0 += 8 * parts) {
-      float v[8];
+    for (int c0 = part; c0 < nact; c0 += kMergeB * parts) {
+      float v[kMergeB];  // all of a batch in flight at once (clamped; masked below)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int c = c0 + j * parts;
-        v[j] = (c < nact) ? ld_agent(&og[(size_t)c * kMaxRep * kHd]) : 0.f;
-      }
+      for (int j = 0; j < kMergeB; ++j) v[j] = ld_agent(&og[(size_t)min(c0 + j * parts, nact - 1) * kMaxRep * kHd]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kMergeB; ++j) {
         const int c = c0 + j * parts;
         if (c < nact) o += v[j] * w[c];
       }
@@ -444,9 +462,8 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   if (tid < klen) {
     float s = 0.f;
     for (int q = 0; q < parts; ++q) s += pbuf[q * span + tid];
-    const int k = k0 + tid, hh = k / kHd, d = k % kHd;
-    const float gv = from_fx(ld_agent(&a.acc_proj[(size_t)hh * 2 * kHd + kHd + d]));
-    xs[tid] = (s / wl[hh - h0]) * sigmoid_f(gv);
+    const int hh = (k0 + tid) / kHd;
+    xs[tid] = (s / wl[hh - h0]) * sigmoid_f(from_fx(graw));
   }
 }
 
