@@ -184,6 +184,15 @@ int setup_persistent(q35_model* m) {
   }
   const int grid = m->step_grid, nh = d.lin_heads, kvh = d.kv_heads;
   const int nmax = step_att_nmax(grid, kvh);
+  // second copies of every linear-attention layer's recurrent state and conv state
+  const size_t rec_n = (size_t)nh * d.lin_dk * d.lin_dv, conv_n = (size_t)(2 * nh * d.lin_dk + nh * d.lin_dv) * 3;
+  int n_lin = 0;
+  for (int l = 0; l < d.n_layers; ++l) n_lin += m->layers[l].full ? 0 : 1;
+  float* alt = nullptr;
+  if (n_lin > 0) {
+    const int rc0 = dev_alloc_t(m, "step_state_alt", (size_t)n_lin * (rec_n + conv_n), &alt);
+    if (rc0) return rc0;
+  }
   std::vector<StepLayer> hl(d.n_layers);
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
@@ -194,6 +203,11 @@ int setup_persistent(q35_model* m) {
     s.qkv_q = L.qkv.q; s.qkv_s = L.qkv.s; s.z_q = L.z.q; s.z_s = L.z.s; s.out_q = L.out.q; s.out_s = L.out.s;
     s.w_b = L.w_b; s.w_a = L.w_a; s.a_log = L.a_log; s.dt_bias = L.dt_bias; s.conv_w = L.conv_w; s.norm_w = L.norm_w;
     s.conv_state = L.conv_state; s.rec = L.rec;
+    if (!L.full) {
+      s.rec_alt = alt;
+      s.conv_alt = alt + rec_n;
+      alt += rec_n + conv_n;
+    }
     s.q_q = L.q.q; s.q_s = L.q.s; s.k_q = L.k.q; s.k_s = L.k.s; s.v_q = L.v.q; s.v_s = L.v.s; s.o_q = L.o.q; s.o_s = L.o.s;
     s.q_norm = L.q_norm; s.k_norm = L.k_norm; s.kc = L.kc; s.vc = L.vc;
     s.gate_q = L.gate.q; s.gate_s = L.gate.s; s.up_q = L.up.q; s.up_s = L.up.s; s.down_q = L.down.q; s.down_s = L.down.s;
@@ -225,7 +239,7 @@ int setup_persistent(q35_model* m) {
   a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
   a.h = m->h; a.acc_proj = m->acc_proj; a.acc_ba = m->acc_ba; a.acc_gu = m->acc_gu;
   a.acc_zero_n = m->acc_proj_n + 2 * nh;
-  a.o_raw = m->o_raw; a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
+  a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
   a.bar = bar;

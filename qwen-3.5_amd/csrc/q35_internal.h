@@ -222,7 +222,7 @@ Q35_DEV bool arrive_last_grid(uint32_t* counters, int* sh_flag) {
 }
 
 // ------------------------------------------------------------------ Q8F KN matvec (split-K)
-enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_SWIGLU = 3, PRO_EMBED_RMS = 4, PRO_ATTN = 5 };
+enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_SWIGLU = 3, PRO_EMBED_RMS = 4, PRO_ATTN = 5, PRO_GDN = 6 };
 struct MvSeg {
   const int8_t* w;  // [K][N]
   const float* s;   // [K][N/64]
@@ -362,6 +362,7 @@ struct StepLayer {
   const float *qkv_s, *z_s, *out_s;
   const float *w_b, *w_a, *a_log, *dt_bias, *conv_w, *norm_w;
   float *conv_state, *rec;
+  float *conv_alt, *rec_alt;  // second copies: odd steps of a launch read these and write the first
   const int8_t *q_q, *k_q, *v_q, *o_q;
   const float *q_s, *k_s, *v_s, *o_s;
   const float *q_norm, *k_norm;
@@ -382,7 +383,7 @@ struct StepArgs {
   const float *rope_cos, *rope_sin;
   fx_t *h, *acc_proj, *acc_ba, *acc_gu;
   int64_t acc_zero_n;  // acc_proj + acc_ba entries cleared by the gate|up stage
-  float *o_raw, *att_ml, *att_o;
+  float *att_ml, *att_o;
   int32_t att_nmax;    // attention chunks per kv head
   float* logits;       // may be null
   float* arg_v; int32_t* arg_i;  // per-block argmax partials [grid]

@@ -10,8 +10,8 @@
 //
 // Stages per token (each ends with a grid barrier):
 //   linear-attention layer: qkvz  [RMSNorm(h) or embedding -> in_proj_qkv|in_proj_z; in_proj_b|a]
-//                           gdn   [conv1d + SiLU, l2norm, gated delta rule step]
-//                           out   [gated RMSNorm(o, z) -> out_proj -> +h; conv-state shift]
+//                           out   [conv1d + SiLU, l2norm, gated delta rule step, gated
+//                                  RMSNorm(o, z) -> out_proj -> +h]
 //   full-attention layer:   qkv   [RMSNorm(h) or embedding -> q|gate, k, v]
 //                           attn  [q/k RMSNorm, RoPE, KV append, split-T softmax partials]
 //                           o     [merge attention partials * sigmoid(gate) -> o_proj -> +h]
@@ -59,15 +59,17 @@ constexpr int kMinChunk = 8;
 constexpr int kMaxNmax = 256;     // attention chunks per kv head
 constexpr int kMaxTouch = 8;      // norm groups / heads one matvec item's rows can span
 constexpr int kDk = 128;          // DeltaNet key head dim
-constexpr int kCS = 8;            // DeltaNet value columns per item
+constexpr int kDv = 128;          // DeltaNet value head dim
+constexpr int kGdnG = kStepThreads / kDv;  // DeltaNet state row groups (4)
+constexpr int kGdnR = kDk / kGdnG;         // DeltaNet state rows per thread (32)
 constexpr int kSmem = 12288;      // floats of LDS shared by all stages (48 KB)
 constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
 
 // LDS carve-up (float offsets)
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
 constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
-constexpr int kGrp = kRed + kRG * kTile;  // gated-norm factors [kMaxTouch]
-static_assert(kGrp + kMaxTouch <= kSmem, "LDS");
+static_assert(kRed + kRG * kTile <= kSmem, "LDS");
+static_assert(512 + 2 * kT + kDv <= kRG * kTile, "DeltaNet scratch fits in kRed");
 static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
 static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
 
@@ -254,21 +256,25 @@ Q35_DEV MvItem mv_item(const Mv& d, int item) {
   return it;
 }
 
+// rows of one item held per lane: U <= kU (the out stage's items have at most dv = 128 rows)
+template <int U>
 struct MvPf {
-  uint4 w[kU];
-  float s[kU];
+  uint4 w[U];
+  float s[U];
 };
+constexpr int kUOut = kDv / kRG;
 
 // Lane (cg, rr) loads 16 columns [cg*16, cg*16+16) of rows rr, rr+32, ... of the item.
 // Loads are unconditional and branch-free so that all of them are in flight at once: a row past
 // the item is clamped to its last row (mv_compute zeroes its contribution), and the columns past
 // N of the last tile are the zero padding of the tiled layout.  32-bit offsets from the matrix
 // base (every tiled matrix is < 4 GB) keep one VGPR per address.
-Q35_DEV void mv_load(const MvItem& it, int K, MvPf& pf) {
+template <int U>
+Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
   const int cg = tix() & 15, rr = tix() >> 4;
   const uint32_t row0 = (uint32_t)it.tl * (uint32_t)K + (uint32_t)it.k0;
 #pragma unroll
-  for (int u = 0; u < kU; ++u) {
+  for (int u = 0; u < U; ++u) {
     if (kRG * u >= it.klen) break;  // uniform
     const uint32_t row = row0 + (uint32_t)min(rr + kRG * u, it.klen - 1);
     pf.w[u] = ldg16(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16)));
@@ -277,13 +283,14 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf& pf) {
 }
 
 // y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.
-Q35_DEV void mv_compute(const MvItem& it, const MvPf& pf, const float* xs, float* red) {
+template <int U>
+Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, float* red) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.f;
 #pragma unroll
-  for (int u = 0; u < kU; ++u) {
+  for (int u = 0; u < U; ++u) {
     if (kRG * u >= it.klen) break;
     const int r = rr + kRG * u;
     const float c = (r < it.klen) ? xs[r] * pf.s[u] : 0.f;
@@ -369,26 +376,147 @@ Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
   return tok;
 }
 
-// Gated RMSNorm per group of G = dv (text_modules.rs RMSNormGated): x = w[k%G] * (o * r_g) * silu(z)
-Q35_DEV void pro_gated(const StepArgs& a, const StepLayer& L, int k0, int klen, float* xs, float* grp) {
-  const int G = a.dv, tid = tix(), lane = tid & 63, wid = tid >> 6;
-  const int g0 = k0 / G, g1 = (k0 + klen - 1) / G;
-  // the thread's own element (klen <= 512 = threads): z, o and w, loaded with the group sums
-  const int ki = k0 + min(tid, klen - 1);
-  const fx_t zr = ld_agent(&a.acc_proj[a.conv_dim + ki]);
-  const float ov = ld_agent(&a.o_raw[ki]);
-  const float wv = ldg(L.norm_w + ki % G);
-  for (int gi = g0 + wid; gi <= g1; gi += kNW) {
-    float ss = 0.f;
-    for (int i = lane; i < G; i += 64) {
-      const float v = ld_agent(&a.o_raw[gi * G + i]);
-      ss += v * v;
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) grp[gi - g0] = 1.0f / sqrtf(ss / (float)G + a.eps);
+// ------------------------------------------------------------------ Gated DeltaNet step
+// The out stage's prologue.  An out item covers rows [k0, k0 + klen) of the core output o, and
+// klen divides dv, so they lie in one value head h.  The gated RMSNorm needs all dv outputs of
+// h, so every block with an item in h runs the whole recurrent step of h (a dk x dv state) and
+// keeps the rows it needs; the block holding tile 0 and the first rows of h writes the new
+// recurrent state and the shifted conv state.  Both states have two copies per layer: step i of
+// a launch reads copy i & 1 and writes the other, so that write never races the other blocks'
+// reads of the old state (their loads are issued before the barrier and may still be queued
+// behind weight loads after it).
+// text_modules.rs:134-162 (causal conv + state shift), :184-187 (l2norm), :365-443 (gated delta
+// rule), RMSNormGated: x = w[k % dv] * (o * rsqrt(mean_h(o^2) + eps)) * silu(z).
+//
+// dk = dv = 128 (every Qwen3.5 text model).  Thread t holds column j = t % 128 of state rows
+// 32 ig .. 32 ig + 31, ig = t / 128: every load and store instruction of a wave covers 256
+// contiguous bytes of one row.  Thread t < 384 also owns conv channel t of the head (q | k | v).
+struct GdnPf {
+  float s[kGdnR];   // old state rows
+  float cs[3];      // conv state of the thread's channel
+  float cw[4];      // conv weights of the thread's channel
+  float nw;         // gated-norm weight of the thread's o row
+  float dtb, alog;
+};
+
+struct GdnBuf {
+  const float *S, *cst;  // read this step
+  float *S_w, *cst_w;    // written this step
+};
+Q35_DEV GdnBuf gdn_buf(const StepLayer& L, int i) {
+  if (i & 1) return GdnBuf{L.rec_alt, L.conv_alt, L.rec, L.conv_state};
+  return GdnBuf{L.rec, L.conv_state, L.rec_alt, L.conv_alt};
+}
+
+// conv channel of the head's q | k | v element t (t < 2dk + dv)
+Q35_DEV int gdn_channel(const StepArgs& a, int h, int t) {
+  if (t < kDk) return h * kDk + t;
+  if (t < 2 * kDk) return a.key_dim + h * kDk + (t - kDk);
+  return 2 * a.key_dim + h * kDv + (t - 2 * kDk);
+}
+
+// Everything of the step that does not depend on the qkvz stage: issued before its barrier.
+Q35_DEV void gdn_load(const StepArgs& a, const StepLayer& L, const MvItem& it, int i, GdnPf& g) {
+  const int tid = tix(), j = tid % kDv, ig = tid / kDv;
+  const int h = it.k0 / kDv;
+  const GdnBuf b = gdn_buf(L, i);
+  // uniform head base + 32-bit lane offsets: one VGPR per address
+  const float* S = b.S + (size_t)h * kDk * kDv;
+  const uint32_t off = (uint32_t)(ig * kGdnR * kDv + j);
+#pragma unroll
+  for (int r = 0; r < kGdnR; ++r) g.s[r] = ld_agent(S + (off + (uint32_t)(r * kDv)));
+  const int c = gdn_channel(a, h, min(tid, 2 * kDk + kDv - 1));
+#pragma unroll
+  for (int e = 0; e < 3; ++e) g.cs[e] = ld_agent(&b.cst[(size_t)c * 3 + e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) g.cw[e] = ldg(L.conv_w + (size_t)c * 4 + e);
+  g.nw = ldg(L.norm_w + (it.k0 + min(tid, it.klen - 1)) % kDv);
+  g.dtb = ldg(L.dt_bias + h);
+  g.alog = ldg(L.a_log + h);
+}
+
+// Sums v (the thread's partial over its rows of column j) over the row groups through LDS
+// part [kT]; every thread gets the sum of its column.
+Q35_DEV float gdn_colsum(float v, float* part) {
+  const int tid = tix(), j = tid % kDv;
+  part[tid] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int g = 0; g < kGdnG; ++g) s += part[g * kDv + j];
+  return s;
+}
+
+Q35_DEV void pro_gdn(const StepArgs& a, const StepLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
+                     float* scratch) {
+  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int j = tid % kDv, ig = tid / kDv;
+  const int h = it.k0 / kDv, nch = 2 * kDk + kDv;
+  float* qkv = scratch;                   // [2dk + dv] conv outputs q | k | v of head h
+  float* wsum = scratch + 2 * kDk + kDv;  // [8]
+  float* part0 = scratch + 512;           // [kT]
+  float* part1 = part0 + kT;              // [kT]
+  float* ov = part1 + kT;                 // [dv]
+  // qkvz-stage outputs: the thread's conv input, its z element and the two gate projections
+  const int c = gdn_channel(a, h, min(tid, nch - 1));
+  const fx_t xr = ld_agent(&a.acc_proj[c]);
+  const fx_t zr = ld_agent(&a.acc_proj[a.conv_dim + it.k0 + min(tid, it.klen - 1)]);
+  const float bs = from_fx(ld_agent(&a.acc_ba[h]));
+  const float as = from_fx(ld_agent(&a.acc_ba[a.nh + h]));
+  const float x = from_fx(xr);
+  if (tid < nch) qkv[tid] = silu_f(((g.cw[0] * g.cs[0] + g.cw[1] * g.cs[1]) + g.cw[2] * g.cs[2]) + g.cw[3] * x);
+  const bool writer = it.tl == 0 && (it.k0 % kDv) == 0;  // uniform
+  const GdnBuf b = gdn_buf(L, i);
+  if (writer && tid < nch) {  // conv state [c] <- [s1, s2, x]
+    float* cw = b.cst_w + (size_t)c * 3;
+    st_agent(&cw[0], g.cs[1]);
+    st_agent(&cw[1], g.cs[2]);
+    st_agent(&cw[2], x);
+  }
+  // gates: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias) (kernels.rs:228-244)
+  const float beta = 1.0f / (1.0f + expf(-bs));
+  const float xg = as + g.dtb;
+  const float pre = logf(expf(xg) + 1.0f);
+  const float decay = expf(-expf(g.alog) * (pre > 20.0f ? xg : pre));
+  __syncthreads();
+  if (wid < 4) {  // waves 0,1: q; waves 2,3: k (dk = 128)
+    const float v = qkv[tid];
+    const float ss = wave_sum(v * v);
+    if (lane == 0) wsum[wid] = ss;
   }
   __syncthreads();
-  if (tid < klen) xs[tid] = (wv * (ov * grp[ki / G - g0])) * silu_f(from_fx(zr));
+  const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
+  const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
+  // S <- decay * S;  m = S^T k
+  float m = 0.f;
+#pragma unroll
+  for (int r = 0; r < kGdnR; ++r) {
+    g.s[r] *= decay;
+    m += g.s[r] * (qkv[kDk + ig * kGdnR + r] * rk);
+  }
+  m = gdn_colsum(m, part0);
+  // delta = (v - m) * beta;  S <- S + k delta^T;  o = S^T q
+  const float dl = (qkv[2 * kDk + j] - m) * beta;
+  float o = 0.f;
+  float* Sw = b.S_w + (size_t)h * kDk * kDv;
+  const uint32_t off = (uint32_t)(ig * kGdnR * kDv + j);
+#pragma unroll
+  for (int r = 0; r < kGdnR; ++r) {
+    const int row = ig * kGdnR + r;
+    g.s[r] += (qkv[kDk + row] * rk) * dl;
+    o += g.s[r] * ((qkv[row] * rq) * a.qscale);
+    if (writer) st_agent(Sw + (off + (uint32_t)(r * kDv)), g.s[r]);
+  }
+  o = gdn_colsum(o, part1);
+  // gated RMSNorm over the dv outputs of h: threads tid < dv (waves 0 and 1) hold them
+  if (tid < kDv) {
+    ov[tid] = o;
+    const float ss = wave_sum(o * o);
+    if (lane == 0) wsum[4 + wid] = ss;
+  }
+  __syncthreads();
+  const float rg = 1.0f / sqrtf((wsum[4] + wsum[5]) / (float)kDv + a.eps);
+  if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(from_fx(zr));
 }
 
 Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
@@ -469,34 +597,27 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
 
 // Side tasks that run right after a stage's barrier (their inputs are final, their outputs are
 // not read before the next barrier), spread over every thread of the grid.
-Q35_DEV void side_tasks(const StepArgs& a, const StepLayer& L, int kind) {
+Q35_DEV void side_tasks(const StepArgs& a, int kind) {
   const int64_t gt = (int64_t)bix() * kT + tix(), gs = (int64_t)gridDim.x * kT;
   if (kind == SMV_QKVZ || kind == SMV_QKV) {  // gate|up accumulator: last read by the previous down stage
     for (int64_t i = gt; i < 2 * (int64_t)a.F; i += gs) st_agent(&a.acc_gu[i], (fx_t)0);
   } else if (kind == SMV_GU) {  // projection + gate accumulators: last read by the out / o stage
     for (int64_t i = gt; i < a.acc_zero_n; i += gs) st_agent(&a.acc_proj[i], (fx_t)0);
-  } else if (kind == SMV_OUT) {  // causal-conv state [c][3] <- [s1, s2, x_c] (text_modules.rs:134-162)
-    for (int64_t c = gt; c < a.conv_dim; c += gs) {
-      float* st = L.conv_state + c * 3;
-      const float s1 = ld_agent(&st[1]), s2 = ld_agent(&st[2]);
-      const float x = from_fx(ld_agent(&a.acc_proj[c]));
-      st_agent(&st[0], s1);
-      st_agent(&st[1], s2);
-      st_agent(&st[2], x);
-    }
   }
 }
 
 // One matvec stage.  The in_proj_b / in_proj_a gate projection (f32, [H][nh] each,
 // kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
-// dot product of its rows with column t of [W_b | W_a].
+// dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need.
+template <int U = kU>
 Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, int i, int p, Bar& bar,
                       const Shared& sh) {
   const Mv d = make_mv(a, L, kind);
   const int nitems = d.t3 * d.nchunk;
   int item = bix();
-  MvPf pf;
+  MvPf<U> pf;
   MvItem it{};
+  GdnPf gp;
   float auxw = 0.f;
   const int naux = 2 * a.nh;
   if (item < nitems) {
@@ -506,15 +627,20 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
       const float* W = it.tile < a.nh ? L.w_b : L.w_a;
       auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
     }
+    if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
   }
   if (!bar_wait(bar, sh.ok)) return false;
-  side_tasks(a, L, kind);
+  side_tasks(a, kind);
   int tok = 0;
   if (pro == PRO_EMBED_RMS && item < nitems) tok = select_token(a, i, p, sh);
   float* xs = sh.smem + kXs;
   float* red = sh.smem + kRed;
   for (bool first = true; item < nitems; item += gridDim.x, first = false) {
-    if (!first) it = mv_item(d, item), mv_load(it, d.K, pf);
+    if (!first) {
+      it = mv_item(d, item);
+      mv_load(it, d.K, pf);
+      if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
+    }
     switch (pro) {
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
@@ -530,8 +656,8 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
         pro_rms<fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen, xs,
                       sh.shs);
         break;
-      case PRO_GATED:
-        pro_gated(a, L, it.k0, it.klen, xs, sh.smem + kGrp);
+      case PRO_GDN:
+        pro_gdn(a, L, it, i, gp, xs, red);
         break;
       case PRO_SWIGLU:
         for (int r = tix(); r < it.klen; r += kT) {
@@ -558,104 +684,6 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
       }
     }
     mv_compute(it, pf, xs, red);
-  }
-  bar_arrive(bar);
-  return true;
-}
-
-// ------------------------------------------------------------------ Gated DeltaNet step
-Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
-  const float acc = ((ldg(w) * ld_agent(&st[0]) + ldg(w + 1) * ld_agent(&st[1])) + ldg(w + 2) * ld_agent(&st[2])) + ldg(w + 3) * xin;
-  return silu_f(acc);
-}
-
-// Item (head h, 8 value columns): lane (row group ig = tid/8, column j = tid%8) holds
-// S[h][2ig, 2ig+1][col0 + j].  text_modules.rs:134-162 (conv), :184-187 (l2norm),
-// :365-443 (recurrent gated delta rule).
-Q35_DEV bool gdn_stage(const StepArgs& a, const StepLayer& L, Bar& bar, const Shared& sh) {
-  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
-  const int nsl = a.dv / kCS, nitems = a.nh * nsl;
-  const int j = tid % kCS, ig = tid / kCS, i0 = 2 * ig;
-  float* qk = sh.smem;            // [256] q | k after conv
-  float* vv = sh.smem + 256;      // [kCS]
-  float* red = sh.smem + 264;     // [kNW][kCS]
-  float* wsum = sh.smem + 264 + kNW * kCS;  // [4]
-  int item = bix();
-  float sr[2] = {0.f, 0.f};
-  auto sptr = [&](int it) {
-    const int h = it / nsl, sl = it % nsl;
-    return L.rec + ((size_t)h * kDk) * a.dv + sl * kCS + j;
-  };
-  if (item < nitems) {
-    float* Sp = sptr(item);
-    sr[0] = ld_agent(&Sp[(size_t)i0 * a.dv]);
-    sr[1] = ld_agent(&Sp[(size_t)(i0 + 1) * a.dv]);
-  }
-  if (!bar_wait(bar, sh.ok)) return false;
-  for (bool first = true; item < nitems; item += gridDim.x, first = false) {
-    const int h = item / nsl, sl = item % nsl, col0 = sl * kCS;
-    float* Sp = sptr(item);
-    if (!first) {
-      sr[0] = ld_agent(&Sp[(size_t)i0 * a.dv]);
-      sr[1] = ld_agent(&Sp[(size_t)(i0 + 1) * a.dv]);
-    }
-    if (tid < 2 * kDk) {  // q (tid < 128) and k channels of head h
-      const int c = (tid < kDk) ? h * kDk + tid : a.key_dim + h * kDk + (tid - kDk);
-      qk[tid] = conv4_silu(from_fx(ld_agent(&a.acc_proj[c])), L.conv_state + (size_t)c * 3, L.conv_w + (size_t)c * 4);
-    } else if (tid < 2 * kDk + kCS) {
-      const int c = 2 * a.key_dim + h * a.dv + col0 + (tid - 2 * kDk);
-      vv[tid - 2 * kDk] = conv4_silu(from_fx(ld_agent(&a.acc_proj[c])), L.conv_state + (size_t)c * 3, L.conv_w + (size_t)c * 4);
-    }
-    // gates: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias) (kernels.rs:228-244)
-    const float bs = from_fx(ld_agent(&a.acc_ba[h]));
-    const float as = from_fx(ld_agent(&a.acc_ba[a.nh + h]));
-    const float beta = 1.0f / (1.0f + expf(-bs));
-    const float xg = as + ldg(L.dt_bias + h);
-    const float pre = logf(expf(xg) + 1.0f);
-    const float g = -expf(ldg(L.a_log + h)) * (pre > 20.0f ? xg : pre);
-    __syncthreads();
-    if (wid < 4) {  // waves 0,1: q; waves 2,3: k
-      const float v = qk[tid];
-      const float ss = wave_sum(v * v);
-      if (lane == 0) wsum[wid] = ss;
-    }
-    __syncthreads();
-    const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
-    const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
-    const float q0 = (qk[i0] * rq) * a.qscale, q1 = (qk[i0 + 1] * rq) * a.qscale;
-    const float k0 = qk[kDk + i0] * rk, k1 = qk[kDk + i0 + 1] * rk;
-    const float decay = expf(g);
-    sr[0] *= decay;
-    sr[1] *= decay;
-    // S^T k for column j: lanes of a wave hold row groups 8w'..8w'+7 (lane = 8*(ig%8) + j)
-    float mp = sr[0] * k0 + sr[1] * k1;
-    mp += __shfl_xor(mp, 8, 64);
-    mp += __shfl_xor(mp, 16, 64);
-    mp += __shfl_xor(mp, 32, 64);
-    if (lane < kCS) red[wid * kCS + lane] = mp;
-    __syncthreads();
-    float m = 0.f;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) m += red[w * kCS + j];
-    const float delta = (vv[j] - m) * beta;
-    sr[0] += k0 * delta;
-    sr[1] += k1 * delta;
-    st_agent(&Sp[(size_t)i0 * a.dv], sr[0]);
-    st_agent(&Sp[(size_t)(i0 + 1) * a.dv], sr[1]);
-    float op = sr[0] * q0 + sr[1] * q1;
-    op += __shfl_xor(op, 8, 64);
-    op += __shfl_xor(op, 16, 64);
-    op += __shfl_xor(op, 32, 64);
-    __syncthreads();  // every lane has read red (m) before it is overwritten
-    if (lane < kCS) red[wid * kCS + lane] = op;
-    __syncthreads();
-    if (tid < kCS) {
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < kNW; ++w) o += red[w * kCS + tid];
-      st_agent(&a.o_raw[h * a.dv + col0 + tid], o);
-    }
-    __syncthreads();
   }
   bar_arrive(bar);
   return true;
@@ -880,6 +908,43 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
   return true;
 }
 
+// After an odd number of steps the newest recurrent and conv states are in the second copies:
+// copy them back, so that every launch starts and ends with the state in rec / conv_state.
+// Float4 elements over all layers, kB per thread in flight.
+Q35_DEV void state_copy_back(const StepArgs& a) {
+  constexpr int kB = 8;
+  const int64_t gt = (int64_t)bix() * kT + tix(), gs = (int64_t)gridDim.x * kT;
+  const int64_t nr = (int64_t)a.nh * kDk * a.dv / 4, nc = (int64_t)a.conv_dim * 3 / 4, per = nr + nc;
+  const int64_t total = (int64_t)a.n_layers * per;
+  for (int64_t e0 = gt; e0 < total; e0 += kB * gs) {
+    float4 v[kB];
+    float* dst[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int64_t e = e0 + u * gs;
+      dst[u] = nullptr;
+      if (e < total) {
+        const int l = (int)(e / per);
+        const int64_t r = e - (int64_t)l * per;
+        const StepLayer& L = a.layers[l];
+        if (!L.full) {
+          const float* src = r < nr ? L.rec_alt + 4 * r : L.conv_alt + 4 * (r - nr);
+          dst[u] = r < nr ? L.rec + 4 * r : L.conv_state + 4 * (r - nr);
+          v[u] = ld4_agent(src);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      if (dst[u] == nullptr) continue;
+      st_agent(dst[u] + 0, v[u].x);
+      st_agent(dst[u] + 1, v[u].y);
+      st_agent(dst[u] + 2, v[u].z);
+      st_agent(dst[u] + 3, v[u].w);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ the kernel
 template <int CPW>
 __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
@@ -898,8 +963,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
       if (!L.full) {
         if (!mv_stage(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
-        if (!gdn_stage(a, L, bar, sh)) return;
-        if (!mv_stage(a, L, SMV_OUT, PRO_GATED, i, p, bar, sh)) return;
+        if (!mv_stage<kUOut>(a, L, SMV_OUT, PRO_GDN, i, p, bar, sh)) return;
       } else {
         if (!mv_stage(a, L, SMV_QKV, pro0, i, p, bar, sh)) return;
         if (!attn_stage(a, L, p, bar, sh)) return;
@@ -910,6 +974,8 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
     }
     if (!lm_stage<CPW>(a, bar, sh)) return;
   }
+  // Every block has passed the last step's lm-stage barrier, so all state writes are complete.
+  if (a.ntok & 1) state_copy_back(a);
   // tail: block 0 turns the last step's block argmaxes into the token
   if (bix() != 0) return;
   if (!bar_wait(bar, sh.ok)) return;
@@ -951,18 +1017,18 @@ int step_validate(const q35_dims& d, int tmax, int grid) {
   if (d.hidden > 4096 || d.hidden > kRmsRegs * kT) return fail(Q35_E_SHAPE, "persistent step: hidden must be <= 4096");
   if (d.hidden % 64 != 0) return fail(Q35_E_SHAPE, "persistent step: hidden must be a multiple of 64");
   if (d.ffn > kRmsRegs * kT * 4) return fail(Q35_E_SHAPE, "persistent step: ffn too large");
-  if (d.lin_dk != kDk || (d.lin_dv % kCS) != 0 || d.conv_k != 4)
-    return fail(Q35_E_SHAPE, "persistent step: DeltaNet needs dk 128, dv % 8 == 0, conv 4");
+  if (d.lin_dk != kDk || d.lin_dv != kDv || d.conv_k != 4)
+    return fail(Q35_E_SHAPE, "persistent step: DeltaNet needs dk 128, dv 128, conv 4");
   if (d.head_dim != kHd || d.kv_heads < 1 || d.attn_heads % d.kv_heads != 0 || d.attn_heads / d.kv_heads > kMaxRep)
     return fail(Q35_E_SHAPE, "persistent step: attention needs head_dim 256 and <= 4 query heads per kv head");
   if ((long long)tmax > (long long)kMaxChunk * step_att_nmax(grid, d.kv_heads))
     return fail(Q35_E_SHAPE, "persistent step: tmax too large for the attention split");
-  if (d.lin_dv > kMaxTouch * 64 || (d.lin_dv % 64) != 0) return fail(Q35_E_SHAPE, "persistent step: bad value head dim");
   return Q35_OK;
 }
 
 // Items per stage: nchunk chunks of each tile, nchunk = floor(grid / tiles) (at least 1), chunk
 // rows rounded up to 16 and at most 512 (more chunks, i.e. a second round, only beyond that).
+// The out stage's chunk divides dv (its DeltaNet prologue serves one value head per item).
 void step_plan(const q35_dims& d, int grid, StepMv* mv) {
   auto tiles = [](long long n) { return (int)((n + kTile - 1) / kTile); };
   const int nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk, conv_dim = 2 * key_dim + vdim;
@@ -980,6 +1046,11 @@ void step_plan(const q35_dims& d, int grid, StepMv* mv) {
     int kch = (s.K + nchunk - 1) / nchunk;
     kch = (kch + 15) & ~15;
     if (kch > kKch) kch = kKch;
+    if (s.kind == SMV_OUT) {
+      int kc = d.lin_dv;
+      while (kc > kch && kc % 32 == 0) kc /= 2;
+      kch = kc;
+    }
     nchunk = (s.K + kch - 1) / kch;
     mv[s.kind] = StepMv{kch, nchunk};
   }

@@ -1,6 +1,8 @@
 """End-to-end decode on the GPU in every launch mode (persistent step kernel, captured hipGraph,
 eager launches) against the oracle: greedy token ids must be identical; the final logits agree
 to rel-L2 <= 1e-5."""
+import os
+
 import numpy as np
 import pytest
 
@@ -140,3 +142,23 @@ def test_2b_persistent_matches_graph_long_context():
     np.testing.assert_array_equal(tp, tg)
     assert rel_l2(lp, lg) <= 1e-4
     m.close()
+
+
+def test_2b_persistent_matches_golden_512():
+    """The benchmarked workload end to end: the 2B-shaped model (weights seed 0), a 512-token
+    prompt and 512 greedy steps through the persistent kernel; all 513 greedy ids equal the
+    oracle's, stored in tests/golden/e2e_2b_seed0.npz by tests/golden/make_e2e_2b.py (smallest
+    oracle top-1 / top-2 margin over the run: 5.1e-4)."""
+    print("[model 2b persistent vs golden 512+512]", flush=True)
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "e2e_2b_seed0.npz"))
+    prompt, want, margins = g["prompt"], g["tokens"], g["margins"]
+    d = q35.dims_2b()
+    m = q35.TextForCausalLM(d, seed=int(g["seed"]), tmax=len(prompt) + len(want) + 64)
+    toks, _ = m.generate(prompt, len(want) - 1, mode="persistent")
+    m.check()
+    m.close()
+    bad = np.flatnonzero(toks != want)
+    if bad.size:
+        i = int(bad[0])
+        pytest.fail(f"{bad.size} ids differ; first at step {i}: got {toks[i]}, oracle {want[i]} "
+                    f"(oracle margin there {margins[i]:.3g})")
