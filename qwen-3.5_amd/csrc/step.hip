@@ -180,6 +180,12 @@ Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
   return *sh_ok != 0;
 }
 
+// The layer table is never written by the kernel: read through the constant address space, its
+// uniform fields are scalar loads (scalar cache) rather than vector loads that would queue behind
+// the weight stream and force vmcnt waits.
+typedef const __attribute__((address_space(4))) StepLayer CLayer;
+Q35_DEV CLayer& layer_at(const StepArgs& a, int l) { return *(CLayer*)(a.layers + l); }
+
 // ------------------------------------------------------------------ matvec stages
 struct Mv {
   const int8_t *w0, *w1, *w2;
@@ -192,7 +198,7 @@ struct Mv {
 
 Q35_DEV int tiles_of(int n) { return (n + kTile - 1) / kTile; }
 
-Q35_DEV Mv make_mv(const StepArgs& a, const StepLayer& L, int kind) {
+Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, int kind) {
   Mv d{};
   const StepMv pl = a.mv[kind];
   d.kch = pl.kch;
@@ -403,7 +409,7 @@ struct GdnBuf {
   const float *S, *cst;  // read this step
   float *S_w, *cst_w;    // written this step
 };
-Q35_DEV GdnBuf gdn_buf(const StepLayer& L, int i) {
+Q35_DEV GdnBuf gdn_buf(CLayer& L, int i) {
   if (i & 1) return GdnBuf{L.rec_alt, L.conv_alt, L.rec, L.conv_state};
   return GdnBuf{L.rec, L.conv_state, L.rec_alt, L.conv_alt};
 }
@@ -416,7 +422,7 @@ Q35_DEV int gdn_channel(const StepArgs& a, int h, int t) {
 }
 
 // Everything of the step that does not depend on the qkvz stage: issued before its barrier.
-Q35_DEV void gdn_load(const StepArgs& a, const StepLayer& L, const MvItem& it, int i, GdnPf& g) {
+Q35_DEV void gdn_load(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g) {
   const int tid = tix(), j = tid % kDv, ig = tid / kDv;
   const int h = it.k0 / kDv;
   const GdnBuf b = gdn_buf(L, i);
@@ -447,7 +453,7 @@ Q35_DEV float gdn_colsum(float v, float* part) {
   return s;
 }
 
-Q35_DEV void pro_gdn(const StepArgs& a, const StepLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
+Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
                      float* scratch) {
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int j = tid % kDv, ig = tid / kDv;
@@ -467,12 +473,6 @@ Q35_DEV void pro_gdn(const StepArgs& a, const StepLayer& L, const MvItem& it, in
   if (tid < nch) qkv[tid] = silu_f(((g.cw[0] * g.cs[0] + g.cw[1] * g.cs[1]) + g.cw[2] * g.cs[2]) + g.cw[3] * x);
   const bool writer = it.tl == 0 && (it.k0 % kDv) == 0;  // uniform
   const GdnBuf b = gdn_buf(L, i);
-  if (writer && tid < nch) {  // conv state [c] <- [s1, s2, x]
-    float* cw = b.cst_w + (size_t)c * 3;
-    st_agent(&cw[0], g.cs[1]);
-    st_agent(&cw[1], g.cs[2]);
-    st_agent(&cw[2], x);
-  }
   // gates: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias) (kernels.rs:228-244)
   const float beta = 1.0f / (1.0f + expf(-bs));
   const float xg = as + g.dtb;
@@ -505,7 +505,16 @@ Q35_DEV void pro_gdn(const StepArgs& a, const StepLayer& L, const MvItem& it, in
     const int row = ig * kGdnR + r;
     g.s[r] += (qkv[kDk + row] * rk) * dl;
     o += g.s[r] * ((qkv[row] * rq) * a.qscale);
-    if (writer) st_agent(Sw + (off + (uint32_t)(r * kDv)), g.s[r]);
+  }
+  if (writer) {  // new state, and the conv state [c] <- [s1, s2, x]; one batch, off the loop above
+#pragma unroll
+    for (int r = 0; r < kGdnR; ++r) st_agent(Sw + (off + (uint32_t)(r * kDv)), g.s[r]);
+    if (tid < nch) {
+      float* cw = b.cst_w + (size_t)c * 3;
+      st_agent(&cw[0], g.cs[1]);
+      st_agent(&cw[1], g.cs[2]);
+      st_agent(&cw[2], x);
+    }
   }
   o = gdn_colsum(o, part1);
   // gated RMSNorm over the dv outputs of h: threads tid < dv (waves 0 and 1) hold them
@@ -610,7 +619,7 @@ Q35_DEV void side_tasks(const StepArgs& a, int kind) {
 // kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
 // dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need.
 template <int U = kU>
-Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, int i, int p, Bar& bar,
+Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int p, Bar& bar,
                       const Shared& sh) {
   const Mv d = make_mv(a, L, kind);
   const int nitems = d.t3 * d.nchunk;
@@ -693,7 +702,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, const StepLayer& L, int kind, int pro, 
 // Item (kv head g, chunk c of `chunk` cached tokens) for the rep query heads of g
 // (text_modules.rs:842-944): q/k RMSNorm (1+w), partial RoPE (:739-774), KV append at p
 // (the item holding p), scores, chunk softmax statistics and P.V.
-Q35_DEV bool attn_stage(const StepArgs& a, const StepLayer& L, int p, Bar& bar, const Shared& sh) {
+Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Shared& sh) {
   if (!bar_wait(bar, sh.ok)) return false;
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int T = p + 1, rep = a.ah / a.kvh;
@@ -959,7 +968,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   for (int i = 0; i < a.ntok; ++i) {
     const int p = p0 + i;
     for (int l = 0; l < a.n_layers; ++l) {
-      const StepLayer& L = a.layers[l];
+      CLayer& L = layer_at(a, l);
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
       if (!L.full) {
         if (!mv_stage(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
