@@ -25,10 +25,27 @@ int fail(int code, const std::string& msg);
 Q35_DEV float silu_f(float v) { return v * (1.0f / (1.0f + expf(-v))); }
 Q35_DEV float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 
+// x from lane (l + N) mod 16 of the same 16-lane row (DPP row_ror: a VALU operand modifier, no
+// trip through the LDS crossbar as a lane shuffle takes)
+template <int N>
+Q35_DEV float row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, the same value in every lane: rotations by 8, 4, 2, 1 within
+// each 16-lane row leave every lane with its row's sum; the four row sums are then read from
+// lanes 0, 16, 32 and 48.  Every lane of the wave must be active.
 Q35_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Sum over a 256-thread block; `sh` needs 4 floats of LDS.  All threads get the result.

@@ -69,7 +69,7 @@ constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
 constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
 static_assert(kRed + kRG * kTile <= kSmem, "LDS");
-static_assert(512 + 2 * kT + kDv <= kRG * kTile, "DeltaNet scratch fits in kRed");
+static_assert(512 + 2 * kT <= kRG * kTile, "DeltaNet scratch fits in kRed");
 static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
 static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
 
@@ -455,14 +455,12 @@ Q35_DEV float gdn_colsum(float v, float* part) {
 
 Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
                      float* scratch) {
-  const int tid = tix(), lane = tid & 63, wid = tid >> 6;
+  const int tid = tix(), lane = tid & 63;
   const int j = tid % kDv, ig = tid / kDv;
   const int h = it.k0 / kDv, nch = 2 * kDk + kDv;
-  float* qkv = scratch;                   // [2dk + dv] conv outputs q | k | v of head h
-  float* wsum = scratch + 2 * kDk + kDv;  // [8]
-  float* part0 = scratch + 512;           // [kT]
-  float* part1 = part0 + kT;              // [kT]
-  float* ov = part1 + kT;                 // [dv]
+  float* qkv = scratch;          // [2dk + dv] conv outputs q | k | v of head h
+  float* part0 = scratch + 512;  // [kT] per-row-group column partials
+  float* part1 = part0 + kT;     // [kT]
   // qkvz-stage outputs: the thread's conv input, its z element and the two gate projections
   const int c = gdn_channel(a, h, min(tid, nch - 1));
   const fx_t xr = ld_agent(&a.acc_proj[c]);
@@ -479,32 +477,30 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   const float pre = logf(expf(xg) + 1.0f);
   const float decay = expf(-expf(g.alog) * (pre > 20.0f ? xg : pre));
   __syncthreads();
-  if (wid < 4) {  // waves 0,1: q; waves 2,3: k (dk = 128)
-    const float v = qkv[tid];
-    const float ss = wave_sum(v * v);
-    if (lane == 0) wsum[wid] = ss;
-  }
-  __syncthreads();
-  const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
-  const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
-  // S <- decay * S;  m = S^T k
+  // l2 norms of q and k (dk = 128): every wave sums all the squares itself, so no second barrier
+  const float q0 = qkv[lane], q1 = qkv[lane + 64], k0 = qkv[kDk + lane], k1 = qkv[kDk + lane + 64];
+  const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+  const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
+  // The l2 normalisations are applied once per column sum instead of per row:
+  // S <- decay * S;  m = rk * S^T k_raw
+  const float* kr = qkv + kDk + ig * kGdnR;
+  const float* qr = qkv + ig * kGdnR;
   float m = 0.f;
 #pragma unroll
   for (int r = 0; r < kGdnR; ++r) {
     g.s[r] *= decay;
-    m += g.s[r] * (qkv[kDk + ig * kGdnR + r] * rk);
+    m += g.s[r] * kr[r];
   }
-  m = gdn_colsum(m, part0);
-  // delta = (v - m) * beta;  S <- S + k delta^T;  o = S^T q
-  const float dl = (qkv[2 * kDk + j] - m) * beta;
+  m = gdn_colsum(m, part0) * rk;
+  // delta = (v - m) * beta;  S <- S + k delta^T = S + k_raw (rk delta)^T;  o = (rq qscale) S^T q_raw
+  const float dlk = ((qkv[2 * kDk + j] - m) * beta) * rk;
   float o = 0.f;
   float* Sw = b.S_w + (size_t)h * kDk * kDv;
   const uint32_t off = (uint32_t)(ig * kGdnR * kDv + j);
 #pragma unroll
   for (int r = 0; r < kGdnR; ++r) {
-    const int row = ig * kGdnR + r;
-    g.s[r] += (qkv[kDk + row] * rk) * dl;
-    o += g.s[r] * ((qkv[row] * rq) * a.qscale);
+    g.s[r] += kr[r] * dlk;
+    o += g.s[r] * qr[r];
   }
   if (writer) {  // new state, and the conv state [c] <- [s1, s2, x]; one batch, off the loop above
 #pragma unroll
@@ -516,16 +512,20 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
       st_agent(&cw[2], x);
     }
   }
-  o = gdn_colsum(o, part1);
-  // gated RMSNorm over the dv outputs of h: threads tid < dv (waves 0 and 1) hold them
-  if (tid < kDv) {
-    ov[tid] = o;
-    const float ss = wave_sum(o * o);
-    if (lane == 0) wsum[4 + wid] = ss;
-  }
+  part1[tid] = o;
   __syncthreads();
-  const float rg = 1.0f / sqrtf((wsum[4] + wsum[5]) / (float)kDv + a.eps);
-  if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(from_fx(zr));
+  // o_j = (rq qscale) * sum over row groups of part1[g][j]; gated RMSNorm over the dv outputs of
+  // h, whose sum of squares every wave forms itself (no further barrier)
+  const float fq = rq * a.qscale;
+  auto ocol = [&](int jj) {
+    float s = 0.f;
+#pragma unroll
+    for (int gg = 0; gg < kGdnG; ++gg) s += part1[gg * kDv + jj];
+    return s * fq;
+  };
+  const float oa = ocol(lane), ob = ocol(lane + 64);
+  const float rg = 1.0f / sqrtf(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
+  if (tid < it.klen) xs[tid] = (g.nw * (ocol(it.k0 % kDv + tid) * rg)) * silu_f(from_fx(zr));
 }
 
 Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
