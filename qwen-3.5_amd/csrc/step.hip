@@ -319,36 +319,39 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
   __syncthreads();
 }
 
-// xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j].  All
-// loads (x and the thread's norm weights) are issued before any value is used (indices clamped,
-// masked afterwards), so the prologue costs one round trip: `load(k)` returns the raw element,
-// `conv` turns it into f32.
-template <class Raw, class Load, class Conv>
+// xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j],
+// j < KR (K <= 512 KR).  All loads (x and the thread's norm weights) are issued before any value
+// is used, and all KR of each (indices clamped, masked afterwards): a compile-time number of
+// loads, so the compiler's waits on them are exact.  The prologue costs one round trip:
+// `load(k)` returns the raw element, `conv` turns it into f32.  `post` (more weight loads of the
+// caller) is issued behind the prologue's loads and before their first use; scheduling barriers
+// keep the compiler from moving either group across it.
+template <int KR, class Raw, class Load, class Conv, class Post>
 Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int k0, int klen, float* xs,
-                     float* shs) {
+                     float* shs, Post post) {
   const int tid = tix();
-  Raw raw[kRmsRegs];
-  float wn[kRmsRegs];
+  Raw raw[KR];
+  float wn[KR];
 #pragma unroll
-  for (int j = 0; j < kRmsRegs; ++j) {
-    if (kT * j >= K) break;  // uniform
+  for (int j = 0; j < KR; ++j) {
     const int k = tid + kT * j;
     raw[j] = load(min(k, K - 1));
     wn[j] = ldg(w + min(max(k, k0), k0 + klen - 1));
   }
-  float v[kRmsRegs];
+  __builtin_amdgcn_sched_barrier(0);
+  post();
+  __builtin_amdgcn_sched_barrier(0);
+  float v[KR];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRmsRegs; ++j) {
-    if (kT * j >= K) break;
+  for (int j = 0; j < KR; ++j) {
     v[j] = (tid + kT * j < K) ? conv(raw[j]) : 0.f;
     ss += v[j] * v[j];
   }
   ss = block_sum(ss, shs);
   const float r = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
-  for (int j = 0; j < kRmsRegs; ++j) {
-    if (kT * j >= K) break;
+  for (int j = 0; j < KR; ++j) {
     const int k = tid + kT * j;
     if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + wn[j]);
   }
@@ -361,6 +364,19 @@ struct HLoad {
 };
 struct HConv {
   Q35_DEV float operator()(fx_t x) const { return from_fx(x); }
+};
+// a row of the Q8F embedding table as pro_rms input: (byte, block scale) pairs
+struct EmbRaw {
+  int8_t q;
+  float s;
+};
+struct EmbLoad {
+  const int8_t* q;
+  const float* s;
+  Q35_DEV EmbRaw operator()(int k) const { return EmbRaw{ldg(q + k), ldg(s + (k >> 6))}; }
+};
+struct EmbConv {
+  Q35_DEV float operator()(EmbRaw x) const { return (float)x.q * x.s; }
 };
 
 // Token of step i at position p: the prompt id while p < plen, else the argmax of the previous
@@ -617,8 +633,9 @@ Q35_DEV void side_tasks(const StepArgs& a, int kind) {
 
 // One matvec stage.  The in_proj_b / in_proj_a gate projection (f32, [H][nh] each,
 // kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
-// dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need.
-template <int U = kU>
+// dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need;
+// KR: hidden-size elements per thread in the RMSNorm prologue (hidden <= 512 KR).
+template <int U, int KR>
 Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int p, Bar& bar,
                       const Shared& sh) {
   const Mv d = make_mv(a, L, kind);
@@ -650,31 +667,27 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
       mv_load(it, d.K, pf);
       if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
     }
+    auto none = []() {};
     switch (pro) {
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
-        const int8_t* eq = a.emb_q + (size_t)tok * K;
-        const float* es = a.emb_s + (size_t)tok * nbK;
-        auto src = [&](int k) { return (float)ldg(eq + k) * ldg(es + (k >> 6)); };
-        auto same = [](float x) { return x; };
-        pro_rms<float>(src, same, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs);
+        const EmbLoad src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
+        pro_rms<KR, EmbRaw>(src, EmbConv{}, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs, none);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row
-          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k], to_fx(src(k)));
+          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k], to_fx(EmbConv{}(src(k))));
       } break;
       case PRO_RMS:
-        pro_rms<fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen, xs,
-                      sh.shs);
+        pro_rms<KR, fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen,
+                          xs, sh.shs, none);
         break;
       case PRO_GDN:
         pro_gdn(a, L, it, i, gp, xs, red);
         break;
-      case PRO_SWIGLU:
-        for (int r = tix(); r < it.klen; r += kT) {
-          const int k = it.k0 + r;
-          const fx_t up = ld_agent(&a.acc_gu[a.F + k]), gate = ld_agent(&a.acc_gu[k]);
-          xs[r] = from_fx(up) * silu_f(from_fx(gate));
-        }
-        break;
+      case PRO_SWIGLU: {  // klen <= 512 = threads: one element per thread
+        const int k = it.k0 + min(tix(), it.klen - 1);
+        const fx_t up = ld_agent(&a.acc_gu[a.F + k]), gate = ld_agent(&a.acc_gu[k]);
+        if (tix() < it.klen) xs[tix()] = from_fx(up) * silu_f(from_fx(gate));
+      } break;
       default:  // PRO_ATTN: merged attention output
         pro_attn(a, p + 1, it.k0, it.klen, xs, red);
         break;
@@ -902,10 +915,12 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
   const int rb0 = bix(), gs = gridDim.x;
   if (rb0 < nrb) load(rb0, wa, sa);
   if (!bar_wait(bar, sh.ok)) return false;
-  pro_rms<fx_t>(HLoad{a.h}, HConv{}, K, a.final_norm, a.eps, 0, K, xs, sh.shs);
+  // the second row block is issued behind the norm's inputs (rows clamped: always in the table)
+  pro_rms<2 * CPW, fx_t>(HLoad{a.h}, HConv{}, K, a.final_norm, a.eps, 0, K, xs, sh.shs,
+                         [&]() { load(rb0 + gs, wb, sb); });
   __syncthreads();
   for (int rb = rb0; rb < nrb; rb += 2 * gs) {
-    if (rb + gs < nrb) load(rb + gs, wb, sb);
+    if (rb != rb0 && rb + gs < nrb) load(rb + gs, wb, sb);
     compute(rb, wa, sa);
     if (rb + gs >= nrb) break;
     if (rb + 2 * gs < nrb) load(rb + 2 * gs, wa, sa);
@@ -957,6 +972,7 @@ Q35_DEV void state_copy_back(const StepArgs& a) {
 // ------------------------------------------------------------------ the kernel
 template <int CPW>
 __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
+  constexpr int KR = 2 * CPW;  // hidden <= 256 CPW = 512 KR
   __shared__ __align__(16) float smem[kSmem];
   __shared__ float shs[kNW];
   __shared__ float shv[kNW];
@@ -971,15 +987,15 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
       CLayer& L = layer_at(a, l);
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
       if (!L.full) {
-        if (!mv_stage(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
-        if (!mv_stage<kUOut>(a, L, SMV_OUT, PRO_GDN, i, p, bar, sh)) return;
+        if (!mv_stage<kU, KR>(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
+        if (!mv_stage<kUOut, KR>(a, L, SMV_OUT, PRO_GDN, i, p, bar, sh)) return;
       } else {
-        if (!mv_stage(a, L, SMV_QKV, pro0, i, p, bar, sh)) return;
+        if (!mv_stage<kU, KR>(a, L, SMV_QKV, pro0, i, p, bar, sh)) return;
         if (!attn_stage(a, L, p, bar, sh)) return;
-        if (!mv_stage(a, L, SMV_O, PRO_ATTN, i, p, bar, sh)) return;
+        if (!mv_stage<kU, KR>(a, L, SMV_O, PRO_ATTN, i, p, bar, sh)) return;
       }
-      if (!mv_stage(a, L, SMV_GU, PRO_RMS, i, p, bar, sh)) return;
-      if (!mv_stage(a, L, SMV_DOWN, PRO_SWIGLU, i, p, bar, sh)) return;
+      if (!mv_stage<kU, KR>(a, L, SMV_GU, PRO_RMS, i, p, bar, sh)) return;
+      if (!mv_stage<kU, KR>(a, L, SMV_DOWN, PRO_SWIGLU, i, p, bar, sh)) return;
     }
     if (!lm_stage<CPW>(a, bar, sh)) return;
   }
