@@ -93,6 +93,15 @@ Q35_DEV uint4 ldg16(const void* p) {
   const q35_u32x4 v = *(const Q35_GLOBAL q35_u32x4*)p;
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// The same with the non-temporal hint, for the weight stream: each weight is read once per
+// decode step and the stream is far larger than the caches, so it should not evict what is
+// reused (the kernel's code, norm weights, the small shared activations).
+Q35_DEV uint4 ldg16_nt(const void* p) {
+  const q35_u32x4 v = __builtin_nontemporal_load((const Q35_GLOBAL q35_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <class T>
+Q35_DEV T ldg_nt(const T* p) { return __builtin_nontemporal_load((const Q35_GLOBAL T*)p); }
 
 Q35_DEV void fx_add(fx_t* p, float v) {
   __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v), __ATOMIC_RELAXED,

@@ -283,8 +283,8 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
   for (int u = 0; u < U; ++u) {
     if (kRG * u >= it.klen) break;  // uniform
     const uint32_t row = row0 + (uint32_t)min(rr + kRG * u, it.klen - 1);
-    pf.w[u] = ldg16(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16)));
-    pf.s[u] = ldg(it.s + (row * (uint32_t)(kTile / 64) + (uint32_t)(cg >> 2)));
+    pf.w[u] = ldg16_nt(it.w + (row * (uint32_t)kTile + (uint32_t)(cg * 16)));
+    pf.s[u] = ldg_nt(it.s + (row * (uint32_t)(kTile / 64) + (uint32_t)(cg >> 2)));
   }
 }
 
@@ -872,8 +872,8 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
       for (int c = 0; c < CPW; ++c) {
         // branch-free: clamped into the table; compute() drops rows past V and chunks past K
         const uint32_t rw = (uint32_t)min(row, a.V - 1), k = (uint32_t)min(16 * (lane + 64 * c), K - 16);
-        wv[r][c] = ldg16(a.emb_q + (rw * (uint32_t)K + k));
-        sv[r][c] = ldg(a.emb_s + (rw * (uint32_t)nbK + (k >> 6)));
+        wv[r][c] = ldg16_nt(a.emb_q + (rw * (uint32_t)K + k));
+        sv[r][c] = ldg_nt(a.emb_s + (rw * (uint32_t)nbK + (k >> 6)));
       }
     }
   };
