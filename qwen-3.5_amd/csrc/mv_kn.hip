@@ -280,8 +280,8 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
     for (int u = 0; u < U; ++u) {
       const int r = r0 + rr + kRowsPerStep * u;
       const bool ok = colok && r < klen;
-      wv[u] = ok ? *reinterpret_cast<const uint4*>(wbase + (size_t)r * N) : make_uint4(0, 0, 0, 0);
-      sv[u] = ok ? sbase[(size_t)r * nb] : 0.f;
+      wv[u] = ok ? ldg16_nt(wbase + (size_t)r * N) : make_uint4(0, 0, 0, 0);
+      sv[u] = ok ? ldg_nt(sbase + (size_t)r * nb) : 0.f;
     }
   };
   load_batch(0);

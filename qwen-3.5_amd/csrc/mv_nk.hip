@@ -126,8 +126,8 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
       for (int c = 0; c < CPW; ++c) {
         const int k = 16 * (lane + 64 * c);
         const bool ok = row < a.N && k < K;
-        wv[r][c] = ok ? *reinterpret_cast<const uint4*>(a.q + (size_t)row * K + k) : make_uint4(0, 0, 0, 0);
-        sv[r][c] = ok ? a.s[(size_t)row * nbK + (k >> 6)] : 0.f;
+        wv[r][c] = ok ? ldg16_nt(a.q + (size_t)row * K + k) : make_uint4(0, 0, 0, 0);
+        sv[r][c] = ok ? ldg_nt(a.s + (size_t)row * nbK + (k >> 6)) : 0.f;
       }
     }
 #pragma unroll
