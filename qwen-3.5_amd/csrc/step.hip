@@ -102,10 +102,9 @@ Q35_DEV float block_sum(float v, float* shs) {
   __syncthreads();
   if (lane == 0) shs[wid] = v;
   __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int w = 0; w < kNW; ++w) t += shs[w];
-  return t;
+  static_assert(kNW == 8, "two 16-byte reads");
+  const float4 a = *reinterpret_cast<const float4*>(shs), b = *reinterpret_cast<const float4*>(shs + 4);
+  return ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;
 }
 
 Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
@@ -310,9 +309,14 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
   for (int q = 0; q < 4; ++q) dst[q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
   __syncthreads();
   if (tid < kTile) {
+    // all 32 partials read before any is summed: one LDS round trip instead of one per batch
+    float pr[kRG];
+#pragma unroll
+    for (int i = 0; i < kRG; ++i) pr[i] = red[i * kTile + tid];
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the sums (not interleaved)
     float v = 0.f;
-#pragma unroll 8
-    for (int i = 0; i < kRG; ++i) v += red[i * kTile + tid];
+#pragma unroll
+    for (int i = 0; i < kRG; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
     if (n < it.N) fx_add(&it.acc[n], v);
   }
@@ -974,7 +978,7 @@ template <int CPW>
 __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   constexpr int KR = 2 * CPW;  // hidden <= 256 CPW = 512 KR
   __shared__ __align__(16) float smem[kSmem];
-  __shared__ float shs[kNW];
+  __shared__ __align__(16) float shs[kNW];
   __shared__ float shv[kNW];
   __shared__ int shi[kNW];
   __shared__ int ok;
