@@ -719,12 +719,37 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
 // Item (kv head g, chunk c of `chunk` cached tokens) for the rep query heads of g
 // (text_modules.rs:842-944): q/k RMSNorm (1+w), partial RoPE (:739-774), KV append at p
 // (the item holding p), scores, chunk softmax statistics and P.V.
+//
+// Nothing the qkv stage writes is needed to fetch the first item's cached K / V rows t < p
+// (written by earlier steps), the q / k norm weights and the thread's RoPE factors, so they are
+// loaded before the barrier: after it the stage has one memory round trip (its q, k, v inputs)
+// instead of four.  Wave w holds rows t0 + w + 8j, j < kAttnPf; rows beyond are loaded in-stage.
+constexpr int kAttnPf = 2;
 Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Shared& sh) {
-  if (!bar_wait(bar, sh.ok)) return false;
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int T = p + 1, rep = a.ah / a.kvh;
   int chunk, nact;
   attn_chunking(a, T, chunk, nact);
+  float4 kp[kAttnPf], vp[kAttnPf];
+  {
+    const int it0 = min((int)bix(), a.kvh * nact - 1);
+    const int g = it0 / nact, t0 = (it0 % nact) * chunk;
+    const float* Kc = L.kc + (size_t)g * a.tmax * kHd;
+    const float* Vc = L.vc + (size_t)g * a.tmax * kHd;
+#pragma unroll
+    for (int j = 0; j < kAttnPf; ++j) {  // clamped to written rows; the row at p comes from LDS
+      const int t = max(0, min(t0 + wid + kNW * j, p - 1));
+      kp[j] = ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]);
+      vp[j] = ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]);
+    }
+  }
+  const float4 qw = make_float4(ldg(L.q_norm + 4 * lane), ldg(L.q_norm + 4 * lane + 1), ldg(L.q_norm + 4 * lane + 2),
+                                ldg(L.q_norm + 4 * lane + 3));
+  const float4 kw = make_float4(ldg(L.k_norm + 4 * lane), ldg(L.k_norm + 4 * lane + 1), ldg(L.k_norm + 4 * lane + 2),
+                                ldg(L.k_norm + 4 * lane + 3));
+  const float csv = ldg(a.rope_cos + (size_t)p * a.rot + tid % a.rot);  // rot divides 512: the same
+  const float snv = ldg(a.rope_sin + (size_t)p * a.rot + tid % a.rot);  // element in every round
+  if (!bar_wait(bar, sh.ok)) return false;
   float* qn = sh.smem;               // [kMaxRep][kHd]
   float* kn = qn + kMaxRep * kHd;    // [kHd]
   float* vn = kn + kHd;              // [kHd]
@@ -734,7 +759,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
   float* hm = ored + kNW * kMaxRep * kHd;  // [kMaxRep]
   float* hl = hm + kMaxRep;                // [kMaxRep]
   const int ldqg = a.ah * kHd * 2;
-  for (int item = bix(); item < a.kvh * nact; item += gridDim.x) {
+  for (int item = bix(), first = 1; item < a.kvh * nact; item += gridDim.x, first = 0) {
     const int g = item / nact, c = item % nact;
     const int t0 = c * chunk, len = min(chunk, T - t0);
     const bool has_new = (c == nact - 1);
@@ -744,18 +769,18 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
         const float4 v = ld4_fx(&a.acc_proj[(size_t)(g * rep + w) * 2 * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
-        qn[w * kHd + d + 0] = (v.x * r) * (1.0f + ldg(L.q_norm + d + 0));
-        qn[w * kHd + d + 1] = (v.y * r) * (1.0f + ldg(L.q_norm + d + 1));
-        qn[w * kHd + d + 2] = (v.z * r) * (1.0f + ldg(L.q_norm + d + 2));
-        qn[w * kHd + d + 3] = (v.w * r) * (1.0f + ldg(L.q_norm + d + 3));
+        qn[w * kHd + d + 0] = (v.x * r) * (1.0f + qw.x);
+        qn[w * kHd + d + 1] = (v.y * r) * (1.0f + qw.y);
+        qn[w * kHd + d + 2] = (v.z * r) * (1.0f + qw.z);
+        qn[w * kHd + d + 3] = (v.w * r) * (1.0f + qw.w);
       } else if (w == rep) {
         const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)g * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
-        kn[d + 0] = (v.x * r) * (1.0f + ldg(L.k_norm + d + 0));
-        kn[d + 1] = (v.y * r) * (1.0f + ldg(L.k_norm + d + 1));
-        kn[d + 2] = (v.z * r) * (1.0f + ldg(L.k_norm + d + 2));
-        kn[d + 3] = (v.w * r) * (1.0f + ldg(L.k_norm + d + 3));
+        kn[d + 0] = (v.x * r) * (1.0f + kw.x);
+        kn[d + 1] = (v.y * r) * (1.0f + kw.y);
+        kn[d + 2] = (v.z * r) * (1.0f + kw.z);
+        kn[d + 3] = (v.w * r) * (1.0f + kw.w);
       } else {
         const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)(a.kvh + g) * kHd + d]);
         *reinterpret_cast<float4*>(&vn[d]) = v;
@@ -764,14 +789,12 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
     __syncthreads();
     // RoPE on dims [0, rot): x' = x*cos + rotate_half(x)*sin
     const int half = a.rot / 2;
-    const float* cs = a.rope_cos + (size_t)p * a.rot;
-    const float* sn = a.rope_sin + (size_t)p * a.rot;
     const int nrot = rep + (has_new ? 1 : 0);
     for (int e = tid; e < nrot * a.rot; e += kT) {
       const int hh = e / a.rot, ii = e % a.rot;
       const float* src = (hh < rep) ? qn + hh * kHd : kn;
       const float rh = (ii < half) ? -src[ii + half] : src[ii - half];
-      rtmp[hh * kHd + ii] = src[ii] * ldg(cs + ii) + rh * ldg(sn + ii);
+      rtmp[hh * kHd + ii] = src[ii] * csv + rh * snv;
     }
     __syncthreads();
     for (int e = tid; e < nrot * a.rot; e += kT) {
@@ -791,9 +814,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
     for (int h = 0; h < kMaxRep; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) q4[h][e] = (h < rep) ? qn[h * kHd + 4 * lane + e] : 0.f;
-    for (int tt = wid; tt < len; tt += kNW) {
-      const int t = t0 + tt;
-      const float4 kv = (t == p) ? *reinterpret_cast<const float4*>(&kn[4 * lane]) : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]);
+    auto score = [&](int tt, float4 kv) {
 #pragma unroll
       for (int h = 0; h < kMaxRep; ++h) {
         if (h >= rep) break;
@@ -801,6 +822,19 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
         dd = wave_sum(dd);
         if (lane == 0) sc[h * kMaxChunk + tt] = dd * a.ascale;
       }
+    };
+    const float4 kn4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
+#pragma unroll
+    for (int j = 0; j < kAttnPf; ++j) {  // rows held since before the barrier (first item)
+      const int tt = wid + kNW * j;
+      if (tt >= len) break;  // uniform
+      const int t = t0 + tt;
+      const float4 kv = (t == p) ? kn4 : (first ? kp[j] : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]));
+      score(tt, kv);
+    }
+    for (int tt = wid + kNW * kAttnPf; tt < len; tt += kNW) {
+      const int t = t0 + tt;
+      score(tt, (t == p) ? kn4 : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]));
     }
     __syncthreads();
     for (int h = wid; h < rep; h += kNW) {
@@ -822,15 +856,25 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
     for (int h = 0; h < kMaxRep; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
-    for (int tt = wid; tt < len; tt += kNW) {
-      const int t = t0 + tt;
-      const float4 vv = (t == p) ? *reinterpret_cast<const float4*>(&vn[4 * lane]) : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]);
+    auto pv = [&](int tt, float4 vv) {
 #pragma unroll
       for (int h = 0; h < kMaxRep; ++h) {
         if (h >= rep) break;
         const float pe = sc[h * kMaxChunk + tt];
         acc[h][0] += pe * vv.x; acc[h][1] += pe * vv.y; acc[h][2] += pe * vv.z; acc[h][3] += pe * vv.w;
       }
+    };
+    const float4 vn4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
+#pragma unroll
+    for (int j = 0; j < kAttnPf; ++j) {
+      const int tt = wid + kNW * j;
+      if (tt >= len) break;  // uniform
+      const int t = t0 + tt;
+      pv(tt, (t == p) ? vn4 : (first ? vp[j] : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane])));
+    }
+    for (int tt = wid + kNW * kAttnPf; tt < len; tt += kNW) {
+      const int t = t0 + tt;
+      pv(tt, (t == p) ? vn4 : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]));
     }
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h)
@@ -1050,6 +1094,8 @@ int step_validate(const q35_dims& d, int tmax, int grid) {
     return fail(Q35_E_SHAPE, "persistent step: DeltaNet needs dk 128, dv 128, conv 4");
   if (d.head_dim != kHd || d.kv_heads < 1 || d.attn_heads % d.kv_heads != 0 || d.attn_heads / d.kv_heads > kMaxRep)
     return fail(Q35_E_SHAPE, "persistent step: attention needs head_dim 256 and <= 4 query heads per kv head");
+  if (d.rot_dim < 2 || d.rot_dim > kHd || (d.rot_dim % 2) != 0 || (kT % d.rot_dim) != 0)
+    return fail(Q35_E_SHAPE, "persistent step: rotary dims must be even, <= 256 and divide 512");
   if ((long long)tmax > (long long)kMaxChunk * step_att_nmax(grid, d.kv_heads))
     return fail(Q35_E_SHAPE, "persistent step: tmax too large for the attention split");
   return Q35_OK;
