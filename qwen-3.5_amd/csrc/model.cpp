@@ -216,9 +216,12 @@ int setup_persistent(q35_model* m) {
   uint32_t* bar = nullptr;
   float *att_ml = nullptr, *att_o = nullptr, *arg_v = nullptr;
   int32_t* arg_i = nullptr;
+  fx_t* gate_acc = nullptr;
+  const size_t gate_n = (size_t)2 * nh * kStepBaStride;
   int rc;
   if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
       (rc = dev_alloc_t(m, "step_barrier", kStepBarBytes / 4, &bar)) ||
+      (rc = dev_alloc_t(m, "step_gate_acc", gate_n, &gate_acc)) ||
       (rc = dev_alloc_t(m, "attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
       (rc = dev_alloc_t(m, "attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
       (rc = dev_alloc_t(m, "argmax_partial_v", (size_t)grid, &arg_v)) ||
@@ -226,6 +229,7 @@ int setup_persistent(q35_model* m) {
     return rc;
   Q35_HIP_TRY(hipMemcpy(dl, hl.data(), hl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
   Q35_HIP_TRY(hipMemset(bar, 0, kStepBarBytes));
+  Q35_HIP_TRY(hipMemset(gate_acc, 0, gate_n * sizeof(fx_t)));  // the step kernel keeps it zero between layers
   StepArgs& a = m->step_args;
   a.layers = dl; a.n_layers = d.n_layers;
   a.H = d.hidden; a.F = d.ffn; a.V = d.vocab; a.nh = nh; a.dk = d.lin_dk; a.dv = d.lin_dv;
@@ -237,8 +241,8 @@ int setup_persistent(q35_model* m) {
   step_plan(d, grid, a.mv);
   a.emb_q = m->embed.q; a.emb_s = m->embed.s; a.final_norm = m->final_norm;
   a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-  a.h = m->h; a.acc_proj = m->acc_proj; a.acc_ba = m->acc_ba; a.acc_gu = m->acc_gu;
-  a.acc_zero_n = m->acc_proj_n + 2 * nh;
+  a.h = m->h; a.acc_proj = m->acc_proj; a.acc_ba = gate_acc; a.acc_gu = m->acc_gu;
+  a.acc_zero_n = m->acc_proj_n;
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
@@ -462,7 +466,7 @@ int q35_model_reset(q35_model* m, void* stream) {
     const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
                        n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
                        n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt" ||
-                       n == "h" || n == "acc_proj" || n == "acc_gu";
+                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
   m->host_pos = 0;

@@ -407,8 +407,9 @@ struct StepArgs {
   StepMv mv[SMV_COUNT];
   const int8_t* emb_q; const float* emb_s; const float* final_norm;
   const float *rope_cos, *rope_sin;
-  fx_t *h, *acc_proj, *acc_ba, *acc_gu;
-  int64_t acc_zero_n;  // acc_proj + acc_ba entries cleared by the gate|up stage
+  fx_t *h, *acc_proj, *acc_gu;
+  fx_t* acc_ba;        // in_proj_b | in_proj_a sums, one per kStepBaStride entries (own cache line)
+  int64_t acc_zero_n;  // acc_proj entries cleared by the gate|up stage
   float *att_ml, *att_o;
   int32_t att_nmax;    // attention chunks per kv head
   float* logits;       // may be null
@@ -418,6 +419,9 @@ struct StepArgs {
   int32_t ntok;
 };
 constexpr size_t kStepBarBytes = 16384;
+// Every block of the qkvz stage adds into the 2 x lin_heads gate accumulators; packed, they
+// would share two cache lines and the atomics would serialise on them.
+constexpr int kStepBaStride = 16;  // fx_t entries (128 bytes)
 constexpr int kStepErrWord = 3072;
 constexpr int kStepThreads = 512;
 // Blocks of the persistent kernel that fit co-resident (one per CU); 0 if the kernel cannot run.

@@ -485,8 +485,8 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   const int c = gdn_channel(a, h, min(tid, nch - 1));
   const fx_t xr = ld_agent(&a.acc_proj[c]);
   const fx_t zr = ld_agent(&a.acc_proj[a.conv_dim + it.k0 + min(tid, it.klen - 1)]);
-  const float bs = from_fx(ld_agent(&a.acc_ba[h]));
-  const float as = from_fx(ld_agent(&a.acc_ba[a.nh + h]));
+  const float bs = from_fx(ld_agent(&a.acc_ba[(size_t)h * kStepBaStride]));
+  const float as = from_fx(ld_agent(&a.acc_ba[(size_t)(a.nh + h) * kStepBaStride]));
   const float x = from_fx(xr);
   if (tid < nch) qkv[tid] = silu_f(((g.cw[0] * g.cs[0] + g.cw[1] * g.cs[1]) + g.cw[2] * g.cs[2]) + g.cw[3] * x);
   const bool writer = it.tl == 0 && (it.k0 % kDv) == 0;  // uniform
@@ -632,6 +632,7 @@ Q35_DEV void side_tasks(const StepArgs& a, int kind) {
     for (int64_t i = gt; i < 2 * (int64_t)a.F; i += gs) st_agent(&a.acc_gu[i], (fx_t)0);
   } else if (kind == SMV_GU) {  // projection + gate accumulators: last read by the out / o stage
     for (int64_t i = gt; i < a.acc_zero_n; i += gs) st_agent(&a.acc_proj[i], (fx_t)0);
+    if (gt < 2 * a.nh) st_agent(&a.acc_ba[gt * kStepBaStride], (fx_t)0);
   }
 }
 
@@ -706,7 +707,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
         }
         const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
         const float s = block_sum(v, sh.shs);
-        if (tix() == 0) fx_add(&a.acc_ba[o], s);
+        if (tix() == 0) fx_add(&a.acc_ba[(size_t)o * kStepBaStride], s);
       }
     }
     mv_compute(it, pf, xs, red);
