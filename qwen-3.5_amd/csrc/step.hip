@@ -69,7 +69,7 @@ constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
 constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
 static_assert(kRed + kRG * kTile <= kSmem, "LDS");
-static_assert(512 + 2 * kT <= kRG * kTile, "DeltaNet scratch fits in kRed");
+static_assert(512 + 2 * kT + kDv <= kRG * kTile, "DeltaNet scratch fits in kRed");
 static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
 static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
 
@@ -96,10 +96,12 @@ struct Shared {
 };
 
 // ------------------------------------------------------------------ block reductions
-Q35_DEV float block_sum(float v, float* shs) {
+// lead_sync = false: the caller guarantees a workgroup barrier between the previous block_sum's
+// reads of shs and this call.
+Q35_DEV float block_sum(float v, float* shs, bool lead_sync = true) {
   v = wave_sum(v);
   const int lane = tix() & 63, wid = tix() >> 6;
-  __syncthreads();
+  if (lead_sync) __syncthreads();
   if (lane == 0) shs[wid] = v;
   __syncthreads();
   static_assert(kNW == 8, "two 16-byte reads");
@@ -352,7 +354,9 @@ Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int
     v[j] = (tid + kT * j < K) ? conv(raw[j]) : 0.f;
     ss += v[j] * v[j];
   }
-  ss = block_sum(ss, shs);
+  // every caller reaches here right after a workgroup barrier (the stage's grid-barrier wait, or
+  // the previous item's reduction), so the block sum needs no leading one
+  ss = block_sum(ss, shs, false);
   const float r = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
@@ -461,18 +465,6 @@ Q35_DEV void gdn_load(const StepArgs& a, CLayer& L, const MvItem& it, int i, Gdn
   g.alog = ldg(L.a_log + h);
 }
 
-// Sums v (the thread's partial over its rows of column j) over the row groups through LDS
-// part [kT]; every thread gets the sum of its column.
-Q35_DEV float gdn_colsum(float v, float* part) {
-  const int tid = tix(), j = tid % kDv;
-  part[tid] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int g = 0; g < kGdnG; ++g) s += part[g * kDv + j];
-  return s;
-}
-
 Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
                      float* scratch) {
   const int tid = tix(), lane = tid & 63;
@@ -481,6 +473,7 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   float* qkv = scratch;          // [2dk + dv] conv outputs q | k | v of head h
   float* part0 = scratch + 512;  // [kT] per-row-group column partials
   float* part1 = part0 + kT;     // [kT]
+  float* ov = part1 + kT;        // [dv] outputs of head h
   // qkvz-stage outputs: the thread's conv input, its z element and the two gate projections
   const int c = gdn_channel(a, h, min(tid, nch - 1));
   const fx_t xr = ld_agent(&a.acc_proj[c]);
@@ -501,30 +494,45 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   const float q0 = qkv[lane], q1 = qkv[lane + 64], k0 = qkv[kDk + lane], k1 = qkv[kDk + lane + 64];
   const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
   const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
-  // The l2 normalisations are applied once per column sum instead of per row:
-  // S <- decay * S;  m = rk * S^T k_raw
+  const float kq = wave_sum(q0 * k0 + q1 * k1);  // k_raw . q_raw
+  // With k = rk k_raw, q = rq qscale q_raw and S the old state:
+  //   S' = decay S,  m = S'^T k = decay rk u,  delta = beta (v - m),  S'' = S' + k delta^T,
+  //   o = S''^T q = rq qscale (decay w + rk kq delta),  u = S^T k_raw,  w = S^T q_raw,
+  // so one pass over the state gives u and w, and only the writer forms S'' (to store it).
   const float* kr = qkv + kDk + ig * kGdnR;
   const float* qr = qkv + ig * kGdnR;
-  float m = 0.f;
+  float u = 0.f, w = 0.f;
 #pragma unroll
   for (int r = 0; r < kGdnR; ++r) {
-    g.s[r] *= decay;
-    m += g.s[r] * kr[r];
+    u += g.s[r] * kr[r];
+    w += g.s[r] * qr[r];
   }
-  m = gdn_colsum(m, part0) * rk;
-  // delta = (v - m) * beta;  S <- S + k delta^T = S + k_raw (rk delta)^T;  o = (rq qscale) S^T q_raw
-  const float dlk = ((qkv[2 * kDk + j] - m) * beta) * rk;
-  float o = 0.f;
-  float* Sw = b.S_w + (size_t)h * kDk * kDv;
-  const uint32_t off = (uint32_t)(ig * kGdnR * kDv + j);
+  part0[tid] = u;
+  part1[tid] = w;
+  __syncthreads();
+  auto colsum = [&](const float* part, int jj) {  // sum over the row groups of column jj
+    float s = 0.f;
 #pragma unroll
-  for (int r = 0; r < kGdnR; ++r) {
-    g.s[r] += kr[r] * dlk;
-    o += g.s[r] * qr[r];
-  }
-  if (writer) {  // new state, and the conv state [c] <- [s1, s2, x]; one batch, off the loop above
+    for (int gg = 0; gg < kGdnG; ++gg) s += part[gg * kDv + jj];
+    return s;
+  };
+  // the thread's column j: delta and output (the ig = 0 threads publish the dv outputs)
+  const float dl = (qkv[2 * kDk + j] - (decay * rk) * colsum(part0, j)) * beta;
+  const float oj = (rq * a.qscale) * (decay * colsum(part1, j) + (rk * kq) * dl);
+  if (tid < kDv) ov[tid] = oj;
+  __syncthreads();
+  // gated RMSNorm over the dv outputs of h, whose sum of squares every wave forms itself
+  const float oa = ov[lane], ob = ov[lane + 64];
+  const float rg = 1.0f / sqrtf(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
+  if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(from_fx(zr));
+  // Off the path to the out_proj multiply-adds: the writer's new state S'' (column j) and conv
+  // state [c] <- [s1, s2, x], stored while the multiply-adds run.
+  if (writer) {
+    const float dlk = dl * rk;
+    float* Sw = b.S_w + (size_t)h * kDk * kDv;
+    const uint32_t off = (uint32_t)(ig * kGdnR * kDv + j);
 #pragma unroll
-    for (int r = 0; r < kGdnR; ++r) st_agent(Sw + (off + (uint32_t)(r * kDv)), g.s[r]);
+    for (int r = 0; r < kGdnR; ++r) st_agent(Sw + (off + (uint32_t)(r * kDv)), decay * g.s[r] + kr[r] * dlk);
     if (tid < nch) {
       float* cw = b.cst_w + (size_t)c * 3;
       st_agent(&cw[0], g.cs[1]);
@@ -532,20 +540,6 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
       st_agent(&cw[2], x);
     }
   }
-  part1[tid] = o;
-  __syncthreads();
-  // o_j = (rq qscale) * sum over row groups of part1[g][j]; gated RMSNorm over the dv outputs of
-  // h, whose sum of squares every wave forms itself (no further barrier)
-  const float fq = rq * a.qscale;
-  auto ocol = [&](int jj) {
-    float s = 0.f;
-#pragma unroll
-    for (int gg = 0; gg < kGdnG; ++gg) s += part1[gg * kDv + jj];
-    return s * fq;
-  };
-  const float oa = ocol(lane), ob = ocol(lane + 64);
-  const float rg = 1.0f / sqrtf(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
-  if (tid < it.klen) xs[tid] = (g.nw * (ocol(it.k0 % kDv + tid) * rg)) * silu_f(from_fx(zr));
 }
 
 Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
