@@ -216,12 +216,13 @@ int setup_persistent(q35_model* m) {
   uint32_t* bar = nullptr;
   float *att_ml = nullptr, *att_o = nullptr, *arg_v = nullptr;
   int32_t* arg_i = nullptr;
-  fx_t* gate_acc = nullptr;
+  fx_t *gate_acc = nullptr, *h_sp = nullptr;
   const size_t gate_n = (size_t)2 * nh * kStepBaStride;
   int rc;
   if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
       (rc = dev_alloc_t(m, "step_barrier", kStepBarBytes / 4, &bar)) ||
       (rc = dev_alloc_t(m, "step_gate_acc", gate_n, &gate_acc)) ||
+      (rc = dev_alloc_t(m, "step_h", (size_t)2 * d.hidden, &h_sp)) ||
       (rc = dev_alloc_t(m, "attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
       (rc = dev_alloc_t(m, "attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
       (rc = dev_alloc_t(m, "argmax_partial_v", (size_t)grid, &arg_v)) ||
@@ -241,7 +242,11 @@ int setup_persistent(q35_model* m) {
   step_plan(d, grid, a.mv);
   a.emb_q = m->embed.q; a.emb_s = m->embed.s; a.final_norm = m->final_norm;
   a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-  a.h = m->h; a.acc_proj = m->acc_proj; a.acc_ba = gate_acc; a.acc_gu = m->acc_gu;
+  // The residual stream gets a buffer of its own with every 128-byte line on a 256-byte slot:
+  // each out / down / o stage adds 256 blocks' partials into it, and 16 consecutive lines took
+  // those atomics about 1.8x as long as lines spread this way.  Each token's first stage
+  // rewrites it from the embedding, so nothing is carried over between tokens.
+  a.h = h_sp; a.acc_proj = m->acc_proj; a.acc_ba = gate_acc; a.acc_gu = m->acc_gu;
   a.acc_zero_n = m->acc_proj_n;
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
@@ -466,7 +471,7 @@ int q35_model_reset(q35_model* m, void* stream) {
     const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
                        n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
                        n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt" ||
-                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc";
+                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc" || n == "step_h";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
   m->host_pos = 0;

@@ -407,7 +407,8 @@ struct StepArgs {
   StepMv mv[SMV_COUNT];
   const int8_t* emb_q; const float* emb_s; const float* final_norm;
   const float *rope_cos, *rope_sin;
-  fx_t *h, *acc_proj, *acc_gu;
+  fx_t* h;  // residual stream: value k at k + (k & ~15), i.e. one 128-byte line of 16 per 256 bytes
+  fx_t *acc_proj, *acc_gu;
   fx_t* acc_ba;        // in_proj_b | in_proj_a sums, one per kStepBaStride entries (own cache line)
   int64_t acc_zero_n;  // acc_proj entries cleared by the gate|up stage
   float *att_ml, *att_o;

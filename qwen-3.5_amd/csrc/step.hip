@@ -195,6 +195,7 @@ struct Mv {
   int n0, n1, n2;
   int t1, t2, t3;  // first tile of segments 1 and 2, total tiles
   int K, kch, nchunk;
+  int spm;  // ~15 when the accumulator is the residual stream (index k at k + (k & ~15)), else 0
 };
 
 Q35_DEV int tiles_of(int n) { return (n + kTile - 1) / kTile; }
@@ -213,7 +214,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, int kind) {
       break;
     case SMV_OUT:
       d.K = a.vdim;
-      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = a.h; d.n0 = a.H;
+      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_QKV: {
@@ -226,7 +227,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, int kind) {
     } break;
     case SMV_O:
       d.K = a.ah * a.hd;
-      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = a.h; d.n0 = a.H;
+      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_GU:
@@ -237,7 +238,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, int kind) {
       break;
     default:  // SMV_DOWN
       d.K = a.F;
-      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = a.h; d.n0 = a.H;
+      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
   }
@@ -248,7 +249,7 @@ struct MvItem {
   const int8_t* w;
   const float* s;
   fx_t* acc;
-  int N, tile, tl, k0, klen;
+  int N, tile, tl, k0, klen, spm;
 };
 
 Q35_DEV MvItem mv_item(const Mv& d, int item) {
@@ -260,6 +261,7 @@ Q35_DEV MvItem mv_item(const Mv& d, int item) {
   else { it.w = d.w2; it.s = d.s2; it.acc = d.a2; it.N = d.n2; it.tl = tile - d.t2; }
   it.k0 = ch * d.kch;
   it.klen = min(d.kch, d.K - it.k0);
+  it.spm = d.spm;
   return it;
 }
 
@@ -320,7 +322,7 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
 #pragma unroll
     for (int i = 0; i < kRG; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
-    if (n < it.N) fx_add(&it.acc[n], v);
+    if (n < it.N) fx_add(&it.acc[n + (n & it.spm)], v);
   }
   __syncthreads();
 }
@@ -368,7 +370,7 @@ Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int
 // the residual stream h (fixed point) as pro_rms input
 struct HLoad {
   const fx_t* h;
-  Q35_DEV fx_t operator()(int k) const { return ld_agent(h + k); }
+  Q35_DEV fx_t operator()(int k) const { return ld_agent(h + (k + (k & ~15))); }
 };
 struct HConv {
   Q35_DEV float operator()(fx_t x) const { return from_fx(x); }
@@ -673,7 +675,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
         const EmbLoad src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
         pro_rms<KR, EmbRaw>(src, EmbConv{}, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs, none);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row
-          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k], to_fx(EmbConv{}(src(k))));
+          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k + (k & ~15)], to_fx(EmbConv{}(src(k))));
       } break;
       case PRO_RMS:
         pro_rms<KR, fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen,
