@@ -67,7 +67,7 @@ constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
 
 // LDS carve-up (float offsets)
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
-constexpr int kRed = kXs + kKch;        // matvec row-group partials [kRG][kTile]
+constexpr int kRed = kXs + kKch;        // matvec wave partials [kNW][kTile]; prologue scratch [kRG][kTile]
 static_assert(kRed + kRG * kTile <= kSmem, "LDS");
 static_assert(512 + 2 * kT + kDv <= kRG * kTile, "DeltaNet scratch fits in kRed");
 static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
@@ -308,19 +308,32 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] += f[j] * c;
   }
-  float4* dst = reinterpret_cast<float4*>(&red[rr * kTile + cg * 16]);
+  // The wave's 4 row groups (its 16-lane rows) are summed in registers with the gfx950 lane
+  // swaps: first between the 32-lane halves (acc[j] with acc[j + 8]), then between neighbouring
+  // rows; afterwards lane (row q, cg) holds columns cg*16 + 4q .. +3 of the wave's partial.
+  float s8[8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) dst[q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+  for (int j = 0; j < 8; ++j) {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j]), __float_as_uint(acc[j + 8]), false, false);
+    s8[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  float t4[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(s8[j]), __float_as_uint(s8[j + 4]), false, false);
+    t4[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  *reinterpret_cast<float4*>(&red[(rr >> 2) * kTile + cg * 16 + 4 * (rr & 3)]) = make_float4(t4[0], t4[1], t4[2], t4[3]);
   __syncthreads();
   if (tid < kTile) {
-    // all 32 partials read before any is summed: one LDS round trip instead of one per batch
-    float pr[kRG];
+    // all kNW wave partials read before any is summed: one LDS round trip
+    float pr[kNW];
 #pragma unroll
-    for (int i = 0; i < kRG; ++i) pr[i] = red[i * kTile + tid];
+    for (int i = 0; i < kNW; ++i) pr[i] = red[i * kTile + tid];
     __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the sums (not interleaved)
     float v = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRG; ++i) v += pr[i];
+    for (int i = 0; i < kNW; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
     if (n < it.N) fx_add(&it.acc[n + (n & it.spm)], v);
   }
