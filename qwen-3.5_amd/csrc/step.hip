@@ -298,11 +298,18 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
   float acc[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  // every row's x is read (clamped index) before the first is used: one LDS round trip, not one
+  // per row behind a branch
+  float xr[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (kRG * u >= it.klen) break;
-    const int r = rr + kRG * u;
-    const float c = (r < it.klen) ? xs[r] * pf.s[u] : 0.f;
+    xr[u] = xs[min(rr + kRG * u, it.klen - 1)];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (kRG * u >= it.klen) break;
+    const float c = (rr + kRG * u < it.klen) ? xr[u] * pf.s[u] : 0.f;
     float f[16];
     unpack16(pf.w[u], f);
 #pragma unroll
@@ -663,10 +670,6 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
   if (item < nitems) {
     it = mv_item(d, item);
     mv_load(it, d.K, pf);
-    if (kind == SMV_QKVZ && it.tile < naux) {  // row clamped; masked where it is used
-      const float* W = it.tile < a.nh ? L.w_b : L.w_a;
-      auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
-    }
     if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
   }
   if (!bar_wait(bar, sh.ok)) return false;
@@ -681,18 +684,25 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
       mv_load(it, d.K, pf);
       if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
     }
-    auto none = []() {};
+    // the qkvz item's gate column (a 64-byte-strided gather) is issued behind the norm's inputs,
+    // not ahead of the barrier poll
+    auto aux_load = [&]() {
+      if (kind == SMV_QKVZ && it.tile < naux && first) {  // row clamped; masked where it is used
+        const float* W = it.tile < a.nh ? L.w_b : L.w_a;
+        auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
+      }
+    };
     switch (pro) {
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
         const EmbLoad src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
-        pro_rms<KR, EmbRaw>(src, EmbConv{}, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs, none);
+        pro_rms<KR, EmbRaw>(src, EmbConv{}, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs, aux_load);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row
           for (int k = tix(); k < K; k += kT) st_agent(&a.h[k + (k & ~15)], to_fx(EmbConv{}(src(k))));
       } break;
       case PRO_RMS:
         pro_rms<KR, fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen,
-                          xs, sh.shs, none);
+                          xs, sh.shs, aux_load);
         break;
       case PRO_GDN:
         pro_gdn(a, L, it, i, gp, xs, red);
