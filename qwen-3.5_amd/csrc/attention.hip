@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
       const int hq = g * rep + w;
       const float4 v = ld4(a.qg, a.qg_f, (size_t)b * a.ld_qg + (size_t)hq * 2 * kHd + 4 * lane);
       const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-      const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+      const float r = rsqrt_f(ss / (float)kHd + a.eps);
       const int d = 4 * lane;
       qn[w][d + 0] = (v.x * r) * (1.0f + a.qnw[d + 0]);
       qn[w][d + 1] = (v.y * r) * (1.0f + a.qnw[d + 1]);
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
     } else if (w == rep) {
       const float4 v = ld4(a.k, a.k_f, (size_t)b * a.ld_kv + (size_t)g * kHd + 4 * lane);
       const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-      const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+      const float r = rsqrt_f(ss / (float)kHd + a.eps);
       const int d = 4 * lane;
       kn[d + 0] = (v.x * r) * (1.0f + a.knw[d + 0]);
       kn[d + 1] = (v.y * r) * (1.0f + a.knw[d + 1]);

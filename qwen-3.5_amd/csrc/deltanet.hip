@@ -77,8 +77,8 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
     if (lane == 0) wsum[wid] = ss;
   }
   __syncthreads();
-  const float rq = 1.0f / sqrtf((wsum[0] + wsum[1]) + 1e-6f);
-  const float rk = 1.0f / sqrtf((wsum[2] + wsum[3]) + 1e-6f);
+  const float rq = rsqrt_f((wsum[0] + wsum[1]) + 1e-6f);
+  const float rk = rsqrt_f((wsum[2] + wsum[3]) + 1e-6f);
   if (tid < kDk) qh[tid] = (qk[tid] * rq) * A.qscale;
   else kh[tid - kDk] = qk[tid] * rk;
 
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   if (a.ba_f) {  // raw projections: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias)
     const float bs = from_fx(a.ba_f[(size_t)b * a.ld_bg + h]);
     const float as = from_fx(a.ba_f[(size_t)b * a.ld_bg + a.nh + h]);
-    beta = 1.0f / (1.0f + expf(-bs));
+    beta = sigmoid_f(bs);
     const float xg = as + a.dt_bias[h];
     const float pre = logf(expf(xg) + 1.0f);
     g = -expf(a.a_log[h]) * (pre > 20.0f ? xg : pre);
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void gate_proj_kernel(const float* x, int
     for (int j = 0; j < subs; ++j) s += red[j * nout + tid];
     float r;
     if (tid < nh) {
-      r = 1.0f / (1.0f + expf(-s));
+      r = sigmoid_f(s);
     } else {
       const float xg = s + dtb[h];
       const float pre = logf(expf(xg) + 1.0f);

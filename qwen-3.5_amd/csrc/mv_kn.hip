@@ -119,7 +119,7 @@ __device__ void mv_prologue(const MvArgs& a, int k0, int klen, float* xs, float*
 #pragma unroll
       for (int j = 0; j < kRmsPerThread; ++j) ss += v[j] * v[j];
       ss = block_sum256(ss, sh);
-      const float r = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      const float r = rsqrt_f(ss / (float)a.K + a.eps);
 #pragma unroll
       for (int j = 0; j < kRmsPerThread; ++j) {
         const int k = tid + kThreads * j;
@@ -141,7 +141,7 @@ __device__ void mv_prologue(const MvArgs& a, int k0, int klen, float* xs, float*
           ss += v * v;
         }
         ss = wave_sum(ss);
-        if (lane == 0) grp[m * kMaxGroups + (gi - g0)] = 1.0f / sqrtf(ss / (float)G + a.eps);
+        if (lane == 0) grp[m * kMaxGroups + (gi - g0)] = rsqrt_f(ss / (float)G + a.eps);
       }
     }
     __syncthreads();

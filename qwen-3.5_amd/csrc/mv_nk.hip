@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
 #pragma unroll
       for (int j = 0; j < CPW * 4; ++j) ss += v[j] * v[j];
       ss = block_sum256(ss, sh);
-      r = 1.0f / sqrtf(ss / (float)K + a.eps);
+      r = rsqrt_f(ss / (float)K + a.eps);
     }
 #pragma unroll
     for (int j = 0; j < CPW * 4; ++j) {

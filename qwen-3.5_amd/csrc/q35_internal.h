@@ -22,8 +22,13 @@ int fail(int code, const std::string& msg);
 // ------------------------------------------------------------------ device helpers
 #define Q35_DEV __device__ __forceinline__
 
-Q35_DEV float silu_f(float v) { return v * (1.0f / (1.0f + expf(-v))); }
-Q35_DEV float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+// 1/x and 1/sqrt(x) as the single hardware instructions (v_rcp_f32, v_rsq_f32; about 1 ulp):
+// the IEEE-rounded divide and square root are ~10-instruction dependent sequences each, and these
+// sit on the latency chain of every norm and gate.  Arguments here are positive and normal.
+Q35_DEV float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
+Q35_DEV float rsqrt_f(float x) { return __builtin_amdgcn_rsqf(x); }
+Q35_DEV float silu_f(float v) { return v * rcp_f(1.0f + expf(-v)); }
+Q35_DEV float sigmoid_f(float v) { return rcp_f(1.0f + expf(-v)); }
 
 // x from lane (l + N) mod 16 of the same 16-lane row (DPP row_ror: a VALU operand modifier, no
 // trip through the LDS crossbar as a lane shuffle takes)

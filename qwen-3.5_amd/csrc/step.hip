@@ -379,7 +379,7 @@ Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int
   // every caller reaches here right after a workgroup barrier (the stage's grid-barrier wait, or
   // the previous item's reduction), so the block sum needs no leading one
   ss = block_sum(ss, shs, false);
-  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
     const int k = tid + kT * j;
@@ -507,15 +507,15 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   const bool writer = it.tl == 0 && (it.k0 % kDv) == 0;  // uniform
   const GdnBuf b = gdn_buf(L, i);
   // gates: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias) (kernels.rs:228-244)
-  const float beta = 1.0f / (1.0f + expf(-bs));
+  const float beta = sigmoid_f(bs);
   const float xg = as + g.dtb;
   const float pre = logf(expf(xg) + 1.0f);
   const float decay = expf(-expf(g.alog) * (pre > 20.0f ? xg : pre));
   __syncthreads();
   // l2 norms of q and k (dk = 128): every wave sums all the squares itself, so no second barrier
   const float q0 = qkv[lane], q1 = qkv[lane + 64], k0 = qkv[kDk + lane], k1 = qkv[kDk + lane + 64];
-  const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
-  const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
+  const float rq = rsqrt_f(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+  const float rk = rsqrt_f(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
   const float kq = wave_sum(q0 * k0 + q1 * k1);  // k_raw . q_raw
   // With k = rk k_raw, q = rq qscale q_raw and S the old state:
   //   S' = decay S,  m = S'^T k = decay rk u,  delta = beta (v - m),  S'' = S' + k delta^T,
@@ -545,7 +545,7 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   __syncthreads();
   // gated RMSNorm over the dv outputs of h, whose sum of squares every wave forms itself
   const float oa = ov[lane], ob = ov[lane + 64];
-  const float rg = 1.0f / sqrtf(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
+  const float rg = rsqrt_f(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
   if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(from_fx(zr));
   // Off the path to the out_proj multiply-adds: the writer's new state S'' (column j) and conv
   // state [c] <- [s1, s2, x], stored while the multiply-adds run.
@@ -636,7 +636,7 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
     float s = 0.f;
     for (int q = 0; q < parts; ++q) s += pbuf[q * span + tid];
     const int hh = (k0 + tid) / kHd;
-    xs[tid] = (s / wl[hh - h0]) * sigmoid_f(from_fx(graw));
+    xs[tid] = (s * rcp_f(wl[hh - h0])) * sigmoid_f(from_fx(graw));
   }
 }
 
@@ -788,7 +788,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
       if (w < rep) {
         const float4 v = ld4_fx(&a.acc_proj[(size_t)(g * rep + w) * 2 * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-        const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+        const float r = rsqrt_f(ss / (float)kHd + a.eps);
         qn[w * kHd + d + 0] = (v.x * r) * (1.0f + qw.x);
         qn[w * kHd + d + 1] = (v.y * r) * (1.0f + qw.y);
         qn[w * kHd + d + 2] = (v.z * r) * (1.0f + qw.z);
@@ -796,7 +796,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
       } else if (w == rep) {
         const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)g * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-        const float r = 1.0f / sqrtf(ss / (float)kHd + a.eps);
+        const float r = rsqrt_f(ss / (float)kHd + a.eps);
         kn[d + 0] = (v.x * r) * (1.0f + kw.x);
         kn[d + 1] = (v.y * r) * (1.0f + kw.y);
         kn[d + 2] = (v.z * r) * (1.0f + kw.z);
