@@ -640,15 +640,22 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   }
 }
 
-// Side tasks that run right after a stage's barrier (their inputs are final, their outputs are
-// not read before the next barrier), spread over every thread of the grid.
+// Block bix()'s contiguous share of p[0, n) set to zero, one element per thread.
+Q35_DEV void zero_share(fx_t* p, int n) {
+  const int nb = (int)gridDim.x, per = (n + nb - 1) / nb, lo = bix() * per, hi = min(n, lo + per);
+  for (int i = lo + tix(); i < hi; i += kT) st_agent(&p[i], (fx_t)0);
+}
+
+// Side tasks of a stage (their inputs are final after its barrier, their outputs are not read
+// before the next one), spread evenly over the grid and issued behind the prologue's loads: a
+// block's loads would otherwise wait for its stores' acknowledgements (vmcnt counts both, in
+// order), and the few blocks holding all the stores arrived last.
 Q35_DEV void side_tasks(const StepArgs& a, int kind) {
-  const int64_t gt = (int64_t)bix() * kT + tix(), gs = (int64_t)gridDim.x * kT;
   if (kind == SMV_QKVZ || kind == SMV_QKV) {  // gate|up accumulator: last read by the previous down stage
-    for (int64_t i = gt; i < 2 * (int64_t)a.F; i += gs) st_agent(&a.acc_gu[i], (fx_t)0);
+    zero_share(a.acc_gu, 2 * a.F);
   } else if (kind == SMV_GU) {  // projection + gate accumulators: last read by the out / o stage
-    for (int64_t i = gt; i < a.acc_zero_n; i += gs) st_agent(&a.acc_proj[i], (fx_t)0);
-    if (gt < 2 * a.nh) st_agent(&a.acc_ba[gt * kStepBaStride], (fx_t)0);
+    zero_share(a.acc_proj, (int)a.acc_zero_n);
+    if (bix() == gridDim.x - 1 && tix() < 2 * a.nh) st_agent(&a.acc_ba[tix() * kStepBaStride], (fx_t)0);
   }
 }
 
@@ -673,7 +680,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
     if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
   }
   if (!bar_wait(bar, sh.ok)) return false;
-  side_tasks(a, kind);
+  if (item >= nitems) side_tasks(a, kind);  // blocks with an item run them in the prologue
   int tok = 0;
   if (pro == PRO_EMBED_RMS && item < nitems) tok = select_token(a, i, p, sh);
   float* xs = sh.smem + kXs;
@@ -691,6 +698,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
         const float* W = it.tile < a.nh ? L.w_b : L.w_a;
         auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
       }
+      if (first) side_tasks(a, kind);
     };
     switch (pro) {
       case PRO_EMBED_RMS: {
