@@ -580,6 +580,16 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   float* pbuf = scratch + kMaxTouch * kMaxNmax; // [kT] per-part sums
   float* wl = pbuf + kT;                        // [kMaxTouch] L
   const int h0 = k0 / kHd, h1 = (k0 + klen - 1) / kHd;
+  // Thread (part, i): output element k0 + i, chunks part, part + parts, ...  The partial outputs
+  // do not depend on the statistics, so the first batch is issued with them: one round trip.
+  const int parts = klen <= 64 ? 8 : (klen <= 128 ? 4 : (klen <= 256 ? 2 : 1));
+  const int span = kT / parts;
+  const int i = tid % span, part = tid / span;
+  const int kk = k0 + min(i, klen - 1), hk = kk / kHd;  // clamped; masked below
+  const float* og = a.att_o + ((size_t)(hk / rep) * a.att_nmax * kMaxRep + hk % rep) * kHd + kk % kHd;  // + c*kMaxRep*kHd
+  float v0[kMergeB];
+#pragma unroll
+  for (int j = 0; j < kMergeB; ++j) v0[j] = ld_agent(&og[(size_t)min(part + j * parts, nact - 1) * kMaxRep * kHd]);
   // the thread's output gate (klen <= 512 = threads), loaded with the chunk statistics
   const int kg = k0 + min(tid, klen - 1);
   const fx_t graw = ld_agent(&a.acc_proj[(size_t)(kg / kHd) * 2 * kHd + kHd + kg % kHd]);
@@ -611,15 +621,15 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
     if (lane == 0) wl[hh - h0] = Ls;
   }
   __syncthreads();
-  const int parts = klen <= 64 ? 8 : (klen <= 128 ? 4 : (klen <= 256 ? 2 : 1));
-  const int span = kT / parts;
-  const int i = tid % span, part = tid / span;
   float o = 0.f;
   if (i < klen) {
-    const int k = k0 + i, hh = k / kHd, d = k % kHd, g = hh / rep, hr = hh % rep;
-    const float* og = a.att_o + ((size_t)g * a.att_nmax * kMaxRep + hr) * kHd + d;  // + c*kMaxRep*kHd
-    const float* w = wts + (hh - h0) * kMaxNmax;
-    for (int c0 = part; c0 < nact; c0 += kMergeB * parts) {
+    const float* w = wts + (hk - h0) * kMaxNmax;
+#pragma unroll
+    for (int j = 0; j < kMergeB; ++j) {
+      const int c = part + j * parts;
+      if (c < nact) o += v0[j] * w[c];
+    }
+    for (int c0 = part + kMergeB * parts; c0 < nact; c0 += kMergeB * parts) {
       float v[kMergeB];  // all of a batch in flight at once (clamped; masked below)
 #pragma unroll
       for (int j = 0; j < kMergeB; ++j) v[j] = ld_agent(&og[(size_t)min(c0 + j * parts, nact - 1) * kMaxRep * kHd]);
