@@ -679,6 +679,16 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
   const Mv d = make_mv(a, L, kind);
   const int nitems = d.t3 * d.nchunk;
   int item = bix();
+  if (kind == SMV_GU) {
+    // The out stage's state writers (out items with tile 0 and k0 % dv == 0, i.e. blocks b < nh cph
+    // with b % cph == 0) arrive last and so issue this stage's weights last: a permutation of
+    // [0, grid) gives them the last slots, which are idle when the stage has fewer items than blocks.
+    const int cph = kDv / a.mv[SMV_OUT].kch, nw = a.nh, g = (int)gridDim.x, b = bix();
+    if (nw * cph <= g) {
+      const bool w = b < nw * cph && b % cph == 0;
+      item = w ? g - nw + b / cph : b - min((b + cph - 1) / cph, nw);
+    }
+  }
   MvPf<U> pf;
   MvItem it{};
   GdnPf gp;
