@@ -27,8 +27,13 @@ int fail(int code, const std::string& msg);
 // sit on the latency chain of every norm and gate.  Arguments here are positive and normal.
 Q35_DEV float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
 Q35_DEV float rsqrt_f(float x) { return __builtin_amdgcn_rsqf(x); }
-Q35_DEV float silu_f(float v) { return v * rcp_f(1.0f + expf(-v)); }
-Q35_DEV float sigmoid_f(float v) { return rcp_f(1.0f + expf(-v)); }
+// e^-v for the logistic function as 2^(-v log2 e) with the hardware exp2 (v_exp_f32): rounding the
+// product gives a relative error of about |v| 2^-24, which a logistic gate does not compound
+// (the DeltaNet decay, applied step after step, keeps the library expf).  Large |v| saturate
+// correctly: 1 + inf -> rcp 0, 1 + 0 -> 1.
+Q35_DEV float exp_neg_hw(float v) { return __builtin_amdgcn_exp2f(-v * 1.44269504088896341f); }
+Q35_DEV float silu_f(float v) { return v * rcp_f(1.0f + exp_neg_hw(v)); }
+Q35_DEV float sigmoid_f(float v) { return rcp_f(1.0f + exp_neg_hw(v)); }
 
 // x from lane (l + N) mod 16 of the same 16-lane row (DPP row_ror: a VALU operand modifier, no
 // trip through the LDS crossbar as a lane shuffle takes)
