@@ -291,9 +291,11 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
   }
 }
 
-// y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.
+// y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.  aux_dst
+// (optional): one more sum, of which each wave holds its part in aux, reduced with the columns.
 template <int U>
-Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, float* red) {
+Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, float* red, float aux = 0.f,
+                        fx_t* aux_dst = nullptr) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
@@ -331,7 +333,14 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
     t4[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
   }
   *reinterpret_cast<float4*>(&red[(rr >> 2) * kTile + cg * 16 + 4 * (rr & 3)]) = make_float4(t4[0], t4[1], t4[2], t4[3]);
+  if (aux_dst && (tid & 63) == 0) red[kNW * kTile + (tid >> 6)] = aux;
   __syncthreads();
+  if (aux_dst && tid == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) s += red[kNW * kTile + w];
+    fx_add(aux_dst, s);
+  }
   if (tid < kTile) {
     // all kNW wave partials read before any is summed: one LDS round trip
     float pr[kNW];
@@ -745,6 +754,10 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
         break;
     }
     __syncthreads();
+    // in_proj_b | in_proj_a column it.tile: each wave's part of the dot product goes into the
+    // matvec reduction (further columns, when there are more than tiles, reduce on their own)
+    float auxp = 0.f;
+    fx_t* auxd = nullptr;
     if (kind == SMV_QKVZ) {
       for (int o = it.tile; o < naux; o += d.t3) {
         float w = auxw;
@@ -753,11 +766,16 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
           w = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (o % a.nh)));
         }
         const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
-        const float s = block_sum(v, sh.shs);
-        if (tix() == 0) fx_add(&a.acc_ba[(size_t)o * kStepBaStride], s);
+        if (o == it.tile) {
+          auxp = wave_sum(v);
+          auxd = &a.acc_ba[(size_t)o * kStepBaStride];
+        } else {
+          const float s = block_sum(v, sh.shs);
+          if (tix() == 0) fx_add(&a.acc_ba[(size_t)o * kStepBaStride], s);
+        }
       }
     }
-    mv_compute(it, pf, xs, red);
+    mv_compute(it, pf, xs, red, auxp, auxd);
   }
   bar_arrive(bar);
   return true;
