@@ -633,20 +633,22 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   float o = 0.f;
   if (i < klen) {
     const float* w = wts + (hk - h0) * kMaxNmax;
+    // every chunk weight is read (clamped) before the first is used: the reads inside the mask's
+    // branches were waited for one by one
+    float wc[kMergeB];
 #pragma unroll
-    for (int j = 0; j < kMergeB; ++j) {
-      const int c = part + j * parts;
-      if (c < nact) o += v0[j] * w[c];
-    }
+    for (int j = 0; j < kMergeB; ++j) wc[j] = w[min(part + j * parts, nact - 1)];
+#pragma unroll
+    for (int j = 0; j < kMergeB; ++j) o += (part + j * parts < nact) ? v0[j] * wc[j] : 0.f;
     for (int c0 = part + kMergeB * parts; c0 < nact; c0 += kMergeB * parts) {
       float v[kMergeB];  // all of a batch in flight at once (clamped; masked below)
 #pragma unroll
       for (int j = 0; j < kMergeB; ++j) v[j] = ld_agent(&og[(size_t)min(c0 + j * parts, nact - 1) * kMaxRep * kHd]);
+      float wv[kMergeB];
 #pragma unroll
-      for (int j = 0; j < kMergeB; ++j) {
-        const int c = c0 + j * parts;
-        if (c < nact) o += v[j] * w[c];
-      }
+      for (int j = 0; j < kMergeB; ++j) wv[j] = w[min(c0 + j * parts, nact - 1)];
+#pragma unroll
+      for (int j = 0; j < kMergeB; ++j) o += (c0 + j * parts < nact) ? v[j] * wv[j] : 0.f;
     }
   }
   pbuf[part * span + i] = o;
