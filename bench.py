@@ -136,7 +136,7 @@ def copy_calibration():
 # counters' reading for a 1 GiB copy (`bench.py --copy-calibration`): x2.0 and x1.0.  Measured for
 # the kernel at the commit that recorded it; profiles/step_kernel_decode_2b_traffic.md has the
 # commands and the per-dispatch values.
-STEP_TRAFFIC_PER_LAUNCH = 139.68e9
+STEP_TRAFFIC_PER_LAUNCH = 139.72e9
 
 
 def cpu_baseline(q35, d, prompt, budget_s=20.0):
