@@ -100,8 +100,11 @@ int q35_q8_embedding_lookup(q35_q8f table, const int32_t* ids, int32_t n, float*
 int q35_gate_proj(const float* x, int32_t B, int32_t in_dim, const float* w_b, const float* w_a,
                   const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream);
 
-/* out[0] = index of the largest logit (ties: lowest index).  Replaces argmax
- * (src/kernels.rs:733-739, kernels :298-371). */
+/* out[0] = index of the largest logit.  Exact ties resolve as the reference's two-stage argmax
+ * does: with c = n/8 and i = k*c + p, the winner minimises (p mod 256, p div 256, k) — the
+ * first strict maximum of its scans.  The last n mod 8 values, which the reference never reads,
+ * are read here and rank after all others on ties; NaN is never returned (all NaN -> 0).
+ * Replaces argmax (src/kernels.rs:733-739, kernels :298-371). */
 int q35_argmax(const float* logits, int64_t n, int32_t* out, void* ws, size_t ws_bytes, void* stream);
 size_t q35_argmax_ws_bytes(int64_t n);
 
@@ -143,7 +146,9 @@ int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const
 
 /* One decode token through gated GQA attention for B rows.  k_cache/v_cache:
  * [B][kv_heads][tmax][head_dim]; d_pos[b] = tokens already cached for row b (the new K/V are
- * written at that index, then attention runs over d_pos[b]+1 tokens); rope_cos/rope_sin:
+ * written at that index, then attention runs over d_pos[b]+1 tokens); d_pos[b] must lie in
+ * [0, tmax): a row whose position does not is skipped and reported by q35_workspace_status;
+ * rope_cos/rope_sin:
  * [tmax][rot_dim] from q35_rope_tables.  Replaces Attention::forward's seq_len==1 branch
  * (src/text_modules.rs:842-944). */
 int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const float* x, int32_t B,
@@ -179,6 +184,13 @@ int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const floa
 /* Workspace large enough for any of the layer calls above with these B / tmax. */
 size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax);
 
+/* Device-side argument errors recorded in a layer workspace by earlier calls on `stream`
+ * (synchronises it), then cleared.  Q35_E_SHAPE: an attention call met a position d_pos[b]
+ * outside [0, tmax); that row's cache and output were left untouched.  No reference counterpart
+ * (the reference panics on the host, text_modules.rs); it exists because the positions live in
+ * device memory, where the host cannot check them without a synchronisation. */
+int q35_workspace_status(void* ws, void* stream);
+
 /* Host: cos/sin tables [tmax][rot_dim] of TextRotaryEmbedding::forward for positions 0..tmax-1
  * (src/text_modules.rs:30-43,73-81; the mRoPE recomposition :45-58 is the identity for text). */
 int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin_host);
@@ -195,7 +207,8 @@ typedef struct q35_model q35_model;
 int q35_model_create_synthetic(const q35_dims* d, uint64_t seed, int32_t tmax, q35_model** out);
 int q35_model_destroy(q35_model* m);
 
-/* Zero every cache and set the position to 0 (the chat loop's /reset, main.rs:65-71). */
+/* Zero every cache and set the position to 0 (the chat loop's /reset, main.rs:65-71).  Also
+ * clears a persistent-kernel failure recorded by q35_model_check. */
 int q35_model_reset(q35_model* m, void* stream);
 
 /* Write the next input token (host value) into the model's device token slot. */
@@ -223,7 +236,10 @@ int q35_model_step(q35_model* m, int32_t use_graph, void* stream);
 int q35_model_decode(q35_model* m, int32_t n_steps, int32_t mode, void* stream);
 
 /* Synchronises the stream and reports a persistent-kernel failure (a grid barrier that timed
- * out; the kernel then exits early and its results are invalid).  Q35_OK otherwise. */
+ * out; the kernel then exits early and its results are invalid).  Q35_OK otherwise.  The failure
+ * is sticky: it is kept in device memory that no launch clears, every later persistent launch
+ * returns at entry without touching the model state, and q35_model_step / _decode / _generate
+ * refuse persistent mode once a check has seen it, until q35_model_reset. */
 int q35_model_check(q35_model* m, void* stream);
 
 /* Grid of the persistent step kernel (blocks, one per CU); returns an error code and message

@@ -142,12 +142,27 @@ void orc_gate_proj(const float* x, int in_dim, const float* w_b, const float* w_
   }
 }
 
-/* Greedy token: largest value, ties to the lowest index (numpy argmax semantics for
- * finite inputs).  The reference's own tie order is orc_argmax_reference_order. */
+/* Tie key of index i under the reference's argmax (kernels.rs:298-371): with c = n/8 and
+ * i = k*c + p, the reference's scans keep the first strict maximum in the order
+ * (p mod 256, p div 256, k).  Indices >= 8c (never read by the reference) come after all of
+ * them, in index order. */
+static uint64_t argmax_key(int64_t i, int64_t n) {
+  const int64_t c = n / 8, s = (c + 255) / 256;
+  if (i >= 8 * c) return (uint64_t)(s * 2048 + (i - 8 * c));
+  const int64_t k = i / c, p = i - k * c;
+  return (uint64_t)((((p % 256) * s) + p / 256) * 8 + k);
+}
+
+/* Greedy token: the largest value; among exactly equal maxima the one the reference's two-stage
+ * argmax returns (argmax_key), which for n a multiple of 8 with n/8 >= 256 is
+ * orc_argmax_reference_order's result.  NaN values are never picked. */
 int32_t orc_argmax(const float* v, int64_t n) {
-  int64_t best = 0;
-  for (int64_t i = 1; i < n; ++i) if (v[i] > v[best]) best = i;
-  return (int32_t)best;
+  int64_t best = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    if (v[i] != v[i]) continue;
+    if (best < 0 || v[i] > v[best] || (v[i] == v[best] && argmax_key(i, n) < argmax_key(best, n))) best = i;
+  }
+  return (int32_t)(best < 0 ? 0 : best);
 }
 
 /* Exact two-stage order of kernels.rs:298-371: unit p scans p + k*(n/8), k<8, strict '>';

@@ -26,7 +26,7 @@ struct AttnArgs {
   AttnCall c;
   float scale;
   int32_t chunk, nchunk;
-  uint32_t* counters;  // [B*nkv]
+  uint32_t* counters;  // [B*nkv] completion counters; counters[kWsErrWord] the sticky error word
   float* part_ml;      // [B*nkv][nchunk][2][kMaxRep]
   float* part_o;       // [B*nkv][nchunk][kMaxRep][hd]
 };
@@ -54,6 +54,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs A)
   const int b = blockIdx.x / (A.nchunk * a.nkv);
   const int rep = a.nh / a.nkv;
   const int pos = a.pos[b];
+  if (pos < 0 || pos >= a.tmax) {  // no cache row or rotary row exists for it: report, touch nothing
+    if (tid == 0 && c == 0 && g == 0) ws_raise(A.counters, kWsErrPos);
+    return;
+  }
   const int T = pos + 1;
   const int nact = (T + A.chunk - 1) / A.chunk;
   if (c >= nact) return;
@@ -281,6 +285,7 @@ int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size
   if (c.rot <= 0 || c.rot > c.hd || (c.rot % 2) != 0) return fail(Q35_E_SHAPE, "attention: bad rotary dim");
   if (c.B < 1 || c.tmax < 1) return fail(Q35_E_SHAPE, "attention: B and tmax must be >= 1");
   if (c.B * c.nkv > kMaxCounters) return fail(Q35_E_SHAPE, "attention: B*kv_heads too large");
+  if ((size_t)c.B * c.nkv * c.tmax * c.hd > (size_t)1 << 40) return fail(Q35_E_SHAPE, "attention: cache too large");
   AttnLayout L = attn_layout(c.B, c.nkv, c.hd, c.tmax);
   if (!counters || !scratch || scratch_bytes < L.ml_bytes + L.o_bytes) return fail(Q35_E_WS, "attention: workspace too small");
   if (L.nchunk > kMaxChunks) return fail(Q35_E_SHAPE, "attention: tmax too large for one merge");

@@ -203,6 +203,21 @@ int q35_argmax(const float* logits, int64_t n, int32_t* out, void* ws, size_t ws
   return argmax_launch(logits, n, out, ws, ws_bytes, S(stream));
 }
 
+int q35_workspace_status(void* ws, void* stream) {
+  if (!ws) return fail(Q35_E_ARG, "workspace_status: null workspace");
+  hipStream_t st = S(stream);
+  uint32_t* word = ws_counters(ws) + kWsErrWord;
+  uint32_t v = 0;
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  Q35_HIP_TRY(hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost));
+  if (v == 0) return Q35_OK;
+  const uint32_t zero = 0;
+  Q35_HIP_TRY(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  if (v & kWsErrPos)
+    return fail(Q35_E_SHAPE, "attention: a row's position d_pos[b] was outside [0, tmax); that row was skipped");
+  return fail(Q35_E_HIP, "workspace: unknown error bits " + std::to_string(v));
+}
+
 size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax) {
   if (!d || B < 1) return 0;
   return kCounterBytes + acc_bytes(*d, B) + scratch_bytes(*d, B, std::max(1, tmax));

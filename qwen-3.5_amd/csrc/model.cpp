@@ -62,6 +62,9 @@ struct q35_model {
   int step_rc = Q35_OK;  // why the persistent kernel cannot run here, if it cannot
   std::string step_msg;
   q35::StepArgs step_args{};
+  uint32_t bar_epoch = 0;  // grid barriers passed by all launches since the counters were zeroed
+  int bar_per_token = 0;   // grid barriers per decode step
+  bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
 };
 
 namespace q35 {
@@ -213,7 +216,7 @@ int setup_persistent(q35_model* m) {
     s.gate_q = L.gate.q; s.gate_s = L.gate.s; s.up_q = L.up.q; s.up_s = L.up.s; s.down_q = L.down.q; s.down_s = L.down.s;
   }
   StepLayer* dl = nullptr;
-  uint32_t* bar = nullptr;
+  uint32_t *bar = nullptr, *err = nullptr;
   float *att_ml = nullptr, *att_o = nullptr, *arg_v = nullptr;
   int32_t* arg_i = nullptr;
   fx_t *gate_acc = nullptr, *h_sp = nullptr;
@@ -221,6 +224,7 @@ int setup_persistent(q35_model* m) {
   int rc;
   if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
       (rc = dev_alloc_t(m, "step_barrier", kStepBarBytes / 4, &bar)) ||
+      (rc = dev_alloc_t(m, "step_error", 1, &err)) ||
       (rc = dev_alloc_t(m, "step_gate_acc", gate_n, &gate_acc)) ||
       (rc = dev_alloc_t(m, "step_h", (size_t)2 * d.hidden, &h_sp)) ||
       (rc = dev_alloc_t(m, "attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
@@ -230,6 +234,7 @@ int setup_persistent(q35_model* m) {
     return rc;
   Q35_HIP_TRY(hipMemcpy(dl, hl.data(), hl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
   Q35_HIP_TRY(hipMemset(bar, 0, kStepBarBytes));
+  Q35_HIP_TRY(hipMemset(err, 0, sizeof(uint32_t)));
   Q35_HIP_TRY(hipMemset(gate_acc, 0, gate_n * sizeof(fx_t)));  // the step kernel keeps it zero between layers
   StepArgs& a = m->step_args;
   a.layers = dl; a.n_layers = d.n_layers;
@@ -251,8 +256,13 @@ int setup_persistent(q35_model* m) {
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
+  a.ord = make_arg_order(d.vocab);
   a.bar = bar;
+  a.bar_base = 0;
+  a.err = err;
   a.ntok = 0;
+  m->bar_epoch = 0;
+  m->bar_per_token = step_barriers_per_token(d);
   return Q35_OK;
 }
 
@@ -280,24 +290,35 @@ int capture(q35_model* m, hipStream_t st) {
   return Q35_OK;
 }
 
-// n consecutive steps in one launch of the persistent kernel
+const char* kStepFailed = "persistent step: a grid barrier timed out; the model state is invalid until q35_model_reset";
+
+// n consecutive steps in one launch of the persistent kernel.  The barrier base is the number of
+// barriers every earlier launch passed; a launch that fails (its error word set) leaves later
+// launches as no-ops until a reset, so the base only has to be right while nothing failed.
 int persistent(q35_model* m, int n, hipStream_t st) {
   if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
+  if (m->step_failed) return fail(Q35_E_HIP, kStepFailed);
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
   StepArgs a = m->step_args;
   a.ntok = n;
+  a.bar_base = m->bar_epoch;
   int rc = step_launch(a, m->step_grid, st);
   if (rc) return rc;
+  m->bar_epoch += (uint32_t)n * (uint32_t)m->bar_per_token;
   m->host_pos += n;
   return Q35_OK;
 }
 
-// Reads the persistent kernel's error word (synchronises the stream).
+// Reads the persistent kernel's sticky error word (synchronises the stream).
 int check_persistent(q35_model* m, hipStream_t st) {
   if (m->step_rc != Q35_OK) return Q35_OK;
-  Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 8, m->step_args.bar + kStepErrWord, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  if (m->step_failed) return fail(Q35_E_HIP, kStepFailed);
+  Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 8, m->step_args.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
   Q35_HIP_TRY(hipStreamSynchronize(st));
-  if (m->pinned[8] != 0) return fail(Q35_E_HIP, "persistent step: a grid barrier timed out; results are invalid");
+  if (m->pinned[8] != 0) {
+    m->step_failed = true;
+    return fail(Q35_E_HIP, kStepFailed);
+  }
   return Q35_OK;
 }
 
@@ -471,10 +492,13 @@ int q35_model_reset(q35_model* m, void* stream) {
     const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
                        n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
                        n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt" ||
-                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc" || n == "step_h";
+                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc" || n == "step_h" ||
+                       n == "step_barrier" || n == "step_error";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
   m->host_pos = 0;
+  m->bar_epoch = 0;
+  m->step_failed = false;
   return Q35_OK;
 }
 

@@ -9,9 +9,10 @@
 // RMSNorm) is staged once per block in LDS.  The R row partials of a lane are folded with a
 // transposed butterfly (each xor stage exchanges half of the remaining rows, then the lanes
 // sharing a row finish the sum): log2(R) + log2(64/R) exchanges for R rows.  Blocks stride over
-// row groups.  The argmax keeps (max, lowest index) per lane -> wave -> block; the last block
-// to finish reduces the block results; (max, lowest index) is a total order, so the result
-// does not depend on the reduction order.
+// row groups.  The argmax keeps the best (value, index) per lane -> wave -> block under the
+// reference's order (ArgOrder: larger value, ties by the reference's scan order); the last block
+// to finish reduces the block results; the order is total, so the result does not depend on the
+// reduction order.
 #include "q35_internal.h"
 #include <climits>
 
@@ -35,6 +36,7 @@ struct NkArgs {
   int32_t pro; const float* pw; float eps;
   int32_t* argmax_out; int32_t* pos_inc; int32_t* hist;
   float* part_v; int32_t* part_i; uint32_t* counter;
+  ArgOrder ord;
 };
 
 Q35_DEV float nk_in(const NkArgs& a, int m, int k) {
@@ -42,8 +44,8 @@ Q35_DEV float nk_in(const NkArgs& a, int m, int k) {
   return a.xf ? from_fx(a.xf[i]) : a.x[i];
 }
 
-// (max, lowest index) over the n published block results, 8 loads in flight per thread.
-Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& v, int& i) {
+// best (value, index) over the n published block results, 8 loads in flight per thread.
+Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& v, int& i, const ArgOrder& o) {
   v = -INFINITY;
   i = INT_MAX;
   for (int b0 = threadIdx.x; b0 < n; b0 += 8 * kThreads) {
@@ -57,13 +59,13 @@ Q35_DEV void reduce_published(const float* pv, const int32_t* pi, int n, float& 
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (argmax_better(vv[j], ii[j], v, i)) { v = vv[j]; i = ii[j]; }
+      if (argmax_better(vv[j], ii[j], v, i, o)) { v = vv[j]; i = ii[j]; }
   }
 }
 
-// Block-wide (max, lowest index) reduction; result valid in all threads.
-Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
-  wave_argmax(v, i);
+// Block-wide argmax reduction; result valid in all threads.
+Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi, const ArgOrder& o) {
+  wave_argmax(v, i, o);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) { shv[wid] = v; shi[wid] = i; }
@@ -71,7 +73,7 @@ Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
   v = shv[0]; i = shi[0];
 #pragma unroll
   for (int w = 1; w < 4; ++w)
-    if (argmax_better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
+    if (argmax_better(shv[w], shi[w], v, i, o)) { v = shv[w]; i = shi[w]; }
 }
 
 template <int MR, int CPW>
@@ -161,19 +163,19 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
       const int row = row0 + lane / (64 / R);
       if ((lane % (64 / R)) == 0 && row < a.N) {
         if (a.y) a.y[(size_t)m * a.ldy + row] = v;
-        if (m == 0 && v > best_v) { best_v = v; best_i = row; }
+        if (m == 0 && argmax_better(v, row, best_v, best_i, a.ord)) { best_v = v; best_i = row; }
       }
     }
   }
 
   if (!a.argmax_out) return;
-  block_argmax(best_v, best_i, shv, shi);
+  block_argmax(best_v, best_i, shv, shi, a.ord);
   if (tid == 0) { st_agent(&a.part_v[blockIdx.x], best_v); st_agent(&a.part_i[blockIdx.x], best_i); }
   if (!arrive_last_grid(a.counter, &flag)) return;
   float v;
   int i;
-  reduce_published(a.part_v, a.part_i, gridDim.x, v, i);
-  block_argmax(v, i, shv, shi);
+  reduce_published(a.part_v, a.part_i, gridDim.x, v, i, a.ord);
+  block_argmax(v, i, shv, shi, a.ord);
   if (tid == 0) {
     const int32_t tok = (i == INT_MAX) ? 0 : i;
     *a.argmax_out = tok;
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void nk_kernel(const NkArgs a) {
 }
 
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* v, int64_t n, float* part_v, int32_t* part_i,
-                                                         uint32_t* counter, int32_t* out) {
+                                                         uint32_t* counter, int32_t* out, const ArgOrder ord) {
   __shared__ float shv[4];
   __shared__ int shi[4];
   __shared__ int flag;
@@ -195,15 +197,15 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* v, int64_
   int bi = INT_MAX;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + tid; i < n; i += (int64_t)gridDim.x * kThreads) {
     const float x = v[i];
-    if (x > bv) { bv = x; bi = (int)i; }
+    if (argmax_better(x, (int)i, bv, bi, ord)) { bv = x; bi = (int)i; }
   }
-  block_argmax(bv, bi, shv, shi);
+  block_argmax(bv, bi, shv, shi, ord);
   if (tid == 0) { st_agent(&part_v[blockIdx.x], bv); st_agent(&part_i[blockIdx.x], bi); }
   if (!arrive_last_grid(counter, &flag)) return;
   float rv;
   int ri;
-  reduce_published(part_v, part_i, gridDim.x, rv, ri);
-  block_argmax(rv, ri, shv, shi);
+  reduce_published(part_v, part_i, gridDim.x, rv, ri, ord);
+  block_argmax(rv, ri, shv, shi, ord);
   if (tid == 0) *out = (ri == INT_MAX) ? 0 : ri;
 }
 
@@ -266,6 +268,7 @@ int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
   a.x = c.x; a.xf = c.xf; a.ldx = c.ldx; a.y = c.y; a.ldy = c.ldy;
   a.pro = c.pro; a.pw = c.pw; a.eps = c.eps;
   a.argmax_out = c.argmax_out; a.pos_inc = c.pos_inc; a.hist = c.hist;
+  a.ord = make_arg_order(c.N);
   const int grid = nk_grid(c.N, c.K);
   a.counter = nullptr; a.part_v = nullptr; a.part_i = nullptr;
   if (c.argmax_out) {
@@ -301,7 +304,7 @@ int argmax_launch(const float* v, int64_t n, int32_t* out, void* ws, size_t ws_b
   char* base = ws_scratch(ws);
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)g), dim3(kThreads), 0, st, v, n,
                      reinterpret_cast<float*>(base), reinterpret_cast<int32_t*>(base + 4096),
-                     ws_counters(ws), out);
+                     ws_counters(ws), out, make_arg_order(n));
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

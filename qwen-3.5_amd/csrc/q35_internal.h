@@ -141,15 +141,43 @@ Q35_DEV uint32_t ld_agent(const uint32_t* p) {
   return __hip_atomic_load((Q35_GLOBAL uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// (max, lowest index) order used by every argmax: a total order, so any reduction tree gives
-// the same winner.
-Q35_DEV bool argmax_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
-Q35_DEV void wave_argmax(float& v, int& i) {
+// Greedy argmax order of the reference (kernels.rs:298-371).  Its first kernel lets unit
+// p < c = n/8 scan p, p + c, ..., p + 7c keeping the first strict maximum; its second has
+// thread t < 256 scan the unit results t, t + 256, ... and thread 0 scan the 256 thread
+// results, each keeping the first strict maximum.  Among exactly equal maxima the winner is
+// therefore the index i = k c + p minimising (p mod 256, p div 256, k), which is not always the
+// lowest index (i = 256 beats i = 1; i = c beats i = 1).  The key below encodes that tuple in 32
+// bits; an argmax is "larger value, or equal value and smaller key", a total order on indices,
+// so any reduction tree (lanes, waves, blocks) returns the reference's winner.  The last n mod 8
+// values, which the reference never reads, rank after all others on ties; the out-of-range
+// index (the INT_MAX sentinel of an empty partial) ranks last.  NaN never wins here.
+struct ArgOrder {
+  uint32_t n, c, s, n8;  // n values; c = n / 8; s = ceil(c / 256); n8 = 8 c
+};
+inline ArgOrder make_arg_order(int64_t n) {
+  ArgOrder o;
+  o.n = (uint32_t)n;
+  o.c = (uint32_t)(n / 8);
+  o.s = (o.c + 255u) / 256u;
+  o.n8 = 8u * o.c;
+  return o;
+}
+Q35_DEV uint32_t arg_key(const ArgOrder& o, int i) {
+  if (i < 0 || (uint32_t)i >= o.n) return 0xffffffffu;
+  const uint32_t u = (uint32_t)i;
+  if (u >= o.n8) return (o.s << 11) + (u - o.n8);
+  const uint32_t k = u / o.c, p = u - k * o.c;
+  return ((((p & 255u) * o.s) + (p >> 8)) << 3) + k;
+}
+Q35_DEV bool argmax_better(float v, int i, float bv, int bi, const ArgOrder& o) {
+  return v > bv || (v == bv && arg_key(o, i) < arg_key(o, bi));
+}
+Q35_DEV void wave_argmax(float& v, int& i, const ArgOrder& o) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (argmax_better(ov, oi, v, i)) { v = ov; i = oi; }
+  for (int s = 32; s > 0; s >>= 1) {
+    const float ov = __shfl_xor(v, s, 64);
+    const int oi = __shfl_xor(i, s, 64);
+    if (argmax_better(ov, oi, v, i, o)) { v = ov; i = oi; }
   }
 }
 
@@ -224,8 +252,16 @@ Q35_DEV bool arrive_last(uint32_t* counter, uint32_t expected, int* sh_flag) {
 // counters (zero between launches; each kernel leaves them zero), scratch follows.  Kernels on
 // one stream run one after another, so they can all reuse the same workspace.
 constexpr size_t kCounterBytes = 65536;
-constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+// The last counter word is the workspace's sticky error word: kernels that validate
+// device-resident arguments (positions) OR a Q35_WS_ERR_* bit into it instead of touching memory
+// out of range; q35_workspace_status reads and clears it.
+constexpr int kWsErrWord = (int)(kCounterBytes / 4) - 1;
+constexpr int kMaxCounters = kWsErrWord;
 inline uint32_t* ws_counters(void* ws) { return static_cast<uint32_t*>(ws); }
+enum : uint32_t { kWsErrPos = 1u };  // an attention position outside [0, tmax)
+Q35_DEV void ws_raise(uint32_t* counters, uint32_t bit) {
+  __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)&counters[kWsErrWord], bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 inline char* ws_scratch(void* ws) { return static_cast<char*>(ws) + kCounterBytes; }
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -426,15 +462,28 @@ struct StepArgs {
   float* logits;       // may be null
   float* arg_v; int32_t* arg_i;  // per-block argmax partials [grid]
   int32_t *token, *pos, *prompt, *plen, *hist;
-  uint32_t* bar;       // barrier counters (kStepBarBytes, zero at launch); bar[kStepErrWord] = error flag
+  ArgOrder ord;        // the reference's argmax order over the vocabulary
+  // Barrier counters (kStepBarBytes).  They are never cleared between launches: each launch
+  // passes bar_base, the number of grid barriers completed by all earlier launches since the
+  // counters were last zeroed (model reset), and waits for counter values relative to it
+  // (wrapping uint32 arithmetic).  So a launch needs no memset (nothing to record in a graph).
+  uint32_t* bar;
+  uint32_t bar_base;
+  // Sticky error word (its own allocation, cleared only by a model reset): set when a barrier
+  // wait times out; every launch that finds it set at entry returns at once without touching
+  // any state, so one failure cannot be followed by launches that compute on a broken state.
+  uint32_t* err;
   int32_t ntok;
 };
 constexpr size_t kStepBarBytes = 16384;
 // Every block of the qkvz stage adds into the 2 x lin_heads gate accumulators; packed, they
 // would share two cache lines and the atomics would serialise on them.
 constexpr int kStepBaStride = 16;  // fx_t entries (128 bytes)
-constexpr int kStepErrWord = 3072;
 constexpr int kStepThreads = 512;
+// Grid barriers one decode step of the persistent kernel passes: 4 per linear-attention layer
+// (qkvz, out, gate|up, down), 5 per full-attention layer (qkv, attn, o, gate|up, down), 1 for
+// the lm_head.
+int step_barriers_per_token(const q35_dims& d);
 // Blocks of the persistent kernel that fit co-resident (one per CU); 0 if the kernel cannot run.
 int step_grid(int hidden);
 // Attention chunks per kv head for a grid (the merge keeps their weights in LDS).

@@ -29,10 +29,12 @@
 //
 // Barrier: blocks arrive on one of 32 group counters (blockIdx % 32) with a non-returning
 // atomic after their stores have completed; the waiting wave reads all group counters with one
-// load per lane.  Counters only grow within a launch (zeroed by the host before it), so the
-// target of the n-th barrier is (blocks in group) * n.  Every wait is bounded: on time-out the
-// block sets the error word and returns, and the other blocks see the word and return too, so
-// the grid always drains.
+// load per lane.  Counters only grow (they are zeroed by a model reset, never by a launch); the
+// launch is told how many barriers earlier launches passed (bar_base), so the target of its
+// n-th barrier is (blocks in group) * (bar_base + n), compared in wrapping uint32 arithmetic.
+// Every wait is bounded: on time-out the block sets the sticky error word and returns, and the
+// other blocks see the word and return too, so the grid always drains; a later launch that
+// finds the word set returns at entry.
 #include "q35_internal.h"
 
 #include <algorithm>
@@ -109,8 +111,8 @@ Q35_DEV float block_sum(float v, float* shs, bool lead_sync = true) {
   return ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;
 }
 
-Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
-  wave_argmax(v, i);
+Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi, const ArgOrder& o) {
+  wave_argmax(v, i, o);
   const int lane = tix() & 63, wid = tix() >> 6;
   __syncthreads();
   if (lane == 0) { shv[wid] = v; shi[wid] = i; }
@@ -119,7 +121,7 @@ Q35_DEV void block_argmax(float& v, int& i, float* shv, int* shi) {
   i = shi[0];
 #pragma unroll
   for (int w = 1; w < kNW; ++w)
-    if (argmax_better(shv[w], shi[w], v, i)) { v = shv[w]; i = shi[w]; }
+    if (argmax_better(shv[w], shi[w], v, i, o)) { v = shv[w]; i = shi[w]; }
 }
 
 Q35_DEV float wave_max(float v) {
@@ -140,7 +142,7 @@ Q35_DEV float4 ld4_fx(const fx_t* p) {
 struct Bar {
   uint32_t* ctr;
   uint32_t* err;
-  uint32_t epoch;  // barriers passed so far by this block
+  uint32_t epoch;  // barriers passed so far by this block, counted from the counters' last reset
 };
 
 // Publishes this block's completion of the current stage: all of its memory operations are
@@ -162,13 +164,13 @@ Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
     const int g = tix();
     const uint32_t nb = gridDim.x;
     const uint32_t per = g < kGroups ? (nb + kGroups - 1 - (uint32_t)g) / kGroups : 0u;
-    const uint32_t target = per * b.epoch;
+    const uint32_t target = per * b.epoch;  // wraps; compared as a signed difference below
     uint32_t spin = 0;
     bool ok = true;
     while (true) {
-      const uint32_t v = g < kGroups ? ld_agent(&b.ctr[g * kCtrStride]) : 0xffffffffu;
+      const uint32_t v = g < kGroups ? ld_agent(&b.ctr[g * kCtrStride]) : target;
       const uint32_t e = ld_agent(b.err);
-      if (__all(v >= target)) break;
+      if (__all((int32_t)(v - target) >= 0)) break;
       if (e != 0u || ++spin > kSpin) { ok = false; break; }
       __builtin_amdgcn_s_sleep(2);
     }
@@ -429,7 +431,7 @@ Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
     float v = -INFINITY;
     int ix = INT_MAX;
     if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
-    block_argmax(v, ix, sh.shv, sh.shi);
+    block_argmax(v, ix, sh.shv, sh.shi, a.ord);
     tok = (ix == INT_MAX) ? 0 : ix;
     if (bix() == 0 && tix() == 0) st_agent(&a.hist[p - 1], tok);
   }
@@ -969,8 +971,8 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
 // ------------------------------------------------------------------ lm_head + argmax
 // Tied embedding [V][H] as lm_head (kernels.rs:251-291): wave w owns R rows per block step,
 // lane l reads the 16-byte chunks 16*(l + 64c), c < CPW, of each row; two steps of loads
-// (2 x 8 per lane, 128 KB per block) are kept in flight.  Block (max, lowest index) -> arg_v /
-// arg_i.
+// (2 x 8 per lane, 128 KB per block) are kept in flight.  Block argmax (reference order,
+// ArgOrder) -> arg_v / arg_i.
 template <int CPW>
 Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
   constexpr int R = 8 / CPW;
@@ -1025,7 +1027,7 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
     const int row = rb * RPB + wid * R + lane / (64 / R);
     if ((lane % (64 / R)) == 0 && row < a.V) {
       if (a.logits) stg(a.logits + row, v);
-      if (v > best_v) { best_v = v; best_i = row; }
+      if (argmax_better(v, row, best_v, best_i, a.ord)) { best_v = v; best_i = row; }
     }
   };
   const int rb0 = bix(), gs = gridDim.x;
@@ -1042,7 +1044,7 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
     if (rb + 2 * gs < nrb) load(rb + 2 * gs, wa, sa);
     compute(rb + gs, wb, sb);
   }
-  block_argmax(best_v, best_i, sh.shv, sh.shi);
+  block_argmax(best_v, best_i, sh.shv, sh.shi, a.ord);
   if (tid == 0) { st_agent(&a.arg_v[bix()], best_v); st_agent(&a.arg_i[bix()], best_i); }
   bar_arrive(bar);
   return true;
@@ -1095,7 +1097,9 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   __shared__ int shi[kNW];
   __shared__ int ok;
   const Shared sh{smem, shs, shv, shi, &ok};
-  Bar bar{a.bar, a.bar + kStepErrWord, 0u};
+  Bar bar{a.bar, a.err, a.bar_base};
+  // a failed earlier launch left the model state invalid: do nothing until a reset
+  if (ld_agent(a.err) != 0u) return;
   const int p0 = ldg(a.pos);
   for (int i = 0; i < a.ntok; ++i) {
     const int p = p0 + i;
@@ -1123,7 +1127,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   float v = -INFINITY;
   int ix = INT_MAX;
   if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
-  block_argmax(v, ix, sh.shv, sh.shi);
+  block_argmax(v, ix, sh.shv, sh.shi, a.ord);
   if (tix() == 0) {
     const int tok = (ix == INT_MAX) ? 0 : ix;
     const int pl = p0 + a.ntok - 1;
@@ -1199,9 +1203,15 @@ void step_plan(const q35_dims& d, int grid, StepMv* mv) {
   }
 }
 
+int step_barriers_per_token(const q35_dims& d) {
+  int n = 1;  // lm_head
+  for (int l = 0; l < d.n_layers; ++l) n += ((l + 1) % d.full_interval == 0) ? 5 : 4;
+  return n;
+}
+
 int step_launch(const StepArgs& a, int grid, hipStream_t st) {
   if (a.ntok < 1) return Q35_OK;
-  Q35_HIP_TRY(hipMemsetAsync(a.bar, 0, kStepBarBytes, st));
+  if (!a.bar || !a.err) return fail(Q35_E_ARG, "persistent step: null barrier or error word");
   StepArgs args = a;
   void* params[] = {&args};
   Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H), dim3(grid), dim3(kT), params, 0, st));

@@ -68,6 +68,7 @@ PROTOTYPES = {
     "q35_attention_core_decode": (ctypes.c_int, [ctypes.POINTER(Dims), c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp,
                                                  c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "q35_layer_ws_bytes": (c_sz, [ctypes.POINTER(Dims), c_i32, c_i32]),
+    "q35_workspace_status": (ctypes.c_int, [c_vp, c_vp]),
     "q35_rope_tables": (ctypes.c_int, [ctypes.POINTER(Dims), c_i32, c_vp, c_vp]),
     "q35_model_create_synthetic": (ctypes.c_int, [ctypes.POINTER(Dims), c_u64, c_i32, ctypes.POINTER(c_vp)]),
     "q35_model_destroy": (ctypes.c_int, [c_vp]),

@@ -9,12 +9,23 @@ Differences from the reference, by design: batches of M rows are accepted (the r
 squeezes [1,1,K] and panics otherwise) and q8_gemv_partial_sum sums every input row (the
 reference kernel skips rows when K / splits is not a multiple of 8, kernels.rs:119-133,504).
 """
+import atexit
+
 import numpy as np
 import torch
 
 from . import _lib as L
 
 _workspaces = {}
+
+
+def release_workspaces():
+    """Drop the cached workspaces (their device memory returns to torch's allocator).  Called
+    at interpreter exit so that no tensor is released during module teardown."""
+    _workspaces.clear()
+
+
+atexit.register(release_workspaces)
 
 
 def _stream():

@@ -3,11 +3,24 @@
 The model, its caches and the captured decode-step graph live in libq35.so; this class only
 owns the handle.
 """
+import atexit
 import ctypes
+import weakref
 
 import numpy as np
 
 from . import _lib as L
+
+_live = weakref.WeakSet()
+
+
+@atexit.register
+def _close_all():
+    """Destroy every model still open while the interpreter and the HIP runtime are fully up
+    (atexit handlers run before module teardown and long before the C runtime's exit
+    handlers), so no device memory is freed from a finaliser during shutdown."""
+    for m in list(_live):
+        m.close()
 
 
 class TextForCausalLM:
@@ -17,6 +30,7 @@ class TextForCausalLM:
         h = ctypes.c_void_p()
         L.check(L.lib().q35_model_create_synthetic(ctypes.byref(self.dims), seed, tmax, ctypes.byref(h)))
         self.h = h
+        _live.add(self)
 
     def close(self):
         if self.h:
@@ -94,6 +108,20 @@ class TextForCausalLM:
         if rc != 0:
             raise RuntimeError(f"hipMemcpy failed: {rc}")
         return out.reshape(shape) if shape is not None else out
+
+    def set_tensor(self, name, values):
+        """Overwrite a model tensor with host values of the same byte size (synchronises)."""
+        import torch
+        ptr, nbytes = self.tensor_ptr(name)
+        v = np.ascontiguousarray(values)
+        if v.nbytes > nbytes:
+            raise ValueError(f"{name}: {v.nbytes} bytes given, tensor holds {nbytes}")
+        torch.cuda.synchronize()
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        rc = hip.hipMemcpy(ctypes.c_void_p(ptr), v.ctypes.data, v.nbytes, 1)  # hipMemcpyHostToDevice
+        if rc != 0:
+            raise RuntimeError(f"hipMemcpy failed: {rc}")
 
 
 def synth_model_tensor(dims, seed, name, n):

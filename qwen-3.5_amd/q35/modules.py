@@ -97,9 +97,12 @@ def gated_delta_rule_decode(mixed_qkv, beta_g, conv_state, conv_w, recurrent_sta
     return out
 
 
-def attention_core_decode(dims, q_gate, k_new, v_new, q_norm, k_norm, k_cache, v_cache, pos, rope_cos, rope_sin):
+def attention_core_decode(dims, q_gate, k_new, v_new, q_norm, k_norm, k_cache, v_cache, pos, rope_cos, rope_sin,
+                          check=False):
     """q/k norm, RoPE, KV append, GQA softmax attention and sigmoid gate for one token
-    (text_modules.rs:860-936).  q_gate [B, heads*512]; k_new/v_new [B, kv_heads*256]."""
+    (text_modules.rs:860-936).  q_gate [B, heads*512]; k_new/v_new [B, kv_heads*256].
+    check=True synchronises and raises Q35Error if a position lay outside [0, tmax) (that row
+    is then skipped on the device, as q35_workspace_status documents)."""
     B = q_gate.shape[0]
     tmax = k_cache.shape[2]
     out = torch.empty((B, dims.attn_heads * dims.head_dim), dtype=torch.float32, device=q_gate.device)
@@ -108,6 +111,8 @@ def attention_core_decode(dims, q_gate, k_new, v_new, q_norm, k_norm, k_cache, v
                                               _p(q_norm), _p(k_norm), k_cache.data_ptr(), v_cache.data_ptr(), tmax,
                                               pos.data_ptr(), _p(rope_cos), _p(rope_sin), out.data_ptr(), ws.data_ptr(),
                                               ws.numel(), _stream()))
+    if check:
+        L.check(L.lib().q35_workspace_status(ws.data_ptr(), _stream()))
     return out
 
 

@@ -146,3 +146,31 @@ def test_argmax_exact_and_ties():
     for n in (1, 63, 1000, 3_000_001):
         w = normal(22, (n,))
         assert int(host(q35.argmax(dev(w)))[0]) == O.argmax(w)
+
+
+def test_argmax_reference_tie_order_bit_exact():
+    """Exact ties resolve as the reference's two-stage argmax does (kernels.rs:298-371), checked
+    against the oracle's literal restatement of those two kernels."""
+    V = 248320
+    c = V // 8
+    for idx in ([255, 256], [5, 5 + c], [1, c], [512, 256], [257, 1], [V - 1, 255], [V - 1, 31039],
+                [c + 3, 2 * c + 3, 3]):
+        v = np.zeros(V, np.float32)
+        v[idx] = 1.0
+        want = O.argmax_reference_order(v)
+        assert int(host(q35.argmax(dev(v)))[0]) == want, idx
+    v = np.zeros(V, np.float32)
+    assert int(host(q35.argmax(dev(v)))[0]) == 0 == O.argmax_reference_order(v)
+    g = np.random.default_rng(7)
+    for n in (2048, 4096, V):
+        for trial in range(6):
+            w = g.integers(0, 3, n).astype(np.float32)
+            if trial % 2:
+                w[g.integers(0, n, 4)] = 9.0
+            assert int(host(q35.argmax(dev(w)))[0]) == O.argmax_reference_order(w) == O.argmax(w), (n, trial)
+    # the n mod 8 values the reference never reads: read here, after all others on ties
+    w = np.zeros(2053, np.float32)
+    w[2051] = 2.0
+    assert int(host(q35.argmax(dev(w)))[0]) == 2051 == O.argmax(w)
+    w[9] = 2.0
+    assert int(host(q35.argmax(dev(w)))[0]) == 9 == O.argmax(w)

@@ -166,3 +166,40 @@ def test_mlp_module_tiled_weights(B):
     out = host(gpu.forward(dev(x)))
     exp = O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), x)
     assert rel_l2(out, exp) <= 1e-5
+
+
+def test_attention_position_outside_cache_is_reported():
+    """A position d_pos[b] outside [0, tmax) is caught on the device: that row's cache rows and
+    output are untouched, the other rows are computed, and the workspace reports Q35_E_SHAPE
+    (then clears, so the next good call passes)."""
+    print("[attention position guard]", flush=True)
+    d = q35.dims_2b()
+    nh, nkv, hd = d.attn_heads, d.kv_heads, d.head_dim
+    B, tmax = 3, 64
+    rng = np.random.default_rng(5)
+    kc = rng.standard_normal((B, nkv, tmax, hd), dtype=np.float32)
+    vc = rng.standard_normal((B, nkv, tmax, hd), dtype=np.float32)
+    qg = normal(70, (B, nh * 2 * hd))
+    kn, vn = normal(71, (B, nkv * hd)), normal(72, (B, nkv * hd))
+    qw, kw = normal(73, (hd,), 0.1), normal(74, (hd,), 0.1)
+    cs, sn = q35.rope_tables(d, tmax)
+    kc_d, vc_d = dev(kc), dev(vc)
+    pos = np.array([tmax - 1, tmax, 5], np.int32)
+    with pytest.raises(q35.Q35Error) as ei:
+        q35.attention_core_decode(d, dev(qg), dev(kn), dev(vn), dev(qw), dev(kw), kc_d, vc_d, dev(pos), dev(cs),
+                                  dev(sn), check=True)
+    assert ei.value.code == q35._lib.Q35_E_SHAPE
+    kc_g, vc_g = host(kc_d), host(vc_d)
+    np.testing.assert_array_equal(kc_g[1], kc[1])
+    np.testing.assert_array_equal(vc_g[1], vc[1])
+    # the good rows went ahead: their new rows differ from the old contents
+    assert not np.array_equal(kc_g[0, :, tmax - 1], kc[0, :, tmax - 1])
+    assert not np.array_equal(kc_g[2, :, 5], kc[2, :, 5])
+    # cleared: a call with valid positions reports nothing
+    pos2 = np.array([3, 4, 5], np.int32)
+    q35.attention_core_decode(d, dev(qg), dev(kn), dev(vn), dev(qw), dev(kw), kc_d, vc_d, dev(pos2), dev(cs),
+                              dev(sn), check=True)
+    pos3 = np.array([-1, 0, 1], np.int32)
+    with pytest.raises(q35.Q35Error):
+        q35.attention_core_decode(d, dev(qg), dev(kn), dev(vn), dev(qw), dev(kw), kc_d, vc_d, dev(pos3), dev(cs),
+                                  dev(sn), check=True)

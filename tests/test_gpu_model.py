@@ -99,6 +99,75 @@ def test_persistent_multi_step_launch_equals_single_steps():
     a.close()
 
 
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
+def test_fused_argmax_reference_tie_order(mode):
+    """The lm_head's fused argmax resolves exact ties as the reference's two-stage argmax
+    (kernels.rs:298-371).  The winning row of the tied embedding table is copied into rows that
+    the reference's scan visits earlier and later, so those logits are bit-identical to the max;
+    the token picked must be the reference order's pick over the GPU's own logits."""
+    print(f"[model argmax ties] mode={mode}", flush=True)
+    d = tiny_dims()
+    c = d.vocab // 8
+    prompt = (np.arange(12, dtype=np.int32) * 97 + 1000) % d.vocab
+    m = q35.TextForCausalLM(d, seed=6, tmax=64)
+    toks, _ = m.generate(prompt, 0, mode=mode)
+    m.check()
+    w = int(toks[0])
+    q = m.tensor("embed_tokens.q", np.int8).reshape(d.vocab, d.hidden).copy()
+    sc = m.tensor("embed_tokens.scale", np.float32).reshape(d.vocab, d.hidden // 64).copy()
+    cand = {256, c + 256, 3 * c + 1, (w + c) % d.vocab, (w % c) + 256 if (w % c) + 256 < c else 512}
+    dups = sorted(cand - {w} - set(prompt.tolist()))  # rows the prompt does not embed
+    assert len(dups) >= 3
+    q[dups] = q[w]
+    sc[dups] = sc[w]
+    m.set_tensor("embed_tokens.q", q)
+    m.set_tensor("embed_tokens.scale", sc)
+    m.reset()
+    toks2, _ = m.generate(prompt, 0, mode=mode)
+    m.check()
+    logits = m.tensor("logits", np.float32)
+    tied = np.flatnonzero(logits == logits.max())
+    print("winner", w, "tied", tied.tolist(), "picked", int(toks2[0]), flush=True)
+    assert len(tied) >= 2 and set(dups) <= set(tied.tolist())
+    assert int(toks2[0]) == O.argmax_reference_order(logits) == O.argmax(logits)
+    m.close()
+
+
+def test_persistent_error_is_sticky():
+    """A persistent-kernel failure (forced from the host by setting the error word, so every
+    block returns at entry) makes later launches no-ops that leave the state untouched; check()
+    keeps raising and persistent steps are refused until reset(), after which decoding matches a
+    fresh model."""
+    print("[model sticky error]", flush=True)
+    d = tiny_dims()
+    prompt = np.arange(9, dtype=np.int32) * 13 % d.vocab
+    ref = q35.TextForCausalLM(d, seed=8, tmax=64)
+    want, _ = ref.generate(prompt, 10, mode="persistent")
+    ref.check()
+    ref.close()
+    m = q35.TextForCausalLM(d, seed=8, tmax=64)
+    m.generate(prompt, 2, mode="persistent")
+    m.check()
+    hist0 = m.tensor("hist", np.int32).copy()
+    pos0 = int(m.tensor("pos", np.int32)[0])
+    m.set_tensor("step_error", np.ones(1, np.uint32))
+    m.decode(5, mode="persistent")
+    m.decode(3, mode="persistent")
+    with pytest.raises(q35.Q35Error):
+        m.check()
+    np.testing.assert_array_equal(m.tensor("hist", np.int32), hist0)
+    assert int(m.tensor("pos", np.int32)[0]) == pos0
+    with pytest.raises(q35.Q35Error):
+        m.decode(1, mode="persistent")
+    with pytest.raises(q35.Q35Error):
+        m.check()
+    m.reset()
+    got, _ = m.generate(prompt, 10, mode="persistent")
+    m.check()
+    np.testing.assert_array_equal(got, want)
+    m.close()
+
+
 def test_model_rejects_overflow():
     d = tiny_dims()
     m = q35.TextForCausalLM(d, seed=1, tmax=8)

@@ -306,3 +306,47 @@ def test_model_step_wiring():
         np.testing.assert_allclose(logits, ref[0], rtol=1e-5, atol=1e-6)
         assert got == O.argmax(ref[0])
         tok = got
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_mlp_decode_closed_form(B, rng):
+    """orc_mlp_decode == down(silu(x Wg) * (x Wu)) (text_modules.rs:1000-1011) in numpy float64
+    from the dequantised weights.  Gate and up are drawn with different scales and a shifted
+    gate, so swapping them or putting the SiLU on `up` moves the result far outside the bar
+    (checked below on the same data)."""
+    H, F = 256, 384
+    cfg = O.Cfg(hidden=H, ffn=F, vocab=1000, n_layers=1, full_interval=4, lin_heads=2, lin_dk=128, lin_dv=128,
+                conv_k=4, attn_heads=8, kv_heads=2, head_dim=256, rot_dim=64, eps=1e-6, theta=1e7)
+    Wg = O.quantize((rng.standard_normal((H, F)) * 0.08 + 0.01).astype(np.float32))
+    Wu = O.quantize((rng.standard_normal((H, F)) * 0.03).astype(np.float32))
+    Wd = O.quantize((rng.standard_normal((F, H)) * 0.05).astype(np.float32))
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    out = O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), x)
+    xd = x.astype(np.float64)
+    g, u = xd @ Wg.dequant(), xd @ Wu.dequant()
+    ref = (u * silu(g)) @ Wd.dequant()
+    assert out.shape == (B, H)
+    assert rel_l2(out, ref) <= 1e-5
+    # the plausible mistakes are far outside that bar on these inputs
+    assert rel_l2((g * silu(u)) @ Wd.dequant(), ref) > 0.1      # gate and up swapped
+    assert rel_l2((silu(u) * silu(g)) @ Wd.dequant(), ref) > 0.1  # SiLU on both
+    assert rel_l2((u * g) @ Wd.dequant(), ref) > 0.1            # SiLU dropped
+
+
+def test_mlp_decode_gate_closed():
+    """Known answer: a gate row pushing every gate pre-activation to -60 makes silu(gate) ~ 0
+    (|silu(-60)| < 6e-25), so the output vanishes whatever `up` holds; with the roles swapped
+    it would not."""
+    H, F = 128, 256
+    cfg = O.Cfg(hidden=H, ffn=F, vocab=1000, n_layers=1, full_interval=4, lin_heads=2, lin_dk=128, lin_dv=128,
+                conv_k=4, attn_heads=8, kv_heads=2, head_dim=256, rot_dim=64, eps=1e-6, theta=1e7)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 1.0
+    wg = np.zeros((H, F), np.float32)
+    wg[0, :] = -60.0
+    wu = np.full((H, F), 0.5, np.float32)
+    wd = np.full((F, H), 0.25, np.float32)
+    out = O.mlp_decode(cfg, O.MlpLayer(O.quantize(wg), O.quantize(wu), O.quantize(wd)), x)
+    assert np.max(np.abs(out)) < 1e-20
+    swapped = O.mlp_decode(cfg, O.MlpLayer(O.quantize(wu), O.quantize(wg), O.quantize(wd)), x)
+    assert np.max(np.abs(swapped)) > 1.0

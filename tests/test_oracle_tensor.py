@@ -143,15 +143,57 @@ def test_argmax_planted_and_ties(rng):
     assert O.argmax(v) == 5000 == int(np.argmax(v))
 
 
-def test_argmax_reference_tie_order_differs():
-    # kernels.rs:298-371: partial unit p = i mod 31040 feeds thread p mod 256, thread 0 wins a
-    # tie first; so of the tied indices 255 and 256 the reference returns 256.
+def test_argmax_reference_tie_order():
+    """kernels.rs:298-371: unit p = i mod c (c = n/8) keeps the first strict maximum of
+    p, p + c, ...; thread t keeps the first of units t, t + 256, ...; thread 0 the first of the
+    256 threads.  Known answers for exact ties, on both the literal two-kernel restatement and
+    the product's key order."""
     V = 248320
-    v = np.zeros(V, np.float32)
-    v[255] = 1.0
-    v[256] = 1.0
-    assert O.argmax(v) == 255
-    assert O.argmax_reference_order(v) == 256
+    c = V // 8
+    cases = [
+        ([255, 256], 256),        # unit 256 feeds thread 0, unit 255 thread 255
+        ([5, 5 + c], 5),          # same unit: the first in its scan
+        ([1, c], c),              # unit 0 (thread 0) beats unit 1
+        ([c + 3, 2 * c + 3, 3], 3),
+        ([512, 256], 256),        # thread 0 scans unit 256 before unit 512
+        ([257, 1], 1),            # thread 1 scans unit 1 before unit 257
+        ([V - 1, 255], V - 1),    # unit c-1 = 31039 sits on thread 63, which beats thread 255
+        ([V - 1, 31039], 31039),
+    ]
+    for idx, want in cases:
+        v = np.zeros(V, np.float32)
+        v[idx] = 1.0
+        assert O.argmax_reference_order(v) == want, idx
+        assert O.argmax(v) == want, idx
+    v = np.zeros(V, np.float32)  # all equal: unit 0, thread 0
+    assert O.argmax_reference_order(v) == 0 == O.argmax(v)
+
+
+@pytest.mark.parametrize("n", [2048, 4096, 8 * 300, 8 * 31040])
+def test_argmax_key_order_equals_two_stage_scan(n):
+    """The product's argmax order (a closed-form key per index) equals the literal simulation of
+    the reference's two kernels on inputs full of exact ties (values from a set of 3)."""
+    g = np.random.default_rng(n)
+    for trial in range(12):
+        v = g.integers(0, 3, n).astype(np.float32)
+        if trial % 3 == 0:
+            v[g.integers(0, n, 5)] = 7.0  # a few tied maxima only
+        assert O.argmax(v) == O.argmax_reference_order(v)
+
+
+def test_argmax_tail_and_nan():
+    """Values past 8*(n/8), which the reference never reads, are read here: a strict maximum
+    there wins; on a tie the indices the reference reads come first.  NaN is never picked."""
+    n = 2048 + 5
+    v = np.zeros(n, np.float32)
+    v[n - 2] = 3.0
+    assert O.argmax(v) == n - 2
+    v[700] = 3.0
+    assert O.argmax(v) == 700
+    w = np.arange(10, dtype=np.float32)
+    w[9] = np.nan
+    assert O.argmax(w) == 8
+    assert O.argmax(np.full(5, np.nan, np.float32)) == 0
 
 
 def test_gate_proj_closed_form(rng):
