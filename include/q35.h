@@ -51,8 +51,13 @@ enum {
  *           256-column tiles stored one after another: q[t][K][256], scale[t][K][4] for
  *           t < ceil(N/256) (columns past N zero).  Same values, so results are identical to
  *           Q35_KN; every K-chunk of a tile is one contiguous run of HBM, which is how the
- *           matvec streams it. */
-enum { Q35_KN = 0, Q35_NK = 1, Q35_KN_TILED = 2 };
+ *           matvec streams it.
+ *   Q35_KN_PANEL: the Q35_KN matrix re-laid out by q35_q8f_pack_kn_panel into 16-column panels,
+ *           q[N/16][K][16], with the scales transposed to scale[N/64][K].  Same values and byte
+ *           count; each panel (16 outputs over all of K) is one contiguous run, so the standalone
+ *           matvec computes it in one block with no cross-block reduction and no workspace.
+ *           Accepted by q35_q8_gemv / q35_q8_gemv_partial_sum only. */
+enum { Q35_KN = 0, Q35_NK = 1, Q35_KN_TILED = 2, Q35_KN_PANEL = 3 };
 
 typedef struct {
   const int8_t* q;
@@ -76,9 +81,10 @@ q35_dims q35_dims_qwen35_2b(void);
 
 /* ---------------------------------------------------------------- tensor level (kernels.rs) */
 
-/* y[M][N] = x[M][K] @ dequant(W).  W.layout selects KN (reference projections) or NK.
- * Full-K semantics (every input row is summed).  M in [1, 64]; K, N multiples of 64.
- * Replaces q8_gemv (src/kernels.rs:681-688, kernel :53-92). */
+/* y[M][N] = x[M][K] @ dequant(W).  W.layout selects KN (reference projections), its tiled or
+ * panel re-layouts, or NK.  Full-K semantics (every input row is summed).  M in [1, 64]; K, N
+ * multiples of 64.  One kernel launch per 8 rows of x (Q35_KN_PANEL needs no workspace: ws may
+ * be NULL).  Replaces q8_gemv (src/kernels.rs:681-688, kernel :53-92). */
 int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream);
 
 /* Same contract; replaces q8_gemv_partial_sum (src/kernels.rs:690-700, impl :495-537, kernels
@@ -282,6 +288,10 @@ int64_t q35_q8f_tiled_scale_count(int32_t K, int32_t N);
 /* Host: re-lay a Q35_KN matrix (q [K][N], scale [K][N/64]) out as Q35_KN_TILED. */
 int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_tiled_host,
                           float* scale_tiled_host);
+/* Host: re-lay a Q35_KN matrix out as Q35_KN_PANEL (q [N/16][K][16], scale [N/64][K]; the same
+ * K*N bytes and K*N/64 scales). */
+int q35_q8f_pack_kn_panel(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_panel_host,
+                          float* scale_panel_host);
 /* Host copy of the f32 values the model builder draws for a named tensor (before
  * quantisation), so a host-side checker can rebuild the same model. */
 int q35_synth_model_tensor(const q35_dims* d, uint64_t seed, const char* name, float* out_host, int64_t n);

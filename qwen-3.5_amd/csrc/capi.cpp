@@ -22,7 +22,7 @@ int check_q8f(const q35_q8f& W, const char* what) {
   if (!W.q || !W.scale) return fail(Q35_E_ARG, std::string(what) + ": null Q8F pointer");
   if (W.rows < 1 || W.cols < 64 || (W.cols % 64) != 0)
     return fail(Q35_E_SHAPE, std::string(what) + ": Q8F cols must be a positive multiple of 64");
-  if (W.layout != Q35_KN && W.layout != Q35_NK && W.layout != Q35_KN_TILED)
+  if (W.layout != Q35_KN && W.layout != Q35_NK && W.layout != Q35_KN_TILED && W.layout != Q35_KN_PANEL)
     return fail(Q35_E_ARG, std::string(what) + ": bad layout");
   if ((reinterpret_cast<uintptr_t>(W.q) & 15) != 0) return fail(Q35_E_ALIGN, std::string(what) + ": q not 16-byte aligned");
   return Q35_OK;
@@ -32,7 +32,8 @@ int check_q8f(const q35_q8f& W, const char* what) {
 int check_kn(const q35_q8f& W, const char* what) {
   const int rc = check_q8f(W, what);
   if (rc) return rc;
-  if (W.layout == Q35_NK) return fail(Q35_E_ARG, std::string(what) + ": projection must be Q35_KN or Q35_KN_TILED");
+  if (W.layout == Q35_NK || W.layout == Q35_KN_PANEL)
+    return fail(Q35_E_ARG, std::string(what) + ": layer projections must be Q35_KN or Q35_KN_TILED");
   return Q35_OK;
 }
 
@@ -127,6 +128,7 @@ q35_dims q35_dims_qwen35_2b(void) {
 }
 
 size_t q35_q8_gemv_ws_bytes(int32_t M, q35_q8f W) {
+  if (W.layout == Q35_KN_PANEL) return 0;
   if (W.layout == Q35_NK) return kCounterBytes;
   const int m = std::max(1, std::min<int>(M, 8));
   return kCounterBytes + align256((size_t)m * W.cols * sizeof(fx_t));
@@ -137,7 +139,15 @@ int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t
   if (rc) return rc;
   if (!x || !y) return fail(Q35_E_ARG, "q8_gemv: null x or y");
   if (M < 1 || M > 64) return fail(Q35_E_SHAPE, "q8_gemv: M must be in [1, 64]");
-  if (W.layout != Q35_NK) {
+  if (W.layout == Q35_KN_PANEL) {  // one launch per 8 rows, no workspace
+    const int K = W.rows, N = W.cols;
+    for (int m0 = 0; m0 < M; m0 += 8)
+      if ((rc = mvp_launch(W.q, W.scale, K, N, x + (size_t)m0 * K, K, std::min(8, M - m0), y + (size_t)m0 * N, N,
+                           S(stream))))
+        return rc;
+    return Q35_OK;
+  }
+  if (W.layout != Q35_NK) {  // split-K with fixed-point sums; one launch per 8 rows
     const int K = W.rows, N = W.cols;
     if (!ws || ws_bytes < q35_q8_gemv_ws_bytes(M, W)) return fail(Q35_E_WS, "q8_gemv: workspace too small");
     fx_t* acc = reinterpret_cast<fx_t*>(ws_scratch(ws));
@@ -146,8 +156,8 @@ int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t
       c.K = K; c.M = std::min(8, M - m0); c.nseg = 1;
       c.seg[0] = seg_of(W, acc, N);
       c.pro = PRO_PLAIN; c.x = x + (size_t)m0 * K; c.ldx = K;
+      c.y_out = y + (size_t)m0 * N; c.ldy = N; c.tile_ctr = ws_counters(ws);
       if ((rc = mv_kn_launch(c, S(stream)))) return rc;
-      if ((rc = fx_to_f32_launch(acc, (int64_t)c.M * N, y + (size_t)m0 * N, true, S(stream)))) return rc;
     }
     return Q35_OK;
   }

@@ -57,6 +57,7 @@ struct MvArgs {
   const float* aux_wb; const float* aux_wa; int32_t aux_nh; fx_t* aux_acc; int32_t aux_ldo;
   fx_t* zero_ptr; int64_t zero_n;
   float* cs_state; const fx_t* cs_x; int32_t cs_ch, cs_ldx, cs_B;
+  float* y_out; int32_t ldy; uint32_t* tile_ctr;
 };
 
 Q35_DEV float in1(const MvArgs& a, int m, int k) {
@@ -240,6 +241,7 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
   __shared__ __align__(16) float red[kRowsPerStep * kTile];
   __shared__ float sh[4];
   __shared__ float grp[MR * kMaxGroups];
+  __shared__ int last_flag;
 
   const int tid = threadIdx.x;
   const int nmain = a.ntiles * a.nsplit;
@@ -326,6 +328,19 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
     for (int i = 0; i < kRowsPerStep; ++i) v += red[i * kTile + tid];
     if (m < a.M && n < seg.N) fx_add(&seg.acc[(size_t)m * seg.ldacc + n], v);
     __syncthreads();
+  }
+  // f32 output: the last block of the tile to finish (its adds and every earlier block's are
+  // complete once the counter says so) converts the tile's sums and re-zeroes them
+  if (!a.y_out) return;
+  if (!arrive_last(&a.tile_ctr[tile], (uint32_t)a.nsplit, &last_flag)) return;
+  if (n < seg.N) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= a.M) break;
+      fx_t* p = &seg.acc[(size_t)m * seg.ldacc + n];
+      a.y_out[(size_t)m * a.ldy + n] = from_fx(ld_agent(p));
+      st_agent(p, (fx_t)0);
+    }
   }
 }
 
@@ -424,6 +439,9 @@ int mv_kn_launch(const MvCall& c, hipStream_t st) {
   a.aux_wb = c.aux_wb; a.aux_wa = c.aux_wa; a.aux_nh = c.aux_nh; a.aux_acc = c.aux_acc; a.aux_ldo = c.aux_ldo;
   a.zero_ptr = c.zero_ptr; a.zero_n = c.zero_n;
   a.cs_state = c.cs_state; a.cs_x = c.cs_x; a.cs_ch = c.cs_ch; a.cs_ldx = c.cs_ldx; a.cs_B = c.cs_B;
+  a.y_out = c.y_out; a.ldy = c.ldy; a.tile_ctr = c.tile_ctr;
+  if (c.y_out && (c.nseg != 1 || c.aux_nh > 0 || !c.tile_ctr || p.ntiles > kMaxCounters))
+    return fail(Q35_E_ARG, "mv_kn: f32 output needs one segment, no gate blocks and a counter per tile");
 
   const int nblocks = p.ntiles * p.nsplit + p.naux;
   const dim3 grid(nblocks), block(kThreads);

@@ -343,9 +343,17 @@ struct MvCall {
   float* cs_state = nullptr;
   const fx_t* cs_x = nullptr;
   int32_t cs_ch = 0, cs_ldx = 0, cs_B = 0;
+  // optional f32 output y[m*ldy + n] of a one-segment call: the last block of each tile converts
+  // the tile's fixed-point sums and re-zeroes them (tile_ctr: one zeroed counter per tile)
+  float* y_out = nullptr;
+  int32_t ldy = 0;
+  uint32_t* tile_ctr = nullptr;
 };
 
 int mv_kn_launch(const MvCall& c, hipStream_t st);
+// y[m][n] = x[m][:] . dequant(W)[:, n] for the Q35_KN_PANEL layout (one launch, M <= 8)
+int mvp_launch(const int8_t* q, const float* s, int32_t K, int32_t N, const float* x, int32_t ldx, int32_t M,
+               float* y, int32_t ldy, hipStream_t st);
 // y[i] = f32(acc[i]) (optionally re-zeroing acc); acc[i] = 0
 int fx_to_f32_launch(fx_t* acc, int64_t n, float* y, bool zero_after, hipStream_t st);
 int fx_zero_launch(fx_t* acc, int64_t n, hipStream_t st);

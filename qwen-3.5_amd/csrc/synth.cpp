@@ -203,6 +203,22 @@ int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t
   return Q35_OK;
 }
 
+int q35_q8f_pack_kn_panel(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_panel_host,
+                          float* scale_panel_host) {
+  if (!q_host || !scale_host || !q_panel_host || !scale_panel_host) return fail(Q35_E_ARG, "pack_kn_panel: null pointer");
+  if (K < 1 || N < 64 || (N % 64) != 0) return fail(Q35_E_SHAPE, "pack_kn_panel: N must be a positive multiple of 64");
+  const int64_t np = N / 16, nb = N / 64;
+  parallel_for(np * K, [&](int64_t i0, int64_t i1) {  // i = panel * K + k
+    for (int64_t i = i0; i < i1; ++i) {
+      const int64_t p = i / K, k = i % K;
+      std::memcpy(q_panel_host + i * 16, q_host + k * (int64_t)N + p * 16, 16);
+    }
+  });
+  for (int64_t b = 0; b < nb; ++b)
+    for (int64_t k = 0; k < K; ++k) scale_panel_host[b * K + k] = scale_host[k * nb + b];
+  return Q35_OK;
+}
+
 int q35_synth_model_tensor(const q35_dims* d, uint64_t seed, const char* name, float* out_host, int64_t n) {
   if (!d || !name || !out_host) return fail(Q35_E_ARG, "synth_model_tensor: null pointer");
   for (const TensorSpec& t : model_specs(*d)) {
