@@ -5,22 +5,25 @@
 // no workspace, one launch that writes f32 y directly, and a fixed summation order
 // (bit-reproducible).
 //
-// Memory pattern: lane l of wave w reads row k = tid + 512 j of the panel (16 bytes), so a wave's
+// Memory pattern: lane l of wave w reads row k = tid + T j of the panel (16 bytes), so a wave's
 // load instruction covers 64 consecutive rows = 1 KB contiguous of int8 plus 256 contiguous bytes of
-// scales; every row of the block is requested before the first is used (all of K for M <= 1 and
-// K <= 8192), so the whole panel is in flight at once.  x[k] is read per row from global memory
-// (it is small and shared by every panel, so it is served by the caches).  The 16 column partials
-// of a lane are folded across the wave with a transposed butterfly, then across the 8 waves
-// through LDS.
+// scales; every row of the block is requested before the first is used, so the whole panel is in
+// flight at once.  The weights carry the non-temporal hint (read once); the scales do not: the 4
+// panels of one 64-column scale block read the same scale row, and the panel order below puts
+// those 4 blocks on one XCD (workgroups go to the 8 XCDs round-robin), so 3 of the 4 reads hit
+// that XCD's L2.  x[k] is read per row from global memory (small and shared by every panel).
+//
+// Reduction of a lane's 16 column partials over the wave: two gfx950 lane swaps
+// (v_permlane32_swap, v_permlane16_swap) leave each 16-lane row with 4 columns summed over 4 lanes,
+// then DPP row rotations sum the 16 lanes of the row — all VALU, no LDS crossbar round trips; the
+// waves' results are added through LDS in a fixed order.
 #include "q35_internal.h"
 
 namespace q35 {
 
 namespace {
 
-constexpr int kT = 512;  // threads per block
-constexpr int kNW = kT / 64;
-constexpr int kP = 16;   // columns per panel
+constexpr int kP = 16;  // columns per panel
 
 struct MvpArgs {
   const int8_t* q;  // [N/16][K][16]
@@ -28,14 +31,49 @@ struct MvpArgs {
   const float* x;   // [M][ldx]
   float* y;         // [M][ldy]
   int32_t K, N, M, ldx, ldy;
+  int32_t remap;    // 1: XCD-aware panel order ((N/16) % 32 == 0)
 };
 
-// J rows per thread in flight per pass, MR input rows per launch.
-template <int MR, int J>
-__global__ __launch_bounds__(kT) void mvp_kernel(const MvpArgs a) {
-  __shared__ float red[kNW][MR][kP];
+Q35_DEV float swap32_sum(float a, float b) {  // lanes < 32: a(l) + a(l+32); lanes >= 32: b(l-32) + b(l)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+Q35_DEV float swap16_sum(float a, float b) {  // within each 32-lane half: rows 0 / 2 keep a, 1 / 3 keep b
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+Q35_DEV float row_sum16(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return v;
+}
+
+// Sum of acc[c] over the 64 lanes; on return every lane of 16-lane row r holds columns 4r .. 4r+3
+// in o[0..3].
+Q35_DEV void fold16(const float (&acc)[kP], float (&o)[4]) {
+  float s8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s8[j] = swap32_sum(acc[j], acc[j + 8]);  // column j (lanes < 32) or j + 8
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = row_sum16(swap16_sum(s8[j], s8[j + 4]));  // column 4r + j
+}
+
+// T threads, J rows per thread in flight per pass, MR input rows per launch.  EXACT: K is a
+// multiple of T*J, so no row is clamped or masked and no load is skipped; the compiler then knows
+// how many loads are outstanding and starts on row j as soon as it lands (with data-dependent
+// early exits it waits for every load of the pass first).
+template <int T, int MR, int J, bool EXACT>
+__global__ __launch_bounds__(T) void mvp_kernel(const MvpArgs a) {
+  constexpr int NW = T / 64;
+  __shared__ __align__(16) float red[NW][MR][kP];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int panel = blockIdx.x;
+  int panel = blockIdx.x;
+  if (a.remap) {  // panels 4g .. 4g+3 (one scale block) on blocks b with equal b % 8, i.e. one XCD
+    const int b = blockIdx.x, xcd = b & 7, slot = b >> 3;
+    panel = 4 * ((slot >> 2) * 8 + xcd) + (slot & 3);
+  }
   const int K = a.K;
   const int8_t* qp = a.q + (size_t)panel * K * kP;
   const float* sp = a.s + (size_t)(panel >> 2) * K;
@@ -45,24 +83,24 @@ __global__ __launch_bounds__(kT) void mvp_kernel(const MvpArgs a) {
 #pragma unroll
     for (int c = 0; c < kP; ++c) acc[m][c] = 0.f;
 
-  for (int k0 = 0; k0 < K; k0 += kT * J) {
+  for (int k0 = 0; k0 < K; k0 += T * J) {
     uint4 w[J];
     float sc[J];
     float xv[MR][J];
-    // issue every load of the pass first (rows clamped into the matrix; masked below)
+    // every load of the pass is issued first (rows clamped into the matrix; masked below)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      if (k0 + kT * j >= K) break;  // uniform
-      const int k = min(k0 + tid + kT * j, K - 1);
+      if (!EXACT && k0 + T * j >= K) break;  // uniform
+      const int k = EXACT ? k0 + tid + T * j : min(k0 + tid + T * j, K - 1);
       w[j] = ldg16_nt(qp + (size_t)k * kP);
-      sc[j] = ldg_nt(sp + k);
+      sc[j] = ldg(sp + k);
 #pragma unroll
       for (int m = 0; m < MR; ++m) xv[m][j] = ldg(a.x + (size_t)min(m, a.M - 1) * a.ldx + k);
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      if (k0 + kT * j >= K) break;
-      const bool ok = k0 + tid + kT * j < K;
+      if (!EXACT && k0 + T * j >= K) break;
+      const bool ok = EXACT || k0 + tid + T * j < K;
       float f[16];
       unpack16(w[j], f);
 #pragma unroll
@@ -73,11 +111,12 @@ __global__ __launch_bounds__(kT) void mvp_kernel(const MvpArgs a) {
       }
     }
   }
-  // wave: each lane ends with the wave's full sum of column lane / 4
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    const float v = fold_rows<kP>(acc[m], lane);
-    if ((lane & 3) == 0) red[wid][m][lane >> 2] = v;
+    float o[4];
+    fold16(acc[m], o);
+    if ((lane & 15) == 0)
+      *reinterpret_cast<float4*>(&red[wid][m][4 * (lane >> 4)]) = make_float4(o[0], o[1], o[2], o[3]);
   }
   __syncthreads();
   if (tid < MR * kP) {
@@ -85,10 +124,30 @@ __global__ __launch_bounds__(kT) void mvp_kernel(const MvpArgs a) {
     if (m < a.M) {
       float v = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < kNW; ++w2) v += red[w2][m][c];
+      for (int w2 = 0; w2 < NW; ++w2) v += red[w2][m][c];
       a.y[(size_t)m * a.ldy + panel * kP + c] = v;
     }
   }
+}
+
+template <int T, int MR, int J, bool EXACT>
+void launch_one(const MvpArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((mvp_kernel<T, MR, J, EXACT>), dim3(a.N / kP), dim3(T), 0, st, a);
+}
+
+// The first J of the list that splits K into exactly as many full passes of T*J rows as the
+// generic kernel (J = Jmax, the list's first entry) needs: an exact kernel with no more passes.
+// Otherwise the generic kernel.
+template <int T, int MR, int Jmax, int J, int... Js>
+void launch_pick(const MvpArgs& a, hipStream_t st) {
+  const int passes = (a.K + T * Jmax - 1) / (T * Jmax);
+  if (a.K % (T * J) == 0 && a.K / (T * J) == passes) launch_one<T, MR, J, true>(a, st);
+  else if constexpr (sizeof...(Js) > 0) launch_pick<T, MR, Jmax, Js...>(a, st);
+  else launch_one<T, MR, Jmax, false>(a, st);
+}
+template <int T, int MR, int Jmax, int... Js>
+void launch_exact(const MvpArgs& a, hipStream_t st) {
+  launch_pick<T, MR, Jmax, Jmax, Js...>(a, st);
 }
 
 }  // namespace
@@ -99,12 +158,15 @@ int mvp_launch(const int8_t* q, const float* s, int32_t K, int32_t N, const floa
   if (K < 1 || N < 64 || (N % 64) != 0) return fail(Q35_E_SHAPE, "q8_gemv (panel): N must be a positive multiple of 64");
   if (M < 1 || M > 8) return fail(Q35_E_SHAPE, "q8_gemv (panel): M in [1, 8] per launch");
   if ((reinterpret_cast<uintptr_t>(q) & 15) != 0) return fail(Q35_E_ALIGN, "q8_gemv (panel): q not 16-byte aligned");
-  MvpArgs a{q, s, x, y, K, N, M, ldx, ldy};
-  const dim3 grid(N / kP), block(kT);
-  if (M == 1) hipLaunchKernelGGL((mvp_kernel<1, 16>), grid, block, 0, st, a);
-  else if (M == 2) hipLaunchKernelGGL((mvp_kernel<2, 8>), grid, block, 0, st, a);
-  else if (M <= 4) hipLaunchKernelGGL((mvp_kernel<4, 4>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((mvp_kernel<8, 4>), grid, block, 0, st, a);
+  const int npanel = N / kP;
+  MvpArgs a{q, s, x, y, K, N, M, ldx, ldy, (npanel % 32) == 0 ? 1 : 0};
+  // M = 1: 512 threads, all of K (<= 8192, in one pass) in flight; M > 1: 256-thread blocks (the
+  // accumulators take more registers, and two blocks per CU keep every panel of a 6144-wide
+  // matrix resident).  The first J of each list that divides K / T gives an exact kernel.
+  if (M == 1) launch_exact<512, 1, 16, 12, 8, 6, 4, 3, 2, 1>(a, st);
+  else if (M == 2) launch_exact<256, 2, 8, 6, 4, 3, 2, 1>(a, st);
+  else if (M <= 4) launch_exact<256, 4, 8, 6, 4, 3, 2, 1>(a, st);
+  else launch_exact<256, 8, 4, 3, 2, 1>(a, st);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -65,6 +65,10 @@ class Q8FTensor:
             assert shape is not None and q.dim() == 3 and q.shape[2] == 256 and scale.shape == q.shape[:2] + (4,)
             self.rows, self.cols = shape
             assert q.shape[:2] == ((self.cols + 255) // 256, self.rows), (q.shape, shape)
+        elif layout == L.Q35_KN_PANEL:
+            assert shape is not None and q.dim() == 3 and q.shape[2] == 16
+            self.rows, self.cols = shape
+            assert q.shape[:2] == (self.cols // 16, self.rows) and scale.shape == (self.cols // 64, self.rows)
         else:
             assert q.dim() == 2 and scale.shape == (q.shape[0], q.shape[1] // 64), (scale.shape, q.shape)
             self.rows, self.cols = q.shape
@@ -97,6 +101,18 @@ class Q8FTensor:
         nt = (N + 255) // 256
         return Q8FTensor(torch.from_numpy(qt.reshape(nt, K, 256)).to(self.q.device),
                          torch.from_numpy(st.reshape(nt, K, 4)).to(self.q.device), L.Q35_KN_TILED, (K, N))
+
+    def panel(self):
+        """Q35_KN -> Q35_KN_PANEL copy, packed on the host through q35_q8f_pack_kn_panel."""
+        assert self.layout == L.Q35_KN
+        K, N = self.rows, self.cols
+        q = np.ascontiguousarray(self.q.cpu().numpy())
+        s = np.ascontiguousarray(self.scale.cpu().numpy())
+        qp = np.empty((N // 16, K, 16), dtype=np.int8)
+        sp = np.empty((N // 64, K), dtype=np.float32)
+        L.check(L.lib().q35_q8f_pack_kn_panel(q.ctypes.data, s.ctypes.data, K, N, qp.ctypes.data, sp.ctypes.data))
+        return Q8FTensor(torch.from_numpy(qp).to(self.q.device), torch.from_numpy(sp).to(self.q.device),
+                         L.Q35_KN_PANEL, (K, N))
 
 
 def _rows(x, k):

@@ -69,6 +69,48 @@ def test_q8_gemv_kn_tiled_odd_shapes(N, K, M):
     assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
 
 
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("N,K", C1_SHAPES)
+def test_q8_gemv_kn_panel_projection_shapes(N, K, M):
+    print(f"[gemv_kn panel] N={N} K={K} M={M}", flush=True)
+    W = q8(1000 + N + K, K, N)
+    x = normal(7, (M, K))
+    y = host(q35.q8_gemv(dev(x), q8_dev(W, q35.Q35_KN).panel()))
+    assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
+
+
+@pytest.mark.parametrize("N,K,M", [(64, 64, 1), (192, 100, 3), (320, 48, 2), (1024, 16, 8), (64, 4096, 5),
+                                   (256, 513, 13), (128, 9000, 1), (512, 8193, 2), (64, 1, 4), (131072, 64, 1)])
+def test_q8_gemv_kn_panel_odd_shapes(N, K, M):
+    """K not a multiple of the block's 512 rows, K past one pass of rows in flight (> 8192 at M=1,
+    > 4096 at M=2), a single row, and M spanning several launches of 8 rows."""
+    print(f"[gemv_kn panel odd] N={N} K={K} M={M}", flush=True)
+    W = q8(3000 + N + K, K, N, sigma=1.0)
+    x = normal(9, (M, K))
+    y = host(q35.q8_gemv_partial_sum(dev(x), q8_dev(W, q35.Q35_KN).panel()))
+    assert y.shape == (M, N)
+    assert rel_l2(y, O.gemv_kn(x, W)) <= TOL
+
+
+def test_q8_gemv_layouts_deterministic_and_reusable():
+    """Repeated calls give bit-identical outputs in every KN layout (fixed summation orders;
+    the split-K accumulators and tile counters are left zero by each call, so a workspace is
+    reused), and one-hot inputs select exact dequantised rows."""
+    N, K = 2048, 6144
+    W = q8(77, K, N, sigma=1.0)  # |q * scale| >= 2^-9: exact on the 2^-32 fixed-point grid too
+    x = dev(normal(78, (3, K)))
+    for lay in ("kn", "tiled", "panel"):
+        Wd = q8_dev(W, q35.Q35_KN)
+        Wd = Wd.tiled() if lay == "tiled" else (Wd.panel() if lay == "panel" else Wd)
+        a = host(q35.q8_gemv(x, Wd))
+        b = host(q35.q8_gemv(x, Wd))
+        np.testing.assert_array_equal(a, b, err_msg=lay)
+        e = np.zeros((1, K), np.float32)
+        e[0, 4321] = 1.0
+        row = host(q35.q8_gemv(dev(e), Wd))[0]
+        np.testing.assert_array_equal(row, W.q[4321].astype(np.float32) * np.repeat(W.s[4321], 64), err_msg=lay)
+
+
 @pytest.mark.parametrize("N,K,M", [(1, 64, 1), (17, 128, 2), (33, 1088, 3), (100, 8192, 1), (4097, 6144, 8)])
 def test_q8_gemv_nk_odd_shapes(N, K, M):
     print(f"[gemv_nk odd] N={N} K={K} M={M}", flush=True)
