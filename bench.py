@@ -1,20 +1,24 @@
 #!/usr/bin/env python3
 """Decode benchmark: greedy tok/s at bs=1 on the Qwen3.5-2B-shaped hybrid decoder (Q8F weights,
-seeded random init), plus the Q8F matvec bandwidth against the 8 TB/s HBM roofline.
+seeded random init), plus per-kernel HBM rates against the 8 TB/s roofline for the Q8F matvec at
+every decode projection shape (M = 1 and 8), the Gated DeltaNet decode step (B = 1, 32) and the
+gated GQA decode attention (B = 1, 16; context 1k / 8k / 32k), and the CPU restatement of the
+reference path timed on this host.
 
-Workload: 24 layers (18 Gated DeltaNet + 6 gated GQA), hidden 2048, FFN 6144, vocab 248320,
-tied embeddings, random-init weights N(0, 0.02) quantised to Q8F, seed 0; a 512-token uniform
-random prompt is fed through the decode step, then W untimed and K timed greedy decode steps.  A
-"step" is one token through the whole model (embedding -> 24 layers -> final norm -> lm_head ->
-argmax) with weights and caches resident in HBM, run by the persistent step kernel (--chunk steps
-per launch; each step's argmax feeds the next step on the device).
+Workload of the headline number: 24 layers (18 Gated DeltaNet + 6 gated GQA), hidden 2048, FFN
+6144, vocab 248320, tied embeddings, random-init weights N(0, 0.02) quantised to Q8F, seed 0; a
+--prompt-token uniform random prompt is fed through the decode step, then --warmup untimed and
+--steps timed greedy decode steps.  A step is one token through the whole model (embedding ->
+24 layers -> final norm -> lm_head -> argmax) with weights and caches resident in HBM, run by the
+persistent step kernel in launches of at most --chunk steps (each step's argmax feeds the next on
+the device).  Exactly --steps steps are timed and exactly --warmup run before them.
 
 Prints one JSON line.  Only one GPU is used; --gpus N > 1 exits with a message.
 """
 import argparse
-import ctypes
 import json
 import os
+import platform
 import sys
 import time
 
@@ -24,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 PUBLISHED_TOKS = 43.0  # README.md:11-13,22 of the reference (RTX 4060 Ti, wgpu, real weights)
+ROTATE_BYTES = 512 << 20  # distinct copies per measured shape: more than the 256 MB last-level cache
 
 
 def q8_bytes(N, K, M):
@@ -49,72 +54,219 @@ def step_bytes(d, ctx):
     return mv + state + kv
 
 
-def time_lm_head(torch, q35, m, d, reps):
-    """Average duration of the lm_head Q8F matvec (kernels.rs q8_lm_head) with HIP events on the
-    stream it is launched on, using the model's tied embedding table."""
-    lib = q35.lib()
-    eq, _ = m.tensor_ptr("embed_tokens.q")
-    es, _ = m.tensor_ptr("embed_tokens.scale")
-    hv = torch.randn(d.hidden, device="cuda")
-    h = hv.data_ptr()
-    W = q35._lib.Q8F(eq, es, d.vocab, d.hidden, q35.Q35_NK)
-    logits = torch.empty(d.vocab, dtype=torch.float32, device="cuda")
-    s = torch.cuda.current_stream()
-    for _ in range(3):
-        q35._lib.check(lib.q35_q8_lm_head(h, 1, W, logits.data_ptr(), s.cuda_stream))
+def gdn_bytes(B, nh=16, dk=128, dv=128):
+    """Bytes the Gated DeltaNet decode step moves for B sequences: recurrent state read + write,
+    the q|k|v projection input, conv state read + write, beta|g, the core output, and the shared
+    conv weights.  (The survey's C2 figure also counts the z input and the out-projection input
+    of the layer, which belong to the next kernel here.)"""
+    conv = 2 * nh * dk + nh * dv
+    return B * (2 * nh * dk * dv * 4 + conv * 4 + 2 * conv * 3 * 4 + 2 * nh * 4 + nh * dv * 4) + conv * 4 * 4
+
+
+def attn_bytes(B, T, nh=8, nkv=2, hd=256):
+    """Bytes of one gated GQA decode-attention call: the T cached K and V rows of every kv head,
+    the q|gate, k, v inputs, the appended K/V row, the output."""
+    return B * (T * 2 * nkv * hd * 4 + (2 * nh * hd + 2 * nkv * hd) * 4 + 2 * nkv * hd * 4 + nh * hd * 4)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def launch_plan(n, chunk):
+    """Launch sizes that run exactly n steps, at most chunk per launch."""
+    return [chunk] * (n // chunk) + ([n % chunk] if n % chunk else [])
+
+
+def per_call_us(torch, st, fn, ncalls, reps=3, warm=1):
+    """Average time per call of fn (which issues ncalls back-to-back calls on stream st), from HIP
+    events recorded on st around `reps` repetitions.  Includes each launch's issue gap."""
+    for _ in range(warm):
+        fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
+    e0.record(st)
     for _ in range(reps):
-        q35._lib.check(lib.q35_q8_lm_head(h, 1, W, logits.data_ptr(), s.cuda_stream))
-    e1.record(s)
+        fn()
+    e1.record(st)
     e1.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / reps  # us
+    return e0.elapsed_time(e1) * 1e3 / (reps * ncalls)
 
 
-def matvec_sweep(torch, q35, m, d, reps=4):
-    """Per-shape KN matvec rate over the model's own weights, rotating through all layers so the
-    working set (> 256 MB) exceeds the MALL; events around back-to-back launches (so the figure
-    includes the ~1.6 us launch gap of each kernel)."""
+def rate(nbytes, us):
+    gbs = nbytes / us / 1e3
+    return {"us_per_call": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def matvec_sweep(torch, q35, st):
+    """Q8F matvec (q8_gemv / q8_gemv_partial_sum, kernels.rs:681-700) at every decode projection
+    shape, M = 1 and 8, in the panel layout (one launch, no workspace), cycling through distinct
+    weight copies totalling >= 512 MB so every call streams from HBM; and the lm_head
+    (q8_lm_head, kernels.rs:724-731) over the tied [V][D] table."""
+    L = q35._lib
     lib = q35.lib()
-    shapes = {
-        "mlp.gate_proj [6144x2048]": ("mlp.gate_proj", d.ffn, d.hidden, range(d.n_layers)),
-        "mlp.down_proj [2048x6144]": ("mlp.down_proj", d.hidden, d.ffn, range(d.n_layers)),
-        "linear_attn.in_proj_qkv [6144x2048]": ("linear_attn.in_proj_qkv", 6144, d.hidden,
-                                                 [l for l in range(d.n_layers) if (l + 1) % 4]),
-        "linear_attn.out_proj [2048x2048]": ("linear_attn.out_proj", d.hidden, 2048,
-                                              [l for l in range(d.n_layers) if (l + 1) % 4]),
-        "self_attn.q_proj [4096x2048]": ("self_attn.q_proj", 4096, d.hidden,
-                                         [l for l in range(d.n_layers) if (l + 1) % 4 == 0]),
-        "self_attn.k_proj [512x2048]": ("self_attn.k_proj", 512, d.hidden,
-                                        [l for l in range(d.n_layers) if (l + 1) % 4 == 0]),
-    }
-    x = torch.randn(max(d.hidden, d.ffn), device="cuda")
-    y = torch.empty(max(d.ffn, 8192), device="cuda")
-    ws = q35.workspace(1 << 24, key="bench_gemv")
-    s = torch.cuda.current_stream()
+    sh = st.cuda_stream
+    shapes = [("gate_proj / up_proj / in_proj_qkv", 6144, 2048), ("down_proj", 2048, 6144),
+              ("q_proj (query|gate)", 4096, 2048), ("k_proj / v_proj", 512, 2048), ("o (config [2048x4096])", 2048, 4096),
+              ("in_proj_qkvz (fused)", 8192, 2048), ("out_proj / o_proj / in_proj_z", 2048, 2048)]
     out = {}
-    for label, (name, N, K, layers) in shapes.items():
-        descs = []
-        for l in layers:
-            q, _ = m.tensor_ptr(f"layers.{l}.{name}.q")
-            sc, _ = m.tensor_ptr(f"layers.{l}.{name}.scale")
-            descs.append(q35._lib.Q8F(q, sc, K, N, q35.Q35_KN_TILED))
-        for W in descs:
-            q35._lib.check(lib.q35_q8_gemv(x.data_ptr(), 1, W, y.data_ptr(), ws.data_ptr(), ws.numel(), s.cuda_stream))
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(reps):
-            for W in descs:
-                q35._lib.check(lib.q35_q8_gemv(x.data_ptr(), 1, W, y.data_ptr(), ws.data_ptr(), ws.numel(),
-                                               s.cuda_stream))
-        e1.record(s)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * len(descs))
-        gbs = q8_bytes(N, K, 1) / us / 1e3
-        out[label] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                      "working_set_MB": round(len(descs) * q8_bytes(N, K, 1) / 1e6, 1)}
+    for label, N, K in shapes:
+        wb = K * N + K * N // 16
+        R = max(2, -(-ROTATE_BYTES // wb))
+        copies = []
+        for _ in range(R):
+            q = torch.randint(-127, 128, (N // 16, K, 16), dtype=torch.int8, device="cuda")
+            s = torch.rand((N // 64, K), device="cuda") * 1e-3
+            copies.append((q, s, L.Q8F(q.data_ptr(), s.data_ptr(), K, N, L.Q35_KN_PANEL)))
+        row = {"N": N, "K": K, "copies": R}
+        for M in (1, 8):
+            x = torch.randn(M, K, device="cuda")
+            y = torch.empty(M, N, device="cuda")
+
+            def run():
+                for _, _, W in copies:
+                    L.check(lib.q35_q8_gemv(x.data_ptr(), M, W, y.data_ptr(), None, 0, sh))
+            row[f"M{M}"] = rate(q8_bytes(N, K, M), per_call_us(torch, st, run, R))
+        out[f"{label} [{N}x{K}]"] = row
+        del copies
+        torch.cuda.empty_cache()
+    V, D = 248320, 2048
+    q = torch.randint(-127, 128, (V, D), dtype=torch.int8, device="cuda")
+    s = torch.rand((V, D // 64), device="cuda") * 1e-3
+    E = L.Q8F(q.data_ptr(), s.data_ptr(), V, D, L.Q35_NK)
+    row = {"N": V, "K": D, "copies": 1, "layout": "NK (tied embedding table)"}
+    for M in (1, 8):
+        h = torch.randn(M, D, device="cuda")
+        lg = torch.empty(M, V, device="cuda")
+
+        def run():
+            L.check(lib.q35_q8_lm_head(h.data_ptr(), M, E, lg.data_ptr(), sh))
+        row[f"M{M}"] = rate(q8_bytes(V, D, M), per_call_us(torch, st, run, 1, reps=20))
+    out[f"lm_head [{V}x{D}]"] = row
+    del q, s
+    torch.cuda.empty_cache()
     return out
+
+
+def gdn_leg(torch, q35, st):
+    """Gated DeltaNet decode step (causal conv update + recurrent gated delta rule,
+    text_modules.rs:134-162,365-443) through q35_gated_delta_rule_decode, 16 heads of 128 x 128,
+    B = 1 and 32, cycling through distinct states totalling >= 512 MB; called through the C ABI
+    with preallocated buffers (no per-call host allocation)."""
+    lib, sh = q35.lib(), st.cuda_stream
+    out = {}
+    nh, dk, dv = 16, 128, 128
+    conv = 2 * nh * dk + nh * dv
+    conv_w = torch.randn(conv, 4, device="cuda") * 0.02
+    for B in (1, 32):
+        per = B * (nh * dk * dv + conv * 3) * 4
+        R = max(2, -(-ROTATE_BYTES // per))
+        sets = []
+        for _ in range(R):
+            sets.append((torch.randn(B, conv, device="cuda"),
+                         torch.cat([torch.sigmoid(torch.randn(B, nh, device="cuda")),
+                                    -torch.nn.functional.softplus(torch.randn(B, nh, device="cuda"))], 1),
+                         torch.randn(B, conv, 3, device="cuda"),
+                         torch.randn(B, nh, dk, dv, device="cuda") * 0.1,
+                         torch.empty(B, nh * dv, device="cuda")))
+
+        def run():
+            for mixed, bg, cs, S, o in sets:
+                q35._lib.check(lib.q35_gated_delta_rule_decode(mixed.data_ptr(), B, bg.data_ptr(), cs.data_ptr(),
+                                                               conv_w.data_ptr(), S.data_ptr(), o.data_ptr(), nh, dk,
+                                                               dv, None, 0, sh))
+        out[f"B{B}"] = dict(rate(gdn_bytes(B, nh, dk, dv), per_call_us(torch, st, run, R)), copies=R)
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
+def attn_leg(torch, q35, st):
+    """Gated GQA decode attention core (q/k RMSNorm, partial RoPE, KV append, softmax(qK^T/16)V,
+    sigmoid gate; text_modules.rs:860-936) through q35_attention_core_decode: 8 query heads, 2 kv
+    heads, head_dim 256, B = 1 and 16, the new token at position T-1 of a T-token f32 cache;
+    called through the C ABI with preallocated buffers and workspace."""
+    import ctypes
+    d = q35.dims_2b()
+    lib, sh = q35.lib(), st.cuda_stream
+    nh, nkv, hd = d.attn_heads, d.kv_heads, d.head_dim
+    out = {}
+    for B in (1, 16):
+        for T in (1024, 8192, 32768):
+            per = 2 * B * nkv * T * hd * 4
+            R = max(1, -(-ROTATE_BYTES // per))
+            cs, sn = q35.rope_tables(d, T)
+            cs_d, sn_d = torch.from_numpy(cs).cuda(), torch.from_numpy(sn).cuda()
+            qw, kw = torch.randn(hd, device="cuda") * 0.1, torch.randn(hd, device="cuda") * 0.1
+            pos = torch.full((B,), T - 1, dtype=torch.int32, device="cuda")
+            ws = torch.zeros(lib.q35_layer_ws_bytes(ctypes.byref(d), B, T), dtype=torch.uint8, device="cuda")
+            o = torch.empty(B, nh * hd, device="cuda")
+            sets = [(torch.randn(B, nkv, T, hd, device="cuda"), torch.randn(B, nkv, T, hd, device="cuda"),
+                     torch.randn(B, nh * 2 * hd, device="cuda"), torch.randn(B, nkv * hd, device="cuda"),
+                     torch.randn(B, nkv * hd, device="cuda")) for _ in range(R)]
+
+            def run():
+                for kc, vc, qg, kn, vn in sets:
+                    q35._lib.check(lib.q35_attention_core_decode(
+                        ctypes.byref(d), qg.data_ptr(), kn.data_ptr(), vn.data_ptr(), nkv * hd, B, qw.data_ptr(),
+                        kw.data_ptr(), kc.data_ptr(), vc.data_ptr(), T, pos.data_ptr(), cs_d.data_ptr(),
+                        sn_d.data_ptr(), o.data_ptr(), ws.data_ptr(), ws.numel(), sh))
+            us = per_call_us(torch, st, run, R, reps=3 if T < 32768 else 5)
+            q35._lib.check(lib.q35_workspace_status(ws.data_ptr(), sh))
+            out[f"B{B}_T{T}"] = dict(rate(attn_bytes(B, T, nh, nkv, hd), us), copies=R)
+            del sets, ws
+            torch.cuda.empty_cache()
+    return out
+
+
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(q35, d, ctx, budget_s=20.0):
+    """CPU restatement of the reference path on this host: the 2B-shaped model, every Q8F matvec
+    as Burn's ndarray path runs it (dequantise the whole int8 matrix to f32, then an f32 GEMV with
+    f32 accumulation), the rest as the oracle restates text_modules.rs; one decode step at the
+    GPU line's context (the cache length is set directly; caches hold zeros).  Timed at 1 thread
+    and at every core of the host."""
+    import oracle as O
+    t0 = time.time()
+    max_steps = 64
+    ref = O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, 0, name, n), ctx + max_steps + 8)
+    build_s = time.time() - t0
+    ncores = O.get_threads()
+    O.set_f32_dequant(True)
+    try:
+        res = {}
+        for threads in (ncores, 1):
+            O.set_threads(threads)
+            ref.set_position(ctx)
+            tok = 11
+            if threads == ncores:
+                tok, _, _ = ref.step(tok)  # warm-up (dequantisation buffer, page faults)
+            n, t1 = 0, time.time()
+            while True:
+                tok, _, _ = ref.step(tok)
+                n += 1
+                if time.time() - t1 >= (budget_s if threads > 1 else budget_s / 2) or n >= max_steps:
+                    break
+            res[threads] = (n, time.time() - t1)
+        O.set_threads(ncores)
+    finally:
+        O.set_f32_dequant(False)
+    na, ta = res[ncores]
+    n1, t1s = res[1]
+    return {"value": round(na / ta, 4), "unit": "tok/s", "cores": ncores, "kind": "port",
+            "value_1_thread": round(n1 / t1s, 4), "cpu": cpu_model_name(),
+            "sample": f"{na} greedy decode steps on {ncores} threads and {n1} on 1 thread, full 2B-shaped model "
+                      f"at context {ctx}; each Q8F matvec dequantises its whole matrix to f32 and runs an f32 "
+                      f"GEMV (oracle/oracle.c, OpenMP, x86-64-v3); model built in {build_s:.0f}s (not timed)"}
 
 
 def copy_calibration():
@@ -131,35 +283,12 @@ def copy_calibration():
     print("copied 3 x 1 GiB", flush=True)
 
 
-# HBM traffic of one step_kernel<2> launch of 64 steps in this workload: FETCH_SIZE + WRITE_SIZE
-# per dispatch from two rocprofv3 --pmc passes over `bench.py --no-cpu --no-sweep`, scaled by the
-# counters' reading for a 1 GiB copy (`bench.py --copy-calibration`): x2.0 and x1.0.  Measured for
-# the kernel at the commit that recorded it; profiles/step_kernel_decode_2b_traffic.md has the
-# commands and the per-dispatch values.
-STEP_TRAFFIC_PER_LAUNCH = 139.72e9
-
-
-def cpu_baseline(q35, d, prompt, budget_s=20.0):
-    """Oracle (CPU restatement) decode tok/s on the host cores, bounded sample."""
-    import oracle as O
-    t0 = time.time()
-    ref = O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, 0, name, n), 64)
-    build_s = time.time() - t0
-    tok = int(prompt[0])
-    for t in prompt[:2]:
-        tok, _, _ = ref.step(int(t))
-    t1 = time.time()
-    tok, _, _ = ref.step(tok)
-    one = time.time() - t1
-    n = max(2, min(32, int(budget_s / max(one, 1e-3))))
-    t1 = time.time()
-    for _ in range(n):
-        tok, _, _ = ref.step(tok)
-    el = time.time() - t1
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(n / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} greedy decode steps of the full 2B-shaped model after a 3-token prefill, "
-                      f"oracle/oracle.c (OpenMP, x86-64-v3), weights built in {build_s:.0f}s (not timed)"}
+# HBM traffic of one step_kernel<2> launch of 64 decode steps at context 576-1088 of this workload:
+# FETCH_SIZE + WRITE_SIZE per dispatch from two rocprofv3 --pmc passes over
+# `bench.py --steps 512 --warmup 64 --no-cpu --no-sweep --no-layers`, each scaled by what the
+# counter reads for a 1 GiB copy (`bench.py --copy-calibration`).  A constant measured on the
+# kernel at the commit named in profiles/step_kernel_decode_2b_traffic.md, not in this run.
+STEP_TRAFFIC_PER_64 = 139.72e9
 
 
 def main():
@@ -169,9 +298,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--chunk", type=int, default=64, help="most decode steps per persistent-kernel launch")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline sample budget (all cores)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape matvec sweep")
-    ap.add_argument("--chunk", type=int, default=64, help="decode steps per persistent-kernel launch")
+    ap.add_argument("--no-layers", action="store_true", help="skip the DeltaNet and attention legs")
     ap.add_argument("--readback", action="store_true",
                     help="also time one launch per token with a host readback each step (main.rs loop)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -184,6 +315,9 @@ def main():
         print("bench.py: this build measures one GPU only (the decode path is single-GPU; multi-GPU is "
               "design-only), so --gpus must be 1", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0 or args.prompt < 1 or args.chunk < 1:
+        print("bench.py: need --steps >= 1, --warmup >= 0, --prompt >= 1, --chunk >= 1", file=sys.stderr)
+        sys.exit(2)
 
     import numpy as np
     import torch
@@ -192,10 +326,9 @@ def main():
     torch.cuda.set_device(0)
     d = q35.dims_2b()
     chunk = args.chunk
-    n_pre = -(-args.prompt // chunk) * chunk
-    n_warm = -(-args.warmup // chunk) * chunk
-    n_timed = -(-args.steps // chunk) * chunk
+    n_pre, n_warm, n_timed = args.prompt, args.warmup, args.steps
     tmax = n_pre + n_warm + n_timed + 8
+    log(f"building the 2B-shaped model (tmax {tmax})")
     t0 = time.time()
     m = q35.TextForCausalLM(d, seed=args.seed, tmax=tmax)
     create_s = time.time() - t0
@@ -205,62 +338,76 @@ def main():
     torch.cuda.set_stream(st)
     sh = st.cuda_stream
 
-    # The prompt goes through the decode step; every persistent launch below is `chunk` steps, so
-    # the kernel's average launch duration in a profile of this command is the timed one.
+    # The prompt goes through the decode step, at most `chunk` steps per persistent launch.
+    log(f"prompt {n_pre} tokens, warm-up {n_warm}, timed {n_timed} steps in launches {launch_plan(n_timed, chunk)}")
     t0 = time.time()
-    m.generate(prompt[:chunk], 0, mode="persistent", stream=sh)
-    for c0 in range(chunk, n_pre, chunk):
-        m.generate(prompt[c0:c0 + chunk], 0, mode="persistent", stream=sh)
+    c0 = 0
+    for n in launch_plan(n_pre, chunk):
+        m.generate(prompt[c0:c0 + n], 0, mode="persistent", stream=sh)
+        c0 += n
     m.check(stream=sh)
     prefill_s = time.time() - t0
-    for _ in range(n_warm // chunk):
-        m.decode(chunk, mode="persistent", stream=sh)
+    for n in launch_plan(n_warm, chunk):
+        m.decode(n, mode="persistent", stream=sh)
     m.check(stream=sh)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_timed // chunk)]
+    plan = launch_plan(n_timed, chunk)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in plan]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for e0, e1 in ev:
+    for (e0, e1), n in zip(ev, plan):
         e0.record(st)
-        m.decode(chunk, mode="persistent", stream=sh)
+        m.decode(n, mode="persistent", stream=sh)
         e1.record(st)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     m.check(stream=sh)
     launch_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
-    kern_s = sum(launch_ms) * 1e-3
     toks = n_timed / el
     ms = el * 1e3 / n_timed
     ctx0 = n_pre + n_warm
-    bytes_timed = sum(step_bytes(d, ctx0 + i + 1) for i in range(n_timed))
-    bytes_per_launch = bytes_timed / len(ev)
-    avg_launch_us = kern_s * 1e6 / len(ev)
-    achieved = bytes_per_launch / (avg_launch_us * 1e-6) / 1e9
+    launch_bytes, c = [], ctx0
+    for n in plan:
+        launch_bytes.append(sum(step_bytes(d, c + i + 1) for i in range(n)))
+        c += n
+    achieved = sum(launch_bytes) / (sum(launch_ms) * 1e-3) / 1e9
     hist = m.tensor("hist", np.int32)[:ctx0 + n_timed]
+    full = [i for i, n in enumerate(plan) if n == chunk]
+    traffic = None
+    if chunk == 64 and full:
+        traffic = STEP_TRAFFIC_PER_64
 
     toks_readback = None
     if args.readback:  # main.rs semantics: one launch per token, token read back and synced each step
         m.reset()
-        m.generate(prompt[:chunk], 0, mode="persistent", stream=sh)
-        _, dec_s = m.generate(prompt[chunk:chunk + 1], 64, mode="persistent", readback_each=True, stream=sh)
+        m.generate(prompt[:min(chunk, n_pre)], 0, mode="persistent", stream=sh)
+        _, dec_s = m.generate(prompt[:1], 64, mode="persistent", readback_each=True, stream=sh)
         toks_readback = 64 / dec_s
-
-    lm_us = time_lm_head(torch, q35, m, d, reps=50)
-    lm_bytes = q8_bytes(d.vocab, d.hidden, 1)
-    lm_gbs = lm_bytes / lm_us / 1e3
-    sweep = None if args.no_sweep else matvec_sweep(torch, q35, m, d)
     m.close()
+
+    if not args.no_sweep:
+        log("matvec sweep")
+    sweep = None if args.no_sweep else matvec_sweep(torch, q35, st)
+    gdn = attn = None
+    if not args.no_layers:
+        log("gated delta rule decode leg")
+        gdn = gdn_leg(torch, q35, st)
+        log("attention decode leg")
+        attn = attn_leg(torch, q35, st)
+    q35.release_workspaces()
+    torch.cuda.synchronize()
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(q35, d, prompt)
+        log("CPU baseline")
+        cpu = cpu_baseline(q35, d, ctx0, args.cpu_seconds)
 
     line = {
         "metric": "decode tok/s bs=1 Qwen3.5-2B-shape Q8F; matvec HBM GB/s vs 8 TB/s peak",
         "value": round(toks, 2),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": n_timed,
+        "warmup": n_warm,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -271,22 +418,28 @@ def main():
                                "GQA layers, hidden 2048, FFN 6144, vocab 248320, tied Q8F embeddings)",
                    "batch": 1, "prompt_len": n_pre, "ctx_range": [ctx0, ctx0 + n_timed],
                    "weights": "int8 Q8F per-64 f32 scales",
-                   "launch": f"persistent step kernel, {chunk} steps per launch, grid {grid}x512"},
-        "roofline": {"kernel": f"step_kernel<2>: persistent decode step, {chunk} tokens per launch",
+                   "launch": f"persistent step kernel, steps per launch {plan}, grid {grid}x512"},
+        "roofline": {"kernel": "step_kernel<2>: persistent decode step",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": STEP_TRAFFIC_PER_LAUNCH if chunk == 64 else None,
-                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_us, 1)},
-        "lm_head_kernel": {"kernel": "nk_kernel<1,2>: standalone Q8F lm_head 248320x2048 (kernels.rs q8_lm_head)",
-                           "achieved_GBs": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-                           "avg_launch_us": round(lm_us, 2)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_note": "FETCH_SIZE+WRITE_SIZE per 64-step launch, calibrated; a constant measured "
+                                     "at the commit in profiles/, not in this run" if traffic else None,
+                     "steps_per_launch": plan[0],
+                     "bytes_per_launch": int(np.mean([launch_bytes[i] for i in full])) if full else int(launch_bytes[0]),
+                     "avg_launch_us": round(1e3 * float(np.mean([launch_ms[i] for i in full])) if full
+                                            else 1e3 * launch_ms[0], 1)},
         "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
         "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
-        "prefill_tok_s_via_decode_step": round(args.prompt / prefill_s, 1),
+        "prefill_tok_s_via_decode_step": round(n_pre / prefill_s, 1),
         "model_build_s": round(create_s, 1),
-        "matvec_kn_sweep": sweep,
+        "matvec_sweep": sweep,
+        "matvec_sweep_note": "panel layout, per-call time from HIP events around back-to-back calls (includes each "
+                             "launch's issue gap); kernel-only durations are in profiles/matvec_c1.md",
+        "gated_delta_rule_decode": gdn,
+        "attention_core_decode": attn,
         "cpu_baseline": cpu,
-        "vs_baseline_note": "published ~43 tok/s is the reference's custom-kernel decode on an RTX 4060 Ti",
+        "vs_baseline_note": "published ~43 tok/s is the reference's custom-kernel decode with real weights on an "
+                            "RTX 4060 Ti (no MI355X figure is published)",
     }
     print(json.dumps(line), flush=True)
 

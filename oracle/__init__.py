@@ -86,6 +86,9 @@ def lib():
             "orc_attn_decode": (None, [P(Cfg), P(AttnW), c_vp, ctypes.c_int, c_vp, c_vp, ctypes.c_int, c_vp, c_vp]),
             "orc_mlp_decode": (None, [P(Cfg), P(MlpW), c_vp, ctypes.c_int, c_vp]),
             "orc_model_step": (c_i32, [P(Cfg), P(ModelW), P(CacheC), c_i32, c_vp, P(ctypes.c_double)]),
+            "orc_set_f32_dequant": (None, [ctypes.c_int]),
+            "orc_set_threads": (None, [ctypes.c_int]),
+            "orc_get_threads": (ctypes.c_int, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -165,6 +168,19 @@ def gate_proj(x, w_b, w_a, a_log, dt_bias):
     lib().orc_gate_proj(x.ctypes.data, x.size, w_b.ctypes.data, w_a.ctypes.data, a_log.ctypes.data,
                         dt_bias.ctypes.data, nh, out.ctypes.data)
     return out
+
+
+def set_f32_dequant(on):
+    """CPU-baseline timing path: Q8F matvecs dequantize the matrix to f32 and run an f32 GEMV."""
+    lib().orc_set_f32_dequant(1 if on else 0)
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+def get_threads():
+    return int(lib().orc_get_threads())
 
 
 def argmax(v):
@@ -365,7 +381,15 @@ class Model:
         arr = lambda xs: (c_vp * n)(*[(_p(x) if x is not None else None) for x in xs])
         self.cache = CacheC(arr(self.conv), arr(self.rec), arr(self.kc), arr(self.vc), tmax, 0)
 
+    def set_position(self, pos):
+        """Set the cache length (tokens already cached) without running them: the caches keep
+        whatever they hold.  Used to time a step at a given context; results are then not a
+        real continuation."""
+        self.cache.pos = int(pos)
+
     def step(self, token, want_logits=False):
+        if not 0 <= self.cache.pos < self.cache.tmax:
+            raise ValueError(f"oracle model: position {self.cache.pos} outside the cache of {self.cache.tmax} tokens")
         logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
         margin = ctypes.c_double(0.0)
         t = lib().orc_model_step(ctypes.byref(self.cfg), ctypes.byref(self.mw), ctypes.byref(self.cache), int(token),

@@ -10,6 +10,7 @@
  */
 #include "oracle.h"
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -50,12 +51,81 @@ int orc_gemv_num_splits(int in_dim, int out_dim) {
   return s;
 }
 
+/* ---- CPU-baseline timing path (not a checker): Burn's dequantize-then-f32-matmul --------
+ * With orc_set_f32_dequant(1) the two Q8F matvecs below stop being the double-accumulated
+ * checker and time the path the workload names for the CPU column: the whole int8 matrix is
+ * dequantised to an f32 copy (Burn materialises it per call; here into one reused buffer, so no
+ * page-fault cost is added), then an f32 GEMV with f32 accumulation, OpenMP over output columns.
+ * orc_set_threads sets the OpenMP thread count. */
+static int g_f32_dequant = 0;
+static float* g_wbuf = NULL;
+static size_t g_wcap = 0;
+void orc_set_f32_dequant(int on) { g_f32_dequant = on; }
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int orc_get_threads(void) { return omp_get_max_threads(); }
+
+static float* dequant_buf(size_t n) {
+  if (n > g_wcap) {
+    free(g_wbuf);
+    g_wbuf = (float*)malloc(n * sizeof(float));
+    g_wcap = g_wbuf ? n : 0;
+  }
+  return g_wbuf;
+}
+
+/* dequantize (rows x cols, blocks of 64 along cols) into an f32 matrix of the same shape */
+static void dequant_f32(orc_q8 W, float* out) {
+  const int R = W.rows, C = W.cols, nb = C / 64;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < R; ++r)
+    for (int c = 0; c < C; ++c) out[(size_t)r * C + c] = (float)W.q[(size_t)r * C + c] * W.s[(size_t)r * nb + c / 64];
+}
+
+static void gemv_kn_f32(const float* x, int M, orc_q8 W, float* y) {
+  const int K = W.rows, N = W.cols;
+  float* Wf = dequant_buf((size_t)K * N);
+  dequant_f32(W, Wf);
+  const int NT = 256, ntiles = (N + NT - 1) / NT;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int m = 0; m < M; ++m) {
+    for (int t = 0; t < ntiles; ++t) {
+      float acc[256];
+      const int n0 = t * NT, n1 = n0 + NT < N ? n0 + NT : N;
+      for (int n = n0; n < n1; ++n) acc[n - n0] = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const float xk = x[(size_t)m * K + k];
+        const float* wr = Wf + (size_t)k * N;
+        for (int n = n0; n < n1; ++n) acc[n - n0] += xk * wr[n];
+      }
+      for (int n = n0; n < n1; ++n) y[(size_t)m * N + n] = acc[n - n0];
+    }
+  }
+}
+
+static void gemv_nk_f32(const float* x, int M, orc_q8 W, float* y, double* y64) {
+  const int N = W.rows, K = W.cols;
+  float* Wf = dequant_buf((size_t)N * K);
+  dequant_f32(W, Wf);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int m = 0; m < M; ++m) {
+    for (int n = 0; n < N; ++n) {
+      const float* wr = Wf + (size_t)n * K;
+      const float* xm = x + (size_t)m * K;
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc += xm[k] * wr[k];
+      y[(size_t)m * N + n] = acc;
+      if (y64) y64[(size_t)m * N + n] = acc;
+    }
+  }
+}
+
 /* y[m][n] = sum_k x[m][k] * q[k][n] * s[k][n/64]   (KN layout, blocks along N).
  * Reference: kernels.rs:53-92 (q8_gemv), :103-165 (q8_gemv_partial_sum + reduction), the
  * Burn Linear dequant+matmul of the seq_len>1 branches.  rowdrop=1 reproduces the rows the
  * partial-sum kernel actually reads (kernels.rs:119-133: each split sums 8*floor(chunk/8)
  * rows), which skips rows whenever K/splits is not a multiple of 8. */
 void orc_q8_gemv_kn(const float* x, int M, orc_q8 W, float* y, int rowdrop) {
+  if (g_f32_dequant && !rowdrop) { gemv_kn_f32(x, M, W, y); return; }
   const int K = W.rows, N = W.cols, nb = N / 64;
   unsigned char* keep = (unsigned char*)malloc((size_t)K);
   for (int k = 0; k < K; ++k) keep[k] = 1;
@@ -92,6 +162,7 @@ void orc_q8_gemv_kn(const float* x, int M, orc_q8 W, float* y, int rowdrop) {
  * Reference: kernels.rs:251-291 (q8_lm_head over the tied embedding table) and the
  * prefill lm_head matmul model.rs:130-138.  y64 (optional) receives the double result. */
 void orc_q8_gemv_nk(const float* x, int M, orc_q8 W, float* y, double* y64) {
+  if (g_f32_dequant) { gemv_nk_f32(x, M, W, y, y64); return; }
   const int N = W.rows, K = W.cols, nb = K / 64;
 #pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m) {

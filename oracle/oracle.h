@@ -112,6 +112,11 @@ void orc_q8_gemv_nk(const float* x, int M, orc_q8 W, float* y, double* y64);
 void orc_embedding_lookup(orc_q8 table, const int32_t* ids, int n, float* out);
 void orc_gate_proj(const float* x, int in_dim, const float* w_b, const float* w_a,
                    const float* a_log, const float* dt_bias, int n_heads, float* out);
+/* CPU-baseline timing only: switch both Q8F matvecs to dequantize-the-matrix + f32 GEMV (f32
+ * accumulation) instead of the double-accumulated checker; set the OpenMP thread count. */
+void orc_set_f32_dequant(int on);
+void orc_set_threads(int n);
+int orc_get_threads(void);
 int32_t orc_argmax(const float* v, int64_t n);
 int32_t orc_argmax_reference_order(const float* v, int64_t n);
 int orc_gemv_num_splits(int in_dim, int out_dim);

@@ -38,11 +38,7 @@ int check_kn(const q35_q8f& W, const char* what) {
 }
 
 // NK rows of x handled per launch: LDS holds MR*K floats.
-int nk_group(int K) {
-  int g = 8;
-  while (g > 1 && g * K > 12288) g /= 2;
-  return g;
-}
+int nk_group(int K) { return nk_max_rows(K); }
 
 MvSeg seg_of(const q35_q8f& W, fx_t* acc, int ldacc) {
   return MvSeg{W.q, W.scale, acc, W.cols, ldacc, W.layout == Q35_KN_TILED ? 1 : 0};

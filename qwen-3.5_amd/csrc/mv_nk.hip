@@ -23,7 +23,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxCpw = 8;        // 16-byte chunks per lane per row: K <= 8192
 constexpr int kMaxGrid = 2048;
-constexpr int kLdsFloats = 12288; // MR*K staged floats (48 KB)
+constexpr size_t kStaticLds = 256;  // the kernel's own shared variables, beside the staged x
 
 // rows per wave per step: 16 loads in flight per lane
 template <int CPW> constexpr int kRowsPerWave = CPW >= 8 ? 2 : (CPW >= 4 ? 4 : 8);
@@ -237,15 +237,42 @@ int nk_grid(int N, int K) {
   return nrb < kMaxGrid ? nrb : kMaxGrid;
 }
 
+// Shared memory one block may use on the current device (160 KB on gfx950), queried once per device.
+size_t lds_per_block() {
+  static size_t cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  if (!cache[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+    cache[dev] = (size_t)v;
+  }
+  return cache[dev];
+}
+
+template <int MR, int CPW>
+void launch_one(dim3 g, size_t lds, hipStream_t st, const NkArgs& a) {
+  if (lds > 65536)  // staging beyond 64 KB of dynamic LDS has to be allowed per kernel
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(nk_kernel<MR, CPW>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL((nk_kernel<MR, CPW>), g, dim3(kThreads), lds, st, a);
+}
+
 template <int MR>
 void launch_mr(int cpw, dim3 g, size_t lds, hipStream_t st, const NkArgs& a) {
-  if (cpw == 1) hipLaunchKernelGGL((nk_kernel<MR, 1>), g, dim3(kThreads), lds, st, a);
-  else if (cpw == 2) hipLaunchKernelGGL((nk_kernel<MR, 2>), g, dim3(kThreads), lds, st, a);
-  else if (cpw == 4) hipLaunchKernelGGL((nk_kernel<MR, 4>), g, dim3(kThreads), lds, st, a);
-  else hipLaunchKernelGGL((nk_kernel<MR, 8>), g, dim3(kThreads), lds, st, a);
+  if (cpw == 1) launch_one<MR, 1>(g, lds, st, a);
+  else if (cpw == 2) launch_one<MR, 2>(g, lds, st, a);
+  else if (cpw == 4) launch_one<MR, 4>(g, lds, st, a);
+  else launch_one<MR, 8>(g, lds, st, a);
 }
 
 }  // namespace
+
+int nk_max_rows(int K) {
+  int g = 8;
+  while (g > 1 && (size_t)g * K * sizeof(float) + kStaticLds > lds_per_block()) g /= 2;
+  return g;
+}
 
 size_t nk_ws_bytes(const NkCall& c) {
   const size_t g = (size_t)nk_grid(c.N, c.K);
@@ -258,7 +285,8 @@ int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st) {
   if (c.K > 1024 * kMaxCpw) return fail(Q35_E_SHAPE, "nk: K > 8192");
   if (c.M < 1 || c.M > 8) return fail(Q35_E_SHAPE, "nk: M in [1,8]");
   const int MR = c.M == 1 ? 1 : (c.M == 2 ? 2 : (c.M <= 4 ? 4 : 8));
-  if ((size_t)MR * c.K > (size_t)kLdsFloats) return fail(Q35_E_SHAPE, "nk: M*K too large for LDS staging");
+  if ((size_t)MR * c.K * sizeof(float) + kStaticLds > lds_per_block())
+    return fail(Q35_E_SHAPE, "nk: M*K too large for LDS staging");
   if ((reinterpret_cast<uintptr_t>(c.q) & 15) != 0) return fail(Q35_E_ALIGN, "nk: weights not 16-byte aligned");
   if (c.pro == PRO_RMS && !c.pw) return fail(Q35_E_ARG, "nk: RMSNorm needs weight");
   if (c.argmax_out && c.M != 1) return fail(Q35_E_SHAPE, "nk: fused argmax needs M == 1");

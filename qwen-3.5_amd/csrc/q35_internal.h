@@ -376,6 +376,8 @@ struct NkCall {
   int32_t* hist = nullptr;        // optional: hist[*pos_inc] = argmax before the increment
 };
 size_t nk_ws_bytes(const NkCall& c);
+// Rows of x (1, 2, 4 or 8) one lm_head launch can stage in LDS for inner dimension K.
+int nk_max_rows(int K);
 int nk_launch(const NkCall& c, void* ws, size_t ws_bytes, hipStream_t st);
 
 // standalone argmax over a device vector

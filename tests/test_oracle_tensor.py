@@ -213,3 +213,23 @@ def test_gate_proj_closed_form(rng):
     np.testing.assert_allclose(out[:nh], beta, rtol=2e-6)
     np.testing.assert_allclose(out[nh:], g, rtol=2e-5)
     assert abs(out[nh + 3] / (-np.exp(a_log[3])) - a[3]) < 1e-4
+
+
+def test_f32_dequant_timing_path_matches_checker(rng):
+    """The CPU-baseline timing path (f32 dequantised matrix, f32 accumulation) computes the same
+    matvecs as the double-accumulated checker to f32 accuracy, in both layouts."""
+    K, N, M = 512, 320, 3
+    W = O.quantize(rng.standard_normal((K, N)).astype(np.float32) * 0.05)
+    E = O.quantize(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ref_kn = O.gemv_kn(x, W)
+    ref_nk, _ = O.gemv_nk(x, E)
+    try:
+        O.set_f32_dequant(True)
+        got_kn = O.gemv_kn(x, W)
+        got_nk, got64 = O.gemv_nk(x, E)
+    finally:
+        O.set_f32_dequant(False)
+    assert rel_l2(got_kn, ref_kn) <= 1e-5 and rel_l2(got_nk, ref_nk) <= 1e-5
+    np.testing.assert_array_equal(got64, got_nk.astype(np.float64))
+    assert not np.array_equal(got_kn, ref_kn)  # it really is the other (f32) path
