@@ -92,6 +92,16 @@ int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t
 int q35_q8_gemv_partial_sum(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t ws_bytes, void* stream);
 size_t q35_q8_gemv_ws_bytes(int32_t M, q35_q8f W);
 
+/* q35_q8_gemv without a workspace and without any allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under hipGraph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same results as q35_q8_gemv (the same kernels).  The
+ * Q35_KN / Q35_KN_TILED split-K scratch is a fixed 1 MiB + 64 KiB device array per GPU (held
+ * until the process ends), so min(M, 8) * N must be <= 131072 (else Q35_E_SHAPE); the panel and
+ * NK layouts need no scratch.  Every call on one GPU shares that GPU's array, which each call
+ * leaves zeroed: calls that overlap on one GPU (different streams, concurrent graph replays)
+ * race and must be serialised by the caller. */
+int q35_q8_gemv_noalloc(const float* x, int32_t M, q35_q8f W, float* y, void* stream);
+
 /* logits[M][V] = h[M][D] @ dequant(E)^T with E the NK [V][D] embedding table.
  * Replaces q8_lm_head (src/kernels.rs:724-731, kernel :251-291). */
 int q35_q8_lm_head(const float* h, int32_t M, q35_q8f E, float* logits, void* stream);

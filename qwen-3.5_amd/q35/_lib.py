@@ -52,6 +52,7 @@ PROTOTYPES = {
     "q35_q8_gemv": (ctypes.c_int, [c_vp, c_i32, Q8F, c_vp, c_vp, c_sz, c_vp]),
     "q35_q8_gemv_partial_sum": (ctypes.c_int, [c_vp, c_i32, Q8F, c_vp, c_vp, c_sz, c_vp]),
     "q35_q8_gemv_ws_bytes": (c_sz, [c_i32, Q8F]),
+    "q35_q8_gemv_noalloc": (ctypes.c_int, [c_vp, c_i32, Q8F, c_vp, c_vp]),
     "q35_q8_lm_head": (ctypes.c_int, [c_vp, c_i32, Q8F, c_vp, c_vp]),
     "q35_q8_embedding_lookup": (ctypes.c_int, [Q8F, c_vp, c_i32, c_vp, c_vp]),
     "q35_gate_proj": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
