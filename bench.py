@@ -158,6 +158,7 @@ def gdn_leg(torch, q35, st):
     nh, dk, dv = 16, 128, 128
     conv = 2 * nh * dk + nh * dv
     conv_w = torch.randn(conv, 4, device="cuda") * 0.02
+    ws = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")  # counters: the conv shift rides on the step
     for B in (1, 32):
         per = B * (nh * dk * dv + conv * 3) * 4
         R = max(2, -(-ROTATE_BYTES // per))
@@ -174,7 +175,7 @@ def gdn_leg(torch, q35, st):
             for mixed, bg, cs, S, o in sets:
                 q35._lib.check(lib.q35_gated_delta_rule_decode(mixed.data_ptr(), B, bg.data_ptr(), cs.data_ptr(),
                                                                conv_w.data_ptr(), S.data_ptr(), o.data_ptr(), nh, dk,
-                                                               dv, None, 0, sh))
+                                                               dv, ws.data_ptr(), ws.numel(), sh))
         out[f"B{B}"] = dict(rate(gdn_bytes(B, nh, dk, dv), per_call_us(torch, st, run, R)), copies=R)
         del sets
         torch.cuda.empty_cache()

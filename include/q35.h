@@ -181,8 +181,10 @@ int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, 
  * out = S^T q.  mixed_qkv: [B][2*key_dim+value_dim] (pre-conv projection output); beta_g:
  * [B][2*lin_heads] = [beta | g] as q35_gate_proj produces; conv_state [B][conv_dim][3] and
  * rec_state [B][lin_heads][128][lin_dv] updated in place; core_out: [B][lin_heads*lin_dv] (before
- * the gated norm).  Replaces causal_conv1d_update + burn_recurrent_gated_delta_rule
- * (src/text_modules.rs:134-162, :365-443) as called at :515-530, :627-652. */
+ * the gated norm).  ws (optional): a zeroed workspace of at least 64 KiB lets one kernel also
+ * advance the conv state (left zeroed for the next call); with ws NULL a second kernel does it.
+ * Replaces causal_conv1d_update + burn_recurrent_gated_delta_rule (src/text_modules.rs:134-162,
+ * :365-443) as called at :515-530, :627-652. */
 int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* beta_g, float* conv_state,
                                 const float* conv_w, float* rec_state, float* core_out, int32_t lin_heads,
                                 int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes, void* stream);
@@ -272,6 +274,26 @@ int q35_model_persistent_info(q35_model* m, int32_t* grid_out);
 int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t n_new,
                        int32_t* out_tokens_host, int32_t use_graph, int32_t readback_each,
                        double* decode_seconds_host, void* stream);
+
+/* Greedy generation with stop ids, as the chat loop of main.rs:100-132 runs it: the prompt is fed
+ * (n_prompt ids), then up to max_new steps; before each step the current token (the argmax
+ * after the previous position) is compared with the n_stop (<= Q35_MAX_STOP_IDS) stop ids
+ * (<|im_end|> and eos, main.rs:105-110) and the loop ends at the first match, which is not
+ * forwarded.  out_tokens_host (room for max_new + 1) receives the *n_out_host produced ids (each
+ * forwarded), then the id that ended the loop: the stop id, or the unforwarded argmax after the
+ * last produced id when max_new were produced.  Afterwards the position is
+ * start + n_prompt + *n_out_host and the token slot holds that last id, so the caller can forward
+ * <|im_end|> as main.rs:141-144 does (q35_model_set_token + q35_model_step).  In
+ * Q35_LAUNCH_PERSISTENT mode the generated steps are one launch that ends itself at a stop id
+ * (no host round trip per token); the other modes read each token back as main.rs:107 does. */
+#define Q35_MAX_STOP_IDS 4
+int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t max_new,
+                             const int32_t* stop_ids_host, int32_t n_stop, int32_t* out_tokens_host,
+                             int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host, void* stream);
+
+/* Tokens consumed so far (the cache length that TextModel::forward derives positions from,
+ * model.rs:37-43). */
+int q35_model_position(q35_model* m, int32_t* pos_out);
 
 /* Device pointer and byte size of a named model tensor, named as the reference's module
  * paths: "embed_tokens", "norm", "layers.{i}.input_layernorm", "layers.{i}.linear_attn.in_proj_qkv"

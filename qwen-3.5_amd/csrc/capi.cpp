@@ -380,7 +380,6 @@ int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, 
 int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* beta_g, float* conv_state,
                                 const float* conv_w, float* rec_state, float* core_out, int32_t lin_heads,
                                 int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes, void* stream) {
-  (void)ws; (void)ws_bytes;
   if (!mixed_qkv || !beta_g || !conv_state || !conv_w || !rec_state || !core_out)
     return fail(Q35_E_ARG, "gated_delta_rule_decode: null pointer");
   if (B < 1 || lin_heads < 1) return fail(Q35_E_SHAPE, "gated_delta_rule_decode: B and heads must be >= 1");
@@ -389,8 +388,11 @@ int q35_gated_delta_rule_decode(const float* mixed_qkv, int32_t B, const float* 
   g.qkv = mixed_qkv; g.ld_qkv = conv_dim; g.bg = beta_g; g.ld_bg = 2 * lin_heads; g.conv_state = conv_state;
   g.conv_w = conv_w; g.S = rec_state; g.o = core_out; g.ld_o = lin_heads * lin_dv; g.B = B; g.nh = lin_heads;
   g.dk = lin_dk; g.dv = lin_dv; g.conv_k = 4;
+  // with a workspace the step kernel advances the conv state itself (one launch)
+  const bool fused = ws && ws_bytes >= kCounterBytes && (int64_t)B * lin_heads <= kMaxCounters;
+  if (fused) g.head_ctr = ws_counters(ws);
   int rc = gdn_step_launch(g, S(stream));
-  if (rc) return rc;
+  if (rc || fused) return rc;
   return conv_shift_launch(conv_state, mixed_qkv, B, conv_dim, S(stream));
 }
 

@@ -8,8 +8,10 @@
 // S[h][0:128][j0:j0+32] (16 KB) is held in registers, 16 rows per thread: decay, S^T k (8-way
 // LDS reduction), delta = (v - S^T k) * beta, rank-1 update, S^T q, write back.  Every value
 // column is independent, so slices need no cross-block reduction; the per-head gated RMSNorm
-// is applied by the out_proj matvec prologue.  The conv state is only read here (all slices of
-// a head read the same q/k channels); it is advanced afterwards by conv_shift or by a side task
+// is applied by the out_proj matvec prologue.  All slices of a head read the same q/k conv
+// channels, so the conv state can only be advanced once every slice has read it: with a
+// counter per (row, head) (head_ctr), the last slice block of the head to finish shifts the head's
+// 2*dk + dv channels itself; otherwise it is advanced afterwards by conv_shift or by a side task
 // of the next matvec launch.
 #include "q35_internal.h"
 
@@ -47,6 +49,7 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   __shared__ float vv[kCS];
   __shared__ float wsum[4];
   __shared__ float red[kRowGroups * kCS];
+  __shared__ int last_flag;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int slice = blockIdx.x % A.nslice;
@@ -123,6 +126,18 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
 #pragma unroll
     for (int i = 0; i < kRowGroups; ++i) o += red[i * kCS + j];
     a.o[(size_t)b * a.ld_o + h * a.dv + slice * kCS + j] = o;
+  }
+  if (!a.head_ctr) return;
+  // the last slice of (b, h) to get here advances the head's conv state: [s1, s2, x]
+  if (!arrive_last(&a.head_ctr[b * a.nh + h], (uint32_t)A.nslice, &last_flag)) return;
+  float* cw = a.conv_state + (size_t)b * A.conv_dim * 3;
+  for (int e = tid; e < 2 * kDk + a.dv; e += kThreads) {
+    const int c = e < kDk ? h * kDk + e : (e < 2 * kDk ? A.key_dim + h * kDk + (e - kDk) : 2 * A.key_dim + h * a.dv + (e - 2 * kDk));
+    float* st = cw + (size_t)c * 3;
+    const float s1 = st[1], s2 = st[2];
+    st[0] = s1;
+    st[1] = s2;
+    st[2] = qkv_at(a, b, c);
   }
 }
 

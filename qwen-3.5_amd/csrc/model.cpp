@@ -263,6 +263,9 @@ int setup_persistent(q35_model* m) {
   a.ntok = 0;
   m->bar_epoch = 0;
   m->bar_per_token = step_barriers_per_token(d);
+  a.bar_per_token = m->bar_per_token;
+  a.n_stop = 0;
+  for (int j = 0; j < 4; ++j) a.stop_ids[j] = -1;
   return Q35_OK;
 }
 
@@ -294,14 +297,18 @@ const char* kStepFailed = "persistent step: a grid barrier timed out; the model 
 
 // n consecutive steps in one launch of the persistent kernel.  The barrier base is the number of
 // barriers every earlier launch passed; a launch that fails (its error word set) leaves later
-// launches as no-ops until a reset, so the base only has to be right while nothing failed.
-int persistent(q35_model* m, int n, hipStream_t st) {
+// launches as no-ops until a reset, so the base only has to be right while nothing failed.  With
+// stop ids the launch may end early (a stopped launch still settles its barrier counters); the
+// caller then re-reads the device position (sync_pos).
+int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nullptr, int n_stop = 0) {
   if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
   if (m->step_failed) return fail(Q35_E_HIP, kStepFailed);
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
   StepArgs a = m->step_args;
   a.ntok = n;
   a.bar_base = m->bar_epoch;
+  a.n_stop = n_stop;
+  for (int j = 0; j < n_stop; ++j) a.stop_ids[j] = stop_ids[j];
   int rc = step_launch(a, m->step_grid, st);
   if (rc) return rc;
   m->bar_epoch += (uint32_t)n * (uint32_t)m->bar_per_token;
@@ -587,6 +594,72 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
   if (pers && (rc = check_persistent(m, st))) return rc;
   if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
   Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + p0 + n_prompt - 1, sizeof(int32_t) * (n_new + 1), hipMemcpyDeviceToHost));
+  return Q35_OK;
+}
+
+int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t max_new,
+                             const int32_t* stop_ids_host, int32_t n_stop, int32_t* out_tokens_host,
+                             int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host, void* stream) {
+  if (!m || !prompt_host || !out_tokens_host || !n_out_host) return fail(Q35_E_ARG, "model_generate_until: null pointer");
+  if (n_stop < 0 || n_stop > Q35_MAX_STOP_IDS || (n_stop > 0 && !stop_ids_host))
+    return fail(Q35_E_ARG, "model_generate_until: between 0 and 4 stop ids");
+  if (use_graph < Q35_LAUNCH_STREAM || use_graph > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_generate_until: bad launch mode");
+  if (n_prompt < 1 || max_new < 0) return fail(Q35_E_SHAPE, "model_generate_until: need n_prompt >= 1, max_new >= 0");
+  const int32_t p0 = m->host_pos;
+  if ((int64_t)p0 + n_prompt + max_new > m->tmax) return fail(Q35_E_SHAPE, "model_generate_until: tmax too small");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt_host[i] < 0 || prompt_host[i] >= m->d.vocab) return fail(Q35_E_ARG, "model_generate_until: prompt id out of range");
+  hipStream_t st = pick(m, stream);
+  Q35_HIP_TRY(hipMemcpyAsync(m->prompt + p0, prompt_host, sizeof(int32_t) * n_prompt, hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const int32_t pe = p0 + n_prompt;  // first generated position
+  m->pinned[0] = pe;
+  Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  int rc;
+  const bool pers = (use_graph == Q35_LAUNCH_PERSISTENT);
+  if (use_graph == Q35_LAUNCH_GRAPH && (rc = capture(m, st))) return rc;
+  if (pers) {
+    if ((rc = persistent(m, n_prompt, st))) return rc;
+  } else {
+    for (int i = 0; i < n_prompt; ++i)
+      if ((rc = step(m, use_graph, st))) return rc;
+  }
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const auto t0 = std::chrono::steady_clock::now();
+  int32_t produced = 0;
+  if (pers) {
+    // one launch; the kernel ends at the first generated step whose input token is a stop id
+    if (max_new > 0 && (rc = persistent(m, max_new, st, stop_ids_host, n_stop))) return rc;
+    Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->pos, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+    if ((rc = check_persistent(m, st))) return rc;
+    const int32_t dpos = m->pinned[0];
+    if (dpos < pe || dpos > pe + max_new) return fail(Q35_E_HIP, "model_generate_until: device position out of range");
+    produced = dpos - pe;
+    m->host_pos = dpos;
+  } else {
+    // main.rs:105-110: read the token, stop on a stop id, else forward it
+    for (; produced < max_new; ++produced) {
+      Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+      Q35_HIP_TRY(hipStreamSynchronize(st));
+      bool stop = false;
+      for (int j = 0; j < n_stop; ++j) stop |= m->pinned[0] == stop_ids_host[j];
+      if (stop) break;
+      if ((rc = step(m, use_graph, st))) return rc;
+    }
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+  }
+  const auto t1 = std::chrono::steady_clock::now();
+  if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
+  Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + pe - 1, sizeof(int32_t) * (produced + 1), hipMemcpyDeviceToHost));
+  *n_out_host = produced;
+  return Q35_OK;
+}
+
+int q35_model_position(q35_model* m, int32_t* pos_out) {
+  if (!m || !pos_out) return fail(Q35_E_ARG, "model_position: null pointer");
+  *pos_out = m->host_pos;
   return Q35_OK;
 }
 

@@ -399,11 +399,13 @@ struct GdnCall {
   // a_log / dt_bias, activated here as kernels.rs:228-244 does
   const float* bg = nullptr; const fx_t* ba_f = nullptr; int32_t ld_bg = 0;
   const float* a_log = nullptr; const float* dt_bias = nullptr;
-  const float* conv_state = nullptr;  // [B][conv_dim][conv_k-1]
+  float* conv_state = nullptr;        // [B][conv_dim][conv_k-1]
   const float* conv_w = nullptr;      // [conv_dim][conv_k]
   float* S = nullptr;                 // [B][nh][dk][dv]
   float* o = nullptr; int32_t ld_o = 0;  // [B][nh*dv] raw core output (before the gated norm)
   int32_t B = 1, nh = 0, dk = 0, dv = 0, conv_k = 0;
+  // optional zeroed counters [B*nh]: the kernel then advances the conv state itself (left zero)
+  uint32_t* head_ctr = nullptr;
 };
 int gdn_step_launch(const GdnCall& c, hipStream_t st);
 // state[b][c] <- [s1, s2, x[b][c]] for all conv_dim channels (f32 x)
@@ -473,6 +475,11 @@ struct StepArgs {
   float* arg_v; int32_t* arg_i;  // per-block argmax partials [grid]
   int32_t *token, *pos, *prompt, *plen, *hist;
   ArgOrder ord;        // the reference's argmax order over the vocabulary
+  // Stop ids (main.rs:108-110): a generated step (position >= plen) whose input token is one of
+  // them is not run; the launch ends there (pos = that position, token = the stop id).
+  int32_t stop_ids[4];
+  int32_t n_stop;
+  int32_t bar_per_token;  // grid barriers per step (so a stopped launch can settle its counters)
   // Barrier counters (kStepBarBytes).  They are never cleared between launches: each launch
   // passes bar_base, the number of grid barriers completed by all earlier launches since the
   // counters were last zeroed (model reset), and waits for counter values relative to it

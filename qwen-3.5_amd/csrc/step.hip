@@ -439,6 +439,18 @@ Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
   return tok;
 }
 
+// A generated step (position past the prompt) whose input token is a stop id is not run.  Every
+// block reduces the same partials, so every block takes the same decision.
+Q35_DEV bool is_stop(const StepArgs& a, int p, int tok) {
+  if (a.n_stop <= 0 || p < ldg(a.plen)) return false;
+  bool s = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s |= (j < a.n_stop) && tok == a.stop_ids[j];
+  return s;
+}
+
+enum { kStageFail = 0, kStageOk = 1, kStageStop = 2 };
+
 // ------------------------------------------------------------------ Gated DeltaNet step
 // The out stage's prologue.  An out item covers rows [k0, k0 + klen) of the core output o, and
 // klen divides dv, so they lie in one value head h.  The gated RMSNorm needs all dv outputs of
@@ -686,9 +698,11 @@ Q35_DEV void side_tasks(const StepArgs& a, int kind) {
 // kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
 // dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need;
 // KR: hidden-size elements per thread in the RMSNorm prologue (hidden <= 512 KR).
+// Returns kStageOk, kStageFail (barrier time-out) or, for the first stage of a step, kStageStop
+// (the step's input token is a stop id; *stop_tok receives it, nothing of the step has run).
 template <int U, int KR>
-Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int p, Bar& bar,
-                      const Shared& sh) {
+Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int p, Bar& bar,
+                     const Shared& sh, int* stop_tok = nullptr) {
   const Mv d = make_mv(a, L, kind);
   const int nitems = d.t3 * d.nchunk;
   int item = bix();
@@ -712,10 +726,19 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
     mv_load(it, d.K, pf);
     if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
   }
-  if (!bar_wait(bar, sh.ok)) return false;
-  if (item >= nitems) side_tasks(a, kind);  // blocks with an item run them in the prologue
+  if (!bar_wait(bar, sh.ok)) return kStageFail;
   int tok = 0;
-  if (pro == PRO_EMBED_RMS && item < nitems) tok = select_token(a, i, p, sh);
+  // Blocks with an item need the token for the embedding; with stop ids every block forms it,
+  // so that every block sees a stop (without them the idle blocks go straight to their side
+  // tasks, whose stores would otherwise wait behind the token's reduction).
+  if (pro == PRO_EMBED_RMS && (item < nitems || a.n_stop > 0)) {
+    tok = select_token(a, i, p, sh);
+    if (is_stop(a, p, tok)) {
+      if (stop_tok) *stop_tok = tok;
+      return kStageStop;
+    }
+  }
+  if (item >= nitems) side_tasks(a, kind);  // blocks with an item run them in the prologue
   float* xs = sh.smem + kXs;
   float* red = sh.smem + kRed;
   for (bool first = true; item < nitems; item += gridDim.x, first = false) {
@@ -782,7 +805,7 @@ Q35_DEV bool mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, in
     mv_compute(it, pf, xs, red, auxp, auxd);
   }
   bar_arrive(bar);
-  return true;
+  return kStageOk;
 }
 
 // ------------------------------------------------------------------ attention partials
@@ -1101,29 +1124,56 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   // a failed earlier launch left the model state invalid: do nothing until a reset
   if (ld_agent(a.err) != 0u) return;
   const int p0 = ldg(a.pos);
-  for (int i = 0; i < a.ntok; ++i) {
+  int executed = a.ntok, stop_tok = 0;
+  for (int i = 0; i < a.ntok && executed == a.ntok; ++i) {
     const int p = p0 + i;
     for (int l = 0; l < a.n_layers; ++l) {
       CLayer& L = layer_at(a, l);
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
+      int r;
       if (!L.full) {
-        if (!mv_stage<kU, KR>(a, L, SMV_QKVZ, pro0, i, p, bar, sh)) return;
+        r = mv_stage<kU, KR>(a, L, SMV_QKVZ, pro0, i, p, bar, sh, &stop_tok);
+        if (r == kStageStop) { executed = i; break; }
+        if (r == kStageFail) return;
         if (!mv_stage<kUOut, KR>(a, L, SMV_OUT, PRO_GDN, i, p, bar, sh)) return;
       } else {
-        if (!mv_stage<kU, KR>(a, L, SMV_QKV, pro0, i, p, bar, sh)) return;
+        r = mv_stage<kU, KR>(a, L, SMV_QKV, pro0, i, p, bar, sh, &stop_tok);
+        if (r == kStageStop) { executed = i; break; }
+        if (r == kStageFail) return;
         if (!attn_stage(a, L, p, bar, sh)) return;
         if (!mv_stage<kU, KR>(a, L, SMV_O, PRO_ATTN, i, p, bar, sh)) return;
       }
       if (!mv_stage<kU, KR>(a, L, SMV_GU, PRO_RMS, i, p, bar, sh)) return;
       if (!mv_stage<kU, KR>(a, L, SMV_DOWN, PRO_SWIGLU, i, p, bar, sh)) return;
     }
+    if (executed != a.ntok) break;
     if (!lm_stage<CPW>(a, bar, sh)) return;
   }
-  // Every block has passed the last step's lm-stage barrier, so all state writes are complete.
-  if (a.ntok & 1) state_copy_back(a);
+  if (executed != a.ntok) {
+    // Stopped before step `executed` ran (every block decided alike): arrive once for all the
+    // barriers the remaining steps would have passed, so the counters end where a full launch
+    // leaves them (the host counts barriers per launch).
+    const uint32_t final_epoch = a.bar_base + (uint32_t)a.ntok * (uint32_t)a.bar_per_token;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tix() == 0)
+      __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&bar.ctr[(bix() % kGroups) * kCtrStride], final_epoch - bar.epoch,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bar.epoch = final_epoch;
+  }
+  // Every block has passed the last executed step's lm-stage barrier (a stop is decided after
+  // it), so all state writes are complete.
+  if (executed & 1) state_copy_back(a);
   // tail: block 0 turns the last step's block argmaxes into the token
   if (bix() != 0) return;
   if (!bar_wait(bar, sh.ok)) return;
+  if (executed != a.ntok) {  // the stop id stays the next token; hist already holds it
+    if (tix() == 0) {
+      stg(a.token, (int32_t)stop_tok);
+      stg(a.pos, (int32_t)(p0 + executed));
+    }
+    return;
+  }
   float v = -INFINITY;
   int ix = INT_MAX;
   if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }

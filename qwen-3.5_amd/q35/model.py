@@ -89,6 +89,26 @@ class TextForCausalLM:
                                            ctypes.byref(secs), stream))
         return out, secs.value
 
+    def generate_until(self, prompt, max_new, stop_ids=(), mode=None, stream=None):
+        """The chat loop's generation (main.rs:100-132): returns (produced, last, decode_seconds),
+        `produced` the ids forwarded after the prompt (at most max_new) and `last` the id that
+        ended the loop (a stop id, or the argmax after the last produced id)."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        s = np.ascontiguousarray(np.asarray(list(stop_ids), dtype=np.int32))
+        out = np.zeros(max_new + 1, np.int32)
+        n = ctypes.c_int32(0)
+        secs = ctypes.c_double(0.0)
+        L.check(L.lib().q35_model_generate_until(self.h, p.ctypes.data, p.size, int(max_new),
+                                                 s.ctypes.data if s.size else None, s.size, out.ctypes.data,
+                                                 ctypes.byref(n), self._mode(mode, None), ctypes.byref(secs),
+                                                 stream))
+        return out[:n.value].copy(), int(out[n.value]), secs.value
+
+    def position(self):
+        v = ctypes.c_int32(0)
+        L.check(L.lib().q35_model_position(self.h, ctypes.byref(v)))
+        return v.value
+
     def tensor_ptr(self, name):
         ptr = ctypes.c_void_p()
         nbytes = ctypes.c_size_t()

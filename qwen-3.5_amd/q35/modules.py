@@ -84,16 +84,19 @@ class MLP:
         return out
 
 
-def gated_delta_rule_decode(mixed_qkv, beta_g, conv_state, conv_w, recurrent_state, heads, dk=128, dv=128):
+def gated_delta_rule_decode(mixed_qkv, beta_g, conv_state, conv_w, recurrent_state, heads, dk=128, dv=128,
+                            fused=True):
     """Conv update + recurrent gated delta rule for one token (text_modules.rs:134-162,
     :365-443).  mixed_qkv [B, conv_dim]; beta_g [B, 2*heads]; states updated in place;
-    returns the core output [B, heads*dv] (before the gated norm)."""
+    returns the core output [B, heads*dv] (before the gated norm).  fused: pass a workspace so
+    that one kernel also advances the conv state (else a second kernel does)."""
     B = mixed_qkv.shape[0]
     out = torch.empty((B, heads * dv), dtype=torch.float32, device=mixed_qkv.device)
-    ws = workspace(1 << 16, mixed_qkv.device, "delta_rule")
+    ws = workspace(1 << 16, mixed_qkv.device, "delta_rule") if fused else None
     L.check(L.lib().q35_gated_delta_rule_decode(_p(mixed_qkv), B, _p(beta_g), conv_state.data_ptr(), _p(conv_w),
                                                 recurrent_state.data_ptr(), out.data_ptr(), heads, dk, dv,
-                                                ws.data_ptr(), ws.numel(), _stream()))
+                                                ws.data_ptr() if fused else None, ws.numel() if fused else 0,
+                                                _stream()))
     return out
 
 

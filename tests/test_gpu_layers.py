@@ -17,10 +17,13 @@ def softplus(x):
     return np.log1p(np.exp(x))
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("B", [1, 32])
-def test_gated_delta_rule_decode_c2(B):
-    """C2: 16 heads, dk = dv = 128, S ~ N(0, 0.1), beta = sigmoid(N(0,1)), decay = exp(-softplus(N(0,1)))."""
-    print(f"[delta rule] B={B}", flush=True)
+def test_gated_delta_rule_decode_c2(B, fused):
+    """C2: 16 heads, dk = dv = 128, S ~ N(0, 0.1), beta = sigmoid(N(0,1)), decay = exp(-softplus(N(0,1))).
+    fused: the conv state is advanced by the step kernel's last block of each head (with a
+    workspace) or by a second kernel (without)."""
+    print(f"[delta rule] B={B} fused={fused}", flush=True)
     nh, dk, dv = 16, 128, 128
     conv_dim = 2 * nh * dk + nh * dv
     S0 = normal(30, (B, nh, dk, dv), 0.1)
@@ -33,7 +36,7 @@ def test_gated_delta_rule_decode_c2(B):
         beta = (1 / (1 + np.exp(-normal(40 + step, (B, nh)).astype(np.float64)))).astype(np.float32)
         g = (-softplus(normal(50 + step, (B, nh)).astype(np.float64))).astype(np.float32)
         bg = np.concatenate([beta, g], axis=1)
-        out = host(q35.gated_delta_rule_decode(dev(mixed), dev(bg), cs_d, dev(cw), S_d, nh, dk, dv))
+        out = host(q35.gated_delta_rule_decode(dev(mixed), dev(bg), cs_d, dev(cw), S_d, nh, dk, dv, fused=fused))
         kd = nh * dk
         for b in range(B):
             conv, cs_h[b] = O.conv_update(mixed[b], cs_h[b], cw)

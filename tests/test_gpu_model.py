@@ -79,6 +79,56 @@ def test_launch_modes_agree_and_reset():
     a.close()
 
 
+def stop_dims():
+    """A 4-layer hybrid whose greedy ids do not repeat one token (38 distinct of 41 at seed 3)."""
+    return q35.make_dims(hidden=512, ffn=1536, vocab=8192, n_layers=4, lin_heads=4, attn_heads=4, kv_heads=2)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_generate_until_stop_ids(mode):
+    """main.rs:105-110: the loop ends at the first current token that is a stop id, which is not
+    forwarded; the tokens before it, the position and the token slot are what the reference
+    leaves.  Decoding on afterwards (the stop id is forwarded next, as main.rs:141-144 does with
+    <|im_end|>) gives the history of a run without stop ids, so a launch that ended early left
+    every state and the barrier counters consistent.  Stops are planted at an even and an odd
+    index (the persistent kernel double-buffers its states per step) and on the first token."""
+    print(f"[model stop ids] mode={mode}", flush=True)
+    d = stop_dims()
+    seed, tmax, n = 3, 96, 40
+    prompt = np.random.default_rng(seed).integers(0, d.vocab, 8).astype(np.int32)
+    rt, _ = oracle_model(d, seed, tmax).generate(prompt, n)
+    unused = next(t for t in range(d.vocab) if t not in set(rt.tolist()))
+    firsts = [j for j in range(4, n) if rt[j] not in set(rt[:j].tolist())]
+    cases = [next(j for j in firsts if j % 2 == 0), next(j for j in firsts if j % 2 == 1), 0]
+    m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    P = len(prompt)
+    for j in cases:
+        m.reset()
+        produced, last, _ = m.generate_until(prompt, n, stop_ids=[unused, int(rt[j])], mode=mode)
+        m.check()
+        print("stop at", j, "produced", len(produced), "last", last, flush=True)
+        np.testing.assert_array_equal(produced, rt[:j])
+        assert last == rt[j]
+        assert m.position() == P + j
+        assert int(m.tensor("pos", np.int32)[0]) == P + j
+        assert int(m.tensor("token", np.int32)[0]) == rt[j]
+        m.decode(n - j, mode=mode)
+        m.check()
+        np.testing.assert_array_equal(m.tensor("hist", np.int32)[P - 1:P + n], rt)
+    # no stop id met: max_new ids produced, the next argmax returned
+    m.reset()
+    produced, last, _ = m.generate_until(prompt, 7, stop_ids=[unused], mode=mode)
+    m.check()
+    np.testing.assert_array_equal(produced, rt[:7])
+    assert last == rt[7] and m.position() == P + 7
+    # a stop id inside the prompt does not end anything: only generated tokens are checked
+    m.reset()
+    produced, last, _ = m.generate_until(prompt, 5, stop_ids=[int(prompt[3]), int(prompt[-1])], mode=mode)
+    m.check()
+    np.testing.assert_array_equal(produced, rt[:5])
+    m.close()
+
+
 def test_persistent_multi_step_launch_equals_single_steps():
     """decode(n) as one launch vs n launches of one step: identical history."""
     print("[model persistent multi]", flush=True)
