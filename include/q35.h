@@ -213,6 +213,53 @@ int q35_workspace_status(void* ws, void* stream);
  * (src/text_modules.rs:30-43,73-81; the mRoPE recomposition :45-58 is the identity for text). */
 int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin_host);
 
+/* ---------------------------------------------------------------- prompt path (seq_len > 1) */
+
+/* y[M][N] (+)= x[M][K] @ dequant(W) on the fp32 matrix cores: each weight is dequantised to f32
+ * (f32(q) * scale) and the products are summed in f32, as the reference's Linear::forward on a
+ * QFloat weight does for a prompt (dequantise, f32 matmul: text_modules.rs:500-508, :578-595,
+ * :638-647, :880-890, :1003-1005).  W: Q35_KN / Q35_KN_TILED (K = rows, N = cols) or Q35_NK
+ * (N = rows, K = cols: the tied lm_head matmul of model.rs:130-138).  x rows ldx floats apart
+ * (16-byte aligned), y rows ldy apart; accumulate = 1 adds into y (a residual add).  K, N
+ * multiples of 64; any M >= 1. */
+int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                void* stream);
+
+/* out[t] = [beta | g] for T prompt rows, as the prompt branch computes them
+ * (text_modules.rs:578-595): beta = sigmoid(x.W_b), g = -exp(A_log) * softplus(x.W_a + dt_bias)
+ * with softplus's identity branch taken when its INPUT exceeds 20 (decode, q35_gate_proj,
+ * tests the result). */
+int q35_gate_proj_prompt(const float* x, int32_t T, int32_t in_dim, const float* w_b, const float* w_a,
+                         const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream);
+
+/* The recurrent core of GatedDeltaNet over T prompt tokens of one sequence (dk = dv = 128):
+ * causal conv1d + SiLU over the prompt continuing conv_state (causal_conv1d_fn with the cached
+ * state prepended, text_modules.rs:164-182,531-554), l2norm(q)*dk^-1/2, l2norm(k), and the
+ * chunked gated delta rule (chunks of 64) continuing rec_state (burn_chunk_gated_delta_rule,
+ * :189-363, as called at :627-652).  mixed_qkv: [T][ld_qkv] pre-conv projection rows;
+ * beta_g: [T][2*lin_heads] from q35_gate_proj_prompt; conv_state [conv_dim][3] and rec_state
+ * [lin_heads][128][128] are updated in place to the state after the prompt; core_out:
+ * [T][lin_heads*128] (before the gated norm).  ws: q35_gated_delta_rule_prefill_ws_bytes(T,
+ * lin_heads) bytes of scratch (no zeroing needed). */
+int q35_gated_delta_rule_prefill(const float* mixed_qkv, int32_t T, int32_t ld_qkv, const float* beta_g,
+                                 float* conv_state, const float* conv_w, float* rec_state, float* core_out,
+                                 int32_t lin_heads, int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes,
+                                 void* stream);
+size_t q35_gated_delta_rule_prefill_ws_bytes(int32_t T, int32_t lin_heads);
+
+/* The attention core for T prompt tokens of one sequence at positions p0..p0+T-1: q_norm/k_norm
+ * (1+w), RoPE, K/V appended at rows p0..p0+T-1 of k_cache/v_cache [kv_heads][tmax][256],
+ * causal GQA softmax(q K^T / 16) V over rows 0..p0+t (the mask of model.rs:59-61), times
+ * sigmoid(gate).  q_gate: [T][ld_qg] q_proj rows (per head [query | gate]); k_new, v_new:
+ * [T][kv_ld]; out: [T][attn_heads*256].  Replaces the prompt branch of Attention::forward
+ * between the projections (text_modules.rs:860-936).  ws: q35_attention_prefill_ws_bytes. */
+int q35_attention_core_prefill(const q35_dims* d, const float* q_gate, int32_t ld_qg, const float* k_new,
+                               const float* v_new, int32_t kv_ld, int32_t T, int32_t p0, const float* q_norm,
+                               const float* k_norm, float* k_cache, float* v_cache, int32_t tmax,
+                               const float* rope_cos, const float* rope_sin, float* out, void* ws, size_t ws_bytes,
+                               void* stream);
+size_t q35_attention_prefill_ws_bytes(const q35_dims* d, int32_t T);
+
 /* ---------------------------------------------------------------- model level (model.rs, main.rs) */
 
 typedef struct q35_model q35_model;
@@ -290,6 +337,20 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
 int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, int32_t max_new,
                              const int32_t* stop_ids_host, int32_t n_stop, int32_t* out_tokens_host,
                              int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host, void* stream);
+
+/* The prompt path: feeds n_prompt ids (host) at the current position as one forward at
+ * seq_len = n_prompt, as TextForCausalLM::forward does for a prompt (model.rs:27-84,130-138;
+ * main.rs:88-95): every projection is a Q8F GEMM on the fp32 matrix cores (f32 dequant, f32
+ * products and accumulation), the Gated DeltaNet layers run the causal conv over the prompt
+ * (continuing the cached conv state) and the chunked gated delta rule (chunks of 64, continuing
+ * the cached recurrent state; text_modules.rs:164-182,189-363), the attention layers causal
+ * attention over the cache.  Only the last row goes through the final norm and the lm_head (the
+ * only logits the greedy loop reads); its argmax is left in the token slot, so decoding
+ * continues from there.  Asynchronous after the prompt upload; prompts longer than the internal
+ * pass size (1024) run in consecutive passes.  OR Q35_PREFILL_GEMM into the mode argument of
+ * q35_model_generate / q35_model_generate_until to feed their prompt this way. */
+#define Q35_PREFILL_GEMM 0x100
+int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, void* stream);
 
 /* Tokens consumed so far (the cache length that TextModel::forward derives positions from,
  * model.rs:37-43). */

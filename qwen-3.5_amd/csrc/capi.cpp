@@ -412,6 +412,81 @@ int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const floa
   return attn_launch(a, ws, ws_bytes, S(stream));
 }
 
+// ---------------------------------------------------------------- prompt (seq_len > 1) surface
+
+int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                void* stream) {
+  int rc = check_q8f(W, "q8_gemm");
+  if (rc) return rc;
+  if (!x || !y) return fail(Q35_E_ARG, "q8_gemm: null pointer");
+  if (W.layout == Q35_KN_PANEL) return fail(Q35_E_ARG, "q8_gemm: layout must be Q35_KN, Q35_KN_TILED or Q35_NK");
+  const bool nk = W.layout == Q35_NK;
+  const int K = nk ? W.cols : W.rows, N = nk ? W.rows : W.cols;
+  if (M < 1) return fail(Q35_E_SHAPE, "q8_gemm: M must be >= 1");
+  if (K % 64 != 0 || N % 64 != 0) return fail(Q35_E_SHAPE, "q8_gemm: K and N must be multiples of 64");
+  if (ldx < K || ldy < N) return fail(Q35_E_SHAPE, "q8_gemm: ldx >= K and ldy >= N required");
+  GemmCall c;
+  c.x = x; c.ldx = ldx; c.M = M; c.K = K; c.nseg = 1; c.accumulate = accumulate ? 1 : 0;
+  c.seg[0] = GemmSeg{W.q, W.scale, y, N, W.layout, ldy};
+  return gemm_launch(c, S(stream));
+}
+
+int q35_gate_proj_prompt(const float* x, int32_t T, int32_t in_dim, const float* w_b, const float* w_a,
+                         const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream) {
+  return gate_proj_simple_launch(x, T, in_dim, w_b, w_a, a_log, dt_bias, n_heads, out, S(stream), 1);
+}
+
+size_t q35_gated_delta_rule_prefill_ws_bytes(int32_t T, int32_t lin_heads) {
+  if (T < 1 || lin_heads < 1) return 0;
+  const size_t nchunk = (size_t)(T + kGdnChunk - 1) / kGdnChunk;
+  return (size_t)lin_heads * nchunk * kGdnScratchPerChunk * sizeof(float);
+}
+
+int q35_gated_delta_rule_prefill(const float* mixed_qkv, int32_t T, int32_t ld_qkv, const float* beta_g,
+                                 float* conv_state, const float* conv_w, float* rec_state, float* core_out,
+                                 int32_t lin_heads, int32_t lin_dk, int32_t lin_dv, void* ws, size_t ws_bytes,
+                                 void* stream) {
+  if (!mixed_qkv || !beta_g || !conv_state || !conv_w || !rec_state || !core_out || !ws)
+    return fail(Q35_E_ARG, "gated_delta_rule_prefill: null pointer");
+  if (T < 1 || lin_heads < 1) return fail(Q35_E_SHAPE, "gated_delta_rule_prefill: T and heads must be >= 1");
+  if (lin_dk != 128 || lin_dv != 128) return fail(Q35_E_SHAPE, "gated_delta_rule_prefill: head dims must be 128");
+  const int key_dim = lin_heads * lin_dk, conv_dim = 2 * key_dim + lin_heads * lin_dv;
+  if (ld_qkv < conv_dim) return fail(Q35_E_SHAPE, "gated_delta_rule_prefill: ld_qkv < conv_dim");
+  if (ws_bytes < q35_gated_delta_rule_prefill_ws_bytes(T, lin_heads))
+    return fail(Q35_E_WS, "gated_delta_rule_prefill: workspace too small");
+  GdnPrefill g;
+  g.raw = mixed_qkv; g.ld_raw = ld_qkv; g.conv_state = conv_state; g.conv_state_out = conv_state; g.conv_w = conv_w;
+  g.bg = beta_g; g.ld_bg = 2 * lin_heads; g.scr = static_cast<float*>(ws); g.S = rec_state; g.out = core_out;
+  g.ld_out = lin_heads * lin_dv; g.T = T; g.nh = lin_heads; g.key_dim = key_dim;
+  g.nchunk = (T + kGdnChunk - 1) / kGdnChunk; g.qscale = powf((float)lin_dk, -0.5f);
+  return gdn_prefill_launch(g, S(stream));
+}
+
+size_t q35_attention_prefill_ws_bytes(const q35_dims* d, int32_t T) {
+  if (!d || T < 1) return 0;
+  return (size_t)T * d->attn_heads * d->head_dim * sizeof(float);
+}
+
+int q35_attention_core_prefill(const q35_dims* d, const float* q_gate, int32_t ld_qg, const float* k_new,
+                               const float* v_new, int32_t kv_ld, int32_t T, int32_t p0, const float* q_norm,
+                               const float* k_norm, float* k_cache, float* v_cache, int32_t tmax,
+                               const float* rope_cos, const float* rope_sin, float* out, void* ws, size_t ws_bytes,
+                               void* stream) {
+  if (!d) return fail(Q35_E_ARG, "attention_core_prefill: null dims");
+  int rc = validate_dims(*d);
+  if (rc) return rc;
+  if (d->head_dim != kHdP) return fail(Q35_E_SHAPE, "attention_core_prefill: head_dim must be 256");
+  if (ld_qg < d->attn_heads * d->head_dim * 2 || kv_ld < d->kv_heads * d->head_dim)
+    return fail(Q35_E_SHAPE, "attention_core_prefill: row strides too small");
+  if (!ws || ws_bytes < q35_attention_prefill_ws_bytes(d, T)) return fail(Q35_E_WS, "attention_core_prefill: workspace too small");
+  AttnPrefill a;
+  a.qg = q_gate; a.ld_qg = ld_qg; a.k = k_new; a.v = v_new; a.ld_kv = kv_ld; a.qnw = q_norm; a.knw = k_norm;
+  a.eps = d->eps; a.rcos = rope_cos; a.rsin = rope_sin; a.rot = d->rot_dim; a.kc = k_cache; a.vc = v_cache;
+  a.tmax = tmax; a.p0 = p0; a.T = T; a.nh = d->attn_heads; a.nkv = d->kv_heads; a.qbuf = static_cast<float*>(ws);
+  a.out = out; a.ld_out = d->attn_heads * d->head_dim; a.scale = (float)(1.0 / std::sqrt((double)d->head_dim));
+  return attn_prefill_launch(a, S(stream));
+}
+
 int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin_host) {
   if (!d || !cos_host || !sin_host || tmax < 1) return fail(Q35_E_ARG, "rope_tables: bad argument");
   const int rot = d->rot_dim, half = rot / 2;

@@ -151,10 +151,12 @@ __global__ __launch_bounds__(kThreads) void conv_shift_kernel(float* state, cons
 
 // Standalone gate projection: one block per batch row; thread t owns output t % (2*nh) and a
 // strided subset of the input rows, partial sums are reduced in LDS in a fixed order, then
-// sigmoid / -exp(A_log)*softplus are applied.
+// sigmoid / -exp(A_log)*softplus are applied.  The softplus switches to the identity when its
+// result exceeds 20 (the decode kernel, kernels.rs:238-243) or, with input_rule, when its input
+// does (the prompt path, text_modules.rs:587-592).
 __global__ __launch_bounds__(kThreads) void gate_proj_kernel(const float* x, int32_t in_dim, const float* wb,
                                                             const float* wa, const float* alog, const float* dtb,
-                                                            int32_t nh, float* out) {
+                                                            int32_t nh, float* out, int32_t input_rule) {
   __shared__ float red[kThreads];
   const int tid = threadIdx.x, b = blockIdx.x;
   const int nout = 2 * nh, subs = kThreads / nout;
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void gate_proj_kernel(const float* x, int
     } else {
       const float xg = s + dtb[h];
       const float pre = logf(expf(xg) + 1.0f);
-      r = -expf(alog[h]) * (pre > 20.0f ? xg : pre);
+      r = -expf(alog[h]) * ((input_rule ? xg : pre) > 20.0f ? xg : pre);
     }
     out[(size_t)b * nout + tid] = r;
   }
@@ -183,11 +185,13 @@ __global__ __launch_bounds__(kThreads) void gate_proj_kernel(const float* x, int
 }  // namespace
 
 int gate_proj_simple_launch(const float* x, int32_t B, int32_t in_dim, const float* wb, const float* wa,
-                            const float* alog, const float* dtb, int32_t nh, float* out, hipStream_t st) {
+                            const float* alog, const float* dtb, int32_t nh, float* out, hipStream_t st,
+                            int32_t input_rule) {
   if (!x || !wb || !wa || !alog || !dtb || !out) return fail(Q35_E_ARG, "gate_proj: null pointer");
   if (B < 1 || in_dim < 1 || nh < 1) return fail(Q35_E_SHAPE, "gate_proj: B, in_dim, n_heads must be >= 1");
   if (2 * nh > kThreads || (kThreads % (2 * nh)) != 0) return fail(Q35_E_SHAPE, "gate_proj: 2*n_heads must divide 256");
-  hipLaunchKernelGGL(gate_proj_kernel, dim3(B), dim3(kThreads), 0, st, x, in_dim, wb, wa, alog, dtb, nh, out);
+  hipLaunchKernelGGL(gate_proj_kernel, dim3(B), dim3(kThreads), 0, st, x, in_dim, wb, wa, alog, dtb, nh, out,
+                     input_rule);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -65,6 +65,10 @@ struct q35_model {
   uint32_t bar_epoch = 0;  // grid barriers passed by all launches since the counters were zeroed
   int bar_per_token = 0;   // grid barriers per decode step
   bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
+  // prompt path (allocated on first use): up to pf_cap tokens per pass
+  int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
+  float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
+  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr;
 };
 
 namespace q35 {
@@ -316,6 +320,125 @@ int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nu
   return Q35_OK;
 }
 
+// ---- prompt path (TextForCausalLM::forward at seq_len > 1, model.rs:27-84,130-138)
+constexpr int kPrefillCap = 1024;  // tokens per pass; longer prompts run in passes
+
+int ensure_prefill(q35_model* m) {
+  if (m->pf_cap > 0) return Q35_OK;
+  const q35_dims& d = m->d;
+  const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
+  const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  const int cap = std::min(kPrefillCap, (m->tmax + kGdnChunk - 1) / kGdnChunk * kGdnChunk);
+  const int ldy = std::max({conv_dim + vdim, ah * hd * 2 + 2 * kvh * hd, 2 * F});
+  const int lda = std::max({vdim, ah * hd, F});
+  const size_t nchunk = (size_t)cap / kGdnChunk;
+  int rc;
+  if ((rc = dev_alloc_t(m, "prefill_x", (size_t)cap * H, &m->pf_x)) ||
+      (rc = dev_alloc_t(m, "prefill_xn", (size_t)cap * H, &m->pf_xn)) ||
+      (rc = dev_alloc_t(m, "prefill_y", (size_t)cap * ldy, &m->pf_y)) ||
+      (rc = dev_alloc_t(m, "prefill_a", (size_t)cap * lda, &m->pf_a)) ||
+      (rc = dev_alloc_t(m, "prefill_core", (size_t)cap * vdim, &m->pf_core)) ||
+      (rc = dev_alloc_t(m, "prefill_bg", (size_t)cap * 2 * nh, &m->pf_bg)) ||
+      (rc = dev_alloc_t(m, "prefill_q", (size_t)cap * ah * hd, &m->pf_q)) ||
+      (rc = dev_alloc_t(m, "prefill_scratch", (size_t)nh * nchunk * kGdnScratchPerChunk, &m->pf_scr)))
+    return rc;
+  m->pf_cap = cap;
+  m->pf_ldy = ldy;
+  m->pf_lda = lda;
+  return Q35_OK;
+}
+
+// One pass over T <= pf_cap prompt tokens ids[0..T) at positions p0..p0+T-1: every layer on all
+// T rows (GEMM projections on the matrix cores, conv + chunked delta rule, causal attention),
+// then the final norm and the tied lm_head for the last row only (the only logits the greedy
+// loop reads, main.rs:93-95), whose argmax goes to the token slot and hist[p0+T-1].
+int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st) {
+  const q35_dims& d = m->d;
+  const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
+  const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  const int LDY = m->pf_ldy;
+  int rc;
+  if ((rc = embed_launch(m->embed.q, m->embed.s, d.vocab, H, ids, T, m->pf_x, st))) return rc;
+  auto seg = [](const q35_model::Q8& w, float* y, int ldy) {
+    return GemmSeg{w.q, w.s, y, w.cols, Q35_KN_TILED, ldy};
+  };
+  for (int l = 0; l < d.n_layers; ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st))) return rc;
+    if (!L.full) {
+      GemmCall g;
+      g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
+      g.seg[0] = seg(L.qkv, m->pf_y, LDY);
+      g.seg[1] = seg(L.z, m->pf_y + conv_dim, LDY);
+      if ((rc = gemm_launch(g, st))) return rc;
+      if ((rc = gate_proj_simple_launch(m->pf_xn, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st, 1))) return rc;
+      GdnPrefill gp;
+      gp.raw = m->pf_y; gp.ld_raw = LDY; gp.conv_state = L.conv_state; gp.conv_state_out = L.conv_state;
+      gp.conv_w = L.conv_w; gp.bg = m->pf_bg; gp.ld_bg = 2 * nh; gp.scr = m->pf_scr; gp.S = L.rec;
+      gp.out = m->pf_core; gp.ld_out = vdim; gp.T = T; gp.nh = nh; gp.key_dim = key_dim;
+      gp.nchunk = (T + kGdnChunk - 1) / kGdnChunk; gp.qscale = powf((float)d.lin_dk, -0.5f);
+      if ((rc = gdn_prefill_launch(gp, st))) return rc;
+      if ((rc = gated_norm_rows_launch(m->pf_core, vdim, m->pf_y + conv_dim, LDY, L.norm_w, T, nh, d.eps, m->pf_a, vdim, st)))
+        return rc;
+      GemmCall o;
+      o.x = m->pf_a; o.ldx = vdim; o.M = T; o.K = vdim; o.nseg = 1; o.accumulate = 1;
+      o.seg[0] = seg(L.out, m->pf_x, H);
+      if ((rc = gemm_launch(o, st))) return rc;
+    } else {
+      const int qw = ah * hd * 2, kvw = kvh * hd;
+      GemmCall g;
+      g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 3;
+      g.seg[0] = seg(L.q, m->pf_y, LDY);
+      g.seg[1] = seg(L.k, m->pf_y + qw, LDY);
+      g.seg[2] = seg(L.v, m->pf_y + qw + kvw, LDY);
+      if ((rc = gemm_launch(g, st))) return rc;
+      AttnPrefill ap;
+      ap.qg = m->pf_y; ap.ld_qg = LDY; ap.k = m->pf_y + qw; ap.v = m->pf_y + qw + kvw; ap.ld_kv = LDY;
+      ap.qnw = L.q_norm; ap.knw = L.k_norm; ap.eps = d.eps; ap.rcos = m->rope_cos; ap.rsin = m->rope_sin;
+      ap.rot = d.rot_dim; ap.kc = L.kc; ap.vc = L.vc; ap.tmax = m->tmax; ap.p0 = p0; ap.T = T; ap.nh = ah;
+      ap.nkv = kvh; ap.qbuf = m->pf_q; ap.out = m->pf_a; ap.ld_out = ah * hd;
+      ap.scale = (float)(1.0 / sqrt((double)hd));
+      if ((rc = attn_prefill_launch(ap, st))) return rc;
+      GemmCall o;
+      o.x = m->pf_a; o.ldx = ah * hd; o.M = T; o.K = ah * hd; o.nseg = 1; o.accumulate = 1;
+      o.seg[0] = seg(L.o, m->pf_x, H);
+      if ((rc = gemm_launch(o, st))) return rc;
+    }
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st))) return rc;
+    GemmCall g;
+    g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
+    g.seg[0] = seg(L.gate, m->pf_y, LDY);
+    g.seg[1] = seg(L.up, m->pf_y + F, LDY);
+    if ((rc = gemm_launch(g, st))) return rc;
+    if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st))) return rc;
+    GemmCall dn;
+    dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
+    dn.seg[0] = seg(L.down, m->pf_x, H);
+    if ((rc = gemm_launch(dn, st))) return rc;
+  }
+  if ((rc = store_i32_launch(m->pos, p0 + T - 1, st))) return rc;
+  NkCall n;
+  n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = 1;
+  n.x = m->pf_x + (size_t)(T - 1) * H; n.ldx = H; n.y = m->logits; n.ldy = d.vocab; n.pro = PRO_RMS;
+  n.pw = m->final_norm; n.eps = d.eps;
+  n.argmax_out = m->token; n.pos_inc = m->pos; n.hist = m->hist;
+  return nk_launch(n, m->ws, m->ws_bytes, st);
+}
+
+// The n prompt ids already in m->prompt[host_pos..) through the prompt path, in passes.
+int prefill(q35_model* m, int n, hipStream_t st) {
+  int rc;
+  if ((rc = ensure_prefill(m))) return rc;
+  if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_prefill: tmax too small");
+  for (int done = 0; done < n;) {
+    const int T = std::min(m->pf_cap, n - done);
+    if ((rc = prefill_pass(m, m->prompt + m->host_pos, T, m->host_pos, st))) return rc;
+    m->host_pos += T;
+    done += T;
+  }
+  return Q35_OK;
+}
+
 // Reads the persistent kernel's sticky error word (synchronises the stream).
 int check_persistent(q35_model* m, hipStream_t st) {
   if (m->step_rc != Q35_OK) return Q35_OK;
@@ -556,6 +679,9 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
                        int32_t* out_tokens_host, int32_t use_graph, int32_t readback_each,
                        double* decode_seconds_host, void* stream) {
   if (!m || !prompt_host || !out_tokens_host) return fail(Q35_E_ARG, "model_generate: null pointer");
+  const bool gemm_prefill = (use_graph & Q35_PREFILL_GEMM) != 0;
+  use_graph &= ~Q35_PREFILL_GEMM;
+  if (use_graph < Q35_LAUNCH_STREAM || use_graph > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_generate: bad launch mode");
   if (n_prompt < 1 || n_new < 0) return fail(Q35_E_SHAPE, "model_generate: need n_prompt >= 1, n_new >= 0");
   const int32_t p0 = m->host_pos;
   if ((int64_t)p0 + n_prompt + n_new > m->tmax) return fail(Q35_E_SHAPE, "model_generate: tmax too small");
@@ -570,7 +696,9 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
   int rc;
   const bool pers = (use_graph == Q35_LAUNCH_PERSISTENT);
   if (use_graph == Q35_LAUNCH_GRAPH && (rc = capture(m, st))) return rc;
-  if (pers) {
+  if (gemm_prefill) {
+    if ((rc = prefill(m, n_prompt, st))) return rc;
+  } else if (pers) {
     if ((rc = persistent(m, n_prompt, st))) return rc;
   } else {
     for (int i = 0; i < n_prompt; ++i)
@@ -601,6 +729,8 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
                              const int32_t* stop_ids_host, int32_t n_stop, int32_t* out_tokens_host,
                              int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host, void* stream) {
   if (!m || !prompt_host || !out_tokens_host || !n_out_host) return fail(Q35_E_ARG, "model_generate_until: null pointer");
+  const bool gemm_prefill = (use_graph & Q35_PREFILL_GEMM) != 0;
+  use_graph &= ~Q35_PREFILL_GEMM;
   if (n_stop < 0 || n_stop > Q35_MAX_STOP_IDS || (n_stop > 0 && !stop_ids_host))
     return fail(Q35_E_ARG, "model_generate_until: between 0 and 4 stop ids");
   if (use_graph < Q35_LAUNCH_STREAM || use_graph > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_generate_until: bad launch mode");
@@ -619,7 +749,9 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
   int rc;
   const bool pers = (use_graph == Q35_LAUNCH_PERSISTENT);
   if (use_graph == Q35_LAUNCH_GRAPH && (rc = capture(m, st))) return rc;
-  if (pers) {
+  if (gemm_prefill) {
+    if ((rc = prefill(m, n_prompt, st))) return rc;
+  } else if (pers) {
     if ((rc = persistent(m, n_prompt, st))) return rc;
   } else {
     for (int i = 0; i < n_prompt; ++i)
@@ -655,6 +787,23 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
   Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + pe - 1, sizeof(int32_t) * (produced + 1), hipMemcpyDeviceToHost));
   *n_out_host = produced;
   return Q35_OK;
+}
+
+int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, void* stream) {
+  if (!m || !prompt_host) return fail(Q35_E_ARG, "model_prefill: null pointer");
+  if (n_prompt < 1) return fail(Q35_E_SHAPE, "model_prefill: need n_prompt >= 1");
+  const int32_t p0 = m->host_pos;
+  if ((int64_t)p0 + n_prompt > m->tmax) return fail(Q35_E_SHAPE, "model_prefill: tmax too small");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt_host[i] < 0 || prompt_host[i] >= m->d.vocab) return fail(Q35_E_ARG, "model_prefill: prompt id out of range");
+  hipStream_t st = pick(m, stream);
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  Q35_HIP_TRY(hipMemcpyAsync(m->prompt + p0, prompt_host, sizeof(int32_t) * n_prompt, hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  m->pinned[0] = p0 + n_prompt;
+  Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  return prefill(m, n_prompt, st);
 }
 
 int q35_model_position(q35_model* m, int32_t* pos_out) {

@@ -1,0 +1,511 @@
+// Prompt (seq_len > 1) kernels besides the GEMM: row RMSNorm, the Gated DeltaNet prompt path
+// (causal conv over the prompt continuing the cached state, then the chunked gated delta rule
+// in two launches), gated RMSNorm, SwiGLU, and the attention prompt path (q/k norms, RoPE and
+// KV append, then causal attention over the cache).
+//
+// Chunked gated delta rule (burn_chunk_gated_delta_rule, text_modules.rs:189-363; chunk 64,
+// :640).  Everything that does not involve the recurrent state is independent per chunk, so
+// the first launch (gdn_chunk_prep) runs one block per (chunk, head) in parallel: conv + SiLU of
+// the head's q/k/v channels (:164-182 with the cached state prepended, :531-554), l2norm and
+// the 128^-1/2 query scale (:219-223), cumulative decay, the strictly lower system
+// -(k_beta k^T) * exp(cum_i - cum_j) and its forward substitution (:282-296), then
+// new_values = U (v beta), k_cumdecay = U (k beta e^cum), the intra-chunk attention
+// (q k^T) * exp(cum_i - cum_j) (j <= i), q e^cum, k e^(cum_last - cum) and e^cum_last; all go to
+// a scratch buffer.  The second launch (gdn_chunk_state) walks the chunks in order (:313-349):
+// the state's value columns are independent, so one block per (head, 16-column slice) keeps its
+// S[:, slice] in LDS and per chunk forms v_new = new_values - k_cumdecay S, the output
+// q_e S + intra v_new, and S = S e^cum_last + k_d^T v_new.
+#include "q35_internal.h"
+
+#include <cmath>
+
+namespace q35 {
+namespace {
+
+constexpr int kPT = 256;
+constexpr int kC = kGdnChunk;     // 64
+constexpr int kDk = 128;          // key and value head dim
+constexpr int kLdq = kDk + 4;     // padded LDS row (floats)
+constexpr int kSl = 16;           // value columns per state-pass block
+constexpr int kNsl = kDk / kSl;   // 8 slices per head
+// scratch per (head, chunk)
+constexpr int kScrNv = 0, kScrKcd = kC * kDk, kScrQe = 2 * kC * kDk, kScrKd = 3 * kC * kDk;
+constexpr int kScrIntra = 4 * kC * kDk, kScrCd = kScrIntra + kC * kC;
+static_assert(kScrCd + 64 == kGdnScratchPerChunk, "scratch layout");
+
+// y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808)
+__global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, int K, const float* w, float eps,
+                                                       float* y, int ldy) {
+  __shared__ float sh[4];
+  const int m = blockIdx.x;
+  const float* xr = x + (int64_t)m * ldx;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < K; k += kPT) {
+    const float v = xr[k];
+    ss += v * v;
+  }
+  ss = block_sum256(ss, sh);
+  const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
+  float* yr = y + (int64_t)m * ldy;
+  for (int k = threadIdx.x; k < K; k += kPT) yr[k] = (xr[k] * r) * (1.0f + w[k]);
+}
+
+// ------------------------------------------------------------------ Gated DeltaNet, prompt
+__global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a) {
+  __shared__ __align__(16) float Qs[kC][kLdq];
+  __shared__ __align__(16) float Ks[kC][kLdq];
+  __shared__ __align__(16) float Vs[kC][kLdq];
+  __shared__ float U[kC][kC + 1];
+  __shared__ float cum[kC], bet[kC], ecum[kC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = blockIdx.x % a.nchunk, h = blockIdx.x / a.nchunk;
+  const int t0 = c * kC;
+  float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
+
+  // causal conv (cached state prepended) + SiLU of the head's 3 x 128 channels
+  for (int e = tid; e < kC * 3 * kDk; e += kPT) {
+    const int i = e / (3 * kDk), j = e - i * 3 * kDk;
+    const int part = j >> 7, jj = j & 127;
+    const int ch = part == 0 ? h * kDk + jj : (part == 1 ? a.key_dim + h * kDk + jj : 2 * a.key_dim + h * kDk + jj);
+    const int t = t0 + i;
+    float v = 0.f;
+    if (t < a.T) {
+      float x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int tt = t - 3 + u;
+        x[u] = tt >= 0 ? a.raw[(int64_t)tt * a.ld_raw + ch] : a.conv_state[(int64_t)ch * 3 + 3 + tt];
+      }
+      const float* w = a.conv_w + (int64_t)ch * 4;
+      v = silu_f(((w[0] * x[0] + w[1] * x[1]) + w[2] * x[2]) + w[3] * x[3]);
+    }
+    (part == 0 ? Qs : (part == 1 ? Ks : Vs))[i][jj] = v;
+  }
+  if (tid < kC) {
+    const int t = t0 + tid;
+    bet[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + h] : 0.f;
+    cum[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + a.nh + h] : 0.f;  // g for now
+  }
+  __syncthreads();
+  // l2norm of q (times dk^-1/2) and k rows
+  for (int r = wid; r < 2 * kC; r += 4) {
+    float* row = r < kC ? Qs[r] : Ks[r - kC];
+    const float v0 = row[lane], v1 = row[lane + 64];
+    float rn = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) + 1e-6f);
+    if (r < kC) {
+      row[lane] = (v0 * rn) * a.qscale;
+      row[lane + 64] = (v1 * rn) * a.qscale;
+    } else {
+      row[lane] = v0 * rn;
+      row[lane + 64] = v1 * rn;
+    }
+  }
+  if (tid == 0) {  // cumulative decay inside the chunk (padded steps add 0)
+    float s = 0.f;
+    for (int i = 0; i < kC; ++i) {
+      s += cum[i];
+      cum[i] = s;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) ecum[tid] = expf(cum[tid]);
+  // U = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i (0 elsewhere); intra = (q_i.k_j) e^(cum_i - cum_j), j <= i
+  {
+    const int i = tid >> 2, jq = (tid & 3) * 16;
+    float dkk[16], dqk[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) { dkk[u] = 0.f; dqk[u] = 0.f; }
+    if (jq <= i) {
+      for (int e = 0; e < kDk; e += 4) {
+        const float4 ki = *(const float4*)&Ks[i][e];
+        const float4 qi = *(const float4*)&Qs[i][e];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const float4 kj = *(const float4*)&Ks[min(jq + u, kC - 1)][e];
+          dkk[u] += ((ki.x * kj.x + ki.y * kj.y) + ki.z * kj.z) + ki.w * kj.w;
+          dqk[u] += ((qi.x * kj.x + qi.y * kj.y) + qi.z * kj.z) + qi.w * kj.w;
+        }
+      }
+    }
+    float* intra = scr + kScrIntra + i * kC;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int j = jq + u;
+      const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
+      U[i][j] = j < i ? -((bet[i] * dkk[u]) * dec) : 0.f;
+      intra[j] = j <= i ? dqk[u] * dec : 0.f;
+    }
+  }
+  __syncthreads();
+  // forward substitution (rows in increasing order): U[i][j] += sum_{j<l<i} U[i][l] U[l][j]
+  if (wid == 0) {
+    for (int i = 2; i < kC; ++i) {
+      float s = 0.f;
+      for (int l = lane + 1; l < i; ++l) s += U[i][l] * U[l][lane];
+      if (lane < i) U[i][lane] += s;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) U[tid][tid] = 1.0f;
+  __syncthreads();
+  // new_values = U (beta v), k_cumdecay = U (beta e^cum k); q e^cum; k e^(cum_last - cum)
+  {
+    const int i = tid >> 2, d0 = (tid & 3) * 32;
+    float an[32], ak[32];
+#pragma unroll
+    for (int d = 0; d < 32; ++d) { an[d] = 0.f; ak[d] = 0.f; }
+    for (int l = 0; l <= i; ++l) {
+      const float ub = U[i][l] * bet[l];
+      const float ube = ub * ecum[l];
+#pragma unroll
+      for (int d = 0; d < 32; d += 4) {
+        const float4 v = *(const float4*)&Vs[l][d0 + d];
+        const float4 k = *(const float4*)&Ks[l][d0 + d];
+        an[d] += ub * v.x; an[d + 1] += ub * v.y; an[d + 2] += ub * v.z; an[d + 3] += ub * v.w;
+        ak[d] += ube * k.x; ak[d + 1] += ube * k.y; ak[d + 2] += ube * k.z; ak[d + 3] += ube * k.w;
+      }
+    }
+    const float eq = ecum[i], ek = expf(cum[kC - 1] - cum[i]);
+    float* nv = scr + kScrNv + i * kDk + d0;
+    float* kcd = scr + kScrKcd + i * kDk + d0;
+    float* qe = scr + kScrQe + i * kDk + d0;
+    float* kd = scr + kScrKd + i * kDk + d0;
+#pragma unroll
+    for (int d = 0; d < 32; d += 4) {
+      *(float4*)(nv + d) = make_float4(an[d], an[d + 1], an[d + 2], an[d + 3]);
+      *(float4*)(kcd + d) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
+      const float4 q = *(const float4*)&Qs[i][d0 + d];
+      const float4 k = *(const float4*)&Ks[i][d0 + d];
+      *(float4*)(qe + d) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
+      *(float4*)(kd + d) = make_float4(k.x * ek, k.y * ek, k.z * ek, k.w * ek);
+    }
+    if (tid == 0) scr[kScrCd] = ecum[kC - 1];
+  }
+}
+
+__global__ __launch_bounds__(kPT) void gdn_chunk_state_kernel(const GdnPrefill a) {
+  __shared__ __align__(16) float Ss[kDk][kSl];
+  __shared__ __align__(16) float Kc[kC][kLdq];
+  __shared__ __align__(16) float Qe[kC][kLdq];
+  __shared__ __align__(16) float Kd[kC][kLdq];
+  __shared__ float In[kC][kC + 1];
+  __shared__ __align__(16) float Vn[kC][kSl];
+  __shared__ float cdv;
+
+  const int tid = threadIdx.x;
+  const int sl = blockIdx.x % kNsl, h = blockIdx.x / kNsl;
+  const int c0 = sl * kSl;
+  float* S = a.S + (int64_t)h * kDk * kDk;
+  // the new conv state of the head's channels: the last 3 inputs (older ones from the old state
+  // when the prompt is shorter than 3); the prep launch has read the old state already
+  if (sl == 0 && a.conv_state_out) {
+    for (int e = tid; e < 3 * kDk; e += kPT) {
+      const int part = e >> 7, jj = e & 127;
+      const int ch = part == 0 ? h * kDk + jj : (part == 1 ? a.key_dim + h * kDk + jj : 2 * a.key_dim + h * kDk + jj);
+      float* st = a.conv_state_out + (int64_t)ch * 3;
+      float n[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int src = k + a.T;  // index into [old s0, s1, s2, x_0, x_1, ...]
+        n[k] = src < 3 ? st[src] : a.raw[(int64_t)(src - 3) * a.ld_raw + ch];
+      }
+      st[0] = n[0]; st[1] = n[1]; st[2] = n[2];
+    }
+  }
+  {
+    const int e = tid >> 1, j = (tid & 1) * 8;
+    const float* src = S + (int64_t)e * kDk + c0 + j;
+    *(float4*)&Ss[e][j] = *(const float4*)src;
+    *(float4*)&Ss[e][j + 4] = *(const float4*)(src + 4);
+  }
+  for (int c = 0; c < a.nchunk; ++c) {
+    const float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
+    for (int e = tid; e < kC * kDk / 4; e += kPT) {
+      const int i = e >> 5, d = (e & 31) * 4;
+      *(float4*)&Kc[i][d] = *(const float4*)(scr + kScrKcd + i * kDk + d);
+      *(float4*)&Qe[i][d] = *(const float4*)(scr + kScrQe + i * kDk + d);
+      *(float4*)&Kd[i][d] = *(const float4*)(scr + kScrKd + i * kDk + d);
+    }
+    for (int e = tid; e < kC * kC; e += kPT) In[e >> 6][e & 63] = scr[kScrIntra + e];
+    {
+      const int i = tid >> 2, j = (tid & 3) * 4;
+      *(float4*)&Vn[i][j] = *(const float4*)(scr + kScrNv + i * kDk + c0 + j);
+    }
+    if (tid == 0) cdv = scr[kScrCd];
+    __syncthreads();
+    const int i = tid >> 2, j = (tid & 3) * 4;
+    {  // v_new = new_values - k_cumdecay S
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      for (int e = 0; e < kDk; ++e) {
+        const float k = Kc[i][e];
+        const float4 sv = *(const float4*)&Ss[e][j];
+        s0 += k * sv.x; s1 += k * sv.y; s2 += k * sv.z; s3 += k * sv.w;
+      }
+      float4 nv = *(const float4*)&Vn[i][j];
+      nv.x -= s0; nv.y -= s1; nv.z -= s2; nv.w -= s3;
+      *(float4*)&Vn[i][j] = nv;
+    }
+    __syncthreads();
+    {  // out = q_e S + intra v_new
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+      for (int e = 0; e < kDk; ++e) {
+        const float q = Qe[i][e];
+        const float4 sv = *(const float4*)&Ss[e][j];
+        o0 += q * sv.x; o1 += q * sv.y; o2 += q * sv.z; o3 += q * sv.w;
+      }
+      float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+      for (int l = 0; l <= i; ++l) {
+        const float w = In[i][l];
+        const float4 v = *(const float4*)&Vn[l][j];
+        p0 += w * v.x; p1 += w * v.y; p2 += w * v.z; p3 += w * v.w;
+      }
+      const int t = c * kC + i;
+      if (t < a.T) *(float4*)(a.out + (int64_t)t * a.ld_out + h * kDk + c0 + j) = make_float4(o0 + p0, o1 + p1, o2 + p2, o3 + p3);
+    }
+    __syncthreads();
+    {  // S = S e^cum_last + k_d^T v_new
+      const int e = tid >> 1, jj = (tid & 1) * 8;
+      const float cd = cdv;
+      float s[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s[u] = Ss[e][jj + u] * cd;
+      for (int l = 0; l < kC; ++l) {
+        const float k = Kd[l][e];
+        const float4 va = *(const float4*)&Vn[l][jj];
+        const float4 vb = *(const float4*)&Vn[l][jj + 4];
+        s[0] += k * va.x; s[1] += k * va.y; s[2] += k * va.z; s[3] += k * va.w;
+        s[4] += k * vb.x; s[5] += k * vb.y; s[6] += k * vb.z; s[7] += k * vb.w;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) Ss[e][jj + u] = s[u];
+    }
+    __syncthreads();
+  }
+  {
+    const int e = tid >> 1, j = (tid & 1) * 8;
+    float* dst = S + (int64_t)e * kDk + c0 + j;
+    *(float4*)dst = *(const float4*)&Ss[e][j];
+    *(float4*)(dst + 4) = *(const float4*)&Ss[e][j + 4];
+  }
+}
+
+// out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100)
+__global__ __launch_bounds__(kPT) void gated_norm_rows_kernel(const float* o, int ldo, const float* z, int ldz,
+                                                              const float* w, int nh, float eps, float* out,
+                                                              int ldout) {
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int h = wid; h < nh; h += 4) {
+    const float* orow = o + (int64_t)t * ldo + h * kDk;
+    const float* zrow = z + (int64_t)t * ldz + h * kDk;
+    const float v0 = orow[lane], v1 = orow[lane + 64];
+    const float r = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) / (float)kDk + eps);
+    float* dst = out + (int64_t)t * ldout + h * kDk;
+    dst[lane] = (w[lane] * (v0 * r)) * silu_f(zrow[lane]);
+    dst[lane + 64] = (w[lane + 64] * (v1 * r)) * silu_f(zrow[lane + 64]);
+  }
+}
+
+// out[t][k] = up * silu(gate): gu = [gate (F) | up (F)] per row (text_modules.rs:1000-1011)
+__global__ __launch_bounds__(kPT) void swiglu_rows_kernel(const float* gu, int ldgu, int F, float* out, int ldout) {
+  const int t = blockIdx.y;
+  for (int k = blockIdx.x * kPT + threadIdx.x; k < F; k += gridDim.x * kPT) {
+    const float* r = gu + (int64_t)t * ldgu;
+    out[(int64_t)t * ldout + k] = r[F + k] * silu_f(r[k]);
+  }
+}
+
+// ------------------------------------------------------------------ attention, prompt
+// Block (t, slot): slot < nh normalises and rotates query head `slot` into qbuf[t][slot]; slot
+// nh + g does kv head g: k_norm + RoPE into the K cache row p0 + t, v copied to the V cache.
+__global__ __launch_bounds__(kPT) void attn_prefill_prep_kernel(const AttnPrefill a) {
+  __shared__ float sh[4];
+  __shared__ float xs[kHdP];
+  const int t = blockIdx.x / (a.nh + a.nkv), slot = blockIdx.x % (a.nh + a.nkv);
+  const int tid = threadIdx.x;
+  const int pos = a.p0 + t;
+  const float* src;
+  const float* nw;
+  if (slot < a.nh) {
+    src = a.qg + (int64_t)t * a.ld_qg + (int64_t)slot * 2 * kHdP;
+    nw = a.qnw;
+  } else {
+    src = a.k + (int64_t)t * a.ld_kv + (int64_t)(slot - a.nh) * kHdP;
+    nw = a.knw;
+  }
+  const float v = src[tid];
+  const float ss = block_sum256(v * v, sh);
+  const float r = rsqrt_f(ss / (float)kHdP + a.eps);
+  xs[tid] = (v * r) * (1.0f + nw[tid]);
+  __syncthreads();
+  float y = xs[tid];
+  if (tid < a.rot) {
+    const int half = a.rot / 2;
+    const float rh = tid < half ? -xs[tid + half] : xs[tid - half];
+    y = xs[tid] * a.rcos[(int64_t)pos * a.rot + tid] + rh * a.rsin[(int64_t)pos * a.rot + tid];
+  }
+  if (slot < a.nh) {
+    a.qbuf[((int64_t)t * a.nh + slot) * kHdP + tid] = y;
+  } else {
+    const int g = slot - a.nh;
+    const int64_t row = ((int64_t)g * a.tmax + pos) * kHdP;
+    a.kc[row + tid] = y;
+    a.vc[row + tid] = a.v[(int64_t)t * a.ld_kv + (int64_t)g * kHdP + tid];
+  }
+}
+
+// Causal GQA attention of the prompt rows.  Block (query tile, kv head g): 64 rows = QT tokens x
+// rep query heads of g; thread (row r = tid/4, quarter qd = tid%4) holds dims [64 qd, 64 qd + 64)
+// of its row's query and output.  Keys stream through LDS 32 at a time (rows padded per
+// quarter so the four quarters' reads fall in different banks); a score is the sum of the four
+// quarters' partial dots; online softmax in log2 units, rescaled once per 8 keys.
+constexpr int kKT = 32;            // keys per LDS tile
+constexpr int kQLd = 68;           // floats per quarter row in LDS (64 + 4)
+__global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) {
+  __shared__ __align__(16) float Ks[kKT][4 * kQLd];
+  __shared__ __align__(16) float Vs[kKT][4 * kQLd];
+  const int tid = threadIdx.x;
+  const int rep = a.nh / a.nkv, QT = 64 / rep;
+  const int qt = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
+  const int r = tid >> 2, qd = tid & 3;
+  const int t = qt * QT + r / rep, hq = g * rep + r % rep;
+  const bool row_ok = t < a.T;
+  const int lim = a.p0 + (row_ok ? t : 0);  // last key this row may see
+  const int tmax_blk = min(a.T, (qt + 1) * QT) - 1;
+  const int nkeys = a.p0 + tmax_blk + 1;
+  float q[64], acc[64];
+  const float* qsrc = a.qbuf + ((int64_t)(row_ok ? t : 0) * a.nh + hq) * kHdP + qd * 64;
+#pragma unroll
+  for (int d = 0; d < 64; d += 4) {
+    const float4 v = *(const float4*)(qsrc + d);
+    q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
+    acc[d] = 0.f; acc[d + 1] = 0.f; acc[d + 2] = 0.f; acc[d + 3] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const float sl2 = a.scale * 1.44269504088896341f;
+  const float* Kg = a.kc + (int64_t)g * a.tmax * kHdP;
+  const float* Vg = a.vc + (int64_t)g * a.tmax * kHdP;
+  for (int k0 = 0; k0 < nkeys; k0 += kKT) {
+    __syncthreads();
+    for (int e = tid; e < kKT * kHdP / 4; e += kPT) {
+      const int j = e >> 6, d = (e & 63) * 4;
+      const int kj = min(k0 + j, nkeys - 1);
+      const int o = (d >> 6) * kQLd + (d & 63);
+      *(float4*)&Ks[j][o] = *(const float4*)(Kg + (int64_t)kj * kHdP + d);
+      *(float4*)&Vs[j][o] = *(const float4*)(Vg + (int64_t)kj * kHdP + d);
+    }
+    __syncthreads();
+    for (int jb = 0; jb < kKT; jb += 8) {
+      float s[8];
+      float bm = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float* kr = &Ks[jb + u][qd * kQLd];
+        float p = 0.f;
+#pragma unroll
+        for (int d = 0; d < 64; d += 4) {
+          const float4 kv = *(const float4*)(kr + d);
+          p += ((q[d] * kv.x + q[d + 1] * kv.y) + q[d + 2] * kv.z) + q[d + 3] * kv.w;
+        }
+        p += __shfl_xor(p, 1, 64);
+        p += __shfl_xor(p, 2, 64);
+        const int kj = k0 + jb + u;
+        s[u] = (kj <= lim) ? p * sl2 : -INFINITY;
+        bm = fmaxf(bm, s[u]);
+      }
+      const float mn = fmaxf(m, bm);
+      if (mn == -INFINITY) continue;  // nothing visible yet for this row
+      const float al = __builtin_amdgcn_exp2f(m - mn);
+      l *= al;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) acc[d] *= al;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float p = __builtin_amdgcn_exp2f(s[u] - mn);
+        l += p;
+        const float* vr = &Vs[jb + u][qd * kQLd];
+#pragma unroll
+        for (int d = 0; d < 64; d += 4) {
+          const float4 vv = *(const float4*)(vr + d);
+          acc[d] += p * vv.x; acc[d + 1] += p * vv.y; acc[d + 2] += p * vv.z; acc[d + 3] += p * vv.w;
+        }
+      }
+      m = mn;
+    }
+  }
+  if (!row_ok) return;
+  const float* gate = a.qg + (int64_t)t * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + qd * 64;
+  float* dst = a.out + (int64_t)t * a.ld_out + (int64_t)hq * kHdP + qd * 64;
+#pragma unroll
+  for (int d = 0; d < 64; d += 4) {
+    const float4 gv = *(const float4*)(gate + d);
+    *(float4*)(dst + d) = make_float4((acc[d] / l) * sigmoid_f(gv.x), (acc[d + 1] / l) * sigmoid_f(gv.y),
+                                      (acc[d + 2] / l) * sigmoid_f(gv.z), (acc[d + 3] / l) * sigmoid_f(gv.w));
+  }
+}
+
+__global__ void store_i32_kernel(int32_t* p, int32_t v) {
+  if (threadIdx.x == 0) *p = v;
+}
+
+}  // namespace
+
+int store_i32_launch(int32_t* p, int32_t v, hipStream_t st) {
+  hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(64), 0, st, p, v);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
+                    hipStream_t st) {
+  if (M < 1) return Q35_OK;
+  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st) {
+  if (!a.raw || !a.conv_state || !a.conv_w || !a.bg || !a.scr || !a.S || !a.out) return fail(Q35_E_ARG, "gdn_prefill: null pointer");
+  if (a.T < 1 || a.nh < 1 || a.nchunk != (a.T + kC - 1) / kC) return fail(Q35_E_SHAPE, "gdn_prefill: bad T / chunks");
+  if ((a.ld_out % 4) != 0) return fail(Q35_E_ALIGN, "gdn_prefill: output rows must be 16-byte aligned");
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(a.nchunk * a.nh), dim3(kPT), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(gdn_chunk_state_kernel, dim3(kNsl * a.nh), dim3(kPT), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, const float* w, int T, int nh, float eps,
+                           float* out, int ldout, hipStream_t st) {
+  if (T < 1) return Q35_OK;
+  hipLaunchKernelGGL(gated_norm_rows_kernel, dim3(T), dim3(kPT), 0, st, o, ldo, z, ldz, w, nh, eps, out, ldout);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st) {
+  if (T < 1) return Q35_OK;
+  const int gx = std::min((F + kPT - 1) / kPT, 8);
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(gx, T), dim3(kPT), 0, st, gu, ldgu, F, out, ldout);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int attn_prefill_launch(const AttnPrefill& a, hipStream_t st) {
+  if (!a.qg || !a.k || !a.v || !a.qnw || !a.knw || !a.rcos || !a.rsin || !a.kc || !a.vc || !a.qbuf || !a.out)
+    return fail(Q35_E_ARG, "attention prefill: null pointer");
+  if (a.T < 1) return Q35_OK;
+  if (a.nkv < 1 || a.nh % a.nkv != 0 || 64 % (a.nh / a.nkv) != 0) return fail(Q35_E_SHAPE, "attention prefill: heads");
+  if (a.p0 < 0 || (int64_t)a.p0 + a.T > a.tmax) return fail(Q35_E_SHAPE, "attention prefill: positions past tmax");
+  if (a.rot < 2 || a.rot > kHdP || (a.rot % 2) != 0) return fail(Q35_E_SHAPE, "attention prefill: rotary dims");
+  if ((a.ld_qg % 4) != 0 || (a.ld_out % 4) != 0) return fail(Q35_E_ALIGN, "attention prefill: row alignment");
+  hipLaunchKernelGGL(attn_prefill_prep_kernel, dim3(a.T * (a.nh + a.nkv)), dim3(kPT), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  const int QT = 64 / (a.nh / a.nkv);
+  const int nqt = (a.T + QT - 1) / QT;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(nqt * a.nkv), dim3(kPT), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+}  // namespace q35

@@ -358,6 +358,29 @@ int mvp_launch(const int8_t* q, const float* s, int32_t K, int32_t N, const floa
 int fx_to_f32_launch(fx_t* acc, int64_t n, float* y, bool zero_after, hipStream_t st);
 int fx_zero_launch(fx_t* acc, int64_t n, hipStream_t st);
 
+// ------------------------------------------------------------------ Q8F GEMM (prompt projections)
+// Y[m][n] (+)= X[m][:] . dequant(W)[:, n] on the fp32 matrix cores; up to kGemmMaxSeg weight
+// matrices over the same X, each writing its own columns of Y.
+constexpr int kGemmMaxSeg = 4;
+struct GemmSeg {
+  const int8_t* q;
+  const float* s;
+  float* y;        // y[m*ldy + n]
+  int32_t N;       // columns (multiple of 64)
+  int32_t layout;  // Q35_KN, Q35_KN_TILED (rows = K) or Q35_NK (rows = N)
+  int32_t ldy;
+};
+struct GemmCall {
+  GemmSeg seg[kGemmMaxSeg];
+  int32_t nseg = 0;
+  const float* x = nullptr;  // [M][ldx], 16-byte aligned rows
+  int32_t ldx = 0, M = 0, K = 0;
+  int32_t accumulate = 0;    // 1: y += result (each element owned by one block), 0: y = result
+};
+int gemm_launch(const GemmCall& c, hipStream_t st);
+// Tile shape the launcher picks for c (BM x BN).
+int gemm_pick(const GemmCall& c, int* bm, int* bn);
+
 // ------------------------------------------------------------------ Q8F NK matvec / lm_head
 struct NkCall {
   const int8_t* q;  // [N][K]
@@ -412,8 +435,10 @@ int gdn_step_launch(const GdnCall& c, hipStream_t st);
 int conv_shift_launch(float* state, const float* x, int32_t B, int32_t ch, hipStream_t st);
 
 // Gate projection without workspace: one block per batch row.
+// input_rule: softplus threshold on its input (the prompt path) instead of its result (decode).
 int gate_proj_simple_launch(const float* x, int32_t B, int32_t in_dim, const float* wb, const float* wa,
-                            const float* alog, const float* dtb, int32_t nh, float* out, hipStream_t st);
+                            const float* alog, const float* dtb, int32_t nh, float* out, hipStream_t st,
+                            int32_t input_rule = 0);
 
 // Gated-RMSNorm alone is folded into the out_proj prologue (PRO_GATED).
 
@@ -436,6 +461,49 @@ size_t attn_ws_bytes(int32_t B, int32_t nh, int32_t nkv, int32_t hd, int32_t tma
 int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st);
 // same, with the completion counters and the chunk-partial scratch given separately
 int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size_t scratch_bytes, hipStream_t st);
+
+// ------------------------------------------------------------------ prompt (seq_len > 1) path
+// *p = v on the stream (a kernel, so it can sit in a captured graph)
+int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);
+// y[m] = RMSNorm(x[m]) * (1 + w) for M rows of K
+int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
+                    hipStream_t st);
+// Gated DeltaNet over a prompt of T tokens (dk = dv = 128): causal conv continuing conv_state,
+// chunked gated delta rule continuing S.  scr: nh * nchunk * kGdnScratchPerChunk floats.
+constexpr int kGdnChunk = 64;
+constexpr int kGdnScratchPerChunk = 4 * 64 * 128 + 64 * 64 + 64;
+struct GdnPrefill {
+  const float* raw = nullptr; int32_t ld_raw = 0;  // pre-conv q|k|v [T][conv_dim] (row stride ld_raw)
+  const float* conv_state = nullptr;               // [conv_dim][3] before the prompt
+  float* conv_state_out = nullptr;                 // written with the state after it (may alias)
+  const float* conv_w = nullptr;                   // [conv_dim][4]
+  const float* bg = nullptr; int32_t ld_bg = 0;    // [T][2 nh]: beta | g
+  float* scr = nullptr;
+  float* S = nullptr;                              // [nh][128][128], updated
+  float* out = nullptr; int32_t ld_out = 0;        // [T][nh*128] core output (before the gated norm)
+  int32_t T = 0, nh = 0, key_dim = 0, nchunk = 0;
+  float qscale = 0.f;
+};
+int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st);
+// out[t][h*128 + i] = (w[i] * (o * rsqrt(mean(o^2) + eps))) * silu(z), per 128-wide head
+int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, const float* w, int T, int nh, float eps,
+                           float* out, int ldout, hipStream_t st);
+// out[t][k] = gu[t][F + k] * silu(gu[t][k])
+int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st);
+// Attention over a prompt of T tokens at positions p0..p0+T-1 (head_dim 256, one sequence).
+constexpr int kHdP = 256;
+struct AttnPrefill {
+  const float* qg = nullptr; int32_t ld_qg = 0;  // q_proj rows, per head [query | gate]
+  const float* k = nullptr; const float* v = nullptr; int32_t ld_kv = 0;
+  const float* qnw = nullptr; const float* knw = nullptr; float eps = 1e-6f;
+  const float* rcos = nullptr; const float* rsin = nullptr; int32_t rot = 0;
+  float* kc = nullptr; float* vc = nullptr; int32_t tmax = 0;  // [nkv][tmax][256]
+  int32_t p0 = 0, T = 0, nh = 0, nkv = 0;
+  float* qbuf = nullptr;                        // scratch [T][nh][256]
+  float* out = nullptr; int32_t ld_out = 0;     // [T][nh*256]
+  float scale = 0.0625f;
+};
+int attn_prefill_launch(const AttnPrefill& a, hipStream_t st);
 
 // ------------------------------------------------------------------ persistent decode step
 // Per-layer pointers of the persistent decode-step kernel (Q8F projections in Q35_KN_TILED).

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "libq35.so")
 Q35_OK, Q35_E_SHAPE, Q35_E_ALIGN, Q35_E_HIP, Q35_E_ARG, Q35_E_WS, Q35_E_NOMEM = range(7)
 Q35_KN, Q35_NK, Q35_KN_TILED, Q35_KN_PANEL = 0, 1, 2, 3
 Q35_LAUNCH_STREAM, Q35_LAUNCH_GRAPH, Q35_LAUNCH_PERSISTENT = 0, 1, 2
+Q35_PREFILL_GEMM = 0x100
 ERROR_NAMES = {1: "Q35_E_SHAPE", 2: "Q35_E_ALIGN", 3: "Q35_E_HIP", 4: "Q35_E_ARG", 5: "Q35_E_WS", 6: "Q35_E_NOMEM"}
 
 c_i32, c_i64, c_u64, c_f32, c_sz, c_vp = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float,
@@ -71,6 +72,14 @@ PROTOTYPES = {
     "q35_layer_ws_bytes": (c_sz, [ctypes.POINTER(Dims), c_i32, c_i32]),
     "q35_workspace_status": (ctypes.c_int, [c_vp, c_vp]),
     "q35_rope_tables": (ctypes.c_int, [ctypes.POINTER(Dims), c_i32, c_vp, c_vp]),
+    "q35_q8_gemm": (ctypes.c_int, [c_vp, c_i32, c_i32, Q8F, c_vp, c_i32, c_i32, c_vp]),
+    "q35_gate_proj_prompt": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "q35_gated_delta_rule_prefill": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
+                                                    c_i32, c_vp, c_sz, c_vp]),
+    "q35_gated_delta_rule_prefill_ws_bytes": (c_sz, [c_i32, c_i32]),
+    "q35_attention_core_prefill": (ctypes.c_int, [ctypes.POINTER(Dims), c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32,
+                                                  c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "q35_attention_prefill_ws_bytes": (c_sz, [ctypes.POINTER(Dims), c_i32]),
     "q35_model_create_synthetic": (ctypes.c_int, [ctypes.POINTER(Dims), c_u64, c_i32, ctypes.POINTER(c_vp)]),
     "q35_model_destroy": (ctypes.c_int, [c_vp]),
     "q35_model_reset": (ctypes.c_int, [c_vp, c_vp]),
@@ -83,6 +92,7 @@ PROTOTYPES = {
                                           ctypes.POINTER(ctypes.c_double), c_vp]),
     "q35_model_generate_until": (ctypes.c_int, [c_vp, c_vp, c_i32, c_i32, c_vp, c_i32, c_vp, ctypes.POINTER(c_i32),
                                                 c_i32, ctypes.POINTER(ctypes.c_double), c_vp]),
+    "q35_model_prefill": (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp]),
     "q35_model_position": (ctypes.c_int, [c_vp, ctypes.POINTER(c_i32)]),
     "q35_model_tensor": (ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_vp), ctypes.POINTER(c_sz)]),
     "q35_synth_normal": (ctypes.c_int, [c_u64, c_u64, c_i64, c_i64, c_f32, c_vp]),

@@ -78,18 +78,19 @@ class TextForCausalLM:
         """Synchronise and raise if a persistent launch failed."""
         L.check(L.lib().q35_model_check(self.h, stream))
 
-    def generate(self, prompt, n_new, use_graph=None, readback_each=False, mode=None, stream=None):
+    def generate(self, prompt, n_new, use_graph=None, readback_each=False, mode=None, stream=None, prefill=False):
         """Returns (tokens[n_new+1], decode_seconds): the argmax after the last prompt token,
-        then the argmax after each of n_new decode steps."""
+        then the argmax after each of n_new decode steps.  prefill=True feeds the prompt through
+        the prompt path (GEMMs, chunked delta rule) instead of one decode step per token."""
         p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
         out = np.zeros(n_new + 1, np.int32)
         secs = ctypes.c_double(0.0)
-        L.check(L.lib().q35_model_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data,
-                                           self._mode(mode, use_graph), 1 if readback_each else 0,
-                                           ctypes.byref(secs), stream))
+        m = self._mode(mode, use_graph) | (L.Q35_PREFILL_GEMM if prefill else 0)
+        L.check(L.lib().q35_model_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data, m,
+                                           1 if readback_each else 0, ctypes.byref(secs), stream))
         return out, secs.value
 
-    def generate_until(self, prompt, max_new, stop_ids=(), mode=None, stream=None):
+    def generate_until(self, prompt, max_new, stop_ids=(), mode=None, stream=None, prefill=False):
         """The chat loop's generation (main.rs:100-132): returns (produced, last, decode_seconds),
         `produced` the ids forwarded after the prompt (at most max_new) and `last` the id that
         ended the loop (a stop id, or the argmax after the last produced id)."""
@@ -98,11 +99,17 @@ class TextForCausalLM:
         out = np.zeros(max_new + 1, np.int32)
         n = ctypes.c_int32(0)
         secs = ctypes.c_double(0.0)
+        m = self._mode(mode, None) | (L.Q35_PREFILL_GEMM if prefill else 0)
         L.check(L.lib().q35_model_generate_until(self.h, p.ctypes.data, p.size, int(max_new),
                                                  s.ctypes.data if s.size else None, s.size, out.ctypes.data,
-                                                 ctypes.byref(n), self._mode(mode, None), ctypes.byref(secs),
-                                                 stream))
+                                                 ctypes.byref(n), m, ctypes.byref(secs), stream))
         return out[:n.value].copy(), int(out[n.value]), secs.value
+
+    def prefill(self, prompt, stream=None):
+        """Feeds the prompt as one forward at seq_len = len(prompt) (the prompt path); the argmax
+        after its last token is left in the token slot.  Asynchronous after the upload."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        L.check(L.lib().q35_model_prefill(self.h, p.ctypes.data, p.size, stream))
 
     def position(self):
         v = ctypes.c_int32(0)
