@@ -7,8 +7,9 @@ reference path timed on this host.
 
 Workload of the headline number: 24 layers (18 Gated DeltaNet + 6 gated GQA), hidden 2048, FFN
 6144, vocab 248320, tied embeddings, random-init weights N(0, 0.02) quantised to Q8F, seed 0; a
---prompt-token uniform random prompt is fed through the decode step, then --warmup untimed and
---steps timed greedy decode steps.  A step is one token through the whole model (embedding ->
+--prompt-token uniform random prompt is prefilled through the prompt path (Q8F GEMMs on the
+fp32 matrix cores, chunked gated delta rule, causal attention; timed and reported with the
+GEMMs' matrix-core utilisation), then --warmup untimed and --steps timed greedy decode steps.  A step is one token through the whole model (embedding ->
 24 layers -> final norm -> lm_head -> argmax) with weights and caches resident in HBM, run by the
 persistent step kernel in launches of at most --chunk steps (each step's argmax feeds the next on
 the device).  Exactly --steps steps are timed and exactly --warmup run before them.
@@ -220,6 +221,56 @@ def attn_leg(torch, q35, st):
     return out
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
+
+
+def prefill_gemm_leg(torch, q35, st, d, T):
+    """The prompt path's projection GEMMs for one T-token prompt through every layer
+    (q35_q8_gemm, fp32 matrix cores): per linear-attention layer in_proj_qkv|in_proj_z
+    [2048 -> 8192] and out_proj [2048 -> 2048], per attention layer q|k|v [2048 -> 5120] and
+    o_proj [2048 -> 2048], per layer gate|up [2048 -> 12288] and down_proj [6144 -> 2048], each
+    layer with weights of its own (Q35_KN_TILED, 1.46 GB in all), timed with HIP events around
+    the whole sequence.  Returns achieved TFLOP/s against the fp32 matrix-core peak."""
+    L = q35._lib
+    lib, sh = q35.lib(), st.cuda_stream
+    H, F = d.hidden, d.ffn
+    nh, vd = d.lin_heads, d.lin_heads * d.lin_dv
+    conv_dim = 2 * nh * d.lin_dk + vd
+    ah, kvh, hd = d.attn_heads, d.kv_heads, d.head_dim
+    calls, keep = [], []
+
+    def mat(K, N):
+        nt = (N + 255) // 256
+        q = torch.randint(-127, 128, (nt, K, 256), dtype=torch.int8, device="cuda")
+        s = torch.rand((nt, K, 4), device="cuda") * 1e-3
+        keep.append((q, s))
+        return L.Q8F(q.data_ptr(), s.data_ptr(), K, N, L.Q35_KN_TILED)
+
+    X = torch.randn(T, max(H, F, vd, ah * hd), device="cuda")
+    Y = torch.empty(T, max(conv_dim + vd, 2 * F, ah * hd * 2 + 2 * kvh * hd), device="cuda")
+    R = torch.zeros(T, H, device="cuda")
+    flops = 0
+    for l in range(d.n_layers):
+        full = (l + 1) % d.full_interval == 0
+        first = (H, ah * hd * 2 + 2 * kvh * hd) if full else (H, conv_dim + vd)
+        second = (ah * hd, H) if full else (vd, H)
+        for (K, N), acc in ((first, 0), (second, 1), ((H, 2 * F), 0), ((F, H), 1)):
+            calls.append((K, N, mat(K, N), acc))
+            flops += 2 * T * K * N
+
+    def run():
+        for K, N, W, acc in calls:
+            out = R if acc else Y
+            L.check(lib.q35_q8_gemm(X.data_ptr(), T, X.stride(0), W, out.data_ptr(), out.stride(0), acc, sh))
+    us = per_call_us(torch, st, run, 1, reps=3)
+    tf = flops / us / 1e6
+    del keep
+    torch.cuda.empty_cache()
+    return {"tokens": T, "gemm_calls": len(calls), "flop": flops, "us": round(us, 1), "TFLOP/s": round(tf, 1),
+            "peak": MFMA_FP32_PEAK_TFLOPS, "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+            "unit": "fp32 matrix-core TFLOP/s (f32 dequantised weights, f32 products and accumulation)"}
+
+
 def cpu_model_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -304,6 +355,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape matvec sweep")
     ap.add_argument("--no-layers", action="store_true", help="skip the DeltaNet and attention legs")
+    ap.add_argument("--prefill-via-decode", action="store_true",
+                    help="also time the prompt fed through the decode step (one token per step)")
     ap.add_argument("--readback", action="store_true",
                     help="also time one launch per token with a host readback each step (main.rs loop)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -339,15 +392,33 @@ def main():
     torch.cuda.set_stream(st)
     sh = st.cuda_stream
 
-    # The prompt goes through the decode step, at most `chunk` steps per persistent launch.
-    log(f"prompt {n_pre} tokens, warm-up {n_warm}, timed {n_timed} steps in launches {launch_plan(n_timed, chunk)}")
-    t0 = time.time()
-    c0 = 0
-    for n in launch_plan(n_pre, chunk):
-        m.generate(prompt[c0:c0 + n], 0, mode="persistent", stream=sh)
-        c0 += n
-    m.check(stream=sh)
-    prefill_s = time.time() - t0
+    # The prompt goes through the prompt path (one forward at seq_len = n_pre: GEMMs on the
+    # matrix cores, chunked delta rule, causal attention).  A first untimed pass allocates its
+    # buffers; the timed pass runs from a reset model.
+    log(f"prompt {n_pre} tokens (prefill), warm-up {n_warm}, timed {n_timed} steps in launches "
+        f"{launch_plan(n_timed, chunk)}")
+    pre_tok_s_decode = None
+    if args.prefill_via_decode:  # the prompt fed one decode step at a time, for comparison
+        t0 = time.time()
+        c0 = 0
+        for n in launch_plan(n_pre, chunk):
+            m.generate(prompt[c0:c0 + n], 0, mode="persistent", stream=sh)
+            c0 += n
+        m.check(stream=sh)
+        pre_tok_s_decode = n_pre / (time.time() - t0)
+    m.reset()
+    m.prefill(prompt, stream=sh)
+    torch.cuda.synchronize()
+    m.reset()
+    torch.cuda.synchronize()
+    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    pe0.record(st)
+    m.prefill(prompt, stream=sh)
+    pe1.record(st)
+    pe1.synchronize()
+    prefill_wall_s = time.perf_counter() - t0
+    prefill_ms = pe0.elapsed_time(pe1)
     for n in launch_plan(n_warm, chunk):
         m.decode(n, mode="persistent", stream=sh)
     m.check(stream=sh)
@@ -385,6 +456,8 @@ def main():
         toks_readback = 64 / dec_s
     m.close()
 
+    log("prompt GEMM leg")
+    pgemm = prefill_gemm_leg(torch, q35, st, d, n_pre)
     if not args.no_sweep:
         log("matvec sweep")
     sweep = None if args.no_sweep else matvec_sweep(torch, q35, st)
@@ -431,7 +504,12 @@ def main():
                                             else 1e3 * launch_ms[0], 1)},
         "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
         "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
-        "prefill_tok_s_via_decode_step": round(n_pre / prefill_s, 1),
+        "prefill": {"tokens": n_pre, "ms": round(prefill_ms, 3), "tok_s": round(n_pre / (prefill_ms * 1e-3), 1),
+                    "wall_ms_incl_prompt_upload": round(prefill_wall_s * 1e3, 3),
+                    "path": "one forward at seq_len = prompt: Q8F GEMMs on the fp32 matrix cores, causal conv + "
+                            "chunked gated delta rule, causal attention; lm_head on the last row",
+                    "gemm_leg": pgemm},
+        "prefill_tok_s_via_decode_step": None if pre_tok_s_decode is None else round(pre_tok_s_decode, 1),
         "model_build_s": round(create_s, 1),
         "matvec_sweep": sweep,
         "matvec_sweep_note": "panel layout, per-call time from HIP events around back-to-back calls (includes each "

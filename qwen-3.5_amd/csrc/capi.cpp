@@ -433,7 +433,7 @@ int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int
 
 int q35_gate_proj_prompt(const float* x, int32_t T, int32_t in_dim, const float* w_b, const float* w_a,
                          const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream) {
-  return gate_proj_simple_launch(x, T, in_dim, w_b, w_a, a_log, dt_bias, n_heads, out, S(stream), 1);
+  return gate_prompt_launch(x, in_dim, T, in_dim, w_b, w_a, a_log, dt_bias, n_heads, out, S(stream));
 }
 
 size_t q35_gated_delta_rule_prefill_ws_bytes(int32_t T, int32_t lin_heads) {

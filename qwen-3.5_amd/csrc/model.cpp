@@ -371,7 +371,7 @@ int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st
       g.seg[0] = seg(L.qkv, m->pf_y, LDY);
       g.seg[1] = seg(L.z, m->pf_y + conv_dim, LDY);
       if ((rc = gemm_launch(g, st))) return rc;
-      if ((rc = gate_proj_simple_launch(m->pf_xn, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st, 1))) return rc;
+      if ((rc = gate_prompt_launch(m->pf_xn, H, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st))) return rc;
       GdnPrefill gp;
       gp.raw = m->pf_y; gp.ld_raw = LDY; gp.conv_state = L.conv_state; gp.conv_state_out = L.conv_state;
       gp.conv_w = L.conv_w; gp.bg = m->pf_bg; gp.ld_bg = 2 * nh; gp.scr = m->pf_scr; gp.S = L.rec;

@@ -51,11 +51,150 @@ __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, 
 }
 
 // ------------------------------------------------------------------ Gated DeltaNet, prompt
+// [beta | g] of 8 prompt rows per block (text_modules.rs:578-595).  Thread (output o = tid % 32,
+// K group kg = tid / 32) loads one weight W[k][o] per k of its group and multiplies it with the
+// 8 rows' x[t][k] (LDS, 512 columns at a time), keeping 8 row sums; the 8 K groups are then
+// summed in LDS in a fixed order.  Softplus takes its identity branch when its input exceeds 20
+// (the prompt branch's rule).
+constexpr int kGateRows = 8, kGateK = 512, kGateGroups = kPT / 32;
+__global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ldx, int T, int K, const float* wb,
+                                                          const float* wa, const float* alog, const float* dtb,
+                                                          int nh, float* out) {
+  __shared__ float xs[kGateRows][kGateK + 4];
+  __shared__ float red[kGateGroups][kGateRows][33];
+  const int tid = threadIdx.x, o = tid & 31, kg = tid >> 5;
+  const int t0 = blockIdx.x * kGateRows;
+  const int nout = 2 * nh, oo = min(o, nout - 1), h = oo % nh;
+  const float* W = (oo < nh ? wb : wa) + h;
+  float acc[kGateRows];
+#pragma unroll
+  for (int r = 0; r < kGateRows; ++r) acc[r] = 0.f;
+  for (int k0 = 0; k0 < K; k0 += kGateK) {
+    __syncthreads();
+    {  // all of the chunk's loads are issued before any is stored (one round trip)
+      constexpr int kL = kGateRows * kGateK / 4 / kPT;  // float4 per thread (8)
+      float4 v[kL];
+#pragma unroll
+      for (int u = 0; u < kL; ++u) {
+        const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4, t = t0 + i;
+        v[u] = (t < T && k0 + kk < K) ? *(const float4*)(x + (int64_t)t * ldx + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kL; ++u) {
+        const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4;
+        xs[i][kk] = v[u].x; xs[i][kk + 1] = v[u].y; xs[i][kk + 2] = v[u].z; xs[i][kk + 3] = v[u].w;
+      }
+    }
+    __syncthreads();
+    const int kn = min(kGateK, K - k0);
+    for (int kb = kg * 8; kb < kn; kb += 8 * kGateGroups) {
+      float w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = (kb + u < kn) ? W[(int64_t)(k0 + kb + u) * nh] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int r = 0; r < kGateRows; ++r) acc[r] += xs[r][kb + u] * w[u];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kGateRows; ++r) red[kg][r][o] = acc[r];
+  __syncthreads();
+  for (int e = tid; e < kGateRows * 32; e += kPT) {
+    const int r = e >> 5, oc = e & 31, t = t0 + r;
+    if (t >= T || oc >= nout) continue;
+    float sv = 0.f;
+#pragma unroll
+    for (int g = 0; g < kGateGroups; ++g) sv += red[g][r][oc];
+    float res;
+    if (oc < nh) {
+      res = sigmoid_f(sv);
+    } else {
+      const int hh = oc - nh;
+      const float xg = sv + dtb[hh];
+      res = -expf(alog[hh]) * (xg > 20.0f ? xg : logf(expf(xg) + 1.0f));
+    }
+    out[(int64_t)t * nout + oc] = res;
+  }
+}
+
+// Tasks of the lower-triangle products: (row i, 4 columns 4 jg .. 4 jg + 3) for 4 jg <= i; rows
+// 4b .. 4b + 3 have b + 1 tasks each, 544 in all.
+constexpr int kTriTasks = 544;
+Q35_DEV void tri_task(int k, int* i, int* jg) {
+  int b = (int)((sqrtf(2.0f * (float)k + 1.0f) - 1.0f) * 0.5f);
+  while (2 * (b + 1) * (b + 2) <= k) ++b;
+  while (2 * b * (b + 1) > k) --b;
+  const int r = k - 2 * b * (b + 1);
+  *i = 4 * b + r / (b + 1);
+  *jg = r % (b + 1);
+}
+
+// X = (I - N)^-1 for N strictly lower 64 x 64 in U (in place: U ends as X minus its unit
+// diagonal), by blocks: each wave inverts a 16 x 16 diagonal block by forward substitution
+// (the reference's row recurrence, text_modules.rs:282-290, on that block), then
+// X_BA = X_BB N_BA X_AA joins 16-blocks into 32-blocks and those into the 64-block
+// (for [[I - N_AA, 0], [-N_BA, I - N_BB]]).  Tm: 64 x 65 scratch.
+Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  {
+    const int b0 = 16 * wid;
+    for (int i = 2; i < 16; ++i) {
+      float s = 0.f;
+      if (lane < i) {
+        for (int l = lane + 1; l < i; ++l) s += U[b0 + i][b0 + l] * U[b0 + l][b0 + lane];
+      }
+      if (lane < i) U[b0 + i][b0 + lane] += s;
+    }
+  }
+  __syncthreads();
+  // 16 -> 32: blocks (1,0) and (3,2) of 16: X = X_BB N X_AA = (I + L_B)(N + N L_A)
+  {
+    const int p = tid >> 7, e0 = tid & 127;  // pair p, two entries per thread
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = e0 + 128 * u, r = e >> 4, c = e & 15;
+      const int rb = 32 * p + 16, cb = 32 * p;  // block rows / cols
+      float t = U[rb + r][cb + c];
+      for (int l = c + 1; l < 16; ++l) t += U[rb + r][cb + l] * U[cb + l][cb + c];
+      Tm[rb + r][cb + c] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = e0 + 128 * u, r = e >> 4, c = e & 15;
+      const int rb = 32 * p + 16, cb = 32 * p;
+      float t = Tm[rb + r][cb + c];
+      for (int l = 0; l < r; ++l) t += U[rb + r][rb + l] * Tm[rb + l][cb + c];
+      U[rb + r][cb + c] = t;
+    }
+  }
+  __syncthreads();
+  // 32 -> 64: block (1,0) of 32
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+    float t = U[32 + r][c];
+    for (int l = c + 1; l < 32; ++l) t += U[32 + r][l] * U[l][c];
+    Tm[32 + r][c] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+    float t = Tm[32 + r][c];
+    for (int l = 0; l < r; ++l) t += U[32 + r][32 + l] * Tm[32 + l][c];
+    U[32 + r][c] = t;
+  }
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float Qs[kC][kLdq];
   __shared__ __align__(16) float Ks[kC][kLdq];
   __shared__ __align__(16) float Vs[kC][kLdq];
   __shared__ float U[kC][kC + 1];
+  __shared__ float Tm[kC][kC + 1];
   __shared__ float cum[kC], bet[kC], ecum[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -63,122 +202,140 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
   const int t0 = c * kC;
   float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
 
-  // causal conv (cached state prepended) + SiLU of the head's 3 x 128 channels
-  for (int e = tid; e < kC * 3 * kDk; e += kPT) {
-    const int i = e / (3 * kDk), j = e - i * 3 * kDk;
-    const int part = j >> 7, jj = j & 127;
-    const int ch = part == 0 ? h * kDk + jj : (part == 1 ? a.key_dim + h * kDk + jj : 2 * a.key_dim + h * kDk + jj);
-    const int t = t0 + i;
-    float v = 0.f;
-    if (t < a.T) {
-      float x[4];
+  // causal conv (cached state prepended) + SiLU: one channel of the head's 3 x 128 per thread
+  // pass, a sliding window of the last three inputs in registers, 16 rows loaded at a time
+  for (int jj = tid; jj < 3 * kDk; jj += kPT) {
+    const int part = jj >> 7, cc = jj & 127;
+    const int ch = part == 0 ? h * kDk + cc : (part == 1 ? a.key_dim + h * kDk + cc : 2 * a.key_dim + h * kDk + cc);
+    float (*dst)[kLdq] = part == 0 ? Qs : (part == 1 ? Ks : Vs);
+    const float* wp = a.conv_w + (int64_t)ch * 4;
+    const float w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3];
+    float x0, x1, x2;
+    {
+      float xw[3];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int tt = t - 3 + u;
-        x[u] = tt >= 0 ? a.raw[(int64_t)tt * a.ld_raw + ch] : a.conv_state[(int64_t)ch * 3 + 3 + tt];
+      for (int u = 0; u < 3; ++u) {
+        const int tt = t0 - 3 + u;
+        xw[u] = tt >= 0 ? a.raw[(int64_t)tt * a.ld_raw + ch] : a.conv_state[(int64_t)ch * 3 + 3 + tt];
       }
-      const float* w = a.conv_w + (int64_t)ch * 4;
-      v = silu_f(((w[0] * x[0] + w[1] * x[1]) + w[2] * x[2]) + w[3] * x[3]);
+      x0 = xw[0]; x1 = xw[1]; x2 = xw[2];
     }
-    (part == 0 ? Qs : (part == 1 ? Ks : Vs))[i][jj] = v;
+    for (int g0 = 0; g0 < kC; g0 += 16) {
+      float xv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int t = t0 + g0 + u;
+        xv[u] = t < a.T ? a.raw[(int64_t)t * a.ld_raw + ch] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int t = t0 + g0 + u;
+        const float y = ((w0 * x0 + w1 * x1) + w2 * x2) + w3 * xv[u];
+        dst[g0 + u][cc] = t < a.T ? silu_f(y) : 0.f;
+        x0 = x1; x1 = x2; x2 = xv[u];
+      }
+    }
   }
   if (tid < kC) {
     const int t = t0 + tid;
     bet[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + h] : 0.f;
     cum[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + a.nh + h] : 0.f;  // g for now
   }
+  for (int e = tid; e < kC * kC; e += kPT) U[e >> 6][e & 63] = 0.f;
   __syncthreads();
   // l2norm of q (times dk^-1/2) and k rows
   for (int r = wid; r < 2 * kC; r += 4) {
     float* row = r < kC ? Qs[r] : Ks[r - kC];
     const float v0 = row[lane], v1 = row[lane + 64];
-    float rn = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) + 1e-6f);
-    if (r < kC) {
-      row[lane] = (v0 * rn) * a.qscale;
-      row[lane + 64] = (v1 * rn) * a.qscale;
-    } else {
-      row[lane] = v0 * rn;
-      row[lane + 64] = v1 * rn;
-    }
+    const float rn = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) + 1e-6f);
+    const float f = r < kC ? a.qscale : 1.0f;
+    row[lane] = (v0 * rn) * f;
+    row[lane + 64] = (v1 * rn) * f;
   }
-  if (tid == 0) {  // cumulative decay inside the chunk (padded steps add 0)
-    float s = 0.f;
-    for (int i = 0; i < kC; ++i) {
-      s += cum[i];
-      cum[i] = s;
+  if (wid == 0) {  // cumulative decay inside the chunk (padded steps add 0): a wave scan
+    float v = cum[lane];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(v, off, 64);
+      if (lane >= off) v += o;
+    }
+    cum[lane] = v;
+    ecum[lane] = expf(v);
+  }
+  __syncthreads();
+  // N = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i; intra = (q_i.k_j) e^(cum_i - cum_j) for j <= i
+  float* intra = scr + kScrIntra;
+  for (int e = tid; e < kC * kC; e += kPT) {  // the blocks of 4 columns past the diagonal block
+    const int i = e >> 6, j = e & 63;
+    if ((j >> 2) > (i >> 2)) intra[e] = 0.f;
+  }
+  for (int k = tid; k < kTriTasks; k += kPT) {
+    int i, jg;
+    tri_task(k, &i, &jg);
+    const int j0 = 4 * jg;
+    float dkk[4] = {0.f, 0.f, 0.f, 0.f}, dqk[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < kDk; e += 4) {
+      const float4 ki = *(const float4*)&Ks[i][e];
+      const float4 qi = *(const float4*)&Qs[i][e];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 kj = *(const float4*)&Ks[j0 + u][e];
+        dkk[u] += ((ki.x * kj.x + ki.y * kj.y) + ki.z * kj.z) + ki.w * kj.w;
+        dqk[u] += ((qi.x * kj.x + qi.y * kj.y) + qi.z * kj.z) + qi.w * kj.w;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u;
+      const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
+      if (j < i) U[i][j] = -((bet[i] * dkk[u]) * dec);
+      intra[i * kC + j] = j <= i ? dqk[u] * dec : 0.f;
     }
   }
   __syncthreads();
-  if (tid < kC) ecum[tid] = expf(cum[tid]);
-  // U = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i (0 elsewhere); intra = (q_i.k_j) e^(cum_i - cum_j), j <= i
+  tri_inverse(U, Tm);
+  // new_values = X (beta v), k_cumdecay = X (beta e^cum k): thread rows p and 63 - p, 16 columns
   {
-    const int i = tid >> 2, jq = (tid & 3) * 16;
-    float dkk[16], dqk[16];
+    const int p = tid >> 3, d0 = (tid & 7) * 16;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) { dkk[u] = 0.f; dqk[u] = 0.f; }
-    if (jq <= i) {
-      for (int e = 0; e < kDk; e += 4) {
-        const float4 ki = *(const float4*)&Ks[i][e];
-        const float4 qi = *(const float4*)&Qs[i][e];
+    for (int half = 0; half < 2; ++half) {
+      const int i = half == 0 ? p : kC - 1 - p;
+      float an[16], ak[16];
+      {
+        const float ub = bet[i], ube = ub * ecum[i];  // the unit diagonal
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          const float4 kj = *(const float4*)&Ks[min(jq + u, kC - 1)][e];
-          dkk[u] += ((ki.x * kj.x + ki.y * kj.y) + ki.z * kj.z) + ki.w * kj.w;
-          dqk[u] += ((qi.x * kj.x + qi.y * kj.y) + qi.z * kj.z) + qi.w * kj.w;
+        for (int d = 0; d < 16; d += 4) {
+          const float4 v = *(const float4*)&Vs[i][d0 + d];
+          const float4 k = *(const float4*)&Ks[i][d0 + d];
+          an[d] = ub * v.x; an[d + 1] = ub * v.y; an[d + 2] = ub * v.z; an[d + 3] = ub * v.w;
+          ak[d] = ube * k.x; ak[d + 1] = ube * k.y; ak[d + 2] = ube * k.z; ak[d + 3] = ube * k.w;
         }
       }
-    }
-    float* intra = scr + kScrIntra + i * kC;
+      for (int l = 0; l < i; ++l) {
+        const float ub = U[i][l] * bet[l];
+        const float ube = ub * ecum[l];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int j = jq + u;
-      const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
-      U[i][j] = j < i ? -((bet[i] * dkk[u]) * dec) : 0.f;
-      intra[j] = j <= i ? dqk[u] * dec : 0.f;
-    }
-  }
-  __syncthreads();
-  // forward substitution (rows in increasing order): U[i][j] += sum_{j<l<i} U[i][l] U[l][j]
-  if (wid == 0) {
-    for (int i = 2; i < kC; ++i) {
-      float s = 0.f;
-      for (int l = lane + 1; l < i; ++l) s += U[i][l] * U[l][lane];
-      if (lane < i) U[i][lane] += s;
-    }
-  }
-  __syncthreads();
-  if (tid < kC) U[tid][tid] = 1.0f;
-  __syncthreads();
-  // new_values = U (beta v), k_cumdecay = U (beta e^cum k); q e^cum; k e^(cum_last - cum)
-  {
-    const int i = tid >> 2, d0 = (tid & 3) * 32;
-    float an[32], ak[32];
-#pragma unroll
-    for (int d = 0; d < 32; ++d) { an[d] = 0.f; ak[d] = 0.f; }
-    for (int l = 0; l <= i; ++l) {
-      const float ub = U[i][l] * bet[l];
-      const float ube = ub * ecum[l];
-#pragma unroll
-      for (int d = 0; d < 32; d += 4) {
-        const float4 v = *(const float4*)&Vs[l][d0 + d];
-        const float4 k = *(const float4*)&Ks[l][d0 + d];
-        an[d] += ub * v.x; an[d + 1] += ub * v.y; an[d + 2] += ub * v.z; an[d + 3] += ub * v.w;
-        ak[d] += ube * k.x; ak[d + 1] += ube * k.y; ak[d + 2] += ube * k.z; ak[d + 3] += ube * k.w;
+        for (int d = 0; d < 16; d += 4) {
+          const float4 v = *(const float4*)&Vs[l][d0 + d];
+          const float4 k = *(const float4*)&Ks[l][d0 + d];
+          an[d] += ub * v.x; an[d + 1] += ub * v.y; an[d + 2] += ub * v.z; an[d + 3] += ub * v.w;
+          ak[d] += ube * k.x; ak[d + 1] += ube * k.y; ak[d + 2] += ube * k.z; ak[d + 3] += ube * k.w;
+        }
       }
-    }
-    const float eq = ecum[i], ek = expf(cum[kC - 1] - cum[i]);
-    float* nv = scr + kScrNv + i * kDk + d0;
-    float* kcd = scr + kScrKcd + i * kDk + d0;
-    float* qe = scr + kScrQe + i * kDk + d0;
-    float* kd = scr + kScrKd + i * kDk + d0;
+      const float eq = ecum[i], ek = expf(cum[kC - 1] - cum[i]);
+      float* nv = scr + kScrNv + i * kDk + d0;
+      float* kcd = scr + kScrKcd + i * kDk + d0;
+      float* qe = scr + kScrQe + i * kDk + d0;
+      float* kd = scr + kScrKd + i * kDk + d0;
 #pragma unroll
-    for (int d = 0; d < 32; d += 4) {
-      *(float4*)(nv + d) = make_float4(an[d], an[d + 1], an[d + 2], an[d + 3]);
-      *(float4*)(kcd + d) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
-      const float4 q = *(const float4*)&Qs[i][d0 + d];
-      const float4 k = *(const float4*)&Ks[i][d0 + d];
-      *(float4*)(qe + d) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
-      *(float4*)(kd + d) = make_float4(k.x * ek, k.y * ek, k.z * ek, k.w * ek);
+      for (int d = 0; d < 16; d += 4) {
+        *(float4*)(nv + d) = make_float4(an[d], an[d + 1], an[d + 2], an[d + 3]);
+        *(float4*)(kcd + d) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
+        const float4 q = *(const float4*)&Qs[i][d0 + d];
+        const float4 k = *(const float4*)&Ks[i][d0 + d];
+        *(float4*)(qe + d) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
+        *(float4*)(kd + d) = make_float4(k.x * ek, k.y * ek, k.z * ek, k.w * ek);
+      }
     }
     if (tid == 0) scr[kScrCd] = ecum[kC - 1];
   }
@@ -219,20 +376,38 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_state_kernel(const GdnPrefill a
     *(float4*)&Ss[e][j] = *(const float4*)src;
     *(float4*)&Ss[e][j + 4] = *(const float4*)(src + 4);
   }
+  constexpr int kLd4 = kC * kDk / 4 / kPT;   // float4 per thread per 64 x 128 matrix (8)
+  constexpr int kLdIn = kC * kC / 4 / kPT;   // float4 per thread of the intra matrix (4)
   for (int c = 0; c < a.nchunk; ++c) {
     const float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
-    for (int e = tid; e < kC * kDk / 4; e += kPT) {
-      const int i = e >> 5, d = (e & 31) * 4;
-      *(float4*)&Kc[i][d] = *(const float4*)(scr + kScrKcd + i * kDk + d);
-      *(float4*)&Qe[i][d] = *(const float4*)(scr + kScrQe + i * kDk + d);
-      *(float4*)&Kd[i][d] = *(const float4*)(scr + kScrKd + i * kDk + d);
+    {  // every load of the chunk is issued before any is stored (one round trip per chunk)
+      float4 vkc[kLd4], vqe[kLd4], vkd[kLd4], vin[kLdIn];
+#pragma unroll
+      for (int u = 0; u < kLd4; ++u) {
+        const int e = tid + u * kPT;
+        vkc[u] = *(const float4*)(scr + kScrKcd + 4 * e);
+        vqe[u] = *(const float4*)(scr + kScrQe + 4 * e);
+        vkd[u] = *(const float4*)(scr + kScrKd + 4 * e);
+      }
+#pragma unroll
+      for (int u = 0; u < kLdIn; ++u) vin[u] = *(const float4*)(scr + kScrIntra + 4 * (tid + u * kPT));
+      const float4 vnv = *(const float4*)(scr + kScrNv + (tid >> 2) * kDk + c0 + (tid & 3) * 4);
+      const float vcd = scr[kScrCd];
+#pragma unroll
+      for (int u = 0; u < kLd4; ++u) {
+        const int e = tid + u * kPT, i = e >> 5, d = (e & 31) * 4;
+        *(float4*)&Kc[i][d] = vkc[u];
+        *(float4*)&Qe[i][d] = vqe[u];
+        *(float4*)&Kd[i][d] = vkd[u];
+      }
+#pragma unroll
+      for (int u = 0; u < kLdIn; ++u) {
+        const int e = 4 * (tid + u * kPT), i = e >> 6, j = e & 63;
+        In[i][j] = vin[u].x; In[i][j + 1] = vin[u].y; In[i][j + 2] = vin[u].z; In[i][j + 3] = vin[u].w;
+      }
+      *(float4*)&Vn[tid >> 2][(tid & 3) * 4] = vnv;
+      if (tid == 0) cdv = vcd;
     }
-    for (int e = tid; e < kC * kC; e += kPT) In[e >> 6][e & 63] = scr[kScrIntra + e];
-    {
-      const int i = tid >> 2, j = (tid & 3) * 4;
-      *(float4*)&Vn[i][j] = *(const float4*)(scr + kScrNv + i * kDk + c0 + j);
-    }
-    if (tid == 0) cdv = scr[kScrCd];
     __syncthreads();
     const int i = tid >> 2, j = (tid & 3) * 4;
     {  // v_new = new_values - k_cumdecay S
@@ -354,29 +529,32 @@ __global__ __launch_bounds__(kPT) void attn_prefill_prep_kernel(const AttnPrefil
   }
 }
 
-// Causal GQA attention of the prompt rows.  Block (query tile, kv head g): 64 rows = QT tokens x
-// rep query heads of g; thread (row r = tid/4, quarter qd = tid%4) holds dims [64 qd, 64 qd + 64)
-// of its row's query and output.  Keys stream through LDS 32 at a time (rows padded per
-// quarter so the four quarters' reads fall in different banks); a score is the sum of the four
-// quarters' partial dots; online softmax in log2 units, rescaled once per 8 keys.
+// Causal GQA attention of the prompt rows.  Block (query tile, kv head g): 16 rows = QT tokens x
+// rep query heads of g (QT = 16 / rep), so a 512-token prompt gives 128 x kv_heads blocks;
+// thread (row r = tid / 16, slice sl = tid % 16) holds dims [16 sl, 16 sl + 16) of its row's
+// query and output.  Keys stream through LDS 32 at a time (each 16-float slice padded to 20 so
+// the 16 slices of a row fall in different banks); a score is the sum of the 16 slices' partial
+// dots (4 lane exchanges); online softmax in log2 units, rescaled once per 8 keys.
 constexpr int kKT = 32;            // keys per LDS tile
-constexpr int kQLd = 68;           // floats per quarter row in LDS (64 + 4)
+constexpr int kSd = 16;            // dims per thread
+constexpr int kSp = 20;            // LDS floats per 16-dim slice
+constexpr int kRows = 16;          // query rows per block
 __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) {
-  __shared__ __align__(16) float Ks[kKT][4 * kQLd];
-  __shared__ __align__(16) float Vs[kKT][4 * kQLd];
+  __shared__ __align__(16) float Ks[kKT][16 * kSp];
+  __shared__ __align__(16) float Vs[kKT][16 * kSp];
   const int tid = threadIdx.x;
-  const int rep = a.nh / a.nkv, QT = 64 / rep;
+  const int rep = a.nh / a.nkv, QT = kRows / rep;
   const int qt = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
-  const int r = tid >> 2, qd = tid & 3;
+  const int r = tid >> 4, sl = tid & 15;
   const int t = qt * QT + r / rep, hq = g * rep + r % rep;
   const bool row_ok = t < a.T;
   const int lim = a.p0 + (row_ok ? t : 0);  // last key this row may see
   const int tmax_blk = min(a.T, (qt + 1) * QT) - 1;
   const int nkeys = a.p0 + tmax_blk + 1;
-  float q[64], acc[64];
-  const float* qsrc = a.qbuf + ((int64_t)(row_ok ? t : 0) * a.nh + hq) * kHdP + qd * 64;
+  float q[kSd], acc[kSd];
+  const float* qsrc = a.qbuf + ((int64_t)(row_ok ? t : 0) * a.nh + hq) * kHdP + sl * kSd;
 #pragma unroll
-  for (int d = 0; d < 64; d += 4) {
+  for (int d = 0; d < kSd; d += 4) {
     const float4 v = *(const float4*)(qsrc + d);
     q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
     acc[d] = 0.f; acc[d + 1] = 0.f; acc[d + 2] = 0.f; acc[d + 3] = 0.f;
@@ -385,30 +563,47 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
   const float sl2 = a.scale * 1.44269504088896341f;
   const float* Kg = a.kc + (int64_t)g * a.tmax * kHdP;
   const float* Vg = a.vc + (int64_t)g * a.tmax * kHdP;
+  // the next tile's rows are loaded into registers while the current tile is computed
+  constexpr int kTl = kKT * kHdP / 4 / kPT;  // float4 per thread per tile (8)
+  q35_f32x4 nk[kTl], nv[kTl];
+  auto load_tile = [&](int base) {
+    static_for<kTl>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int e = tid + u * kPT, j = e >> 6, d = (e & 63) * 4;
+      const int kj = min(base + j, nkeys - 1);
+      nk[u] = *(const q35_f32x4*)(Kg + (int64_t)kj * kHdP + d);
+      nv[u] = *(const q35_f32x4*)(Vg + (int64_t)kj * kHdP + d);
+    });
+  };
+  load_tile(0);
   for (int k0 = 0; k0 < nkeys; k0 += kKT) {
     __syncthreads();
-    for (int e = tid; e < kKT * kHdP / 4; e += kPT) {
-      const int j = e >> 6, d = (e & 63) * 4;
-      const int kj = min(k0 + j, nkeys - 1);
-      const int o = (d >> 6) * kQLd + (d & 63);
-      *(float4*)&Ks[j][o] = *(const float4*)(Kg + (int64_t)kj * kHdP + d);
-      *(float4*)&Vs[j][o] = *(const float4*)(Vg + (int64_t)kj * kHdP + d);
-    }
+    static_for<kTl>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int e = tid + u * kPT, j = e >> 6, d = (e & 63) * 4;
+      const int o = (d >> 4) * kSp + (d & 15);
+      *(q35_f32x4*)&Ks[j][o] = nk[u];
+      *(q35_f32x4*)&Vs[j][o] = nv[u];
+    });
     __syncthreads();
-    for (int jb = 0; jb < kKT; jb += 8) {
+    if (k0 + kKT < nkeys) load_tile(k0 + kKT);
+    const int kend = min(kKT, nkeys - k0);
+    for (int jb = 0; jb < kend; jb += 8) {
       float s[8];
       float bm = -INFINITY;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float* kr = &Ks[jb + u][qd * kQLd];
+        const float* kr = &Ks[jb + u][sl * kSp];
         float p = 0.f;
 #pragma unroll
-        for (int d = 0; d < 64; d += 4) {
+        for (int d = 0; d < kSd; d += 4) {
           const float4 kv = *(const float4*)(kr + d);
           p += ((q[d] * kv.x + q[d + 1] * kv.y) + q[d + 2] * kv.z) + q[d + 3] * kv.w;
         }
         p += __shfl_xor(p, 1, 64);
         p += __shfl_xor(p, 2, 64);
+        p += __shfl_xor(p, 4, 64);
+        p += __shfl_xor(p, 8, 64);
         const int kj = k0 + jb + u;
         s[u] = (kj <= lim) ? p * sl2 : -INFINITY;
         bm = fmaxf(bm, s[u]);
@@ -418,14 +613,14 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
       const float al = __builtin_amdgcn_exp2f(m - mn);
       l *= al;
 #pragma unroll
-      for (int d = 0; d < 64; ++d) acc[d] *= al;
+      for (int d = 0; d < kSd; ++d) acc[d] *= al;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float p = __builtin_amdgcn_exp2f(s[u] - mn);
         l += p;
-        const float* vr = &Vs[jb + u][qd * kQLd];
+        const float* vr = &Vs[jb + u][sl * kSp];
 #pragma unroll
-        for (int d = 0; d < 64; d += 4) {
+        for (int d = 0; d < kSd; d += 4) {
           const float4 vv = *(const float4*)(vr + d);
           acc[d] += p * vv.x; acc[d + 1] += p * vv.y; acc[d + 2] += p * vv.z; acc[d + 3] += p * vv.w;
         }
@@ -434,10 +629,10 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
     }
   }
   if (!row_ok) return;
-  const float* gate = a.qg + (int64_t)t * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + qd * 64;
-  float* dst = a.out + (int64_t)t * a.ld_out + (int64_t)hq * kHdP + qd * 64;
+  const float* gate = a.qg + (int64_t)t * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + sl * kSd;
+  float* dst = a.out + (int64_t)t * a.ld_out + (int64_t)hq * kHdP + sl * kSd;
 #pragma unroll
-  for (int d = 0; d < 64; d += 4) {
+  for (int d = 0; d < kSd; d += 4) {
     const float4 gv = *(const float4*)(gate + d);
     *(float4*)(dst + d) = make_float4((acc[d] / l) * sigmoid_f(gv.x), (acc[d + 1] / l) * sigmoid_f(gv.y),
                                       (acc[d + 2] / l) * sigmoid_f(gv.z), (acc[d + 3] / l) * sigmoid_f(gv.w));
@@ -460,6 +655,18 @@ int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float
                     hipStream_t st) {
   if (M < 1) return Q35_OK;
   hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, const float* wa, const float* alog,
+                       const float* dtb, int nh, float* out, hipStream_t st) {
+  if (!x || !wb || !wa || !alog || !dtb || !out) return fail(Q35_E_ARG, "gate_proj_prompt: null pointer");
+  if (T < 1 || K < 64 || (K % 64) != 0 || nh < 1 || 2 * nh > 32)
+    return fail(Q35_E_SHAPE, "gate_proj_prompt: K a multiple of 64 and 2 heads <= 32");
+  if ((ldx % 4) != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0) return fail(Q35_E_ALIGN, "gate_proj_prompt: x rows must be 16-byte aligned");
+  hipLaunchKernelGGL(gate_prompt_kernel, dim3((T + kGateRows - 1) / kGateRows), dim3(kPT), 0, st, x, ldx, T, K, wb,
+                     wa, alog, dtb, nh, out);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
@@ -495,13 +702,13 @@ int attn_prefill_launch(const AttnPrefill& a, hipStream_t st) {
   if (!a.qg || !a.k || !a.v || !a.qnw || !a.knw || !a.rcos || !a.rsin || !a.kc || !a.vc || !a.qbuf || !a.out)
     return fail(Q35_E_ARG, "attention prefill: null pointer");
   if (a.T < 1) return Q35_OK;
-  if (a.nkv < 1 || a.nh % a.nkv != 0 || 64 % (a.nh / a.nkv) != 0) return fail(Q35_E_SHAPE, "attention prefill: heads");
+  if (a.nkv < 1 || a.nh % a.nkv != 0 || kRows % (a.nh / a.nkv) != 0) return fail(Q35_E_SHAPE, "attention prefill: heads");
   if (a.p0 < 0 || (int64_t)a.p0 + a.T > a.tmax) return fail(Q35_E_SHAPE, "attention prefill: positions past tmax");
   if (a.rot < 2 || a.rot > kHdP || (a.rot % 2) != 0) return fail(Q35_E_SHAPE, "attention prefill: rotary dims");
   if ((a.ld_qg % 4) != 0 || (a.ld_out % 4) != 0) return fail(Q35_E_ALIGN, "attention prefill: row alignment");
   hipLaunchKernelGGL(attn_prefill_prep_kernel, dim3(a.T * (a.nh + a.nkv)), dim3(kPT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
-  const int QT = 64 / (a.nh / a.nkv);
+  const int QT = kRows / (a.nh / a.nkv);
   const int nqt = (a.T + QT - 1) / QT;
   hipLaunchKernelGGL(attn_prefill_kernel, dim3(nqt * a.nkv), dim3(kPT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());

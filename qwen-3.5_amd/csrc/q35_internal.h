@@ -4,6 +4,7 @@
 #include <stdint.h>
 #include <stddef.h>
 #include <string>
+#include <type_traits>
 #include "../../include/q35.h"
 
 namespace q35 {
@@ -99,6 +100,9 @@ template <class T>
 Q35_DEV void stg(T* p, T v) { *(Q35_GLOBAL T*)p = v; }
 // 16-byte global load (p 16-byte aligned)
 typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
+// Native 4 x f32 vector.  Register arrays that stay live across a runtime loop must use it: arrays
+// of HIP's float4 struct there are left in private memory (scratch), these are kept in VGPRs.
+typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
 Q35_DEV uint4 ldg16(const void* p) {
   const q35_u32x4 v = *(const Q35_GLOBAL q35_u32x4*)p;
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -178,6 +182,17 @@ Q35_DEV void wave_argmax(float& v, int& i, const ArgOrder& o) {
     const float ov = __shfl_xor(v, s, 64);
     const int oi = __shfl_xor(i, s, 64);
     if (argmax_better(ov, oi, v, i, o)) { v = ov; i = oi; }
+  }
+}
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1 at compile time: register arrays indexed
+// through it see constant indices from the start (a #pragma unroll loop only gets them after
+// unrolling, which is too late for arrays that live across a runtime loop: those stay in memory).
+template <int N, class F>
+Q35_DEV void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
   }
 }
 
@@ -468,6 +483,9 @@ int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);
 // y[m] = RMSNorm(x[m]) * (1 + w) for M rows of K
 int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
                     hipStream_t st);
+// [beta | g] rows of a prompt (x [T][ldx], softplus identity branch when its input exceeds 20)
+int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, const float* wa, const float* alog,
+                       const float* dtb, int nh, float* out, hipStream_t st);
 // Gated DeltaNet over a prompt of T tokens (dk = dv = 128): causal conv continuing conv_state,
 // chunked gated delta rule continuing S.  scr: nh * nchunk * kGdnScratchPerChunk floats.
 constexpr int kGdnChunk = 64;
