@@ -270,6 +270,17 @@ typedef struct q35_model q35_model;
  * the tensors main.rs:159-222 quantises.  Allocates weights, caches for tmax tokens and the step
  * workspace.  Replaces TextForCausalLMConfig::init + load_file (main.rs:29-37). */
 int q35_model_create_synthetic(const q35_dims* d, uint64_t seed, int32_t tmax, q35_model** out);
+
+/* Builds the decoder from a Hugging Face safetensors checkpoint as the reference's loader does
+ * (main.rs:160-222): keys `model.language_model.<path>` (or without the `model.` prefix, which
+ * the reference strips), `.A_log` read as `.a_log`; Linear weights transposed from PyTorch's
+ * [out][in] to [in][out] (PyTorchToBurnAdapter); F32 / F16 / BF16 values cast to f32
+ * (FloatCastAdapter); embed_tokens, the MLP, attention and DeltaNet in/out projections quantised
+ * to Q8F per block of 64 (main.rs:175-220), everything else (norms, in_proj_b / in_proj_a, conv1d,
+ * A_log, dt_bias) kept f32.  A missing tensor, a shape that disagrees with d, or an unsupported
+ * dtype is reported (Q35_E_ARG / Q35_E_SHAPE), naming the key.  Tensors the decoder does not
+ * read (lm_head with tied embeddings, vision tower, ...) are ignored. */
+int q35_model_create_from_safetensors(const q35_dims* d, const char* path, int32_t tmax, q35_model** out);
 int q35_model_destroy(q35_model* m);
 
 /* Zero every cache and set the position to 0 (the chat loop's /reset, main.rs:65-71).  Also
@@ -385,6 +396,11 @@ int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t
  * K*N bytes and K*N/64 scales). */
 int q35_q8f_pack_kn_panel(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_panel_host,
                           float* scale_panel_host);
+/* Host: the f32 values q35_model_create_from_safetensors takes for decoder tensor `name` (the
+ * builder's names, as q35_model_tensor lists them without the .q/.scale suffix) from the
+ * checkpoint at `path`, in the builder's layout ([in][out] for Linear weights), before Q8F
+ * quantisation.  n must be the tensor's element count.  For tests and tools. */
+int q35_safetensors_tensor(const char* path, const q35_dims* d, const char* name, float* out_host, int64_t n);
 /* Host copy of the f32 values the model builder draws for a named tensor (before
  * quantisation), so a host-side checker can rebuild the same model. */
 int q35_synth_model_tensor(const q35_dims* d, uint64_t seed, const char* name, float* out_host, int64_t n);

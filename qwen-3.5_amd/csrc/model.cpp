@@ -470,11 +470,13 @@ int step(q35_model* m, int use_graph, hipStream_t st) {
 }  // namespace
 }  // namespace q35
 
-using namespace q35;
+namespace q35 {
+namespace {
 
-extern "C" {
+// The f32 values of one decoder tensor in the builder's layout (see TensorSpec).
+using ValuesFn = std::function<int(const TensorSpec&, float*)>;
 
-int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, q35_model** out) {
+int build_model(const q35_dims* dp, uint64_t seed, int32_t tmax, const ValuesFn& values, q35_model** out) {
   if (!dp || !out) return fail(Q35_E_ARG, "model_create: null pointer");
   *out = nullptr;
   int rc = validate_dims(*dp);
@@ -496,7 +498,7 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
   for (const TensorSpec& t : model_specs(d)) {
     const size_t n = (size_t)t.rows * t.cols;
     host.resize(n);
-    synth_values(t, seed, host.data());
+    if ((rc = values(t, host.data()))) return bail(rc);
     if (t.kind == kF32) {
       float* p;
       if ((rc = dev_alloc_t(m, t.name, n, &p))) return bail(rc);
@@ -605,6 +607,28 @@ int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, 
   if (hipStreamSynchronize(m->own_stream) != hipSuccess) return bail(fail(Q35_E_HIP, "sync"));
   *out = m;
   return Q35_OK;
+}
+
+}  // namespace
+}  // namespace q35
+
+using namespace q35;
+
+extern "C" {
+
+int q35_model_create_synthetic(const q35_dims* dp, uint64_t seed, int32_t tmax, q35_model** out) {
+  return build_model(dp, seed, tmax, [seed](const TensorSpec& t, float* v) {
+    synth_values(t, seed, v);
+    return Q35_OK;
+  }, out);
+}
+
+int q35_model_create_from_safetensors(const q35_dims* dp, const char* path, int32_t tmax, q35_model** out) {
+  if (!dp || !path || !out) return fail(Q35_E_ARG, "model_create_from_safetensors: null pointer");
+  int rc = Q35_OK;
+  SafeTensorsPtr st = open_safetensors(path, &rc);
+  if (rc) return rc;
+  return build_model(dp, 0, tmax, [&st](const TensorSpec& t, float* v) { return safetensors_values(*st, t, v); }, out);
 }
 
 int q35_model_destroy(q35_model* m) {

@@ -1,6 +1,7 @@
 // Host-only declarations: synthetic init, quantiser, tensor table, model internals.
 #pragma once
 #include <functional>
+#include <memory>
 #include <string>
 #include <vector>
 #include "q35_internal.h"
@@ -31,5 +32,15 @@ void pack_kn_tiled(const int8_t* q, const float* s, int64_t K, int64_t N, int8_t
 std::vector<TensorSpec> model_specs(const q35_dims& d);
 void synth_values(const TensorSpec& t, uint64_t seed, float* out);
 int validate_dims(const q35_dims& d);
+
+// safetensors checkpoint (weights.cpp)
+struct SafeTensors;
+struct SafeTensorsClose {
+  void operator()(SafeTensors* s) const;
+};
+using SafeTensorsPtr = std::unique_ptr<SafeTensors, SafeTensorsClose>;
+SafeTensorsPtr open_safetensors(const std::string& path, int* rc);
+// the f32 values of decoder tensor t in the builder's layout (Linear weights transposed to [in][out])
+int safetensors_values(const SafeTensors& st, const TensorSpec& t, float* out);
 
 }  // namespace q35

@@ -81,6 +81,8 @@ PROTOTYPES = {
                                                   c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "q35_attention_prefill_ws_bytes": (c_sz, [ctypes.POINTER(Dims), c_i32]),
     "q35_model_create_synthetic": (ctypes.c_int, [ctypes.POINTER(Dims), c_u64, c_i32, ctypes.POINTER(c_vp)]),
+    "q35_model_create_from_safetensors": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.c_char_p, c_i32,
+                                                         ctypes.POINTER(c_vp)]),
     "q35_model_destroy": (ctypes.c_int, [c_vp]),
     "q35_model_reset": (ctypes.c_int, [c_vp, c_vp]),
     "q35_model_set_token": (ctypes.c_int, [c_vp, c_i32, c_vp]),
@@ -103,6 +105,7 @@ PROTOTYPES = {
     "q35_q8f_tiled_scale_count": (c_i64, [ctypes.c_int32, ctypes.c_int32]),
     "q35_q8f_pack_kn_tiled": (ctypes.c_int, [c_vp, c_vp, ctypes.c_int32, ctypes.c_int32, c_vp, c_vp]),
     "q35_q8f_pack_kn_panel": (ctypes.c_int, [c_vp, c_vp, ctypes.c_int32, ctypes.c_int32, c_vp, c_vp]),
+    "q35_safetensors_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(Dims), ctypes.c_char_p, c_vp, c_i64]),
     "q35_synth_model_tensor": (ctypes.c_int, [ctypes.POINTER(Dims), c_u64, ctypes.c_char_p, c_vp, c_i64]),
 }
 

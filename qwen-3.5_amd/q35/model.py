@@ -32,6 +32,20 @@ class TextForCausalLM:
         self.h = h
         _live.add(self)
 
+    @classmethod
+    def from_safetensors(cls, path, dims=None, tmax=2048):
+        """The decoder with the weights of a Hugging Face safetensors checkpoint (main.rs:160-222
+        ingestion: key remap, [out][in] -> [in][out], f32, Q8F per block of 64)."""
+        self = cls.__new__(cls)
+        self.dims = dims if dims is not None else L.dims_2b()
+        self.seed, self.tmax = None, tmax
+        h = ctypes.c_void_p()
+        L.check(L.lib().q35_model_create_from_safetensors(ctypes.byref(self.dims), str(path).encode(), tmax,
+                                                          ctypes.byref(h)))
+        self.h = h
+        _live.add(self)
+        return self
+
     def close(self):
         if self.h:
             L.lib().q35_model_destroy(self.h)
@@ -155,6 +169,14 @@ def synth_model_tensor(dims, seed, name, n):
     """f32 values the model builder draws for tensor `name` (before Q8F quantisation)."""
     out = np.empty(n, np.float32)
     L.check(L.lib().q35_synth_model_tensor(ctypes.byref(dims), seed, name.encode(), out.ctypes.data, n))
+    return out
+
+
+def safetensors_tensor(path, dims, name, n):
+    """f32 values the safetensors loader takes for decoder tensor `name` (Linear weights as
+    [in][out]), before quantisation; host only."""
+    out = np.empty(n, np.float32)
+    L.check(L.lib().q35_safetensors_tensor(str(path).encode(), ctypes.byref(dims), name.encode(), out.ctypes.data, n))
     return out
 
 
