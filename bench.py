@@ -55,6 +55,27 @@ def step_bytes(d, ctx):
     return mv + state + kv
 
 
+def weight_bytes(d):
+    """Q8F weights + f32 scales + f32 gate-projection weights one decode step streams."""
+    return step_bytes(d, 0) - seq_state_bytes(d, 0)
+
+
+def seq_state_bytes(d, ctx):
+    """Per-sequence bytes of one decode step: DeltaNet states read + written, conv weights, the KV
+    rows read at context ctx, and the matvec inputs / outputs."""
+    H, F, V = d.hidden, d.ffn, d.vocab
+    nh, vd = d.lin_heads, d.lin_heads * d.lin_dv
+    conv_dim = 2 * nh * d.lin_dk + vd
+    ah, kvh, hd = d.attn_heads, d.kv_heads, d.head_dim
+    n_full = sum(1 for l in range(d.n_layers) if (l + 1) % d.full_interval == 0)
+    n_lin = d.n_layers - n_full
+    io = n_lin * (4 * H + 4 * (conv_dim + vd) + 4 * vd + 4 * H) + n_full * (
+        4 * H + 4 * (ah * hd * 2 + 2 * kvh * hd) + 4 * ah * hd + 4 * H) + d.n_layers * (
+        4 * H + 8 * F + 4 * F + 4 * H) + 4 * H + 4 * V
+    state = n_lin * (2 * nh * d.lin_dk * d.lin_dv * 4 + 2 * conv_dim * 3 * 4)
+    return io + state + n_full * (2 * kvh * ctx * hd * 4)
+
+
 def gdn_bytes(B, nh=16, dk=128, dv=128):
     """Bytes the Gated DeltaNet decode step moves for B sequences: recurrent state read + write,
     the q|k|v projection input, conv state read + write, beta|g, the core output, and the shared
@@ -271,6 +292,42 @@ def prefill_gemm_leg(torch, q35, st, d, T):
             "unit": "fp32 matrix-core TFLOP/s (f32 dequantised weights, f32 products and accumulation)"}
 
 
+def batch_leg(torch, q35, st, d, n_pre, n_steps=64, batches=(8, 16, 32)):
+    """Batched greedy decode (q35_batch_*: B sequences through the whole step, every projection
+    streaming its weights once per 8 rows): B prompts of n_pre random ids through the prompt path,
+    4 untimed and n_steps timed batched steps (captured graph), timed with HIP events.  Reports
+    aggregate tok/s and the algorithmic rate: weights once per step + each sequence's states, KV
+    rows and matvec inputs/outputs."""
+    import numpy as np
+    out = {}
+    tmax = n_pre + n_steps + 16
+    m = q35.TextForCausalLM(d, seed=0, tmax=tmax)
+    sh = st.cuda_stream
+    W = weight_bytes(d)
+    for B in batches:
+        bt = q35.BatchDecoder(m, B, tmax)
+        rng = np.random.default_rng(B)
+        prompts = [rng.integers(0, d.vocab, n_pre).astype(np.int32) for _ in range(B)]
+        bt.generate(prompts, 4, mode="graph", prefill=True, stream=sh)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        bt.decode(n_steps, mode="graph", stream=sh)
+        e1.record(st)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1)
+        ctx0 = n_pre + 5
+        nbytes = sum(W + B * seq_state_bytes(d, ctx0 + i) for i in range(n_steps))
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"B{B}"] = {"tok_s": round(B * n_steps / (ms * 1e-3), 1), "ms_per_step": round(ms / n_steps, 4),
+                        "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "ctx_range": [ctx0, ctx0 + n_steps]}
+        bt.close()
+        torch.cuda.empty_cache()
+    m.close()
+    return out
+
+
 def cpu_model_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -355,6 +412,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape matvec sweep")
     ap.add_argument("--no-layers", action="store_true", help="skip the DeltaNet and attention legs")
+    ap.add_argument("--no-batch", action="store_true", help="skip the batched decode leg")
     ap.add_argument("--prefill-via-decode", action="store_true",
                     help="also time the prompt fed through the decode step (one token per step)")
     ap.add_argument("--readback", action="store_true",
@@ -458,6 +516,10 @@ def main():
 
     log("prompt GEMM leg")
     pgemm = prefill_gemm_leg(torch, q35, st, d, n_pre)
+    batched = None
+    if not args.no_batch:
+        log("batched decode leg")
+        batched = batch_leg(torch, q35, st, d, n_pre)
     if not args.no_sweep:
         log("matvec sweep")
     sweep = None if args.no_sweep else matvec_sweep(torch, q35, st)
@@ -509,6 +571,10 @@ def main():
                     "path": "one forward at seq_len = prompt: Q8F GEMMs on the fp32 matrix cores, causal conv + "
                             "chunked gated delta rule, causal attention; lm_head on the last row",
                     "gemm_leg": pgemm},
+        "batched_decode": batched,
+        "batched_decode_note": None if batched is None else
+            "B sequences per step (q35_batch, hipGraph), each with a 512-token prompt prefilled; frac counts "
+            "the weights once per step plus every sequence's states, KV rows and matvec inputs/outputs",
         "prefill_tok_s_via_decode_step": None if pre_tok_s_decode is None else round(pre_tok_s_decode, 1),
         "model_build_s": round(create_s, 1),
         "matvec_sweep": sweep,

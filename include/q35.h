@@ -374,6 +374,39 @@ int q35_model_position(q35_model* m, int32_t* pos_out);
  * "layers.{i}.self_attn.k_cache", "logits", "token", "pos", ...  Used by tests and tools. */
 int q35_model_tensor(q35_model* m, const char* name, void** dptr, size_t* bytes);
 
+/* ---------------------------------------------------------------- batched decode */
+
+/* B independent sequences decoded together with one model's weights (the reference decodes one
+ * sequence; kernels.rs:447,683 squeeze to bs = 1).  Each sequence has its own conv / recurrent
+ * states, KV cache of tmax rows (tmax <= the model's), position, prompt, token and history; one
+ * step runs every projection once for up to 8 sequences (Q8F matvec row groups), the DeltaNet
+ * and attention kernels over all B rows at their own positions, the lm_head rows, and a
+ * per-sequence greedy argmax with the reference's tie order.  Q35_LAUNCH_STREAM launches the step's
+ * kernels one by one, Q35_LAUNCH_GRAPH replays a captured hipGraph of them. */
+typedef struct q35_batch q35_batch;
+int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out);
+int q35_batch_destroy(q35_batch* b);
+/* Zero every sequence's caches and positions. */
+int q35_batch_reset(q35_batch* b, void* stream);
+/* One decode step of all B sequences (each row's next prompt id, else its last argmax). */
+int q35_batch_step(q35_batch* b, int32_t mode, void* stream);
+int q35_batch_decode(q35_batch* b, int32_t n_steps, int32_t mode, void* stream);
+/* Greedy generation for B prompts (prompts_host: the B prompts one after another, lens_host[B]
+ * their lengths) at each sequence's current position: out_tokens_host [B][n_new + 1] receives,
+ * per sequence, the argmax after its last prompt id and after each of n_new steps, as
+ * q35_model_generate does for one.  Prompts are fed through the decode step (every row steps
+ * max(len) + n_new times; a row with a shorter prompt generates past n_new, so tmax must allow
+ * that) or, with Q35_PREFILL_GEMM in mode, through the prompt path one sequence at a time and
+ * then n_new batched steps.  decode_seconds_host (optional): wall time of the batched steps. */
+int q35_batch_generate(q35_batch* b, const int32_t* prompts_host, const int32_t* lens_host, int32_t n_new,
+                       int32_t* out_tokens_host, int32_t mode, double* decode_seconds_host, void* stream);
+/* Host copy of the B positions. */
+int q35_batch_position(q35_batch* b, int32_t* pos_out_host);
+/* Device pointer and bytes of a batch tensor ("layers.{i}.linear_attn.recurrent_state" [B][...],
+ * "layers.{i}.self_attn.k_cache" [B][kv_heads][tmax][256], "logits" [B][V], "hist" [B][tmax],
+ * "pos", "token", ...). */
+int q35_batch_tensor(q35_batch* b, const char* name, void** dptr, size_t* bytes);
+
 /* ---------------------------------------------------------------- host utilities */
 
 /* Seeded N(0, sigma) f32 values: counter-based splitmix64 + Box-Muller in double; element i of

@@ -1,0 +1,402 @@
+// Batched greedy decode: B independent sequences through the whole decode step at once, sharing
+// one model's weights.  The reference decodes one sequence (kernels.rs:447,683 squeeze to bs = 1);
+// here every projection streams its weights once for up to 8 sequences (row groups of the Q8F
+// matvec), while each sequence keeps its own conv / recurrent states, KV cache, position,
+// prompt, token and history.  A step is the single-sequence graph step with M = B:
+//   embedding of each row's token (its next prompt id, or its last argmax)
+//   per layer: [RMSNorm -> qkvz | qkv] -> DeltaNet step / attention (all rows, own positions)
+//              -> [gated norm -> out | o] -> [RMSNorm -> gate|up] -> [SwiGLU -> down]
+//   final RMSNorm + lm_head rows -> argmax per row (reference tie order) -> token, position + 1
+// Residual rows are 64-bit fixed-point accumulators as in the single-sequence step, so residual
+// adds are the projections' own atomics.  The step can be captured in a hipGraph (all control
+// data is in device memory).  Prompts are fed either through the decode step (rows at their
+// own positions, ragged lengths) or through the prompt path one sequence at a time.
+#include "model_internal.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+
+namespace q35 {
+int batch_embed_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
+                       const int32_t* plen, const int32_t* pos, fx_t* h, int B, hipStream_t st);
+int batch_argmax_groups(int V);
+int batch_argmax_launch(const float* logits, int V, int B, float* pv, int32_t* pi, int32_t* token, int32_t* pos,
+                        int32_t* hist, int ldh, hipStream_t st);
+}  // namespace q35
+
+struct q35_batch {
+  q35_model* m = nullptr;
+  int B = 0, tmax = 0;
+  std::vector<int32_t> host_pos;  // per row
+  std::map<std::string, q35_model::Buf> tensors;
+  std::vector<void*> allocs;
+  std::vector<float*> conv, rec, kc, vc;  // per layer, [B][...]
+  q35::fx_t *h = nullptr, *acc_proj = nullptr, *acc_ba = nullptr, *acc_gu = nullptr;
+  int64_t proj_n = 0;
+  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr, *pv = nullptr;
+  int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr, *pi = nullptr;
+  int32_t* pinned = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipStream_t own_stream = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+};
+
+namespace q35 {
+namespace {
+
+constexpr int kRowGroup = 8;  // rows per matvec launch
+
+int balloc(q35_batch* b, const std::string& name, size_t bytes, void** out) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes < 256 ? 256 : bytes);
+  if (e != hipSuccess) return fail(Q35_E_NOMEM, "hipMalloc(batch " + name + "): " + hipGetErrorString(e));
+  b->allocs.push_back(p);
+  b->tensors[name] = {p, bytes};
+  *out = p;
+  return Q35_OK;
+}
+template <class T>
+int balloc_t(q35_batch* b, const std::string& name, size_t n, T** out) {
+  void* p = nullptr;
+  const int rc = balloc(b, name, n * sizeof(T), &p);
+  *out = static_cast<T*>(p);
+  return rc;
+}
+
+void bdestroy(q35_batch* b) {
+  if (!b) return;
+  if (b->exec) (void)hipGraphExecDestroy(b->exec);
+  if (b->graph) (void)hipGraphDestroy(b->graph);
+  for (void* p : b->allocs) (void)hipFree(p);
+  if (b->pinned) (void)hipHostFree(b->pinned);
+  if (b->own_stream) (void)hipStreamDestroy(b->own_stream);
+  delete b;
+}
+
+hipStream_t bpick(q35_batch* b, void* s) { return s ? static_cast<hipStream_t>(s) : b->own_stream; }
+
+// One decode step of all B rows (the launch sequence a graph captures).
+int batch_step_launch(q35_batch* bt, hipStream_t st) {
+  const q35_model* m = bt->m;
+  const q35_dims& d = m->d;
+  const int B = bt->B, H = d.hidden, F = d.ffn;
+  const int nh = d.lin_heads, dk = d.lin_dk, dv = d.lin_dv;
+  const int key_dim = nh * dk, vdim = nh * dv, conv_dim = 2 * key_dim + vdim, ldq = (int)bt->proj_n;
+  const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  const int ldqg = ah * hd * 2, kvw = kvh * hd;
+  int rc;
+  if ((rc = batch_embed_launch(m->embed.q, m->embed.s, H, bt->token, bt->prompt, bt->tmax, bt->plen, bt->pos, bt->h, B, st)))
+    return rc;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    for (int r0 = 0; r0 < B; r0 += kRowGroup) {
+      const int M = std::min(kRowGroup, B - r0);
+      MvCall c;
+      c.K = H; c.M = M; c.xf = bt->h + (size_t)r0 * H; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps; c.pro = PRO_RMS;
+      if (r0 == 0) { c.zero_ptr = bt->acc_gu; c.zero_n = (int64_t)B * 2 * F; }  // last read by the previous down stage
+      fx_t* ap = bt->acc_proj + (size_t)r0 * ldq;
+      if (!L.full) {
+        c.nseg = 2;
+        c.seg[0] = MvSeg{L.qkv.q, L.qkv.s, ap, conv_dim, ldq, 1};
+        c.seg[1] = MvSeg{L.z.q, L.z.s, ap + conv_dim, vdim, ldq, 1};
+        c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = bt->acc_ba + (size_t)r0 * 2 * nh; c.aux_ldo = 2 * nh;
+      } else {
+        c.nseg = 3;
+        c.seg[0] = MvSeg{L.q.q, L.q.s, ap, ldqg, ldq, 1};
+        c.seg[1] = MvSeg{L.k.q, L.k.s, ap + ldqg, kvw, ldq, 1};
+        c.seg[2] = MvSeg{L.v.q, L.v.s, ap + ldqg + kvw, kvw, ldq, 1};
+      }
+      if ((rc = mv_kn_launch(c, st))) return rc;
+    }
+    if (!L.full) {
+      GdnCall g;
+      g.qkv_f = bt->acc_proj; g.ld_qkv = ldq; g.ba_f = bt->acc_ba; g.ld_bg = 2 * nh; g.a_log = L.a_log;
+      g.dt_bias = L.dt_bias; g.conv_state = bt->conv[l]; g.conv_w = L.conv_w; g.S = bt->rec[l]; g.o = bt->o_raw;
+      g.ld_o = vdim; g.B = B; g.nh = nh; g.dk = dk; g.dv = dv; g.conv_k = d.conv_k;
+      if ((rc = gdn_step_launch(g, st))) return rc;
+      for (int r0 = 0; r0 < B; r0 += kRowGroup) {
+        const int M = std::min(kRowGroup, B - r0);
+        MvCall c2;
+        c2.K = vdim; c2.M = M; c2.nseg = 1;
+        c2.seg[0] = MvSeg{L.out.q, L.out.s, bt->h + (size_t)r0 * H, H, H, 1};
+        c2.pro = PRO_GATED; c2.x = bt->o_raw + (size_t)r0 * vdim; c2.ldx = vdim;
+        c2.x2f = bt->acc_proj + (size_t)r0 * ldq + conv_dim; c2.ldx2 = ldq;
+        c2.pw = L.norm_w; c2.group = dv; c2.eps = d.eps;
+        c2.cs_state = bt->conv[l] + (size_t)r0 * conv_dim * 3; c2.cs_x = bt->acc_proj + (size_t)r0 * ldq;
+        c2.cs_ch = conv_dim; c2.cs_ldx = ldq; c2.cs_B = M;
+        if ((rc = mv_kn_launch(c2, st))) return rc;
+      }
+    } else {
+      AttnCall a;
+      a.qg_f = bt->acc_proj; a.ld_qg = ldq; a.k_f = bt->acc_proj + ldqg; a.v_f = bt->acc_proj + ldqg + kvw;
+      a.ld_kv = ldq; a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
+      a.rcos = m->rope_cos; a.rsin = m->rope_sin; a.rot = d.rot_dim;
+      a.kc = bt->kc[l]; a.vc = bt->vc[l]; a.tmax = bt->tmax; a.pos = bt->pos;
+      a.out = bt->attn; a.ld_out = ah * hd; a.B = B; a.nh = ah; a.nkv = kvh; a.hd = hd;
+      if ((rc = attn_launch(a, bt->ws, bt->ws_bytes, st))) return rc;
+      for (int r0 = 0; r0 < B; r0 += kRowGroup) {
+        const int M = std::min(kRowGroup, B - r0);
+        MvCall c2;
+        c2.K = ah * hd; c2.M = M; c2.nseg = 1;
+        c2.seg[0] = MvSeg{L.o.q, L.o.s, bt->h + (size_t)r0 * H, H, H, 1};
+        c2.pro = PRO_PLAIN; c2.x = bt->attn + (size_t)r0 * ah * hd; c2.ldx = ah * hd;
+        if ((rc = mv_kn_launch(c2, st))) return rc;
+      }
+    }
+    for (int r0 = 0; r0 < B; r0 += kRowGroup) {
+      const int M = std::min(kRowGroup, B - r0);
+      MvCall c3;
+      c3.K = H; c3.M = M; c3.nseg = 2;
+      fx_t* gu = bt->acc_gu + (size_t)r0 * 2 * F;
+      c3.seg[0] = MvSeg{L.gate.q, L.gate.s, gu, F, 2 * F, 1};
+      c3.seg[1] = MvSeg{L.up.q, L.up.s, gu + F, F, 2 * F, 1};
+      c3.pro = PRO_RMS; c3.xf = bt->h + (size_t)r0 * H; c3.ldx = H; c3.pw = L.post_norm; c3.eps = d.eps;
+      if (r0 == 0) {  // projection + gate accumulators: last read by this layer's out / attention stage
+        c3.zero_ptr = bt->acc_proj;
+        c3.zero_n = (int64_t)B * ldq + (int64_t)B * 2 * nh;  // acc_ba follows acc_proj
+      }
+      if ((rc = mv_kn_launch(c3, st))) return rc;
+    }
+    for (int r0 = 0; r0 < B; r0 += kRowGroup) {
+      const int M = std::min(kRowGroup, B - r0);
+      MvCall c4;
+      c4.K = F; c4.M = M; c4.nseg = 1;
+      c4.seg[0] = MvSeg{L.down.q, L.down.s, bt->h + (size_t)r0 * H, H, H, 1};
+      c4.pro = PRO_SWIGLU; c4.xf = bt->acc_gu + (size_t)r0 * 2 * F; c4.ldx = 2 * F; c4.swiglu_off = F;
+      if ((rc = mv_kn_launch(c4, st))) return rc;
+    }
+  }
+  const int nkr = nk_max_rows(H);
+  for (int r0 = 0; r0 < B; r0 += nkr) {
+    NkCall n;
+    n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = std::min(nkr, B - r0);
+    n.xf = bt->h + (size_t)r0 * H; n.ldx = H; n.y = bt->logits + (size_t)r0 * d.vocab; n.ldy = d.vocab;
+    n.pro = PRO_RMS; n.pw = m->final_norm; n.eps = d.eps;
+    if ((rc = nk_launch(n, nullptr, 0, st))) return rc;
+  }
+  return batch_argmax_launch(bt->logits, d.vocab, B, bt->pv, bt->pi, bt->token, bt->pos, bt->hist, bt->tmax, st);
+}
+
+int bcapture(q35_batch* b, hipStream_t st) {
+  if (b->exec) return Q35_OK;
+  Q35_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  const int rc = batch_step_launch(b, st);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(st, &g);
+  if (rc != Q35_OK) { if (g) (void)hipGraphDestroy(g); return rc; }
+  if (e != hipSuccess) return fail(Q35_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+  const hipError_t e2 = hipGraphInstantiate(&b->exec, g, nullptr, nullptr, 0);
+  if (e2 != hipSuccess) { (void)hipGraphDestroy(g); return fail(Q35_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e2)); }
+  b->graph = g;
+  return Q35_OK;
+}
+
+int bstep(q35_batch* b, int mode, hipStream_t st) {
+  for (int r = 0; r < b->B; ++r)
+    if (b->host_pos[r] >= b->tmax) return fail(Q35_E_SHAPE, "batch_step: a row's cache is full (position == tmax)");
+  if (mode == Q35_LAUNCH_GRAPH) {
+    int rc = bcapture(b, st);
+    if (rc) return rc;
+    Q35_HIP_TRY(hipGraphLaunch(b->exec, st));
+  } else {
+    const int rc = batch_step_launch(b, st);
+    if (rc) return rc;
+  }
+  for (int r = 0; r < b->B; ++r) b->host_pos[r] += 1;
+  return Q35_OK;
+}
+
+// The prompt-path view of row r's state.
+SeqView row_view(q35_batch* b, int r) {
+  const q35_dims& d = b->m->d;
+  const size_t conv_n = (size_t)(2 * d.lin_heads * d.lin_dk + d.lin_heads * d.lin_dv) * (d.conv_k - 1);
+  const size_t rec_n = (size_t)d.lin_heads * d.lin_dk * d.lin_dv, kv_n = (size_t)d.kv_heads * b->tmax * d.head_dim;
+  SeqView v;
+  for (size_t l = 0; l < b->conv.size(); ++l) {
+    v.conv.push_back(b->conv[l] ? b->conv[l] + r * conv_n : nullptr);
+    v.rec.push_back(b->rec[l] ? b->rec[l] + r * rec_n : nullptr);
+    v.kc.push_back(b->kc[l] ? b->kc[l] + r * kv_n : nullptr);
+    v.vc.push_back(b->vc[l] ? b->vc[l] + r * kv_n : nullptr);
+  }
+  v.token = b->token + r;
+  v.pos = b->pos + r;
+  v.hist = b->hist + (size_t)r * b->tmax;
+  v.tmax = b->tmax;
+  return v;
+}
+
+}  // namespace
+}  // namespace q35
+
+using namespace q35;
+
+extern "C" {
+
+int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
+  if (!m || !out) return fail(Q35_E_ARG, "batch_create: null pointer");
+  *out = nullptr;
+  if (B < 1 || B > 256) return fail(Q35_E_SHAPE, "batch_create: B must be in [1, 256]");
+  if (tmax < 1) return fail(Q35_E_SHAPE, "batch_create: tmax must be >= 1");
+  if (tmax > m->tmax) return fail(Q35_E_SHAPE, "batch_create: tmax larger than the model's (its rotary tables)");
+  q35_batch* b = new q35_batch();
+  b->m = m; b->B = B; b->tmax = tmax;
+  b->host_pos.assign(B, 0);
+  auto bail = [&](int code) { bdestroy(b); return code; };
+  if (hipStreamCreateWithFlags(&b->own_stream, hipStreamNonBlocking) != hipSuccess) return bail(fail(Q35_E_HIP, "hipStreamCreate failed"));
+  const q35_dims& d = m->d;
+  const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
+  const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  int rc;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    float *cs = nullptr, *rs = nullptr, *k = nullptr, *v = nullptr;
+    if (!m->layers[l].full) {
+      if ((rc = balloc_t(b, p + "linear_attn.conv_state", (size_t)B * conv_dim * (d.conv_k - 1), &cs)) ||
+          (rc = balloc_t(b, p + "linear_attn.recurrent_state", (size_t)B * nh * d.lin_dk * d.lin_dv, &rs)))
+        return bail(rc);
+    } else {
+      if ((rc = balloc_t(b, p + "self_attn.k_cache", (size_t)B * kvh * tmax * hd, &k)) ||
+          (rc = balloc_t(b, p + "self_attn.v_cache", (size_t)B * kvh * tmax * hd, &v)))
+        return bail(rc);
+    }
+    b->conv.push_back(cs); b->rec.push_back(rs); b->kc.push_back(k); b->vc.push_back(v);
+  }
+  b->proj_n = std::max<int64_t>(conv_dim + vdim, (int64_t)ah * hd * 2 + 2 * kvh * hd);
+  const int G = batch_argmax_groups(d.vocab);
+  fx_t* both = nullptr;
+  if ((rc = balloc_t(b, "acc_proj", (size_t)B * (b->proj_n + 2 * nh), &both))) return bail(rc);
+  b->acc_proj = both;
+  b->acc_ba = both + (size_t)B * b->proj_n;
+  if ((rc = balloc_t(b, "h", (size_t)B * H, &b->h)) || (rc = balloc_t(b, "acc_gu", (size_t)B * 2 * F, &b->acc_gu)) ||
+      (rc = balloc_t(b, "o_raw", (size_t)B * vdim, &b->o_raw)) || (rc = balloc_t(b, "attn", (size_t)B * ah * hd, &b->attn)) ||
+      (rc = balloc_t(b, "logits", (size_t)B * d.vocab, &b->logits)) || (rc = balloc_t(b, "argmax_pv", (size_t)B * G, &b->pv)) ||
+      (rc = balloc_t(b, "argmax_pi", (size_t)B * G, &b->pi)) || (rc = balloc_t(b, "token", B, &b->token)) ||
+      (rc = balloc_t(b, "pos", B, &b->pos)) || (rc = balloc_t(b, "prompt", (size_t)B * tmax, &b->prompt)) ||
+      (rc = balloc_t(b, "plen", B, &b->plen)) || (rc = balloc_t(b, "hist", (size_t)B * tmax, &b->hist)))
+    return bail(rc);
+  b->ws_bytes = align256(attn_ws_bytes(B, ah, kvh, hd, tmax));
+  if ((rc = balloc(b, "workspace", b->ws_bytes, &b->ws))) return bail(rc);
+  if (hipHostMalloc(reinterpret_cast<void**>(&b->pinned), sizeof(int32_t) * 2 * B, hipHostMallocDefault) != hipSuccess)
+    return bail(fail(Q35_E_NOMEM, "hipHostMalloc failed"));
+  if (hipMemset(b->ws, 0, b->ws_bytes) != hipSuccess) return bail(fail(Q35_E_HIP, "workspace clear"));
+  if ((rc = q35_batch_reset(b, nullptr))) return bail(rc);
+  if (hipStreamSynchronize(b->own_stream) != hipSuccess) return bail(fail(Q35_E_HIP, "sync"));
+  *out = b;
+  return Q35_OK;
+}
+
+int q35_batch_destroy(q35_batch* b) {
+  if (!b) return Q35_OK;
+  (void)hipDeviceSynchronize();
+  bdestroy(b);
+  return Q35_OK;
+}
+
+int q35_batch_reset(q35_batch* b, void* stream) {
+  if (!b) return fail(Q35_E_ARG, "batch_reset: null batch");
+  hipStream_t st = bpick(b, stream);
+  for (auto& kv : b->tensors)
+    if (kv.first != "workspace") Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
+  std::fill(b->host_pos.begin(), b->host_pos.end(), 0);
+  return Q35_OK;
+}
+
+int q35_batch_step(q35_batch* b, int32_t mode, void* stream) {
+  if (!b) return fail(Q35_E_ARG, "batch_step: null batch");
+  if (mode != Q35_LAUNCH_STREAM && mode != Q35_LAUNCH_GRAPH) return fail(Q35_E_ARG, "batch_step: mode must be stream or graph");
+  return bstep(b, mode, bpick(b, stream));
+}
+
+int q35_batch_decode(q35_batch* b, int32_t n_steps, int32_t mode, void* stream) {
+  if (!b) return fail(Q35_E_ARG, "batch_decode: null batch");
+  if (n_steps < 0) return fail(Q35_E_SHAPE, "batch_decode: n_steps must be >= 0");
+  for (int i = 0; i < n_steps; ++i) {
+    const int rc = q35_batch_step(b, mode, stream);
+    if (rc) return rc;
+  }
+  return Q35_OK;
+}
+
+int q35_batch_generate(q35_batch* b, const int32_t* prompts_host, const int32_t* lens_host, int32_t n_new,
+                       int32_t* out_tokens_host, int32_t mode, double* decode_seconds_host, void* stream) {
+  if (!b || !prompts_host || !lens_host || !out_tokens_host) return fail(Q35_E_ARG, "batch_generate: null pointer");
+  const bool gemm_prefill = (mode & Q35_PREFILL_GEMM) != 0;
+  mode &= ~Q35_PREFILL_GEMM;
+  if (mode != Q35_LAUNCH_STREAM && mode != Q35_LAUNCH_GRAPH) return fail(Q35_E_ARG, "batch_generate: mode must be stream or graph");
+  if (n_new < 0) return fail(Q35_E_SHAPE, "batch_generate: n_new must be >= 0");
+  const int B = b->B, V = b->m->d.vocab;
+  int maxlen = 0;
+  int64_t off = 0;
+  for (int r = 0; r < B; ++r) {
+    if (lens_host[r] < 1) return fail(Q35_E_SHAPE, "batch_generate: every prompt needs >= 1 id");
+    maxlen = std::max(maxlen, lens_host[r]);
+    for (int i = 0; i < lens_host[r]; ++i)
+      if (prompts_host[off + i] < 0 || prompts_host[off + i] >= V) return fail(Q35_E_ARG, "batch_generate: prompt id out of range");
+    off += lens_host[r];
+  }
+  // decode-step feeding runs every row for max(len) + n_new steps; the prompt path exactly n_new
+  const int steps = gemm_prefill ? n_new : maxlen - 1 + n_new + 1;
+  std::vector<int32_t> start(B);
+  for (int r = 0; r < B; ++r) {
+    start[r] = b->host_pos[r];
+    const int64_t need = (int64_t)start[r] + (gemm_prefill ? lens_host[r] + n_new : steps);
+    if (need > b->tmax) return fail(Q35_E_SHAPE, "batch_generate: tmax too small");
+  }
+  hipStream_t st = bpick(b, stream);
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  off = 0;
+  for (int r = 0; r < B; ++r) {
+    Q35_HIP_TRY(hipMemcpy(b->prompt + (size_t)r * b->tmax + start[r], prompts_host + off, sizeof(int32_t) * lens_host[r],
+                          hipMemcpyHostToDevice));
+    off += lens_host[r];
+    b->pinned[r] = start[r] + lens_host[r];
+  }
+  Q35_HIP_TRY(hipMemcpy(b->plen, b->pinned, sizeof(int32_t) * B, hipMemcpyHostToDevice));
+  int rc;
+  if (gemm_prefill) {
+    q35_model* m = b->m;
+    if ((rc = ensure_prefill(m))) return rc;
+    for (int r = 0; r < B; ++r) {
+      const SeqView v = row_view(b, r);
+      for (int done = 0; done < lens_host[r];) {
+        const int T = std::min(m->pf_cap, lens_host[r] - done);
+        const int p0 = b->host_pos[r];
+        if ((rc = prefill_pass(m, v, b->prompt + (size_t)r * b->tmax + p0, T, p0, st))) return rc;
+        b->host_pos[r] += T;
+        done += T;
+      }
+    }
+  }
+  if (mode == Q35_LAUNCH_GRAPH && (rc = bcapture(b, st))) return rc;
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < steps; ++i)
+    if ((rc = bstep(b, mode, st))) return rc;
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const auto t1 = std::chrono::steady_clock::now();
+  if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
+  for (int r = 0; r < B; ++r)
+    Q35_HIP_TRY(hipMemcpy(out_tokens_host + (size_t)r * (n_new + 1), b->hist + (size_t)r * b->tmax + start[r] + lens_host[r] - 1,
+                          sizeof(int32_t) * (n_new + 1), hipMemcpyDeviceToHost));
+  return Q35_OK;
+}
+
+int q35_batch_position(q35_batch* b, int32_t* pos_out_host) {
+  if (!b || !pos_out_host) return fail(Q35_E_ARG, "batch_position: null pointer");
+  for (int r = 0; r < b->B; ++r) pos_out_host[r] = b->host_pos[r];
+  return Q35_OK;
+}
+
+int q35_batch_tensor(q35_batch* b, const char* name, void** dptr, size_t* bytes) {
+  if (!b || !name || !dptr) return fail(Q35_E_ARG, "batch_tensor: null pointer");
+  auto it = b->tensors.find(name);
+  if (it == b->tensors.end()) return fail(Q35_E_ARG, std::string("batch_tensor: unknown tensor ") + name);
+  *dptr = it->second.p;
+  if (bytes) *bytes = it->second.bytes;
+  return Q35_OK;
+}
+
+}  // extern "C"

@@ -23,56 +23,9 @@
 #include <map>
 #include <vector>
 
-struct q35_model {
-  q35_dims d;
-  uint64_t seed = 0;
-  int32_t tmax = 0;
-  int32_t host_pos = 0;  // host mirror of the device position
-  struct Buf { void* p; size_t bytes; };
-  std::map<std::string, Buf> tensors;
-  std::vector<void*> allocs;
-  struct Q8 { const int8_t* q; const float* s; int rows, cols; };
-  struct Layer {
-    bool full = false;
-    const float *in_norm = nullptr, *post_norm = nullptr;
-    Q8 qkv{}, z{}, out{}, q{}, k{}, v{}, o{}, gate{}, up{}, down{};
-    const float *w_b = nullptr, *w_a = nullptr, *a_log = nullptr, *dt_bias = nullptr, *conv_w = nullptr, *norm_w = nullptr;
-    const float *q_norm = nullptr, *k_norm = nullptr;
-    float *conv_state = nullptr, *rec = nullptr, *kc = nullptr, *vc = nullptr;
-  };
-  std::vector<Layer> layers;
-  Q8 embed{};
-  const float* final_norm = nullptr;
-  float *rope_cos = nullptr, *rope_sin = nullptr;
-  q35::fx_t* h = nullptr;         // residual stream [hidden]
-  q35::fx_t* acc_proj = nullptr;  // q|k|v|z (linear) or q|k|v (full) projection outputs
-  q35::fx_t* acc_ba = nullptr;    // raw in_proj_b | in_proj_a sums [2*lin_heads]
-  q35::fx_t* acc_gu = nullptr;    // gate | up [2*ffn]
-  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr;
-  int64_t acc_proj_n = 0;
-  int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr;
-  int32_t* pinned = nullptr;
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
-  hipStream_t own_stream = nullptr;
-  hipGraphExec_t exec = nullptr;
-  hipGraph_t graph = nullptr;
-  // persistent decode-step kernel (launch mode 2)
-  int step_grid = 0;
-  int step_rc = Q35_OK;  // why the persistent kernel cannot run here, if it cannot
-  std::string step_msg;
-  q35::StepArgs step_args{};
-  uint32_t bar_epoch = 0;  // grid barriers passed by all launches since the counters were zeroed
-  int bar_per_token = 0;   // grid barriers per decode step
-  bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
-  // prompt path (allocated on first use): up to pf_cap tokens per pass
-  int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
-  float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
-  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr;
-};
+#include "model_internal.h"
 
 namespace q35 {
-namespace {
 
 int dev_alloc(q35_model* m, const std::string& name, size_t bytes, void** out) {
   void* p = nullptr;
@@ -84,15 +37,9 @@ int dev_alloc(q35_model* m, const std::string& name, size_t bytes, void** out) {
   return Q35_OK;
 }
 
-template <class T>
-int dev_alloc_t(q35_model* m, const std::string& name, size_t n, T** out) {
-  void* p = nullptr;
-  int rc = dev_alloc(m, name, n * sizeof(T), &p);
-  *out = static_cast<T*>(p);
-  return rc;
-}
-
 hipStream_t pick(q35_model* m, void* s) { return s ? static_cast<hipStream_t>(s) : m->own_stream; }
+
+namespace {
 
 int launch_step(q35_model* m, hipStream_t st) {
   const q35_dims& d = m->d;
@@ -320,8 +267,25 @@ int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nu
   return Q35_OK;
 }
 
+}  // namespace
+
 // ---- prompt path (TextForCausalLM::forward at seq_len > 1, model.rs:27-84,130-138)
 constexpr int kPrefillCap = 1024;  // tokens per pass; longer prompts run in passes
+
+SeqView model_view(q35_model* m) {
+  SeqView v;
+  for (const q35_model::Layer& L : m->layers) {
+    v.conv.push_back(L.conv_state);
+    v.rec.push_back(L.rec);
+    v.kc.push_back(L.kc);
+    v.vc.push_back(L.vc);
+  }
+  v.token = m->token;
+  v.pos = m->pos;
+  v.hist = m->hist;
+  v.tmax = m->tmax;
+  return v;
+}
 
 int ensure_prefill(q35_model* m) {
   if (m->pf_cap > 0) return Q35_OK;
@@ -352,7 +316,7 @@ int ensure_prefill(q35_model* m) {
 // T rows (GEMM projections on the matrix cores, conv + chunked delta rule, causal attention),
 // then the final norm and the tied lm_head for the last row only (the only logits the greedy
 // loop reads, main.rs:93-95), whose argmax goes to the token slot and hist[p0+T-1].
-int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st) {
+int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int p0, hipStream_t st) {
   const q35_dims& d = m->d;
   const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
   const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
@@ -373,8 +337,8 @@ int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st
       if ((rc = gemm_launch(g, st))) return rc;
       if ((rc = gate_prompt_launch(m->pf_xn, H, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st))) return rc;
       GdnPrefill gp;
-      gp.raw = m->pf_y; gp.ld_raw = LDY; gp.conv_state = L.conv_state; gp.conv_state_out = L.conv_state;
-      gp.conv_w = L.conv_w; gp.bg = m->pf_bg; gp.ld_bg = 2 * nh; gp.scr = m->pf_scr; gp.S = L.rec;
+      gp.raw = m->pf_y; gp.ld_raw = LDY; gp.conv_state = v.conv[l]; gp.conv_state_out = v.conv[l];
+      gp.conv_w = L.conv_w; gp.bg = m->pf_bg; gp.ld_bg = 2 * nh; gp.scr = m->pf_scr; gp.S = v.rec[l];
       gp.out = m->pf_core; gp.ld_out = vdim; gp.T = T; gp.nh = nh; gp.key_dim = key_dim;
       gp.nchunk = (T + kGdnChunk - 1) / kGdnChunk; gp.qscale = powf((float)d.lin_dk, -0.5f);
       if ((rc = gdn_prefill_launch(gp, st))) return rc;
@@ -395,7 +359,7 @@ int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st
       AttnPrefill ap;
       ap.qg = m->pf_y; ap.ld_qg = LDY; ap.k = m->pf_y + qw; ap.v = m->pf_y + qw + kvw; ap.ld_kv = LDY;
       ap.qnw = L.q_norm; ap.knw = L.k_norm; ap.eps = d.eps; ap.rcos = m->rope_cos; ap.rsin = m->rope_sin;
-      ap.rot = d.rot_dim; ap.kc = L.kc; ap.vc = L.vc; ap.tmax = m->tmax; ap.p0 = p0; ap.T = T; ap.nh = ah;
+      ap.rot = d.rot_dim; ap.kc = v.kc[l]; ap.vc = v.vc[l]; ap.tmax = v.tmax; ap.p0 = p0; ap.T = T; ap.nh = ah;
       ap.nkv = kvh; ap.qbuf = m->pf_q; ap.out = m->pf_a; ap.ld_out = ah * hd;
       ap.scale = (float)(1.0 / sqrt((double)hd));
       if ((rc = attn_prefill_launch(ap, st))) return rc;
@@ -416,14 +380,16 @@ int prefill_pass(q35_model* m, const int32_t* ids, int T, int p0, hipStream_t st
     dn.seg[0] = seg(L.down, m->pf_x, H);
     if ((rc = gemm_launch(dn, st))) return rc;
   }
-  if ((rc = store_i32_launch(m->pos, p0 + T - 1, st))) return rc;
+  if ((rc = store_i32_launch(v.pos, p0 + T - 1, st))) return rc;
   NkCall n;
   n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = 1;
   n.x = m->pf_x + (size_t)(T - 1) * H; n.ldx = H; n.y = m->logits; n.ldy = d.vocab; n.pro = PRO_RMS;
   n.pw = m->final_norm; n.eps = d.eps;
-  n.argmax_out = m->token; n.pos_inc = m->pos; n.hist = m->hist;
+  n.argmax_out = v.token; n.pos_inc = v.pos; n.hist = v.hist;
   return nk_launch(n, m->ws, m->ws_bytes, st);
 }
+
+namespace {
 
 // The n prompt ids already in m->prompt[host_pos..) through the prompt path, in passes.
 int prefill(q35_model* m, int n, hipStream_t st) {
@@ -432,7 +398,7 @@ int prefill(q35_model* m, int n, hipStream_t st) {
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_prefill: tmax too small");
   for (int done = 0; done < n;) {
     const int T = std::min(m->pf_cap, n - done);
-    if ((rc = prefill_pass(m, m->prompt + m->host_pos, T, m->host_pos, st))) return rc;
+    if ((rc = prefill_pass(m, model_view(m), m->prompt + m->host_pos, T, m->host_pos, st))) return rc;
     m->host_pos += T;
     done += T;
   }

@@ -1,0 +1,83 @@
+// The decoder model's host-side state, shared by the model entry points (model.cpp) and the
+// batched decoder (batch.cpp).  Not part of the C ABI.
+#pragma once
+#include "q35_host.h"
+
+#include <map>
+#include <string>
+#include <vector>
+
+struct q35_model {
+  q35_dims d;
+  uint64_t seed = 0;
+  int32_t tmax = 0;
+  int32_t host_pos = 0;  // host mirror of the device position
+  struct Buf { void* p; size_t bytes; };
+  std::map<std::string, Buf> tensors;
+  std::vector<void*> allocs;
+  struct Q8 { const int8_t* q; const float* s; int rows, cols; };
+  struct Layer {
+    bool full = false;
+    const float *in_norm = nullptr, *post_norm = nullptr;
+    Q8 qkv{}, z{}, out{}, q{}, k{}, v{}, o{}, gate{}, up{}, down{};
+    const float *w_b = nullptr, *w_a = nullptr, *a_log = nullptr, *dt_bias = nullptr, *conv_w = nullptr, *norm_w = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    float *conv_state = nullptr, *rec = nullptr, *kc = nullptr, *vc = nullptr;
+  };
+  std::vector<Layer> layers;
+  Q8 embed{};
+  const float* final_norm = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  q35::fx_t* h = nullptr;         // residual stream [hidden]
+  q35::fx_t* acc_proj = nullptr;  // q|k|v|z (linear) or q|k|v (full) projection outputs
+  q35::fx_t* acc_ba = nullptr;    // raw in_proj_b | in_proj_a sums [2*lin_heads]
+  q35::fx_t* acc_gu = nullptr;    // gate | up [2*ffn]
+  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr;
+  int64_t acc_proj_n = 0;
+  int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr;
+  int32_t* pinned = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipStream_t own_stream = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  // persistent decode-step kernel (launch mode 2)
+  int step_grid = 0;
+  int step_rc = Q35_OK;  // why the persistent kernel cannot run here, if it cannot
+  std::string step_msg;
+  q35::StepArgs step_args{};
+  uint32_t bar_epoch = 0;  // grid barriers passed by all launches since the counters were zeroed
+  int bar_per_token = 0;   // grid barriers per decode step
+  bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
+  // prompt path (allocated on first use): up to pf_cap tokens per pass
+  int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
+  float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
+  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr;
+};
+
+namespace q35 {
+
+int dev_alloc(q35_model* m, const std::string& name, size_t bytes, void** out);
+template <class T>
+int dev_alloc_t(q35_model* m, const std::string& name, size_t n, T** out) {
+  void* p = nullptr;
+  int rc = dev_alloc(m, name, n * sizeof(T), &p);
+  *out = static_cast<T*>(p);
+  return rc;
+}
+hipStream_t pick(q35_model* m, void* s);
+
+// Where a prompt pass reads and writes one sequence's state: per-layer caches (null where a layer
+// has none), the token slot, the position and the history (positions 0 .. tmax-1).
+struct SeqView {
+  std::vector<float*> conv, rec, kc, vc;
+  int32_t *token = nullptr, *pos = nullptr, *hist = nullptr;
+  int32_t tmax = 0;
+};
+SeqView model_view(q35_model* m);
+// Allocates the prompt-path scratch on first use.
+int ensure_prefill(q35_model* m);
+// One prompt pass of T <= m->pf_cap tokens (device ids) at positions p0.. of sequence v.
+int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int p0, hipStream_t st);
+
+}  // namespace q35

@@ -102,9 +102,9 @@ __device__ void mv_prologue(const MvArgs& a, int k0, int klen, float* xs, float*
   if (a.pro == PRO_RMS || a.pro == PRO_EMBED_RMS) {
     // thread t holds x[t + 256 j]: all loads of the row are issued at once, then the same
     // registers feed the block's slice of xs (one round trip to memory for the prologue)
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      if (m >= a.M) break;
+    // (a runtime row loop: unrolled over MR rows with an early exit, the multi-row kernels kept
+    // the rows' registers in private memory)
+    for (int m = 0; m < (MR == 1 ? 1 : a.M); ++m) {
       float v[kRmsPerThread];
 #pragma unroll
       for (int j = 0; j < kRmsPerThread; ++j) {
@@ -188,7 +188,7 @@ __device__ void mv_aux_block(const MvArgs& a, int ab, float* xs, float* red, flo
   const int nh = a.aux_nh, groups = kThreads / nh;
   const int h = tid % nh, rg = tid / nh;
   const int nrow = (klen + groups - 1) / groups;
-  constexpr int J = 16;
+  constexpr int J = MR >= 4 ? 8 : 16;
   float wb[J], wa[J];
   auto load = [&](int j0) {
 #pragma unroll
@@ -222,16 +222,17 @@ __device__ void mv_aux_block(const MvArgs& a, int ab, float* xs, float* red, flo
   const int nout = 2 * nh;
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    if (m >= a.M) break;
-    red[rg * nout + h] = accb[m];
-    red[rg * nout + nh + h] = acca[m];
-    __syncthreads();
-    if (tid < nout) {
-      float s = 0.f;
-      for (int g = 0; g < groups; ++g) s += red[g * nout + tid];
-      fx_add(&a.aux_acc[(size_t)m * a.aux_ldo + tid], s);
+    if (m < a.M) {  // uniform: every thread takes the same branch
+      red[rg * nout + h] = accb[m];
+      red[rg * nout + nh + h] = acca[m];
+      __syncthreads();
+      if (tid < nout) {
+        float s = 0.f;
+        for (int g = 0; g < groups; ++g) s += red[g * nout + tid];
+        fx_add(&a.aux_acc[(size_t)m * a.aux_ldo + tid], s);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -275,14 +276,18 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
   // All of a block's rows (up to 16 per lane for M == 1) are requested before the prologue,
   // so the whole weight chunk is in flight while x is being prepared.
   constexpr int U = kRowsInFlight<MR>;
-  uint4 wv[U];
+  // (M == 1 keeps every row in flight in uint4 registers; the multi-row kernels use native
+  // vectors, which the compiler keeps in registers across the loop)
+  using WV = std::conditional_t<MR == 1, uint4, q35_u32x4>;
+  WV wv[U];
   float sv[U];
   auto load_batch = [&](int r0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = r0 + rr + kRowsPerStep * u;
       const bool ok = colok && r < klen;
-      wv[u] = ok ? ldg16_nt(wbase + (size_t)r * N) : make_uint4(0, 0, 0, 0);
+      if constexpr (MR == 1) wv[u] = ok ? ldg16_nt(wbase + (size_t)r * N) : make_uint4(0, 0, 0, 0);
+      else wv[u] = ok ? ldg16v_nt(wbase + (size_t)r * N) : q35_u32x4{0u, 0u, 0u, 0u};
       sv[u] = ok ? ldg_nt(sbase + (size_t)r * nb) : 0.f;
     }
   };
@@ -304,7 +309,8 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
       const int r = r0 + rr + kRowsPerStep * u;
       if (r0 + kRowsPerStep * u >= klen) break;
       float f[16];
-      unpack16(wv[u], f);
+      if constexpr (MR == 1) unpack16(wv[u], f);
+      else unpack16v(wv[u], f);
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         const float c = (r < klen) ? xs[m * kKchMax + r] * sv[u] : 0.f;

@@ -23,6 +23,11 @@ int fail(int code, const std::string& msg);
 // ------------------------------------------------------------------ device helpers
 #define Q35_DEV __device__ __forceinline__
 
+// Native 4 x u32 / 4 x f32 vectors.  Register arrays that stay live across a runtime loop must
+// use these: arrays of HIP's uint4 / float4 structs there are left in private memory (scratch).
+typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
+typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
+
 // 1/x and 1/sqrt(x) as the single hardware instructions (v_rcp_f32, v_rsq_f32; about 1 ulp):
 // the IEEE-rounded divide and square root are ~10-instruction dependent sequences each, and these
 // sit on the latency chain of every norm and gate.  Arguments here are positive and normal.
@@ -70,6 +75,13 @@ Q35_DEV float block_sum256(float v, float* sh) {
 }
 
 // 16 signed bytes -> 16 floats
+Q35_DEV void unpack16v(const q35_u32x4 w, float* f) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[q * 4 + j] = (float)(int8_t)(w[q] >> (8 * j));
+  }
+}
 Q35_DEV void unpack16(const uint4 w, float* f) {
   const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -99,10 +111,6 @@ Q35_DEV T ldg(const T* p) { return *(const Q35_GLOBAL T*)p; }
 template <class T>
 Q35_DEV void stg(T* p, T v) { *(Q35_GLOBAL T*)p = v; }
 // 16-byte global load (p 16-byte aligned)
-typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
-// Native 4 x f32 vector.  Register arrays that stay live across a runtime loop must use it: arrays
-// of HIP's float4 struct there are left in private memory (scratch), these are kept in VGPRs.
-typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
 Q35_DEV uint4 ldg16(const void* p) {
   const q35_u32x4 v = *(const Q35_GLOBAL q35_u32x4*)p;
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -116,6 +124,8 @@ Q35_DEV uint4 ldg16_nt(const void* p) {
 }
 template <class T>
 Q35_DEV T ldg_nt(const T* p) { return __builtin_nontemporal_load((const Q35_GLOBAL T*)p); }
+// The same as a native vector (for register arrays that stay live across a runtime loop)
+Q35_DEV q35_u32x4 ldg16v_nt(const void* p) { return __builtin_nontemporal_load((const Q35_GLOBAL q35_u32x4*)p); }
 
 Q35_DEV void fx_add(fx_t* p, float v) {
   __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v), __ATOMIC_RELAXED,

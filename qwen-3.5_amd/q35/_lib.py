@@ -97,6 +97,14 @@ PROTOTYPES = {
     "q35_model_prefill": (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp]),
     "q35_model_position": (ctypes.c_int, [c_vp, ctypes.POINTER(c_i32)]),
     "q35_model_tensor": (ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_vp), ctypes.POINTER(c_sz)]),
+    "q35_batch_create": (ctypes.c_int, [c_vp, c_i32, c_i32, ctypes.POINTER(c_vp)]),
+    "q35_batch_destroy": (ctypes.c_int, [c_vp]),
+    "q35_batch_reset": (ctypes.c_int, [c_vp, c_vp]),
+    "q35_batch_step": (ctypes.c_int, [c_vp, c_i32, c_vp]),
+    "q35_batch_decode": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp]),
+    "q35_batch_generate": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_vp, c_i32, ctypes.POINTER(ctypes.c_double), c_vp]),
+    "q35_batch_position": (ctypes.c_int, [c_vp, c_vp]),
+    "q35_batch_tensor": (ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_vp), ctypes.POINTER(c_sz)]),
     "q35_synth_normal": (ctypes.c_int, [c_u64, c_u64, c_i64, c_i64, c_f32, c_vp]),
     "q35_synth_uniform": (ctypes.c_int, [c_u64, c_u64, c_i64, c_i64, c_f32, c_f32, c_vp]),
     "q35_synth_stream_id": (c_u64, [ctypes.c_char_p]),

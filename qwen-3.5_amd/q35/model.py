@@ -172,6 +172,68 @@ def synth_model_tensor(dims, seed, name, n):
     return out
 
 
+class BatchDecoder:
+    """B sequences decoded together with the weights of `model` (a TextForCausalLM), each with
+    its own caches, position and history (q35_batch_*)."""
+
+    def __init__(self, model, B, tmax=None):
+        self.model, self.B = model, int(B)
+        self.tmax = int(tmax if tmax is not None else model.tmax)
+        h = ctypes.c_void_p()
+        L.check(L.lib().q35_batch_create(model.h, self.B, self.tmax, ctypes.byref(h)))
+        self.h = h
+        _live.add(self)
+
+    def close(self):
+        if self.h:
+            L.lib().q35_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        L.check(L.lib().q35_batch_reset(self.h, None))
+
+    def step(self, mode="graph", stream=None):
+        L.check(L.lib().q35_batch_step(self.h, TextForCausalLM.MODES[mode], stream))
+
+    def decode(self, n_steps, mode="graph", stream=None):
+        L.check(L.lib().q35_batch_decode(self.h, int(n_steps), TextForCausalLM.MODES[mode], stream))
+
+    def generate(self, prompts, n_new, mode="graph", prefill=False, stream=None):
+        """prompts: B id sequences (any lengths) -> (tokens [B][n_new + 1], decode_seconds)."""
+        assert len(prompts) == self.B
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompts]))
+        lens = np.ascontiguousarray(np.array([len(p) for p in prompts], np.int32))
+        out = np.zeros((self.B, n_new + 1), np.int32)
+        secs = ctypes.c_double(0.0)
+        m = TextForCausalLM.MODES[mode] | (L.Q35_PREFILL_GEMM if prefill else 0)
+        L.check(L.lib().q35_batch_generate(self.h, flat.ctypes.data, lens.ctypes.data, int(n_new), out.ctypes.data, m,
+                                           ctypes.byref(secs), stream))
+        return out, secs.value
+
+    def positions(self):
+        out = np.zeros(self.B, np.int32)
+        L.check(L.lib().q35_batch_position(self.h, out.ctypes.data))
+        return out
+
+    def tensor(self, name, dtype):
+        import torch
+        ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
+        L.check(L.lib().q35_batch_tensor(self.h, name.encode(), ctypes.byref(ptr), ctypes.byref(nbytes)))
+        torch.cuda.synchronize()
+        out = np.empty(nbytes.value // np.dtype(dtype).itemsize, dtype)
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        if hip.hipMemcpy(out.ctypes.data, ptr, nbytes.value, 2) != 0:
+            raise RuntimeError("hipMemcpy failed")
+        return out
+
+
 def safetensors_tensor(path, dims, name, n):
     """f32 values the safetensors loader takes for decoder tensor `name` (Linear weights as
     [in][out]), before quantisation; host only."""

@@ -1,0 +1,88 @@
+"""Batched greedy decode (B sequences through the whole step at once) against independent
+single-sequence runs: every row's greedy ids equal the oracle's for that sequence alone (tiny
+hybrid model; B = 3, 8 and 11, so row groups of 8 and a partial group are covered; ragged
+prompt lengths; stream launches and the captured graph; prompts through the decode step and
+through the prompt path), and at the 2B shape each row equals the single-sequence persistent
+kernel, with the benchmarked 512-token prompt's row equal to its golden ids."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import q35
+
+pytestmark = pytest.mark.gpu
+
+
+def hybrid_dims():
+    return q35.make_dims(hidden=512, ffn=1536, vocab=8192, n_layers=4, lin_heads=4, attn_heads=4, kv_heads=2)
+
+
+def oracle_run(d, seed, prompt, n_new, tmax):
+    ref = O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, seed, name, n), tmax)
+    return ref.generate(prompt, n_new)[0]
+
+
+@pytest.mark.parametrize("B", [3, 8, 11])
+@pytest.mark.parametrize("mode,prefill", [("graph", False), ("stream", False), ("graph", True)])
+def test_batch_rows_match_independent_oracle_runs(B, mode, prefill):
+    print(f"[batch] B={B} mode={mode} prefill={prefill}", flush=True)
+    d = hybrid_dims()
+    seed, n_new = 3, 20
+    rng = np.random.default_rng(B)
+    lens = rng.integers(1, 40, B)
+    prompts = [rng.integers(0, d.vocab, n).astype(np.int32) for n in lens]
+    tmax = int(lens.max()) + n_new + 8
+    m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    bt = q35.BatchDecoder(m, B, tmax)
+    toks, _ = bt.generate(prompts, n_new, mode=mode, prefill=prefill)
+    for r in range(B):
+        want = oracle_run(d, seed, prompts[r], n_new, tmax)
+        np.testing.assert_array_equal(toks[r], want, err_msg=f"row {r} (prompt length {lens[r]})")
+    if prefill:
+        np.testing.assert_array_equal(bt.positions(), lens + n_new)
+    bt.close()
+    m.close()
+
+
+def test_batch_continues_and_resets():
+    """Decoding on after generate, and a reset batch, give the same ids as a fresh run."""
+    d = hybrid_dims()
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, d.vocab, n).astype(np.int32) for n in (7, 12, 3, 9)]
+    m = q35.TextForCausalLM(d, seed=3, tmax=96)
+    bt = q35.BatchDecoder(m, 4, 96)
+    t1, _ = bt.generate(prompts, 10, mode="graph")
+    bt.decode(5, mode="graph")
+    hist = bt.tensor("hist", np.int32).reshape(4, 96)
+    bt.reset()
+    t2, _ = bt.generate(prompts, 10, mode="graph")
+    np.testing.assert_array_equal(t1, t2)
+    for r, p in enumerate(prompts):
+        want = oracle_run(d, 3, p, 10 + (12 - len(p)) + 5, 96)
+        np.testing.assert_array_equal(hist[r, len(p) - 1:len(p) - 1 + len(want)], want, err_msg=str(r))
+    bt.close()
+    m.close()
+
+
+def test_batch_2b_rows_match_single_sequence_decode():
+    print("[batch 2b] B=16", flush=True)
+    d = q35.dims_2b()
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "e2e_2b_seed0.npz"))
+    B, n_new = 16, 24
+    rng = np.random.default_rng(16)
+    prompts = [g["prompt"]] + [rng.integers(0, d.vocab, n).astype(np.int32) for n in rng.integers(5, 60, B - 1)]
+    tmax = len(g["prompt"]) + n_new + 8
+    m = q35.TextForCausalLM(d, seed=int(g["seed"]), tmax=tmax)
+    bt = q35.BatchDecoder(m, B, tmax)
+    toks, secs = bt.generate(prompts, n_new, mode="graph", prefill=True)
+    print(f"batched steps: {B * n_new / secs:.0f} tok/s", flush=True)
+    np.testing.assert_array_equal(toks[0], g["tokens"][:n_new + 1])
+    for r in range(1, B):
+        m.reset()
+        want, _ = m.generate(prompts[r], n_new, mode="persistent")
+        m.check()
+        np.testing.assert_array_equal(toks[r], want, err_msg=f"row {r}")
+    bt.close()
+    m.close()
