@@ -363,6 +363,14 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
 #define Q35_PREFILL_GEMM 0x100
 int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, void* stream);
 
+/* The decode half of q35_model_generate_until from the current position: the token slot (the
+ * argmax after the last fed token) is the first current token; up to max_new steps, ending at
+ * the first current token that is a stop id.  Same outputs.  For a chat loop that feeds a turn
+ * with q35_model_prefill and then streams the reply in chunks (main.rs:100-132). */
+int q35_model_decode_until(q35_model* m, int32_t max_new, const int32_t* stop_ids_host, int32_t n_stop,
+                           int32_t* out_tokens_host, int32_t* n_out_host, int32_t use_graph,
+                           double* decode_seconds_host, void* stream);
+
 /* Tokens consumed so far (the cache length that TextModel::forward derives positions from,
  * model.rs:37-43). */
 int q35_model_position(q35_model* m, int32_t* pos_out);

@@ -578,6 +578,16 @@ int build_model(const q35_dims* dp, uint64_t seed, int32_t tmax, const ValuesFn&
 }  // namespace
 }  // namespace q35
 
+namespace q35 {
+namespace {
+// Greedy steps from position pe (the token slot holds the current token) until a stop id or
+// max_new steps; see q35_model_generate_until.
+int decode_until(q35_model* m, int32_t pe, int32_t max_new, const int32_t* stop_ids_host, int32_t n_stop,
+                 int32_t* out_tokens_host, int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host,
+                 hipStream_t st);
+}  // namespace
+}  // namespace q35
+
 using namespace q35;
 
 extern "C" {
@@ -747,6 +757,40 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
     for (int i = 0; i < n_prompt; ++i)
       if ((rc = step(m, use_graph, st))) return rc;
   }
+  return decode_until(m, pe, max_new, stop_ids_host, n_stop, out_tokens_host, n_out_host, use_graph,
+                      decode_seconds_host, st);
+}
+
+int q35_model_decode_until(q35_model* m, int32_t max_new, const int32_t* stop_ids_host, int32_t n_stop,
+                           int32_t* out_tokens_host, int32_t* n_out_host, int32_t use_graph,
+                           double* decode_seconds_host, void* stream) {
+  if (!m || !out_tokens_host || !n_out_host) return fail(Q35_E_ARG, "model_decode_until: null pointer");
+  if (n_stop < 0 || n_stop > Q35_MAX_STOP_IDS || (n_stop > 0 && !stop_ids_host))
+    return fail(Q35_E_ARG, "model_decode_until: between 0 and 4 stop ids");
+  if (use_graph < Q35_LAUNCH_STREAM || use_graph > Q35_LAUNCH_PERSISTENT) return fail(Q35_E_ARG, "model_decode_until: bad launch mode");
+  if (max_new < 0) return fail(Q35_E_SHAPE, "model_decode_until: max_new must be >= 0");
+  if (m->host_pos < 1) return fail(Q35_E_SHAPE, "model_decode_until: nothing decoded yet (feed a prompt first)");
+  if ((int64_t)m->host_pos + max_new > m->tmax) return fail(Q35_E_SHAPE, "model_decode_until: tmax too small");
+  hipStream_t st = pick(m, stream);
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  m->pinned[0] = m->host_pos;  // generated steps from here on: the token slot feeds them
+  Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  return decode_until(m, m->host_pos, max_new, stop_ids_host, n_stop, out_tokens_host, n_out_host, use_graph,
+                      decode_seconds_host, st);
+}
+
+}  // extern "C"
+
+namespace q35 {
+namespace {
+
+int decode_until(q35_model* m, int32_t pe, int32_t max_new, const int32_t* stop_ids_host, int32_t n_stop,
+                 int32_t* out_tokens_host, int32_t* n_out_host, int32_t use_graph, double* decode_seconds_host,
+                 hipStream_t st) {
+  int rc;
+  const bool pers = (use_graph == Q35_LAUNCH_PERSISTENT);
+  if (use_graph == Q35_LAUNCH_GRAPH && (rc = capture(m, st))) return rc;
   Q35_HIP_TRY(hipStreamSynchronize(st));
   const auto t0 = std::chrono::steady_clock::now();
   int32_t produced = 0;
@@ -778,6 +822,11 @@ int q35_model_generate_until(q35_model* m, const int32_t* prompt_host, int32_t n
   *n_out_host = produced;
   return Q35_OK;
 }
+
+}  // namespace
+}  // namespace q35
+
+extern "C" {
 
 int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt, void* stream) {
   if (!m || !prompt_host) return fail(Q35_E_ARG, "model_prefill: null pointer");

@@ -119,6 +119,18 @@ class TextForCausalLM:
                                                  ctypes.byref(n), m, ctypes.byref(secs), stream))
         return out[:n.value].copy(), int(out[n.value]), secs.value
 
+    def decode_until(self, max_new, stop_ids=(), mode=None, stream=None):
+        """Greedy steps from the current token slot until a stop id or max_new steps: returns
+        (produced, last, decode_seconds) as generate_until does."""
+        s = np.ascontiguousarray(np.asarray(list(stop_ids), dtype=np.int32))
+        out = np.zeros(max_new + 1, np.int32)
+        n = ctypes.c_int32(0)
+        secs = ctypes.c_double(0.0)
+        L.check(L.lib().q35_model_decode_until(self.h, int(max_new), s.ctypes.data if s.size else None, s.size,
+                                               out.ctypes.data, ctypes.byref(n), self._mode(mode, None),
+                                               ctypes.byref(secs), stream))
+        return out[:n.value].copy(), int(out[n.value]), secs.value
+
     def prefill(self, prompt, stream=None):
         """Feeds the prompt as one forward at seq_len = len(prompt) (the prompt path); the argmax
         after its last token is left in the token slot.  Asynchronous after the upload."""
