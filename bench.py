@@ -115,6 +115,42 @@ def per_call_us(torch, st, fn, ncalls, reps=3, warm=1):
     return e0.elapsed_time(e1) * 1e3 / (reps * ncalls)
 
 
+def graph_per_call_us(torch, st, fn, ncalls, reps=5):
+    """Average time per call of fn (ncalls back-to-back kernel launches on stream st, nothing that
+    allocates or synchronises) captured once in a HIP graph and replayed `reps` times between HIP
+    events on st: device time per call including the graph's launch gap, without the host's
+    per-call issue cost."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        fn()
+    with torch.cuda.stream(st):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    with torch.cuda.stream(st):
+        for _ in range(reps):
+            g.replay()
+    e1.record(st)
+    e1.synchronize()
+    del g
+    return e0.elapsed_time(e1) * 1e3 / (reps * ncalls)
+
+
+def fit_floor(points):
+    """Least-squares t = t0 + bytes / bw over (bytes, us) points: the per-launch floor t0 (launch,
+    first-byte latency, reduction and store) and the streaming rate bw (GB/s) once running."""
+    n = len(points)
+    mx = sum(b for b, _ in points) / n
+    my = sum(t for _, t in points) / n
+    sxx = sum((b - mx) ** 2 for b, _ in points)
+    sxy = sum((b - mx) * (t - my) for b, t in points)
+    slope = sxy / sxx
+    return {"floor_us": round(my - slope * mx, 3), "stream_GB/s": round(1e-3 / slope, 1)}
+
+
 def rate(nbytes, us):
     gbs = nbytes / us / 1e3
     return {"us_per_call": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -132,6 +168,7 @@ def matvec_sweep(torch, q35, st):
               ("q_proj (query|gate)", 4096, 2048), ("k_proj / v_proj", 512, 2048), ("o (config [2048x4096])", 2048, 4096),
               ("in_proj_qkvz (fused)", 8192, 2048), ("out_proj / o_proj / in_proj_z", 2048, 2048)]
     out = {}
+    fits = {1: [], 8: []}
     for label, N, K in shapes:
         wb = K * N + K * N // 16
         R = max(2, -(-ROTATE_BYTES // wb))
@@ -148,7 +185,8 @@ def matvec_sweep(torch, q35, st):
             def run():
                 for _, _, W in copies:
                     L.check(lib.q35_q8_gemv(x.data_ptr(), M, W, y.data_ptr(), None, 0, sh))
-            row[f"M{M}"] = rate(q8_bytes(N, K, M), per_call_us(torch, st, run, R))
+            row[f"M{M}"] = rate(q8_bytes(N, K, M), graph_per_call_us(torch, st, run, R))
+            fits[M].append((q8_bytes(N, K, M), row[f"M{M}"]["us_per_call"]))
         out[f"{label} [{N}x{K}]"] = row
         del copies
         torch.cuda.empty_cache()
@@ -167,6 +205,9 @@ def matvec_sweep(torch, q35, st):
     out[f"lm_head [{V}x{D}]"] = row
     del q, s
     torch.cuda.empty_cache()
+    fits[1].append((q8_bytes(V, D, 1), row["M1"]["us_per_call"]))
+    out["fit_M1"] = fit_floor(fits[1])
+    out["fit_M8"] = fit_floor(fits[8])
     return out
 
 
@@ -400,6 +441,64 @@ def copy_calibration():
 STEP_TRAFFIC_PER_64 = 139.72e9
 
 
+# bench legs in the order main() runs them, each recognised by the first dispatch of its kernel
+# (the matvec sweep is listed per run of consecutive dispatches: one run per shape and row count,
+# in the order of SWEEP_SHAPES, M = 1 then M = 8)
+TRACE_PHASES = (("model build + prompt prefill", None, False),
+                ("decode (persistent step kernel)", "step_kernel", False),
+                ("prompt GEMM leg", "gemm_kernel", False), ("batched decode leg", "batch_embed_kernel", False),
+                ("matvec sweep", "mvp_kernel", True), ("gated delta rule decode leg", "gdn_step_kernel", False),
+                ("attention decode leg", "attn_chunk_kernel", False))
+
+
+def trace_summary(d):
+    """Kernel-only durations of a rocprofv3 --kernel-trace run (the *kernel_trace.csv under d),
+    split into the bench legs (TRACE_PHASES, by dispatch order) and grouped by kernel and grid
+    size: calls, average, median and minimum microseconds."""
+    import collections
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))
+    if not files:
+        print(f"no kernel_trace.csv under {d}", file=sys.stderr)
+        sys.exit(2)
+    rows = []
+    for r in csv.DictReader(open(files[0])):
+        g = int(r.get("Grid_Size_X", r.get("Grid_Size", 0)) or 0)
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        rows.append((t0, r["Kernel_Name"], g, (t1 - t0) / 1e3))
+    rows.sort()
+    starts, i = [], 0
+    for name, marker, runs in TRACE_PHASES:
+        if marker is None:
+            starts.append((name, 0, runs))
+            continue
+        j = next((k for k in range(i, len(rows)) if marker in rows[k][1]), None)
+        if j is not None:
+            starts.append((name, j, runs))
+            i = j + 1
+    for p, (name, j0, runs) in enumerate(starts):
+        j1 = starts[p + 1][1] if p + 1 < len(starts) else len(rows)
+        groups = collections.defaultdict(list)
+        order, run, prev = [], 0, None
+        for _, kname, g, us in rows[j0:j1]:
+            key = (kname[:110], g)
+            if runs and key != prev and "q35::" in kname:
+                run, prev = run + 1, key
+            key = (run if runs and "q35::" in kname else 0,) + key
+            if key not in groups:
+                order.append(key)
+            groups[key].append(us)
+        print(f"\n## {name}: dispatches {j0}..{j1 - 1}")
+        print(f"{'calls':>7} {'grid':>9} {'avg_us':>10} {'med_us':>10} {'min_us':>10}  kernel")
+        keys = order if runs else sorted(groups, key=lambda k: -sum(groups[k]))
+        for key in keys:
+            v = sorted(groups[key])
+            if runs and key[0] == 0:
+                continue  # library kernels between the runs (weight generation)
+            print(f"{len(v):7d} {key[2]:9d} {sum(v) / len(v):10.3f} {v[len(v) // 2]:10.3f} {v[0]:10.3f}  {key[1]}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -419,7 +518,12 @@ def main():
                     help="also time one launch per token with a host readback each step (main.rs loop)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference point for FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="only summarise a rocprofv3 kernel trace under DIR by kernel and grid")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.copy_calibration:
         copy_calibration()
         return
@@ -578,8 +682,10 @@ def main():
         "prefill_tok_s_via_decode_step": None if pre_tok_s_decode is None else round(pre_tok_s_decode, 1),
         "model_build_s": round(create_s, 1),
         "matvec_sweep": sweep,
-        "matvec_sweep_note": "panel layout, per-call time from HIP events around back-to-back calls (includes each "
-                             "launch's issue gap); kernel-only durations are in profiles/matvec_c1.md",
+        "matvec_sweep_note": "panel layout; per-call device time of back-to-back calls captured in one HIP graph (HIP "
+                             "events around the replays; includes the graph's launch gap, not the host's issue "
+                             "cost); fit_M1 / fit_M8: least-squares t = floor + bytes / stream rate over the "
+                             "shapes; kernel-only durations are in profiles/matvec_c1.md",
         "gated_delta_rule_decode": gdn,
         "attention_core_decode": attn,
         "cpu_baseline": cpu,
