@@ -1,16 +1,20 @@
 // Batched greedy decode: B independent sequences through the whole decode step at once, sharing
 // one model's weights.  The reference decodes one sequence (kernels.rs:447,683 squeeze to bs = 1);
-// here every projection streams its weights once for up to 8 sequences (row groups of the Q8F
-// matvec), while each sequence keeps its own conv / recurrent states, KV cache, position,
-// prompt, token and history.  A step is the single-sequence graph step with M = B:
-//   embedding of each row's token (its next prompt id, or its last argmax)
-//   per layer: [RMSNorm -> qkvz | qkv] -> DeltaNet step / attention (all rows, own positions)
-//              -> [gated norm -> out | o] -> [RMSNorm -> gate|up] -> [SwiGLU -> down]
+// here every projection streams its weights once for up to 32 sequences (the matrix-core batch
+// kernels of mvb.hip, on an MB-layout copy of the weights built once per model), while each
+// sequence keeps its own conv / recurrent states, KV cache, position, prompt, token and history.
+// A step:
+//   embedding of each row's token (its next prompt id, or its last argmax) -> f32 residual row,
+//     with the row's sum of squares for the first RMSNorm
+//   per layer: [RMSNorm -> qkv|z (+ DeltaNet gate sums) | q|k|v] -> DeltaNet step / attention
+//              (all rows, own positions) -> [gated RMSNorm -> out | o] += residual
+//              -> [RMSNorm -> gate|up] -> [SwiGLU -> down] += residual
 //   final RMSNorm + lm_head rows -> argmax per row (reference tie order) -> token, position + 1
-// Residual rows are 64-bit fixed-point accumulators as in the single-sequence step, so residual
-// adds are the projections' own atomics.  The step can be captured in a hipGraph (all control
-// data is in device memory).  Prompts are fed either through the decode step (rows at their
-// own positions, ragged lengths) or through the prompt path one sequence at a time.
+// Each RMSNorm's per-row statistic is accumulated by the projection that last updated the
+// residual rows (fixed point, order-independent), so no kernel re-reads whole rows for it.  The
+// step can be captured in a hipGraph (all control data is in device memory).  Prompts are fed
+// either through the decode step (rows at their own positions, ragged lengths) or through the
+// prompt path one sequence at a time.
 #include "model_internal.h"
 
 #include <algorithm>
@@ -18,8 +22,9 @@
 #include <cstring>
 
 namespace q35 {
-int batch_embed_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
-                       const int32_t* plen, const int32_t* pos, fx_t* h, int B, hipStream_t st);
+int batch_embed_f32_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
+                           const int32_t* plen, const int32_t* pos, float* h, fx_t* ss, fx_t* zero_ptr, int64_t zero_n,
+                           int B, hipStream_t st);
 int batch_argmax_groups(int V);
 int batch_argmax_launch(const float* logits, int V, int B, float* pv, int32_t* pi, int32_t* token, int32_t* pos,
                         int32_t* hist, int ldh, hipStream_t st);
@@ -32,9 +37,15 @@ struct q35_batch {
   std::map<std::string, q35_model::Buf> tensors;
   std::vector<void*> allocs;
   std::vector<float*> conv, rec, kc, vc;  // per layer, [B][...]
-  q35::fx_t *h = nullptr, *acc_proj = nullptr, *acc_ba = nullptr, *acc_gu = nullptr;
+  float *h = nullptr;      // residual rows [B][hidden]
+  float *proj = nullptr;   // q|k|v|z (linear) or q|k|v (full) projection rows [B][proj_n]
+  float *gu = nullptr;     // gate | up rows [B][2 ffn]
+  float *o_raw = nullptr, *attn = nullptr, *xn = nullptr, *logits = nullptr, *pv = nullptr, *part = nullptr;
+  q35::fx_t* ss = nullptr;   // RMSNorm statistics [2 layers + 1][B]
+  q35::fx_t* gates = nullptr;  // DeltaNet gate sums [layers][B][32] (follows ss)
   int64_t proj_n = 0;
-  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr, *pv = nullptr;
+  size_t part_floats = 0;
+  uint32_t *mb_ctr = nullptr, *gdn_ctr = nullptr;
   int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr, *pi = nullptr;
   int32_t* pinned = nullptr;
   void* ws = nullptr;
@@ -47,7 +58,9 @@ struct q35_batch {
 namespace q35 {
 namespace {
 
-constexpr int kRowGroup = 8;  // rows per matvec launch
+constexpr int kRowGroup = 32;  // rows per projection launch
+constexpr int kGateLd = 32;    // gate-sum row stride (2 x lin_heads <= 32)
+constexpr int kMbCounters = 4096;
 
 int balloc(q35_batch* b, const std::string& name, size_t bytes, void** out) {
   void* p = nullptr;
@@ -82,101 +95,102 @@ hipStream_t bpick(q35_batch* b, void* s) { return s ? static_cast<hipStream_t>(s
 int batch_step_launch(q35_batch* bt, hipStream_t st) {
   const q35_model* m = bt->m;
   const q35_dims& d = m->d;
-  const int B = bt->B, H = d.hidden, F = d.ffn;
+  const int B = bt->B, H = d.hidden, F = d.ffn, NL = d.n_layers;
   const int nh = d.lin_heads, dk = d.lin_dk, dv = d.lin_dv;
   const int key_dim = nh * dk, vdim = nh * dv, conv_dim = 2 * key_dim + vdim, ldq = (int)bt->proj_n;
   const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
   const int ldqg = ah * hd * 2, kvw = kvh * hd;
   int rc;
-  if ((rc = batch_embed_launch(m->embed.q, m->embed.s, H, bt->token, bt->prompt, bt->tmax, bt->plen, bt->pos, bt->h, B, st)))
+  // embedding rows + the first norm's statistic; clears every other statistic and gate sum
+  if ((rc = batch_embed_f32_launch(m->embed.q, m->embed.s, H, bt->token, bt->prompt, bt->tmax, bt->plen, bt->pos, bt->h,
+                                   bt->ss, bt->ss + B, (int64_t)2 * NL * B + (int64_t)NL * B * kGateLd, B, st)))
     return rc;
-  for (int l = 0; l < d.n_layers; ++l) {
+  auto base = [&](MbCall& c, int M) {
+    c.M = M; c.eps = d.eps;
+    c.part = bt->part; c.part_floats = bt->part_floats; c.ctr = bt->mb_ctr; c.nctr = kMbCounters;
+  };
+  for (int l = 0; l < NL; ++l) {
     const q35_model::Layer& L = m->layers[l];
+    const q35_model::MbLayer& W = m->mb[l];
+    fx_t* ss_in = bt->ss + (size_t)(2 * l) * B;
+    fx_t* ss_mid = bt->ss + (size_t)(2 * l + 1) * B;
+    fx_t* ss_next = bt->ss + (size_t)(2 * l + 2) * B;
+    fx_t* gates = bt->gates + (size_t)l * B * kGateLd;
     for (int r0 = 0; r0 < B; r0 += kRowGroup) {
-      const int M = std::min(kRowGroup, B - r0);
-      MvCall c;
-      c.K = H; c.M = M; c.xf = bt->h + (size_t)r0 * H; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps; c.pro = PRO_RMS;
-      if (r0 == 0) { c.zero_ptr = bt->acc_gu; c.zero_n = (int64_t)B * 2 * F; }  // last read by the previous down stage
-      fx_t* ap = bt->acc_proj + (size_t)r0 * ldq;
+      MbCall c;
+      base(c, std::min(kRowGroup, B - r0));
+      c.K = H; c.x = bt->h + (size_t)r0 * H; c.ldx = H; c.pro = MB_PRO_RMS; c.pw = L.in_norm; c.ss = ss_in + r0;
+      float* pr = bt->proj + (size_t)r0 * ldq;
       if (!L.full) {
         c.nseg = 2;
-        c.seg[0] = MvSeg{L.qkv.q, L.qkv.s, ap, conv_dim, ldq, 1};
-        c.seg[1] = MvSeg{L.z.q, L.z.s, ap + conv_dim, vdim, ldq, 1};
-        c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = bt->acc_ba + (size_t)r0 * 2 * nh; c.aux_ldo = 2 * nh;
+        c.seg[0] = MbSeg{W.qkv.q, W.qkv.s, pr, conv_dim, ldq};
+        c.seg[1] = MbSeg{W.z.q, W.z.s, pr + conv_dim, vdim, ldq};
+        c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = gates + (size_t)r0 * kGateLd; c.aux_ldo = kGateLd;
       } else {
         c.nseg = 3;
-        c.seg[0] = MvSeg{L.q.q, L.q.s, ap, ldqg, ldq, 1};
-        c.seg[1] = MvSeg{L.k.q, L.k.s, ap + ldqg, kvw, ldq, 1};
-        c.seg[2] = MvSeg{L.v.q, L.v.s, ap + ldqg + kvw, kvw, ldq, 1};
+        c.seg[0] = MbSeg{W.q.q, W.q.s, pr, ldqg, ldq};
+        c.seg[1] = MbSeg{W.k.q, W.k.s, pr + ldqg, kvw, ldq};
+        c.seg[2] = MbSeg{W.v.q, W.v.s, pr + ldqg + kvw, kvw, ldq};
       }
-      if ((rc = mv_kn_launch(c, st))) return rc;
+      if ((rc = mb_launch(c, st))) return rc;
     }
     if (!L.full) {
       GdnCall g;
-      g.qkv_f = bt->acc_proj; g.ld_qkv = ldq; g.ba_f = bt->acc_ba; g.ld_bg = 2 * nh; g.a_log = L.a_log;
-      g.dt_bias = L.dt_bias; g.conv_state = bt->conv[l]; g.conv_w = L.conv_w; g.S = bt->rec[l]; g.o = bt->o_raw;
-      g.ld_o = vdim; g.B = B; g.nh = nh; g.dk = dk; g.dv = dv; g.conv_k = d.conv_k;
+      g.qkv = bt->proj; g.ld_qkv = ldq; g.ba_f = gates; g.ld_bg = kGateLd; g.a_log = L.a_log; g.dt_bias = L.dt_bias;
+      g.conv_state = bt->conv[l]; g.conv_w = L.conv_w; g.S = bt->rec[l]; g.o = bt->o_raw; g.ld_o = vdim;
+      g.B = B; g.nh = nh; g.dk = dk; g.dv = dv; g.conv_k = d.conv_k; g.head_ctr = bt->gdn_ctr;
       if ((rc = gdn_step_launch(g, st))) return rc;
       for (int r0 = 0; r0 < B; r0 += kRowGroup) {
-        const int M = std::min(kRowGroup, B - r0);
-        MvCall c2;
-        c2.K = vdim; c2.M = M; c2.nseg = 1;
-        c2.seg[0] = MvSeg{L.out.q, L.out.s, bt->h + (size_t)r0 * H, H, H, 1};
-        c2.pro = PRO_GATED; c2.x = bt->o_raw + (size_t)r0 * vdim; c2.ldx = vdim;
-        c2.x2f = bt->acc_proj + (size_t)r0 * ldq + conv_dim; c2.ldx2 = ldq;
-        c2.pw = L.norm_w; c2.group = dv; c2.eps = d.eps;
-        c2.cs_state = bt->conv[l] + (size_t)r0 * conv_dim * 3; c2.cs_x = bt->acc_proj + (size_t)r0 * ldq;
-        c2.cs_ch = conv_dim; c2.cs_ldx = ldq; c2.cs_B = M;
-        if ((rc = mv_kn_launch(c2, st))) return rc;
+        MbCall c;
+        base(c, std::min(kRowGroup, B - r0));
+        c.K = vdim; c.x = bt->o_raw + (size_t)r0 * vdim; c.ldx = vdim; c.pro = MB_PRO_GATED;
+        c.z = bt->proj + (size_t)r0 * ldq + conv_dim; c.ldz = ldq; c.group = dv; c.pw = L.norm_w;
+        c.nseg = 1; c.seg[0] = MbSeg{W.out.q, W.out.s, bt->h + (size_t)r0 * H, H, H};
+        c.add = 1; c.ss_out = ss_mid + r0;
+        if ((rc = mb_launch(c, st))) return rc;
       }
     } else {
       AttnCall a;
-      a.qg_f = bt->acc_proj; a.ld_qg = ldq; a.k_f = bt->acc_proj + ldqg; a.v_f = bt->acc_proj + ldqg + kvw;
-      a.ld_kv = ldq; a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
+      a.qg = bt->proj; a.ld_qg = ldq; a.k = bt->proj + ldqg; a.v = bt->proj + ldqg + kvw; a.ld_kv = ldq;
+      a.qnw = L.q_norm; a.knw = L.k_norm; a.eps = d.eps;
       a.rcos = m->rope_cos; a.rsin = m->rope_sin; a.rot = d.rot_dim;
       a.kc = bt->kc[l]; a.vc = bt->vc[l]; a.tmax = bt->tmax; a.pos = bt->pos;
       a.out = bt->attn; a.ld_out = ah * hd; a.B = B; a.nh = ah; a.nkv = kvh; a.hd = hd;
       if ((rc = attn_launch(a, bt->ws, bt->ws_bytes, st))) return rc;
       for (int r0 = 0; r0 < B; r0 += kRowGroup) {
-        const int M = std::min(kRowGroup, B - r0);
-        MvCall c2;
-        c2.K = ah * hd; c2.M = M; c2.nseg = 1;
-        c2.seg[0] = MvSeg{L.o.q, L.o.s, bt->h + (size_t)r0 * H, H, H, 1};
-        c2.pro = PRO_PLAIN; c2.x = bt->attn + (size_t)r0 * ah * hd; c2.ldx = ah * hd;
-        if ((rc = mv_kn_launch(c2, st))) return rc;
+        MbCall c;
+        base(c, std::min(kRowGroup, B - r0));
+        c.K = ah * hd; c.x = bt->attn + (size_t)r0 * ah * hd; c.ldx = ah * hd; c.pro = MB_PRO_PLAIN;
+        c.nseg = 1; c.seg[0] = MbSeg{W.o.q, W.o.s, bt->h + (size_t)r0 * H, H, H};
+        c.add = 1; c.ss_out = ss_mid + r0;
+        if ((rc = mb_launch(c, st))) return rc;
       }
     }
     for (int r0 = 0; r0 < B; r0 += kRowGroup) {
-      const int M = std::min(kRowGroup, B - r0);
-      MvCall c3;
-      c3.K = H; c3.M = M; c3.nseg = 2;
-      fx_t* gu = bt->acc_gu + (size_t)r0 * 2 * F;
-      c3.seg[0] = MvSeg{L.gate.q, L.gate.s, gu, F, 2 * F, 1};
-      c3.seg[1] = MvSeg{L.up.q, L.up.s, gu + F, F, 2 * F, 1};
-      c3.pro = PRO_RMS; c3.xf = bt->h + (size_t)r0 * H; c3.ldx = H; c3.pw = L.post_norm; c3.eps = d.eps;
-      if (r0 == 0) {  // projection + gate accumulators: last read by this layer's out / attention stage
-        c3.zero_ptr = bt->acc_proj;
-        c3.zero_n = (int64_t)B * ldq + (int64_t)B * 2 * nh;  // acc_ba follows acc_proj
-      }
-      if ((rc = mv_kn_launch(c3, st))) return rc;
+      MbCall c;
+      base(c, std::min(kRowGroup, B - r0));
+      c.K = H; c.x = bt->h + (size_t)r0 * H; c.ldx = H; c.pro = MB_PRO_RMS; c.pw = L.post_norm; c.ss = ss_mid + r0;
+      float* gu = bt->gu + (size_t)r0 * 2 * F;
+      c.nseg = 2;
+      c.seg[0] = MbSeg{W.gate.q, W.gate.s, gu, F, 2 * F};
+      c.seg[1] = MbSeg{W.up.q, W.up.s, gu + F, F, 2 * F};
+      if ((rc = mb_launch(c, st))) return rc;
     }
     for (int r0 = 0; r0 < B; r0 += kRowGroup) {
-      const int M = std::min(kRowGroup, B - r0);
-      MvCall c4;
-      c4.K = F; c4.M = M; c4.nseg = 1;
-      c4.seg[0] = MvSeg{L.down.q, L.down.s, bt->h + (size_t)r0 * H, H, H, 1};
-      c4.pro = PRO_SWIGLU; c4.xf = bt->acc_gu + (size_t)r0 * 2 * F; c4.ldx = 2 * F; c4.swiglu_off = F;
-      if ((rc = mv_kn_launch(c4, st))) return rc;
+      MbCall c;
+      base(c, std::min(kRowGroup, B - r0));
+      c.K = F; c.x = bt->gu + (size_t)r0 * 2 * F; c.ldx = 2 * F; c.pro = MB_PRO_SWIGLU; c.swiglu_off = F;
+      c.nseg = 1; c.seg[0] = MbSeg{W.down.q, W.down.s, bt->h + (size_t)r0 * H, H, H};
+      c.add = 1; c.ss_out = ss_next + r0;
+      if ((rc = mb_launch(c, st))) return rc;
     }
   }
-  const int nkr = nk_max_rows(H);
-  for (int r0 = 0; r0 < B; r0 += nkr) {
-    NkCall n;
-    n.q = m->embed.q; n.s = m->embed.s; n.N = d.vocab; n.K = H; n.M = std::min(nkr, B - r0);
-    n.xf = bt->h + (size_t)r0 * H; n.ldx = H; n.y = bt->logits + (size_t)r0 * d.vocab; n.ldy = d.vocab;
-    n.pro = PRO_RMS; n.pw = m->final_norm; n.eps = d.eps;
-    if ((rc = nk_launch(n, nullptr, 0, st))) return rc;
-  }
+  // final RMSNorm, then the tied lm_head (model.rs:113-129) for every row
+  if ((rc = rms_rows_launch(bt->h, H, B, H, m->final_norm, d.eps, bt->xn, H, st))) return rc;
+  for (int r0 = 0; r0 < B; r0 += kRowGroup)
+    if ((rc = mb_lm_head_launch(m->embed.q, m->embed.s, d.vocab, H, bt->xn + (size_t)r0 * H, H,
+                                std::min(kRowGroup, B - r0), bt->logits + (size_t)r0 * d.vocab, d.vocab, st)))
+      return rc;
   return batch_argmax_launch(bt->logits, d.vocab, B, bt->pv, bt->pi, bt->token, bt->pos, bt->hist, bt->tmax, st);
 }
 
@@ -208,6 +222,45 @@ int bstep(q35_batch* b, int mode, hipStream_t st) {
   for (int r = 0; r < b->B; ++r) b->host_pos[r] += 1;
   return Q35_OK;
 }
+
+}  // namespace
+
+// MB-layout copies of every projection (once per model; the tile-major originals stay in use by
+// the single-sequence paths).
+int ensure_mb(q35_model* m, hipStream_t st) {
+  if (!m->mb.empty()) return Q35_OK;
+  std::vector<q35_model::MbLayer> mb(m->layers.size());
+  int rc;
+  auto conv = [&](const q35_model::Q8& w, const std::string& name, q35_model::Mb& out) -> int {
+    if (!w.q) return Q35_OK;
+    int8_t* q = nullptr;
+    float* s = nullptr;
+    int r;
+    if ((r = dev_alloc_t(m, "mb." + name, (size_t)w.rows * w.cols, &q)) ||
+        (r = dev_alloc_t(m, "mb." + name + ".scale", (size_t)w.rows * (w.cols / 64), &s)) ||
+        (r = mb_convert_launch(w.q, w.s, w.rows, w.cols, q, s, st)))
+      return r;
+    out.q = q;
+    out.s = s;
+    return Q35_OK;
+  };
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    const std::string p = "layers." + std::to_string(l) + ".";
+    q35_model::MbLayer& o = mb[l];
+    if ((rc = conv(L.qkv, p + "in_proj_qkv", o.qkv)) || (rc = conv(L.z, p + "in_proj_z", o.z)) ||
+        (rc = conv(L.out, p + "out_proj", o.out)) || (rc = conv(L.q, p + "q_proj", o.q)) ||
+        (rc = conv(L.k, p + "k_proj", o.k)) || (rc = conv(L.v, p + "v_proj", o.v)) || (rc = conv(L.o, p + "o_proj", o.o)) ||
+        (rc = conv(L.gate, p + "gate_proj", o.gate)) || (rc = conv(L.up, p + "up_proj", o.up)) ||
+        (rc = conv(L.down, p + "down_proj", o.down)))
+      return rc;
+  }
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  m->mb = std::move(mb);
+  return Q35_OK;
+}
+
+namespace {
 
 // The prompt-path view of row r's state.
 SeqView row_view(q35_batch* b, int r) {
@@ -249,7 +302,11 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   const q35_dims& d = m->d;
   const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
   const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
+  if (H % 128 || F % 128 || vdim % 128 || (ah * hd) % 128 || kvh * hd % 64 || d.lin_dv > 128 || 2 * nh > kGateLd)
+    return bail(fail(Q35_E_SHAPE, "batch_create: the batched kernels need hidden, ffn, the DeltaNet value width and the "
+                                  "attention width to be multiples of 128, value heads of <= 128 and <= 16 DeltaNet heads"));
   int rc;
+  if ((rc = ensure_mb(m, b->own_stream))) return bail(rc);
   for (int l = 0; l < d.n_layers; ++l) {
     const std::string p = "layers." + std::to_string(l) + ".";
     float *cs = nullptr, *rs = nullptr, *k = nullptr, *v = nullptr;
@@ -266,11 +323,20 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   }
   b->proj_n = std::max<int64_t>(conv_dim + vdim, (int64_t)ah * hd * 2 + 2 * kvh * hd);
   const int G = batch_argmax_groups(d.vocab);
-  fx_t* both = nullptr;
-  if ((rc = balloc_t(b, "acc_proj", (size_t)B * (b->proj_n + 2 * nh), &both))) return bail(rc);
-  b->acc_proj = both;
-  b->acc_ba = both + (size_t)B * b->proj_n;
-  if ((rc = balloc_t(b, "h", (size_t)B * H, &b->h)) || (rc = balloc_t(b, "acc_gu", (size_t)B * 2 * F, &b->acc_gu)) ||
+  const int NL = d.n_layers;
+  // split-K partials: the largest any projection launch of this batch needs
+  const int M0 = std::min(B, kRowGroup);
+  const int shapes[6][2] = {{H, conv_dim + vdim}, {vdim, H}, {H, ah * hd * 2 + 2 * kvh * hd}, {ah * hd, H}, {H, 2 * F}, {F, H}};
+  for (const auto& kn : shapes) b->part_floats = std::max(b->part_floats, mb_part_floats(kn[1] / 64, kn[0], M0));
+  fx_t* stats = nullptr;
+  if ((rc = balloc_t(b, "norm_stats", (size_t)(2 * NL + 1) * B + (size_t)NL * B * kGateLd, &stats))) return bail(rc);
+  b->ss = stats;
+  b->gates = stats + (size_t)(2 * NL + 1) * B;
+  if ((rc = balloc_t(b, "h", (size_t)B * H, &b->h)) || (rc = balloc_t(b, "proj", (size_t)B * b->proj_n, &b->proj)) ||
+      (rc = balloc_t(b, "gu", (size_t)B * 2 * F, &b->gu)) || (rc = balloc_t(b, "xn", (size_t)B * H, &b->xn)) ||
+      (rc = balloc_t(b, "partials", std::max<size_t>(b->part_floats, 64), &b->part)) ||
+      (rc = balloc_t(b, "mb_counters", kMbCounters, &b->mb_ctr)) ||
+      (rc = balloc_t(b, "gdn_counters", (size_t)B * nh, &b->gdn_ctr)) ||
       (rc = balloc_t(b, "o_raw", (size_t)B * vdim, &b->o_raw)) || (rc = balloc_t(b, "attn", (size_t)B * ah * hd, &b->attn)) ||
       (rc = balloc_t(b, "logits", (size_t)B * d.vocab, &b->logits)) || (rc = balloc_t(b, "argmax_pv", (size_t)B * G, &b->pv)) ||
       (rc = balloc_t(b, "argmax_pi", (size_t)B * G, &b->pi)) || (rc = balloc_t(b, "token", B, &b->token)) ||

@@ -25,6 +25,30 @@ __global__ __launch_bounds__(kBT) void batch_embed_kernel(const int8_t* q, const
     h[(int64_t)b * D + k] = to_fx((float)qr[k] * sr[k >> 6]);
 }
 
+// f32 residual rows for the batched step on the matrix cores: row b's embedding (as above) into
+// h[b] and its sum of squares into ss[b] (the first RMSNorm's statistic); every block also
+// clears its share of zero_ptr[0 .. zero_n) (accumulators the step adds into).
+__global__ __launch_bounds__(kBT) void batch_embed_f32_kernel(const int8_t* q, const float* s, int D,
+                                                             const int32_t* token, const int32_t* prompt, int ldp,
+                                                             const int32_t* plen, const int32_t* pos, float* h, fx_t* ss,
+                                                             fx_t* zero_ptr, int64_t zero_n) {
+  __shared__ float sh[4];
+  for (int64_t i = (int64_t)blockIdx.x * kBT + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * kBT) zero_ptr[i] = 0;
+  const int b = blockIdx.x;
+  const int p = pos[b];
+  const int tok = p < plen[b] ? prompt[(int64_t)b * ldp + p] : token[b];
+  const int8_t* qr = q + (int64_t)tok * D;
+  const float* sr = s + (int64_t)tok * (D / 64);
+  float acc = 0.f;
+  for (int k = threadIdx.x; k < D; k += kBT) {
+    const float e = (float)qr[k] * sr[k >> 6];
+    h[(int64_t)b * D + k] = e;
+    acc += e * e;
+  }
+  acc = block_sum256(acc, sh);
+  if (threadIdx.x == 0) ss[b] = to_fx(acc);
+}
+
 Q35_DEV void block_argmax256(float& v, int& i, float* shv, int* shi, const ArgOrder& o) {
   wave_argmax(v, i, o);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -80,6 +104,15 @@ __global__ __launch_bounds__(kBT) void batch_argmax_final_kernel(const float* pv
 }
 
 }  // namespace
+
+int batch_embed_f32_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
+                           const int32_t* plen, const int32_t* pos, float* h, fx_t* ss, fx_t* zero_ptr, int64_t zero_n,
+                           int B, hipStream_t st) {
+  hipLaunchKernelGGL(batch_embed_f32_kernel, dim3(B), dim3(kBT), 0, st, q, s, D, token, prompt, ldp, plen, pos, h, ss,
+                     zero_ptr, zero_n);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
 
 int batch_embed_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
                        const int32_t* plen, const int32_t* pos, fx_t* h, int B, hipStream_t st) {

@@ -53,6 +53,11 @@ struct q35_model {
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
   float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr;
+  // batched decode (allocated on first use): every projection again in the MB layout of the
+  // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
+  struct Mb { const int8_t* q = nullptr; const float* s = nullptr; };
+  struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down; };
+  std::vector<MbLayer> mb;
 };
 
 namespace q35 {
@@ -79,5 +84,7 @@ SeqView model_view(q35_model* m);
 int ensure_prefill(q35_model* m);
 // One prompt pass of T <= m->pf_cap tokens (device ids) at positions p0.. of sequence v.
 int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int p0, hipStream_t st);
+// Builds the MB-layout copies of the projection weights on first use.
+int ensure_mb(q35_model* m, hipStream_t st);
 
 }  // namespace q35

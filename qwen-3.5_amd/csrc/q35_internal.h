@@ -487,6 +487,47 @@ int attn_launch(const AttnCall& c, void* ws, size_t ws_bytes, hipStream_t st);
 // same, with the completion counters and the chunk-partial scratch given separately
 int attn_launch_split(const AttnCall& c, uint32_t* counters, char* scratch, size_t scratch_bytes, hipStream_t st);
 
+// ------------------------------------------------------------------ batched projections (mvb.hip)
+// Y[m][n] = X~[m][:] . dequant(W)[:, n] for up to 32 rows on the fp32 matrix cores, weights in
+// the MB layout (mb_convert_launch).  X~ is x transformed by the prologue: plain, RMSNorm (with
+// the rows' sums of squares `ss` from the producer), gated RMSNorm with SiLU(z) over groups of
+// `group` values, or SwiGLU (up at column offset swiglu_off).  Outputs are stored, or added to y
+// (residual rows) with each updated row's sum of squares added to ss_out (fixed point).
+enum { MB_PRO_PLAIN = 0, MB_PRO_RMS = 1, MB_PRO_GATED = 2, MB_PRO_SWIGLU = 3 };
+constexpr int kMbMaxSeg = 4;
+struct MbSeg {
+  const int8_t* q = nullptr;  // MB layout [N/64][K/16][64][16]
+  const float* s = nullptr;   // [N/64][K]
+  float* y = nullptr;         // y[m*ldy + n]
+  int32_t N = 0, ldy = 0;
+};
+struct MbCall {
+  MbSeg seg[kMbMaxSeg];
+  int32_t nseg = 0;
+  int32_t K = 0, M = 0;
+  const float* x = nullptr; int32_t ldx = 0;
+  int32_t pro = MB_PRO_PLAIN;
+  const float* pw = nullptr; float eps = 1e-6f;
+  const fx_t* ss = nullptr;
+  const float* z = nullptr; int32_t ldz = 0, group = 0;
+  int32_t swiglu_off = 0;
+  int32_t add = 0; fx_t* ss_out = nullptr;
+  // DeltaNet gate projection side task (raw x~ . in_proj_b | x~ . in_proj_a into aux_acc)
+  const float* aux_wb = nullptr; const float* aux_wa = nullptr; int32_t aux_nh = 0;
+  fx_t* aux_acc = nullptr; int32_t aux_ldo = 0;
+  // split-K partials and one counter per 64-column block (zero between launches)
+  float* part = nullptr; size_t part_floats = 0; uint32_t* ctr = nullptr; int32_t nctr = 0;
+};
+int mb_launch(const MbCall& c, hipStream_t st);
+// Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
+size_t mb_part_floats(int ncb, int K, int M);
+// Tile-major projection weights (q[t][K][256], scale[t][K][4]) -> MB layout.
+int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
+                      hipStream_t st);
+// logits[m][n] = x[m] . dequant(E[n]) over the tied NK table, M <= 32 rows, x already normalised
+int mb_lm_head_launch(const int8_t* q, const float* s, int32_t V, int32_t K, const float* x, int32_t ldx, int32_t M,
+                      float* y, int32_t ldy, hipStream_t st);
+
 // ------------------------------------------------------------------ prompt (seq_len > 1) path
 // *p = v on the stream (a kernel, so it can sit in a captured graph)
 int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);

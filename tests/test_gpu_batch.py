@@ -1,6 +1,6 @@
 """Batched greedy decode (B sequences through the whole step at once) against independent
 single-sequence runs: every row's greedy ids equal the oracle's for that sequence alone (tiny
-hybrid model; B = 3, 8 and 11, so row groups of 8 and a partial group are covered; ragged
+hybrid model; B = 3, 8, 11 and 33, so 16- and 32-row launches and a second row group are covered; ragged
 prompt lengths; stream launches and the captured graph; prompts through the decode step and
 through the prompt path), and at the 2B shape each row equals the single-sequence persistent
 kernel, with the benchmarked 512-token prompt's row equal to its golden ids."""
@@ -24,7 +24,7 @@ def oracle_run(d, seed, prompt, n_new, tmax):
     return ref.generate(prompt, n_new)[0]
 
 
-@pytest.mark.parametrize("B", [3, 8, 11])
+@pytest.mark.parametrize("B", [3, 8, 11, 33])
 @pytest.mark.parametrize("mode,prefill", [("graph", False), ("stream", False), ("graph", True)])
 def test_batch_rows_match_independent_oracle_runs(B, mode, prefill):
     print(f"[batch] B={B} mode={mode} prefill={prefill}", flush=True)
@@ -42,6 +42,33 @@ def test_batch_rows_match_independent_oracle_runs(B, mode, prefill):
         np.testing.assert_array_equal(toks[r], want, err_msg=f"row {r} (prompt length {lens[r]})")
     if prefill:
         np.testing.assert_array_equal(bt.positions(), lens + n_new)
+    bt.close()
+    m.close()
+
+
+@pytest.mark.parametrize("B", [5, 20])
+def test_batch_logits_match_oracle(B):
+    """Every row's last-step logits against the oracle's for that sequence alone (rel-L2 <= 1e-4
+    after the prompt and 12 greedy steps), for a 16-row (B = 5) and a 32-row (B = 20) launch."""
+    print(f"[batch logits] B={B}", flush=True)
+    d = hybrid_dims()
+    seed, n_new, plen = 4, 12, 9
+    rng = np.random.default_rng(100 + B)
+    prompts = [rng.integers(0, d.vocab, plen).astype(np.int32) for _ in range(B)]
+    tmax = plen + n_new + 8
+    m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    bt = q35.BatchDecoder(m, B, tmax)
+    toks, _ = bt.generate(prompts, n_new, mode="graph")
+    logits = bt.tensor("logits", np.float32).reshape(B, d.vocab).copy()
+    for r in range(B):
+        ref = O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, seed, name, n), tmax)
+        for tok in prompts[r]:
+            t, _, _ = ref.step(tok)
+        for i in range(n_new):
+            t, _, lg = ref.step(t, want_logits=(i == n_new - 1))
+        np.testing.assert_array_equal(toks[r][-1], t, err_msg=f"row {r}")
+        err = np.linalg.norm(logits[r] - lg) / np.linalg.norm(lg)
+        assert err <= 1e-4, f"row {r}: logits rel-L2 {err:.2e}"
     bt.close()
     m.close()
 
