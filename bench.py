@@ -444,9 +444,10 @@ STEP_TRAFFIC_PER_64 = 139.72e9
 # bench legs in the order main() runs them, each recognised by the first dispatch of its kernel
 # (the matvec sweep is listed per run of consecutive dispatches: one run per shape and row count,
 # in the order of SWEEP_SHAPES, M = 1 then M = 8)
+# (legs after the batched decode leg start after its last dispatch, whose kernels they share)
 TRACE_PHASES = (("model build + prompt prefill", None, False),
-                ("decode (persistent step kernel)", "step_kernel", False),
-                ("prompt GEMM leg", "gemm_kernel", False), ("batched decode leg", "batch_embed_kernel", False),
+                ("decode (persistent step kernel)", "step_kernel<", False),
+                ("prompt GEMM leg", "gemm_kernel", False), ("batched decode leg", "batch_embed", False),
                 ("matvec sweep", "mvp_kernel", True), ("gated delta rule decode leg", "gdn_step_kernel", False),
                 ("attention decode leg", "attn_chunk_kernel", False))
 
@@ -469,10 +470,13 @@ def trace_summary(d):
         rows.append((t0, r["Kernel_Name"], g, (t1 - t0) / 1e3))
     rows.sort()
     starts, i = [], 0
+    batch_end = max((k for k in range(len(rows)) if "batch_argmax" in rows[k][1]), default=-1)
     for name, marker, runs in TRACE_PHASES:
         if marker is None:
             starts.append((name, 0, runs))
             continue
+        if name != "batched decode leg" and starts and starts[-1][0] == "batched decode leg":
+            i = batch_end + 1
         j = next((k for k in range(i, len(rows)) if marker in rows[k][1]), None)
         if j is not None:
             starts.append((name, j, runs))
