@@ -288,7 +288,8 @@ MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
 
 def prefill_gemm_leg(torch, q35, st, d, T):
     """The prompt path's projection GEMMs for one T-token prompt through every layer
-    (q35_q8_gemm, fp32 matrix cores): per linear-attention layer in_proj_qkv|in_proj_z
+    (q35_q8_gemm_ws, fp32 matrix cores, with the split-K workspace the prompt path gives them;
+    split launches include their reduction kernel): per linear-attention layer in_proj_qkv|in_proj_z
     [2048 -> 8192] and out_proj [2048 -> 2048], per attention layer q|k|v [2048 -> 5120] and
     o_proj [2048 -> 2048], per layer gate|up [2048 -> 12288] and down_proj [6144 -> 2048], each
     layer with weights of its own (Q35_KN_TILED, 1.46 GB in all), timed with HIP events around
@@ -320,10 +321,14 @@ def prefill_gemm_leg(torch, q35, st, d, T):
             calls.append((K, N, mat(K, N), acc))
             flops += 2 * T * K * N
 
+    ws_bytes = max(lib.q35_q8_gemm_ws_bytes(T, W) for _, _, W, _ in calls)
+    ws = torch.empty(ws_bytes // 4 + 64, dtype=torch.float32, device="cuda")
+
     def run():
         for K, N, W, acc in calls:
             out = R if acc else Y
-            L.check(lib.q35_q8_gemm(X.data_ptr(), T, X.stride(0), W, out.data_ptr(), out.stride(0), acc, sh))
+            L.check(lib.q35_q8_gemm_ws(X.data_ptr(), T, X.stride(0), W, out.data_ptr(), out.stride(0), acc,
+                                       ws.data_ptr(), ws_bytes, sh))
     us = per_call_us(torch, st, run, 1, reps=3)
     tf = flops / us / 1e6
     del keep

@@ -224,6 +224,13 @@ int q35_rope_tables(const q35_dims* d, int32_t tmax, float* cos_host, float* sin
  * multiples of 64; any M >= 1. */
 int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
                 void* stream);
+/* The same with a workspace of q35_q8_gemm_ws_bytes(M, W) bytes: the launcher may then split K
+ * over more blocks (for shapes with few output tiles, e.g. the 2048-wide out / o / down
+ * projections) and add the splits' partial sums in a fixed order in a second kernel.  Results
+ * differ from q35_q8_gemm only in f32 summation order.  ws = NULL behaves as q35_q8_gemm. */
+size_t q35_q8_gemm_ws_bytes(int32_t M, q35_q8f W);
+int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                   void* ws, size_t ws_bytes, void* stream);
 
 /* out[t] = [beta | g] for T prompt rows, as the prompt branch computes them
  * (text_modules.rs:578-595): beta = sigmoid(x.W_b), g = -exp(A_log) * softplus(x.W_a + dt_bias)

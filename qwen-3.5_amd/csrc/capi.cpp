@@ -431,6 +431,33 @@ int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int
   return gemm_launch(c, S(stream));
 }
 
+size_t q35_q8_gemm_ws_bytes(int32_t M, q35_q8f W) {
+  if (M < 1) return 0;
+  const int N = W.layout == Q35_NK ? W.rows : W.cols;
+  return gemm_part_floats(M, N) * sizeof(float);
+}
+
+int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                   void* ws, size_t ws_bytes, void* stream) {
+  if (!ws) return q35_q8_gemm(x, M, ldx, W, y, ldy, accumulate, stream);
+  int rc = check_q8f(W, "q8_gemm_ws");
+  if (rc) return rc;
+  if (!x || !y) return fail(Q35_E_ARG, "q8_gemm_ws: null pointer");
+  if (W.layout == Q35_KN_PANEL) return fail(Q35_E_ARG, "q8_gemm_ws: layout must be Q35_KN, Q35_KN_TILED or Q35_NK");
+  const bool nk = W.layout == Q35_NK;
+  const int K = nk ? W.cols : W.rows, N = nk ? W.rows : W.cols;
+  if (M < 1) return fail(Q35_E_SHAPE, "q8_gemm_ws: M must be >= 1");
+  if (K % 64 != 0 || N % 64 != 0) return fail(Q35_E_SHAPE, "q8_gemm_ws: K and N must be multiples of 64");
+  if (ldx < K || ldy < N) return fail(Q35_E_SHAPE, "q8_gemm_ws: ldx >= K and ldy >= N required");
+  if ((reinterpret_cast<uintptr_t>(ws) & 15) != 0) return fail(Q35_E_ALIGN, "q8_gemm_ws: workspace not 16-byte aligned");
+  GemmCall c;
+  c.x = x; c.ldx = ldx; c.M = M; c.K = K; c.nseg = 1; c.accumulate = accumulate ? 1 : 0;
+  c.seg[0] = GemmSeg{W.q, W.scale, y, N, W.layout, ldy};
+  c.part = static_cast<float*>(ws);
+  c.part_floats = ws_bytes / sizeof(float);
+  return gemm_launch(c, S(stream));
+}
+
 int q35_gate_proj_prompt(const float* x, int32_t T, int32_t in_dim, const float* w_b, const float* w_a,
                          const float* a_log, const float* dt_bias, int32_t n_heads, float* out, void* stream) {
   return gate_prompt_launch(x, in_dim, T, in_dim, w_b, w_a, a_log, dt_bias, n_heads, out, S(stream));

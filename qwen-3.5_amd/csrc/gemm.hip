@@ -39,13 +39,15 @@ struct GSeg {
   const int8_t* q;
   const float* s;
   float* y;
-  int32_t N, layout, ldy, ntiles, tile0;
+  int32_t N, layout, ldy, ntiles, tile0, c0;  // c0: first column in the concatenated partials
 };
 struct GArgs {
   GSeg seg[kGemmMaxSeg];
   int32_t nseg;
   const float* x;
   int32_t ldx, M, K, mtiles, accumulate, nblocks;
+  int32_t ksplit, kchunk, ncat;  // K splits of kchunk rows; partials part[split][M][ncat]
+  float* part;
 };
 
 // Logical tile of hardware block b: the blocks of one XCD (b % 8) get consecutive logical ids.
@@ -63,7 +65,10 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(const GArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int L = xcd_remap((int)blockIdx.x, a.nblocks);
-  const int gt = L / a.mtiles, mt = L - gt * a.mtiles;
+  // logical block = (tile column, K split, M tile), M fastest: the blocks sharing a weight tile
+  // are consecutive (one XCD)
+  const int gs = L / a.mtiles, mt = L - gs * a.mtiles;
+  const int gt = gs / a.ksplit, split = gs - gt * a.ksplit;
   // the segment of tile gt, selected field by field with constant indices (a dynamic index into
   // the kernel-argument array would copy it to private memory)
   GSeg sg = a.seg[0];
@@ -72,6 +77,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(const GArgs a) {
     if (i < a.nseg && gt >= a.seg[i].tile0) sg = a.seg[i];
   const int n0 = (gt - sg.tile0) * BN, m0 = mt * BM;
   const int K = a.K;
+  const int kbeg = split * a.kchunk, kend = min(K, kbeg + a.kchunk);
 
   // ---- weight tile addressing
   // KN / KN_TILED: thread (r = tid % 32, c16 = tid / 32) loads row k0 + r, columns c16*16..+15.
@@ -151,13 +157,13 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(const GArgs a) {
 
   const int wm = w >> 1, wn = w & 1;
   const int li = lane & 31, lh = lane >> 5;
-  const int nk_steps = K / kBK;
-  gload(0);
+  const int nk_steps = (kend - kbeg) / kBK;
+  gload(kbeg);
   lstore(0);
   __syncthreads();
   for (int kb = 0; kb < nk_steps; ++kb) {
     const int buf = kb & 1;
-    if (kb + 1 < nk_steps) gload((kb + 1) * kBK);
+    if (kb + 1 < nk_steps) gload(kbeg + (kb + 1) * kBK);
     const float* Ab = &As[buf][0];
     const float* Bb = &Bs[buf][0];
 #pragma unroll
@@ -194,16 +200,42 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(const GArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int col = n0 + wn * WN + j * 32 + li;
-      float* yc = sg.y + col;
+      float* yc = a.ksplit > 1 ? a.part + (int64_t)split * a.M * a.ncat + sg.c0 + col : sg.y + col;
+      const int64_t ld = a.ksplit > 1 ? a.ncat : sg.ldy;
+      const bool acc_y = a.accumulate && a.ksplit == 1;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (row < a.M) {
-          float* p = yc + (int64_t)row * sg.ldy;
-          *p = a.accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+          float* p = yc + (int64_t)row * ld;
+          *p = acc_y ? *p + acc[i][j][r] : acc[i][j][r];
         }
       }
     }
+}
+
+// Split-K finish: y (+)= sum over the splits of part[s][m][c], in split order (deterministic);
+// one thread per 4 consecutive columns of one row.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const GArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nq = a.ncat >> 2;
+  if (i >= (int64_t)a.M * nq) return;
+  const int m = (int)(i / nq), c = (int)(i % nq) * 4;
+  GSeg sg = a.seg[0];
+#pragma unroll
+  for (int s = 1; s < kGemmMaxSeg; ++s)
+    if (s < a.nseg && c >= a.seg[s].c0) sg = a.seg[s];
+  const float* p = a.part + (int64_t)m * a.ncat + c;
+  float4 v = *(const float4*)p;
+  for (int s = 1; s < a.ksplit; ++s) {
+    const float4 u = *(const float4*)(p + (int64_t)s * a.M * a.ncat);
+    v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+  }
+  float* y = sg.y + (int64_t)m * sg.ldy + (c - sg.c0);
+  if (a.accumulate) {
+    v.x += y[0]; v.y += y[1]; v.z += y[2]; v.w += y[3];
+  }
+  y[0] = v.x; y[1] = v.y; y[2] = v.z; y[3] = v.w;
 }
 
 int g_cus = 0;
@@ -218,31 +250,48 @@ int device_cus() {
 }
 
 template <int BM, int BN>
-int launch_tile(const GemmCall& c, hipStream_t st) {
+int launch_tile(const GemmCall& c, int ksplit, hipStream_t st) {
   GArgs a{};
   a.nseg = c.nseg;
   a.x = c.x; a.ldx = c.ldx; a.M = c.M; a.K = c.K; a.accumulate = c.accumulate;
   a.mtiles = (c.M + BM - 1) / BM;
-  int tiles = 0;
+  int tiles = 0, ncat = 0;
   for (int i = 0; i < c.nseg; ++i) {
     const GemmSeg& s = c.seg[i];
-    a.seg[i] = GSeg{s.q, s.s, s.y, s.N, s.layout, s.ldy, s.N / BN, tiles};
+    a.seg[i] = GSeg{s.q, s.s, s.y, s.N, s.layout, s.ldy, s.N / BN, tiles, ncat};
     tiles += s.N / BN;
+    ncat += s.N;
   }
-  a.nblocks = tiles * a.mtiles;
+  a.ksplit = ksplit;
+  a.kchunk = ((c.K / kBK + ksplit - 1) / ksplit) * kBK;
+  a.ncat = ncat;
+  a.part = c.part;
+  a.nblocks = tiles * ksplit * a.mtiles;
   hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(a.nblocks), dim3(kGT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
+  if (ksplit > 1) {
+    const int64_t n = (int64_t)c.M * (ncat / 4);
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+    Q35_HIP_TRY(hipGetLastError());
+  }
   return Q35_OK;
 }
 
 }  // namespace
 
-// Tile shape: the one with the least estimated time, ceil(tiles / CUs) rounds of BM x BN work
-// each, a 64-wide tile costing 1.25x per element (it reads twice the LDS operands per MFMA).
-int gemm_pick(const GemmCall& c, int* bm, int* bn) {
+// Tile shape and K splits: the least estimated time.  A launch takes ceil(blocks / CUs) rounds,
+// each the block's MFMA work at the efficiency measured for its tile (128 x 128: 0.70 of peak per
+// CU, 64-wide tiles 0.67 / 0.45: they read more LDS operands per MFMA); split K adds a second
+// kernel that reads the splits' partials and writes y (~4 TB/s, plus a launch).
+int gemm_pick(const GemmCall& c, int* bm, int* bn, int* ksplit) {
   bool n128 = true;
-  for (int i = 0; i < c.nseg; ++i) n128 = n128 && (c.seg[i].N % 128 == 0);
+  int64_t ncat = 0;
+  for (int i = 0; i < c.nseg; ++i) {
+    n128 = n128 && (c.seg[i].N % 128 == 0);
+    ncat += c.seg[i].N;
+  }
   const int cus = device_cus();
+  const double cu_flops = 157.3e12 / 256.0;
   double best = 1e300;
   const int cand[4][2] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
   for (const auto& t : cand) {
@@ -250,10 +299,16 @@ int gemm_pick(const GemmCall& c, int* bm, int* bn) {
     long long tiles = 0;
     for (int i = 0; i < c.nseg; ++i) tiles += c.seg[i].N / t[1];
     tiles *= (c.M + t[0] - 1) / t[0];
-    const double rounds = (double)((tiles + cus - 1) / cus);
-    const double eff = (t[0] == 128 ? 1.0 : 1.25) * (t[1] == 128 ? 1.0 : 1.25);
-    const double cost = rounds * t[0] * t[1] * eff;
-    if (cost < best - 1e-9) { best = cost; *bm = t[0]; *bn = t[1]; }
+    const double eff = (t[0] == 128 && t[1] == 128) ? 0.70 : (t[0] == 64 && t[1] == 64) ? 0.45 : 0.67;
+    for (int ks = 1; ks <= kGemmMaxSplit; ks *= 2) {
+      if (ks > 1 && (!c.part || c.part_floats < (size_t)ks * c.M * ncat || c.K / kBK < 2 * ks)) break;
+      const int kch = ((c.K / kBK + ks - 1) / ks) * kBK;
+      const long long blocks = tiles * ks;
+      const double rounds = (double)((blocks + cus - 1) / cus);
+      double cost = rounds * 2.0 * t[0] * t[1] * kch / (cu_flops * eff);
+      if (ks > 1) cost += (double)c.M * ncat * (ks + 1) * 4.0 / 4e12 + 3e-6;
+      if (cost < best * 0.97) { best = cost; *bm = t[0]; *bn = t[1]; *ksplit = ks; }
+    }
   }
   return Q35_OK;
 }
@@ -270,12 +325,12 @@ int gemm_launch(const GemmCall& c, hipStream_t st) {
     if (s.layout != Q35_KN && s.layout != Q35_KN_TILED && s.layout != Q35_NK) return fail(Q35_E_ARG, "gemm: layout");
     if ((reinterpret_cast<uintptr_t>(s.q) & 15) != 0) return fail(Q35_E_ALIGN, "gemm: q not 16-byte aligned");
   }
-  int bm = 128, bn = 128;
-  gemm_pick(c, &bm, &bn);
-  if (bm == 128 && bn == 128) return launch_tile<128, 128>(c, st);
-  if (bm == 64 && bn == 128) return launch_tile<64, 128>(c, st);
-  if (bm == 128 && bn == 64) return launch_tile<128, 64>(c, st);
-  return launch_tile<64, 64>(c, st);
+  int bm = 128, bn = 128, ks = 1;
+  gemm_pick(c, &bm, &bn, &ks);
+  if (bm == 128 && bn == 128) return launch_tile<128, 128>(c, ks, st);
+  if (bm == 64 && bn == 128) return launch_tile<64, 128>(c, ks, st);
+  if (bm == 128 && bn == 64) return launch_tile<128, 64>(c, ks, st);
+  return launch_tile<64, 64>(c, ks, st);
 }
 
 }  // namespace q35

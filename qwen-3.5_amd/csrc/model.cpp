@@ -304,7 +304,8 @@ int ensure_prefill(q35_model* m) {
       (rc = dev_alloc_t(m, "prefill_core", (size_t)cap * vdim, &m->pf_core)) ||
       (rc = dev_alloc_t(m, "prefill_bg", (size_t)cap * 2 * nh, &m->pf_bg)) ||
       (rc = dev_alloc_t(m, "prefill_q", (size_t)cap * ah * hd, &m->pf_q)) ||
-      (rc = dev_alloc_t(m, "prefill_scratch", (size_t)nh * nchunk * kGdnScratchPerChunk, &m->pf_scr)))
+      (rc = dev_alloc_t(m, "prefill_scratch", (size_t)nh * nchunk * kGdnScratchPerChunk, &m->pf_scr)) ||
+      (rc = dev_alloc_t(m, "prefill_partials", gemm_part_floats(cap, H), &m->pf_part)))
     return rc;
   m->pf_cap = cap;
   m->pf_ldy = ldy;
@@ -334,6 +335,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
       g.seg[0] = seg(L.qkv, m->pf_y, LDY);
       g.seg[1] = seg(L.z, m->pf_y + conv_dim, LDY);
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
       if ((rc = gemm_launch(g, st))) return rc;
       if ((rc = gate_prompt_launch(m->pf_xn, H, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st))) return rc;
       GdnPrefill gp;
@@ -347,6 +349,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       GemmCall o;
       o.x = m->pf_a; o.ldx = vdim; o.M = T; o.K = vdim; o.nseg = 1; o.accumulate = 1;
       o.seg[0] = seg(L.out, m->pf_x, H);
+      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
       if ((rc = gemm_launch(o, st))) return rc;
     } else {
       const int qw = ah * hd * 2, kvw = kvh * hd;
@@ -355,6 +358,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       g.seg[0] = seg(L.q, m->pf_y, LDY);
       g.seg[1] = seg(L.k, m->pf_y + qw, LDY);
       g.seg[2] = seg(L.v, m->pf_y + qw + kvw, LDY);
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
       if ((rc = gemm_launch(g, st))) return rc;
       AttnPrefill ap;
       ap.qg = m->pf_y; ap.ld_qg = LDY; ap.k = m->pf_y + qw; ap.v = m->pf_y + qw + kvw; ap.ld_kv = LDY;
@@ -366,6 +370,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       GemmCall o;
       o.x = m->pf_a; o.ldx = ah * hd; o.M = T; o.K = ah * hd; o.nseg = 1; o.accumulate = 1;
       o.seg[0] = seg(L.o, m->pf_x, H);
+      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
       if ((rc = gemm_launch(o, st))) return rc;
     }
     if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st))) return rc;
@@ -373,12 +378,14 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
     g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
     g.seg[0] = seg(L.gate, m->pf_y, LDY);
     g.seg[1] = seg(L.up, m->pf_y + F, LDY);
-    if ((rc = gemm_launch(g, st))) return rc;
+    g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      if ((rc = gemm_launch(g, st))) return rc;
     if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st))) return rc;
     GemmCall dn;
     dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
     dn.seg[0] = seg(L.down, m->pf_x, H);
-    if ((rc = gemm_launch(dn, st))) return rc;
+    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      if ((rc = gemm_launch(dn, st))) return rc;
   }
   if ((rc = store_i32_launch(v.pos, p0 + T - 1, st))) return rc;
   NkCall n;

@@ -52,7 +52,7 @@ struct q35_model {
   // prompt path (allocated on first use): up to pf_cap tokens per pass
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
-  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr;
+  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr, *pf_part = nullptr;
   // batched decode (allocated on first use): every projection again in the MB layout of the
   // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
   struct Mb { const int8_t* q = nullptr; const float* s = nullptr; };

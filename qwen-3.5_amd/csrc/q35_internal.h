@@ -401,10 +401,17 @@ struct GemmCall {
   const float* x = nullptr;  // [M][ldx], 16-byte aligned rows
   int32_t ldx = 0, M = 0, K = 0;
   int32_t accumulate = 0;    // 1: y += result (each element owned by one block), 0: y = result
+  // optional split-K partials [splits][M][sum of N]: the launcher may then split K when that is
+  // estimated faster, and sums the splits in a fixed order in a second kernel
+  float* part = nullptr;
+  size_t part_floats = 0;
 };
 int gemm_launch(const GemmCall& c, hipStream_t st);
-// Tile shape the launcher picks for c (BM x BN).
-int gemm_pick(const GemmCall& c, int* bm, int* bn);
+// Tile shape and K splits the launcher picks for c (BM x BN, ksplit).
+int gemm_pick(const GemmCall& c, int* bm, int* bn, int* ksplit);
+// Partial floats that let gemm_launch consider up to kGemmMaxSplit K splits for M rows of N columns.
+constexpr int kGemmMaxSplit = 4;
+inline size_t gemm_part_floats(int M, int64_t N) { return (size_t)kGemmMaxSplit * M * N; }
 
 // ------------------------------------------------------------------ Q8F NK matvec / lm_head
 struct NkCall {

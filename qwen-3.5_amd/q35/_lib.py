@@ -73,6 +73,8 @@ PROTOTYPES = {
     "q35_workspace_status": (ctypes.c_int, [c_vp, c_vp]),
     "q35_rope_tables": (ctypes.c_int, [ctypes.POINTER(Dims), c_i32, c_vp, c_vp]),
     "q35_q8_gemm": (ctypes.c_int, [c_vp, c_i32, c_i32, Q8F, c_vp, c_i32, c_i32, c_vp]),
+    "q35_q8_gemm_ws_bytes": (ctypes.c_size_t, [c_i32, Q8F]),
+    "q35_q8_gemm_ws": (ctypes.c_int, [c_vp, c_i32, c_i32, Q8F, c_vp, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
     "q35_gate_proj_prompt": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "q35_gated_delta_rule_prefill": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                                                     c_i32, c_vp, c_sz, c_vp]),

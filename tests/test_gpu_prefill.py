@@ -69,6 +69,27 @@ def test_q8_gemm_strides_and_accumulate():
     np.testing.assert_array_equal(y[:, :64], y0[:, :64])
 
 
+@pytest.mark.parametrize("accumulate", [False, True])
+@pytest.mark.parametrize("K,N", [(2048, 2048), (6144, 2048), (4096, 2048), (2048, 512)])
+@pytest.mark.parametrize("M", [130, 512])
+def test_q8_gemm_split_k(M, K, N, accumulate):
+    """q35_q8_gemm_ws: the narrow residual projections (out / o / down: N = 2048) split K over
+    more blocks and sum the splits in a second kernel; results against float64, the accumulate
+    form onto a strided y slice (rows of y wider than N)."""
+    print(f"[gemm split] M={M} K={K} N={N} acc={accumulate}", flush=True)
+    W = q8(230 + K // 64 + N, K, N)
+    x = normal(231 + M, (M, K))
+    y0 = normal(232 + M, (M, N + 64))
+    yd = dev(y0)
+    q35.q8_gemm(dev(x), q8_dev(W, q35.Q35_KN).tiled(), yd[:, 64:], accumulate=accumulate, split_k=True)
+    y = host(yd)
+    ref = x.astype(np.float64) @ W.dequant()
+    if accumulate:
+        ref = ref + y0[:, 64:].astype(np.float64)
+    assert rel_l2(y[:, 64:], ref) <= 1e-5
+    np.testing.assert_array_equal(y[:, :64], y0[:, :64])
+
+
 # ---------------------------------------------------------------- Gated DeltaNet prompt path
 
 def test_gate_proj_prompt_input_rule():
