@@ -340,7 +340,7 @@ def prefill_gemm_leg(torch, q35, st, d, T):
 
 def batch_leg(torch, q35, st, d, n_pre, n_steps=64, batches=(8, 16, 32)):
     """Batched greedy decode (q35_batch_*: B sequences through the whole step, every projection
-    streaming its weights once per 8 rows): B prompts of n_pre random ids through the prompt path,
+    streaming its weights once per 32 rows through the matrix cores): B prompts of n_pre random ids through the prompt path,
     4 untimed and n_steps timed batched steps (captured graph), timed with HIP events.  Reports
     aggregate tok/s and the algorithmic rate: weights once per step + each sequence's states, KV
     rows and matvec inputs/outputs."""

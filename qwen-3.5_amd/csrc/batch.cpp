@@ -40,7 +40,8 @@ struct q35_batch {
   float *h = nullptr;      // residual rows [B][hidden]
   float *proj = nullptr;   // q|k|v|z (linear) or q|k|v (full) projection rows [B][proj_n]
   float *gu = nullptr;     // gate | up rows [B][2 ffn]
-  float *o_raw = nullptr, *attn = nullptr, *xn = nullptr, *logits = nullptr, *pv = nullptr, *part = nullptr;
+  float *o_raw = nullptr, *attn = nullptr, *logits = nullptr, *pv = nullptr, *part = nullptr, *invf = nullptr;
+  _Float16* split16 = nullptr;  // the lm_head's split input rows (hi, lo) of one row group
   q35::fx_t* ss = nullptr;   // RMSNorm statistics [2 layers + 1][B]
   q35::fx_t* gates = nullptr;  // DeltaNet gate sums [layers][B][32] (follows ss)
   int64_t proj_n = 0;
@@ -185,11 +186,11 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       if ((rc = mb_launch(c, st))) return rc;
     }
   }
-  // final RMSNorm, then the tied lm_head (model.rs:113-129) for every row
-  if ((rc = rms_rows_launch(bt->h, H, B, H, m->final_norm, d.eps, bt->xn, H, st))) return rc;
+  // final RMSNorm and the tied lm_head (model.rs:113-129) for every row
   for (int r0 = 0; r0 < B; r0 += kRowGroup)
-    if ((rc = mb_lm_head_launch(m->embed.q, m->embed.s, d.vocab, H, bt->xn + (size_t)r0 * H, H,
-                                std::min(kRowGroup, B - r0), bt->logits + (size_t)r0 * d.vocab, d.vocab, st)))
+    if ((rc = mb_lm_head_launch(m->embed.q, m->embed_scale_t, d.vocab, H, bt->h + (size_t)r0 * H, H, m->final_norm, d.eps,
+                                std::min(kRowGroup, B - r0), bt->split16, bt->invf, bt->logits + (size_t)r0 * d.vocab,
+                                d.vocab, st)))
       return rc;
   return batch_argmax_launch(bt->logits, d.vocab, B, bt->pv, bt->pi, bt->token, bt->pos, bt->hist, bt->tmax, st);
 }
@@ -255,8 +256,13 @@ int ensure_mb(q35_model* m, hipStream_t st) {
         (rc = conv(L.down, p + "down_proj", o.down)))
       return rc;
   }
+  float* sT = nullptr;
+  if ((rc = dev_alloc_t(m, "mb.embed_scale_t", (size_t)m->d.vocab * (m->d.hidden / 64), &sT)) ||
+      (rc = mb_scale_transpose_launch(m->embed.s, m->d.vocab, m->d.hidden, sT, st)))
+    return rc;
   Q35_HIP_TRY(hipStreamSynchronize(st));
   m->mb = std::move(mb);
+  m->embed_scale_t = sT;
   return Q35_OK;
 }
 
@@ -302,9 +308,11 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   const q35_dims& d = m->d;
   const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
   const int conv_dim = 2 * key_dim + vdim, ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
-  if (H % 128 || F % 128 || vdim % 128 || (ah * hd) % 128 || kvh * hd % 64 || d.lin_dv > 128 || 2 * nh > kGateLd)
-    return bail(fail(Q35_E_SHAPE, "batch_create: the batched kernels need hidden, ffn, the DeltaNet value width and the "
-                                  "attention width to be multiples of 128, value heads of <= 128 and <= 16 DeltaNet heads"));
+  if (H % 512 || H > 2048 || F % 128 || vdim % 128 || (ah * hd) % 128 || kvh * hd % 64 || d.lin_dv > 128 ||
+      2 * nh > kGateLd)
+    return bail(fail(Q35_E_SHAPE, "batch_create: the batched kernels need a hidden size of 512, 1024, 1536 or 2048, ffn, "
+                                  "the DeltaNet value width and the attention width multiples of 128, value heads of <= "
+                                  "128 and <= 16 DeltaNet heads"));
   int rc;
   if ((rc = ensure_mb(m, b->own_stream))) return bail(rc);
   for (int l = 0; l < d.n_layers; ++l) {
@@ -333,7 +341,8 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   b->ss = stats;
   b->gates = stats + (size_t)(2 * NL + 1) * B;
   if ((rc = balloc_t(b, "h", (size_t)B * H, &b->h)) || (rc = balloc_t(b, "proj", (size_t)B * b->proj_n, &b->proj)) ||
-      (rc = balloc_t(b, "gu", (size_t)B * 2 * F, &b->gu)) || (rc = balloc_t(b, "xn", (size_t)B * H, &b->xn)) ||
+      (rc = balloc_t(b, "gu", (size_t)B * 2 * F, &b->gu)) || (rc = balloc_t(b, "lm_split16", (size_t)2 * kRowGroup * H, &b->split16)) ||
+      (rc = balloc_t(b, "lm_invf", kRowGroup, &b->invf)) ||
       (rc = balloc_t(b, "partials", std::max<size_t>(b->part_floats, 64), &b->part)) ||
       (rc = balloc_t(b, "mb_counters", kMbCounters, &b->mb_ctr)) ||
       (rc = balloc_t(b, "gdn_counters", (size_t)B * nh, &b->gdn_ctr)) ||

@@ -58,6 +58,7 @@ struct q35_model {
   struct Mb { const int8_t* q = nullptr; const float* s = nullptr; };
   struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down; };
   std::vector<MbLayer> mb;
+  const float* embed_scale_t = nullptr;  // the embedding table's scales transposed [hidden/64][vocab]
 };
 
 namespace q35 {

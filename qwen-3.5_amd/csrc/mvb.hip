@@ -1,32 +1,39 @@
-// Batched decode projections on the fp32 matrix cores: Y[m][n] = sum_k X~[m][k] * dequant(W)[k][n]
-// for up to 32 decode rows m at once (the B sequences of a batched step), so that every weight
-// matrix is streamed once per step for all rows.  The arithmetic is the reference's Linear on a
-// QFloat weight (text_modules.rs:500-508, :578-595, :638-647, :880-890, :1003-1005;
-// kernels.rs:53-92 for the Q8F block scales): each weight is dequantised to f32 (q * scale, one
-// rounding) and multiplied with v_mfma_f32_16x16x4_f32, i.e. f32 products, f32 accumulation.
+// Batched decode projections on the matrix cores: Y[m][n] = sum_k X~[m][k] * dequant(W)[k][n] for
+// up to 32 decode rows m at once (the B sequences of a batched step), so that every weight matrix
+// is streamed once per step for all rows.  This is the reference's Linear on a QFloat weight
+// (text_modules.rs:500-508, :578-595, :638-647, :880-890, :1003-1005; kernels.rs:53-92 for the
+// Q8F block scales) with f32-equivalent arithmetic on the f16 matrix cores
+// (v_mfma_f32_16x16x32_f16, f32 accumulation):
+//   * the int8 weights are exact in f16;
+//   * the scale of a weight's 64-column block multiplies the input instead, y = x~ * s (f32, the
+//     scale varies along k only), and y is carried as two f16 values hi + lo (hi = f16(y * 2^e),
+//     lo = f16(y * 2^e - hi)), about 22 significant bits, with 2^e a power of two per row chosen
+//     so that the row's largest |y| lands in [2^13, 2^14);
+//   * q * hi and q * lo are exact in the f32 accumulator; the result is scaled back by 2^-e.
 //
-// Weight layout (Q35 "MB", built once from the tile-major projection layout): per 64-column
-// block cb and 16-row step ks, 1 KB in which lane l = 16 g + c of a wave finds, as one 16-byte
-// load, the bytes u = q + 128 of q[16 ks + 4 g + j][64 cb + 16 nt + c] (j = 0..3) for each of
-// the 4 column tiles nt.  Those are exactly its A operands (row c of tile nt, k slot g) for the
-// 4 MFMA sub-steps j, with the k order permuted inside the step (the sum is unchanged).  Scales
-// are stored per column block, scale[cb][K], so a lane's 4 scales are one 16-byte read.
+// Weight layout (MB, built once from the tile-major projection layout): per 64-column block cb and
+// 32-row step ks, 2 KB in which lane l = 16 g + c of a wave finds, as two 16-byte loads, the bytes
+// u = q + 128 of q[32 ks + 8 g + j][64 cb + 16 nt + c] (j = 0..7) for each of the 4 column tiles
+// nt: exactly its A operands (row c of tile nt, k slot g) of one MFMA, with the k order permuted
+// inside the step (the sum is unchanged).  u converts to f16 as the bit pattern 0x6400 | u
+// (= 1024 + u) minus 1152.  Scales are stored per column block, scale[cb][K].
 //
-// Block = 4 waves = one column block (64 outputs) x the block's K range (at most 1024 / MT
-// rows).  The block first stages its Mp x K-range input rows, transformed by the prologue
-// (RMSNorm, gated RMSNorm or SwiGLU of the producer's output), in LDS with one round trip; then
-// the waves stream their weights with no further synchronisation: wave p takes the k steps
-// 2p and 2p+1 of every 128-row round, its weights loaded 4 rounds ahead, and reads its B
-// operands (16-byte reads) from the staged rows.  The 4 waves' accumulators are summed through
-// LDS in a fixed order.  A block with the whole K writes its outputs directly; with split-K the
-// blocks of a column block publish partials and the last to arrive sums them in split order
-// (deterministic).  Residual projections add into the f32 residual rows and accumulate each
-// row's sum of squares for the next RMSNorm (fixed point, so the sum is order-independent).
+// Block = 4 waves = one column block (64 outputs) x the block's K range (at most 1024 / MT rows).
+// The block first stages its Mp x K-range input rows: transformed by the prologue (RMSNorm, gated
+// RMSNorm or SwiGLU of the producer's output), multiplied by the column block's scales and split
+// into the hi / lo planes in LDS, with one global round trip.  Then the waves stream their
+// weights with no further synchronisation: wave p takes the 32-row step p of every 128-row round,
+// its weights loaded 4 rounds ahead.  The 4 waves' accumulators are summed through LDS in a fixed
+// order.  A block with the whole K writes its outputs directly; with split-K the blocks of a
+// column block publish partials and the last to arrive sums them in split order (deterministic).
+// Residual projections add into the f32 residual rows and accumulate each row's sum of squares
+// for the next RMSNorm (fixed point, so the sum is order-independent).
 //
 // The lm_head (mbn_kernel) reads the tied [V][D] table directly: lane l = 16 g + c takes 16
 // consecutive bytes of vocab row c of a tile (k = 16 g .. 16 g + 15 of a 64-wide scale block),
-// which are its A operands for 16 sub-steps; the row's block scale is applied to the dequantised
-// value.  Blocks of 4 waves x 64 vocab rows copy the 16 normalised x rows whole into LDS.
+// its A operands for two MFMAs; the block scale depends on the output row there, so each 64-k
+// block is accumulated separately and added with the rows' scales (read from a transposed copy of
+// the scale table).  Its input rows arrive already normalised and split (rms_rows_split_kernel).
 #include "q35_internal.h"
 
 #include <algorithm>
@@ -36,12 +43,15 @@ namespace q35 {
 namespace {
 
 constexpr int kT = 256;            // threads per block (4 waves)
-constexpr int kRound = 128;        // K rows per round (4 waves x 2 k steps of 16)
+constexpr int kRound = 128;        // K rows per round (4 waves x one 32-row step)
 constexpr int kDepth = 4;          // rounds of weights in flight per wave (mbk)
 constexpr int kNDepth = 2;         // rounds in flight per wave (mbn)
 constexpr int kNKmax = 2048;       // lm_head: largest hidden size (the whole x rows sit in LDS)
+constexpr int kNLd = kNKmax + 8;   // lm_head: padded LDS row of one plane (halves)
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 struct MbkSeg {
   const int8_t* q;  // MB layout
@@ -63,33 +73,60 @@ struct MbkArgs {
 Q35_DEV f4 ld4(const float* p) { return *(const Q35_GLOBAL f4*)p; }
 Q35_DEV f4 lds4(const float* p) { return *(const f4*)p; }
 
-// Byte j of dw holds u = q + 128 (q the int8 weight): f32(q) * s, rounded once, computed as
-// fma(u, s, -128 s) (u converts with one instruction; -128 s is exact).
-Q35_DEV float dq_byte(uint32_t dw, int j, float s, float neg128s) {
-  return __builtin_fmaf((float)((dw >> (8 * j)) & 0xffu), s, neg128s);
+// Two weights u0, u1 (bytes sel of dw, u = q + 128) -> f16 pair (q0, q1), exact.
+Q35_DEV h2 u8_pair(uint32_t dw, uint32_t sel) {
+  const uint32_t v = __builtin_amdgcn_perm(0x64646464u, dw, sel);  // halves 0x6400 | u
+  return __builtin_bit_cast(h2, v) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+// The 8 weights of bytes 0..3 of da and 0..3 of db as an f16 MFMA operand.
+Q35_DEV h8 a8_from(uint32_t da, uint32_t db) {
+  const h2 p0 = u8_pair(da, 0x04010400u), p1 = u8_pair(da, 0x04030402u);
+  const h2 p2 = u8_pair(db, 0x04010400u), p3 = u8_pair(db, 0x04030402u);
+  return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+// 2^(14 - E) and its inverse for a row whose largest |value| is amax < 2^E (E from the float's
+// exponent field; rows of zeros get 1)
+Q35_DEV void split_scale(float amax, float& f, float& inv) {
+  const int bits = __float_as_int(amax);
+  const int E = amax > 0.f ? ((bits >> 23) & 0xff) - 126 : 14;
+  const int e = min(max(14 - E, -100), 100);
+  f = __int_as_float((127 + e) << 23);
+  inv = __int_as_float((127 - e) << 23);
+}
+// y -> (hi, lo) f16 halves (packed conversions, rounding toward zero), y = hi + lo to about 22
+// bits: y - hi is exact in f32, and lo keeps its leading 11 bits
+typedef __fp16 hf2 __attribute__((ext_vector_type(2)));
+Q35_DEV void split2(float y0, float y1, uint32_t& hi, uint32_t& lo) {
+  const hf2 h = __builtin_amdgcn_cvt_pkrtz(y0, y1);
+  const hf2 l = __builtin_amdgcn_cvt_pkrtz(y0 - (float)h[0], y1 - (float)h[1]);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
 }
 
-// A block's x rows live in LDS for its whole K range: at most 1024 / MT rows of Mp = 16 MT rows
-// (64 KB), each row padded by 4 floats so that the 16 rows a B-operand read touches start in
-// different banks.
+// A block's input rows live in LDS for its whole K range: at most 1024 / MT rows of Mp = 16 MT
+// rows, as an f32 staging area (aux blocks) or as the hi / lo f16 planes, each row padded so that
+// the 16 rows a B-operand read touches start in different banks.
 template <int MT>
 struct XBuf {
   static constexpr int Mp = 16 * MT;
   static constexpr int KR = 1024 / MT;         // rows of K per block
-  static constexpr int LD = KR + 4;            // floats per staged x row
+  static constexpr int LD = KR + 4;            // floats per staged f32 row
+  static constexpr int LDH = KR + 8;           // halves per row of one f16 plane
   static constexpr int NCH = KR / kRound;      // 128-row chunks
   static constexpr int TPR = kT / Mp;          // staging threads per x row: 16 or 8
   static constexpr int VPT = kRound / TPR;     // values per thread per chunk: 8 or 16
+  static constexpr int BYTES = (Mp * LD * 4 > 2 * Mp * LDH * 2) ? Mp * LD * 4 : 2 * Mp * LDH * 2;
 };
 
-// Stage x~ for rows [k0, k0 + klen) (klen a multiple of 128, <= KR) into xs: every load the
-// range needs (x, the second operand, the norm weights, the row statistic) is issued first, so
-// staging costs one round trip; then each chunk is transformed by the prologue and written.
-// Thread t covers row t / TPR of every chunk, columns (t % TPR) * VPT .. + VPT; the rows of the
-// chunk past M repeat row M - 1 (their outputs are never stored).  The column block's weight
-// scales for the range go to scs.
-template <int MT>
-Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, float* xs, float* scs, const float* scl) {
+// Stage x~ for rows [k0, k0 + klen) (klen a multiple of 128, <= KR): every load the range needs
+// (x, the second operand, the norm weights, the row statistic) is issued first, so staging costs
+// one round trip.  Thread t covers row t / TPR of every chunk, columns (t % TPR) * VPT .. + VPT;
+// the rows of the chunk past M repeat row M - 1 (their outputs are never stored).
+//   SPLIT = false: x~ is written as f32 rows (xs, [Mp][LD]).
+//   SPLIT = true: y = x~ * scale of the column block, split into hi / lo planes (xs: hi
+//   [Mp][LDH] then lo), with the row's inverse power of two in invf[row].
+template <int MT, bool SPLIT>
+Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs, const float* scl, float* invf) {
   using X = XBuf<MT>;
   const int t = threadIdx.x, mr = t / X::TPR, m = min(mr, a.M - 1), c0 = (t % X::TPR) * X::VPT;
   const int nch = klen / kRound;
@@ -97,9 +134,9 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, float* xs, float* scs, 
   const float* xr = a.x + (size_t)m * a.ldx + k0 + c0;
   const float* ur = gated ? a.z + (size_t)m * a.ldz + k0 + c0 : xr + a.swiglu_off;
   float v[X::NCH][X::VPT], u[X::NCH][X::VPT];
-  float wg[X::VPT];  // norm weights: gated (the same VPT for every chunk), RMS (into u)
+  float wg[X::VPT];  // gated norm weights (the same VPT for every chunk); RMS weights go to u
   f4 sc = f4{0.f, 0.f, 0.f, 0.f};
-  if (scl && 4 * t < klen) sc = ld4(scl + k0 + 4 * t);
+  if (SPLIT && 4 * t < klen) sc = ld4(scl + k0 + 4 * t);
   const fx_t ssv = ldg(a.ss + m);  // (a valid dummy address without RMS: no branch, so the wait
                                    // for it lands after the x loads below are issued)
   if (gated) {
@@ -122,7 +159,7 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, float* xs, float* scs, 
       }
     }
   }
-  if (scs && 4 * t < klen) *(f4*)(scs + 4 * t) = sc;
+  if (SPLIT && 4 * t < klen) *(f4*)(scs + 4 * t) = sc;
   // y = x * rsqrt(mean(x^2) + eps) * (1 + w)  (text_modules.rs:800-808); the row's sum of
   // squares comes from the projection that produced x
   const float r = rsqrt_f(from_fx(ssv) * rcp_f((float)a.K) + a.eps);
@@ -147,12 +184,50 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, float* xs, float* scs, 
 #pragma unroll
       for (int i = 0; i < X::VPT; ++i) v[ci][i] = u[ci][i] * silu_f(v[ci][i]);
     }
-    if (ci < nch) {
-      float* dst = xs + mr * X::LD + ci * kRound + c0;
+  }
+  if (!SPLIT) {
+    float* xs = reinterpret_cast<float*>(xbuf);
 #pragma unroll
-      for (int i = 0; i < X::VPT; i += 4) *(f4*)(dst + i) = f4{v[ci][i], v[ci][i + 1], v[ci][i + 2], v[ci][i + 3]};
+    for (int ci = 0; ci < X::NCH; ++ci)
+      if (ci < nch) {
+        float* dst = xs + mr * X::LD + ci * kRound + c0;
+#pragma unroll
+        for (int i = 0; i < X::VPT; i += 4) *(f4*)(dst + i) = f4{v[ci][i], v[ci][i + 1], v[ci][i + 2], v[ci][i + 3]};
+      }
+    return;
+  }
+  __syncthreads();  // scales in LDS
+  float amax = 0.f;
+#pragma unroll
+  for (int ci = 0; ci < X::NCH; ++ci) {
+#pragma unroll
+    for (int i = 0; i < X::VPT; i += 4) {
+      const f4 s4 = lds4(scs + min(ci, nch - 1) * kRound + c0 + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[ci][i + j] *= s4[j];
+        amax = fmaxf(amax, fabsf(v[ci][i + j]));
+      }
     }
   }
+  for (int o = 1; o < X::TPR; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  float f, inv;
+  split_scale(amax, f, inv);
+  if ((t % X::TPR) == 0) invf[mr] = inv;
+  _Float16* hp = reinterpret_cast<_Float16*>(xbuf) + mr * X::LDH + c0;
+  _Float16* lp = hp + X::Mp * X::LDH;
+#pragma unroll
+  for (int ci = 0; ci < X::NCH; ++ci)
+    if (ci < nch) {
+#pragma unroll
+      for (int i = 0; i < X::VPT; i += 8) {
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split2(v[ci][i + 2 * j] * f, v[ci][i + 2 * j + 1] * f, hi[j], lo[j]);
+        *(q35_u32x4*)(hp + ci * kRound + i) = q35_u32x4{hi[0], hi[1], hi[2], hi[3]};
+        *(q35_u32x4*)(lp + ci * kRound + i) = q35_u32x4{lo[0], lo[1], lo[2], lo[3]};
+      }
+    }
 }
 
 // Segment of column block cb (constant-index field selection).
@@ -168,11 +243,12 @@ Q35_DEV MbkSeg seg_of(const MbkArgs& a, int cb) {
 // block ab sums rows [128 ab, 128 ab + 128) of x~ . W for every row m and adds the raw sums to
 // aux_acc (fixed point); the DeltaNet step applies the gates' activations.
 template <int MT>
-Q35_DEV void mbk_aux(const MbkArgs& a, int ab, float* xs, float* red) {
+Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
   using X = XBuf<MT>;
   const int t = threadIdx.x, kc = ab * kRound;
-  stage_x<MT>(a, kc, kRound, xs, nullptr, nullptr);
+  stage_x<MT, false>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr);
   __syncthreads();
+  const float* xs = reinterpret_cast<const float*>(xbuf);
   const int nh = a.aux_nh, no = 2 * nh;  // no <= 32
   const int o = t & 31, rg = t >> 5;     // 8 row groups of 16
   float w[16];
@@ -203,16 +279,17 @@ template <int MT>
 __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
   using X = XBuf<MT>;
   constexpr int Mp = X::Mp;
-  __shared__ __align__(16) float xs[Mp * X::LD];  // staged x~; reused for the wave reduction
+  __shared__ __align__(16) char xbuf[X::BYTES];  // staged x~ (f32 or hi / lo); then the reduction
   __shared__ __align__(16) float scs[X::KR];
   __shared__ __align__(16) float aux_red[256];
+  __shared__ float invf[Mp];
   __shared__ float sq[4][Mp];
   __shared__ int last_flag;
-  static_assert(4 * 16 * MT * 64 <= Mp * X::LD, "reduction buffer");
+  static_assert(4 * 16 * MT * 64 * 4 <= X::BYTES, "reduction buffer");
 
   const int nmain = a.ncb * a.nsplit;
   if ((int)blockIdx.x >= nmain) {
-    mbk_aux<MT>(a, (int)blockIdx.x - nmain, xs, aux_red);
+    mbk_aux<MT>(a, (int)blockIdx.x - nmain, xbuf, aux_red);
     return;
   }
   const int tid = threadIdx.x, lane = tid & 63, p = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -221,23 +298,26 @@ __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
   const int lcb = cb - sg.cb0;
   const int k0 = split * a.kr, klen = min(a.kr, a.K - k0);
   const int nround = klen / kRound;
-  const int nks = a.K >> 4;
-  // wave p's k steps in round r: 8 r + 2 p + e (e = 0, 1), relative to k0
-  const int8_t* wq = sg.q + ((size_t)lcb * nks + (k0 >> 4) + 2 * p) * 1024 + lane * 16;
+  const int nks = a.K >> 5;
+  // wave p's 32-row step in round r: 4 r + p, relative to k0
+  const int8_t* wq = sg.q + ((size_t)lcb * nks + (k0 >> 5) + p) * 2048 + lane * 32;
 
-  // Rounds past the block's range load 16 bytes per lane of its (cached) scales instead, so every
+  // Rounds past the block's range load 32 bytes per lane of its (cached) scales instead, so every
   // round issues the same loads and the compiler's waits count them exactly.
   const float* scl = sg.s + (size_t)lcb * a.K;
-  const int8_t* dummy = reinterpret_cast<const int8_t*>(scl) + lane * 16;
+  const int8_t* dummy = reinterpret_cast<const int8_t*>(scl) + lane * 32;
   q35_u32x4 wr[kDepth][2];
   auto load_round = [&](int r, q35_u32x4 (&w)[2]) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) w[e] = ldg16v_nt(r < nround ? wq + ((size_t)r * 8 + e) * 1024 : dummy);
+    const int8_t* src = r < nround ? wq + (size_t)r * 4 * 2048 : dummy;
+    w[0] = ldg16v_nt(src);
+    w[1] = ldg16v_nt(src + 16);
   };
   static_for<kDepth>([&](auto d) { load_round(d, wr[d]); });
-  stage_x<MT>(a, k0, klen, xs, scs, scl);
+  stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, invf);
   __syncthreads();
 
+  const _Float16* xh = reinterpret_cast<const _Float16*>(xbuf);
+  const _Float16* xl = xh + Mp * X::LDH;
   f4 acc[4][MT];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
@@ -249,41 +329,36 @@ __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
   static_for<X::NCH>([&](auto rc) {
     constexpr int r = rc, d = r % kDepth;
     if (r < nround) {
+      const int kl = r * kRound + 32 * p + 8 * g;
+      h8 bh[MT], bl[MT];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int kl = r * kRound + 16 * (2 * p + e) + 4 * g;
-          f4 xv[MT];
+      for (int mt = 0; mt < MT; ++mt) {
+        bh[mt] = *(const h8*)(xh + (16 * mt + c) * X::LDH + kl);
+        bl[mt] = *(const h8*)(xl + (16 * mt + c) * X::LDH + kl);
+      }
+      const q35_u32x4 w0 = wr[d][0], w1 = wr[d][1];
+      const h8 aw[4] = {a8_from(w0[0], w0[1]), a8_from(w0[2], w0[3]), a8_from(w1[0], w1[1]), a8_from(w1[2], w1[3])};
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) xv[mt] = lds4(xs + (16 * mt + c) * X::LD + kl);
-          const f4 sv = lds4(scs + kl);
-          const q35_u32x4 w = wr[d][e];
-          // dequantise the 16 weights first (independent), then issue the MFMAs with the four
-          // column tiles' accumulator chains interleaved
-          float av[4][4];
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float nb = -128.0f * sv[j];
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bh[mt], acc[nt][mt], 0, 0, 0);
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) av[nt][j] = dq_byte(w[nt], j, sv[j], nb);
-          }
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-              for (int mt = 0; mt < MT; ++mt)
-                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[nt][j], xv[mt][j], acc[nt][mt], 0, 0, 0);
-        }
-        if (r + kDepth < X::NCH) {
-          load_round(r + kDepth, wr[d]);
-          asm volatile("" ::: "memory");  // keep the prefetch here (not sunk to its use)
-        }
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bl[mt], acc[nt][mt], 0, 0, 0);
+      if (r + kDepth < X::NCH) {
+        load_round(r + kDepth, wr[d]);
+        asm volatile("" ::: "memory");  // keep the prefetch here (not sunk to its use)
+      }
     }
   });
 
   // Sum the 4 waves' partial sums: wave p writes its accumulators, then finalises column tile
-  // nt = p (16 columns x Mp rows) from all four in wave order.
-  float* red = xs;
+  // nt = p (16 columns x Mp rows) from all four in wave order; the row's 2^-e undoes the split's
+  // scaling.
+  float* red = reinterpret_cast<float*>(xbuf);
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
@@ -297,7 +372,7 @@ __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
     f4 v = *(const f4*)&red[((0 * 4 + p) * MT + mt) * 256 + lane * 4];
 #pragma unroll
     for (int q = 1; q < 4; ++q) v += *(const f4*)&red[((q * 4 + p) * MT + mt) * 256 + lane * 4];
-    out[mt] = v;
+    out[mt] = v * invf[16 * mt + c];
   }
   // lane holds columns n = 16 p + 4 g + i (i = 0..3) of row m = 16 mt + c
   const int ncol0 = 64 * lcb + 16 * p + 4 * g;
@@ -349,54 +424,52 @@ __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
 
 // ------------------------------------------------------------------ lm_head over the NK table
 struct MbnArgs {
-  const int8_t* q;  // [V][K]
-  const float* s;   // [V][K/64]
+  const int8_t* q;   // [V][K]
+  const float* sT;   // scales transposed, [K/64][V]
   int32_t V, K, M;
-  const float* x; int32_t ldx;  // normalised rows [M][ldx]
-  float* y; int32_t ldy;        // logits [M][ldy]
+  const _Float16* xh; const _Float16* xl; int32_t ld16;  // split rows [M][ld16] (hi, lo)
+  const float* invf;                                      // [M]
+  float* y; int32_t ldy;                                  // logits [M][ldy]
 };
 
 // One 16-byte copy per lane from global memory into LDS: lane l writes dst + 16 l (dst is
 // wave-uniform).  Counted by vmcnt like any vector load.
-Q35_DEV void dma16(const void* src, float* dst) {
+Q35_DEV void dma16(const void* src, void* dst) {
   __builtin_amdgcn_global_load_lds((const Q35_GLOBAL void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
 
-// 16 rows (M <= 16) per launch; the whole normalised x rows are copied into LDS once.
+// 16 rows (M <= 16) per launch; the split x rows are copied into LDS whole, once.
 __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
-  constexpr int LD = kNKmax + 4;
-  __shared__ __align__(16) float xs[16 * LD];
+  __shared__ __align__(16) _Float16 xs[2][16 * kNLd];  // hi, lo planes
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int nbase = (int)blockIdx.x * 256 + 64 * w;  // this wave's 64 vocab rows
-  const int nround = a.K / kRound, nkb = a.K >> 6;
+  const int nround = a.K / kRound;
 
-  // x rows into LDS: segments of 256 floats (one wave instruction each), rows past M repeat M - 1
-  const int nseg = 16 * (a.K / 256);
+  // x rows into LDS: segments of 512 halves (one wave instruction each); rows past M repeat M - 1
+  const int spr = a.K / 512, nseg = 2 * 16 * spr;
   for (int sgi = w; sgi < nseg; sgi += 4) {
-    const int m = sgi / (a.K / 256), k = (sgi % (a.K / 256)) * 256;
-    dma16(a.x + (size_t)min(m, a.M - 1) * a.ldx + k + 4 * lane, xs + m * LD + k);
+    const int pl = sgi / (16 * spr), rem = sgi % (16 * spr), m = rem / spr, k = (rem % spr) * 512;
+    const _Float16* src = (pl ? a.xl : a.xh) + (size_t)min(m, a.M - 1) * a.ld16 + k + 8 * lane;
+    dma16(src, &xs[pl][m * kNLd + k]);
   }
   // lane's rows n = nbase + 16 nt + c (clamped for the loads; not stored past V)
   const int8_t* rowp[4];
-  const float* srow[4];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int n = min(nbase + 16 * nt + c, a.V - 1);
-    rowp[nt] = a.q + (size_t)n * a.K + 16 * g;
-    srow[nt] = a.s + (size_t)n * nkb;
-  }
+  for (int nt = 0; nt < 4; ++nt) rowp[nt] = a.q + (size_t)min(nbase + 16 * nt + c, a.V - 1) * a.K + 16 * g;
+  // the output rows' scales: rows nbase + 16 nt + 4 g .. + 3 of block kb (clamped)
+  const int srow = nbase + 4 * g;
   // (rounds past K load the first round again: every round issues the same loads, so the
   // compiler's waits count them exactly)
   q35_u32x4 wr[kNDepth][2][4];
-  float sr[kNDepth][2][4];
-  auto load_round = [&](int r, q35_u32x4 (&wv)[2][4], float (&sv)[2][4]) {
+  f4 sr[kNDepth][2][4];
+  auto load_round = [&](int r, q35_u32x4 (&wv)[2][4], f4 (&sv)[2][4]) {
     const int rr = r < nround ? r : 0;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         wv[kb][nt] = ldg16v_nt(rowp[nt] + rr * kRound + 64 * kb);
-        sv[kb][nt] = ldg(srow[nt] + 2 * rr + kb);
+        sv[kb][nt] = ld4(a.sT + (size_t)(2 * rr + kb) * a.V + min(srow + 16 * nt, a.V - 4));
       }
   };
   static_for<kNDepth>([&](auto d) { load_round(d, wr[d], sr[d]); });
@@ -411,43 +484,92 @@ __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
     constexpr int r = rc, d = r % kNDepth;
     if (r < nround) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          // x[c][k + 16 g + i], i = 0..15, k = 128 r + 64 kb
-          f4 xv[4];
+      for (int kb = 0; kb < 2; ++kb) {
+        // k = 128 r + 64 kb + 16 g + 8 s + j: sub-step s takes bytes 8 s .. 8 s + 7 of the lane's 16
+        const int kl = r * kRound + 64 * kb + 16 * g;
+        h8 bh[2], bl[2];
 #pragma unroll
-          for (int h = 0; h < 4; ++h) xv[h] = lds4(xs + c * LD + r * kRound + 64 * kb + 16 * g + 4 * h);
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {  // 4 sub-steps at a time: dequantise, then interleave
-            float av[4][4];
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-              const float scl = sr[d][kb][nt];
-              const uint32_t dw = wr[d][kb][nt][h] ^ 0x80808080u;  // int8 -> u = q + 128
-#pragma unroll
-              for (int j = 0; j < 4; ++j) av[nt][j] = dq_byte(dw, j, scl, -128.0f * scl);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-              for (int nt = 0; nt < 4; ++nt)
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[nt][j], xv[h][j], acc[nt], 0, 0, 0);
-          }
+        for (int s = 0; s < 2; ++s) {
+          bh[s] = *(const h8*)&xs[0][c * kNLd + kl + 8 * s];
+          bl[s] = *(const h8*)&xs[1][c * kNLd + kl + 8 * s];
         }
-        if (r + kNDepth < kNKmax / kRound) {
-          load_round(r + kNDepth, wr[d], sr[d]);
-          asm volatile("" ::: "memory");  // keep the prefetch here (not sunk to its use)
+        f4 tb[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const q35_u32x4 wv = wr[d][kb][nt] ^ 0x80808080u;  // int8 -> u = q + 128
+          const h8 a0 = a8_from(wv[0], wv[1]), a1 = a8_from(wv[2], wv[3]);
+          f4 t = f4{0.f, 0.f, 0.f, 0.f};
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh[0], t, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh[1], t, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bl[0], t, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl[1], t, 0, 0, 0);
+          tb[nt] = t;
         }
+        // rows n = nbase + 16 nt + 4 g + i of this 64-k block scale by s[n][kb]
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt] += tb[nt] * sr[d][kb][nt];
+      }
+      if (r + kNDepth < kNKmax / kRound) {
+        load_round(r + kNDepth, wr[d], sr[d]);
+        asm volatile("" ::: "memory");  // keep the prefetch here (not sunk to its use)
+      }
     }
   });
   // lane holds rows n = nbase + 16 nt + 4 g + i of column m = c
   if (c < a.M) {
+    const float inv = a.invf[c];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = nbase + 16 * nt + 4 * g + i;
-        if (n < a.V) a.y[(size_t)c * a.ldy + n] = acc[nt][i];
+        if (n < a.V) a.y[(size_t)c * a.ldy + n] = acc[nt][i] * inv;
       }
+  }
+}
+
+// Final RMSNorm of the residual rows (text_modules.rs:800-808) with the lm_head input split:
+// y = x * rsqrt(mean(x^2) + eps) * (1 + w), then hi / lo f16 planes of y * 2^e and 2^-e per row.
+__global__ __launch_bounds__(kT) void rms_rows_split_kernel(const float* x, int ldx, int K, const float* w, float eps,
+                                                            _Float16* yh, _Float16* yl, int ld16, float* invf) {
+  __shared__ float sh[4];
+  const int m = blockIdx.x;
+  const float* xr = x + (size_t)m * ldx;
+  float v[kNKmax / kT];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNKmax / kT; ++j) {
+    const int k = threadIdx.x + kT * j;
+    v[j] = k < K ? xr[k] : 0.f;
+    ss += v[j] * v[j];
+  }
+  ss = block_sum256(ss, sh);
+  const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNKmax / kT; ++j) {
+    const int k = threadIdx.x + kT * j;
+    v[j] = k < K ? (v[j] * r) * (1.0f + w[k]) : 0.f;
+    amax = fmaxf(amax, fabsf(v[j]));
+  }
+  __syncthreads();
+  // block max (wave max by xor shuffles, then across the 4 waves)
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+  float f, inv;
+  split_scale(amax, f, inv);
+  if (threadIdx.x == 0) invf[m] = inv;
+#pragma unroll
+  for (int j = 0; j < kNKmax / kT; ++j) {
+    const int k = threadIdx.x + kT * j;
+    if (k < K) {
+      const float y = v[j] * f;
+      const _Float16 h = (_Float16)y;
+      yh[(size_t)m * ld16 + k] = h;
+      yl[(size_t)m * ld16 + k] = (_Float16)(y - (float)h);
+    }
   }
 }
 
@@ -455,28 +577,31 @@ __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
 // Tile-major projection layout (q[t][K][256], scale[t][K][4], the last tile padded to 256
 // columns) -> MB layout (see the top).
 __global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int N, int8_t* qb, float* sb) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 16-byte lane record
-  const size_t nrec = (size_t)K * N / 16;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-byte lane record
+  const size_t nrec = (size_t)K * N / 32;
   if (i < nrec) {
     const int lane = (int)(i & 63);
-    const size_t blk = i >> 6;  // cb * (K/16) + ks
-    const int nks = K >> 4;
+    const size_t blk = i >> 6;  // cb * (K/32) + ks
+    const int nks = K >> 5;
     const int cb = (int)(blk / nks), ks = (int)(blk % nks);
     const int g = lane >> 4, c = lane & 15;
     const int t = cb >> 2, cw = (cb & 3) * 64;
-    uint32_t dw[4];
+    uint32_t dw[8];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      uint32_t v = 0;
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = 16 * ks + 4 * g + j;
-        const uint8_t b = (uint8_t)qt[((size_t)t * K + k) * 256 + cw + 16 * nt + c] ^ 0x80u;  // u = q + 128
-        v |= (uint32_t)b << (8 * j);
+      for (int h = 0; h < 2; ++h) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = 32 * ks + 8 * g + 4 * h + j;
+          const uint8_t b = (uint8_t)qt[((size_t)t * K + k) * 256 + cw + 16 * nt + c] ^ 0x80u;  // u = q + 128
+          v |= (uint32_t)b << (8 * j);
+        }
+        dw[2 * nt + h] = v;
       }
-      dw[nt] = v;
-    }
-    *(uint4*)(qb + i * 16) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    *(uint4*)(qb + i * 32) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    *(uint4*)(qb + i * 32 + 16) = make_uint4(dw[4], dw[5], dw[6], dw[7]);
   }
   const size_t ns = (size_t)K * (N / 64);
   if (i < ns) {  // scale[cb][k] = st[t][k][cb % 4]
@@ -485,15 +610,32 @@ __global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int 
   }
 }
 
+// sT[kb][n] = s[n][kb] (the lm_head scales by 64-k block)
+__global__ void scale_transpose_kernel(const float* s, int V, int nkb, float* sT) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (size_t)V * nkb) {
+    const int kb = (int)(i / V), n = (int)(i % V);
+    sT[i] = s[(size_t)n * nkb + kb];
+  }
+}
+
 }  // namespace
 
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
                       hipStream_t st) {
   if (!q_tiled || !s_tiled || !q_mb || !s_mb) return fail(Q35_E_ARG, "mb_convert: null pointer");
-  if (K < 16 || K % 16 || N < 64 || N % 64) return fail(Q35_E_SHAPE, "mb_convert: need K % 16 == 0, N % 64 == 0");
-  const size_t n = std::max((size_t)K * N / 16, (size_t)K * (N / 64));
+  if (K < 32 || K % 32 || N < 64 || N % 64) return fail(Q35_E_SHAPE, "mb_convert: need K % 32 == 0, N % 64 == 0");
+  const size_t n = std::max((size_t)K * N / 32, (size_t)K * (N / 64));
   hipLaunchKernelGGL(mb_convert_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q_tiled, s_tiled, K, N,
                      q_mb, s_mb);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+int mb_scale_transpose_launch(const float* s, int32_t V, int32_t K, float* sT, hipStream_t st) {
+  if (!s || !sT || V < 4 || K < 64 || K % 64) return fail(Q35_E_ARG, "mb_scale_transpose: bad arguments");
+  const size_t n = (size_t)V * (K / 64);
+  hipLaunchKernelGGL(scale_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, V, K / 64, sT);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
@@ -568,17 +710,22 @@ int mb_launch(const MbCall& c, hipStream_t st) {
   return Q35_OK;
 }
 
-int mb_lm_head_launch(const int8_t* q, const float* s, int32_t V, int32_t K, const float* x, int32_t ldx, int32_t M,
-                      float* y, int32_t ldy, hipStream_t st) {
-  if (!q || !s || !x || !y) return fail(Q35_E_ARG, "mb_lm_head: null pointer");
+int mb_lm_head_launch(const int8_t* q, const float* sT, int32_t V, int32_t K, const float* h, int32_t ldh,
+                      const float* norm_w, float eps, int32_t M, _Float16* split16, float* invf, float* y, int32_t ldy,
+                      hipStream_t st) {
+  if (!q || !sT || !h || !norm_w || !split16 || !invf || !y) return fail(Q35_E_ARG, "mb_lm_head: null pointer");
   if (M < 1 || M > 32) return fail(Q35_E_SHAPE, "mb_lm_head: M in [1, 32]");
-  if (K < 256 || K % 256 || K > kNKmax || V < 1)
-    return fail(Q35_E_SHAPE, "mb_lm_head: K must be a multiple of 256, at most 2048");
-  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3))
-    return fail(Q35_E_ALIGN, "mb_lm_head: 16-byte aligned table and rows");
+  if (K < 512 || K % 512 || K > kNKmax || V < 4 || V % 4)
+    return fail(Q35_E_SHAPE, "mb_lm_head: K must be a multiple of 512, at most 2048, and V of 4");
+  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(split16) & 15))
+    return fail(Q35_E_ALIGN, "mb_lm_head: 16-byte aligned table and split rows");
+  _Float16* yh = split16;
+  _Float16* yl = split16 + (size_t)M * K;
+  hipLaunchKernelGGL(rms_rows_split_kernel, dim3(M), dim3(kT), 0, st, h, ldh, K, norm_w, eps, yh, yl, K, invf);
   const dim3 grid((unsigned)((V + 255) / 256));
   for (int m0 = 0; m0 < M; m0 += 16) {  // 16 rows per pass over the table
-    MbnArgs a{q, s, V, K, std::min(16, M - m0), x + (size_t)m0 * ldx, ldx, y + (size_t)m0 * ldy, ldy};
+    MbnArgs a{q, sT, V, K, std::min(16, M - m0), yh + (size_t)m0 * K, yl + (size_t)m0 * K, K, invf + m0,
+              y + (size_t)m0 * ldy, ldy};
     hipLaunchKernelGGL(mbn_kernel, grid, dim3(kT), 0, st, a);
   }
   Q35_HIP_TRY(hipGetLastError());

@@ -531,9 +531,14 @@ size_t mb_part_floats(int ncb, int K, int M);
 // Tile-major projection weights (q[t][K][256], scale[t][K][4]) -> MB layout.
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
                       hipStream_t st);
-// logits[m][n] = x[m] . dequant(E[n]) over the tied NK table, M <= 32 rows, x already normalised
-int mb_lm_head_launch(const int8_t* q, const float* s, int32_t V, int32_t K, const float* x, int32_t ldx, int32_t M,
-                      float* y, int32_t ldy, hipStream_t st);
+// logits[m][n] = RMSNorm(h[m]) . dequant(E[n]) over the tied NK table (scales transposed,
+// sT[K/64][V]), M <= 32 rows, K a multiple of 512 up to 2048; split16 holds 2 * M * K halves and
+// invf M floats of scratch.
+int mb_lm_head_launch(const int8_t* q, const float* sT, int32_t V, int32_t K, const float* h, int32_t ldh,
+                      const float* norm_w, float eps, int32_t M, _Float16* split16, float* invf, float* y, int32_t ldy,
+                      hipStream_t st);
+// sT[kb][n] = s[n][kb] for the lm_head's scale table s[V][K/64].
+int mb_scale_transpose_launch(const float* s, int32_t V, int32_t K, float* sT, hipStream_t st);
 
 // ------------------------------------------------------------------ prompt (seq_len > 1) path
 // *p = v on the stream (a kernel, so it can sit in a captured graph)
