@@ -125,8 +125,11 @@ struct XBuf {
 //   SPLIT = false: x~ is written as f32 rows (xs, [Mp][LD]).
 //   SPLIT = true: y = x~ * scale of the column block, split into hi / lo planes (xs: hi
 //   [Mp][LDH] then lo), with the row's inverse power of two in invf[row].
-template <int MT, bool SPLIT>
-Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs, const float* scl, float* invf) {
+// `issue` runs right after the staging loads are issued: the caller's weight prefetch goes
+// behind them, so the staging arithmetic waits only for its own loads (loads return in order).
+template <int MT, bool SPLIT, typename Issue>
+Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs, const float* scl, float* pws,
+                     float* invf, Issue&& issue) {
   using X = XBuf<MT>;
   const int t = threadIdx.x, mr = t / X::TPR, m = min(mr, a.M - 1), c0 = (t % X::TPR) * X::VPT;
   const int nch = klen / kRound;
@@ -134,9 +137,13 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
   const float* xr = a.x + (size_t)m * a.ldx + k0 + c0;
   const float* ur = gated ? a.z + (size_t)m * a.ldz + k0 + c0 : xr + a.swiglu_off;
   float v[X::NCH][X::VPT], u[X::NCH][X::VPT];
-  float wg[X::VPT];  // gated norm weights (the same VPT for every chunk); RMS weights go to u
-  f4 sc = f4{0.f, 0.f, 0.f, 0.f};
-  if (SPLIT && 4 * t < klen) sc = ld4(scl + k0 + 4 * t);
+  float wg[X::VPT];  // gated norm weights (the same VPT for every chunk)
+  // the block's scales and (RMS) norm weights go to LDS once (SPLIT), one 16-byte piece a thread
+  f4 sc = f4{0.f, 0.f, 0.f, 0.f}, pw4 = f4{0.f, 0.f, 0.f, 0.f};
+  if (SPLIT && 4 * t < klen) {
+    sc = ld4(scl + k0 + 4 * t);
+    if (rms) pw4 = ld4(a.pw + k0 + 4 * t);
+  }
   const fx_t ssv = ldg(a.ss + m);  // (a valid dummy address without RMS: no branch, so the wait
                                    // for it lands after the x loads below are issued)
   if (gated) {
@@ -153,22 +160,27 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
     for (int i = 0; i < X::VPT; i += 4) {
       const f4 q = ld4(xr + cc + i);
       v[ci][i] = q[0]; v[ci][i + 1] = q[1]; v[ci][i + 2] = q[2]; v[ci][i + 3] = q[3];
-      if (two || rms) {
+      if (two || (rms && !SPLIT)) {
         const f4 w = ld4(rms ? a.pw + k0 + cc + c0 + i : ur + cc + i);
         u[ci][i] = w[0]; u[ci][i + 1] = w[1]; u[ci][i + 2] = w[2]; u[ci][i + 3] = w[3];
       }
     }
   }
-  if (SPLIT && 4 * t < klen) *(f4*)(scs + 4 * t) = sc;
+  issue();
+  asm volatile("" ::: "memory");
+  if (SPLIT && 4 * t < klen) {
+    *(f4*)(scs + 4 * t) = sc;
+    if (rms) *(f4*)(pws + 4 * t) = pw4;
+  }
   // y = x * rsqrt(mean(x^2) + eps) * (1 + w)  (text_modules.rs:800-808); the row's sum of
-  // squares comes from the projection that produced x
+  // squares comes from the projection that produced x; with SPLIT, (1 + w) is applied below
   const float r = rsqrt_f(from_fx(ssv) * rcp_f((float)a.K) + a.eps);
   const int tpg = gated ? a.group / X::VPT : 1;  // gated: threads per group (power of two <= TPR)
 #pragma unroll
   for (int ci = 0; ci < X::NCH; ++ci) {
     if (rms) {
 #pragma unroll
-      for (int i = 0; i < X::VPT; ++i) v[ci][i] = (v[ci][i] * r) * (1.0f + u[ci][i]);
+      for (int i = 0; i < X::VPT; ++i) v[ci][i] = SPLIT ? v[ci][i] * r : (v[ci][i] * r) * (1.0f + u[ci][i]);
     } else if (gated) {
       // RMSNormGated (text_modules.rs:91-100): per group of `group` values of the row,
       // w * (x * rsqrt(mean(x^2) + eps)) * silu(z); the group's threads are consecutive lanes
@@ -202,9 +214,12 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
   for (int ci = 0; ci < X::NCH; ++ci) {
 #pragma unroll
     for (int i = 0; i < X::VPT; i += 4) {
-      const f4 s4 = lds4(scs + min(ci, nch - 1) * kRound + c0 + i);
+      const int kk = min(ci, nch - 1) * kRound + c0 + i;
+      const f4 s4 = lds4(scs + kk);
+      const f4 w4 = rms ? lds4(pws + kk) : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        if (rms) v[ci][i + j] = v[ci][i + j] * (1.0f + w4[j]);
         v[ci][i + j] *= s4[j];
         amax = fmaxf(amax, fabsf(v[ci][i + j]));
       }
@@ -246,7 +261,7 @@ template <int MT>
 Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
   using X = XBuf<MT>;
   const int t = threadIdx.x, kc = ab * kRound;
-  stage_x<MT, false>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr);
+  stage_x<MT, false>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr, nullptr, [] {});
   __syncthreads();
   const float* xs = reinterpret_cast<const float*>(xbuf);
   const int nh = a.aux_nh, no = 2 * nh;  // no <= 32
@@ -276,11 +291,12 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
 }
 
 template <int MT>
-__global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
+__global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   using X = XBuf<MT>;
   constexpr int Mp = X::Mp;
   __shared__ __align__(16) char xbuf[X::BYTES];  // staged x~ (f32 or hi / lo); then the reduction
   __shared__ __align__(16) float scs[X::KR];
+  __shared__ __align__(16) float pws[X::KR];
   __shared__ __align__(16) float aux_red[256];
   __shared__ float invf[Mp];
   __shared__ float sq[4][Mp];
@@ -312,8 +328,8 @@ __global__ __launch_bounds__(kT, 1) void mbk_kernel(const MbkArgs a) {
     w[0] = ldg16v_nt(src);
     w[1] = ldg16v_nt(src + 16);
   };
-  static_for<kDepth>([&](auto d) { load_round(d, wr[d]); });
-  stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, invf);
+  stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, pws, invf,
+                    [&] { static_for<kDepth>([&](auto d) { load_round(d, wr[d]); }); });
   __syncthreads();
 
   const _Float16* xh = reinterpret_cast<const _Float16*>(xbuf);
