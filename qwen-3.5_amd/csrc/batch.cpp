@@ -124,14 +124,14 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       float* pr = bt->proj + (size_t)r0 * ldq;
       if (!L.full) {
         c.nseg = 2;
-        c.seg[0] = MbSeg{W.qkv.q, W.qkv.s, pr, conv_dim, ldq};
-        c.seg[1] = MbSeg{W.z.q, W.z.s, pr + conv_dim, vdim, ldq};
+        c.seg[0] = MbSeg{W.qkv.q, W.qkv.s, pr, conv_dim, ldq, W.qkv.f};
+        c.seg[1] = MbSeg{W.z.q, W.z.s, pr + conv_dim, vdim, ldq, W.z.f};
         c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = gates + (size_t)r0 * kGateLd; c.aux_ldo = kGateLd;
       } else {
         c.nseg = 3;
-        c.seg[0] = MbSeg{W.q.q, W.q.s, pr, ldqg, ldq};
-        c.seg[1] = MbSeg{W.k.q, W.k.s, pr + ldqg, kvw, ldq};
-        c.seg[2] = MbSeg{W.v.q, W.v.s, pr + ldqg + kvw, kvw, ldq};
+        c.seg[0] = MbSeg{W.q.q, W.q.s, pr, ldqg, ldq, W.q.f};
+        c.seg[1] = MbSeg{W.k.q, W.k.s, pr + ldqg, kvw, ldq, W.k.f};
+        c.seg[2] = MbSeg{W.v.q, W.v.s, pr + ldqg + kvw, kvw, ldq, W.v.f};
       }
       if ((rc = mb_launch(c, st))) return rc;
     }
@@ -173,8 +173,8 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       c.K = H; c.x = bt->h + (size_t)r0 * H; c.ldx = H; c.pro = MB_PRO_RMS; c.pw = L.post_norm; c.ss = ss_mid + r0;
       float* gu = bt->gu + (size_t)r0 * 2 * F;
       c.nseg = 2;
-      c.seg[0] = MbSeg{W.gate.q, W.gate.s, gu, F, 2 * F};
-      c.seg[1] = MbSeg{W.up.q, W.up.s, gu + F, F, 2 * F};
+      c.seg[0] = MbSeg{W.gate.q, W.gate.s, gu, F, 2 * F, W.gate.f};
+      c.seg[1] = MbSeg{W.up.q, W.up.s, gu + F, F, 2 * F, W.up.f};
       if ((rc = mb_launch(c, st))) return rc;
     }
     for (int r0 = 0; r0 < B; r0 += kRowGroup) {
@@ -232,28 +232,37 @@ int ensure_mb(q35_model* m, hipStream_t st) {
   if (!m->mb.empty()) return Q35_OK;
   std::vector<q35_model::MbLayer> mb(m->layers.size());
   int rc;
-  auto conv = [&](const q35_model::Q8& w, const std::string& name, q35_model::Mb& out) -> int {
+  // norm_w: the RMSNorm weights of the projection's prologue (its input is normalised in the
+  // launch), for the direct path's split factors
+  auto conv = [&](const q35_model::Q8& w, const std::string& name, q35_model::Mb& out,
+                  const float* norm_w = nullptr) -> int {
     if (!w.q) return Q35_OK;
     int8_t* q = nullptr;
     float* s = nullptr;
+    float* f = nullptr;
     int r;
     if ((r = dev_alloc_t(m, "mb." + name, (size_t)w.rows * w.cols, &q)) ||
         (r = dev_alloc_t(m, "mb." + name + ".scale", (size_t)w.rows * (w.cols / 64), &s)) ||
         (r = mb_convert_launch(w.q, w.s, w.rows, w.cols, q, s, st)))
       return r;
+    if (norm_w && ((r = dev_alloc_t(m, "mb." + name + ".split", (size_t)(w.cols / 64), &f)) ||
+                   (r = mb_split_factor_launch(s, w.rows, w.cols, norm_w, f, st))))
+      return r;
     out.q = q;
     out.s = s;
+    out.f = f;
     return Q35_OK;
   };
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const q35_model::Layer& L = m->layers[l];
     const std::string p = "layers." + std::to_string(l) + ".";
     q35_model::MbLayer& o = mb[l];
-    if ((rc = conv(L.qkv, p + "in_proj_qkv", o.qkv)) || (rc = conv(L.z, p + "in_proj_z", o.z)) ||
-        (rc = conv(L.out, p + "out_proj", o.out)) || (rc = conv(L.q, p + "q_proj", o.q)) ||
-        (rc = conv(L.k, p + "k_proj", o.k)) || (rc = conv(L.v, p + "v_proj", o.v)) || (rc = conv(L.o, p + "o_proj", o.o)) ||
-        (rc = conv(L.gate, p + "gate_proj", o.gate)) || (rc = conv(L.up, p + "up_proj", o.up)) ||
-        (rc = conv(L.down, p + "down_proj", o.down)))
+    const float *nin = L.in_norm, *npost = L.post_norm;
+    if ((rc = conv(L.qkv, p + "in_proj_qkv", o.qkv, nin)) || (rc = conv(L.z, p + "in_proj_z", o.z, nin)) ||
+        (rc = conv(L.out, p + "out_proj", o.out)) || (rc = conv(L.q, p + "q_proj", o.q, nin)) ||
+        (rc = conv(L.k, p + "k_proj", o.k, nin)) || (rc = conv(L.v, p + "v_proj", o.v, nin)) ||
+        (rc = conv(L.o, p + "o_proj", o.o)) || (rc = conv(L.gate, p + "gate_proj", o.gate, npost)) ||
+        (rc = conv(L.up, p + "up_proj", o.up, npost)) || (rc = conv(L.down, p + "down_proj", o.down)))
       return rc;
   }
   float* sT = nullptr;

@@ -48,6 +48,8 @@ constexpr int kDepth = 4;          // rounds of weights in flight per wave (mbk)
 constexpr int kNDepth = 2;         // rounds in flight per wave (mbn)
 constexpr int kNKmax = 2048;       // lm_head: largest hidden size (the whole x rows sit in LDS)
 constexpr int kNLd = kNKmax + 8;   // lm_head: padded LDS row of one plane (halves)
+constexpr int kAuxLd = kRound + 4; // f32 staging row of the gate side blocks (one 128-row chunk)
+constexpr int kDirectKR = 1024;    // rows of K per block on the RMS direct path
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -57,6 +59,7 @@ struct MbkSeg {
   const int8_t* q;  // MB layout
   const float* s;   // [N/64][K]
   float* y;
+  const float* f;   // [N/64] split factors of the RMS direct path
   int32_t N, ldy, cb0;  // cb0: first column block of the segment in the launch
 };
 struct MbkArgs {
@@ -110,19 +113,22 @@ template <int MT>
 struct XBuf {
   static constexpr int Mp = 16 * MT;
   static constexpr int KR = 1024 / MT;         // rows of K per block
-  static constexpr int LD = KR + 4;            // floats per staged f32 row
   static constexpr int LDH = KR + 8;           // halves per row of one f16 plane
   static constexpr int NCH = KR / kRound;      // 128-row chunks
   static constexpr int TPR = kT / Mp;          // staging threads per x row: 16 or 8
   static constexpr int VPT = kRound / TPR;     // values per thread per chunk: 8 or 16
-  static constexpr int BYTES = (Mp * LD * 4 > 2 * Mp * LDH * 2) ? Mp * LD * 4 : 2 * Mp * LDH * 2;
+  static constexpr int AUX = Mp * kAuxLd * 4;  // f32 staging of one chunk (gate side blocks)
+  static constexpr int RED = 4 * 16 * MT * 64 * 4;  // the 4 waves' accumulators
+  static constexpr int PLANES = 2 * Mp * LDH * 2;
+  static constexpr int BYTES = PLANES > AUX ? (PLANES > RED ? PLANES : RED) : (AUX > RED ? AUX : RED);
+  static constexpr int DBYTES = AUX > RED ? AUX : RED;  // direct path: no planes
 };
 
 // Stage x~ for rows [k0, k0 + klen) (klen a multiple of 128, <= KR): every load the range needs
 // (x, the second operand, the norm weights, the row statistic) is issued first, so staging costs
 // one round trip.  Thread t covers row t / TPR of every chunk, columns (t % TPR) * VPT .. + VPT;
 // the rows of the chunk past M repeat row M - 1 (their outputs are never stored).
-//   SPLIT = false: x~ is written as f32 rows (xs, [Mp][LD]).
+//   SPLIT = false (klen = 128): x~ is written as f32 rows (xs, [Mp][kAuxLd]).
 //   SPLIT = true: y = x~ * scale of the column block, split into hi / lo planes (xs: hi
 //   [Mp][LDH] then lo), with the row's inverse power of two in invf[row].
 // `issue` runs right after the staging loads are issued: the caller's weight prefetch goes
@@ -202,7 +208,7 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
 #pragma unroll
     for (int ci = 0; ci < X::NCH; ++ci)
       if (ci < nch) {
-        float* dst = xs + mr * X::LD + ci * kRound + c0;
+        float* dst = xs + mr * kAuxLd + ci * kRound + c0;
 #pragma unroll
         for (int i = 0; i < X::VPT; i += 4) *(f4*)(dst + i) = f4{v[ci][i], v[ci][i + 1], v[ci][i + 2], v[ci][i + 3]};
       }
@@ -259,7 +265,6 @@ Q35_DEV MbkSeg seg_of(const MbkArgs& a, int cb) {
 // aux_acc (fixed point); the DeltaNet step applies the gates' activations.
 template <int MT>
 Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
-  using X = XBuf<MT>;
   const int t = threadIdx.x, kc = ab * kRound;
   stage_x<MT, false>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr, nullptr, [] {});
   __syncthreads();
@@ -277,7 +282,7 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
   for (int m = 0; m < a.M; ++m) {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc += xs[m * X::LD + rg * 16 + i] * w[i];
+    for (int i = 0; i < 16; ++i) acc += xs[m * kAuxLd + rg * 16 + i] * w[i];
     red[rg * 32 + o] = acc;
     __syncthreads();
     if (t < no) {
@@ -290,18 +295,25 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
   }
 }
 
-template <int MT>
+// DIRECT (RMSNorm prologue only): no staging.  Each lane forms its own B operands round by round
+// from x, the norm weights and the scales it loads with the round's weights, y = ((x * r) * (1 +
+// w)) * s, split with the column block's factor f = 2^e (a power of two fixed per column block:
+// |x * r| <= sqrt(K) for an RMS-normalised row, so sqrt(K) * max|1 + w| * max|s| bounds every |y|
+// of the block and f puts that bound in [2^13, 2^14)).  The bound is loose for most rows, which
+// costs nothing: hi / lo keep about 22 bits of each y down to 2^-17 of the bound.
+template <int MT, bool DIRECT>
 __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   using X = XBuf<MT>;
   constexpr int Mp = X::Mp;
-  __shared__ __align__(16) char xbuf[X::BYTES];  // staged x~ (f32 or hi / lo); then the reduction
-  __shared__ __align__(16) float scs[X::KR];
-  __shared__ __align__(16) float pws[X::KR];
+  constexpr int NCH = DIRECT ? kDirectKR / kRound : X::NCH;  // rounds per block at most
+  // staged x~ (f32 or hi / lo planes); then the reduction
+  __shared__ __align__(16) char xbuf[DIRECT ? X::DBYTES : X::BYTES];
+  __shared__ __align__(16) float scs[DIRECT ? 4 : X::KR];
+  __shared__ __align__(16) float pws[DIRECT ? 4 : X::KR];
   __shared__ __align__(16) float aux_red[256];
   __shared__ float invf[Mp];
   __shared__ float sq[4][Mp];
   __shared__ int last_flag;
-  static_assert(4 * 16 * MT * 64 * 4 <= X::BYTES, "reduction buffer");
 
   const int nmain = a.ncb * a.nsplit;
   if ((int)blockIdx.x >= nmain) {
@@ -318,19 +330,54 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   // wave p's 32-row step in round r: 4 r + p, relative to k0
   const int8_t* wq = sg.q + ((size_t)lcb * nks + (k0 >> 5) + p) * 2048 + lane * 32;
 
-  // Rounds past the block's range load 32 bytes per lane of its (cached) scales instead, so every
-  // round issues the same loads and the compiler's waits count them exactly.
+  // Rounds past the block's range load 32 bytes per lane of its (cached) scale row instead (inside
+  // the row: K >= 128), so every round issues the same loads and the compiler's waits count them
+  // exactly.
   const float* scl = sg.s + (size_t)lcb * a.K;
-  const int8_t* dummy = reinterpret_cast<const int8_t*>(scl) + lane * 32;
+  const int8_t* dummy = reinterpret_cast<const int8_t*>(scl + min(lane * 8, a.K - 8));
   q35_u32x4 wr[kDepth][2];
-  auto load_round = [&](int r, q35_u32x4 (&w)[2]) {
+  // direct path: the round's scales, norm weights and x rows (8 consecutive k of the lane's slot)
+  f4 sr[DIRECT ? kDepth : 1][2], pr[DIRECT ? kDepth : 1][2], xr[DIRECT ? kDepth : 1][MT][2];
+  const float* xrow[MT];
+  float rrow[MT];
+  const int kl0 = k0 + 32 * p + 8 * g;  // the lane's first k (round 0)
+  auto load_round = [&](int r, int d) {
     const int8_t* src = r < nround ? wq + (size_t)r * 4 * 2048 : dummy;
-    w[0] = ldg16v_nt(src);
-    w[1] = ldg16v_nt(src + 16);
+    wr[d][0] = ldg16v_nt(src);
+    wr[d][1] = ldg16v_nt(src + 16);
+    if constexpr (DIRECT) {  // rounds past the range reload the last one (cached)
+      const int kk = kl0 + min(r, nround - 1) * kRound;
+      sr[d][0] = ld4(scl + kk);
+      sr[d][1] = ld4(scl + kk + 4);
+      pr[d][0] = ld4(a.pw + kk);
+      pr[d][1] = ld4(a.pw + kk + 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xr[d][mt][0] = ld4(xrow[mt] + kk);
+        xr[d][mt][1] = ld4(xrow[mt] + kk + 4);
+      }
+    }
   };
-  stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, pws, invf,
-                    [&] { static_for<kDepth>([&](auto d) { load_round(d, wr[d]); }); });
-  __syncthreads();
+  float fcb = 1.f;
+  if constexpr (DIRECT) {
+    fx_t ssv[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = min(16 * mt + c, a.M - 1);  // rows past M repeat row M - 1 (never stored)
+      xrow[mt] = a.x + (size_t)m * a.ldx;
+      ssv[mt] = ldg(a.ss + m);
+    }
+    fcb = ldg(sg.f + lcb);
+    static_for<kDepth>([&](auto d) { load_round(d, d); });
+    // y = x * rsqrt(mean(x^2) + eps) * (1 + w)  (text_modules.rs:800-808); the row's sum of
+    // squares comes from the projection that produced x
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) rrow[mt] = rsqrt_f(from_fx(ssv[mt]) * rcp_f((float)a.K) + a.eps);
+  } else {
+    stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, pws, invf,
+                      [&] { static_for<kDepth>([&](auto d) { load_round(d, d); }); });
+    __syncthreads();
+  }
 
   const _Float16* xh = reinterpret_cast<const _Float16*>(xbuf);
   const _Float16* xl = xh + Mp * X::LDH;
@@ -340,17 +387,42 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // every round unrolled (at most KR / 128 of them), so the compiler's waits for the weight
-  // loads count exactly the rounds still in flight
-  static_for<X::NCH>([&](auto rc) {
+  // every round unrolled (at most NCH of them), so the compiler's waits for the weight loads
+  // count exactly the rounds still in flight
+  static_for<NCH>([&](auto rc) {
     constexpr int r = rc, d = r % kDepth;
     if (r < nround) {
       const int kl = r * kRound + 32 * p + 8 * g;
       h8 bh[MT], bl[MT];
+      if constexpr (DIRECT) {
+        float sf[8], wp[8];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        bh[mt] = *(const h8*)(xh + (16 * mt + c) * X::LDH + kl);
-        bl[mt] = *(const h8*)(xl + (16 * mt + c) * X::LDH + kl);
+        for (int j = 0; j < 4; ++j) {
+          sf[j] = sr[d][0][j] * fcb;  // exact: fcb is a power of two
+          sf[4 + j] = sr[d][1][j] * fcb;
+          wp[j] = 1.0f + pr[d][0][j];
+          wp[4 + j] = 1.0f + pr[d][1][j];
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float y[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            y[j] = ((xr[d][mt][0][j] * rrow[mt]) * wp[j]) * sf[j];
+            y[4 + j] = ((xr[d][mt][1][j] * rrow[mt]) * wp[4 + j]) * sf[4 + j];
+          }
+          uint32_t hi[4], lo[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) split2(y[2 * j], y[2 * j + 1], hi[j], lo[j]);
+          bh[mt] = __builtin_bit_cast(h8, q35_u32x4{hi[0], hi[1], hi[2], hi[3]});
+          bl[mt] = __builtin_bit_cast(h8, q35_u32x4{lo[0], lo[1], lo[2], lo[3]});
+        }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          bh[mt] = *(const h8*)(xh + (16 * mt + c) * X::LDH + kl);
+          bl[mt] = *(const h8*)(xl + (16 * mt + c) * X::LDH + kl);
+        }
       }
       const q35_u32x4 w0 = wr[d][0], w1 = wr[d][1];
       const h8 aw[4] = {a8_from(w0[0], w0[1]), a8_from(w0[2], w0[3]), a8_from(w1[0], w1[1]), a8_from(w1[2], w1[3])};
@@ -364,12 +436,22 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bl[mt], acc[nt][mt], 0, 0, 0);
-      if (r + kDepth < X::NCH) {
-        load_round(r + kDepth, wr[d]);
+      if (r + kDepth < NCH) {
+        load_round(r + kDepth, d);
         asm volatile("" ::: "memory");  // keep the prefetch here (not sunk to its use)
       }
     }
   });
+
+  // lane holds columns n = 16 p + 4 g + i (i = 0..3) of row m = 16 mt + c after the reduction;
+  // residual projections read those outputs' old values now (rows clamped), so the round trip
+  // overlaps the reduction and the split-K hand-off
+  const int ncol0 = 64 * lcb + 16 * p + 4 * g;
+  f4 yold[MT];
+  if (a.add) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) yold[mt] = ld4(sg.y + (size_t)min(16 * mt + c, a.M - 1) * sg.ldy + ncol0);
+  }
 
   // Sum the 4 waves' partial sums: wave p writes its accumulators, then finalises column tile
   // nt = p (16 columns x Mp rows) from all four in wave order; the row's 2^-e undoes the split's
@@ -388,10 +470,9 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
     f4 v = *(const f4*)&red[((0 * 4 + p) * MT + mt) * 256 + lane * 4];
 #pragma unroll
     for (int q = 1; q < 4; ++q) v += *(const f4*)&red[((q * 4 + p) * MT + mt) * 256 + lane * 4];
-    out[mt] = v * invf[16 * mt + c];
+    // the split's 2^e undone: per row (staged) or per column block (direct; 2^-e exactly)
+    out[mt] = v * (DIRECT ? __int_as_float((254 << 23) - __float_as_int(fcb)) : invf[16 * mt + c]);
   }
-  // lane holds columns n = 16 p + 4 g + i (i = 0..3) of row m = 16 mt + c
-  const int ncol0 = 64 * lcb + 16 * p + 4 * g;
   if (a.nsplit > 1) {
     float* pp = a.part + ((size_t)cb * a.nsplit + split) * Mp * 64;
 #pragma unroll
@@ -399,16 +480,28 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) st_agent(pp + (16 * mt + c) * 64 + 16 * p + 4 * g + i, out[mt][i]);
     if (!arrive_last(a.ctr + cb, (uint32_t)a.nsplit, &last_flag)) return;
-    // the last block of the column block sums the partials in split order
-    const float* pb = a.part + (size_t)cb * a.nsplit * Mp * 64;
+    // the last block of the column block sums the partials in split order, up to kSumU splits
+    // per round trip (all their loads issued before the first add; the partials bypass the
+    // caches, so no load is issued for splits that do not exist)
+    constexpr int kSumU = MT == 1 ? 16 : 8;
+    const float* pb = a.part + (size_t)cb * a.nsplit * Mp * 64 + 16 * p + 4 * g;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      f4 v = f4{0.f, 0.f, 0.f, 0.f};
-      for (int s2 = 0; s2 < a.nsplit; ++s2) {
-        const float* q = pb + (size_t)s2 * Mp * 64 + (16 * mt + c) * 64 + 16 * p + 4 * g;
-        v += f4{ld_agent(q), ld_agent(q + 1), ld_agent(q + 2), ld_agent(q + 3)};
-      }
-      out[mt] = v;
+    for (int mt = 0; mt < MT; ++mt) out[mt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.nsplit; s0 += kSumU) {
+      f4 pv[kSumU][MT];
+#pragma unroll
+      for (int u = 0; u < kSumU; ++u)
+        if (s0 + u < a.nsplit)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const float* q = pb + (size_t)(s0 + u) * Mp * 64 + (16 * mt + c) * 64;
+            pv[u][mt] = f4{ld_agent(q), ld_agent(q + 1), ld_agent(q + 2), ld_agent(q + 3)};
+          }
+#pragma unroll
+      for (int u = 0; u < kSumU; ++u)
+        if (s0 + u < a.nsplit)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) out[mt] += pv[u][mt];
     }
   }
   // write (or add) the outputs of rows m < M; residual adds also sum the new rows' squares
@@ -421,7 +514,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = out[mt][i];
-        if (a.add) v += yr[i];
+        if (a.add) v += yold[mt][i];
         yr[i] = v;
         sqs += v * v;
       }
@@ -656,10 +749,54 @@ int mb_scale_transpose_launch(const float* s, int32_t V, int32_t K, float* sT, h
   return Q35_OK;
 }
 
+namespace {
+
+// Split factors of the RMS direct path: f[cb] = 2^e with sqrt(K) * max|1 + w| * max_k |s[cb][k]|
+// * 2^e in [2^13, 2^14) (a bound on |y| of every row, see mbk_kernel).
+__global__ __launch_bounds__(kT) void mb_split_factor_kernel(const float* sb, int K, const float* w, float* f) {
+  __shared__ float sh[2][kT / 64];
+  const int cb = blockIdx.x, t = threadIdx.x;
+  float smax = 0.f, wmax = 0.f;
+  for (int k = t; k < K; k += kT) {
+    smax = fmaxf(smax, fabsf(sb[(size_t)cb * K + k]));
+    wmax = fmaxf(wmax, fabsf(1.0f + w[k]));
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    smax = fmaxf(smax, __shfl_xor(smax, o));
+    wmax = fmaxf(wmax, __shfl_xor(wmax, o));
+  }
+  if ((t & 63) == 0) {
+    sh[0][t >> 6] = smax;
+    sh[1][t >> 6] = wmax;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int i = 1; i < kT / 64; ++i) {
+      smax = fmaxf(smax, sh[0][i]);
+      wmax = fmaxf(wmax, sh[1][i]);
+    }
+    // (1 + 2^-10: room for the rounding of the row statistic and the products)
+    const float bound = sqrtf((float)K) * wmax * smax * (1.0f + 0x1p-10f);
+    float fv, inv;
+    split_scale(bound, fv, inv);
+    f[cb] = fv;
+  }
+}
+
+}  // namespace
+
+int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st) {
+  if (!s_mb || !norm_w || !f || K < 1 || N < 64 || N % 64) return fail(Q35_E_ARG, "mb_split_factor: bad arguments");
+  hipLaunchKernelGGL(mb_split_factor_kernel, dim3((unsigned)(N / 64)), dim3(kT), 0, st, s_mb, K, norm_w, f);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
 // Split-K plan for M rows: the fewest splits of whole 128-row rounds that give >= 160 blocks,
-// with at most 1024 / MT rows per block (its x rows sit in LDS).
-void mb_plan(int ncb, int K, int M, int* nsplit, int* kr) {
-  const int nr = K / kRound, rmax = (M <= 16 ? 1024 : 512) / kRound;
+// with at most 1024 / MT rows per block when its x rows are staged in LDS, kDirectKR on the
+// direct path.
+void mb_plan(int ncb, int K, int M, bool direct, int* nsplit, int* kr) {
+  const int nr = K / kRound, rmax = (direct ? kDirectKR : M <= 16 ? 1024 : 512) / kRound;
   int s = (nr + rmax - 1) / rmax;
   while (ncb * s < 160 && s < nr) ++s;
   const int rpb = (nr + s - 1) / s;
@@ -668,10 +805,14 @@ void mb_plan(int ncb, int K, int M, int* nsplit, int* kr) {
 }
 
 size_t mb_part_floats(int ncb, int K, int M) {
-  int s, kr;
-  mb_plan(ncb, K, M, &s, &kr);
-  const int Mp = M <= 16 ? 16 : 32;
-  return s > 1 ? (size_t)ncb * s * Mp * 64 : 0;
+  size_t n = 0;
+  for (const bool direct : {false, true}) {
+    int s, kr;
+    mb_plan(ncb, K, M, direct, &s, &kr);
+    const int Mp = M <= 16 ? 16 : 32;
+    n = std::max(n, s > 1 ? (size_t)ncb * s * Mp * 64 : (size_t)0);
+  }
+  return n;
 }
 
 int mb_launch(const MbCall& c, hipStream_t st) {
@@ -695,8 +836,10 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     const MbSeg& s = c.seg[i];
     if (!s.q || !s.s || !s.y) return fail(Q35_E_ARG, "mb_launch: null segment");
     if (s.N < 64 || s.N % 64) return fail(Q35_E_SHAPE, "mb_launch: segment N % 64");
+    if (c.add && ((reinterpret_cast<uintptr_t>(s.y) & 15) || (s.ldy & 3)))
+      return fail(Q35_E_ALIGN, "mb_launch: residual rows 16-byte aligned");
     if ((reinterpret_cast<uintptr_t>(s.q) & 15)) return fail(Q35_E_ALIGN, "mb_launch: weights 16-byte aligned");
-    a.seg[i] = MbkSeg{s.q, s.s, s.y, s.N, s.ldy, ncb};
+    a.seg[i] = MbkSeg{s.q, s.s, s.y, s.f, s.N, s.ldy, ncb};
     ncb += s.N / 64;
   }
   for (int i = c.nseg; i < kMbMaxSeg; ++i) {
@@ -704,7 +847,9 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     a.seg[i].cb0 = INT32_MAX;
   }
   a.ncb = ncb;
-  mb_plan(ncb, c.K, c.M, &a.nsplit, &a.kr);
+  bool direct = c.pro == MB_PRO_RMS;
+  for (int i = 0; i < c.nseg; ++i) direct = direct && c.seg[i].f;
+  mb_plan(ncb, c.K, c.M, direct, &a.nsplit, &a.kr);
   a.x = c.x; a.ldx = c.ldx; a.pro = c.pro; a.pw = c.pw; a.eps = c.eps;
   a.ss = c.pro == MB_PRO_RMS ? c.ss : reinterpret_cast<const fx_t*>(c.x);  // rows of x: >= 8 M bytes
   a.z = c.z; a.ldz = c.ldz; a.group = c.group; a.swiglu_off = c.swiglu_off;
@@ -720,8 +865,13 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     a.part = c.part; a.ctr = c.ctr;
   }
   const dim3 grid((unsigned)(ncb * a.nsplit + a.naux));
-  if (c.M <= 16) hipLaunchKernelGGL(mbk_kernel<1>, grid, dim3(kT), 0, st, a);
-  else hipLaunchKernelGGL(mbk_kernel<2>, grid, dim3(kT), 0, st, a);
+  if (c.M <= 16) {
+    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, true>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false>), grid, dim3(kT), 0, st, a);
+  } else {
+    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, true>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, false>), grid, dim3(kT), 0, st, a);
+  }
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

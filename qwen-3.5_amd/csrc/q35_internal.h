@@ -507,6 +507,9 @@ struct MbSeg {
   const float* s = nullptr;   // [N/64][K]
   float* y = nullptr;         // y[m*ldy + n]
   int32_t N = 0, ldy = 0;
+  // split factors [N/64] (mb_split_factor_launch, with the RMSNorm weights of the launch's
+  // prologue): with them on every segment an RMS launch takes the direct path (no staging)
+  const float* f = nullptr;
 };
 struct MbCall {
   MbSeg seg[kMbMaxSeg];
@@ -528,6 +531,8 @@ struct MbCall {
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
 size_t mb_part_floats(int ncb, int K, int M);
+// Split factors of an MB weight for RMS launches whose norm weights are norm_w.
+int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st);
 // Tile-major projection weights (q[t][K][256], scale[t][K][4]) -> MB layout.
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
                       hipStream_t st);
