@@ -56,15 +56,21 @@ enum {
  *           q[N/16][K][16], with the scales transposed to scale[N/64][K].  Same values and byte
  *           count; each panel (16 outputs over all of K) is one contiguous run, so the standalone
  *           matvec computes it in one block with no cross-block reduction and no workspace.
- *           Accepted by q35_q8_gemv / q35_q8_gemv_partial_sum only. */
-enum { Q35_KN = 0, Q35_NK = 1, Q35_KN_TILED = 2, Q35_KN_PANEL = 3 };
+ *           Accepted by q35_q8_gemv / q35_q8_gemv_partial_sum only.
+ *   Q35_KN_MB: the Q35_KN matrix re-laid out on the device by q35_q8f_pack_mb for the f16
+ *           matrix cores: per 64-column block cb and 32-row step ks a 2 KB record in which lane
+ *           l = 16 g + c of a 64-lane wave finds the bytes q + 128 of rows 32 ks + 8 g + j
+ *           (j < 8) of columns 64 cb + 16 t + c, t < 4 (its operands of four 16x16x32 MFMAs);
+ *           scales transposed to scale[N/64][K].  Same values and byte count.  Accepted by
+ *           q35_q8_gemm_ws only (K and N multiples of 128). */
+enum { Q35_KN = 0, Q35_NK = 1, Q35_KN_TILED = 2, Q35_KN_PANEL = 3, Q35_KN_MB = 4 };
 
 typedef struct {
   const int8_t* q;
   const float* scale;
   int32_t rows;
   int32_t cols;
-  int32_t layout; /* Q35_KN, Q35_NK or Q35_KN_TILED */
+  int32_t layout; /* Q35_KN, Q35_NK, Q35_KN_TILED, Q35_KN_PANEL or Q35_KN_MB */
 } q35_q8f;
 
 /* Shape constants of the decoder; mirrors the fields of TextConfig that the decode path
@@ -227,7 +233,12 @@ int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int
 /* The same with a workspace of q35_q8_gemm_ws_bytes(M, W) bytes: the launcher may then split K
  * over more blocks (for shapes with few output tiles, e.g. the 2048-wide out / o / down
  * projections) and add the splits' partial sums in a fixed order in a second kernel.  Results
- * differ from q35_q8_gemm only in f32 summation order.  ws = NULL behaves as q35_q8_gemm. */
+ * differ from q35_q8_gemm only in f32 summation order.  ws = NULL behaves as q35_q8_gemm.
+ * W in Q35_KN_MB (a workspace is then required) runs on the f16 matrix cores with f32-equivalent
+ * products: the int8 values are exact in f16, each block scale multiplies x instead, and x * scale
+ * is carried as two f16 halves hi + lo (~22 significant bits, with a power-of-two factor per row
+ * of x chosen from the row's largest |x| and the matrix's largest scale) whose products with q
+ * are exact in the f32 accumulator; results differ from the fp32 path by f32 rounding. */
 size_t q35_q8_gemm_ws_bytes(int32_t M, q35_q8f W);
 int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
                    void* ws, size_t ws_bytes, void* stream);
@@ -440,6 +451,10 @@ int64_t q35_q8f_tiled_scale_count(int32_t K, int32_t N);
 /* Host: re-lay a Q35_KN matrix (q [K][N], scale [K][N/64]) out as Q35_KN_TILED. */
 int q35_q8f_pack_kn_tiled(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_tiled_host,
                           float* scale_tiled_host);
+/* Device: re-lay a Q35_KN or Q35_KN_TILED matrix W (device memory) out as Q35_KN_MB into q_mb
+ * (K*N bytes) and scale_mb (K*N/64 floats), on `stream`.  K a multiple of 32, N of 64.  No
+ * reference counterpart (a load-time layout, as q35_q8f_pack_kn_tiled). */
+int q35_q8f_pack_mb(q35_q8f W, int8_t* q_mb, float* scale_mb, void* stream);
 /* Host: re-lay a Q35_KN matrix out as Q35_KN_PANEL (q [N/16][K][16], scale [N/64][K]; the same
  * K*N bytes and K*N/64 scales). */
 int q35_q8f_pack_kn_panel(const int8_t* q_host, const float* scale_host, int32_t K, int32_t N, int8_t* q_panel_host,

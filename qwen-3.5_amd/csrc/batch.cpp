@@ -442,7 +442,7 @@ int q35_batch_generate(q35_batch* b, const int32_t* prompts_host, const int32_t*
   int rc;
   if (gemm_prefill) {
     q35_model* m = b->m;
-    if ((rc = ensure_prefill(m))) return rc;
+    if ((rc = ensure_prefill(m, st))) return rc;
     for (int r = 0; r < B; ++r) {
       const SeqView v = row_view(b, r);
       for (int done = 0; done < lens_host[r];) {

@@ -416,6 +416,7 @@ int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const floa
 
 int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
                 void* stream) {
+  if (W.layout == Q35_KN_MB) return fail(Q35_E_WS, "q8_gemm: Q35_KN_MB needs q35_q8_gemm_ws with a workspace");
   int rc = check_q8f(W, "q8_gemm");
   if (rc) return rc;
   if (!x || !y) return fail(Q35_E_ARG, "q8_gemm: null pointer");
@@ -434,12 +435,30 @@ int q35_q8_gemm(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int
 size_t q35_q8_gemm_ws_bytes(int32_t M, q35_q8f W) {
   if (M < 1) return 0;
   const int N = W.layout == Q35_NK ? W.rows : W.cols;
-  return gemm_part_floats(M, N) * sizeof(float);
+  const size_t aux = W.layout == Q35_KN_MB ? gemm_aux_floats(M) : 0;
+  return (aux + gemm_part_floats(M, N)) * sizeof(float);
 }
 
 int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
                    void* ws, size_t ws_bytes, void* stream) {
   if (!ws) return q35_q8_gemm(x, M, ldx, W, y, ldy, accumulate, stream);
+  if (W.layout == Q35_KN_MB) {  // f16 matrix cores: workspace = row / scale maxima, then partials
+    if (!W.q || !W.scale || !x || !y) return fail(Q35_E_ARG, "q8_gemm_ws: null pointer");
+    const int K = W.rows, N = W.cols;
+    if (M < 1 || K < 64 || K % 64 || N < 128 || N % 128)
+      return fail(Q35_E_SHAPE, "q8_gemm_ws: Q35_KN_MB needs M >= 1, K a multiple of 64 and N of 128");
+    if (ldx < K || ldy < N) return fail(Q35_E_SHAPE, "q8_gemm_ws: ldx >= K and ldy >= N required");
+    if ((reinterpret_cast<uintptr_t>(ws) & 15) != 0) return fail(Q35_E_ALIGN, "q8_gemm_ws: workspace not 16-byte aligned");
+    const size_t aux = gemm_aux_floats(M);
+    if (ws_bytes < aux * sizeof(float)) return fail(Q35_E_WS, "q8_gemm_ws: workspace too small");
+    GemmCall c;
+    c.x = x; c.ldx = ldx; c.M = M; c.K = K; c.nseg = 1; c.accumulate = accumulate ? 1 : 0;
+    c.seg[0] = GemmSeg{W.q, W.scale, y, N, Q35_KN_MB, ldy};
+    c.aux = static_cast<float*>(ws);
+    c.part = c.aux + aux;
+    c.part_floats = ws_bytes / sizeof(float) - aux;
+    return gemm_launch(c, S(stream));
+  }
   int rc = check_q8f(W, "q8_gemm_ws");
   if (rc) return rc;
   if (!x || !y) return fail(Q35_E_ARG, "q8_gemm_ws: null pointer");
@@ -456,6 +475,14 @@ int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, 
   c.part = static_cast<float*>(ws);
   c.part_floats = ws_bytes / sizeof(float);
   return gemm_launch(c, S(stream));
+}
+
+int q35_q8f_pack_mb(q35_q8f W, int8_t* q_mb, float* scale_mb, void* stream) {
+  if (!W.q || !W.scale || !q_mb || !scale_mb) return fail(Q35_E_ARG, "q8f_pack_mb: null pointer");
+  if (W.layout != Q35_KN && W.layout != Q35_KN_TILED) return fail(Q35_E_ARG, "q8f_pack_mb: W must be Q35_KN or Q35_KN_TILED");
+  if (W.rows < 32 || W.rows % 32 || W.cols < 64 || W.cols % 64)
+    return fail(Q35_E_SHAPE, "q8f_pack_mb: K a multiple of 32 and N of 64 required");
+  return mb_convert_launch(W.q, W.scale, W.rows, W.cols, q_mb, scale_mb, S(stream), W.layout == Q35_KN_TILED ? 1 : 0);
 }
 
 int q35_gate_proj_prompt(const float* x, int32_t T, int32_t in_dim, const float* w_b, const float* w_a,

@@ -48,6 +48,8 @@ struct GArgs {
   int32_t ldx, M, K, mtiles, accumulate, nblocks;
   int32_t ksplit, kchunk, ncat;  // K splits of kchunk rows; partials part[split][M][ncat]
   float* part;
+  float* amax;   // MB path: |x| maximum of each row [M]
+  float* spart;  // MB path: partial maxima of every segment's |scale| [kPrepS]
 };
 
 // Logical tile of hardware block b: the blocks of one XCD (b % 8) get consecutive logical ids.
@@ -238,6 +240,201 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GArgs a) {
   y[0] = v.x; y[1] = v.y; y[2] = v.z; y[3] = v.w;
 }
 
+// ------------------------------------------------------------------ f16 matrix cores (Q35_KN_MB)
+// The same product on v_mfma_f32_16x16x32_f16 with f32-equivalent arithmetic.  The 8-bit weights
+// are exact in f16 (read straight from the MB records, the A operands of four MFMAs per lane);
+// the scale of a weight's 64-column block varies along k only, so it multiplies x instead:
+// y = x * 2^e * scale[cb][k] (f32, 2^e a power of two per row of x), carried as two f16 halves
+// hi + lo (~22 significant bits) whose products with q are exact in the f32 accumulator; the tile
+// is scaled back by 2^-e.  2^e is fixed for the whole launch from the row's largest |x| and the
+// weights' largest |scale|, so every |y| < 2^14 (f16 overflows at 65504).
+//
+// Block = 4 waves in a 2 x 2 grid over a BM x 128 tile; wave (wm, wn) owns rows wm*BM/2.. of
+// column block n0/64 + wn (4 column tiles of 16) and accumulates (BM/32) x 4 tiles of 16 x 16.
+// K advances 64 at a time (two MB steps): the next step's x tile (f32, scaled by 2^e while it is
+// written to LDS), weights and scales are loaded while the current step's MFMAs run.  Each lane
+// forms its own B operands (x row 16 i + c, 8 consecutive k) from LDS and the column block's
+// scales in registers.
+constexpr int kHBK = 64;          // K per main-loop step (two 32-row MB steps)
+constexpr int kXLd = kHBK + 4;    // padded f32 row of the staged x tile (rows 4 banks apart)
+constexpr int kPrepS = 64;        // blocks of the scale-maximum pass (one wave's lanes)
+
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+// Row maxima of |x| (blocks < nrb: one wave per row) and partial maxima of every segment's |scale|
+// (blocks nrb .. nrb + kPrepS - 1, a strided share each).
+__global__ __launch_bounds__(256) void hgemm_prep_kernel(const GArgs a, int nrb) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if ((int)blockIdx.x < nrb) {
+    const int m = (int)blockIdx.x * 4 + w;
+    if (m >= a.M) return;  // (this branch has no block barrier)
+    const float* xr = a.x + (int64_t)m * a.ldx;
+    float mx = 0.f;
+    for (int k = 4 * lane; k < a.K; k += 256) {
+      const float4 v = *(const float4*)(xr + k);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) a.amax[m] = mx;
+    return;
+  }
+  const int p = (int)blockIdx.x - nrb;
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < kGemmMaxSeg; ++i) {
+    if (i >= a.nseg) break;
+    const float* sc = a.seg[i].s;
+    const int64_t n = (int64_t)(a.seg[i].N >> 6) * a.K;
+    for (int64_t j = (int64_t)p * 256 + tid; j < n; j += (int64_t)kPrepS * 256) mx = fmaxf(mx, fabsf(sc[j]));
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  if (tid == 0) a.spart[p] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <int BM>
+__global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
+  constexpr int WM = BM / 2, MT = WM / 16;  // rows per wave, 16-row tiles per wave
+  constexpr int XV = BM / 16;               // x tile float4 per thread (16 threads per 64-float row)
+  __shared__ __align__(16) float Xs[2][BM * kXLd];
+  __shared__ float fsh[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  const int L = xcd_remap((int)blockIdx.x, a.nblocks);
+  const int gs = L / a.mtiles, mt = L - gs * a.mtiles;
+  const int gt = gs / a.ksplit, split = gs - gt * a.ksplit;
+  GSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < kGemmMaxSeg; ++i)
+    if (i < a.nseg && gt >= a.seg[i].tile0) sg = a.seg[i];
+  const int n0 = (gt - sg.tile0) * 128, m0 = mt * BM;
+  const int K = a.K, nks = K >> 5;
+  const int kbeg = split * a.kchunk, kend = min(K, kbeg + a.kchunk);
+  const int wm = w >> 1, wn = w & 1;
+  const int cb = (n0 >> 6) + wn;  // the wave's column block within its segment
+
+  // 2^e of each row: (row max |x|) x (max |scale|) x 2^e < 2^14, with room for rounding
+  {
+    float S = a.spart[lane];
+    for (int o = 32; o > 0; o >>= 1) S = fmaxf(S, __shfl_xor(S, o));
+    if (tid < BM) {
+      float f, inv;
+      split_scale(a.amax[min(m0 + tid, a.M - 1)] * S * (1.0f + 0x1p-10f), f, inv);
+      fsh[tid] = f;
+    }
+  }
+  __syncthreads();
+
+  // x tile: thread loads rows xr0 + 16 i (clamped to M - 1; zeroed when stored), floats xc..xc+3
+  const int xr0 = tid >> 4, xc = (tid & 15) * 4;
+  float fx[XV];
+  const float* xp[XV];
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int r = m0 + xr0 + 16 * i;
+    fx[i] = r < a.M ? fsh[xr0 + 16 * i] : 0.f;
+    xp[i] = a.x + (int64_t)min(r, a.M - 1) * a.ldx + xc;
+  }
+  mf4 xa[XV];
+  auto xload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) xa[i] = *(const Q35_GLOBAL mf4*)(xp[i] + k0);
+  };
+  auto xstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) *(mf4*)&Xs[buf][(xr0 + 16 * i) * kXLd + xc] = xa[i] * fx[i];
+  };
+  // weights: the lane's 32 bytes of each 32-row MB step of the wave's column block; scales
+  // scale[cb][k] of its 8 k
+  const int8_t* wq = sg.q + (int64_t)cb * nks * 2048 + lane * 32;
+  const float* sc = sg.s + (int64_t)cb * K + 8 * g;
+  q35_u32x4 wr[2][2];
+  mf4 sr[2][2];
+  auto wload = [&](int k0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ks = (k0 >> 5) + h;
+      wr[h][0] = *(const Q35_GLOBAL q35_u32x4*)(wq + (int64_t)ks * 2048);
+      wr[h][1] = *(const Q35_GLOBAL q35_u32x4*)(wq + (int64_t)ks * 2048 + 16);
+      sr[h][0] = *(const Q35_GLOBAL mf4*)(sc + 32 * ks);
+      sr[h][1] = *(const Q35_GLOBAL mf4*)(sc + 32 * ks + 4);
+    }
+  };
+
+  mf4 acc[4][MT];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[nt][i] = mf4{0.f, 0.f, 0.f, 0.f};
+
+  const int nsteps = (kend - kbeg) / kHBK;
+  xload(kbeg);
+  wload(kbeg);
+  xstore(0);
+  __syncthreads();
+  for (int kb = 0; kb < nsteps; ++kb) {
+    const int buf = kb & 1;
+    q35_u32x4 wc[2][2];
+    mf4 scur[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      wc[h][0] = wr[h][0]; wc[h][1] = wr[h][1];
+      scur[h][0] = sr[h][0]; scur[h][1] = sr[h][1];
+    }
+    if (kb + 1 < nsteps) {
+      xload(kbeg + (kb + 1) * kHBK);
+      wload(kbeg + (kb + 1) * kHBK);
+    }
+    const float* Xb = &Xs[buf][0];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const q35_h8 aw[4] = {a8_from(wc[h][0][0], wc[h][0][1]), a8_from(wc[h][0][2], wc[h][0][3]),
+                            a8_from(wc[h][1][0], wc[h][1][1]), a8_from(wc[h][1][2], wc[h][1][3])};
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const float* xr = Xb + (wm * WM + 16 * i + c) * kXLd + 32 * h + 8 * g;
+        const mf4 x0 = *(const mf4*)xr, x1 = *(const mf4*)(xr + 4);
+        uint32_t hi[4], lo[4];
+        split2(x0[0] * scur[h][0][0], x0[1] * scur[h][0][1], hi[0], lo[0]);
+        split2(x0[2] * scur[h][0][2], x0[3] * scur[h][0][3], hi[1], lo[1]);
+        split2(x1[0] * scur[h][1][0], x1[1] * scur[h][1][1], hi[2], lo[2]);
+        split2(x1[2] * scur[h][1][2], x1[3] * scur[h][1][3], hi[3], lo[3]);
+        const q35_h8 bh = __builtin_bit_cast(q35_h8, q35_u32x4{hi[0], hi[1], hi[2], hi[3]});
+        const q35_h8 bl = __builtin_bit_cast(q35_h8, q35_u32x4{lo[0], lo[1], lo[2], lo[3]});
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bh, acc[nt][i], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bl, acc[nt][i], 0, 0, 0);
+      }
+    }
+    if (kb + 1 < nsteps) xstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // lane holds D[n = 16 nt + 4 g + r][m = 16 i + c] of the wave's tile: 4 consecutive columns of
+  // one row per (nt, i)
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int rl = wm * WM + 16 * i + c, row = m0 + rl;
+    if (row >= a.M) continue;
+    const float inv = __int_as_float((254 << 23) - __float_as_int(fsh[rl]));  // 2^-e, exact
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = n0 + wn * 64 + 16 * nt + 4 * g;
+      mf4 v = acc[nt][i] * inv;
+      if (a.ksplit > 1) {
+        *(mf4*)(a.part + ((int64_t)split * a.M + row) * a.ncat + sg.c0 + col) = v;
+      } else {
+        mf4* y = (mf4*)(sg.y + (int64_t)row * sg.ldy + col);
+        if (a.accumulate) v += *y;
+        *y = v;
+      }
+    }
+  }
+}
+
 int g_cus = 0;
 int device_cus() {
   if (g_cus > 0) return g_cus;
@@ -275,6 +472,64 @@ int launch_tile(const GemmCall& c, int ksplit, hipStream_t st) {
     Q35_HIP_TRY(hipGetLastError());
   }
   return Q35_OK;
+}
+
+template <int BM>
+int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
+  GArgs a{};
+  a.nseg = c.nseg;
+  a.x = c.x; a.ldx = c.ldx; a.M = c.M; a.K = c.K; a.accumulate = c.accumulate;
+  a.mtiles = (c.M + BM - 1) / BM;
+  int tiles = 0, ncat = 0;
+  for (int i = 0; i < c.nseg; ++i) {
+    const GemmSeg& s = c.seg[i];
+    a.seg[i] = GSeg{s.q, s.s, s.y, s.N, s.layout, s.ldy, s.N / 128, tiles, ncat};
+    tiles += s.N / 128;
+    ncat += s.N;
+  }
+  a.ksplit = ksplit;
+  a.kchunk = ((c.K / kHBK + ksplit - 1) / ksplit) * kHBK;
+  a.ncat = ncat;
+  a.part = c.part;
+  a.nblocks = tiles * ksplit * a.mtiles;
+  a.amax = c.aux;
+  a.spart = c.aux + (gemm_aux_floats(c.M) - kPrepS);
+  const int nrb = (c.M + 3) / 4;
+  hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)(nrb + kPrepS)), dim3(256), 0, st, a, nrb);
+  hipLaunchKernelGGL((hgemm_kernel<BM>), dim3(a.nblocks), dim3(kGT), 0, st, a);
+  Q35_HIP_TRY(hipGetLastError());
+  if (ksplit > 1) {
+    const int64_t n = (int64_t)c.M * (ncat / 4);
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+    Q35_HIP_TRY(hipGetLastError());
+  }
+  return Q35_OK;
+}
+
+// MB path: tile BM x 128 (BM = 128 or 64) and K splits by the same estimate, at the efficiency
+// assumed for the f16 kernel (two MFMAs per product)
+void gemm_pick_mb(const GemmCall& c, int* bm, int* ksplit) {
+  int64_t ncat = 0, tiles128 = 0;
+  for (int i = 0; i < c.nseg; ++i) {
+    ncat += c.seg[i].N;
+    tiles128 += c.seg[i].N / 128;
+  }
+  const int cus = device_cus();
+  const double cu_flops = 2.5e15 / 2.0 / 256.0;
+  double best = 1e300;
+  for (const int tbm : {128, 64}) {
+    const long long tiles = tiles128 * ((c.M + tbm - 1) / tbm);
+    const double eff = tbm == 128 ? 0.35 : 0.28;
+    for (int ks = 1; ks <= kGemmMaxSplit; ks *= 2) {
+      if (ks > 1 && (!c.part || c.part_floats < (size_t)ks * c.M * ncat || c.K / kHBK < 2 * ks)) break;
+      const int kch = ((c.K / kHBK + ks - 1) / ks) * kHBK;
+      const long long blocks = tiles * ks;
+      const double rounds = (double)((blocks + 2 * cus - 1) / (2 * cus));  // two blocks per CU
+      double cost = rounds * 2.0 * 2.0 * tbm * 128.0 * kch / (cu_flops * eff);
+      if (ks > 1) cost += (double)c.M * ncat * (ks + 1) * 4.0 / 4e12 + 3e-6;
+      if (cost < best * 0.97) { best = cost; *bm = tbm; *ksplit = ks; }
+    }
+  }
 }
 
 }  // namespace
@@ -315,6 +570,26 @@ int gemm_pick(const GemmCall& c, int* bm, int* bn, int* ksplit) {
 
 int gemm_launch(const GemmCall& c, hipStream_t st) {
   if (!c.x || c.nseg < 1 || c.nseg > kGemmMaxSeg) return fail(Q35_E_ARG, "gemm: bad arguments");
+  int nmb = 0;
+  for (int i = 0; i < c.nseg; ++i) nmb += c.seg[i].layout == Q35_KN_MB;
+  if (nmb) {
+    if (nmb != c.nseg) return fail(Q35_E_ARG, "gemm: Q35_KN_MB segments cannot be mixed with other layouts");
+    if (!c.aux) return fail(Q35_E_WS, "gemm: Q35_KN_MB needs a workspace");
+    if (c.M < 1 || c.K < kHBK || (c.K % kHBK) != 0) return fail(Q35_E_SHAPE, "gemm: Q35_KN_MB needs K a multiple of 64");
+    if ((c.ldx % 4) != 0 || (reinterpret_cast<uintptr_t>(c.x) & 15) != 0)
+      return fail(Q35_E_ALIGN, "gemm: x rows must be 16-byte aligned");
+    for (int i = 0; i < c.nseg; ++i) {
+      const GemmSeg& s = c.seg[i];
+      if (!s.q || !s.s || !s.y) return fail(Q35_E_ARG, "gemm: null segment pointer");
+      if (s.N < 128 || (s.N % 128) != 0) return fail(Q35_E_SHAPE, "gemm: Q35_KN_MB needs N a multiple of 128");
+      if ((reinterpret_cast<uintptr_t>(s.q) & 15) || (reinterpret_cast<uintptr_t>(s.s) & 15) ||
+          (reinterpret_cast<uintptr_t>(s.y) & 15) || (s.ldy % 4))
+        return fail(Q35_E_ALIGN, "gemm: Q35_KN_MB needs 16-byte aligned q, scales and y rows");
+    }
+    int bm = 128, ks = 1;
+    gemm_pick_mb(c, &bm, &ks);
+    return bm == 128 ? launch_mb<128>(c, ks, st) : launch_mb<64>(c, ks, st);
+  }
   if (c.M < 1 || c.K < kBK || (c.K % 64) != 0) return fail(Q35_E_SHAPE, "gemm: M >= 1 and K a multiple of 64 required");
   if ((c.ldx % 4) != 0 || (reinterpret_cast<uintptr_t>(c.x) & 15) != 0)
     return fail(Q35_E_ALIGN, "gemm: x rows must be 16-byte aligned");

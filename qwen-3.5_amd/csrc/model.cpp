@@ -287,7 +287,9 @@ SeqView model_view(q35_model* m) {
   return v;
 }
 
-int ensure_prefill(q35_model* m) {
+int ensure_prefill(q35_model* m, hipStream_t st) {
+  int rc;
+  if ((rc = ensure_mb(m, st))) return rc;  // the projections' GEMMs read the MB copies
   if (m->pf_cap > 0) return Q35_OK;
   const q35_dims& d = m->d;
   const int H = d.hidden, F = d.ffn, nh = d.lin_heads, vdim = nh * d.lin_dv, key_dim = nh * d.lin_dk;
@@ -296,7 +298,6 @@ int ensure_prefill(q35_model* m) {
   const int ldy = std::max({conv_dim + vdim, ah * hd * 2 + 2 * kvh * hd, 2 * F});
   const int lda = std::max({vdim, ah * hd, F});
   const size_t nchunk = (size_t)cap / kGdnChunk;
-  int rc;
   if ((rc = dev_alloc_t(m, "prefill_x", (size_t)cap * H, &m->pf_x)) ||
       (rc = dev_alloc_t(m, "prefill_xn", (size_t)cap * H, &m->pf_xn)) ||
       (rc = dev_alloc_t(m, "prefill_y", (size_t)cap * ldy, &m->pf_y)) ||
@@ -305,7 +306,8 @@ int ensure_prefill(q35_model* m) {
       (rc = dev_alloc_t(m, "prefill_bg", (size_t)cap * 2 * nh, &m->pf_bg)) ||
       (rc = dev_alloc_t(m, "prefill_q", (size_t)cap * ah * hd, &m->pf_q)) ||
       (rc = dev_alloc_t(m, "prefill_scratch", (size_t)nh * nchunk * kGdnScratchPerChunk, &m->pf_scr)) ||
-      (rc = dev_alloc_t(m, "prefill_partials", gemm_part_floats(cap, H), &m->pf_part)))
+      (rc = dev_alloc_t(m, "prefill_partials", gemm_part_floats(cap, H), &m->pf_part)) ||
+      (rc = dev_alloc_t(m, "prefill_gemm_aux", gemm_aux_floats(cap), &m->pf_aux)))
     return rc;
   m->pf_cap = cap;
   m->pf_ldy = ldy;
@@ -324,18 +326,20 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
   const int LDY = m->pf_ldy;
   int rc;
   if ((rc = embed_launch(m->embed.q, m->embed.s, d.vocab, H, ids, T, m->pf_x, st))) return rc;
-  auto seg = [](const q35_model::Q8& w, float* y, int ldy) {
-    return GemmSeg{w.q, w.s, y, w.cols, Q35_KN_TILED, ldy};
+  // projections on the f16 matrix cores from the MB copies of the weights
+  auto seg = [](const q35_model::Q8& w, const q35_model::Mb& mb, float* y, int ldy) {
+    return GemmSeg{mb.q, mb.s, y, w.cols, Q35_KN_MB, ldy};
   };
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
+    const q35_model::MbLayer& W = m->mb[l];
     if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st))) return rc;
     if (!L.full) {
       GemmCall g;
       g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
-      g.seg[0] = seg(L.qkv, m->pf_y, LDY);
-      g.seg[1] = seg(L.z, m->pf_y + conv_dim, LDY);
-      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      g.seg[0] = seg(L.qkv, W.qkv, m->pf_y, LDY);
+      g.seg[1] = seg(L.z, W.z, m->pf_y + conv_dim, LDY);
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
       if ((rc = gate_prompt_launch(m->pf_xn, H, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st))) return rc;
       GdnPrefill gp;
@@ -348,17 +352,17 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
         return rc;
       GemmCall o;
       o.x = m->pf_a; o.ldx = vdim; o.M = T; o.K = vdim; o.nseg = 1; o.accumulate = 1;
-      o.seg[0] = seg(L.out, m->pf_x, H);
-      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      o.seg[0] = seg(L.out, W.out, m->pf_x, H);
+      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     } else {
       const int qw = ah * hd * 2, kvw = kvh * hd;
       GemmCall g;
       g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 3;
-      g.seg[0] = seg(L.q, m->pf_y, LDY);
-      g.seg[1] = seg(L.k, m->pf_y + qw, LDY);
-      g.seg[2] = seg(L.v, m->pf_y + qw + kvw, LDY);
-      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      g.seg[0] = seg(L.q, W.q, m->pf_y, LDY);
+      g.seg[1] = seg(L.k, W.k, m->pf_y + qw, LDY);
+      g.seg[2] = seg(L.v, W.v, m->pf_y + qw + kvw, LDY);
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
       AttnPrefill ap;
       ap.qg = m->pf_y; ap.ld_qg = LDY; ap.k = m->pf_y + qw; ap.v = m->pf_y + qw + kvw; ap.ld_kv = LDY;
@@ -369,22 +373,22 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       if ((rc = attn_prefill_launch(ap, st))) return rc;
       GemmCall o;
       o.x = m->pf_a; o.ldx = ah * hd; o.M = T; o.K = ah * hd; o.nseg = 1; o.accumulate = 1;
-      o.seg[0] = seg(L.o, m->pf_x, H);
-      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+      o.seg[0] = seg(L.o, W.o, m->pf_x, H);
+      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     }
     if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st))) return rc;
     GemmCall g;
     g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
-    g.seg[0] = seg(L.gate, m->pf_y, LDY);
-    g.seg[1] = seg(L.up, m->pf_y + F, LDY);
-    g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+    g.seg[0] = seg(L.gate, W.gate, m->pf_y, LDY);
+    g.seg[1] = seg(L.up, W.up, m->pf_y + F, LDY);
+    g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
     if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st))) return rc;
     GemmCall dn;
     dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
-    dn.seg[0] = seg(L.down, m->pf_x, H);
-    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden);
+    dn.seg[0] = seg(L.down, W.down, m->pf_x, H);
+    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux;
       if ((rc = gemm_launch(dn, st))) return rc;
   }
   if ((rc = store_i32_launch(v.pos, p0 + T - 1, st))) return rc;
@@ -401,7 +405,7 @@ namespace {
 // The n prompt ids already in m->prompt[host_pos..) through the prompt path, in passes.
 int prefill(q35_model* m, int n, hipStream_t st) {
   int rc;
-  if ((rc = ensure_prefill(m))) return rc;
+  if ((rc = ensure_prefill(m, st))) return rc;
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_prefill: tmax too small");
   for (int done = 0; done < n;) {
     const int T = std::min(m->pf_cap, n - done);

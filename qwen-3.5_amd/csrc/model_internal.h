@@ -52,7 +52,7 @@ struct q35_model {
   // prompt path (allocated on first use): up to pf_cap tokens per pass
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
-  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr, *pf_part = nullptr;
+  float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr, *pf_part = nullptr, *pf_aux = nullptr;
   // batched decode (allocated on first use): every projection again in the MB layout of the
   // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
   struct Mb { const int8_t* q = nullptr; const float* s = nullptr; const float* f = nullptr; };
@@ -81,8 +81,8 @@ struct SeqView {
   int32_t tmax = 0;
 };
 SeqView model_view(q35_model* m);
-// Allocates the prompt-path scratch on first use.
-int ensure_prefill(q35_model* m);
+// Allocates the prompt-path scratch and builds the MB weight copies on first use.
+int ensure_prefill(q35_model* m, hipStream_t st);
 // One prompt pass of T <= m->pf_cap tokens (device ids) at positions p0.. of sequence v.
 int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int p0, hipStream_t st);
 // Builds the MB-layout copies of the projection weights on first use.

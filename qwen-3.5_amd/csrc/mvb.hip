@@ -52,8 +52,8 @@ constexpr int kAuxLd = kRound + 4; // f32 staging row of the gate side blocks (o
 constexpr int kDirectKR = 1024;    // rows of K per block on the RMS direct path
 
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef q35_h2 h2;
+typedef q35_h8 h8;
 
 struct MbkSeg {
   const int8_t* q;  // MB layout
@@ -75,36 +75,6 @@ struct MbkArgs {
 
 Q35_DEV f4 ld4(const float* p) { return *(const Q35_GLOBAL f4*)p; }
 Q35_DEV f4 lds4(const float* p) { return *(const f4*)p; }
-
-// Two weights u0, u1 (bytes sel of dw, u = q + 128) -> f16 pair (q0, q1), exact.
-Q35_DEV h2 u8_pair(uint32_t dw, uint32_t sel) {
-  const uint32_t v = __builtin_amdgcn_perm(0x64646464u, dw, sel);  // halves 0x6400 | u
-  return __builtin_bit_cast(h2, v) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
-}
-// The 8 weights of bytes 0..3 of da and 0..3 of db as an f16 MFMA operand.
-Q35_DEV h8 a8_from(uint32_t da, uint32_t db) {
-  const h2 p0 = u8_pair(da, 0x04010400u), p1 = u8_pair(da, 0x04030402u);
-  const h2 p2 = u8_pair(db, 0x04010400u), p3 = u8_pair(db, 0x04030402u);
-  return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
-// 2^(14 - E) and its inverse for a row whose largest |value| is amax < 2^E (E from the float's
-// exponent field; rows of zeros get 1)
-Q35_DEV void split_scale(float amax, float& f, float& inv) {
-  const int bits = __float_as_int(amax);
-  const int E = amax > 0.f ? ((bits >> 23) & 0xff) - 126 : 14;
-  const int e = min(max(14 - E, -100), 100);
-  f = __int_as_float((127 + e) << 23);
-  inv = __int_as_float((127 - e) << 23);
-}
-// y -> (hi, lo) f16 halves (packed conversions, rounding toward zero), y = hi + lo to about 22
-// bits: y - hi is exact in f32, and lo keeps its leading 11 bits
-typedef __fp16 hf2 __attribute__((ext_vector_type(2)));
-Q35_DEV void split2(float y0, float y1, uint32_t& hi, uint32_t& lo) {
-  const hf2 h = __builtin_amdgcn_cvt_pkrtz(y0, y1);
-  const hf2 l = __builtin_amdgcn_cvt_pkrtz(y0 - (float)h[0], y1 - (float)h[1]);
-  hi = __builtin_bit_cast(uint32_t, h);
-  lo = __builtin_bit_cast(uint32_t, l);
-}
 
 // A block's input rows live in LDS for its whole K range: at most 1024 / MT rows of Mp = 16 MT
 // rows, as an f32 staging area (aux blocks) or as the hi / lo f16 planes, each row padded so that
@@ -684,8 +654,9 @@ __global__ __launch_bounds__(kT) void rms_rows_split_kernel(const float* x, int 
 
 // ------------------------------------------------------------------ layout conversion
 // Tile-major projection layout (q[t][K][256], scale[t][K][4], the last tile padded to 256
-// columns) -> MB layout (see the top).
-__global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int N, int8_t* qb, float* sb) {
+// columns; tiled = 1) or row-major KN (q[K][N], scale[K][N/64]; tiled = 0) -> MB layout (see the
+// top).
+__global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int N, int tiled, int8_t* qb, float* sb) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-byte lane record
   const size_t nrec = (size_t)K * N / 32;
   if (i < nrec) {
@@ -704,7 +675,8 @@ __global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int k = 32 * ks + 8 * g + 4 * h + j;
-          const uint8_t b = (uint8_t)qt[((size_t)t * K + k) * 256 + cw + 16 * nt + c] ^ 0x80u;  // u = q + 128
+          const size_t src = tiled ? ((size_t)t * K + k) * 256 + cw + 16 * nt + c : (size_t)k * N + 64 * cb + 16 * nt + c;
+          const uint8_t b = (uint8_t)qt[src] ^ 0x80u;  // u = q + 128
           v |= (uint32_t)b << (8 * j);
         }
         dw[2 * nt + h] = v;
@@ -713,9 +685,9 @@ __global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int 
     *(uint4*)(qb + i * 32 + 16) = make_uint4(dw[4], dw[5], dw[6], dw[7]);
   }
   const size_t ns = (size_t)K * (N / 64);
-  if (i < ns) {  // scale[cb][k] = st[t][k][cb % 4]
+  if (i < ns) {  // scale[cb][k] = st[t][k][cb % 4] (tiled) or st[k][cb]
     const int cb = (int)(i / K), k = (int)(i % K);
-    sb[i] = st[((size_t)(cb >> 2) * K + k) * 4 + (cb & 3)];
+    sb[i] = tiled ? st[((size_t)(cb >> 2) * K + k) * 4 + (cb & 3)] : st[(size_t)k * (N / 64) + cb];
   }
 }
 
@@ -731,12 +703,12 @@ __global__ void scale_transpose_kernel(const float* s, int V, int nkb, float* sT
 }  // namespace
 
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
-                      hipStream_t st) {
+                      hipStream_t st, int tiled) {
   if (!q_tiled || !s_tiled || !q_mb || !s_mb) return fail(Q35_E_ARG, "mb_convert: null pointer");
   if (K < 32 || K % 32 || N < 64 || N % 64) return fail(Q35_E_SHAPE, "mb_convert: need K % 32 == 0, N % 64 == 0");
   const size_t n = std::max((size_t)K * N / 32, (size_t)K * (N / 64));
   hipLaunchKernelGGL(mb_convert_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q_tiled, s_tiled, K, N,
-                     q_mb, s_mb);
+                     tiled, q_mb, s_mb);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -127,6 +127,41 @@ Q35_DEV T ldg_nt(const T* p) { return __builtin_nontemporal_load((const Q35_GLOB
 // The same as a native vector (for register arrays that stay live across a runtime loop)
 Q35_DEV q35_u32x4 ldg16v_nt(const void* p) { return __builtin_nontemporal_load((const Q35_GLOBAL q35_u32x4*)p); }
 
+// ---- f32-equivalent products on the f16 matrix cores (v_mfma_f32_16x16x32_f16): 8-bit weights
+// are exact in f16; an f32 input y is carried as hi + lo halves.
+typedef _Float16 q35_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 q35_h8 __attribute__((ext_vector_type(8)));
+typedef __fp16 q35_hf2 __attribute__((ext_vector_type(2)));
+// Two weights u0, u1 (bytes sel of dw, u = q + 128) -> f16 pair (q0, q1), exact.
+Q35_DEV q35_h2 u8_pair(uint32_t dw, uint32_t sel) {
+  const uint32_t v = __builtin_amdgcn_perm(0x64646464u, dw, sel);  // halves 0x6400 | u
+  return __builtin_bit_cast(q35_h2, v) - q35_h2{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+// The 8 weights of bytes 0..3 of da and 0..3 of db as an f16 MFMA operand.
+Q35_DEV q35_h8 a8_from(uint32_t da, uint32_t db) {
+  const q35_h2 p0 = u8_pair(da, 0x04010400u), p1 = u8_pair(da, 0x04030402u);
+  const q35_h2 p2 = u8_pair(db, 0x04010400u), p3 = u8_pair(db, 0x04030402u);
+  return q35_h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+// 2^(14 - E) and its inverse for a row whose largest |value| is amax < 2^E (E from the float's
+// exponent field; rows of zeros get 1)
+Q35_DEV void split_scale(float amax, float& f, float& inv) {
+  const int bits = __float_as_int(amax);
+  const int E = amax > 0.f ? ((bits >> 23) & 0xff) - 126 : 14;
+  const int e = min(max(14 - E, -126), 126);  // (both 2^e and 2^-e normal)
+  f = __int_as_float((127 + e) << 23);
+  inv = __int_as_float((127 - e) << 23);
+}
+// y -> (hi, lo) f16 halves (packed conversions, rounding toward zero), y = hi + lo to about 22
+// bits: y - hi is exact in f32, and lo keeps its leading 11 bits
+Q35_DEV void split2(float y0, float y1, uint32_t& hi, uint32_t& lo) {
+  const q35_hf2 h = __builtin_amdgcn_cvt_pkrtz(y0, y1);
+  const q35_hf2 l = __builtin_amdgcn_cvt_pkrtz(y0 - (float)h[0], y1 - (float)h[1]);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
+
 Q35_DEV void fx_add(fx_t* p, float v) {
   __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -392,7 +427,7 @@ struct GemmSeg {
   const float* s;
   float* y;        // y[m*ldy + n]
   int32_t N;       // columns (multiple of 64)
-  int32_t layout;  // Q35_KN, Q35_KN_TILED (rows = K) or Q35_NK (rows = N)
+  int32_t layout;  // Q35_KN, Q35_KN_TILED, Q35_KN_MB (rows = K) or Q35_NK (rows = N)
   int32_t ldy;
 };
 struct GemmCall {
@@ -405,7 +440,11 @@ struct GemmCall {
   // estimated faster, and sums the splits in a fixed order in a second kernel
   float* part = nullptr;
   size_t part_floats = 0;
+  // Q35_KN_MB launches (every segment MB): kGemmAuxFloats(M) floats for the row and scale maxima
+  float* aux = nullptr;
 };
+// Scratch floats of an MB launch: row maxima [M] and scale partial maxima [64], 64-aligned.
+inline size_t gemm_aux_floats(int M) { return ((size_t)M + 63) / 64 * 64 + 64; }
 int gemm_launch(const GemmCall& c, hipStream_t st);
 // Tile shape and K splits the launcher picks for c (BM x BN, ksplit).
 int gemm_pick(const GemmCall& c, int* bm, int* bn, int* ksplit);
@@ -533,9 +572,10 @@ int mb_launch(const MbCall& c, hipStream_t st);
 size_t mb_part_floats(int ncb, int K, int M);
 // Split factors of an MB weight for RMS launches whose norm weights are norm_w.
 int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st);
-// Tile-major projection weights (q[t][K][256], scale[t][K][4]) -> MB layout.
+// Tile-major projection weights (q[t][K][256], scale[t][K][4]; or, tiled = 0, row-major KN)
+// -> MB layout.
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
-                      hipStream_t st);
+                      hipStream_t st, int tiled = 1);
 // logits[m][n] = RMSNorm(h[m]) . dequant(E[n]) over the tied NK table (scales transposed,
 // sT[K/64][V]), M <= 32 rows, K a multiple of 512 up to 2048; split16 holds 2 * M * K halves and
 // invf M floats of scratch.

@@ -11,7 +11,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_DIR, "libq35.so")
 
 Q35_OK, Q35_E_SHAPE, Q35_E_ALIGN, Q35_E_HIP, Q35_E_ARG, Q35_E_WS, Q35_E_NOMEM = range(7)
-Q35_KN, Q35_NK, Q35_KN_TILED, Q35_KN_PANEL = 0, 1, 2, 3
+Q35_KN, Q35_NK, Q35_KN_TILED, Q35_KN_PANEL, Q35_KN_MB = 0, 1, 2, 3, 4
 Q35_LAUNCH_STREAM, Q35_LAUNCH_GRAPH, Q35_LAUNCH_PERSISTENT = 0, 1, 2
 Q35_PREFILL_GEMM = 0x100
 ERROR_NAMES = {1: "Q35_E_SHAPE", 2: "Q35_E_ALIGN", 3: "Q35_E_HIP", 4: "Q35_E_ARG", 5: "Q35_E_WS", 6: "Q35_E_NOMEM"}
@@ -117,6 +117,7 @@ PROTOTYPES = {
     "q35_q8f_tiled_scale_count": (c_i64, [ctypes.c_int32, ctypes.c_int32]),
     "q35_q8f_pack_kn_tiled": (ctypes.c_int, [c_vp, c_vp, ctypes.c_int32, ctypes.c_int32, c_vp, c_vp]),
     "q35_q8f_pack_kn_panel": (ctypes.c_int, [c_vp, c_vp, ctypes.c_int32, ctypes.c_int32, c_vp, c_vp]),
+    "q35_q8f_pack_mb": (ctypes.c_int, [Q8F, c_vp, c_vp, c_vp]),
     "q35_safetensors_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(Dims), ctypes.c_char_p, c_vp, c_i64]),
     "q35_synth_model_tensor": (ctypes.c_int, [ctypes.POINTER(Dims), c_u64, ctypes.c_char_p, c_vp, c_i64]),
 }

@@ -57,6 +57,8 @@ class Q8FTensor:
     layout Q35_NK: q [N][K],          scale [N][K/64]  (embedding table, kernels.rs:253-255)
     layout Q35_KN_TILED: the Q35_KN matrix cut into 256-column tiles, tile-major:
         q [ceil(N/256)][K][256], scale [ceil(N/256)][K][4], columns past N zero
+    layout Q35_KN_MB: the f16 matrix-core records (q [N/64][K/32][2048] bytes q + 128, scale
+        [N/64][K]), made on the device by mb()
     """
 
     def __init__(self, q, scale, layout=L.Q35_KN, shape=None):
@@ -65,6 +67,10 @@ class Q8FTensor:
             assert shape is not None and q.dim() == 3 and q.shape[2] == 256 and scale.shape == q.shape[:2] + (4,)
             self.rows, self.cols = shape
             assert q.shape[:2] == ((self.cols + 255) // 256, self.rows), (q.shape, shape)
+        elif layout == L.Q35_KN_MB:
+            assert shape is not None and q.numel() == shape[0] * shape[1]
+            self.rows, self.cols = shape
+            assert scale.shape == (self.cols // 64, self.rows)
         elif layout == L.Q35_KN_PANEL:
             assert shape is not None and q.dim() == 3 and q.shape[2] == 16
             self.rows, self.cols = shape
@@ -101,6 +107,16 @@ class Q8FTensor:
         nt = (N + 255) // 256
         return Q8FTensor(torch.from_numpy(qt.reshape(nt, K, 256)).to(self.q.device),
                          torch.from_numpy(st.reshape(nt, K, 4)).to(self.q.device), L.Q35_KN_TILED, (K, N))
+
+    def mb(self, stream=None):
+        """Q35_KN / Q35_KN_TILED -> Q35_KN_MB copy, packed on the device (q35_q8f_pack_mb)."""
+        assert self.layout in (L.Q35_KN, L.Q35_KN_TILED)
+        K, N = self.rows, self.cols
+        qm = torch.empty((N // 64, K // 32, 2048), dtype=torch.int8, device=self.q.device)
+        sm = torch.empty((N // 64, K), dtype=torch.float32, device=self.q.device)
+        st = stream if stream is not None else _stream()
+        L.check(L.lib().q35_q8f_pack_mb(self.desc(), qm.data_ptr(), sm.data_ptr(), st))
+        return Q8FTensor(qm, sm, L.Q35_KN_MB, (K, N))
 
     def panel(self):
         """Q35_KN -> Q35_KN_PANEL copy, packed on the host through q35_q8f_pack_kn_panel."""

@@ -21,15 +21,17 @@ def _p(t):
 
 
 def q8_gemm(x, W, y=None, accumulate=False, split_k=False):
-    """y[M][N] (+)= x[M][K] @ dequant(W) on the fp32 matrix cores.  split_k: pass a workspace
-    (q35_q8_gemm_ws), so that the launcher may split K for shapes with few output tiles."""
+    """y[M][N] (+)= x[M][K] @ dequant(W) on the fp32 matrix cores, or on the f16 matrix cores with
+    f32-equivalent products for W in Q35_KN_MB (always with a workspace).  split_k: pass a
+    workspace (q35_q8_gemm_ws), so that the launcher may split K for shapes with few output
+    tiles."""
     assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
     M = x.shape[0]
     if y is None:
         y = torch.empty((M, W.out_dim), dtype=torch.float32, device=x.device)
     assert y.stride(1) == 1 and y.shape[0] == M
     acc = 1 if accumulate else 0
-    if split_k:
+    if split_k or W.layout == L.Q35_KN_MB:
         nb = L.lib().q35_q8_gemm_ws_bytes(M, W.desc())
         ws = workspace(nb, x.device, key="gemm")
         L.check(L.lib().q35_q8_gemm_ws(x.data_ptr(), M, x.stride(0), W.desc(), y.data_ptr(), y.stride(0), acc,

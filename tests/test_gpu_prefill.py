@@ -2,6 +2,9 @@
 
 * q35_q8_gemm (fp32 matrix cores) against a float64 x @ dequant(W): rel-L2 <= 1e-5, in every
   weight layout, with row strides and accumulation;
+* q35_q8f_pack_mb against the MB record layout rebuilt in numpy (bit-exact), and q35_q8_gemm_ws
+  on the f16 matrix cores (Q35_KN_MB) against float64: rel-L2 <= 1e-5 overall and per row, rows
+  of very different magnitudes, zero rows, accumulation, split K;
 * the causal conv + chunked gated delta rule against T recurrent oracle steps (the reference's
   chunked rule equals them, which tests/test_oracle_modules.py pins): core output rel-L2 <= 1e-5,
   recurrent state <= 1e-4, conv state bit-exact (copies of inputs);
@@ -84,6 +87,86 @@ def test_q8_gemm_split_k(M, K, N, accumulate):
     q35.q8_gemm(dev(x), q8_dev(W, q35.Q35_KN).tiled(), yd[:, 64:], accumulate=accumulate, split_k=True)
     y = host(yd)
     ref = x.astype(np.float64) @ W.dequant()
+    if accumulate:
+        ref = ref + y0[:, 64:].astype(np.float64)
+    assert rel_l2(y[:, 64:], ref) <= 1e-5
+    np.testing.assert_array_equal(y[:, :64], y0[:, :64])
+
+
+def mb_layout_np(W):
+    """The Q35_KN_MB records of a host Q8F [K][N] matrix, rebuilt from the layout's definition:
+    per (cb, ks) 2048 bytes, lane l = 16 g + c holds q + 128 of rows 32 ks + 8 g + j (j < 8) for
+    columns 64 cb + 16 t + c, t < 4, as [t][j]; scales transposed to [N/64][K]."""
+    K, N = W.q.shape
+    u = (W.q.astype(np.int16) + 128).astype(np.uint8)            # [K][N]
+    v = u.reshape(K // 32, 4, 8, N // 64, 4, 16)                 # [ks][g][j][cb][t][c]
+    rec = v.transpose(3, 0, 1, 5, 4, 2)                          # [cb][ks][g][c][t][j]
+    return rec.reshape(N // 64, K // 32, 2048), np.ascontiguousarray(W.s.T)
+
+
+@pytest.mark.parametrize("layout", ["kn", "tiled"])
+def test_pack_mb_layout_exact(layout):
+    K, N = 256, 384
+    W = q8(240, K, N)
+    Wd = q8_dev(W, q35.Q35_KN)
+    if layout == "tiled":
+        Wd = Wd.tiled()
+    Wm = Wd.mb()
+    qm, sm = mb_layout_np(W)
+    np.testing.assert_array_equal(host(Wm.q).view(np.uint8), qm)
+    np.testing.assert_array_equal(host(Wm.scale), sm)
+
+
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048), (2048, 512), (4096, 2048), (64, 128), (2048, 8192)])
+@pytest.mark.parametrize("M", [1, 5, 130, 512])
+def test_q8_gemm_mb(M, K, N):
+    """Q35_KN_MB on the f16 matrix cores (int8 exact in f16, x * scale as hi + lo halves) against
+    float64, whole-matrix and per-row."""
+    print(f"[gemm mb] M={M} K={K} N={N}", flush=True)
+    W = q8(250 + K // 64 + N, K, N)
+    x = normal(251 + M, (M, K))
+    y = host(q35.q8_gemm(dev(x), q8_dev(W, q35.Q35_KN).tiled().mb()))
+    ref = x.astype(np.float64) @ W.dequant()
+    assert rel_l2(y, ref) <= 1e-5
+    for r in range(M):
+        assert rel_l2(y[r], ref[r]) <= 1e-5, r
+
+
+def test_q8_gemm_mb_row_magnitudes_and_zero_rows():
+    """Rows from 1e-30 to 1e+20 (the power of two follows each row's largest |x|), rows of zeros,
+    a row with one outlier 1e6 x its other entries, scales of very different sizes per block."""
+    M, K, N = 40, 2048, 1024
+    rng = np.random.default_rng(5)
+    W = q8(260, K, N)
+    W.s[:, ::3] *= 1e-3  # block scales spanning 1e3 within a row of weights
+    x = normal(261, (M, K))
+    mags = 10.0 ** rng.uniform(-30, 20, M)
+    x = (x * mags[:, None]).astype(np.float32)
+    x[3] = 0.0
+    x[17] = 0.0
+    x[8, 100] *= 1e6
+    y = host(q35.q8_gemm(dev(x), q8_dev(W, q35.Q35_KN).mb()))
+    ref = x.astype(np.float64) @ W.dequant()
+    for r in range(M):
+        if not np.any(x[r]):
+            np.testing.assert_array_equal(y[r], 0.0)
+        else:
+            assert rel_l2(y[r], ref[r]) <= 1e-5, (r, mags[r])
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+@pytest.mark.parametrize("K,N", [(2048, 2048), (6144, 2048), (4096, 2048)])
+@pytest.mark.parametrize("M", [130, 512])
+def test_q8_gemm_mb_split_k_strided(M, K, N, accumulate):
+    """The MB path's split-K launches and the residual add into a strided y slice."""
+    print(f"[gemm mb split] M={M} K={K} N={N} acc={accumulate}", flush=True)
+    W = q8(270 + K // 64 + N, K, N)
+    xf = normal(271 + M, (M, K + 64))
+    y0 = normal(272 + M, (M, N + 64))
+    yd = dev(y0)
+    q35.q8_gemm(dev(xf)[:, 64:], q8_dev(W, q35.Q35_KN).tiled().mb(), yd[:, 64:], accumulate=accumulate)
+    y = host(yd)
+    ref = xf[:, 64:].astype(np.float64) @ W.dequant()
     if accumulate:
         ref = ref + y0[:, 64:].astype(np.float64)
     assert rel_l2(y[:, 64:], ref) <= 1e-5
