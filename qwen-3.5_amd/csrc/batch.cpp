@@ -240,10 +240,13 @@ int ensure_mb(q35_model* m, hipStream_t st) {
     int8_t* q = nullptr;
     float* s = nullptr;
     float* f = nullptr;
+    float* smax = nullptr;
     int r;
     if ((r = dev_alloc_t(m, "mb." + name, (size_t)w.rows * w.cols, &q)) ||
         (r = dev_alloc_t(m, "mb." + name + ".scale", (size_t)w.rows * (w.cols / 64), &s)) ||
-        (r = mb_convert_launch(w.q, w.s, w.rows, w.cols, q, s, st)))
+        (r = dev_alloc_t(m, "mb." + name + ".scale_max", 1, &smax)) ||
+        (r = mb_convert_launch(w.q, w.s, w.rows, w.cols, q, s, st)) ||
+        (r = mb_scale_max_launch(s, (int64_t)w.rows * (w.cols / 64), smax, st)))
       return r;
     if (norm_w && ((r = dev_alloc_t(m, "mb." + name + ".split", (size_t)(w.cols / 64), &f)) ||
                    (r = mb_split_factor_launch(s, w.rows, w.cols, norm_w, f, st))))
@@ -251,6 +254,7 @@ int ensure_mb(q35_model* m, hipStream_t st) {
     out.q = q;
     out.s = s;
     out.f = f;
+    out.smax = smax;
     return Q35_OK;
   };
   for (size_t l = 0; l < m->layers.size(); ++l) {

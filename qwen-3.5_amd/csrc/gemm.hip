@@ -40,6 +40,7 @@ struct GSeg {
   const float* s;
   float* y;
   int32_t N, layout, ldy, ntiles, tile0, c0;  // c0: first column in the concatenated partials
+  const float* smax;  // MB path: the weights' largest |scale| when known (else the prep pass finds it)
 };
 struct GArgs {
   GSeg seg[kGemmMaxSeg];
@@ -261,25 +262,33 @@ constexpr int kPrepS = 64;        // blocks of the scale-maximum pass (one wave'
 
 typedef float mf4 __attribute__((ext_vector_type(4)));
 
-// Row maxima of |x| (blocks < nrb: one wave per row) and partial maxima of every segment's |scale|
-// (blocks nrb .. nrb + kPrepS - 1, a strided share each).
-__global__ __launch_bounds__(256) void hgemm_prep_kernel(const GArgs a, int nrb) {
+// Row maxima of |x| (blocks < M: one row each, every load issued before the first use) and,
+// without precomputed ones, partial maxima of every segment's |scale| (blocks M .. M + kPrepS - 1,
+// a strided share each).
+__global__ __launch_bounds__(256) void hgemm_prep_kernel(const GArgs a) {
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if ((int)blockIdx.x < nrb) {
-    const int m = (int)blockIdx.x * 4 + w;
-    if (m >= a.M) return;  // (this branch has no block barrier)
-    const float* xr = a.x + (int64_t)m * a.ldx;
+  if ((int)blockIdx.x < a.M) {
+    const float* xr = a.x + (int64_t)blockIdx.x * a.ldx;
     float mx = 0.f;
-    for (int k = 4 * lane; k < a.K; k += 256) {
-      const float4 v = *(const float4*)(xr + k);
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    for (int k0 = 0; k0 < a.K; k0 += 8 * 1024) {
+      mf4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + 1024 * u + 4 * tid;
+        v[u] = k < a.K ? *(const Q35_GLOBAL mf4*)(xr + k) : mf4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3]))));
     }
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) a.amax[m] = mx;
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    if (tid == 0) a.amax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     return;
   }
-  const int p = (int)blockIdx.x - nrb;
+  const int p = (int)blockIdx.x - a.M;
   float mx = 0.f;
 #pragma unroll
   for (int i = 0; i < kGemmMaxSeg; ++i) {
@@ -317,8 +326,15 @@ __global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
 
   // 2^e of each row: (row max |x|) x (max |scale|) x 2^e < 2^14, with room for rounding
   {
-    float S = a.spart[lane];
-    for (int o = 32; o > 0; o >>= 1) S = fmaxf(S, __shfl_xor(S, o));
+    float S = 0.f;
+    if (a.seg[0].smax) {  // precomputed for every segment
+#pragma unroll
+      for (int i = 0; i < kGemmMaxSeg; ++i)
+        if (i < a.nseg) S = fmaxf(S, *a.seg[i].smax);
+    } else {
+      S = a.spart[lane];
+      for (int o = 32; o > 0; o >>= 1) S = fmaxf(S, __shfl_xor(S, o));
+    }
     if (tid < BM) {
       float f, inv;
       split_scale(a.amax[min(m0 + tid, a.M - 1)] * S * (1.0f + 0x1p-10f), f, inv);
@@ -392,10 +408,18 @@ __global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
     for (int h = 0; h < 2; ++h) {
       const q35_h8 aw[4] = {a8_from(wc[h][0][0], wc[h][0][1]), a8_from(wc[h][0][2], wc[h][0][3]),
                             a8_from(wc[h][1][0], wc[h][1][1]), a8_from(wc[h][1][2], wc[h][1][3])};
+      // every LDS read of this half step first, so one wait covers them
+      mf4 xv[MT][2];
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const float* xr = Xb + (wm * WM + 16 * i + c) * kXLd + 32 * h + 8 * g;
-        const mf4 x0 = *(const mf4*)xr, x1 = *(const mf4*)(xr + 4);
+        xv[i][0] = *(const mf4*)xr;
+        xv[i][1] = *(const mf4*)(xr + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink each read to its use)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const mf4 x0 = xv[i][0], x1 = xv[i][1];
         uint32_t hi[4], lo[4];
         split2(x0[0] * scur[h][0][0], x0[1] * scur[h][0][1], hi[0], lo[0]);
         split2(x0[2] * scur[h][0][2], x0[3] * scur[h][0][3], hi[1], lo[1]);
@@ -483,7 +507,7 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   int tiles = 0, ncat = 0;
   for (int i = 0; i < c.nseg; ++i) {
     const GemmSeg& s = c.seg[i];
-    a.seg[i] = GSeg{s.q, s.s, s.y, s.N, s.layout, s.ldy, s.N / 128, tiles, ncat};
+    a.seg[i] = GSeg{s.q, s.s, s.y, s.N, s.layout, s.ldy, s.N / 128, tiles, ncat, s.smax};
     tiles += s.N / 128;
     ncat += s.N;
   }
@@ -494,8 +518,11 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   a.nblocks = tiles * ksplit * a.mtiles;
   a.amax = c.aux;
   a.spart = c.aux + (gemm_aux_floats(c.M) - kPrepS);
-  const int nrb = (c.M + 3) / 4;
-  hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)(nrb + kPrepS)), dim3(256), 0, st, a, nrb);
+  bool smax = true;
+  for (int i = 0; i < c.nseg; ++i) smax = smax && c.seg[i].smax;
+  if (!smax)
+    for (int i = 0; i < c.nseg; ++i) a.seg[i].smax = nullptr;
+  hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)(c.M + (smax ? 0 : kPrepS))), dim3(256), 0, st, a);
   hipLaunchKernelGGL((hgemm_kernel<BM>), dim3(a.nblocks), dim3(kGT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   if (ksplit > 1) {

@@ -328,7 +328,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
   if ((rc = embed_launch(m->embed.q, m->embed.s, d.vocab, H, ids, T, m->pf_x, st))) return rc;
   // projections on the f16 matrix cores from the MB copies of the weights
   auto seg = [](const q35_model::Q8& w, const q35_model::Mb& mb, float* y, int ldy) {
-    return GemmSeg{mb.q, mb.s, y, w.cols, Q35_KN_MB, ldy};
+    return GemmSeg{mb.q, mb.s, y, w.cols, Q35_KN_MB, ldy, mb.smax};
   };
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];

@@ -55,7 +55,12 @@ struct q35_model {
   float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr, *pf_part = nullptr, *pf_aux = nullptr;
   // batched decode (allocated on first use): every projection again in the MB layout of the
   // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
-  struct Mb { const int8_t* q = nullptr; const float* s = nullptr; const float* f = nullptr; };
+  struct Mb {
+    const int8_t* q = nullptr;
+    const float* s = nullptr;
+    const float* f = nullptr;     // batched RMS launches: split factor per column block
+    const float* smax = nullptr;  // max |scale| (prompt GEMMs)
+  };
   struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down; };
   std::vector<MbLayer> mb;
   const float* embed_scale_t = nullptr;  // the embedding table's scales transposed [hidden/64][vocab]

@@ -757,6 +757,28 @@ __global__ __launch_bounds__(kT) void mb_split_factor_kernel(const float* sb, in
 
 }  // namespace
 
+namespace {
+__global__ __launch_bounds__(1024) void scale_max_kernel(const float* s, int64_t n, float* out) {
+  __shared__ float red[16];
+  float mx = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) mx = fmaxf(mx, fabsf(s[i]));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, red[i]);
+    out[0] = mx;
+  }
+}
+}  // namespace
+
+int mb_scale_max_launch(const float* s, int64_t n, float* out, hipStream_t st) {
+  if (!s || !out || n < 1) return fail(Q35_E_ARG, "mb_scale_max: bad arguments");
+  hipLaunchKernelGGL(scale_max_kernel, dim3(1), dim3(1024), 0, st, s, n, out);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
 int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st) {
   if (!s_mb || !norm_w || !f || K < 1 || N < 64 || N % 64) return fail(Q35_E_ARG, "mb_split_factor: bad arguments");
   hipLaunchKernelGGL(mb_split_factor_kernel, dim3((unsigned)(N / 64)), dim3(kT), 0, st, s_mb, K, norm_w, f);

@@ -429,6 +429,7 @@ struct GemmSeg {
   int32_t N;       // columns (multiple of 64)
   int32_t layout;  // Q35_KN, Q35_KN_TILED, Q35_KN_MB (rows = K) or Q35_NK (rows = N)
   int32_t ldy;
+  const float* smax = nullptr;  // Q35_KN_MB: device copy of max |scale| (mb_scale_max_launch), optional
 };
 struct GemmCall {
   GemmSeg seg[kGemmMaxSeg];
@@ -570,6 +571,8 @@ struct MbCall {
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
 size_t mb_part_floats(int ncb, int K, int M);
+// out[0] = max |s[i]| over n floats (one block).
+int mb_scale_max_launch(const float* s, int64_t n, float* out, hipStream_t st);
 // Split factors of an MB weight for RMS launches whose norm weights are norm_w.
 int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st);
 // Tile-major projection weights (q[t][K][256], scale[t][K][4]; or, tiled = 0, row-major KN)
