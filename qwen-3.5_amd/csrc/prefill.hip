@@ -69,32 +69,39 @@ __global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ld
   float acc[kGateRows];
 #pragma unroll
   for (int r = 0; r < kGateRows; ++r) acc[r] = 0.f;
+  constexpr int kIt = kGateK / (8 * kGateGroups);
   for (int k0 = 0; k0 < K; k0 += kGateK) {
+    const int kn = min(kGateK, K - k0);  // a multiple of 64
     __syncthreads();
-    {  // all of the chunk's loads are issued before any is stored (one round trip)
-      constexpr int kL = kGateRows * kGateK / 4 / kPT;  // float4 per thread (8)
-      float4 v[kL];
+    // all of the chunk's loads are issued before any is used (one round trip): the x rows, and
+    // the weights of the thread's 8-row groups kb = 8 kg + 64 it (rows clamped inside the chunk)
+    constexpr int kL = kGateRows * kGateK / 4 / kPT;  // float4 per thread (8)
+    float4 v[kL];
 #pragma unroll
-      for (int u = 0; u < kL; ++u) {
-        const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4, t = t0 + i;
-        v[u] = (t < T && k0 + kk < K) ? *(const float4*)(x + (int64_t)t * ldx + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+    for (int u = 0; u < kL; ++u) {
+      const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4, t = t0 + i;
+      v[u] = (t < T && k0 + kk < K) ? *(const float4*)(x + (int64_t)t * ldx + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float w[kIt][8];
 #pragma unroll
-      for (int u = 0; u < kL; ++u) {
-        const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4;
-        xs[i][kk] = v[u].x; xs[i][kk + 1] = v[u].y; xs[i][kk + 2] = v[u].z; xs[i][kk + 3] = v[u].w;
-      }
+    for (int it = 0; it < kIt; ++it)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[it][u] = W[(int64_t)(k0 + min(kg * 8 + 64 * it, kn - 8) + u) * nh];
+#pragma unroll
+    for (int u = 0; u < kL; ++u) {
+      const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4;
+      xs[i][kk] = v[u].x; xs[i][kk + 1] = v[u].y; xs[i][kk + 2] = v[u].z; xs[i][kk + 3] = v[u].w;
     }
     __syncthreads();
-    const int kn = min(kGateK, K - k0);
-    for (int kb = kg * 8; kb < kn; kb += 8 * kGateGroups) {
-      float w[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) w[u] = (kb + u < kn) ? W[(int64_t)(k0 + kb + u) * nh] : 0.f;
+    for (int it = 0; it < kIt; ++it) {
+      const int kb = kg * 8 + 64 * it;
+      if (kb < kn) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int r = 0; r < kGateRows; ++r) acc[r] += xs[r][kb + u] * w[u];
+          for (int r = 0; r < kGateRows; ++r) acc[r] += xs[r][kb + u] * w[it][u];
+      }
     }
   }
 #pragma unroll
