@@ -39,7 +39,7 @@ struct q35_batch {
   std::vector<float*> conv, rec, kc, vc;  // per layer, [B][...]
   float *h = nullptr;      // residual rows [B][hidden]
   float *proj = nullptr;   // q|k|v|z (linear) or q|k|v (full) projection rows [B][proj_n]
-  float *gu = nullptr;     // gate | up rows [B][2 ffn]
+  float *gu = nullptr;     // gate | up rows [B][2 ffn], and a second copy for two split partials
   float *o_raw = nullptr, *attn = nullptr, *logits = nullptr, *pv = nullptr, *part = nullptr, *invf = nullptr;
   _Float16* split16 = nullptr;  // the lm_head's split input rows (hi, lo) of one row group
   q35::fx_t* ss = nullptr;   // RMSNorm statistics [2 layers + 1][B]
@@ -102,6 +102,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
   const int ah = d.attn_heads, kvh = d.kv_heads, hd = d.head_dim;
   const int ldqg = ah * hd * 2, kvw = kvh * hd;
   int rc;
+  std::vector<int32_t> gu_two((B + kRowGroup - 1) / kRowGroup, 0);  // gate|up left two partials
   // embedding rows + the first norm's statistic; clears every other statistic and gate sum
   if ((rc = batch_embed_f32_launch(m->embed.q, m->embed.s, H, bt->token, bt->prompt, bt->tmax, bt->plen, bt->pos, bt->h,
                                    bt->ss, bt->ss + B, (int64_t)2 * NL * B + (int64_t)NL * B * kGateLd, B, st)))
@@ -175,12 +176,19 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       c.nseg = 2;
       c.seg[0] = MbSeg{W.gate.q, W.gate.s, gu, F, 2 * F, W.gate.f};
       c.seg[1] = MbSeg{W.up.q, W.up.s, gu + F, F, 2 * F, W.up.f};
+      // with two K splits the down projection sums the two partial copies itself (no hand-off)
+      c.defer_stride = (int64_t)B * 2 * F;
+      c.deferred_out = &gu_two[r0 / kRowGroup];
       if ((rc = mb_launch(c, st))) return rc;
     }
     for (int r0 = 0; r0 < B; r0 += kRowGroup) {
       MbCall c;
       base(c, std::min(kRowGroup, B - r0));
       c.K = F; c.x = bt->gu + (size_t)r0 * 2 * F; c.ldx = 2 * F; c.pro = MB_PRO_SWIGLU; c.swiglu_off = F;
+      if (gu_two[r0 / kRowGroup]) {
+        c.xsum = 2;
+        c.xsstride = (int64_t)B * 2 * F;
+      }
       c.nseg = 1; c.seg[0] = MbSeg{W.down.q, W.down.s, bt->h + (size_t)r0 * H, H, H};
       c.add = 1; c.ss_out = ss_next + r0;
       if ((rc = mb_launch(c, st))) return rc;
@@ -354,7 +362,7 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   b->ss = stats;
   b->gates = stats + (size_t)(2 * NL + 1) * B;
   if ((rc = balloc_t(b, "h", (size_t)B * H, &b->h)) || (rc = balloc_t(b, "proj", (size_t)B * b->proj_n, &b->proj)) ||
-      (rc = balloc_t(b, "gu", (size_t)B * 2 * F, &b->gu)) || (rc = balloc_t(b, "lm_split16", (size_t)2 * kRowGroup * H, &b->split16)) ||
+      (rc = balloc_t(b, "gu", (size_t)2 * B * 2 * F, &b->gu)) || (rc = balloc_t(b, "lm_split16", (size_t)2 * kRowGroup * H, &b->split16)) ||
       (rc = balloc_t(b, "lm_invf", kRowGroup, &b->invf)) ||
       (rc = balloc_t(b, "partials", std::max<size_t>(b->part_floats, 64), &b->part)) ||
       (rc = balloc_t(b, "mb_counters", kMbCounters, &b->mb_ctr)) ||

@@ -69,6 +69,8 @@ struct MbkArgs {
   int32_t pro; const float* pw; float eps; const fx_t* ss;
   const float* z; int32_t ldz, group, swiglu_off;
   int32_t add; fx_t* ss_out;
+  int64_t dstride;   // > 0 with nsplit == 2: split s writes its partial to y + s * dstride (no hand-off)
+  int64_t xsstride;  // consumer of such partials (XS = 2): the second copy's offset
   const float* aux_wb; const float* aux_wa; int32_t aux_nh; fx_t* aux_acc; int32_t aux_ldo, naux;
   float* part; uint32_t* ctr;
 };
@@ -103,7 +105,9 @@ struct XBuf {
 //   [Mp][LDH] then lo), with the row's inverse power of two in invf[row].
 // `issue` runs right after the staging loads are issued: the caller's weight prefetch goes
 // behind them, so the staging arithmetic waits only for its own loads (loads return in order).
-template <int MT, bool SPLIT, typename Issue>
+// XS = 2: the input rows are two split-K partials of the producer, xsstride floats apart (summed
+// here in split order, as the producer's own hand-off would have).
+template <int MT, bool SPLIT, int XS = 1, typename Issue>
 Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs, const float* scl, float* pws,
                      float* invf, Issue&& issue) {
   using X = XBuf<MT>;
@@ -134,10 +138,12 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
     const int cc = min(ci, nch - 1) * kRound;  // (chunks past the range reload the last one)
 #pragma unroll
     for (int i = 0; i < X::VPT; i += 4) {
-      const f4 q = ld4(xr + cc + i);
+      f4 q = ld4(xr + cc + i);
+      if constexpr (XS == 2) q = q + ld4(xr + a.xsstride + cc + i);
       v[ci][i] = q[0]; v[ci][i + 1] = q[1]; v[ci][i + 2] = q[2]; v[ci][i + 3] = q[3];
       if (two || (rms && !SPLIT)) {
-        const f4 w = ld4(rms ? a.pw + k0 + cc + c0 + i : ur + cc + i);
+        f4 w = ld4(rms ? a.pw + k0 + cc + c0 + i : ur + cc + i);
+        if constexpr (XS == 2) w = w + ld4(ur + a.xsstride + cc + i);  // (SwiGLU only)
         u[ci][i] = w[0]; u[ci][i + 1] = w[1]; u[ci][i + 2] = w[2]; u[ci][i + 3] = w[3];
       }
     }
@@ -271,7 +277,7 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
 // |x * r| <= sqrt(K) for an RMS-normalised row, so sqrt(K) * max|1 + w| * max|s| bounds every |y|
 // of the block and f puts that bound in [2^13, 2^14)).  The bound is loose for most rows, which
 // costs nothing: hi / lo keep about 22 bits of each y down to 2^-17 of the bound.
-template <int MT, bool DIRECT>
+template <int MT, bool DIRECT, int XS = 1>
 __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   using X = XBuf<MT>;
   constexpr int Mp = X::Mp;
@@ -344,8 +350,8 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) rrow[mt] = rsqrt_f(from_fx(ssv[mt]) * rcp_f((float)a.K) + a.eps);
   } else {
-    stage_x<MT, true>(a, k0, klen, xbuf, scs, scl, pws, invf,
-                      [&] { static_for<kDepth>([&](auto d) { load_round(d, d); }); });
+    stage_x<MT, true, XS>(a, k0, klen, xbuf, scs, scl, pws, invf,
+                          [&] { static_for<kDepth>([&](auto d) { load_round(d, d); }); });
     __syncthreads();
   }
 
@@ -442,6 +448,15 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
     for (int q = 1; q < 4; ++q) v += *(const f4*)&red[((q * 4 + p) * MT + mt) * 256 + lane * 4];
     // the split's 2^e undone: per row (staged) or per column block (direct; 2^-e exactly)
     out[mt] = v * (DIRECT ? __int_as_float((254 << 23) - __float_as_int(fcb)) : invf[16 * mt + c]);
+  }
+  if (a.dstride > 0) {  // two splits, each writes its partial (scaled) for the consumer to sum
+    float* yb = sg.y + (size_t)split * a.dstride;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + c;
+      if (m < a.M) *(f4*)(yb + (size_t)m * sg.ldy + ncol0) = out[mt];
+    }
+    return;
   }
   if (a.nsplit > 1) {
     float* pp = a.part + ((size_t)cb * a.nsplit + split) * Mp * 64;
@@ -848,18 +863,32 @@ int mb_launch(const MbCall& c, hipStream_t st) {
   a.ss = c.pro == MB_PRO_RMS ? c.ss : reinterpret_cast<const fx_t*>(c.x);  // rows of x: >= 8 M bytes
   a.z = c.z; a.ldz = c.ldz; a.group = c.group; a.swiglu_off = c.swiglu_off;
   a.add = c.add; a.ss_out = c.ss_out;
+  // two-split launches of up to 16 rows without a residual add may leave their partials to the
+  // consumer (for 17..32 rows the consumer's doubled staging costs more than the hand-off saves)
+  a.dstride = (c.defer_stride > 0 && a.nsplit == 2 && c.M <= 16 && !c.add && !c.ss_out) ? c.defer_stride : 0;
+  if (c.deferred_out) *c.deferred_out = a.dstride > 0 ? 1 : 0;
+  if (a.dstride)
+    for (int i = 0; i < c.nseg; ++i)
+      if ((reinterpret_cast<uintptr_t>(c.seg[i].y) & 15) || (c.seg[i].ldy & 3) || (c.defer_stride & 3))
+        return fail(Q35_E_ALIGN, "mb_launch: deferred partial rows 16-byte aligned");
+  const int xs = c.xsum == 2 ? 2 : 1;
+  if (c.xsum != 1 && (c.xsum != 2 || c.pro != MB_PRO_SWIGLU || c.M > 16 || (c.xsstride & 3)))
+    return fail(Q35_E_ARG, "mb_launch: a two-partial input is supported for the SwiGLU prologue of <= 16 rows only");
+  a.xsstride = xs == 2 ? c.xsstride : 0;
   a.aux_wb = c.aux_wb; a.aux_wa = c.aux_wa; a.aux_nh = c.aux_nh; a.aux_acc = c.aux_acc; a.aux_ldo = c.aux_ldo;
   a.naux = c.aux_acc ? c.K / kRound : 0;
   if (c.aux_acc && (c.aux_nh < 1 || 2 * c.aux_nh > 32 || !c.aux_wb || !c.aux_wa))
     return fail(Q35_E_ARG, "mb_launch: gate side task needs 1..16 heads and both weights");
-  if (a.nsplit > 1) {
+  if (a.nsplit > 1 && !a.dstride) {
     const size_t need = (size_t)ncb * a.nsplit * (c.M <= 16 ? 16 : 32) * 64;
     if (!c.part || c.part_floats < need || !c.ctr || c.nctr < ncb)
       return fail(Q35_E_WS, "mb_launch: split-K partials / counters too small");
     a.part = c.part; a.ctr = c.ctr;
   }
   const dim3 grid((unsigned)(ncb * a.nsplit + a.naux));
-  if (c.M <= 16) {
+  if (xs == 2) {  // (staged SwiGLU prologue, <= 16 rows)
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2>), grid, dim3(kT), 0, st, a);
+  } else if (c.M <= 16) {
     if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, true>), grid, dim3(kT), 0, st, a);
     else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false>), grid, dim3(kT), 0, st, a);
   } else {

@@ -567,6 +567,12 @@ struct MbCall {
   fx_t* aux_acc = nullptr; int32_t aux_ldo = 0;
   // split-K partials and one counter per 64-column block (zero between launches)
   float* part = nullptr; size_t part_floats = 0; uint32_t* ctr = nullptr; int32_t nctr = 0;
+  // defer_stride > 0 (no residual add, M <= 16): when the plan splits K in two, split s writes its
+  // partial rows to seg.y + s * defer_stride and the launch ends without a hand-off;
+  // *deferred_out tells.
+  int64_t defer_stride = 0; int32_t* deferred_out = nullptr;
+  // xsum = 2 (SwiGLU prologue, M <= 16): each input value is x[...] + x[... + xsstride], such partials
+  int32_t xsum = 1; int64_t xsstride = 0;
 };
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
