@@ -348,13 +348,17 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
   }
 }
 
-__global__ __launch_bounds__(kPT) void gdn_chunk_state_kernel(const GdnPrefill a) {
+// 512 threads: the two halves of the block split each product's k range (v_new, q_e S) and add
+// their halves in a fixed order, so every chain of dependent FMAs is half as long.
+constexpr int kST = 512;
+__global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float Ss[kDk][kSl];
   __shared__ __align__(16) float Kc[kC][kLdq];
   __shared__ __align__(16) float Qe[kC][kLdq];
   __shared__ __align__(16) float Kd[kC][kLdq];
   __shared__ float In[kC][kC + 1];
   __shared__ __align__(16) float Vn[kC][kSl];
+  __shared__ __align__(16) float Red[kC][kSl];  // the upper half's partial sums
   __shared__ float cdv;
 
   const int tid = threadIdx.x;
@@ -364,7 +368,7 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_state_kernel(const GdnPrefill a
   // the new conv state of the head's channels: the last 3 inputs (older ones from the old state
   // when the prompt is shorter than 3); the prep launch has read the old state already
   if (sl == 0 && a.conv_state_out) {
-    for (int e = tid; e < 3 * kDk; e += kPT) {
+    for (int e = tid; e < 3 * kDk; e += kST) {
       const int part = e >> 7, jj = e & 127;
       const int ch = part == 0 ? h * kDk + jj : (part == 1 ? a.key_dim + h * kDk + jj : 2 * a.key_dim + h * kDk + jj);
       float* st = a.conv_state_out + (int64_t)ch * 3;
@@ -377,99 +381,103 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_state_kernel(const GdnPrefill a
       st[0] = n[0]; st[1] = n[1]; st[2] = n[2];
     }
   }
-  {
-    const int e = tid >> 1, j = (tid & 1) * 8;
-    const float* src = S + (int64_t)e * kDk + c0 + j;
-    *(float4*)&Ss[e][j] = *(const float4*)src;
-    *(float4*)&Ss[e][j + 4] = *(const float4*)(src + 4);
-  }
-  constexpr int kLd4 = kC * kDk / 4 / kPT;   // float4 per thread per 64 x 128 matrix (8)
-  constexpr int kLdIn = kC * kC / 4 / kPT;   // float4 per thread of the intra matrix (4)
+  // thread (e4 = tid / 4, j4 = 4 (tid % 4)): S rows e4, columns j4..j4+3 of the slice
+  const int e4 = tid >> 2, j4 = (tid & 3) * 4;
+  *(float4*)&Ss[e4][j4] = *(const float4*)(S + (int64_t)e4 * kDk + c0 + j4);
+  constexpr int kLd4 = kC * kDk / 4 / kST;   // float4 per thread per 64 x 128 matrix (4)
+  constexpr int kLdIn = kC * kC / 4 / kST;   // float4 per thread of the intra matrix (2)
+  const int hf = tid >> 8, i = (tid & 255) >> 2, j = (tid & 3) * 4;  // half, row, 4 columns
   for (int c = 0; c < a.nchunk; ++c) {
     const float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
     {  // every load of the chunk is issued before any is stored (one round trip per chunk)
       float4 vkc[kLd4], vqe[kLd4], vkd[kLd4], vin[kLdIn];
 #pragma unroll
       for (int u = 0; u < kLd4; ++u) {
-        const int e = tid + u * kPT;
+        const int e = tid + u * kST;
         vkc[u] = *(const float4*)(scr + kScrKcd + 4 * e);
         vqe[u] = *(const float4*)(scr + kScrQe + 4 * e);
         vkd[u] = *(const float4*)(scr + kScrKd + 4 * e);
       }
 #pragma unroll
-      for (int u = 0; u < kLdIn; ++u) vin[u] = *(const float4*)(scr + kScrIntra + 4 * (tid + u * kPT));
-      const float4 vnv = *(const float4*)(scr + kScrNv + (tid >> 2) * kDk + c0 + (tid & 3) * 4);
+      for (int u = 0; u < kLdIn; ++u) vin[u] = *(const float4*)(scr + kScrIntra + 4 * (tid + u * kST));
+      const int vr = (tid & 255) >> 2;  // (the lower half loads the new values)
+      const float4 vnv = *(const float4*)(scr + kScrNv + vr * kDk + c0 + (tid & 3) * 4);
       const float vcd = scr[kScrCd];
 #pragma unroll
       for (int u = 0; u < kLd4; ++u) {
-        const int e = tid + u * kPT, i = e >> 5, d = (e & 31) * 4;
-        *(float4*)&Kc[i][d] = vkc[u];
-        *(float4*)&Qe[i][d] = vqe[u];
-        *(float4*)&Kd[i][d] = vkd[u];
+        const int e = tid + u * kST, r = e >> 5, d = (e & 31) * 4;
+        *(float4*)&Kc[r][d] = vkc[u];
+        *(float4*)&Qe[r][d] = vqe[u];
+        *(float4*)&Kd[r][d] = vkd[u];
       }
 #pragma unroll
       for (int u = 0; u < kLdIn; ++u) {
-        const int e = 4 * (tid + u * kPT), i = e >> 6, j = e & 63;
-        In[i][j] = vin[u].x; In[i][j + 1] = vin[u].y; In[i][j + 2] = vin[u].z; In[i][j + 3] = vin[u].w;
+        const int e = 4 * (tid + u * kST), r = e >> 6, q = e & 63;
+        In[r][q] = vin[u].x; In[r][q + 1] = vin[u].y; In[r][q + 2] = vin[u].z; In[r][q + 3] = vin[u].w;
       }
-      *(float4*)&Vn[tid >> 2][(tid & 3) * 4] = vnv;
+      if (hf == 0) *(float4*)&Vn[vr][(tid & 3) * 4] = vnv;
       if (tid == 0) cdv = vcd;
     }
     __syncthreads();
-    const int i = tid >> 2, j = (tid & 3) * 4;
-    {  // v_new = new_values - k_cumdecay S
+    {  // v_new = new_values - k_cumdecay S: half hf sums e in [64 hf, 64 hf + 64)
       float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-      for (int e = 0; e < kDk; ++e) {
+      const int eb = 64 * hf;
+      for (int e = eb; e < eb + 64; ++e) {
         const float k = Kc[i][e];
         const float4 sv = *(const float4*)&Ss[e][j];
         s0 += k * sv.x; s1 += k * sv.y; s2 += k * sv.z; s3 += k * sv.w;
       }
-      float4 nv = *(const float4*)&Vn[i][j];
-      nv.x -= s0; nv.y -= s1; nv.z -= s2; nv.w -= s3;
-      *(float4*)&Vn[i][j] = nv;
+      if (hf == 1) *(float4*)&Red[i][j] = make_float4(s0, s1, s2, s3);
+      __syncthreads();
+      if (hf == 0) {
+        const float4 r = *(const float4*)&Red[i][j];
+        float4 nv = *(const float4*)&Vn[i][j];
+        nv.x -= s0 + r.x; nv.y -= s1 + r.y; nv.z -= s2 + r.z; nv.w -= s3 + r.w;
+        *(float4*)&Vn[i][j] = nv;
+      }
     }
     __syncthreads();
-    {  // out = q_e S + intra v_new
+    {  // out = q_e S + intra v_new: the upper half takes e in [64, 128), the lower half e in
+       // [0, 64) and the intra-chunk sum; added as (lower + upper) + intra
       float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-      for (int e = 0; e < kDk; ++e) {
+      const int eb = 64 * hf;
+      for (int e = eb; e < eb + 64; ++e) {
         const float q = Qe[i][e];
         const float4 sv = *(const float4*)&Ss[e][j];
         o0 += q * sv.x; o1 += q * sv.y; o2 += q * sv.z; o3 += q * sv.w;
       }
+      if (hf == 1) *(float4*)&Red[i][j] = make_float4(o0, o1, o2, o3);
       float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-      for (int l = 0; l <= i; ++l) {
-        const float w = In[i][l];
-        const float4 v = *(const float4*)&Vn[l][j];
-        p0 += w * v.x; p1 += w * v.y; p2 += w * v.z; p3 += w * v.w;
+      if (hf == 0) {
+        for (int l = 0; l <= i; ++l) {
+          const float w = In[i][l];
+          const float4 v = *(const float4*)&Vn[l][j];
+          p0 += w * v.x; p1 += w * v.y; p2 += w * v.z; p3 += w * v.w;
+        }
       }
-      const int t = c * kC + i;
-      if (t < a.T) *(float4*)(a.out + (int64_t)t * a.ld_out + h * kDk + c0 + j) = make_float4(o0 + p0, o1 + p1, o2 + p2, o3 + p3);
+      __syncthreads();
+      if (hf == 0) {
+        const float4 r = *(const float4*)&Red[i][j];
+        const int t = c * kC + i;
+        if (t < a.T)
+          *(float4*)(a.out + (int64_t)t * a.ld_out + h * kDk + c0 + j) =
+              make_float4((o0 + r.x) + p0, (o1 + r.y) + p1, (o2 + r.z) + p2, (o3 + r.w) + p3);
+      }
     }
-    __syncthreads();
-    {  // S = S e^cum_last + k_d^T v_new
-      const int e = tid >> 1, jj = (tid & 1) * 8;
+    {  // S = S e^cum_last + k_d^T v_new: thread (e4, j4), all 64 rows of the chunk
       const float cd = cdv;
-      float s[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s[u] = Ss[e][jj + u] * cd;
+      float s0 = Ss[e4][j4] * cd, s1 = Ss[e4][j4 + 1] * cd, s2 = Ss[e4][j4 + 2] * cd, s3 = Ss[e4][j4 + 3] * cd;
       for (int l = 0; l < kC; ++l) {
-        const float k = Kd[l][e];
-        const float4 va = *(const float4*)&Vn[l][jj];
-        const float4 vb = *(const float4*)&Vn[l][jj + 4];
-        s[0] += k * va.x; s[1] += k * va.y; s[2] += k * va.z; s[3] += k * va.w;
-        s[4] += k * vb.x; s[5] += k * vb.y; s[6] += k * vb.z; s[7] += k * vb.w;
+        const float k = Kd[l][e4];
+        const float4 v = *(const float4*)&Vn[l][j4];
+        s0 += k * v.x; s1 += k * v.y; s2 += k * v.z; s3 += k * v.w;
       }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) Ss[e][jj + u] = s[u];
+      __syncthreads();  // every read of S and Vn of this chunk is done
+      *(float4*)&Ss[e4][j4] = make_float4(s0, s1, s2, s3);
     }
     __syncthreads();
   }
-  {
-    const int e = tid >> 1, j = (tid & 1) * 8;
-    float* dst = S + (int64_t)e * kDk + c0 + j;
-    *(float4*)dst = *(const float4*)&Ss[e][j];
-    *(float4*)(dst + 4) = *(const float4*)&Ss[e][j + 4];
-  }
+  *(float4*)(S + (int64_t)e4 * kDk + c0 + j4) = *(const float4*)&Ss[e4][j4];
 }
 
 // out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100)
@@ -684,7 +692,7 @@ int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st) {
   if ((a.ld_out % 4) != 0) return fail(Q35_E_ALIGN, "gdn_prefill: output rows must be 16-byte aligned");
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(a.nchunk * a.nh), dim3(kPT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL(gdn_chunk_state_kernel, dim3(kNsl * a.nh), dim3(kPT), 0, st, a);
+  hipLaunchKernelGGL(gdn_chunk_state_kernel, dim3(kNsl * a.nh), dim3(kST), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
