@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
   float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
 
   // causal conv (cached state prepended) + SiLU: one channel of the head's 3 x 128 per thread
-  // pass, a sliding window of the last three inputs in registers, 16 rows loaded at a time
+  // pass, a sliding window of the last three inputs in registers
   for (int jj = tid; jj < 3 * kDk; jj += kPT) {
     const int part = jj >> 7, cc = jj & 127;
     const int ch = part == 0 ? h * kDk + cc : (part == 1 ? a.key_dim + h * kDk + cc : 2 * a.key_dim + h * kDk + cc);
@@ -227,20 +227,17 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
       }
       x0 = xw[0]; x1 = xw[1]; x2 = xw[2];
     }
-    for (int g0 = 0; g0 < kC; g0 += 16) {
-      float xv[16];
+    // all of the chunk's inputs of the channel in flight at once (rows clamped, masked below)
+    float xv[kC];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int t = t0 + g0 + u;
-        xv[u] = t < a.T ? a.raw[(int64_t)t * a.ld_raw + ch] : 0.f;
-      }
+    for (int u = 0; u < kC; ++u) xv[u] = a.raw[(int64_t)min(t0 + u, a.T - 1) * a.ld_raw + ch];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int t = t0 + g0 + u;
-        const float y = ((w0 * x0 + w1 * x1) + w2 * x2) + w3 * xv[u];
-        dst[g0 + u][cc] = t < a.T ? silu_f(y) : 0.f;
-        x0 = x1; x1 = x2; x2 = xv[u];
-      }
+    for (int u = 0; u < kC; ++u) {
+      const int t = t0 + u;
+      const float xin = t < a.T ? xv[u] : 0.f;
+      const float y = ((w0 * x0 + w1 * x1) + w2 * x2) + w3 * xin;
+      dst[u][cc] = t < a.T ? silu_f(y) : 0.f;
+      x0 = x1; x1 = x2; x2 = xin;
     }
   }
   if (tid < kC) {
