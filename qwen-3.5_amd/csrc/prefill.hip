@@ -142,9 +142,10 @@ Q35_DEV void tri_task(int k, int* i, int* jg) {
 // (the reference's row recurrence, text_modules.rs:282-290, on that block), then
 // X_BA = X_BB N_BA X_AA joins 16-blocks into 32-blocks and those into the 64-block
 // (for [[I - N_AA, 0], [-N_BA, I - N_BB]]).  Tm: 64 x 65 scratch.
+// (512 threads: waves 0-3 take the diagonal blocks, every thread one or two entries after that)
 Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  {
+  if (wid < 4) {
     const int b0 = 16 * wid;
     for (int i = 2; i < 16; ++i) {
       float s = 0.f;
@@ -157,20 +158,15 @@ Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
   __syncthreads();
   // 16 -> 32: blocks (1,0) and (3,2) of 16: X = X_BB N X_AA = (I + L_B)(N + N L_A)
   {
-    const int p = tid >> 7, e0 = tid & 127;  // pair p, two entries per thread
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = e0 + 128 * u, r = e >> 4, c = e & 15;
-      const int rb = 32 * p + 16, cb = 32 * p;  // block rows / cols
+    const int p = tid >> 8, e = tid & 255, r = e >> 4, c = e & 15;  // pair p, one entry per thread
+    const int rb = 32 * p + 16, cb = 32 * p;                         // block rows / cols
+    {
       float t = U[rb + r][cb + c];
       for (int l = c + 1; l < 16; ++l) t += U[rb + r][cb + l] * U[cb + l][cb + c];
       Tm[rb + r][cb + c] = t;
     }
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = e0 + 128 * u, r = e >> 4, c = e & 15;
-      const int rb = 32 * p + 16, cb = 32 * p;
+    {
       float t = Tm[rb + r][cb + c];
       for (int l = 0; l < r; ++l) t += U[rb + r][rb + l] * Tm[rb + l][cb + c];
       U[rb + r][cb + c] = t;
@@ -179,16 +175,16 @@ Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
   __syncthreads();
   // 32 -> 64: block (1,0) of 32
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + 512 * u, r = e >> 5, c = e & 31;
     float t = U[32 + r][c];
     for (int l = c + 1; l < 32; ++l) t += U[32 + r][l] * U[l][c];
     Tm[32 + r][c] = t;
   }
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + 512 * u, r = e >> 5, c = e & 31;
     float t = Tm[32 + r][c];
     for (int l = 0; l < r; ++l) t += U[32 + r][32 + l] * Tm[32 + l][c];
     U[32 + r][c] = t;
@@ -196,7 +192,8 @@ Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a) {
+constexpr int kPP = 512;  // threads of the prep pass
+__global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float Qs[kC][kLdq];
   __shared__ __align__(16) float Ks[kC][kLdq];
   __shared__ __align__(16) float Vs[kC][kLdq];
@@ -211,7 +208,7 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
 
   // causal conv (cached state prepended) + SiLU: one channel of the head's 3 x 128 per thread
   // pass, a sliding window of the last three inputs in registers
-  for (int jj = tid; jj < 3 * kDk; jj += kPT) {
+  for (int jj = tid; jj < 3 * kDk; jj += kPP) {
     const int part = jj >> 7, cc = jj & 127;
     const int ch = part == 0 ? h * kDk + cc : (part == 1 ? a.key_dim + h * kDk + cc : 2 * a.key_dim + h * kDk + cc);
     float (*dst)[kLdq] = part == 0 ? Qs : (part == 1 ? Ks : Vs);
@@ -245,10 +242,10 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
     bet[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + h] : 0.f;
     cum[tid] = t < a.T ? a.bg[(int64_t)t * a.ld_bg + a.nh + h] : 0.f;  // g for now
   }
-  for (int e = tid; e < kC * kC; e += kPT) U[e >> 6][e & 63] = 0.f;
+  for (int e = tid; e < kC * kC; e += kPP) U[e >> 6][e & 63] = 0.f;
   __syncthreads();
   // l2norm of q (times dk^-1/2) and k rows
-  for (int r = wid; r < 2 * kC; r += 4) {
+  for (int r = wid; r < 2 * kC; r += kPP / 64) {
     float* row = r < kC ? Qs[r] : Ks[r - kC];
     const float v0 = row[lane], v1 = row[lane + 64];
     const float rn = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) + 1e-6f);
@@ -269,11 +266,11 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
   __syncthreads();
   // N = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i; intra = (q_i.k_j) e^(cum_i - cum_j) for j <= i
   float* intra = scr + kScrIntra;
-  for (int e = tid; e < kC * kC; e += kPT) {  // the blocks of 4 columns past the diagonal block
+  for (int e = tid; e < kC * kC; e += kPP) {  // the blocks of 4 columns past the diagonal block
     const int i = e >> 6, j = e & 63;
     if ((j >> 2) > (i >> 2)) intra[e] = 0.f;
   }
-  for (int k = tid; k < kTriTasks; k += kPT) {
+  for (int k = tid; k < kTriTasks; k += kPP) {
     int i, jg;
     tri_task(k, &i, &jg);
     const int j0 = 4 * jg;
@@ -298,17 +295,17 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
   }
   __syncthreads();
   tri_inverse(U, Tm);
-  // new_values = X (beta v), k_cumdecay = X (beta e^cum k): thread rows p and 63 - p, 16 columns
+  // new_values = X (beta v), k_cumdecay = X (beta e^cum k): thread rows p and 63 - p, 8 columns
   {
-    const int p = tid >> 3, d0 = (tid & 7) * 16;
+    const int p = tid >> 4, d0 = (tid & 15) * 8;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int i = half == 0 ? p : kC - 1 - p;
-      float an[16], ak[16];
+      float an[8], ak[8];
       {
         const float ub = bet[i], ube = ub * ecum[i];  // the unit diagonal
 #pragma unroll
-        for (int d = 0; d < 16; d += 4) {
+        for (int d = 0; d < 8; d += 4) {
           const float4 v = *(const float4*)&Vs[i][d0 + d];
           const float4 k = *(const float4*)&Ks[i][d0 + d];
           an[d] = ub * v.x; an[d + 1] = ub * v.y; an[d + 2] = ub * v.z; an[d + 3] = ub * v.w;
@@ -319,7 +316,7 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
         const float ub = U[i][l] * bet[l];
         const float ube = ub * ecum[l];
 #pragma unroll
-        for (int d = 0; d < 16; d += 4) {
+        for (int d = 0; d < 8; d += 4) {
           const float4 v = *(const float4*)&Vs[l][d0 + d];
           const float4 k = *(const float4*)&Ks[l][d0 + d];
           an[d] += ub * v.x; an[d + 1] += ub * v.y; an[d + 2] += ub * v.z; an[d + 3] += ub * v.w;
@@ -332,7 +329,7 @@ __global__ __launch_bounds__(kPT) void gdn_chunk_prep_kernel(const GdnPrefill a)
       float* qe = scr + kScrQe + i * kDk + d0;
       float* kd = scr + kScrKd + i * kDk + d0;
 #pragma unroll
-      for (int d = 0; d < 16; d += 4) {
+      for (int d = 0; d < 8; d += 4) {
         *(float4*)(nv + d) = make_float4(an[d], an[d + 1], an[d + 2], an[d + 3]);
         *(float4*)(kcd + d) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
         const float4 q = *(const float4*)&Qs[i][d0 + d];
@@ -687,7 +684,7 @@ int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st) {
   if (!a.raw || !a.conv_state || !a.conv_w || !a.bg || !a.scr || !a.S || !a.out) return fail(Q35_E_ARG, "gdn_prefill: null pointer");
   if (a.T < 1 || a.nh < 1 || a.nchunk != (a.T + kC - 1) / kC) return fail(Q35_E_SHAPE, "gdn_prefill: bad T / chunks");
   if ((a.ld_out % 4) != 0) return fail(Q35_E_ALIGN, "gdn_prefill: output rows must be 16-byte aligned");
-  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(a.nchunk * a.nh), dim3(kPT), 0, st, a);
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(a.nchunk * a.nh), dim3(kPP), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(gdn_chunk_state_kernel, dim3(kNsl * a.nh), dim3(kST), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
