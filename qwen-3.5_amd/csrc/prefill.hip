@@ -541,20 +541,23 @@ __global__ __launch_bounds__(kPT) void attn_prefill_prep_kernel(const AttnPrefil
 // Causal GQA attention of the prompt rows.  Block (query tile, kv head g): 16 rows = QT tokens x
 // rep query heads of g (QT = 16 / rep), so a 512-token prompt gives 128 x kv_heads blocks;
 // thread (row r = tid / 16, slice sl = tid % 16) holds dims [16 sl, 16 sl + 16) of its row's
-// query and output.  Keys stream through LDS 32 at a time (each 16-float slice padded to 20 so
-// the 16 slices of a row fall in different banks); a score is the sum of the 16 slices' partial
-// dots (4 lane exchanges); online softmax in log2 units, rescaled once per 8 keys.
-constexpr int kKT = 32;            // keys per LDS tile
+// query and output.  Keys stream through LDS 16 at a time per half block (each 16-float slice
+// padded to 20 so the 16 slices of a row fall in different banks): the block's two halves of 256
+// threads take alternate 16-key tiles, each with its own online softmax, and merge their (max,
+// sum, output) at the end.  A score is the sum of the 16 slices' partial dots (4 lane exchanges);
+// online softmax in log2 units, rescaled once per 8 keys.
+constexpr int kKT = 16;            // keys per LDS tile (per half block)
+constexpr int kAT = 512;           // threads per block (two halves)
 constexpr int kSd = 16;            // dims per thread
 constexpr int kSp = 20;            // LDS floats per 16-dim slice
 constexpr int kRows = 16;          // query rows per block
-__global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) {
-  __shared__ __align__(16) float Ks[kKT][16 * kSp];
-  __shared__ __align__(16) float Vs[kKT][16 * kSp];
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(kAT) void attn_prefill_kernel(const AttnPrefill a) {
+  __shared__ __align__(16) float Ks[2][kKT][16 * kSp];
+  __shared__ __align__(16) float Vs[2][kKT][16 * kSp];
+  const int tid = threadIdx.x, hb = tid >> 8, lt = tid & 255;  // half block, thread in the half
   const int rep = a.nh / a.nkv, QT = kRows / rep;
   const int qt = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
-  const int r = tid >> 4, sl = tid & 15;
+  const int r = lt >> 4, sl = lt & 15;
   const int t = qt * QT + r / rep, hq = g * rep + r % rep;
   const bool row_ok = t < a.T;
   const int lim = a.p0 + (row_ok ? t : 0);  // last key this row may see
@@ -572,37 +575,39 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
   const float sl2 = a.scale * 1.44269504088896341f;
   const float* Kg = a.kc + (int64_t)g * a.tmax * kHdP;
   const float* Vg = a.vc + (int64_t)g * a.tmax * kHdP;
-  // the next tile's rows are loaded into registers while the current tile is computed
-  constexpr int kTl = kKT * kHdP / 4 / kPT;  // float4 per thread per tile (8)
+  // half hb takes the tiles at keys 2 kKT i + kKT hb; the next tile's rows are loaded into
+  // registers while the current one is computed
+  constexpr int kTl = kKT * kHdP / 4 / 256;  // float4 per thread per tile (4)
   q35_f32x4 nk[kTl], nv[kTl];
   auto load_tile = [&](int base) {
     static_for<kTl>([&](auto U) {
       constexpr int u = decltype(U)::value;
-      const int e = tid + u * kPT, j = e >> 6, d = (e & 63) * 4;
+      const int e = lt + u * 256, j = e >> 6, d = (e & 63) * 4;
       const int kj = min(base + j, nkeys - 1);
       nk[u] = *(const q35_f32x4*)(Kg + (int64_t)kj * kHdP + d);
       nv[u] = *(const q35_f32x4*)(Vg + (int64_t)kj * kHdP + d);
     });
   };
-  load_tile(0);
-  for (int k0 = 0; k0 < nkeys; k0 += kKT) {
+  load_tile(kKT * hb);
+  for (int kb = 0; kb < nkeys; kb += 2 * kKT) {  // (the same trip count in both halves)
+    const int k0 = kb + kKT * hb;
     __syncthreads();
     static_for<kTl>([&](auto U) {
       constexpr int u = decltype(U)::value;
-      const int e = tid + u * kPT, j = e >> 6, d = (e & 63) * 4;
+      const int e = lt + u * 256, j = e >> 6, d = (e & 63) * 4;
       const int o = (d >> 4) * kSp + (d & 15);
-      *(q35_f32x4*)&Ks[j][o] = nk[u];
-      *(q35_f32x4*)&Vs[j][o] = nv[u];
+      *(q35_f32x4*)&Ks[hb][j][o] = nk[u];
+      *(q35_f32x4*)&Vs[hb][j][o] = nv[u];
     });
     __syncthreads();
-    if (k0 + kKT < nkeys) load_tile(k0 + kKT);
-    const int kend = min(kKT, nkeys - k0);
+    if (k0 + 2 * kKT < nkeys) load_tile(k0 + 2 * kKT);
+    const int kend = min(kKT, nkeys - k0);  // (<= 0: this half's tile is past the keys)
     for (int jb = 0; jb < kend; jb += 8) {
       float s[8];
       float bm = -INFINITY;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float* kr = &Ks[jb + u][sl * kSp];
+        const float* kr = &Ks[hb][jb + u][sl * kSp];
         float p = 0.f;
 #pragma unroll
         for (int d = 0; d < kSd; d += 4) {
@@ -627,7 +632,7 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
       for (int u = 0; u < 8; ++u) {
         const float p = __builtin_amdgcn_exp2f(s[u] - mn);
         l += p;
-        const float* vr = &Vs[jb + u][sl * kSp];
+        const float* vr = &Vs[hb][jb + u][sl * kSp];
 #pragma unroll
         for (int d = 0; d < kSd; d += 4) {
           const float4 vv = *(const float4*)(vr + d);
@@ -637,7 +642,26 @@ __global__ __launch_bounds__(kPT) void attn_prefill_kernel(const AttnPrefill a) 
       m = mn;
     }
   }
-  if (!row_ok) return;
+  // merge the upper half's state into the lower half's (key 0, in the lower half's first tile, is
+  // visible to every row, so the lower half's maximum is finite)
+  float* mg = &Ks[0][0][0];  // (kSd + 2) floats per thread of the upper half
+  __syncthreads();
+  if (hb == 1) {
+#pragma unroll
+    for (int d = 0; d < kSd; ++d) mg[lt * (kSd + 2) + d] = acc[d];
+    mg[lt * (kSd + 2) + kSd] = m;
+    mg[lt * (kSd + 2) + kSd + 1] = l;
+  }
+  __syncthreads();
+  if (hb == 1 || !row_ok) return;
+  {
+    const float m1 = mg[lt * (kSd + 2) + kSd], l1 = mg[lt * (kSd + 2) + kSd + 1];
+    const float mx = fmaxf(m, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);  // (m1 = -inf: 0)
+    l = l * a0 + l1 * a1;
+#pragma unroll
+    for (int d = 0; d < kSd; ++d) acc[d] = acc[d] * a0 + mg[lt * (kSd + 2) + d] * a1;
+  }
   const float* gate = a.qg + (int64_t)t * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + sl * kSd;
   float* dst = a.out + (int64_t)t * a.ld_out + (int64_t)hq * kHdP + sl * kSd;
 #pragma unroll
@@ -719,7 +743,7 @@ int attn_prefill_launch(const AttnPrefill& a, hipStream_t st) {
   Q35_HIP_TRY(hipGetLastError());
   const int QT = kRows / (a.nh / a.nkv);
   const int nqt = (a.T + QT - 1) / QT;
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(nqt * a.nkv), dim3(kPT), 0, st, a);
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(nqt * a.nkv), dim3(kAT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
