@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GArgs a) {
 // is scaled back by 2^-e.  2^e is fixed for the whole launch from the row's largest |x| and the
 // weights' largest |scale|, so every |y| < 2^14 (f16 overflows at 65504).
 //
-// Block = 4 waves in a 2 x 2 grid over a BM x 128 tile; wave (wm, wn) owns rows wm*BM/2.. of
+// Block = 4 waves in a 2 x 2 grid over a BM x 128 tile (launched with BM = 64); wave (wm, wn) owns rows wm*BM/2.. of
 // column block n0/64 + wn (4 column tiles of 16) and accumulates (BM/32) x 4 tiles of 16 x 16.
 // K advances 64 at a time (two MB steps): the next step's x tile (f32, scaled by 2^e while it is
 // written to LDS), weights and scales are loaded while the current step's MFMAs run.  Each lane
@@ -533,29 +533,30 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   return Q35_OK;
 }
 
-// MB path: tile BM x 128 (BM = 128 or 64) and K splits by the same estimate, at the efficiency
-// assumed for the f16 kernel (two MFMAs per product)
+// MB path: 64 x 128 tiles (64-row tiles measured faster than 128-row ones at every prompt shape:
+// their 35 KB of LDS lets three or four blocks share a CU, so a launch spreads evenly over the
+// CUs) and the K split of least estimated time.  Measured at 512 rows: a block alone on a CU takes
+// ~1.09 us per 64-row K step, and a CU holding two or more blocks retires one block-step every
+// ~0.91 us; a split adds the reduction kernel (reads every split's partials, writes y: ~4 TB/s,
+// plus a launch).
 void gemm_pick_mb(const GemmCall& c, int* bm, int* ksplit) {
-  int64_t ncat = 0, tiles128 = 0;
+  int64_t ncat = 0, tiles = 0;
   for (int i = 0; i < c.nseg; ++i) {
     ncat += c.seg[i].N;
-    tiles128 += c.seg[i].N / 128;
+    tiles += c.seg[i].N / 128;
   }
+  tiles *= (c.M + 63) / 64;
   const int cus = device_cus();
-  const double cu_flops = 2.5e15 / 2.0 / 256.0;
   double best = 1e300;
-  for (const int tbm : {128, 64}) {
-    const long long tiles = tiles128 * ((c.M + tbm - 1) / tbm);
-    const double eff = tbm == 128 ? 0.35 : 0.28;
-    for (int ks = 1; ks <= kGemmMaxSplit; ks *= 2) {
-      if (ks > 1 && (!c.part || c.part_floats < (size_t)ks * c.M * ncat || c.K / kHBK < 2 * ks)) break;
-      const int kch = ((c.K / kHBK + ks - 1) / ks) * kHBK;
-      const long long blocks = tiles * ks;
-      const double rounds = (double)((blocks + 2 * cus - 1) / (2 * cus));  // two blocks per CU
-      double cost = rounds * 2.0 * 2.0 * tbm * 128.0 * kch / (cu_flops * eff);
-      if (ks > 1) cost += (double)c.M * ncat * (ks + 1) * 4.0 / 4e12 + 3e-6;
-      if (cost < best * 0.97) { best = cost; *bm = tbm; *ksplit = ks; }
-    }
+  *bm = 64;
+  *ksplit = 1;
+  for (int ks = 1; ks <= kGemmMaxSplit; ks *= 2) {
+    if (ks > 1 && (!c.part || c.part_floats < (size_t)ks * c.M * ncat || c.K / kHBK < 2 * ks)) break;
+    const int steps = (c.K / kHBK + ks - 1) / ks;
+    const long long per_cu = (tiles * ks + cus - 1) / cus;
+    double cost = per_cu <= 1 ? steps * 1.09e-6 : (double)per_cu * steps * 0.91e-6;
+    if (ks > 1) cost += (double)c.M * ncat * (ks + 1) * 4.0 / 4e12 + 3e-6;
+    if (cost < best * 0.97) { best = cost; *ksplit = ks; }
   }
 }
 
@@ -613,9 +614,9 @@ int gemm_launch(const GemmCall& c, hipStream_t st) {
           (reinterpret_cast<uintptr_t>(s.y) & 15) || (s.ldy % 4))
         return fail(Q35_E_ALIGN, "gemm: Q35_KN_MB needs 16-byte aligned q, scales and y rows");
     }
-    int bm = 128, ks = 1;
+    int bm = 64, ks = 1;
     gemm_pick_mb(c, &bm, &ks);
-    return bm == 128 ? launch_mb<128>(c, ks, st) : launch_mb<64>(c, ks, st);
+    return launch_mb<64>(c, ks, st);
   }
   if (c.M < 1 || c.K < kBK || (c.K % 64) != 0) return fail(Q35_E_SHAPE, "gemm: M >= 1 and K a multiple of 64 required");
   if ((c.ldx % 4) != 0 || (reinterpret_cast<uintptr_t>(c.x) & 15) != 0)
