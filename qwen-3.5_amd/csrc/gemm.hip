@@ -50,6 +50,7 @@ struct GArgs {
   int32_t ksplit, kchunk, ncat;  // K splits of kchunk rows; partials part[split][M][ncat]
   float* part;
   float* amax;   // MB path: |x| maximum of each row [M]
+  int32_t prep_rows;  // MB path: rows whose maximum the prep pass finds (M, or 0 when given)
   float* spart;  // MB path: partial maxima of every segment's |scale| [kPrepS]
 };
 
@@ -262,13 +263,13 @@ constexpr int kPrepS = 64;        // blocks of the scale-maximum pass (one wave'
 
 typedef float mf4 __attribute__((ext_vector_type(4)));
 
-// Row maxima of |x| (blocks < M: one row each, every load issued before the first use) and,
-// without precomputed ones, partial maxima of every segment's |scale| (blocks M .. M + kPrepS - 1,
-// a strided share each).
+// Row maxima of |x| (blocks < prep_rows: one row each, every load issued before the first use)
+// and, without precomputed ones, partial maxima of every segment's |scale| (the next kPrepS
+// blocks, a strided share each).
 __global__ __launch_bounds__(256) void hgemm_prep_kernel(const GArgs a) {
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if ((int)blockIdx.x < a.M) {
+  if ((int)blockIdx.x < a.prep_rows) {
     const float* xr = a.x + (int64_t)blockIdx.x * a.ldx;
     float mx = 0.f;
     for (int k0 = 0; k0 < a.K; k0 += 8 * 1024) {
@@ -288,7 +289,7 @@ __global__ __launch_bounds__(256) void hgemm_prep_kernel(const GArgs a) {
     if (tid == 0) a.amax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     return;
   }
-  const int p = (int)blockIdx.x - a.M;
+  const int p = (int)blockIdx.x - a.prep_rows;
   float mx = 0.f;
 #pragma unroll
   for (int i = 0; i < kGemmMaxSeg; ++i) {
@@ -516,13 +517,15 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   a.ncat = ncat;
   a.part = c.part;
   a.nblocks = tiles * ksplit * a.mtiles;
-  a.amax = c.aux;
+  a.amax = c.amax ? const_cast<float*>(c.amax) : c.aux;
+  a.prep_rows = c.amax ? 0 : c.M;
   a.spart = c.aux + (gemm_aux_floats(c.M) - kPrepS);
   bool smax = true;
   for (int i = 0; i < c.nseg; ++i) smax = smax && c.seg[i].smax;
   if (!smax)
     for (int i = 0; i < c.nseg; ++i) a.seg[i].smax = nullptr;
-  hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)(c.M + (smax ? 0 : kPrepS))), dim3(256), 0, st, a);
+  const int prep_blocks = a.prep_rows + (smax ? 0 : kPrepS);
+  if (prep_blocks > 0) hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)prep_blocks), dim3(256), 0, st, a);
   hipLaunchKernelGGL((hgemm_kernel<BM>), dim3(a.nblocks), dim3(kGT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   if (ksplit > 1) {

@@ -333,13 +333,14 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
     const q35_model::MbLayer& W = m->mb[l];
-    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st))) return rc;
+    // the producers of the GEMM inputs write their row maxima into the GEMMs' scratch (pf_aux)
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st, m->pf_aux))) return rc;
     if (!L.full) {
       GemmCall g;
       g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
       g.seg[0] = seg(L.qkv, W.qkv, m->pf_y, LDY);
       g.seg[1] = seg(L.z, W.z, m->pf_y + conv_dim, LDY);
-      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux; g.amax = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
       if ((rc = gate_prompt_launch(m->pf_xn, H, T, H, L.w_b, L.w_a, L.a_log, L.dt_bias, nh, m->pf_bg, st))) return rc;
       GdnPrefill gp;
@@ -348,12 +349,13 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       gp.out = m->pf_core; gp.ld_out = vdim; gp.T = T; gp.nh = nh; gp.key_dim = key_dim;
       gp.nchunk = (T + kGdnChunk - 1) / kGdnChunk; gp.qscale = powf((float)d.lin_dk, -0.5f);
       if ((rc = gdn_prefill_launch(gp, st))) return rc;
-      if ((rc = gated_norm_rows_launch(m->pf_core, vdim, m->pf_y + conv_dim, LDY, L.norm_w, T, nh, d.eps, m->pf_a, vdim, st)))
+      if ((rc = gated_norm_rows_launch(m->pf_core, vdim, m->pf_y + conv_dim, LDY, L.norm_w, T, nh, d.eps, m->pf_a, vdim, st,
+                                       m->pf_aux)))
         return rc;
       GemmCall o;
       o.x = m->pf_a; o.ldx = vdim; o.M = T; o.K = vdim; o.nseg = 1; o.accumulate = 1;
       o.seg[0] = seg(L.out, W.out, m->pf_x, H);
-      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux;
+      o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux; o.amax = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     } else {
       const int qw = ah * hd * 2, kvw = kvh * hd;
@@ -362,7 +364,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       g.seg[0] = seg(L.q, W.q, m->pf_y, LDY);
       g.seg[1] = seg(L.k, W.k, m->pf_y + qw, LDY);
       g.seg[2] = seg(L.v, W.v, m->pf_y + qw + kvw, LDY);
-      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
+      g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux; g.amax = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
       AttnPrefill ap;
       ap.qg = m->pf_y; ap.ld_qg = LDY; ap.k = m->pf_y + qw; ap.v = m->pf_y + qw + kvw; ap.ld_kv = LDY;
@@ -377,18 +379,18 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     }
-    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st))) return rc;
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st, m->pf_aux))) return rc;
     GemmCall g;
     g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
     g.seg[0] = seg(L.gate, W.gate, m->pf_y, LDY);
     g.seg[1] = seg(L.up, W.up, m->pf_y + F, LDY);
-    g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux;
+    g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux; g.amax = m->pf_aux;
       if ((rc = gemm_launch(g, st))) return rc;
-    if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st))) return rc;
+    if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st, m->pf_aux))) return rc;
     GemmCall dn;
     dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
     dn.seg[0] = seg(L.down, W.down, m->pf_x, H);
-    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux;
+    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux; dn.amax = m->pf_aux;
       if ((rc = gemm_launch(dn, st))) return rc;
   }
   if ((rc = store_i32_launch(v.pos, p0 + T - 1, st))) return rc;

@@ -33,9 +33,19 @@ constexpr int kScrNv = 0, kScrKcd = kC * kDk, kScrQe = 2 * kC * kDk, kScrKd = 3 
 constexpr int kScrIntra = 4 * kC * kDk, kScrCd = kScrIntra + kC * kC;
 static_assert(kScrCd + 64 == kGdnScratchPerChunk, "scratch layout");
 
-// y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808)
+// Largest value over a 256-thread block (every thread passes one); thread 0 stores it.
+Q35_DEV void block_max256_store(float v, float* sh, float* dst) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) *dst = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+
+// y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808).  amax (optional):
+// max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.
 __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, int K, const float* w, float eps,
-                                                       float* y, int ldy) {
+                                                       float* y, int ldy, float* amax) {
   __shared__ float sh[4];
   const int m = blockIdx.x;
   const float* xr = x + (int64_t)m * ldx;
@@ -47,7 +57,13 @@ __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, 
   ss = block_sum256(ss, sh);
   const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
   float* yr = y + (int64_t)m * ldy;
-  for (int k = threadIdx.x; k < K; k += kPT) yr[k] = (xr[k] * r) * (1.0f + w[k]);
+  float mx = 0.f;
+  for (int k = threadIdx.x; k < K; k += kPT) {
+    const float v = (xr[k] * r) * (1.0f + w[k]);
+    yr[k] = v;
+    mx = fmaxf(mx, fabsf(v));
+  }
+  if (amax) block_max256_store(mx, sh, amax + m);
 }
 
 // ------------------------------------------------------------------ Gated DeltaNet, prompt
@@ -474,29 +490,45 @@ __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a
   *(float4*)(S + (int64_t)e4 * kDk + c0 + j4) = *(const float4*)&Ss[e4][j4];
 }
 
-// out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100)
+// out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100);
+// amax (optional): max |out[t]| of each row
 __global__ __launch_bounds__(kPT) void gated_norm_rows_kernel(const float* o, int ldo, const float* z, int ldz,
                                                               const float* w, int nh, float eps, float* out,
-                                                              int ldout) {
+                                                              int ldout, float* amax) {
+  __shared__ float sh[4];
   const int t = blockIdx.x, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float mx = 0.f;
   for (int h = wid; h < nh; h += 4) {
     const float* orow = o + (int64_t)t * ldo + h * kDk;
     const float* zrow = z + (int64_t)t * ldz + h * kDk;
     const float v0 = orow[lane], v1 = orow[lane + 64];
     const float r = rsqrt_f(wave_sum(v0 * v0 + v1 * v1) / (float)kDk + eps);
     float* dst = out + (int64_t)t * ldout + h * kDk;
-    dst[lane] = (w[lane] * (v0 * r)) * silu_f(zrow[lane]);
-    dst[lane + 64] = (w[lane + 64] * (v1 * r)) * silu_f(zrow[lane + 64]);
+    const float y0 = (w[lane] * (v0 * r)) * silu_f(zrow[lane]);
+    const float y1 = (w[lane + 64] * (v1 * r)) * silu_f(zrow[lane + 64]);
+    dst[lane] = y0;
+    dst[lane + 64] = y1;
+    mx = fmaxf(mx, fmaxf(fabsf(y0), fabsf(y1)));
   }
+  if (amax) block_max256_store(mx, sh, amax + t);
 }
 
-// out[t][k] = up * silu(gate): gu = [gate (F) | up (F)] per row (text_modules.rs:1000-1011)
-__global__ __launch_bounds__(kPT) void swiglu_rows_kernel(const float* gu, int ldgu, int F, float* out, int ldout) {
-  const int t = blockIdx.y;
-  for (int k = blockIdx.x * kPT + threadIdx.x; k < F; k += gridDim.x * kPT) {
-    const float* r = gu + (int64_t)t * ldgu;
-    out[(int64_t)t * ldout + k] = r[F + k] * silu_f(r[k]);
+// out[t][k] = up * silu(gate): gu = [gate (F) | up (F)] per row (text_modules.rs:1000-1011); one
+// block per row, 4 columns per thread and step; amax (optional): max |out[t]| of each row
+__global__ __launch_bounds__(kPT) void swiglu_rows_kernel(const float* gu, int ldgu, int F, float* out, int ldout,
+                                                          float* amax) {
+  __shared__ float sh[4];
+  const int t = blockIdx.x;
+  const float* r = gu + (int64_t)t * ldgu;
+  float* dst = out + (int64_t)t * ldout;
+  float mx = 0.f;
+  for (int k = 4 * threadIdx.x; k < F; k += 4 * kPT) {
+    const float4 g = *(const float4*)(r + k), u = *(const float4*)(r + F + k);
+    const float4 y = make_float4(u.x * silu_f(g.x), u.y * silu_f(g.y), u.z * silu_f(g.z), u.w * silu_f(g.w));
+    *(float4*)(dst + k) = y;
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
   }
+  if (amax) block_max256_store(mx, sh, amax + t);
 }
 
 // ------------------------------------------------------------------ attention, prompt
@@ -685,9 +717,9 @@ int store_i32_launch(int32_t* p, int32_t v, hipStream_t st) {
 }
 
 int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
-                    hipStream_t st) {
+                    hipStream_t st, float* amax) {
   if (M < 1) return Q35_OK;
-  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy);
+  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy, amax);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
@@ -716,17 +748,19 @@ int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st) {
 }
 
 int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, const float* w, int T, int nh, float eps,
-                           float* out, int ldout, hipStream_t st) {
+                           float* out, int ldout, hipStream_t st, float* amax) {
   if (T < 1) return Q35_OK;
-  hipLaunchKernelGGL(gated_norm_rows_kernel, dim3(T), dim3(kPT), 0, st, o, ldo, z, ldz, w, nh, eps, out, ldout);
+  hipLaunchKernelGGL(gated_norm_rows_kernel, dim3(T), dim3(kPT), 0, st, o, ldo, z, ldz, w, nh, eps, out, ldout, amax);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
 
-int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st) {
+int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st, float* amax) {
   if (T < 1) return Q35_OK;
-  const int gx = std::min((F + kPT - 1) / kPT, 8);
-  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(gx, T), dim3(kPT), 0, st, gu, ldgu, F, out, ldout);
+  if ((F % 4) != 0 || (ldgu % 4) != 0 || (ldout % 4) != 0 || (reinterpret_cast<uintptr_t>(gu) & 15) ||
+      (reinterpret_cast<uintptr_t>(out) & 15))
+    return fail(Q35_E_ALIGN, "swiglu_rows: 16-byte aligned rows and F a multiple of 4 required");
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(T), dim3(kPT), 0, st, gu, ldgu, F, out, ldout, amax);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -443,6 +443,8 @@ struct GemmCall {
   size_t part_floats = 0;
   // Q35_KN_MB launches (every segment MB): kGemmAuxFloats(M) floats for the row and scale maxima
   float* aux = nullptr;
+  // Q35_KN_MB: max |x| of each row [M] when the producer of x has computed it (skips that pass)
+  const float* amax = nullptr;
 };
 // Scratch floats of an MB launch: row maxima [M] and scale partial maxima [64], 64-aligned.
 inline size_t gemm_aux_floats(int M) { return ((size_t)M + 63) / 64 * 64 + 64; }
@@ -599,7 +601,7 @@ int mb_scale_transpose_launch(const float* s, int32_t V, int32_t K, float* sT, h
 int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);
 // y[m] = RMSNorm(x[m]) * (1 + w) for M rows of K
 int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
-                    hipStream_t st);
+                    hipStream_t st, float* amax = nullptr);
 // [beta | g] rows of a prompt (x [T][ldx], softplus identity branch when its input exceeds 20)
 int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, const float* wa, const float* alog,
                        const float* dtb, int nh, float* out, hipStream_t st);
@@ -622,9 +624,9 @@ struct GdnPrefill {
 int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st);
 // out[t][h*128 + i] = (w[i] * (o * rsqrt(mean(o^2) + eps))) * silu(z), per 128-wide head
 int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, const float* w, int T, int nh, float eps,
-                           float* out, int ldout, hipStream_t st);
+                           float* out, int ldout, hipStream_t st, float* amax = nullptr);
 // out[t][k] = gu[t][F + k] * silu(gu[t][k])
-int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st);
+int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st, float* amax = nullptr);
 // Attention over a prompt of T tokens at positions p0..p0+T-1 (head_dim 256, one sequence).
 constexpr int kHdP = 256;
 struct AttnPrefill {
