@@ -358,20 +358,35 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
   }
 }
 
-// 512 threads: the two halves of the block split each product's k range (v_new, q_e S) and add
-// their halves in a fixed order, so every chain of dependent FMAs is half as long.
+// The chunk recurrence on the f32 matrix cores (v_mfma_f32_16x16x4_f32: f32 products, f32
+// accumulation, like the reference's f32 matmuls).  Block = one head's 16-column slice of the value
+// dimension, 8 waves.  Per chunk:
+//   v_new = new_values - k_cumdecay S    (wave: 16 chunk rows x half of the 128 key rows)
+//   S'    = S e^cum_last + k_d^T v_new    (wave: 16 key rows)          } concurrently: S' goes to
+//   out   = q_e S + intra v_new          (wave: 16 chunk rows x half)  } the other state buffer
+// The halves of each key-row sum are added as (lower + upper), then the intra-chunk term, in a fixed
+// order.  Each lane takes 4 consecutive k of its operand rows as one 16-byte LDS read and feeds them
+// to 4 MFMAs (k = 4 g + m in step m), the same k order on both operands, so the products summed are
+// exactly those of the plain sum.  The state slice lives in LDS transposed ([column][key row]) so
+// that these reads are contiguous.  The next chunk's inputs are loaded into registers while a chunk
+// is computed.
 constexpr int kST = 512;
+constexpr int kStLd = kDk + 4;  // transposed state rows (key rows contiguous)
+constexpr int kInLd = kC + 4;   // intra matrix / transposed v_new rows
+typedef float mfma_f4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a) {
-  __shared__ __align__(16) float Ss[kDk][kSl];
+  __shared__ __align__(16) float St[2][kSl][kStLd];
   __shared__ __align__(16) float Kc[kC][kLdq];
   __shared__ __align__(16) float Qe[kC][kLdq];
   __shared__ __align__(16) float Kd[kC][kLdq];
-  __shared__ float In[kC][kC + 1];
-  __shared__ __align__(16) float Vn[kC][kSl];
-  __shared__ __align__(16) float Red[kC][kSl];  // the upper half's partial sums
+  __shared__ __align__(16) float In[kC][kInLd];
+  __shared__ __align__(16) float Vn0[kC][kSl];     // new values (before the state term)
+  __shared__ __align__(16) float VnT[kSl][kInLd];  // v_new, transposed
+  __shared__ __align__(16) mfma_f4 RedV[4][64];    // upper halves' v_new partials
+  __shared__ __align__(16) mfma_f4 RedO[4][64];    // upper halves' output partials
   __shared__ float cdv;
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c16 = l & 15, g = l >> 4;
   const int sl = blockIdx.x % kNsl, h = blockIdx.x / kNsl;
   const int c0 = sl * kSl;
   float* S = a.S + (int64_t)h * kDk * kDk;
@@ -393,101 +408,120 @@ __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a
   }
   // thread (e4 = tid / 4, j4 = 4 (tid % 4)): S rows e4, columns j4..j4+3 of the slice
   const int e4 = tid >> 2, j4 = (tid & 3) * 4;
-  *(float4*)&Ss[e4][j4] = *(const float4*)(S + (int64_t)e4 * kDk + c0 + j4);
+  {
+    const float4 v = *(const float4*)(S + (int64_t)e4 * kDk + c0 + j4);
+    St[0][j4][e4] = v.x; St[0][j4 + 1][e4] = v.y; St[0][j4 + 2][e4] = v.z; St[0][j4 + 3][e4] = v.w;
+  }
   constexpr int kLd4 = kC * kDk / 4 / kST;   // float4 per thread per 64 x 128 matrix (4)
   constexpr int kLdIn = kC * kC / 4 / kST;   // float4 per thread of the intra matrix (2)
-  const int hf = tid >> 8, i = (tid & 255) >> 2, j = (tid & 3) * 4;  // half, row, 4 columns
-  for (int c = 0; c < a.nchunk; ++c) {
+  const int rt = w & 3, kh = w >> 2;          // chunk-row tile and key-row half of the wave
+  q35_f32x4 vkc[kLd4], vqe[kLd4], vkd[kLd4], vin[kLdIn], vnv;
+  float vcd;
+  const int vr = (tid & 255) >> 2;  // (the lower half stores the new values)
+  auto load_chunk = [&](int c) {
     const float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
-    {  // every load of the chunk is issued before any is stored (one round trip per chunk)
-      float4 vkc[kLd4], vqe[kLd4], vkd[kLd4], vin[kLdIn];
-#pragma unroll
-      for (int u = 0; u < kLd4; ++u) {
-        const int e = tid + u * kST;
-        vkc[u] = *(const float4*)(scr + kScrKcd + 4 * e);
-        vqe[u] = *(const float4*)(scr + kScrQe + 4 * e);
-        vkd[u] = *(const float4*)(scr + kScrKd + 4 * e);
-      }
-#pragma unroll
-      for (int u = 0; u < kLdIn; ++u) vin[u] = *(const float4*)(scr + kScrIntra + 4 * (tid + u * kST));
-      const int vr = (tid & 255) >> 2;  // (the lower half loads the new values)
-      const float4 vnv = *(const float4*)(scr + kScrNv + vr * kDk + c0 + (tid & 3) * 4);
-      const float vcd = scr[kScrCd];
-#pragma unroll
-      for (int u = 0; u < kLd4; ++u) {
-        const int e = tid + u * kST, r = e >> 5, d = (e & 31) * 4;
-        *(float4*)&Kc[r][d] = vkc[u];
-        *(float4*)&Qe[r][d] = vqe[u];
-        *(float4*)&Kd[r][d] = vkd[u];
-      }
-#pragma unroll
-      for (int u = 0; u < kLdIn; ++u) {
-        const int e = 4 * (tid + u * kST), r = e >> 6, q = e & 63;
-        In[r][q] = vin[u].x; In[r][q + 1] = vin[u].y; In[r][q + 2] = vin[u].z; In[r][q + 3] = vin[u].w;
-      }
-      if (hf == 0) *(float4*)&Vn[vr][(tid & 3) * 4] = vnv;
-      if (tid == 0) cdv = vcd;
-    }
+    static_for<kLd4>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int e = tid + u * kST;
+      vkc[u] = *(const q35_f32x4*)(scr + kScrKcd + 4 * e);
+      vqe[u] = *(const q35_f32x4*)(scr + kScrQe + 4 * e);
+      vkd[u] = *(const q35_f32x4*)(scr + kScrKd + 4 * e);
+    });
+    static_for<kLdIn>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      vin[u] = *(const q35_f32x4*)(scr + kScrIntra + 4 * (tid + u * kST));
+    });
+    vnv = *(const q35_f32x4*)(scr + kScrNv + vr * kDk + c0 + (tid & 3) * 4);
+    vcd = scr[kScrCd];
+  };
+  load_chunk(0);
+  int cur = 0;
+  for (int c = 0; c < a.nchunk; ++c) {
+    static_for<kLd4>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int e = tid + u * kST, r = e >> 5, d = (e & 31) * 4;
+      *(q35_f32x4*)&Kc[r][d] = vkc[u];
+      *(q35_f32x4*)&Qe[r][d] = vqe[u];
+      *(q35_f32x4*)&Kd[r][d] = vkd[u];
+    });
+    static_for<kLdIn>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int e = 4 * (tid + u * kST), r = e >> 6, q = e & 63;
+      *(q35_f32x4*)&In[r][q] = vin[u];
+    });
+    if (tid < 256) *(q35_f32x4*)&Vn0[vr][(tid & 3) * 4] = vnv;
+    if (tid == 0) cdv = vcd;
     __syncthreads();
-    {  // v_new = new_values - k_cumdecay S: half hf sums e in [64 hf, 64 hf + 64)
-      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-      const int eb = 64 * hf;
-      for (int e = eb; e < eb + 64; ++e) {
-        const float k = Kc[i][e];
-        const float4 sv = *(const float4*)&Ss[e][j];
-        s0 += k * sv.x; s1 += k * sv.y; s2 += k * sv.z; s3 += k * sv.w;
+    if (c + 1 < a.nchunk) load_chunk(c + 1);
+
+    // v_new: rows 16 rt + 4 g + r, column c16; key rows [64 kh, 64 kh + 64)
+    {
+      mfma_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int e0 = 64 * kh + 16 * kk + 4 * g;
+        const mfma_f4 av = *(const mfma_f4*)&Kc[16 * rt + c16][e0];
+        const mfma_f4 bv = *(const mfma_f4*)&St[cur][c16][e0];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], acc, 0, 0, 0);
       }
-      if (hf == 1) *(float4*)&Red[i][j] = make_float4(s0, s1, s2, s3);
+      if (kh == 1) RedV[rt][l] = acc;
       __syncthreads();
-      if (hf == 0) {
-        const float4 r = *(const float4*)&Red[i][j];
-        float4 nv = *(const float4*)&Vn[i][j];
-        nv.x -= s0 + r.x; nv.y -= s1 + r.y; nv.z -= s2 + r.z; nv.w -= s3 + r.w;
-        *(float4*)&Vn[i][j] = nv;
+      if (kh == 0) {
+        const mfma_f4 up = RedV[rt][l];
+        mfma_f4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = Vn0[16 * rt + 4 * g + r][c16] - (acc[r] + up[r]);
+        *(mfma_f4*)&VnT[c16][16 * rt + 4 * g] = v;
       }
+      __syncthreads();
     }
-    __syncthreads();
-    {  // out = q_e S + intra v_new: the upper half takes e in [64, 128), the lower half e in
-       // [0, 64) and the intra-chunk sum; added as (lower + upper) + intra
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-      const int eb = 64 * hf;
-      for (int e = eb; e < eb + 64; ++e) {
-        const float q = Qe[i][e];
-        const float4 sv = *(const float4*)&Ss[e][j];
-        o0 += q * sv.x; o1 += q * sv.y; o2 += q * sv.z; o3 += q * sv.w;
+    // S' rows 16 w + 4 g + r (column c16) into the other buffer; out partials of (rt, kh)
+    {
+      const float cd = cdv;
+      mfma_f4 sacc = *(const mfma_f4*)&St[cur][c16][16 * w + 4 * g] * cd;
+#pragma unroll
+      for (int lb = 0; lb < 4; ++lb) {
+        const mfma_f4 bv = *(const mfma_f4*)&VnT[c16][16 * lb + 4 * g];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(Kd[16 * lb + 4 * g + m][16 * w + c16], bv[m], sacc, 0, 0, 0);
       }
-      if (hf == 1) *(float4*)&Red[i][j] = make_float4(o0, o1, o2, o3);
-      float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-      if (hf == 0) {
-        for (int l = 0; l <= i; ++l) {
-          const float w = In[i][l];
-          const float4 v = *(const float4*)&Vn[l][j];
-          p0 += w * v.x; p1 += w * v.y; p2 += w * v.z; p3 += w * v.w;
+      mfma_f4 oacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int e0 = 64 * kh + 16 * kk + 4 * g;
+        const mfma_f4 av = *(const mfma_f4*)&Qe[16 * rt + c16][e0];
+        const mfma_f4 bv = *(const mfma_f4*)&St[cur][c16][e0];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) oacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], oacc, 0, 0, 0);
+      }
+      mfma_f4 pacc = {0.f, 0.f, 0.f, 0.f};
+      if (kh == 0) {
+        for (int lb = 0; lb <= rt; ++lb) {  // (the intra matrix is zero past the diagonal)
+          const mfma_f4 av = *(const mfma_f4*)&In[16 * rt + c16][16 * lb + 4 * g];
+          const mfma_f4 bv = *(const mfma_f4*)&VnT[c16][16 * lb + 4 * g];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], pacc, 0, 0, 0);
         }
       }
+      *(mfma_f4*)&St[cur ^ 1][c16][16 * w + 4 * g] = sacc;
+      if (kh == 1) RedO[rt][l] = oacc;
       __syncthreads();
-      if (hf == 0) {
-        const float4 r = *(const float4*)&Red[i][j];
-        const int t = c * kC + i;
-        if (t < a.T)
-          *(float4*)(a.out + (int64_t)t * a.ld_out + h * kDk + c0 + j) =
-              make_float4((o0 + r.x) + p0, (o1 + r.y) + p1, (o2 + r.z) + p2, (o3 + r.w) + p3);
+      if (kh == 0) {
+        const mfma_f4 up = RedO[rt][l];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = c * kC + 16 * rt + 4 * g + r;
+          if (t < a.T) a.out[(int64_t)t * a.ld_out + h * kDk + c0 + c16] = (oacc[r] + up[r]) + pacc[r];
+        }
       }
     }
-    {  // S = S e^cum_last + k_d^T v_new: thread (e4, j4), all 64 rows of the chunk
-      const float cd = cdv;
-      float s0 = Ss[e4][j4] * cd, s1 = Ss[e4][j4 + 1] * cd, s2 = Ss[e4][j4 + 2] * cd, s3 = Ss[e4][j4 + 3] * cd;
-      for (int l = 0; l < kC; ++l) {
-        const float k = Kd[l][e4];
-        const float4 v = *(const float4*)&Vn[l][j4];
-        s0 += k * v.x; s1 += k * v.y; s2 += k * v.z; s3 += k * v.w;
-      }
-      __syncthreads();  // every read of S and Vn of this chunk is done
-      *(float4*)&Ss[e4][j4] = make_float4(s0, s1, s2, s3);
-    }
-    __syncthreads();
+    __syncthreads();  // every read of this chunk's inputs and of St[cur] is done
+    cur ^= 1;
   }
-  *(float4*)(S + (int64_t)e4 * kDk + c0 + j4) = *(const float4*)&Ss[e4][j4];
+  *(float4*)(S + (int64_t)e4 * kDk + c0 + j4) =
+      make_float4(St[cur][j4][e4], St[cur][j4 + 1][e4], St[cur][j4 + 2][e4], St[cur][j4 + 3][e4]);
 }
 
 // out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100);
