@@ -32,6 +32,19 @@ constexpr int kNsl = kDk / kSl;   // 8 slices per head
 constexpr int kScrNv = 0, kScrKcd = kC * kDk, kScrQe = 2 * kC * kDk, kScrKd = 3 * kC * kDk;
 constexpr int kScrIntra = 4 * kC * kDk, kScrCd = kScrIntra + kC * kC;
 static_assert(kScrCd + 64 == kGdnScratchPerChunk, "scratch layout");
+// Element order of the scratch matrices: the state pass reads them as MFMA operands, each lane
+// l = 16 g + c16 of a wave taking 4 consecutive k as one float4, so they are stored lane-major
+// (every load of a wave is 1 KB contiguous).  k_cumdecay and q_e [row i][key e]: wave tile (i/16,
+// e/64), step (e/16) % 4, lane (g = (e/4) % 4, c16 = i % 16), k = e % 4.  k_d [row l][key e], read
+// as k_d^T: wave e/16, step l/16, lane (g = (l/4) % 4, c16 = e % 16), k = l % 4.  intra [i][j]:
+// tile i/16, step j/16, lane (g = (j/4) % 4, c16 = i % 16), k = j % 4.  New values [i][column d]
+// (an output-tile operand): slice d/16, tile i/16, lane (g = (i/4) % 4, c16 = d % 16), r = i % 4.
+Q35_DEV int scr_a(int i, int e) {
+  return ((((i >> 4) * 2 + (e >> 6)) * 4 + ((e >> 4) & 3)) * 64 + ((e >> 2) & 3) * 16 + (i & 15)) * 4 + (e & 3);
+}
+Q35_DEV int scr_kd(int l, int e) { return (((e >> 4) * 4 + (l >> 4)) * 64 + ((l >> 2) & 3) * 16 + (e & 15)) * 4 + (l & 3); }
+Q35_DEV int scr_in(int i, int j) { return (((i >> 4) * 4 + (j >> 4)) * 64 + ((j >> 2) & 3) * 16 + (i & 15)) * 4 + (j & 3); }
+Q35_DEV int scr_nv(int i, int d) { return (((d >> 4) * 4 + (i >> 4)) * 64 + ((i >> 2) & 3) * 16 + (d & 15)) * 4 + (i & 3); }
 
 // Largest value over a 256-thread block (every thread passes one); thread 0 stores it.
 Q35_DEV void block_max256_store(float v, float* sh, float* dst) {
@@ -282,9 +295,9 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
   __syncthreads();
   // N = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i; intra = (q_i.k_j) e^(cum_i - cum_j) for j <= i
   float* intra = scr + kScrIntra;
-  for (int e = tid; e < kC * kC; e += kPP) {  // the blocks of 4 columns past the diagonal block
-    const int i = e >> 6, j = e & 63;
-    if ((j >> 2) > (i >> 2)) intra[e] = 0.f;
+  for (int e = tid; e < kC * kC / 4; e += kPP) {  // the blocks of 4 columns past the diagonal block
+    const int i = e >> 4, j = (e & 15) * 4;
+    if ((j >> 2) > (i >> 2)) *(float4*)(intra + scr_in(i, j)) = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int k = tid; k < kTriTasks; k += kPP) {
     int i, jg;
@@ -301,13 +314,24 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
         dqk[u] += ((qi.x * kj.x + qi.y * kj.y) + qi.z * kj.z) + qi.w * kj.w;
       }
     }
+    float iv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int j = j0 + u;
       const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
       if (j < i) U[i][j] = -((bet[i] * dkk[u]) * dec);
-      intra[i * kC + j] = j <= i ? dqk[u] * dec : 0.f;
+      iv[u] = j <= i ? dqk[u] * dec : 0.f;
     }
+    *(float4*)(intra + scr_in(i, j0)) = make_float4(iv[0], iv[1], iv[2], iv[3]);
+  }
+  // k_d = k e^(cum_last - cum): 4 chunk rows of one key per float4 of its lane-major layout
+  for (int e = tid; e < kC * kDk / 4; e += kPP) {
+    const int w = e >> 8, lb = (e >> 6) & 3, ln = e & 63, g = ln >> 4, c16 = ln & 15;
+    const int l = 16 * lb + 4 * g, k = 16 * w + c16;
+    float kv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kv[m] = Ks[l + m][k] * expf(cum[kC - 1] - cum[l + m]);
+    *(float4*)(scr + kScrKd + scr_kd(l, k)) = make_float4(kv[0], kv[1], kv[2], kv[3]);
   }
   __syncthreads();
   tri_inverse(U, Tm);
@@ -339,19 +363,15 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
           ak[d] += ube * k.x; ak[d + 1] += ube * k.y; ak[d + 2] += ube * k.z; ak[d + 3] += ube * k.w;
         }
       }
-      const float eq = ecum[i], ek = expf(cum[kC - 1] - cum[i]);
-      float* nv = scr + kScrNv + i * kDk + d0;
-      float* kcd = scr + kScrKcd + i * kDk + d0;
-      float* qe = scr + kScrQe + i * kDk + d0;
-      float* kd = scr + kScrKd + i * kDk + d0;
+      const float eq = ecum[i];
 #pragma unroll
       for (int d = 0; d < 8; d += 4) {
-        *(float4*)(nv + d) = make_float4(an[d], an[d + 1], an[d + 2], an[d + 3]);
-        *(float4*)(kcd + d) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
-        const float4 q = *(const float4*)&Qs[i][d0 + d];
-        const float4 k = *(const float4*)&Ks[i][d0 + d];
-        *(float4*)(qe + d) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
-        *(float4*)(kd + d) = make_float4(k.x * ek, k.y * ek, k.z * ek, k.w * ek);
+        const int e = d0 + d;
+        *(float4*)(scr + kScrKcd + scr_a(i, e)) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
+        const float4 q = *(const float4*)&Qs[i][e];
+        *(float4*)(scr + kScrQe + scr_a(i, e)) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) scr[kScrNv + scr_nv(i, e + u)] = an[d + u];
       }
     }
     if (tid == 0) scr[kScrCd] = ecum[kC - 1];
@@ -365,26 +385,28 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
 //   S'    = S e^cum_last + k_d^T v_new    (wave: 16 key rows)          } concurrently: S' goes to
 //   out   = q_e S + intra v_new          (wave: 16 chunk rows x half)  } the other state buffer
 // The halves of each key-row sum are added as (lower + upper), then the intra-chunk term, in a fixed
-// order.  Each lane takes 4 consecutive k of its operand rows as one 16-byte LDS read and feeds them
-// to 4 MFMAs (k = 4 g + m in step m), the same k order on both operands, so the products summed are
-// exactly those of the plain sum.  The state slice lives in LDS transposed ([column][key row]) so
-// that these reads are contiguous.  The next chunk's inputs are loaded into registers while a chunk
-// is computed.
+// order.  Each lane takes 4 consecutive k of its operand rows and feeds them to 4 MFMAs (k = 4 g + m
+// in step m), the same k order on both operands, so the products summed are exactly those of the
+// plain sum.  Every k_cumdecay / q_e / k_d / intra / new-value element is used by one wave only, so
+// the waves load theirs straight into registers (the next chunk's while the current one is
+// computed); only the state slice (transposed, [column][key row], double-buffered) and v_new
+// (transposed) are shared through LDS.  Three barriers per chunk.
 constexpr int kST = 512;
 constexpr int kStLd = kDk + 4;  // transposed state rows (key rows contiguous)
-constexpr int kInLd = kC + 4;   // intra matrix / transposed v_new rows
+constexpr int kInLd = kC + 4;   // transposed v_new rows
 typedef float mfma_f4 __attribute__((ext_vector_type(4)));
+struct StateOps {  // one wave's operands of one chunk, in MFMA layout
+  mfma_f4 ka[4], qa[4], ia[4];  // k_cumdecay / q_e rows 16 rt + c16, keys 64 kh + 16 kk + 4 g + m;
+                                // intra rows 16 rt + c16, columns 16 lb + 4 g + m
+  float kd[4][4];               // k_d[16 lb + 4 g + m][16 w + c16]
+  float vn0[4];                 // new values [16 rt + 4 g + r][c0 + c16]
+  float cd;
+};
 __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float St[2][kSl][kStLd];
-  __shared__ __align__(16) float Kc[kC][kLdq];
-  __shared__ __align__(16) float Qe[kC][kLdq];
-  __shared__ __align__(16) float Kd[kC][kLdq];
-  __shared__ __align__(16) float In[kC][kInLd];
-  __shared__ __align__(16) float Vn0[kC][kSl];     // new values (before the state term)
   __shared__ __align__(16) float VnT[kSl][kInLd];  // v_new, transposed
   __shared__ __align__(16) mfma_f4 RedV[4][64];    // upper halves' v_new partials
   __shared__ __align__(16) mfma_f4 RedO[4][64];    // upper halves' output partials
-  __shared__ float cdv;
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c16 = l & 15, g = l >> 4;
   const int sl = blockIdx.x % kNsl, h = blockIdx.x / kNsl;
@@ -412,58 +434,41 @@ __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a
     const float4 v = *(const float4*)(S + (int64_t)e4 * kDk + c0 + j4);
     St[0][j4][e4] = v.x; St[0][j4 + 1][e4] = v.y; St[0][j4 + 2][e4] = v.z; St[0][j4 + 3][e4] = v.w;
   }
-  constexpr int kLd4 = kC * kDk / 4 / kST;   // float4 per thread per 64 x 128 matrix (4)
-  constexpr int kLdIn = kC * kC / 4 / kST;   // float4 per thread of the intra matrix (2)
-  const int rt = w & 3, kh = w >> 2;          // chunk-row tile and key-row half of the wave
-  q35_f32x4 vkc[kLd4], vqe[kLd4], vkd[kLd4], vin[kLdIn], vnv;
-  float vcd;
-  const int vr = (tid & 255) >> 2;  // (the lower half stores the new values)
-  auto load_chunk = [&](int c) {
+  const int rt = w & 3, kh = w >> 2;  // chunk-row tile and key-row half of the wave
+  auto load_ops = [&](int c, StateOps& o) {
     const float* scr = a.scr + ((int64_t)h * a.nchunk + c) * kGdnScratchPerChunk;
-    static_for<kLd4>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      const int e = tid + u * kST;
-      vkc[u] = *(const q35_f32x4*)(scr + kScrKcd + 4 * e);
-      vqe[u] = *(const q35_f32x4*)(scr + kScrQe + 4 * e);
-      vkd[u] = *(const q35_f32x4*)(scr + kScrKd + 4 * e);
-    });
-    static_for<kLdIn>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      vin[u] = *(const q35_f32x4*)(scr + kScrIntra + 4 * (tid + u * kST));
-    });
-    vnv = *(const q35_f32x4*)(scr + kScrNv + vr * kDk + c0 + (tid & 3) * 4);
-    vcd = scr[kScrCd];
+    const float* kr = scr + kScrKcd + (rt * 2 + kh) * 4 * 256 + 4 * l;
+    const float* qr = scr + kScrQe + (rt * 2 + kh) * 4 * 256 + 4 * l;
+    const float* ir = scr + kScrIntra + rt * 4 * 256 + 4 * l;
+    const float* dr = scr + kScrKd + w * 4 * 256 + 4 * l;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      o.ka[kk] = *(const mfma_f4*)(kr + 256 * kk);
+      o.qa[kk] = *(const mfma_f4*)(qr + 256 * kk);
+      o.ia[kk] = *(const mfma_f4*)(ir + 256 * kk);
+      const mfma_f4 dv = *(const mfma_f4*)(dr + 256 * kk);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) o.kd[kk][m] = dv[m];
+    }
+    const mfma_f4 nv = *(const mfma_f4*)(scr + kScrNv + (sl * 4 + rt) * 256 + 4 * l);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o.vn0[r] = nv[r];
+    o.cd = scr[kScrCd];
   };
-  load_chunk(0);
-  int cur = 0;
+  StateOps cur, nxt;
+  load_ops(0, cur);
+  __syncthreads();
+  int sb = 0;  // state buffer of the current chunk
   for (int c = 0; c < a.nchunk; ++c) {
-    static_for<kLd4>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      const int e = tid + u * kST, r = e >> 5, d = (e & 31) * 4;
-      *(q35_f32x4*)&Kc[r][d] = vkc[u];
-      *(q35_f32x4*)&Qe[r][d] = vqe[u];
-      *(q35_f32x4*)&Kd[r][d] = vkd[u];
-    });
-    static_for<kLdIn>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      const int e = 4 * (tid + u * kST), r = e >> 6, q = e & 63;
-      *(q35_f32x4*)&In[r][q] = vin[u];
-    });
-    if (tid < 256) *(q35_f32x4*)&Vn0[vr][(tid & 3) * 4] = vnv;
-    if (tid == 0) cdv = vcd;
-    __syncthreads();
-    if (c + 1 < a.nchunk) load_chunk(c + 1);
-
+    if (c + 1 < a.nchunk) load_ops(c + 1, nxt);
     // v_new: rows 16 rt + 4 g + r, column c16; key rows [64 kh, 64 kh + 64)
     {
       mfma_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int e0 = 64 * kh + 16 * kk + 4 * g;
-        const mfma_f4 av = *(const mfma_f4*)&Kc[16 * rt + c16][e0];
-        const mfma_f4 bv = *(const mfma_f4*)&St[cur][c16][e0];
+        const mfma_f4 bv = *(const mfma_f4*)&St[sb][c16][64 * kh + 16 * kk + 4 * g];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], acc, 0, 0, 0);
+        for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.ka[kk][m], bv[m], acc, 0, 0, 0);
       }
       if (kh == 1) RedV[rt][l] = acc;
       __syncthreads();
@@ -471,41 +476,38 @@ __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a
         const mfma_f4 up = RedV[rt][l];
         mfma_f4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = Vn0[16 * rt + 4 * g + r][c16] - (acc[r] + up[r]);
+        for (int r = 0; r < 4; ++r) v[r] = cur.vn0[r] - (acc[r] + up[r]);
         *(mfma_f4*)&VnT[c16][16 * rt + 4 * g] = v;
       }
       __syncthreads();
     }
     // S' rows 16 w + 4 g + r (column c16) into the other buffer; out partials of (rt, kh)
     {
-      const float cd = cdv;
-      mfma_f4 sacc = *(const mfma_f4*)&St[cur][c16][16 * w + 4 * g] * cd;
+      mfma_f4 sacc = *(const mfma_f4*)&St[sb][c16][16 * w + 4 * g] * cur.cd;
 #pragma unroll
       for (int lb = 0; lb < 4; ++lb) {
         const mfma_f4 bv = *(const mfma_f4*)&VnT[c16][16 * lb + 4 * g];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(Kd[16 * lb + 4 * g + m][16 * w + c16], bv[m], sacc, 0, 0, 0);
+        for (int m = 0; m < 4; ++m) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.kd[lb][m], bv[m], sacc, 0, 0, 0);
       }
       mfma_f4 oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int e0 = 64 * kh + 16 * kk + 4 * g;
-        const mfma_f4 av = *(const mfma_f4*)&Qe[16 * rt + c16][e0];
-        const mfma_f4 bv = *(const mfma_f4*)&St[cur][c16][e0];
+        const mfma_f4 bv = *(const mfma_f4*)&St[sb][c16][64 * kh + 16 * kk + 4 * g];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) oacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], oacc, 0, 0, 0);
+        for (int m = 0; m < 4; ++m) oacc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.qa[kk][m], bv[m], oacc, 0, 0, 0);
       }
       mfma_f4 pacc = {0.f, 0.f, 0.f, 0.f};
       if (kh == 0) {
-        for (int lb = 0; lb <= rt; ++lb) {  // (the intra matrix is zero past the diagonal)
-          const mfma_f4 av = *(const mfma_f4*)&In[16 * rt + c16][16 * lb + 4 * g];
+#pragma unroll
+        for (int lb = 0; lb < 4; ++lb) {
+          if (lb > rt) break;  // (the intra matrix is zero past the diagonal)
           const mfma_f4 bv = *(const mfma_f4*)&VnT[c16][16 * lb + 4 * g];
 #pragma unroll
-          for (int m = 0; m < 4; ++m) pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[m], bv[m], pacc, 0, 0, 0);
+          for (int m = 0; m < 4; ++m) pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.ia[lb][m], bv[m], pacc, 0, 0, 0);
         }
       }
-      *(mfma_f4*)&St[cur ^ 1][c16][16 * w + 4 * g] = sacc;
+      *(mfma_f4*)&St[sb ^ 1][c16][16 * w + 4 * g] = sacc;
       if (kh == 1) RedO[rt][l] = oacc;
       __syncthreads();
       if (kh == 0) {
@@ -517,11 +519,14 @@ __global__ __launch_bounds__(kST) void gdn_chunk_state_kernel(const GdnPrefill a
         }
       }
     }
-    __syncthreads();  // every read of this chunk's inputs and of St[cur] is done
-    cur ^= 1;
+    // (no barrier here: the next chunk writes VnT, RedV, RedO and St[sb] only after barriers that
+    // every read of them in this chunk precedes)
+    cur = nxt;
+    sb ^= 1;
   }
+  __syncthreads();
   *(float4*)(S + (int64_t)e4 * kDk + c0 + j4) =
-      make_float4(St[cur][j4][e4], St[cur][j4 + 1][e4], St[cur][j4 + 2][e4], St[cur][j4 + 3][e4]);
+      make_float4(St[sb][j4][e4], St[sb][j4 + 1][e4], St[sb][j4 + 2][e4], St[sb][j4 + 3][e4]);
 }
 
 // out[t][h*G + i] = (w[i] * (o * rsqrt(mean_h(o^2) + eps))) * silu(z)  (text_modules.rs:91-100);
