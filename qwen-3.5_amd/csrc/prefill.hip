@@ -154,18 +154,6 @@ __global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ld
   }
 }
 
-// Tasks of the lower-triangle products: (row i, 4 columns 4 jg .. 4 jg + 3) for 4 jg <= i; rows
-// 4b .. 4b + 3 have b + 1 tasks each, 544 in all.
-constexpr int kTriTasks = 544;
-Q35_DEV void tri_task(int k, int* i, int* jg) {
-  int b = (int)((sqrtf(2.0f * (float)k + 1.0f) - 1.0f) * 0.5f);
-  while (2 * (b + 1) * (b + 2) <= k) ++b;
-  while (2 * b * (b + 1) > k) --b;
-  const int r = k - 2 * b * (b + 1);
-  *i = 4 * b + r / (b + 1);
-  *jg = r % (b + 1);
-}
-
 // X = (I - N)^-1 for N strictly lower 64 x 64 in U (in place: U ends as X minus its unit
 // diagonal), by blocks: each wave inverts a 16 x 16 diagonal block by forward substitution
 // (the reference's row recurrence, text_modules.rs:282-290, on that block), then
@@ -221,6 +209,7 @@ Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
   __syncthreads();
 }
 
+typedef float mfma_f4 __attribute__((ext_vector_type(4)));
 constexpr int kPP = 512;  // threads of the prep pass
 __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float Qs[kC][kLdq];
@@ -293,36 +282,41 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
     ecum[lane] = expf(v);
   }
   __syncthreads();
-  // N = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i; intra = (q_i.k_j) e^(cum_i - cum_j) for j <= i
+  // N = -(beta_i k_i.k_j) e^(cum_i - cum_j) for j < i; intra = (q_i.k_j) e^(cum_i - cum_j) for j <= i:
+  // the 10 16 x 16 tiles on and below the diagonal of K K^T and Q K^T on the f32 matrix cores (a
+  // wave per tile; lane l = 16 g + c16 feeds keys 16 kk + 4 g + m to step m of both operands), the 6
+  // tiles above it zero
   float* intra = scr + kScrIntra;
-  for (int e = tid; e < kC * kC / 4; e += kPP) {  // the blocks of 4 columns past the diagonal block
-    const int i = e >> 4, j = (e & 15) * 4;
-    if ((j >> 2) > (i >> 2)) *(float4*)(intra + scr_in(i, j)) = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  for (int k = tid; k < kTriTasks; k += kPP) {
-    int i, jg;
-    tri_task(k, &i, &jg);
-    const int j0 = 4 * jg;
-    float dkk[4] = {0.f, 0.f, 0.f, 0.f}, dqk[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int e = 0; e < kDk; e += 4) {
-      const float4 ki = *(const float4*)&Ks[i][e];
-      const float4 qi = *(const float4*)&Qs[i][e];
+  {
+    const int g = lane >> 4, c16 = lane & 15;
+    for (int e = tid; e < 6 * 64; e += kPP) {
+      const int t = e >> 6, ti = t < 3 ? 0 : (t < 5 ? 1 : 2), tj = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+      *(float4*)(intra + ((ti * 4 + tj) * 64 + (e & 63)) * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int tt = wid; tt < 10; tt += kPP / 64) {
+      const int ti = tt >= 6 ? 3 : (tt >= 3 ? 2 : (tt >= 1 ? 1 : 0)), tj = tt - ti * (ti + 1) / 2;
+      mfma_f4 gk = {0.f, 0.f, 0.f, 0.f}, gq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float4 kj = *(const float4*)&Ks[j0 + u][e];
-        dkk[u] += ((ki.x * kj.x + ki.y * kj.y) + ki.z * kj.z) + ki.w * kj.w;
-        dqk[u] += ((qi.x * kj.x + qi.y * kj.y) + qi.z * kj.z) + qi.w * kj.w;
+      for (int kk = 0; kk < kDk / 16; ++kk) {
+        const int e0 = 16 * kk + 4 * g;
+        const mfma_f4 ka = *(const mfma_f4*)&Ks[16 * ti + c16][e0];
+        const mfma_f4 qa = *(const mfma_f4*)&Qs[16 * ti + c16][e0];
+        const mfma_f4 kb = *(const mfma_f4*)&Ks[16 * tj + c16][e0];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          gk = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[m], kb[m], gk, 0, 0, 0);
+          gq = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[m], kb[m], gq, 0, 0, 0);
+        }
+      }
+      const int jj = 16 * tj + c16;  // the lane's column; rows 16 ti + 4 g + r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ii = 16 * ti + 4 * g + r;
+        const float dec = jj <= ii ? expf(cum[ii] - cum[jj]) : 0.f;
+        if (jj < ii) U[ii][jj] = -((bet[ii] * gk[r]) * dec);
+        intra[scr_in(ii, jj)] = jj <= ii ? gq[r] * dec : 0.f;
       }
     }
-    float iv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = j0 + u;
-      const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
-      if (j < i) U[i][j] = -((bet[i] * dkk[u]) * dec);
-      iv[u] = j <= i ? dqk[u] * dec : 0.f;
-    }
-    *(float4*)(intra + scr_in(i, j0)) = make_float4(iv[0], iv[1], iv[2], iv[3]);
   }
   // k_d = k e^(cum_last - cum): 4 chunk rows of one key per float4 of its lane-major layout
   for (int e = tid; e < kC * kDk / 4; e += kPP) {
@@ -335,44 +329,36 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
   }
   __syncthreads();
   tri_inverse(U, Tm);
-  // new_values = X (beta v), k_cumdecay = X (beta e^cum k): thread rows p and 63 - p, 8 columns
+  // new_values = (I + X) (beta v), k_cumdecay = (I + X) (beta e^cum k) on the f32 matrix cores (X:
+  // the strictly lower inverse in U, zero elsewhere): wave = 16 value / key columns, the four row
+  // tiles over the column blocks up to the diagonal
   {
-    const int p = tid >> 4, d0 = (tid & 15) * 8;
+    const int g = lane >> 4, c16 = lane & 15, dcol = 16 * wid + c16;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int i = half == 0 ? p : kC - 1 - p;
-      float an[8], ak[8];
-      {
-        const float ub = bet[i], ube = ub * ecum[i];  // the unit diagonal
+    for (int ti = 0; ti < 4; ++ti) {
+      mfma_f4 an = {0.f, 0.f, 0.f, 0.f}, ak = {0.f, 0.f, 0.f, 0.f};
+      const int il = 16 * ti + c16;
+      for (int lb = 0; lb <= ti; ++lb) {
 #pragma unroll
-        for (int d = 0; d < 8; d += 4) {
-          const float4 v = *(const float4*)&Vs[i][d0 + d];
-          const float4 k = *(const float4*)&Ks[i][d0 + d];
-          an[d] = ub * v.x; an[d + 1] = ub * v.y; an[d + 2] = ub * v.z; an[d + 3] = ub * v.w;
-          ak[d] = ube * k.x; ak[d + 1] = ube * k.y; ak[d + 2] = ube * k.z; ak[d + 3] = ube * k.w;
+        for (int m = 0; m < 4; ++m) {
+          const int ll = 16 * lb + 4 * g + m;
+          const float av = U[il][ll] + (ll == il ? 1.0f : 0.0f);
+          const float b = bet[ll];
+          an = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b * Vs[ll][dcol], an, 0, 0, 0);
+          ak = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (b * ecum[ll]) * Ks[ll][dcol], ak, 0, 0, 0);
         }
       }
-      for (int l = 0; l < i; ++l) {
-        const float ub = U[i][l] * bet[l];
-        const float ube = ub * ecum[l];
+      // lane: rows 16 ti + 4 g + r of column dcol
+      *(float4*)(scr + kScrNv + scr_nv(16 * ti + 4 * g, dcol)) = make_float4(an[0], an[1], an[2], an[3]);
 #pragma unroll
-        for (int d = 0; d < 8; d += 4) {
-          const float4 v = *(const float4*)&Vs[l][d0 + d];
-          const float4 k = *(const float4*)&Ks[l][d0 + d];
-          an[d] += ub * v.x; an[d + 1] += ub * v.y; an[d + 2] += ub * v.z; an[d + 3] += ub * v.w;
-          ak[d] += ube * k.x; ak[d + 1] += ube * k.y; ak[d + 2] += ube * k.z; ak[d + 3] += ube * k.w;
-        }
-      }
+      for (int r = 0; r < 4; ++r) scr[kScrKcd + scr_a(16 * ti + 4 * g + r, dcol)] = ak[r];
+    }
+    // q_e = q e^cum
+    for (int e = tid; e < kC * kDk / 4; e += kPP) {
+      const int i = e >> 5, d = (e & 31) * 4;
       const float eq = ecum[i];
-#pragma unroll
-      for (int d = 0; d < 8; d += 4) {
-        const int e = d0 + d;
-        *(float4*)(scr + kScrKcd + scr_a(i, e)) = make_float4(ak[d], ak[d + 1], ak[d + 2], ak[d + 3]);
-        const float4 q = *(const float4*)&Qs[i][e];
-        *(float4*)(scr + kScrQe + scr_a(i, e)) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) scr[kScrNv + scr_nv(i, e + u)] = an[d + u];
-      }
+      const float4 q = *(const float4*)&Qs[i][d];
+      *(float4*)(scr + kScrQe + scr_a(i, d)) = make_float4(q.x * eq, q.y * eq, q.z * eq, q.w * eq);
     }
     if (tid == 0) scr[kScrCd] = ecum[kC - 1];
   }
@@ -394,7 +380,6 @@ __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a)
 constexpr int kST = 512;
 constexpr int kStLd = kDk + 4;  // transposed state rows (key rows contiguous)
 constexpr int kInLd = kC + 4;   // transposed v_new rows
-typedef float mfma_f4 __attribute__((ext_vector_type(4)));
 struct StateOps {  // one wave's operands of one chunk, in MFMA layout
   mfma_f4 ka[4], qa[4], ia[4];  // k_cumdecay / q_e rows 16 rt + c16, keys 64 kh + 16 kk + 4 g + m;
                                 // intra rows 16 rt + c16, columns 16 lb + 4 g + m
