@@ -594,137 +594,136 @@ __global__ __launch_bounds__(kPT) void attn_prefill_prep_kernel(const AttnPrefil
   }
 }
 
-// Causal GQA attention of the prompt rows.  Block (query tile, kv head g): 16 rows = QT tokens x
-// rep query heads of g (QT = 16 / rep), so a 512-token prompt gives 128 x kv_heads blocks;
-// thread (row r = tid / 16, slice sl = tid % 16) holds dims [16 sl, 16 sl + 16) of its row's
-// query and output.  Keys stream through LDS 16 at a time per half block (each 16-float slice
-// padded to 20 so the 16 slices of a row fall in different banks): the block's two halves of 256
-// threads take alternate 16-key tiles, each with its own online softmax, and merge their (max,
-// sum, output) at the end.  A score is the sum of the 16 slices' partial dots (4 lane exchanges);
-// online softmax in log2 units, rescaled once per 8 keys.
-constexpr int kKT = 16;            // keys per LDS tile (per half block)
-constexpr int kAT = 512;           // threads per block (two halves)
-constexpr int kSd = 16;            // dims per thread
-constexpr int kSp = 20;            // LDS floats per 16-dim slice
+// Causal GQA attention of the prompt rows on the f32 matrix cores (v_mfma_f32_16x16x4_f32: f32
+// products and accumulation, like the f32 matmuls of the reference's attention).  Block (query
+// tile, kv head g): 16 rows = QT tokens x rep query heads of g (QT = 16 / rep), so a 512-token
+// prompt gives 128 x kv_heads blocks.  Its 4 waves take every 4th 16-key tile, each with its own
+// online softmax (f32, log2 units), and merge their (max, sum, output) in wave order at the end.
+// A wave computes S^T = K Q^T for its tile (lane l = 16 g + c16: keys 4 g + r of query row c16)
+// and O^T += V^T P^T, whose lane holds dims 16 i + 4 g + r of the same row c16: the row's running
+// max, sum and rescale stay in the lane (the 16 keys of a row sit in lanes c16 + 16 g, reduced by
+// two exchanges).  Keys and values pass through a per-wave LDS slot, the next tile's loaded into
+// registers while the current one is computed; the block's 16 query rows sit in LDS.
 constexpr int kRows = 16;          // query rows per block
-__global__ __launch_bounds__(kAT) void attn_prefill_kernel(const AttnPrefill a) {
-  __shared__ __align__(16) float Ks[2][kKT][16 * kSp];
-  __shared__ __align__(16) float Vs[2][kKT][16 * kSp];
-  const int tid = threadIdx.x, hb = tid >> 8, lt = tid & 255;  // half block, thread in the half
+constexpr int kAW = 4;             // waves per block
+constexpr int kAT = 64 * kAW;
+constexpr int kKvLd = kHdP + 4;    // padded key / value / query rows in LDS (rows 4 banks apart)
+__global__ __launch_bounds__(kAT, 1) void attn_prefill_kernel(const AttnPrefill a) {
+  __shared__ __align__(16) float Qs[kRows][kKvLd];
+  __shared__ __align__(16) float KV[kAW][2][16][kKvLd];  // per wave: key tile, value tile
+  __shared__ float Mw[kAW][kRows], Lw[kAW][kRows];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c16 = l & 15, g = l >> 4;
   const int rep = a.nh / a.nkv, QT = kRows / rep;
-  const int qt = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
-  const int r = lt >> 4, sl = lt & 15;
-  const int t = qt * QT + r / rep, hq = g * rep + r % rep;
-  const bool row_ok = t < a.T;
-  const int lim = a.p0 + (row_ok ? t : 0);  // last key this row may see
+  const int qt = blockIdx.x / a.nkv, gk = blockIdx.x % a.nkv;
+  const int t = qt * QT + c16 / rep;  // the lane's query row c16: token t
+  const int lim = a.p0 + min(t, a.T - 1);  // last key row c16 may see (rows past T are discarded)
   const int tmax_blk = min(a.T, (qt + 1) * QT) - 1;
   const int nkeys = a.p0 + tmax_blk + 1;
-  float q[kSd], acc[kSd];
-  const float* qsrc = a.qbuf + ((int64_t)(row_ok ? t : 0) * a.nh + hq) * kHdP + sl * kSd;
-#pragma unroll
-  for (int d = 0; d < kSd; d += 4) {
-    const float4 v = *(const float4*)(qsrc + d);
-    q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
-    acc[d] = 0.f; acc[d + 1] = 0.f; acc[d + 2] = 0.f; acc[d + 3] = 0.f;
+  for (int e = tid; e < kRows * kHdP / 4; e += kAT) {
+    const int r = e >> 6, d = (e & 63) * 4;
+    const int tr = min(qt * QT + r / rep, a.T - 1), hr = gk * rep + r % rep;
+    *(q35_f32x4*)&Qs[r][d] = *(const q35_f32x4*)(a.qbuf + ((int64_t)tr * a.nh + hr) * kHdP + d);
   }
-  float m = -INFINITY, l = 0.f;
-  const float sl2 = a.scale * 1.44269504088896341f;
-  const float* Kg = a.kc + (int64_t)g * a.tmax * kHdP;
-  const float* Vg = a.vc + (int64_t)g * a.tmax * kHdP;
-  // half hb takes the tiles at keys 2 kKT i + kKT hb; the next tile's rows are loaded into
-  // registers while the current one is computed
-  constexpr int kTl = kKT * kHdP / 4 / 256;  // float4 per thread per tile (4)
-  q35_f32x4 nk[kTl], nv[kTl];
-  auto load_tile = [&](int base) {
-    static_for<kTl>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      const int e = lt + u * 256, j = e >> 6, d = (e & 63) * 4;
-      const int kj = min(base + j, nkeys - 1);
-      nk[u] = *(const q35_f32x4*)(Kg + (int64_t)kj * kHdP + d);
-      nv[u] = *(const q35_f32x4*)(Vg + (int64_t)kj * kHdP + d);
-    });
+  const float* Kg = a.kc + (int64_t)gk * a.tmax * kHdP;
+  const float* Vg = a.vc + (int64_t)gk * a.tmax * kHdP;
+  float (*Kt)[kKvLd] = KV[w][0];
+  float (*Vt)[kKvLd] = KV[w][1];
+  q35_f32x4 nk[16], nv[16];  // the next tile: key row u, dims 4 l .. 4 l + 3
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int kj = min(k0 + u, nkeys - 1);
+      nk[u] = *(const q35_f32x4*)(Kg + (int64_t)kj * kHdP + 4 * l);
+      nv[u] = *(const q35_f32x4*)(Vg + (int64_t)kj * kHdP + 4 * l);
+    }
   };
-  load_tile(kKT * hb);
-  for (int kb = 0; kb < nkeys; kb += 2 * kKT) {  // (the same trip count in both halves)
-    const int k0 = kb + kKT * hb;
-    __syncthreads();
-    static_for<kTl>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      const int e = lt + u * 256, j = e >> 6, d = (e & 63) * 4;
-      const int o = (d >> 4) * kSp + (d & 15);
-      *(q35_f32x4*)&Ks[hb][j][o] = nk[u];
-      *(q35_f32x4*)&Vs[hb][j][o] = nv[u];
-    });
-    __syncthreads();
-    if (k0 + 2 * kKT < nkeys) load_tile(k0 + 2 * kKT);
-    const int kend = min(kKT, nkeys - k0);  // (<= 0: this half's tile is past the keys)
-    for (int jb = 0; jb < kend; jb += 8) {
-      float s[8];
-      float bm = -INFINITY;
+  mfma_f4 o[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float* kr = &Ks[hb][jb + u][sl * kSp];
-        float p = 0.f;
+  for (int i = 0; i < 16; ++i) o[i] = mfma_f4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+  const float sl2 = a.scale * 1.44269504088896341f;
+  int k0 = 16 * w;
+  if (k0 < nkeys) load_tile(k0);
+  __syncthreads();  // Qs
+  for (; k0 < nkeys; k0 += 16 * kAW) {
+    // (the wave's reads of its slot in the previous tile precede these stores: LDS is in order)
 #pragma unroll
-        for (int d = 0; d < kSd; d += 4) {
-          const float4 kv = *(const float4*)(kr + d);
-          p += ((q[d] * kv.x + q[d + 1] * kv.y) + q[d + 2] * kv.z) + q[d + 3] * kv.w;
-        }
-        p += __shfl_xor(p, 1, 64);
-        p += __shfl_xor(p, 2, 64);
-        p += __shfl_xor(p, 4, 64);
-        p += __shfl_xor(p, 8, 64);
-        const int kj = k0 + jb + u;
-        s[u] = (kj <= lim) ? p * sl2 : -INFINITY;
-        bm = fmaxf(bm, s[u]);
-      }
-      const float mn = fmaxf(m, bm);
-      if (mn == -INFINITY) continue;  // nothing visible yet for this row
-      const float al = __builtin_amdgcn_exp2f(m - mn);
-      l *= al;
+    for (int u = 0; u < 16; ++u) {
+      *(q35_f32x4*)&Kt[u][4 * l] = nk[u];
+      *(q35_f32x4*)&Vt[u][4 * l] = nv[u];
+    }
+    if (k0 + 16 * kAW < nkeys) load_tile(k0 + 16 * kAW);
+    mfma_f4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int d = 0; d < kSd; ++d) acc[d] *= al;
+    for (int kk = 0; kk < kHdP / 16; ++kk) {
+      const mfma_f4 ka = *(const mfma_f4*)&Kt[c16][16 * kk + 4 * g];
+      const mfma_f4 qb = *(const mfma_f4*)&Qs[c16][16 * kk + 4 * g];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float p = __builtin_amdgcn_exp2f(s[u] - mn);
-        l += p;
-        const float* vr = &Vs[hb][jb + u][sl * kSp];
+      for (int mm = 0; mm < 4; ++mm) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[mm], qb[mm], sc, 0, 0, 0);
+    }
+    float sv[4], bm = -INFINITY;
 #pragma unroll
-        for (int d = 0; d < kSd; d += 4) {
-          const float4 vv = *(const float4*)(vr + d);
-          acc[d] += p * vv.x; acc[d + 1] += p * vv.y; acc[d + 2] += p * vv.z; acc[d + 3] += p * vv.w;
-        }
-      }
+    for (int r = 0; r < 4; ++r) {
+      sv[r] = (k0 + 4 * g + r <= lim) ? sc[r] * sl2 : -INFINITY;
+      bm = fmaxf(bm, sv[r]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    float p[4], alpha = 1.f;
+    if (mn == -INFINITY) {  // nothing visible yet for this row
+      p[0] = p[1] = p[2] = p[3] = 0.f;
+    } else {
+      alpha = __builtin_amdgcn_exp2f(m - mn);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[r] - mn);
       m = mn;
     }
+    float ps = (p[0] + p[1]) + (p[2] + p[3]);
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * alpha + ps;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o[i] *= alpha;
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm)
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Vt[4 * g + mm][16 * i + c16], p[mm], o[i], 0, 0, 0);
+    }
   }
-  // merge the upper half's state into the lower half's (key 0, in the lower half's first tile, is
-  // visible to every row, so the lower half's maximum is finite)
-  float* mg = &Ks[0][0][0];  // (kSd + 2) floats per thread of the upper half
+  // merge the waves' states (key 0, in wave 0's first tile, is visible to every row, so wave 0's
+  // maximum is finite)
   __syncthreads();
-  if (hb == 1) {
+  float* Om = &KV[0][0][0][0];  // [kAW][kRows][kKvLd]
 #pragma unroll
-    for (int d = 0; d < kSd; ++d) mg[lt * (kSd + 2) + d] = acc[d];
-    mg[lt * (kSd + 2) + kSd] = m;
-    mg[lt * (kSd + 2) + kSd + 1] = l;
+  for (int i = 0; i < 16; ++i) *(mfma_f4*)&Om[(w * kRows + c16) * kKvLd + 16 * i + 4 * g] = o[i];
+  if (g == 0) {
+    Mw[w][c16] = m;
+    Lw[w][c16] = lsum;
   }
   __syncthreads();
-  if (hb == 1 || !row_ok) return;
-  {
-    const float m1 = mg[lt * (kSd + 2) + kSd], l1 = mg[lt * (kSd + 2) + kSd + 1];
-    const float mx = fmaxf(m, m1);
-    const float a0 = __builtin_amdgcn_exp2f(m - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);  // (m1 = -inf: 0)
-    l = l * a0 + l1 * a1;
+  const int q = tid >> 4, d0 = (tid & 15) * 16;
+  const int tq = qt * QT + q / rep, hq = gk * rep + q % rep;
+  if (tq >= a.T) return;
+  float M = Mw[0][q];
 #pragma unroll
-    for (int d = 0; d < kSd; ++d) acc[d] = acc[d] * a0 + mg[lt * (kSd + 2) + d] * a1;
+  for (int ww = 1; ww < kAW; ++ww) M = fmaxf(M, Mw[ww][q]);
+  float f[kAW], L = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < kAW; ++ww) {
+    f[ww] = __builtin_amdgcn_exp2f(Mw[ww][q] - M);  // (-inf: 0)
+    L += Lw[ww][q] * f[ww];
   }
-  const float* gate = a.qg + (int64_t)t * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + sl * kSd;
-  float* dst = a.out + (int64_t)t * a.ld_out + (int64_t)hq * kHdP + sl * kSd;
+  const float* gate = a.qg + (int64_t)tq * a.ld_qg + (int64_t)hq * 2 * kHdP + kHdP + d0;
+  float* dst = a.out + (int64_t)tq * a.ld_out + (int64_t)hq * kHdP + d0;
 #pragma unroll
-  for (int d = 0; d < kSd; d += 4) {
+  for (int d = 0; d < 16; d += 4) {
+    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < kAW; ++ww) acc += *(const q35_f32x4*)&Om[(ww * kRows + q) * kKvLd + d0 + d] * f[ww];
     const float4 gv = *(const float4*)(gate + d);
-    *(float4*)(dst + d) = make_float4((acc[d] / l) * sigmoid_f(gv.x), (acc[d + 1] / l) * sigmoid_f(gv.y),
-                                      (acc[d + 2] / l) * sigmoid_f(gv.z), (acc[d + 3] / l) * sigmoid_f(gv.w));
+    *(float4*)(dst + d) = make_float4((acc[0] / L) * sigmoid_f(gv.x), (acc[1] / L) * sigmoid_f(gv.y),
+                                      (acc[2] / L) * sigmoid_f(gv.z), (acc[3] / L) * sigmoid_f(gv.w));
   }
 }
 
