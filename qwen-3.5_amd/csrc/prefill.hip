@@ -56,25 +56,54 @@ Q35_DEV void block_max256_store(float v, float* sh, float* dst) {
 }
 
 // y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808).  amax (optional):
-// max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.
+// max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.  Rows of up to
+// kRmsHeld * 4 * 256 floats (K a multiple of 4, rows 16-byte aligned) stay in registers between
+// the sum of squares and the scaling (one read of x); longer ones are read twice.
+constexpr int kRmsHeld = 4;  // float4 per thread held
 __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, int K, const float* w, float eps,
                                                        float* y, int ldy, float* amax) {
   __shared__ float sh[4];
   const int m = blockIdx.x;
   const float* xr = x + (int64_t)m * ldx;
-  float ss = 0.f;
-  for (int k = threadIdx.x; k < K; k += kPT) {
-    const float v = xr[k];
-    ss += v * v;
-  }
-  ss = block_sum256(ss, sh);
-  const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
   float* yr = y + (int64_t)m * ldy;
   float mx = 0.f;
-  for (int k = threadIdx.x; k < K; k += kPT) {
-    const float v = (xr[k] * r) * (1.0f + w[k]);
-    yr[k] = v;
-    mx = fmaxf(mx, fabsf(v));
+  if (K <= kRmsHeld * 4 * kPT && (K & 3) == 0 &&
+      ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(yr) | reinterpret_cast<uintptr_t>(w)) & 15) == 0) {
+    float4 v[kRmsHeld];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kRmsHeld; ++u) {
+      const int k = 4 * (threadIdx.x + u * kPT);
+      v[u] = k < K ? *(const float4*)(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kRmsHeld; ++u) ss += ((v[u].x * v[u].x + v[u].y * v[u].y) + v[u].z * v[u].z) + v[u].w * v[u].w;
+    ss = block_sum256(ss, sh);
+    const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
+#pragma unroll
+    for (int u = 0; u < kRmsHeld; ++u) {
+      const int k = 4 * (threadIdx.x + u * kPT);
+      if (k < K) {
+        const float4 wv = *(const float4*)(w + k);
+        const float4 o = make_float4((v[u].x * r) * (1.0f + wv.x), (v[u].y * r) * (1.0f + wv.y),
+                                     (v[u].z * r) * (1.0f + wv.z), (v[u].w * r) * (1.0f + wv.w));
+        *(float4*)(yr + k) = o;
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+      }
+    }
+  } else {
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < K; k += kPT) {
+      const float v = xr[k];
+      ss += v * v;
+    }
+    ss = block_sum256(ss, sh);
+    const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
+    for (int k = threadIdx.x; k < K; k += kPT) {
+      const float v = (xr[k] * r) * (1.0f + w[k]);
+      yr[k] = v;
+      mx = fmaxf(mx, fabsf(v));
+    }
   }
   if (amax) block_max256_store(mx, sh, amax + m);
 }
