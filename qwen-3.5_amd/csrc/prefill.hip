@@ -109,18 +109,19 @@ __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, 
 }
 
 // ------------------------------------------------------------------ Gated DeltaNet, prompt
-// [beta | g] of 8 prompt rows per block (text_modules.rs:578-595).  Thread (output o = tid % 32,
-// K group kg = tid / 32) loads one weight W[k][o] per k of its group and multiplies it with the
-// 8 rows' x[t][k] (LDS, 512 columns at a time), keeping 8 row sums; the 8 K groups are then
-// summed in LDS in a fixed order.  Softplus takes its identity branch when its input exceeds 20
-// (the prompt branch's rule).
-constexpr int kGateRows = 8, kGateK = 512, kGateGroups = kPT / 32;
-__global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ldx, int T, int K, const float* wb,
-                                                          const float* wa, const float* alog, const float* dtb,
-                                                          int nh, float* out) {
-  __shared__ float xs[kGateRows][kGateK + 4];
-  __shared__ float red[kGateGroups][kGateRows][33];
-  const int tid = threadIdx.x, o = tid & 31, kg = tid >> 5;
+// [beta | g] of 4 prompt rows per block (text_modules.rs:578-595).  Four groups of 256 threads
+// take the 512-column chunks of K in turn (all four chunks of a 2048-wide row in one round trip).
+// In a group, thread (output o = tid % 32, K group kg = tid / 32) loads one weight W[k][o] per k
+// of its group and multiplies it with the block's rows' x[t][k] (LDS), keeping a sum per row; the groups'
+// and K groups' sums are then added in LDS in a fixed order.  Softplus takes its identity branch
+// when its input exceeds 20 (the prompt branch's rule).
+constexpr int kGateRows = 4, kGateK = 512, kGateGroups = kPT / 32, kGateCG = 4, kGateT = kGateCG * kPT;
+__global__ __launch_bounds__(kGateT) void gate_prompt_kernel(const float* x, int ldx, int T, int K, const float* wb,
+                                                             const float* wa, const float* alog, const float* dtb,
+                                                             int nh, float* out) {
+  __shared__ float xs[kGateCG][kGateRows][kGateK + 4];
+  __shared__ float red[kGateCG][kGateGroups][kGateRows][33];
+  const int cg = threadIdx.x / kPT, tid = threadIdx.x % kPT, o = tid & 31, kg = tid >> 5;
   const int t0 = blockIdx.x * kGateRows;
   const int nout = 2 * nh, oo = min(o, nout - 1), h = oo % nh;
   const float* W = (oo < nh ? wb : wa) + h;
@@ -128,8 +129,9 @@ __global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ld
 #pragma unroll
   for (int r = 0; r < kGateRows; ++r) acc[r] = 0.f;
   constexpr int kIt = kGateK / (8 * kGateGroups);
-  for (int k0 = 0; k0 < K; k0 += kGateK) {
-    const int kn = min(kGateK, K - k0);  // a multiple of 64
+  for (int kb = 0; kb < K; kb += kGateCG * kGateK) {  // (the same trip count in every group)
+    const int k0 = kb + cg * kGateK;
+    const int kn = max(0, min(kGateK, K - k0));  // a multiple of 64; 0 past the end
     __syncthreads();
     // all of the chunk's loads are issued before any is used (one round trip): the x rows, and
     // the weights of the thread's 8-row groups kb = 8 kg + 64 it (rows clamped inside the chunk)
@@ -138,39 +140,41 @@ __global__ __launch_bounds__(kPT) void gate_prompt_kernel(const float* x, int ld
 #pragma unroll
     for (int u = 0; u < kL; ++u) {
       const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4, t = t0 + i;
-      v[u] = (t < T && k0 + kk < K) ? *(const float4*)(x + (int64_t)t * ldx + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[u] = (t < T && kk < kn) ? *(const float4*)(x + (int64_t)t * ldx + k0 + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float w[kIt][8];
 #pragma unroll
     for (int it = 0; it < kIt; ++it)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) w[it][u] = W[(int64_t)(k0 + min(kg * 8 + 64 * it, kn - 8) + u) * nh];
+      for (int u = 0; u < 8; ++u) w[it][u] = kn > 0 ? W[(int64_t)(k0 + min(kg * 8 + 64 * it, kn - 8) + u) * nh] : 0.f;
 #pragma unroll
     for (int u = 0; u < kL; ++u) {
       const int e = tid + u * kPT, i = e / (kGateK / 4), kk = (e % (kGateK / 4)) * 4;
-      xs[i][kk] = v[u].x; xs[i][kk + 1] = v[u].y; xs[i][kk + 2] = v[u].z; xs[i][kk + 3] = v[u].w;
+      xs[cg][i][kk] = v[u].x; xs[cg][i][kk + 1] = v[u].y; xs[cg][i][kk + 2] = v[u].z; xs[cg][i][kk + 3] = v[u].w;
     }
     __syncthreads();
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const int kb = kg * 8 + 64 * it;
-      if (kb < kn) {
+      const int kq = kg * 8 + 64 * it;
+      if (kq < kn) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
 #pragma unroll
-          for (int r = 0; r < kGateRows; ++r) acc[r] += xs[r][kb + u] * w[it][u];
+          for (int r = 0; r < kGateRows; ++r) acc[r] += xs[cg][r][kq + u] * w[it][u];
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < kGateRows; ++r) red[kg][r][o] = acc[r];
+  for (int r = 0; r < kGateRows; ++r) red[cg][kg][r][o] = acc[r];
   __syncthreads();
-  for (int e = tid; e < kGateRows * 32; e += kPT) {
+  for (int e = threadIdx.x; e < kGateRows * 32; e += kGateT) {
     const int r = e >> 5, oc = e & 31, t = t0 + r;
     if (t >= T || oc >= nout) continue;
     float sv = 0.f;
 #pragma unroll
-    for (int g = 0; g < kGateGroups; ++g) sv += red[g][r][oc];
+    for (int c = 0; c < kGateCG; ++c)
+#pragma unroll
+      for (int g = 0; g < kGateGroups; ++g) sv += red[c][g][r][oc];
     float res;
     if (oc < nh) {
       res = sigmoid_f(sv);
@@ -782,7 +786,7 @@ int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, c
   if (T < 1 || K < 64 || (K % 64) != 0 || nh < 1 || 2 * nh > 32)
     return fail(Q35_E_SHAPE, "gate_proj_prompt: K a multiple of 64 and 2 heads <= 32");
   if ((ldx % 4) != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0) return fail(Q35_E_ALIGN, "gate_proj_prompt: x rows must be 16-byte aligned");
-  hipLaunchKernelGGL(gate_prompt_kernel, dim3((T + kGateRows - 1) / kGateRows), dim3(kPT), 0, st, x, ldx, T, K, wb,
+  hipLaunchKernelGGL(gate_prompt_kernel, dim3((T + kGateRows - 1) / kGateRows), dim3(kGateT), 0, st, x, ldx, T, K, wb,
                      wa, alog, dtb, nh, out);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
