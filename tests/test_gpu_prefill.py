@@ -225,10 +225,11 @@ def test_gated_delta_rule_prefill_matches_recurrent_steps(T, warm):
 
 # ---------------------------------------------------------------- attention prompt path
 
-@pytest.mark.parametrize("T,p0", [(1, 0), (17, 0), (100, 0), (33, 40)])
+@pytest.mark.parametrize("T,p0", [(1, 0), (17, 0), (100, 0), (33, 40), (64, 0), (130, 300), (5, 500)])
 def test_attention_core_prefill(T, p0):
     """C3 head layout (8 q heads, 2 kv heads, 256 dims, RoPE on 64, theta 1e7): rows at
-    positions p0..p0+T-1 attend causally to the cache rows 0..p0+t."""
+    positions p0..p0+T-1 attend causally to the cache rows 0..p0+t.  The cases cover one and many
+    16-key tiles per wave, a ragged last tile and a long cached context before a short prompt."""
     print(f"[attention prefill] T={T} p0={p0}", flush=True)
     d = q35.dims_2b()
     nh, nkv, hd = d.attn_heads, d.kv_heads, d.head_dim
