@@ -187,62 +187,100 @@ __global__ __launch_bounds__(kGateT) void gate_prompt_kernel(const float* x, int
   }
 }
 
+typedef float mfma_f4 __attribute__((ext_vector_type(4)));
+
+// 16 x 16 tile product on the f32 matrix cores: acc += A B over 16 k, A(i, k) and B(k, j) read by
+// the callers' accessors; lane l = 16 g + c16 feeds k = 4 g + m to step m and holds
+// D[4 g + r][c16] (register r).
+template <typename FA, typename FB>
+Q35_DEV mfma_f4 tile_mm16(FA A, FB B, mfma_f4 acc) {
+  const int c16 = threadIdx.x & 15, g = (threadIdx.x >> 4) & 3;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A(c16, 4 * g + m), B(4 * g + m, c16), acc, 0, 0, 0);
+  return acc;
+}
+
 // X = (I - N)^-1 for N strictly lower 64 x 64 in U (in place: U ends as X minus its unit
-// diagonal), by blocks: each wave inverts a 16 x 16 diagonal block by forward substitution
-// (the reference's row recurrence, text_modules.rs:282-290, on that block), then
+// diagonal; zero above it), by blocks on the f32 matrix cores (the reference's row recurrence,
+// text_modules.rs:282-290, solves the same system): waves 0-3 each invert a 16 x 16 diagonal block
+// as (I + N)(I + N^2)(I + N^4)(I + N^8) (N^16 = 0 for a strictly lower 16 x 16 block), then
 // X_BA = X_BB N_BA X_AA joins 16-blocks into 32-blocks and those into the 64-block
 // (for [[I - N_AA, 0], [-N_BA, I - N_BB]]).  Tm: 64 x 65 scratch.
-// (512 threads: waves 0-3 take the diagonal blocks, every thread one or two entries after that)
 Q35_DEV void tri_inverse(float (*U)[kC + 1], float (*Tm)[kC + 1]) {
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (wid < 4) {
+  const int tid = threadIdx.x, wid = tid >> 6, c16 = tid & 15, g = (tid >> 4) & 3;
+  const mfma_f4 z = {0.f, 0.f, 0.f, 0.f};
+  auto put = [&](float (*D)[kC + 1], int r0, int c0, mfma_f4 v) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) D[r0 + 4 * g + r][c0 + c16] = v[r];
+  };
+  if (wid < 4) {  // diagonal block b0; scratch: Tm rows b0 .. b0 + 15 (blocks 0..3 of columns)
     const int b0 = 16 * wid;
-    for (int i = 2; i < 16; ++i) {
-      float s = 0.f;
-      if (lane < i) {
-        for (int l = lane + 1; l < i; ++l) s += U[b0 + i][b0 + l] * U[b0 + l][b0 + lane];
-      }
-      if (lane < i) U[b0 + i][b0 + lane] += s;
-    }
-  }
-  __syncthreads();
-  // 16 -> 32: blocks (1,0) and (3,2) of 16: X = X_BB N X_AA = (I + L_B)(N + N L_A)
-  {
-    const int p = tid >> 8, e = tid & 255, r = e >> 4, c = e & 15;  // pair p, one entry per thread
-    const int rb = 32 * p + 16, cb = 32 * p;                         // block rows / cols
-    {
-      float t = U[rb + r][cb + c];
-      for (int l = c + 1; l < 16; ++l) t += U[rb + r][cb + l] * U[cb + l][cb + c];
-      Tm[rb + r][cb + c] = t;
-    }
-    __syncthreads();
-    {
-      float t = Tm[rb + r][cb + c];
-      for (int l = 0; l < r; ++l) t += U[rb + r][rb + l] * Tm[rb + l][cb + c];
-      U[rb + r][cb + c] = t;
-    }
-  }
-  __syncthreads();
-  // 32 -> 64: block (1,0) of 32
+    auto N = [&](int i, int k) { return U[b0 + i][b0 + k]; };
+    auto S = [&](int q) { return [=](int i, int k) { return Tm[b0 + i][16 * q + k]; }; };
+    put(Tm, b0, 16, tile_mm16(N, N, z));              // N^2
+    put(Tm, b0, 32, tile_mm16(S(1), S(1), z));        // N^4
+    put(Tm, b0, 48, tile_mm16(S(2), S(2), z));        // N^8
+    {  // X1 = N + N^2 + N N^2  (= (I + N)(I + N^2) - I)
+      const mfma_f4 p = tile_mm16(N, S(1), z);
+      mfma_f4 v;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int e = tid + 512 * u, r = e >> 5, c = e & 31;
-    float t = U[32 + r][c];
-    for (int l = c + 1; l < 32; ++l) t += U[32 + r][l] * U[l][c];
-    Tm[32 + r][c] = t;
+      for (int r = 0; r < 4; ++r) v[r] = (N(4 * g + r, c16) + Tm[b0 + 4 * g + r][16 + c16]) + p[r];
+      put(Tm, b0, 0, v);
+    }
+    {  // X2 = X1 + N^4 + X1 N^4
+      const mfma_f4 p = tile_mm16(S(0), S(2), z);
+      mfma_f4 v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = (Tm[b0 + 4 * g + r][c16] + Tm[b0 + 4 * g + r][32 + c16]) + p[r];
+      put(Tm, b0, 16, v);
+    }
+    {  // X3 = X2 + N^8 + X2 N^8
+      const mfma_f4 p = tile_mm16(S(1), S(3), z);
+      mfma_f4 v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = (Tm[b0 + 4 * g + r][16 + c16] + Tm[b0 + 4 * g + r][48 + c16]) + p[r];
+      put(U, b0, b0, v);
+    }
   }
   __syncthreads();
+  // 16 -> 32: blocks (1,0) and (3,2) of 16, a wave each: Tm_BA = N_BA (I + L_A), X_BA = (I + L_B) Tm_BA
+  if (wid < 2) {
+    const int ra = 32 * wid, rb = ra + 16;
+    auto NBA = [&](int i, int k) { return U[rb + i][ra + k]; };
+    auto IA = [&](int k, int j) { return U[ra + k][ra + j] + (k == j ? 1.0f : 0.0f); };
+    put(Tm, rb, ra, tile_mm16(NBA, IA, z));
+    auto IB = [&](int i, int k) { return U[rb + i][rb + k] + (i == k ? 1.0f : 0.0f); };
+    auto T = [&](int k, int j) { return Tm[rb + k][ra + j]; };
+    put(U, rb, ra, tile_mm16(IB, T, z));
+  }
+  __syncthreads();
+  // 32 -> 64: block (1,0) of 32, a wave per 16 x 16 output tile (rt, ct)
+  if (wid < 4) {
+    const int rt = wid >> 1, ct = wid & 1;
+    mfma_f4 acc = z;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int e = tid + 512 * u, r = e >> 5, c = e & 31;
-    float t = Tm[32 + r][c];
-    for (int l = 0; l < r; ++l) t += U[32 + r][32 + l] * Tm[32 + l][c];
-    U[32 + r][c] = t;
+    for (int kb = 0; kb < 2; ++kb) {
+      auto A = [&](int i, int k) { return U[32 + 16 * rt + i][16 * kb + k]; };
+      auto B = [&](int k, int j) { return U[16 * kb + k][16 * ct + j] + (16 * kb + k == 16 * ct + j ? 1.0f : 0.0f); };
+      acc = tile_mm16(A, B, acc);
+    }
+    put(Tm, 32 + 16 * rt, 16 * ct, acc);
+  }
+  __syncthreads();
+  if (wid < 4) {
+    const int rt = wid >> 1, ct = wid & 1;
+    mfma_f4 acc = z;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      auto A = [&](int i, int k) { return U[32 + 16 * rt + i][32 + 16 * kb + k] + (16 * rt + i == 16 * kb + k ? 1.0f : 0.0f); };
+      auto B = [&](int k, int j) { return Tm[32 + 16 * kb + k][16 * ct + j]; };
+      acc = tile_mm16(A, B, acc);
+    }
+    put(U, 32 + 16 * rt, 16 * ct, acc);
   }
   __syncthreads();
 }
 
-typedef float mfma_f4 __attribute__((ext_vector_type(4)));
 constexpr int kPP = 512;  // threads of the prep pass
 __global__ __launch_bounds__(kPP) void gdn_chunk_prep_kernel(const GdnPrefill a) {
   __shared__ __align__(16) float Qs[kC][kLdq];
