@@ -528,7 +528,9 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   if (prep_blocks > 0) hipLaunchKernelGGL(hgemm_prep_kernel, dim3((unsigned)prep_blocks), dim3(256), 0, st, a);
   hipLaunchKernelGGL((hgemm_kernel<BM>), dim3(a.nblocks), dim3(kGT), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
-  if (ksplit > 1) {
+  const bool defer = c.defer_reduce && c.nseg == 1;
+  if (c.ksplit_out) *c.ksplit_out = defer ? ksplit : 1;  // partial sums the caller must add
+  if (ksplit > 1 && !defer) {
     const int64_t n = (int64_t)c.M * (ncat / 4);
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
     Q35_HIP_TRY(hipGetLastError());

@@ -330,11 +330,18 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
   auto seg = [](const q35_model::Q8& w, const q35_model::Mb& mb, float* y, int ldy) {
     return GemmSeg{mb.q, mb.s, y, w.cols, Q35_KN_MB, ldy, mb.smax};
   };
+  // The residual projections (out, o, down) leave their K splits in pf_part; the RMSNorm that next
+  // reads the residual adds them in (pend splits).  The producers of the GEMM inputs write their
+  // row maxima into the GEMMs' scratch (pf_aux).
+  int pend = 1;
+  const int64_t pstride = (int64_t)T * H;
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
     const q35_model::MbLayer& W = m->mb[l];
-    // the producers of the GEMM inputs write their row maxima into the GEMMs' scratch (pf_aux)
-    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st, m->pf_aux))) return rc;
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.in_norm, d.eps, m->pf_xn, H, st, m->pf_aux, m->pf_part, pend,
+                              pstride, H)))
+      return rc;
+    pend = 1;
     if (!L.full) {
       GemmCall g;
       g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
@@ -355,6 +362,7 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       GemmCall o;
       o.x = m->pf_a; o.ldx = vdim; o.M = T; o.K = vdim; o.nseg = 1; o.accumulate = 1;
       o.seg[0] = seg(L.out, W.out, m->pf_x, H);
+      o.defer_reduce = 1; o.ksplit_out = &pend;
       o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux; o.amax = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     } else {
@@ -376,10 +384,14 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       GemmCall o;
       o.x = m->pf_a; o.ldx = ah * hd; o.M = T; o.K = ah * hd; o.nseg = 1; o.accumulate = 1;
       o.seg[0] = seg(L.o, W.o, m->pf_x, H);
+      o.defer_reduce = 1; o.ksplit_out = &pend;
       o.part = m->pf_part; o.part_floats = gemm_part_floats(m->pf_cap, d.hidden); o.aux = m->pf_aux;
       if ((rc = gemm_launch(o, st))) return rc;
     }
-    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st, m->pf_aux))) return rc;
+    if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st, m->pf_aux, m->pf_part, pend,
+                              pstride, H)))
+      return rc;
+    pend = 1;
     GemmCall g;
     g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
     g.seg[0] = seg(L.gate, W.gate, m->pf_y, LDY);
@@ -390,6 +402,8 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
     GemmCall dn;
     dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
     dn.seg[0] = seg(L.down, W.down, m->pf_x, H);
+    dn.defer_reduce = l + 1 < d.n_layers ? 1 : 0;  // (the lm_head reads the last residual row)
+    dn.ksplit_out = &pend;
     dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux; dn.amax = m->pf_aux;
       if ((rc = gemm_launch(dn, st))) return rc;
   }

@@ -56,25 +56,45 @@ Q35_DEV void block_max256_store(float v, float* sh, float* dst) {
 }
 
 // y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808).  amax (optional):
-// max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.  Rows of up to
+// max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.  With nsplit >
+// 1, x[m] is first replaced by ((part_0 + part_1) + ...) + x[m], the K splits of the GEMM that
+// accumulates into x added in split order as its reduction kernel would.  Rows of up to
 // kRmsHeld * 4 * 256 floats (K a multiple of 4, rows 16-byte aligned) stay in registers between
 // the sum of squares and the scaling (one read of x); longer ones are read twice.
 constexpr int kRmsHeld = 4;  // float4 per thread held
-__global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, int K, const float* w, float eps,
-                                                       float* y, int ldy, float* amax) {
+__global__ __launch_bounds__(kPT) void rms_rows_kernel(float* x, int ldx, int K, const float* w, float eps,
+                                                       float* y, int ldy, float* amax, const float* part,
+                                                       int nsplit, int64_t sstride, int ldp) {
   __shared__ float sh[4];
   const int m = blockIdx.x;
-  const float* xr = x + (int64_t)m * ldx;
+  float* xr = x + (int64_t)m * ldx;
   float* yr = y + (int64_t)m * ldy;
+  const float* pr = part ? part + (int64_t)m * ldp : nullptr;
   float mx = 0.f;
   if (K <= kRmsHeld * 4 * kPT && (K & 3) == 0 &&
-      ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(yr) | reinterpret_cast<uintptr_t>(w)) & 15) == 0) {
+      ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(yr) | reinterpret_cast<uintptr_t>(w) |
+        reinterpret_cast<uintptr_t>(pr)) & 15) == 0 && (nsplit <= 1 || (sstride & 3) == 0)) {
     float4 v[kRmsHeld];
     float ss = 0.f;
 #pragma unroll
     for (int u = 0; u < kRmsHeld; ++u) {
       const int k = 4 * (threadIdx.x + u * kPT);
       v[u] = k < K ? *(const float4*)(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (nsplit > 1) {
+#pragma unroll
+      for (int u = 0; u < kRmsHeld; ++u) {
+        const int k = 4 * (threadIdx.x + u * kPT);
+        if (k < K) {
+          float4 t = *(const float4*)(pr + k);
+          for (int s = 1; s < nsplit; ++s) {
+            const float4 q = *(const float4*)(pr + s * sstride + k);
+            t.x += q.x; t.y += q.y; t.z += q.z; t.w += q.w;
+          }
+          v[u] = make_float4(t.x + v[u].x, t.y + v[u].y, t.z + v[u].z, t.w + v[u].w);
+          *(float4*)(xr + k) = v[u];
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < kRmsHeld; ++u) ss += ((v[u].x * v[u].x + v[u].y * v[u].y) + v[u].z * v[u].z) + v[u].w * v[u].w;
@@ -94,7 +114,13 @@ __global__ __launch_bounds__(kPT) void rms_rows_kernel(const float* x, int ldx, 
   } else {
     float ss = 0.f;
     for (int k = threadIdx.x; k < K; k += kPT) {
-      const float v = xr[k];
+      float v = xr[k];
+      if (nsplit > 1) {
+        float t = pr[k];
+        for (int s = 1; s < nsplit; ++s) t += pr[s * sstride + k];
+        v = t + v;
+        xr[k] = v;
+      }
       ss += v * v;
     }
     ss = block_sum256(ss, sh);
@@ -810,10 +836,12 @@ int store_i32_launch(int32_t* p, int32_t v, hipStream_t st) {
   return Q35_OK;
 }
 
-int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
-                    hipStream_t st, float* amax) {
+int rms_rows_launch(float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
+                    hipStream_t st, float* amax, const float* part, int nsplit, int64_t sstride, int ldp) {
   if (M < 1) return Q35_OK;
-  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy, amax);
+  if (nsplit > 1 && !part) return fail(Q35_E_ARG, "rms_rows: split partials missing");
+  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy, amax,
+                     nsplit > 1 ? part : nullptr, nsplit, sstride, ldp);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

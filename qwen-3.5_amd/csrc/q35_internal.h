@@ -445,6 +445,12 @@ struct GemmCall {
   float* aux = nullptr;
   // Q35_KN_MB: max |x| of each row [M] when the producer of x has computed it (skips that pass)
   const float* amax = nullptr;
+  // Q35_KN_MB, one segment: with defer_reduce set, a launch that splits K leaves the splits'
+  // partial sums in part ([split][M][N]) instead of adding them into y; *ksplit_out (when given)
+  // reports how many the caller must add (1: none, y was written), in split order and then y when
+  // accumulating (rms_rows_launch does, before it normalises the rows)
+  int32_t defer_reduce = 0;
+  int32_t* ksplit_out = nullptr;
 };
 // Scratch floats of an MB launch: row maxima [M] and scale partial maxima [64], 64-aligned.
 inline size_t gemm_aux_floats(int M) { return ((size_t)M + 63) / 64 * 64 + 64; }
@@ -600,8 +606,12 @@ int mb_scale_transpose_launch(const float* s, int32_t V, int32_t K, float* sT, h
 // *p = v on the stream (a kernel, so it can sit in a captured graph)
 int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);
 // y[m] = RMSNorm(x[m]) * (1 + w) for M rows of K
-int rms_rows_launch(const float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
-                    hipStream_t st, float* amax = nullptr);
+// y = RMSNorm(x) (1 + w) per row; amax (optional): each row's max |y|.  part (optional, nsplit >
+// 1): K-split partial sums of a deferred GEMM that accumulates into x: x = ((part_0 + part_1) + ...)
+// + x is formed and written back to x first (split s, row m at part + s * sstride + m * ldp).
+int rms_rows_launch(float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
+                    hipStream_t st, float* amax = nullptr, const float* part = nullptr, int nsplit = 1,
+                    int64_t sstride = 0, int ldp = 0);
 // [beta | g] rows of a prompt (x [T][ldx], softplus identity branch when its input exceeds 20)
 int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, const float* wa, const float* alog,
                        const float* dtb, int nh, float* out, hipStream_t st);
