@@ -51,6 +51,9 @@ struct GArgs {
   float* part;
   float* amax;   // MB path: |x| maximum of each row [M]
   int32_t prep_rows;  // MB path: rows whose maximum the prep pass finds (M, or 0 when given)
+  float* act;         // MB path: SwiGLU output of alternating gate / up column blocks (else null)
+  float* act_amax;
+  int32_t ld_act;
   float* spart;  // MB path: partial maxima of every segment's |scale| [kPrepS]
 };
 
@@ -440,6 +443,45 @@ __global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
 
   // lane holds D[n = 16 nt + 4 g + r][m = 16 i + c] of the wave's tile: 4 consecutive columns of
   // one row per (nt, i)
+  if (a.act) {
+    // SwiGLU: the tile's column blocks are gate (wave wn = 0) and up (wn = 1) of the same 64 act
+    // columns, at the same lane positions; the up wave hands its values over through LDS (the x
+    // staging buffer, idle after the loop's last barrier)
+    float* ex = &Xs[0][0] + wm * (MT * 4 * 4 * 64);
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const float inv = __int_as_float((254 << 23) - __float_as_int(fsh[wm * WM + 16 * i + c]));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) *(mf4*)(ex + ((i * 4 + nt) * 64 + lane) * 4) = acc[nt][i] * inv;
+      }
+    }
+    __syncthreads();
+    if (wn == 1) return;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int rl = wm * WM + 16 * i + c, row = m0 + rl;
+      const float inv = __int_as_float((254 << 23) - __float_as_int(fsh[rl]));
+      float mx = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const mf4 gt4 = acc[nt][i] * inv, up = *(const mf4*)(ex + ((i * 4 + nt) * 64 + lane) * 4);
+        mf4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = up[r] * silu_f(gt4[r]);
+          mx = fmaxf(mx, fabsf(v[r]));
+        }
+        if (row < a.M) *(mf4*)(a.act + (int64_t)row * a.ld_act + (n0 >> 1) + 16 * nt + 4 * g) = v;
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (g == 0 && row < a.M)  // (non-negative floats order as their bit patterns)
+        __hip_atomic_fetch_max((Q35_GLOBAL uint32_t*)(a.act_amax + row), __float_as_uint(mx), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int rl = wm * WM + 16 * i + c, row = m0 + rl;
@@ -517,6 +559,9 @@ int launch_mb(const GemmCall& c, int ksplit, hipStream_t st) {
   a.ncat = ncat;
   a.part = c.part;
   a.nblocks = tiles * ksplit * a.mtiles;
+  a.act = c.act;
+  a.act_amax = c.act_amax;
+  a.ld_act = c.ld_act;
   a.amax = c.amax ? const_cast<float*>(c.amax) : c.aux;
   a.prep_rows = c.amax ? 0 : c.M;
   a.spart = c.aux + (gemm_aux_floats(c.M) - kPrepS);
@@ -555,6 +600,7 @@ void gemm_pick_mb(const GemmCall& c, int* bm, int* ksplit) {
   double best = 1e300;
   *bm = 64;
   *ksplit = 1;
+  if (c.act) return;  // (the SwiGLU epilogue needs whole sums)
   for (int ks = 1; ks <= kGemmMaxSplit; ks *= 2) {
     if (ks > 1 && (!c.part || c.part_floats < (size_t)ks * c.M * ncat || c.K / kHBK < 2 * ks)) break;
     const int steps = (c.K / kHBK + ks - 1) / ks;
@@ -619,6 +665,8 @@ int gemm_launch(const GemmCall& c, hipStream_t st) {
           (reinterpret_cast<uintptr_t>(s.y) & 15) || (s.ldy % 4))
         return fail(Q35_E_ALIGN, "gemm: Q35_KN_MB needs 16-byte aligned q, scales and y rows");
     }
+    if (c.act && (c.nseg != 1 || !c.act_amax || (c.ld_act % 4) != 0 || (reinterpret_cast<uintptr_t>(c.act) & 15)))
+      return fail(Q35_E_ARG, "gemm: the SwiGLU output needs one segment, row maxima and 16-byte aligned rows");
     int bm = 64, ks = 1;
     gemm_pick_mb(c, &bm, &ks);
     return launch_mb<64>(c, ks, st);

@@ -307,8 +307,32 @@ int ensure_prefill(q35_model* m, hipStream_t st) {
       (rc = dev_alloc_t(m, "prefill_q", (size_t)cap * ah * hd, &m->pf_q)) ||
       (rc = dev_alloc_t(m, "prefill_scratch", (size_t)nh * nchunk * kGdnScratchPerChunk, &m->pf_scr)) ||
       (rc = dev_alloc_t(m, "prefill_partials", gemm_part_floats(cap, H), &m->pf_part)) ||
-      (rc = dev_alloc_t(m, "prefill_gemm_aux", gemm_aux_floats(cap), &m->pf_aux)))
+      (rc = dev_alloc_t(m, "prefill_gemm_aux", gemm_aux_floats(cap), &m->pf_aux)) ||
+      (rc = dev_alloc_t(m, "prefill_act_max", (size_t)cap, &m->pf_act_max)))
     return rc;
+  // gate | up interleaved by 64-column block for the fused SwiGLU: an MB copy keeps each column
+  // block's records (K * 64 bytes) and scales (K floats) contiguous, so the two copies are
+  // interleaved with strided copies
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    q35_model::MbLayer& W = m->mb[l];
+    const int K = d.hidden, nb = F / 64;
+    const std::string p = "layers." + std::to_string(l) + ".";
+    int8_t* q = nullptr;
+    float *s = nullptr, *smax = nullptr;
+    if ((rc = dev_alloc_t(m, "mb." + p + "gate_up_interleaved", (size_t)2 * F * K, &q)) ||
+        (rc = dev_alloc_t(m, "mb." + p + "gate_up_interleaved.scale", (size_t)2 * nb * K, &s)) ||
+        (rc = dev_alloc_t(m, "mb." + p + "gate_up_interleaved.scale_max", 1, &smax)))
+      return rc;
+    const size_t qb = (size_t)K * 64, sb = (size_t)K * sizeof(float);
+    Q35_HIP_TRY(hipMemcpy2DAsync(q, 2 * qb, W.gate.q, qb, qb, nb, hipMemcpyDeviceToDevice, st));
+    Q35_HIP_TRY(hipMemcpy2DAsync(q + qb, 2 * qb, W.up.q, qb, qb, nb, hipMemcpyDeviceToDevice, st));
+    Q35_HIP_TRY(hipMemcpy2DAsync(s, 2 * sb, W.gate.s, sb, sb, nb, hipMemcpyDeviceToDevice, st));
+    Q35_HIP_TRY(hipMemcpy2DAsync(s + K, 2 * sb, W.up.s, sb, sb, nb, hipMemcpyDeviceToDevice, st));
+    if ((rc = mb_scale_max_launch(s, (int64_t)2 * nb * K, smax, st))) return rc;
+    W.gu.q = q;
+    W.gu.s = s;
+    W.gu.smax = smax;
+  }
   m->pf_cap = cap;
   m->pf_ldy = ldy;
   m->pf_lda = lda;
@@ -389,22 +413,23 @@ int prefill_pass(q35_model* m, const SeqView& v, const int32_t* ids, int T, int 
       if ((rc = gemm_launch(o, st))) return rc;
     }
     if ((rc = rms_rows_launch(m->pf_x, H, T, H, L.post_norm, d.eps, m->pf_xn, H, st, m->pf_aux, m->pf_part, pend,
-                              pstride, H)))
+                              pstride, H, m->pf_act_max)))
       return rc;
     pend = 1;
+    // gate | up (interleaved by column block) with the SwiGLU in the GEMM's epilogue: the rows
+    // up * silu(gate) and their maxima (cleared by the RMSNorm above) come straight out of it
     GemmCall g;
-    g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 2;
-    g.seg[0] = seg(L.gate, W.gate, m->pf_y, LDY);
-    g.seg[1] = seg(L.up, W.up, m->pf_y + F, LDY);
+    g.x = m->pf_xn; g.ldx = H; g.M = T; g.K = H; g.nseg = 1;
+    g.seg[0] = GemmSeg{W.gu.q, W.gu.s, m->pf_y, 2 * F, Q35_KN_MB, LDY, W.gu.smax};
     g.part = m->pf_part; g.part_floats = gemm_part_floats(m->pf_cap, d.hidden); g.aux = m->pf_aux; g.amax = m->pf_aux;
-      if ((rc = gemm_launch(g, st))) return rc;
-    if ((rc = swiglu_rows_launch(m->pf_y, LDY, T, F, m->pf_a, F, st, m->pf_aux))) return rc;
+    g.act = m->pf_a; g.ld_act = F; g.act_amax = m->pf_act_max;
+    if ((rc = gemm_launch(g, st))) return rc;
     GemmCall dn;
     dn.x = m->pf_a; dn.ldx = F; dn.M = T; dn.K = F; dn.nseg = 1; dn.accumulate = 1;
     dn.seg[0] = seg(L.down, W.down, m->pf_x, H);
     dn.defer_reduce = l + 1 < d.n_layers ? 1 : 0;  // (the lm_head reads the last residual row)
     dn.ksplit_out = &pend;
-    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux; dn.amax = m->pf_aux;
+    dn.part = m->pf_part; dn.part_floats = gemm_part_floats(m->pf_cap, d.hidden); dn.aux = m->pf_aux; dn.amax = m->pf_act_max;
       if ((rc = gemm_launch(dn, st))) return rc;
   }
   if ((rc = store_i32_launch(v.pos, p0 + T - 1, st))) return rc;

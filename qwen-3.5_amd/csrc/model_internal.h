@@ -53,6 +53,7 @@ struct q35_model {
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;
   float *pf_bg = nullptr, *pf_q = nullptr, *pf_scr = nullptr, *pf_part = nullptr, *pf_aux = nullptr;
+  float* pf_act_max = nullptr;  // row maxima of the SwiGLU rows (down_proj's input)
   // batched decode (allocated on first use): every projection again in the MB layout of the
   // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
   struct Mb {
@@ -61,7 +62,9 @@ struct q35_model {
     const float* f = nullptr;     // batched RMS launches: split factor per column block
     const float* smax = nullptr;  // max |scale| (prompt GEMMs)
   };
-  struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down; };
+  // gu: gate and up interleaved by 64-column block (the prompt GEMM's fused SwiGLU; built with
+  // the prompt buffers)
+  struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down, gu; };
   std::vector<MbLayer> mb;
   const float* embed_scale_t = nullptr;  // the embedding table's scales transposed [hidden/64][vocab]
 };

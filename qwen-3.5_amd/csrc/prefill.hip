@@ -58,15 +58,17 @@ Q35_DEV void block_max256_store(float v, float* sh, float* dst) {
 // y[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w)  (text_modules.rs:800-808).  amax (optional):
 // max |y[m]| of each row, the row maxima the matrix-core GEMM that consumes y needs.  With nsplit >
 // 1, x[m] is first replaced by ((part_0 + part_1) + ...) + x[m], the K splits of the GEMM that
-// accumulates into x added in split order as its reduction kernel would.  Rows of up to
+// accumulates into x added in split order as its reduction kernel would.  clear (optional): set to
+// zero per row (the next GEMM's SwiGLU row maxima, raised by atomics).  Rows of up to
 // kRmsHeld * 4 * 256 floats (K a multiple of 4, rows 16-byte aligned) stay in registers between
 // the sum of squares and the scaling (one read of x); longer ones are read twice.
 constexpr int kRmsHeld = 4;  // float4 per thread held
 __global__ __launch_bounds__(kPT) void rms_rows_kernel(float* x, int ldx, int K, const float* w, float eps,
                                                        float* y, int ldy, float* amax, const float* part,
-                                                       int nsplit, int64_t sstride, int ldp) {
+                                                       int nsplit, int64_t sstride, int ldp, float* clear) {
   __shared__ float sh[4];
   const int m = blockIdx.x;
+  if (clear && threadIdx.x == 0) clear[m] = 0.f;
   float* xr = x + (int64_t)m * ldx;
   float* yr = y + (int64_t)m * ldy;
   const float* pr = part ? part + (int64_t)m * ldp : nullptr;
@@ -634,24 +636,6 @@ __global__ __launch_bounds__(kPT) void gated_norm_rows_kernel(const float* o, in
   if (amax) block_max256_store(mx, sh, amax + t);
 }
 
-// out[t][k] = up * silu(gate): gu = [gate (F) | up (F)] per row (text_modules.rs:1000-1011); one
-// block per row, 4 columns per thread and step; amax (optional): max |out[t]| of each row
-__global__ __launch_bounds__(kPT) void swiglu_rows_kernel(const float* gu, int ldgu, int F, float* out, int ldout,
-                                                          float* amax) {
-  __shared__ float sh[4];
-  const int t = blockIdx.x;
-  const float* r = gu + (int64_t)t * ldgu;
-  float* dst = out + (int64_t)t * ldout;
-  float mx = 0.f;
-  for (int k = 4 * threadIdx.x; k < F; k += 4 * kPT) {
-    const float4 g = *(const float4*)(r + k), u = *(const float4*)(r + F + k);
-    const float4 y = make_float4(u.x * silu_f(g.x), u.y * silu_f(g.y), u.z * silu_f(g.z), u.w * silu_f(g.w));
-    *(float4*)(dst + k) = y;
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-  }
-  if (amax) block_max256_store(mx, sh, amax + t);
-}
-
 // ------------------------------------------------------------------ attention, prompt
 // Block (t, slot): slot < nh normalises and rotates query head `slot` into qbuf[t][slot]; slot
 // nh + g does kv head g: k_norm + RoPE into the K cache row p0 + t, v copied to the V cache.
@@ -837,11 +821,12 @@ int store_i32_launch(int32_t* p, int32_t v, hipStream_t st) {
 }
 
 int rms_rows_launch(float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
-                    hipStream_t st, float* amax, const float* part, int nsplit, int64_t sstride, int ldp) {
+                    hipStream_t st, float* amax, const float* part, int nsplit, int64_t sstride, int ldp,
+                    float* clear) {
   if (M < 1) return Q35_OK;
   if (nsplit > 1 && !part) return fail(Q35_E_ARG, "rms_rows: split partials missing");
   hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(kPT), 0, st, x, ldx, K, w, eps, y, ldy, amax,
-                     nsplit > 1 ? part : nullptr, nsplit, sstride, ldp);
+                     nsplit > 1 ? part : nullptr, nsplit, sstride, ldp, clear);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
@@ -873,16 +858,6 @@ int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, con
                            float* out, int ldout, hipStream_t st, float* amax) {
   if (T < 1) return Q35_OK;
   hipLaunchKernelGGL(gated_norm_rows_kernel, dim3(T), dim3(kPT), 0, st, o, ldo, z, ldz, w, nh, eps, out, ldout, amax);
-  Q35_HIP_TRY(hipGetLastError());
-  return Q35_OK;
-}
-
-int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st, float* amax) {
-  if (T < 1) return Q35_OK;
-  if ((F % 4) != 0 || (ldgu % 4) != 0 || (ldout % 4) != 0 || (reinterpret_cast<uintptr_t>(gu) & 15) ||
-      (reinterpret_cast<uintptr_t>(out) & 15))
-    return fail(Q35_E_ALIGN, "swiglu_rows: 16-byte aligned rows and F a multiple of 4 required");
-  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(T), dim3(kPT), 0, st, gu, ldgu, F, out, ldout, amax);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

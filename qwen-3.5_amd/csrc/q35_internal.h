@@ -451,6 +451,13 @@ struct GemmCall {
   // accumulating (rms_rows_launch does, before it normalises the rows)
   int32_t defer_reduce = 0;
   int32_t* ksplit_out = nullptr;
+  // Q35_KN_MB, one segment whose 64-column blocks alternate gate and up (block 2 j: gate columns
+  // 64 j .., block 2 j + 1: up columns 64 j ..): the launch writes act[m][64 j + c] =
+  // up * silu(gate) (N / 2 columns) instead of y, and raises act_amax[m] (zero beforehand) to each
+  // row's max |act|; K is not split
+  float* act = nullptr;
+  int32_t ld_act = 0;
+  float* act_amax = nullptr;
 };
 // Scratch floats of an MB launch: row maxima [M] and scale partial maxima [64], 64-aligned.
 inline size_t gemm_aux_floats(int M) { return ((size_t)M + 63) / 64 * 64 + 64; }
@@ -611,7 +618,7 @@ int store_i32_launch(int32_t* p, int32_t v, hipStream_t st);
 // + x is formed and written back to x first (split s, row m at part + s * sstride + m * ldp).
 int rms_rows_launch(float* x, int ldx, int M, int K, const float* w, float eps, float* y, int ldy,
                     hipStream_t st, float* amax = nullptr, const float* part = nullptr, int nsplit = 1,
-                    int64_t sstride = 0, int ldp = 0);
+                    int64_t sstride = 0, int ldp = 0, float* clear = nullptr);
 // [beta | g] rows of a prompt (x [T][ldx], softplus identity branch when its input exceeds 20)
 int gate_prompt_launch(const float* x, int ldx, int T, int K, const float* wb, const float* wa, const float* alog,
                        const float* dtb, int nh, float* out, hipStream_t st);
@@ -636,7 +643,6 @@ int gdn_prefill_launch(const GdnPrefill& a, hipStream_t st);
 int gated_norm_rows_launch(const float* o, int ldo, const float* z, int ldz, const float* w, int T, int nh, float eps,
                            float* out, int ldout, hipStream_t st, float* amax = nullptr);
 // out[t][k] = gu[t][F + k] * silu(gu[t][k])
-int swiglu_rows_launch(const float* gu, int ldgu, int T, int F, float* out, int ldout, hipStream_t st, float* amax = nullptr);
 // Attention over a prompt of T tokens at positions p0..p0+T-1 (head_dim 256, one sequence).
 constexpr int kHdP = 256;
 struct AttnPrefill {
