@@ -2,10 +2,11 @@
 // :184-187 l2norm, :365-443 burn_recurrent_gated_delta_rule), plus the standalone gate
 // projection (kernels.rs:174-247) and the causal-conv state shift.
 //
-// Step block (b, head h, 32-column slice of the value dim): 256 threads.  Threads 0..255 run
-// the 4-tap depthwise conv + SiLU for the head's 128 q and 128 k channels, threads 0..31 for
-// the slice's v channels; q and k are L2-normalised in LDS.  The state slice
-// S[h][0:128][j0:j0+32] (16 KB) is held in registers, 16 rows per thread: decay, S^T k (8-way
+// Step block (b, head h, slice of 32 or, for many rows, all 128 columns of the value dim): 256
+// threads.  Threads 0..255 run the 4-tap depthwise conv + SiLU for the head's 128 q and 128 k
+// channels, the first threads the slice's v channels; q and k are L2-normalised in LDS.  The
+// state slice S[h][0:128][j0:j0+CS] (16 or 64 KB) is held in registers, 16 rows per thread (one
+// column, or a float4 of columns): decay, S^T k (8-way
 // LDS reduction), delta = (v - S^T k) * beta, rank-1 update, S^T q, write back.  Every value
 // column is independent, so slices need no cross-block reduction; the per-head gated RMSNorm
 // is applied by the out_proj matvec prologue.  All slices of a head read the same q/k conv
@@ -20,9 +21,8 @@ namespace q35 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kCS = 32;          // value columns per block
 constexpr int kDk = 128;
-constexpr int kRowGroups = kThreads / kCS;  // 8
+constexpr int kRowGroups = kThreads / 32;  // 8 row groups of 32 column groups
 constexpr int kRowsPerThread = kDk / kRowGroups;  // 16
 
 struct GdnArgs {
@@ -41,14 +41,16 @@ Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
   return silu_f(acc);
 }
 
+template <int CS>
 __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
+  constexpr int VW = CS / 32;  // value columns per thread (4: one float4)
   const GdnCall& a = A.c;
   __shared__ float qk[2 * kDk];
   __shared__ float qh[kDk];
   __shared__ float kh[kDk];
-  __shared__ float vv[kCS];
+  __shared__ float vv[CS];
   __shared__ float wsum[4];
-  __shared__ float red[kRowGroups * kCS];
+  __shared__ float red[kRowGroups * CS];
   __shared__ int last_flag;
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -57,20 +59,28 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   const int b = blockIdx.x / (A.nslice * a.nh);
   const float* cs = a.conv_state + (size_t)b * A.conv_dim * 3;
 
-  // state slice loads first: their latency overlaps the conv / norm work
-  const int j = tid % kCS, ig = tid / kCS;
+  // state slice loads first: their latency overlaps the conv / norm work.  Thread (column group
+  // jq = tid % 32, row group ig = tid / 32): columns VW jq .. VW jq + VW - 1, rows 16 ig .. + 15
+  const int jq = tid % 32, ig = tid / 32, j0 = VW * jq;
   const int i0 = ig * kRowsPerThread;
-  float* Sp = a.S + (((size_t)b * a.nh + h) * kDk) * a.dv + slice * kCS + j;
-  float sr[kRowsPerThread];
+  float* Sp = a.S + (((size_t)b * a.nh + h) * kDk) * a.dv + slice * CS + j0;
+  float sr[kRowsPerThread][VW];
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) sr[r] = Sp[(size_t)(i0 + r) * a.dv];
+  for (int r = 0; r < kRowsPerThread; ++r) {
+    if constexpr (VW == 4) {
+      const float4 v = *(const float4*)(Sp + (size_t)(i0 + r) * a.dv);
+      sr[r][0] = v.x; sr[r][1] = v.y; sr[r][2] = v.z; sr[r][3] = v.w;
+    } else {
+      sr[r][0] = Sp[(size_t)(i0 + r) * a.dv];
+    }
+  }
 
   {  // q (tid < 128) and k (tid >= 128) channels of head h
     const int c = (tid < kDk) ? h * kDk + tid : A.key_dim + h * kDk + (tid - kDk);
     qk[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
   }
-  if (tid < kCS) {
-    const int c = 2 * A.key_dim + h * a.dv + slice * kCS + tid;
+  if (tid < CS) {
+    const int c = 2 * A.key_dim + h * a.dv + slice * CS + tid;
     vv[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
   }
   __syncthreads();
@@ -100,32 +110,52 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   const float decay = expf(g);
   __syncthreads();
 
+  float mp[VW];
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) sr[r] = sr[r] * decay;
-  float mp = 0.f;
+  for (int u = 0; u < VW; ++u) mp[u] = 0.f;
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) mp += sr[r] * kh[i0 + r];
-  red[ig * kCS + j] = mp;
+  for (int r = 0; r < kRowsPerThread; ++r)
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      sr[r][u] = sr[r][u] * decay;
+      mp[u] += sr[r][u] * kh[i0 + r];
+    }
+#pragma unroll
+  for (int u = 0; u < VW; ++u) red[ig * CS + j0 + u] = mp[u];
   __syncthreads();
-  float m = 0.f;
+  float delta[VW];
 #pragma unroll
-  for (int i = 0; i < kRowGroups; ++i) m += red[i * kCS + j];
-  const float delta = (vv[j] - m) * beta;
+  for (int u = 0; u < VW; ++u) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowGroups; ++i) m += red[i * CS + j0 + u];
+    delta[u] = (vv[j0 + u] - m) * beta;
+  }
   __syncthreads();
-  float op = 0.f;
+  float op[VW];
+#pragma unroll
+  for (int u = 0; u < VW; ++u) op[u] = 0.f;
 #pragma unroll
   for (int r = 0; r < kRowsPerThread; ++r) {
-    sr[r] = sr[r] + kh[i0 + r] * delta;
-    Sp[(size_t)(i0 + r) * a.dv] = sr[r];
-    op += sr[r] * qh[i0 + r];
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      sr[r][u] = sr[r][u] + kh[i0 + r] * delta[u];
+      op[u] += sr[r][u] * qh[i0 + r];
+    }
+    if constexpr (VW == 4) {
+      *(float4*)(Sp + (size_t)(i0 + r) * a.dv) = make_float4(sr[r][0], sr[r][1], sr[r][2], sr[r][3]);
+    } else {
+      Sp[(size_t)(i0 + r) * a.dv] = sr[r][0];
+    }
   }
-  red[ig * kCS + j] = op;
+#pragma unroll
+  for (int u = 0; u < VW; ++u) red[ig * CS + j0 + u] = op[u];
   __syncthreads();
-  if (ig == 0) {
+  if (tid < CS) {
     float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRowGroups; ++i) o += red[i * kCS + j];
-    a.o[(size_t)b * a.ld_o + h * a.dv + slice * kCS + j] = o;
+    for (int i = 0; i < kRowGroups; ++i) o += red[i * CS + tid];
+    a.o[(size_t)b * a.ld_o + h * a.dv + slice * CS + tid] = o;
   }
   if (!a.head_ctr) return;
   // the last slice of (b, h) to get here advances the head's conv state: [s1, s2, x]
@@ -200,17 +230,23 @@ int gdn_step_launch(const GdnCall& c, hipStream_t st) {
   if ((!c.qkv && !c.qkv_f) || !c.conv_state || !c.conv_w || !c.S || !c.o) return fail(Q35_E_ARG, "gdn_step: null pointer");
   if (!c.bg && !(c.ba_f && c.a_log && c.dt_bias)) return fail(Q35_E_ARG, "gdn_step: need bg, or ba_f with a_log and dt_bias");
   if (c.dk != kDk) return fail(Q35_E_SHAPE, "gdn_step: key head dim must be 128");
-  if (c.dv <= 0 || (c.dv % kCS) != 0) return fail(Q35_E_SHAPE, "gdn_step: value head dim must be a multiple of 32");
+  if (c.dv <= 0 || (c.dv % 32) != 0) return fail(Q35_E_SHAPE, "gdn_step: value head dim must be a multiple of 32");
   if (c.conv_k != 4) return fail(Q35_E_SHAPE, "gdn_step: conv kernel must be 4");
   if (c.B < 1 || c.nh < 1) return fail(Q35_E_SHAPE, "gdn_step: B and heads must be >= 1");
   GdnArgs a;
   a.c = c;
   a.key_dim = c.nh * c.dk;
   a.conv_dim = 2 * a.key_dim + c.nh * c.dv;
-  a.nslice = c.dv / kCS;
   a.qscale = powf((float)c.dk, -0.5f);
+  // whole-head blocks (128 columns, a float4 per thread and row: long row segments, the head's
+  // q / k conv and norms done once) when there are enough of them to fill the GPU; 32-column
+  // slices otherwise
+  const bool wide = (c.dv % 128) == 0 && (int64_t)c.B * c.nh >= 256 &&
+                    (reinterpret_cast<uintptr_t>(c.S) & 15) == 0 && (c.dv % 4) == 0;
+  a.nslice = c.dv / (wide ? 128 : 32);
   const int grid = c.B * c.nh * a.nslice;
-  hipLaunchKernelGGL(gdn_step_kernel, dim3(grid), dim3(kThreads), 0, st, a);
+  if (wide) hipLaunchKernelGGL(gdn_step_kernel<128>, dim3(grid), dim3(kThreads), 0, st, a);
+  else hipLaunchKernelGGL(gdn_step_kernel<32>, dim3(grid), dim3(kThreads), 0, st, a);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
