@@ -532,17 +532,19 @@ Q35_DEV void dma16(const void* src, void* dst) {
   __builtin_amdgcn_global_load_lds((const Q35_GLOBAL void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
 
-// 16 rows (M <= 16) per launch; the split x rows are copied into LDS whole, once.
+// R rows (M <= R: 16, or 8 so that two blocks fit a CU's LDS) per launch; the split x rows are
+// copied into LDS whole, once (lanes of rows past R read row R - 1; their outputs are dropped).
+template <int R>
 __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
-  __shared__ __align__(16) _Float16 xs[2][16 * kNLd];  // hi, lo planes
+  __shared__ __align__(16) _Float16 xs[2][R * kNLd];  // hi, lo planes
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int nbase = (int)blockIdx.x * 256 + 64 * w;  // this wave's 64 vocab rows
   const int nround = a.K / kRound;
 
   // x rows into LDS: segments of 512 halves (one wave instruction each); rows past M repeat M - 1
-  const int spr = a.K / 512, nseg = 2 * 16 * spr;
+  const int spr = a.K / 512, nseg = 2 * R * spr;
   for (int sgi = w; sgi < nseg; sgi += 4) {
-    const int pl = sgi / (16 * spr), rem = sgi % (16 * spr), m = rem / spr, k = (rem % spr) * 512;
+    const int pl = sgi / (R * spr), rem = sgi % (R * spr), m = rem / spr, k = (rem % spr) * 512;
     const _Float16* src = (pl ? a.xl : a.xh) + (size_t)min(m, a.M - 1) * a.ld16 + k + 8 * lane;
     dma16(src, &xs[pl][m * kNLd + k]);
   }
@@ -584,8 +586,8 @@ __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
         h8 bh[2], bl[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          bh[s] = *(const h8*)&xs[0][c * kNLd + kl + 8 * s];
-          bl[s] = *(const h8*)&xs[1][c * kNLd + kl + 8 * s];
+          bh[s] = *(const h8*)&xs[0][min(c, R - 1) * kNLd + kl + 8 * s];
+          bl[s] = *(const h8*)&xs[1][min(c, R - 1) * kNLd + kl + 8 * s];
         }
         f4 tb[4];
 #pragma unroll
@@ -915,7 +917,8 @@ int mb_lm_head_launch(const int8_t* q, const float* sT, int32_t V, int32_t K, co
   for (int m0 = 0; m0 < M; m0 += 16) {  // 16 rows per pass over the table
     MbnArgs a{q, sT, V, K, std::min(16, M - m0), yh + (size_t)m0 * K, yl + (size_t)m0 * K, K, invf + m0,
               y + (size_t)m0 * ldy, ldy};
-    hipLaunchKernelGGL(mbn_kernel, grid, dim3(kT), 0, st, a);
+    if (a.M <= 8) hipLaunchKernelGGL(mbn_kernel<8>, grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(mbn_kernel<16>, grid, dim3(kT), 0, st, a);
   }
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
