@@ -283,6 +283,7 @@ def attn_leg(torch, q35, st):
     return out
 
 
+PREFILL_PASSES = 5  # timed prompt passes (mean reported)
 MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix-core peak
 
@@ -585,19 +586,27 @@ def main():
             c0 += n
         m.check(stream=sh)
         pre_tok_s_decode = n_pre / (time.time() - t0)
-    m.reset()
-    m.prefill(prompt, stream=sh)
+    # three untimed passes (buffers, then the clocks settle: successive passes ran 7.0 -> 6.6 ms),
+    # then PREFILL_PASSES timed passes, each from a reset model; the mean is reported
+    for _ in range(3):
+        m.reset()
+        m.prefill(prompt, stream=sh)
     torch.cuda.synchronize()
-    m.reset()
-    torch.cuda.synchronize()
-    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    pe0.record(st)
-    m.prefill(prompt, stream=sh)
-    pe1.record(st)
-    pe1.synchronize()
-    prefill_wall_s = time.perf_counter() - t0
-    prefill_ms = pe0.elapsed_time(pe1)
+    prefill_pass_ms = []
+    prefill_wall_s = None
+    for _ in range(PREFILL_PASSES):
+        m.reset()
+        torch.cuda.synchronize()
+        pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        pe0.record(st)
+        m.prefill(prompt, stream=sh)
+        pe1.record(st)
+        pe1.synchronize()
+        if prefill_wall_s is None:
+            prefill_wall_s = time.perf_counter() - t0
+        prefill_pass_ms.append(pe0.elapsed_time(pe1))
+    prefill_ms = float(np.mean(prefill_pass_ms))
     for n in launch_plan(n_warm, chunk):
         m.decode(n, mode="persistent", stream=sh)
     m.check(stream=sh)
@@ -688,6 +697,7 @@ def main():
         "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
         "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
         "prefill": {"tokens": n_pre, "ms": round(prefill_ms, 3), "tok_s": round(n_pre / (prefill_ms * 1e-3), 1),
+                    "timed_passes_ms": [round(x, 3) for x in prefill_pass_ms],
                     "wall_ms_incl_prompt_upload": round(prefill_wall_s * 1e3, 3),
                     "path": "one forward at seq_len = prompt: Q8F GEMMs on the f16 matrix cores (f32-equivalent "
                             "products), causal conv + chunked gated delta rule, causal attention; lm_head on the last "
