@@ -421,6 +421,9 @@ __global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
         xv[i][1] = *(const mf4*)(xr + 4);
       }
       __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink each read to its use)
+      // the wave issues its MFMAs at raised priority, so that the SIMD's other waves fill the
+      // MFMAs' shadow with their vector-ALU work rather than delay them (4-5% on the prompt GEMMs)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const mf4 x0 = xv[i][0], x1 = xv[i][1];
@@ -437,6 +440,7 @@ __global__ __launch_bounds__(kGT, 2) void hgemm_kernel(const GArgs a) {
         for (int nt = 0; nt < 4; ++nt) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[nt], bl, acc[nt][i], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (kb + 1 < nsteps) xstore(buf ^ 1);
     __syncthreads();
   }
