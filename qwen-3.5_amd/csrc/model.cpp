@@ -167,26 +167,31 @@ int setup_persistent(q35_model* m) {
     s.gate_q = L.gate.q; s.gate_s = L.gate.s; s.up_q = L.up.q; s.up_s = L.up.s; s.down_q = L.down.q; s.down_s = L.down.s;
   }
   StepLayer* dl = nullptr;
-  uint32_t *bar = nullptr, *err = nullptr;
-  float *att_ml = nullptr, *att_o = nullptr, *arg_v = nullptr;
-  int32_t* arg_i = nullptr;
-  fx_t *gate_acc = nullptr, *h_sp = nullptr;
-  const size_t gate_n = (size_t)2 * nh * kStepBaStride;
+  uint32_t *err = nullptr, *tokseq = nullptr;
+  uint64_t *att_ml = nullptr, *att_o = nullptr, *argp = nullptr;
+  fx_t *acc = nullptr, *h_sp = nullptr;
+  // per layer: projection outputs | gate|up | in_proj_b|a sums (each sum on its own cache line)
+  const int64_t gu_off = ((int64_t)m->acc_proj_n + 15) / 16 * 16, ba_off = gu_off + 2 * (int64_t)d.ffn;
+  const int64_t acc_stride = ba_off + 2 * (int64_t)nh * kStepBaStride;
   int rc;
   if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
-      (rc = dev_alloc_t(m, "step_barrier", kStepBarBytes / 4, &bar)) ||
       (rc = dev_alloc_t(m, "step_error", 1, &err)) ||
-      (rc = dev_alloc_t(m, "step_gate_acc", gate_n, &gate_acc)) ||
-      (rc = dev_alloc_t(m, "step_h", (size_t)2 * d.hidden, &h_sp)) ||
-      (rc = dev_alloc_t(m, "attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
-      (rc = dev_alloc_t(m, "attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
-      (rc = dev_alloc_t(m, "argmax_partial_v", (size_t)grid, &arg_v)) ||
-      (rc = dev_alloc_t(m, "argmax_partial_i", (size_t)grid, &arg_i)))
+      (rc = dev_alloc_t(m, "step_tokseq", 1, &tokseq)) ||
+      (rc = dev_alloc_t(m, "step_acc", (size_t)2 * d.n_layers * acc_stride, &acc)) ||
+      (rc = dev_alloc_t(m, "step_h", (size_t)2 * 2 * d.hidden, &h_sp)) ||
+      (rc = dev_alloc_t(m, "step_attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
+      (rc = dev_alloc_t(m, "step_attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
+      (rc = dev_alloc_t(m, "step_argmax_partial", (size_t)2 * grid, &argp)))
     return rc;
   Q35_HIP_TRY(hipMemcpy(dl, hl.data(), hl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
-  Q35_HIP_TRY(hipMemset(bar, 0, kStepBarBytes));
+  // counted accumulators, tags and the token counter start from zero (a model reset clears them again)
   Q35_HIP_TRY(hipMemset(err, 0, sizeof(uint32_t)));
-  Q35_HIP_TRY(hipMemset(gate_acc, 0, gate_n * sizeof(fx_t)));  // the step kernel keeps it zero between layers
+  Q35_HIP_TRY(hipMemset(tokseq, 0, sizeof(uint32_t)));
+  Q35_HIP_TRY(hipMemset(acc, 0, (size_t)2 * d.n_layers * acc_stride * sizeof(fx_t)));
+  Q35_HIP_TRY(hipMemset(h_sp, 0, (size_t)4 * d.hidden * sizeof(fx_t)));
+  Q35_HIP_TRY(hipMemset(att_ml, 0, (size_t)kvh * nmax * 8 * sizeof(uint64_t)));
+  Q35_HIP_TRY(hipMemset(att_o, 0, (size_t)kvh * nmax * 4 * 256 * sizeof(uint64_t)));
+  Q35_HIP_TRY(hipMemset(argp, 0, (size_t)2 * grid * sizeof(uint64_t)));
   StepArgs& a = m->step_args;
   a.layers = dl; a.n_layers = d.n_layers;
   a.H = d.hidden; a.F = d.ffn; a.V = d.vocab; a.nh = nh; a.dk = d.lin_dk; a.dv = d.lin_dv;
@@ -198,23 +203,16 @@ int setup_persistent(q35_model* m) {
   step_plan(d, grid, a.mv);
   a.emb_q = m->embed.q; a.emb_s = m->embed.s; a.final_norm = m->final_norm;
   a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-  // The residual stream gets a buffer of its own with every 128-byte line on a 256-byte slot:
-  // each out / down / o stage adds 256 blocks' partials into it, and 16 consecutive lines took
-  // those atomics about 1.8x as long as lines spread this way.  Each token's first stage
-  // rewrites it from the embedding, so nothing is carried over between tokens.
-  a.h = h_sp; a.acc_proj = m->acc_proj; a.acc_ba = gate_acc; a.acc_gu = m->acc_gu;
-  a.acc_zero_n = m->acc_proj_n;
+  // The residual stream gets buffers of its own (one per token parity) with every 128-byte line
+  // on a 256-byte slot: each out / down / o stage adds 256 blocks' partials into it, and 16
+  // consecutive lines took those atomics about 1.8x as long as lines spread this way.
+  a.h = h_sp; a.acc = acc; a.acc_stride = acc_stride; a.acc_gu_off = gu_off; a.acc_ba_off = ba_off;
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
-  a.logits = m->logits; a.arg_v = arg_v; a.arg_i = arg_i;
+  a.logits = m->logits; a.argp = argp; a.tokseq = tokseq;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
   a.ord = make_arg_order(d.vocab);
-  a.bar = bar;
-  a.bar_base = 0;
   a.err = err;
   a.ntok = 0;
-  m->bar_epoch = 0;
-  m->bar_per_token = step_barriers_per_token(d);
-  a.bar_per_token = m->bar_per_token;
   a.n_stop = 0;
   for (int j = 0; j < 4; ++j) a.stop_ids[j] = -1;
   return Q35_OK;
@@ -244,7 +242,8 @@ int capture(q35_model* m, hipStream_t st) {
   return Q35_OK;
 }
 
-const char* kStepFailed = "persistent step: a grid barrier timed out; the model state is invalid until q35_model_reset";
+const char* kStepFailed = "persistent step: a wait for another block's results timed out; the model state is invalid until q35_model_reset";
+const char* kStepRange = "persistent step: a value to be accumulated in fixed point was not finite or |v| >= 2^22; the model state is invalid until q35_model_reset";
 
 // n consecutive steps in one launch of the persistent kernel.  The barrier base is the number of
 // barriers every earlier launch passed; a launch that fails (its error word set) leaves later
@@ -253,16 +252,14 @@ const char* kStepFailed = "persistent step: a grid barrier timed out; the model 
 // caller then re-reads the device position (sync_pos).
 int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nullptr, int n_stop = 0) {
   if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
-  if (m->step_failed) return fail(Q35_E_HIP, kStepFailed);
+  if (m->step_failed) return fail(Q35_E_HIP, m->step_fail_msg);
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
   StepArgs a = m->step_args;
   a.ntok = n;
-  a.bar_base = m->bar_epoch;
   a.n_stop = n_stop;
   for (int j = 0; j < n_stop; ++j) a.stop_ids[j] = stop_ids[j];
   int rc = step_launch(a, m->step_grid, st);
   if (rc) return rc;
-  m->bar_epoch += (uint32_t)n * (uint32_t)m->bar_per_token;
   m->host_pos += n;
   return Q35_OK;
 }
@@ -289,6 +286,16 @@ SeqView model_view(q35_model* m) {
 
 int ensure_prefill(q35_model* m, hipStream_t st) {
   int rc;
+  {
+    // Checked before anything is allocated or launched: the chunked delta rule's state and
+    // output strides are fixed at 128 x 128 per head, and every prompt GEMM width (hidden, ffn,
+    // conv_dim, value dim, 2 * attn_heads * 256, kv_heads * 256) must be a multiple of 128.
+    const q35_dims& d = m->d;
+    if (d.lin_dk != 128 || d.lin_dv != 128)
+      return fail(Q35_E_SHAPE, "prompt path: linear-attention heads need dk = dv = 128");
+    if (d.hidden % 128 || d.ffn % 128)
+      return fail(Q35_E_SHAPE, "prompt path: hidden and ffn must be multiples of 128");
+  }
   if ((rc = ensure_mb(m, st))) return rc;  // the projections' GEMMs read the MB copies
   if (m->pf_cap > 0) return Q35_OK;
   const q35_dims& d = m->d;
@@ -460,12 +467,13 @@ int prefill(q35_model* m, int n, hipStream_t st) {
 // Reads the persistent kernel's sticky error word (synchronises the stream).
 int check_persistent(q35_model* m, hipStream_t st) {
   if (m->step_rc != Q35_OK) return Q35_OK;
-  if (m->step_failed) return fail(Q35_E_HIP, kStepFailed);
+  if (m->step_failed) return fail(Q35_E_HIP, m->step_fail_msg);
   Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 8, m->step_args.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
   Q35_HIP_TRY(hipStreamSynchronize(st));
   if (m->pinned[8] != 0) {
     m->step_failed = true;
-    return fail(Q35_E_HIP, kStepFailed);
+    m->step_fail_msg = (m->pinned[8] & kStepErrRange) ? kStepRange : kStepFailed;
+    return fail(Q35_E_HIP, m->step_fail_msg);
   }
   return Q35_OK;
 }
@@ -674,12 +682,12 @@ int q35_model_reset(q35_model* m, void* stream) {
     const bool state = n.find("conv_state") != std::string::npos || n.find("recurrent_state") != std::string::npos ||
                        n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
                        n == "token" || n == "pos" || n == "plen" || n == "hist" || n == "prompt" ||
-                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_gate_acc" || n == "step_h" ||
-                       n == "step_barrier" || n == "step_error";
+                       n == "h" || n == "acc_proj" || n == "acc_gu" || n == "step_h" || n == "step_acc" ||
+                       n == "step_tokseq" || n == "step_argmax_partial" || n == "step_attn_partial_ml" ||
+                       n == "step_attn_partial_o" || n == "step_error";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
   m->host_pos = 0;
-  m->bar_epoch = 0;
   m->step_failed = false;
   return Q35_OK;
 }

@@ -46,9 +46,8 @@ struct q35_model {
   int step_rc = Q35_OK;  // why the persistent kernel cannot run here, if it cannot
   std::string step_msg;
   q35::StepArgs step_args{};
-  uint32_t bar_epoch = 0;  // grid barriers passed by all launches since the counters were zeroed
-  int bar_per_token = 0;   // grid barriers per decode step
   bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
+  const char* step_fail_msg = "";
   // prompt path (allocated on first use): up to pf_cap tokens per pass
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;

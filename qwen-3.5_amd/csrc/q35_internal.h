@@ -686,42 +686,38 @@ struct StepArgs {
   StepMv mv[SMV_COUNT];
   const int8_t* emb_q; const float* emb_s; const float* final_norm;
   const float *rope_cos, *rope_sin;
-  fx_t* h;  // residual stream: value k at k + (k & ~15), i.e. one 128-byte line of 16 per 256 bytes
-  fx_t *acc_proj, *acc_gu;
-  fx_t* acc_ba;        // in_proj_b | in_proj_a sums, one per kStepBaStride entries (own cache line)
-  int64_t acc_zero_n;  // acc_proj entries cleared by the gate|up stage
-  float *att_ml, *att_o;
-  int32_t att_nmax;    // attention chunks per kv head
-  float* logits;       // may be null
-  float* arg_v; int32_t* arg_i;  // per-block argmax partials [grid]
+  // Counted fixed-point accumulators (value * 2^32 plus one 2^56 per contribution; see step.hip),
+  // one set per token parity: token t uses set t & 1, and the lm stage of token t clears the
+  // other set for token t + 1.
+  fx_t* h;              // [2][2 * H] residual stream: value k at k + (k & ~15) (one 128-byte line per 256 bytes)
+  fx_t* acc;            // [2][n_layers][acc_stride] per layer: projections | gate|up | in_proj_b|a sums
+  int64_t acc_stride;   // fx_t entries per layer
+  int64_t acc_gu_off, acc_ba_off;  // offsets of the gate|up and the b|a sums inside a layer's entries
+  // Attention partials, tagged: (tag << 32) | f32 bits, tag = a number unique to the token and layer
+  uint64_t *att_ml, *att_o;
+  int32_t att_nmax;     // attention chunks per kv head
+  float* logits;        // may be null
+  uint64_t* argp;       // per-block argmax partials [2][grid] (token parity): tag (14 bits) | index (18 bits) | f32 value
+  uint32_t* tokseq;     // tokens the kernel has run since the last model reset (selects the parity set)
   int32_t *token, *pos, *prompt, *plen, *hist;
-  ArgOrder ord;        // the reference's argmax order over the vocabulary
+  ArgOrder ord;         // the reference's argmax order over the vocabulary
   // Stop ids (main.rs:108-110): a generated step (position >= plen) whose input token is one of
   // them is not run; the launch ends there (pos = that position, token = the stop id).
   int32_t stop_ids[4];
   int32_t n_stop;
-  int32_t bar_per_token;  // grid barriers per step (so a stopped launch can settle its counters)
-  // Barrier counters (kStepBarBytes).  They are never cleared between launches: each launch
-  // passes bar_base, the number of grid barriers completed by all earlier launches since the
-  // counters were last zeroed (model reset), and waits for counter values relative to it
-  // (wrapping uint32 arithmetic).  So a launch needs no memset (nothing to record in a graph).
-  uint32_t* bar;
-  uint32_t bar_base;
-  // Sticky error word (its own allocation, cleared only by a model reset): set when a barrier
-  // wait times out; every launch that finds it set at entry returns at once without touching
-  // any state, so one failure cannot be followed by launches that compute on a broken state.
+  // Sticky error word (its own allocation, cleared only by a model reset): bit 0 is set when a
+  // wait for another block's results times out, bit 1 when a value to be accumulated in fixed
+  // point is not finite or too large (|v| >= 2^22).  Every launch that finds it set at entry
+  // returns at once without touching any state, so one failure cannot be followed by launches
+  // that compute on a broken state.
   uint32_t* err;
   int32_t ntok;
 };
-constexpr size_t kStepBarBytes = 16384;
+constexpr uint32_t kStepErrTimeout = 1u, kStepErrRange = 2u;
 // Every block of the qkvz stage adds into the 2 x lin_heads gate accumulators; packed, they
 // would share two cache lines and the atomics would serialise on them.
 constexpr int kStepBaStride = 16;  // fx_t entries (128 bytes)
 constexpr int kStepThreads = 512;
-// Grid barriers one decode step of the persistent kernel passes: 4 per linear-attention layer
-// (qkvz, out, gate|up, down), 5 per full-attention layer (qkv, attn, o, gate|up, down), 1 for
-// the lm_head.
-int step_barriers_per_token(const q35_dims& d);
 // Blocks of the persistent kernel that fit co-resident (one per CU); 0 if the kernel cannot run.
 int step_grid(int hidden);
 // Attention chunks per kv head for a grid (the merge keeps their weights in LDS).

@@ -1,14 +1,13 @@
 // Persistent decode step: the whole TextForCausalLM forward at seq_len 1 (model.rs:27-84,
 // 113-129) plus the greedy argmax (main.rs:131), for `ntok` consecutive tokens, in ONE launch.
 //
-// Why: a decode step streams ~2 GB of Q8F weights through ~120 dependent stages.  As separate
+// Why: a decode step streams ~2 GB of Q8F weights through ~100 dependent stages.  As separate
 // kernels every stage boundary costs a launch gap plus a ramp-up/drain with HBM idle; here the
-// grid is one co-resident block per CU (cooperative launch) and stages are separated by a grid
-// barrier.  Each block issues the weight loads of its next stage *between* arriving at the
-// barrier and polling it, so the weight stream of stage s+1 overlaps the barrier latency and
-// the tail of stage s.
+// grid is one co-resident block per CU (cooperative launch) that runs every stage.  Each block
+// issues the weight loads of its next stage as soon as it has published its part of the current
+// one, so the weight stream of stage s+1 overlaps the tail of stage s.
 //
-// Stages per token (each ends with a grid barrier):
+// Stages per token (each consumes the outputs of the one before):
 //   linear-attention layer: qkvz  [RMSNorm(h) or embedding -> in_proj_qkv|in_proj_z; in_proj_b|a]
 //                           out   [conv1d + SiLU, l2norm, gated delta rule step, gated
 //                                  RMSNorm(o, z) -> out_proj -> +h]
@@ -27,14 +26,29 @@
 // value exchanged between blocks inside the launch is written with agent-scope atomics or
 // sc1 stores and read with sc1 loads (no stale per-CU / per-XCD cache lines).
 //
-// Barrier: blocks arrive on one of 32 group counters (blockIdx % 32) with a non-returning
-// atomic after their stores have completed; the waiting wave reads all group counters with one
-// load per lane.  Counters only grow (they are zeroed by a model reset, never by a launch); the
-// launch is told how many barriers earlier launches passed (bar_base), so the target of its
-// n-th barrier is (blocks in group) * (bar_base + n), compared in wrapping uint32 arithmetic.
-// Every wait is bounded: on time-out the block sets the sticky error word and returns, and the
-// other blocks see the word and return too, so the grid always drains; a later launch that
-// finds the word set returns at entry.
+// Synchronisation: there is no grid barrier.  Every value one block hands to another carries its
+// own completion state, and the consumer spins on the data itself:
+//  * split-K accumulators (residual stream, projection outputs) are counted fixed point: each
+//    contribution adds value * 2^32 + 2^56, so the top byte counts contributions (modulo 256) and
+//    a word is complete when it holds the number of contributions its stage makes (every item
+//    of a stage adds once to each column of its tile, so that number is the stage's chunk count);
+//  * values that are stored rather than added (attention partials, argmax partials) carry a tag
+//    unique to the token and layer that wrote them.
+// A consumer issues its next stage's weight loads, then its inputs; when an input is not yet
+// complete, the wave polls one incomplete word (one load per poll) and then re-reads.  That is
+// one memory round trip from the last producer's add to the consumer's data, where an arrive
+// (after the adds' acknowledgements), a barrier poll and a separate input read took three.
+// Ordering of the plain stores that are not tagged (KV rows, DeltaNet states, the clearing of
+// the next token's accumulators) follows from the data: a block waits for its stores to
+// complete before its next published contribution, and every later reader of them first
+// observes that contribution (or one that depends on it).  Accumulators are never re-used
+// within a token (one set per layer), and the lm stage of token t clears the set of token t + 1
+// (token parity); every block reads all argmax partials of token t before it starts token t + 1,
+// so the clearing is complete before any block adds into that set.
+// Every wait is bounded: on time-out a block sets the sticky error word and returns; other
+// blocks poll the word while they wait and return too, so the grid always drains; a later
+// launch that finds the word set returns at entry.  The launch is cooperative only so that all
+// blocks are co-resident (a block that waits needs its producers running).
 #include "q35_internal.h"
 
 #include <algorithm>
@@ -51,9 +65,7 @@ constexpr int kRG = kT / 16;      // matvec row groups (16 lanes cover a 256-byt
 constexpr int kU = 16;            // rows per lane per item
 constexpr int kKch = kRG * kU;    // rows per item, at most 512
 constexpr int kRmsRegs = 8;       // RMSNorm prologue: K <= 8 * 512
-constexpr int kGroups = 32;       // barrier counters
-constexpr int kCtrStride = 64;    // uint32 words between counters (own 256-byte line each)
-constexpr uint32_t kSpin = 1u << 20;
+constexpr uint32_t kSpin = 1u << 21;  // polls before a wait gives up (seconds)
 constexpr int kHd = 256;          // attention head dim
 constexpr int kMaxRep = 4;        // query heads per kv head
 constexpr int kMaxChunk = 256;    // cached tokens per attention item
@@ -66,6 +78,8 @@ constexpr int kGdnG = kStepThreads / kDv;  // DeltaNet state row groups (4)
 constexpr int kGdnR = kDk / kGdnG;         // DeltaNet state rows per thread (32)
 constexpr int kSmem = 12288;      // floats of LDS shared by all stages (48 KB)
 constexpr int kMergeB = 16;       // attention-merge partials loaded per batch
+constexpr int kArgIdxBits = 18;   // argmax partial: index bits (vocabulary < 2^18)
+constexpr uint32_t kArgNone = (1u << kArgIdxBits) - 1;
 
 // LDS carve-up (float offsets)
 constexpr int kXs = 0;                  // matvec x chunk [kKch]
@@ -94,7 +108,7 @@ struct Shared {
   float* shs;  // [kNW] block sums
   float* shv;  // [kNW] argmax values
   int* shi;    // [kNW] argmax indices
-  int* ok;
+  int* fail;   // set by any wave whose wait failed (time-out or error word); read after a barrier
 };
 
 // ------------------------------------------------------------------ block reductions
@@ -130,57 +144,100 @@ Q35_DEV float wave_max(float v) {
   return v;
 }
 
-Q35_DEV float4 ld4_agent(const float* p) {
-  return make_float4(ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3));
+Q35_DEV uint64_t ld_agent64(const uint64_t* p) {
+  return __hip_atomic_load((Q35_GLOBAL uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-Q35_DEV float4 ld4_fx(const fx_t* p) {
-  const fx_t a = ld_agent(p), b = ld_agent(p + 1), c = ld_agent(p + 2), d = ld_agent(p + 3);
-  return make_float4(from_fx(a), from_fx(b), from_fx(c), from_fx(d));
-}
-
-// ------------------------------------------------------------------ grid barrier
-struct Bar {
-  uint32_t* ctr;
-  uint32_t* err;
-  uint32_t epoch;  // barriers passed so far by this block, counted from the counters' last reset
-};
-
-// Publishes this block's completion of the current stage: all of its memory operations are
-// complete (s_waitcnt 0 in every wave, then the workgroup barrier) before the counter add.
-Q35_DEV void bar_arrive(Bar& b) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tix() == 0)
-    __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&b.ctr[(bix() % kGroups) * kCtrStride], 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  b.epoch += 1;
+Q35_DEV void st_agent64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store((Q35_GLOBAL uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waits until every block has arrived `epoch` times.  Wave 0 polls: lane g < 32 reads group
-// counter g.  Returns false (in every thread of the block) on time-out or when another block
-// has raised the error word.
-Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
-  if (tix() < 64) {
-    const int g = tix();
-    const uint32_t nb = gridDim.x;
-    const uint32_t per = g < kGroups ? (nb + kGroups - 1 - (uint32_t)g) / kGroups : 0u;
-    const uint32_t target = per * b.epoch;  // wraps; compared as a signed difference below
-    uint32_t spin = 0;
-    bool ok = true;
-    while (true) {
-      const uint32_t v = g < kGroups ? ld_agent(&b.ctr[g * kCtrStride]) : target;
-      const uint32_t e = ld_agent(b.err);
-      if (__all((int32_t)(v - target) >= 0)) break;
-      if (e != 0u || ++spin > kSpin) { ok = false; break; }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    if (tix() == 0) {
-      if (!ok) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)b.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *sh_ok = ok ? 1 : 0;
-    }
+// ------------------------------------------------------------------ counted words and tags
+// A counted accumulator word: two's complement value * 2^32 plus (contributions mod 256) * 2^56.
+// With |value| < 2^23 the word minus e * 2^56 lies in (-2^55, 2^55) exactly when it holds e
+// contributions, and it is then the value itself.
+Q35_DEV uint64_t cnt_of(uint32_t e) { return (uint64_t)e << 56; }
+Q35_DEV bool fxc_ok(fx_t w, uint32_t e) { return ((uint64_t)w - cnt_of(e) + (1ull << 55)) < (1ull << 56); }
+Q35_DEV float fxc_val(fx_t w, uint32_t e) { return from_fx((fx_t)((uint64_t)w - cnt_of(e))); }
+
+Q35_DEV void raise_err(const StepArgs& a, uint32_t bit) {
+  __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)a.err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One contribution v to a counted word (fire-and-forget agent-scope atomic).  A value that is not
+// finite or whose magnitude reaches 2^22 (the total must stay below 2^23) is not added: it sets
+// the range bit of the error word, which the host reports after the launch.
+Q35_DEV void fxc_add(const StepArgs& a, fx_t* p, float v) {
+  if (!(fabsf(v) < 4194304.0f)) {
+    raise_err(a, kStepErrRange);
+    v = 0.f;
   }
-  __syncthreads();
-  return *sh_ok != 0;
+  __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v) + (1ull << 56),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged f32 (attention partials): (tag << 32) | bits
+Q35_DEV uint64_t tagged(float v, uint32_t tag) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
+Q35_DEV bool tag_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+Q35_DEV float tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
+// Tag of the attention partials of token ti, layer l (never 0, the value of a cleared buffer,
+// for the first tokens after a reset)
+Q35_DEV uint32_t att_tag(const StepArgs& a, uint32_t ti, int l) { return ti * (uint32_t)a.n_layers + (uint32_t)l + 1u; }
+// Argmax partial of token ti: tag (14 bits) | index (18 bits) | f32 value
+Q35_DEV uint32_t arg_tag(uint32_t ti) { return (ti + 1u) & 0x3fffu; }
+Q35_DEV uint64_t arg_pack(float v, int i, uint32_t ti) {
+  const uint32_t ix = (i == INT_MAX) ? kArgNone : (uint32_t)i;
+  return ((uint64_t)arg_tag(ti) << 50) | ((uint64_t)ix << 32) | __float_as_uint(v);
+}
+Q35_DEV bool arg_ok(uint64_t w, uint32_t ti) { return (uint32_t)(w >> 50) == arg_tag(ti); }
+Q35_DEV void arg_unpack(uint64_t w, float& v, int& i) {
+  const uint32_t ix = (uint32_t)(w >> 32) & kArgNone;
+  v = __uint_as_float((uint32_t)w);
+  i = (ix == kArgNone) ? INT_MAX : (int)ix;
+}
+
+Q35_DEV const void* readlane_ptr(const void* p, int lane) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, lane), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), lane);
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+
+// Polls one word (the same address in every lane, so one load per poll) until ready(word).
+// Returns false once the error word is set or after kSpin polls (then it sets the time-out bit).
+template <class Ready>
+Q35_DEV bool wait_on(const StepArgs& a, const uint64_t* p, Ready ready) {
+  for (uint32_t n = 1;; ++n) {
+    if (ready(ld_agent64(p))) return true;
+    if ((n & 31) == 0) {
+      if (ld_agent(a.err) != 0u) return false;
+      if (n >= kSpin) {
+        raise_err(a, kStepErrTimeout);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Completes a thread's N input words w (loaded once already): test(j, w[j]) says whether word j
+// is complete, load_all(w) reloads every word (addresses recomputed, so nothing extra stays live
+// in registers), addr(j) is the address of word j (j wave-uniform).  While some lane of the wave
+// has an incomplete word, the wave polls the first such word, then reloads.  Wave-level (no
+// workgroup barrier); returns false on error / time-out.
+template <int N, class W, class LoadAll, class Addr, class Test>
+Q35_DEV bool gather(const StepArgs& a, W (&w)[N], LoadAll load_all, Addr addr, Test test) {
+  while (true) {
+    int jf = N;
+#pragma unroll
+    for (int j = N - 1; j >= 0; --j)
+      if (!test(j, (uint64_t)w[j])) jf = j;
+    const uint64_t bad = __ballot(jf < N);
+    if (bad == 0) return true;
+    const int lf = __ffsll((unsigned long long)bad) - 1;
+    const int jw = __builtin_amdgcn_readlane(jf, lf);
+    const uint64_t* pw = static_cast<const uint64_t*>(readlane_ptr(addr(jw), lf));
+    if (!wait_on(a, pw, [&](uint64_t x) { return test(jw, x); })) return false;
+    load_all(w);
+  }
 }
 
 // The layer table is never written by the kernel: read through the constant address space, its
@@ -188,6 +245,15 @@ Q35_DEV bool bar_wait(const Bar& b, int* sh_ok) {
 // the weight stream and force vmcnt waits.
 typedef const __attribute__((address_space(4))) StepLayer CLayer;
 Q35_DEV CLayer& layer_at(const StepArgs& a, int l) { return *(CLayer*)(a.layers + l); }
+
+// Per token and layer: where this token's counted accumulators are and what a complete word holds.
+struct Tok {
+  fx_t* h;       // residual stream of this token (parity set)
+  fx_t* acc;     // this layer's accumulators (parity set)
+  uint32_t hc;   // contributions a complete residual word holds at this point of the token
+  uint32_t ti;   // tokens run since the last reset, this one included (minus 1)
+  int l;         // layer
+};
 
 // ------------------------------------------------------------------ matvec stages
 struct Mv {
@@ -202,45 +268,46 @@ struct Mv {
 
 Q35_DEV int tiles_of(int n) { return (n + kTile - 1) / kTile; }
 
-Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, int kind) {
+Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, const Tok& t, int kind) {
   Mv d{};
   const StepMv pl = a.mv[kind];
   d.kch = pl.kch;
   d.nchunk = pl.nchunk;
+  fx_t* proj = t.acc;
   switch (kind) {
     case SMV_QKVZ:
       d.K = a.H;
-      d.w0 = L.qkv_q; d.s0 = L.qkv_s; d.a0 = a.acc_proj; d.n0 = a.conv_dim;
-      d.w1 = L.z_q; d.s1 = L.z_s; d.a1 = a.acc_proj + a.conv_dim; d.n1 = a.vdim;
+      d.w0 = L.qkv_q; d.s0 = L.qkv_s; d.a0 = proj; d.n0 = a.conv_dim;
+      d.w1 = L.z_q; d.s1 = L.z_s; d.a1 = proj + a.conv_dim; d.n1 = a.vdim;
       d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2;
       break;
     case SMV_OUT:
       d.K = a.vdim;
-      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_QKV: {
       const int ldqg = a.ah * a.hd * 2, nkv = a.kvh * a.hd;
       d.K = a.H;
-      d.w0 = L.q_q; d.s0 = L.q_s; d.a0 = a.acc_proj; d.n0 = ldqg;
-      d.w1 = L.k_q; d.s1 = L.k_s; d.a1 = a.acc_proj + ldqg; d.n1 = nkv;
-      d.w2 = L.v_q; d.s2 = L.v_s; d.a2 = a.acc_proj + ldqg + nkv; d.n2 = nkv;
+      d.w0 = L.q_q; d.s0 = L.q_s; d.a0 = proj; d.n0 = ldqg;
+      d.w1 = L.k_q; d.s1 = L.k_s; d.a1 = proj + ldqg; d.n1 = nkv;
+      d.w2 = L.v_q; d.s2 = L.v_s; d.a2 = proj + ldqg + nkv; d.n2 = nkv;
       d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2 + tiles_of(d.n2);
     } break;
     case SMV_O:
       d.K = a.ah * a.hd;
-      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_GU:
       d.K = a.H;
-      d.w0 = L.gate_q; d.s0 = L.gate_s; d.a0 = a.acc_gu; d.n0 = a.F;
-      d.w1 = L.up_q; d.s1 = L.up_s; d.a1 = a.acc_gu + a.F; d.n1 = a.F;
+      d.w0 = L.gate_q; d.s0 = L.gate_s; d.a0 = t.acc + a.acc_gu_off; d.n0 = a.F;
+      d.w1 = L.up_q; d.s1 = L.up_s; d.a1 = t.acc + a.acc_gu_off + a.F; d.n1 = a.F;
       d.t1 = tiles_of(d.n0); d.t2 = d.t1 + tiles_of(d.n1); d.t3 = d.t2;
       break;
     default:  // SMV_DOWN
       d.K = a.F;
-      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = a.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
   }
@@ -295,9 +362,12 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
 
 // y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.  aux_dst
 // (optional): one more sum, of which each wave holds its part in aux, reduced with the columns.
+// wait_stores: every store the block issued before (cleared accumulators, KV rows, DeltaNet
+// states) completes before the first contribution is added, so whoever observes the
+// contributions can read what those stores wrote.
 template <int U>
-Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, float* red, float aux = 0.f,
-                        fx_t* aux_dst = nullptr) {
+Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, const float* xs, float* red,
+                        bool wait_stores, float aux = 0.f, fx_t* aux_dst = nullptr) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
@@ -336,12 +406,13 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
   }
   *reinterpret_cast<float4*>(&red[(rr >> 2) * kTile + cg * 16 + 4 * (rr & 3)]) = make_float4(t4[0], t4[1], t4[2], t4[3]);
   if (aux_dst && (tid & 63) == 0) red[kNW * kTile + (tid >> 6)] = aux;
+  if (wait_stores) __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (aux_dst && tid == 0) {
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < kNW; ++w) s += red[kNW * kTile + w];
-    fx_add(aux_dst, s);
+    fxc_add(a, aux_dst, s);
   }
   if (tid < kTile) {
     // all kNW wave partials read before any is summed: one LDS round trip
@@ -353,7 +424,7 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
 #pragma unroll
     for (int i = 0; i < kNW; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
-    if (n < it.N) fx_add(&it.acc[n + (n & it.spm)], v);
+    if (n < it.N) fxc_add(a, &it.acc[n + (n & it.spm)], v);
   }
   __syncthreads();
 }
@@ -361,82 +432,108 @@ Q35_DEV void mv_compute(const MvItem& it, const MvPf<U>& pf, const float* xs, fl
 // xs[i] = x[k0+i] * rsqrt(mean(x^2) + eps) * (1 + w[k0+i]); thread t holds x[t + 512 j],
 // j < KR (K <= 512 KR).  All loads (x and the thread's norm weights) are issued before any value
 // is used, and all KR of each (indices clamped, masked afterwards): a compile-time number of
-// loads, so the compiler's waits on them are exact.  The prologue costs one round trip:
-// `load(k)` returns the raw element, `conv` turns it into f32.  `post` (more weight loads of the
-// caller) is issued behind the prologue's loads and before their first use; scheduling barriers
-// keep the compiler from moving either group across it.
-template <int KR, class Raw, class Load, class Conv, class Post>
-Q35_DEV void pro_rms(Load load, Conv conv, int K, const float* w, float eps, int k0, int klen, float* xs,
-                     float* shs, Post post) {
+// loads, so the compiler's waits on them are exact.  The prologue costs one round trip when its
+// input is complete: `src.load(k)` returns the raw element, `src.complete` waits for incomplete
+// ones (counted inputs), `src.conv` turns it into f32.  `post` (more weight loads of the caller)
+// is issued behind the prologue's loads and before their first use; scheduling barriers keep the
+// compiler from moving either group across it.  Returns false when a wait failed.
+template <int KR, class Raw, class Src, class Post>
+Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, int K, const float* w, int k0, int klen, float* xs, float* shs,
+                     Post post) {
   const int tid = tix();
   Raw raw[KR];
   float wn[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
     const int k = tid + kT * j;
-    raw[j] = load(min(k, K - 1));
+    raw[j] = src.load(min(k, K - 1));
     wn[j] = ldg(w + min(max(k, k0), k0 + klen - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
   post();
   __builtin_amdgcn_sched_barrier(0);
+  const bool ok = src.template complete<KR>(a, raw, K);
   float v[KR];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
-    v[j] = (tid + kT * j < K) ? conv(raw[j]) : 0.f;
+    v[j] = (tid + kT * j < K) ? src.conv(raw[j]) : 0.f;
     ss += v[j] * v[j];
   }
-  // every caller reaches here right after a workgroup barrier (the stage's grid-barrier wait, or
-  // the previous item's reduction), so the block sum needs no leading one
+  // every caller reaches here right after a workgroup barrier (the stage's start, or the
+  // previous item's reduction), so the block sum needs no leading one
   ss = block_sum(ss, shs, false);
-  const float r = rsqrt_f(ss * rcp_f((float)K) + eps);
+  const float r = rsqrt_f(ss * rcp_f((float)K) + a.eps);
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
     const int k = tid + kT * j;
     if (k >= k0 && k < k0 + klen) xs[k - k0] = (v[j] * r) * (1.0f + wn[j]);
   }
+  return ok;
 }
 
-// the residual stream h (fixed point) as pro_rms input
-struct HLoad {
+// the residual stream h (counted fixed point, e contributions) as pro_rms input
+struct HSrc {
   const fx_t* h;
-  Q35_DEV fx_t operator()(int k) const { return ld_agent(h + (k + (k & ~15))); }
-};
-struct HConv {
-  Q35_DEV float operator()(fx_t x) const { return from_fx(x); }
+  uint32_t e;
+  Q35_DEV const fx_t* at(int k) const { return h + (k + (k & ~15)); }
+  Q35_DEV fx_t load(int k) const { return ld_agent(at(k)); }
+  Q35_DEV float conv(fx_t x) const { return fxc_val(x, e); }
+  template <int KR>
+  Q35_DEV bool complete(const StepArgs& a, fx_t (&raw)[KR], int K) const {
+    return gather<KR>(
+        a, raw,
+        [&](fx_t (&r)[KR]) {
+#pragma unroll
+          for (int j = 0; j < KR; ++j) r[j] = load(min(tix() + kT * j, K - 1));
+        },
+        [&](int j) { return (const void*)at(min(tix() + kT * j, K - 1)); },
+        [&](int, uint64_t w) { return fxc_ok((fx_t)w, e); });
+  }
 };
 // a row of the Q8F embedding table as pro_rms input: (byte, block scale) pairs
 struct EmbRaw {
   int8_t q;
   float s;
 };
-struct EmbLoad {
+struct EmbSrc {
   const int8_t* q;
   const float* s;
-  Q35_DEV EmbRaw operator()(int k) const { return EmbRaw{ldg(q + k), ldg(s + (k >> 6))}; }
-};
-struct EmbConv {
-  Q35_DEV float operator()(EmbRaw x) const { return (float)x.q * x.s; }
+  Q35_DEV EmbRaw load(int k) const { return EmbRaw{ldg(q + k), ldg(s + (k >> 6))}; }
+  Q35_DEV float conv(EmbRaw x) const { return (float)x.q * x.s; }
+  template <int KR>
+  Q35_DEV bool complete(const StepArgs&, EmbRaw (&)[KR], int) const { return true; }
 };
 
+// The argmax of token ti from the per-block partials (the reference's order), once all carry
+// that token's tag.  Returns false when a wait failed.
+Q35_DEV bool reduce_argmax(const StepArgs& a, uint32_t ti, const Shared& sh, int& tok) {
+  float v = -INFINITY;
+  int ix = INT_MAX;
+  const uint64_t* ap = a.argp + (size_t)(ti & 1u) * gridDim.x + min(tix(), (int)gridDim.x - 1);
+  uint64_t w[1] = {ld_agent64(ap)};
+  const bool ok = gather<1>(
+      a, w, [&](uint64_t (&x)[1]) { x[0] = ld_agent64(ap); }, [&](int) { return (const void*)ap; },
+      [&](int, uint64_t x) { return arg_ok(x, ti); });
+  if (tix() < (int)gridDim.x) arg_unpack(w[0], v, ix);
+  block_argmax(v, ix, sh.shv, sh.shi, a.ord);
+  tok = (ix == INT_MAX) ? 0 : ix;
+  return ok;
+}
+
 // Token of step i at position p: the prompt id while p < plen, else the argmax of the previous
-// step (reduced here from the per-block partials), or *token for the launch's first step.
-// Block 0 records the previous step's argmax in hist.
-Q35_DEV int select_token(const StepArgs& a, int i, int p, const Shared& sh) {
-  int tok;
+// step, or *token for the launch's first step.  Block 0 records the previous step's argmax in
+// hist.  Returns false when a wait failed.
+Q35_DEV bool select_token(const StepArgs& a, const Tok& t, int i, int p, const Shared& sh, int& tok) {
+  bool ok = true;
   if (i == 0) {
     tok = ld_agent(a.token);
   } else {
-    float v = -INFINITY;
-    int ix = INT_MAX;
-    if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
-    block_argmax(v, ix, sh.shv, sh.shi, a.ord);
-    tok = (ix == INT_MAX) ? 0 : ix;
+    ok = reduce_argmax(a, t.ti - 1, sh, tok);
     if (bix() == 0 && tix() == 0) st_agent(&a.hist[p - 1], tok);
   }
   if (p < ldg(a.plen)) tok = ldg(a.prompt + p);
-  return tok;
+  return ok;
 }
 
 // A generated step (position past the prompt) whose input token is a stop id is not run.  Every
@@ -458,8 +555,8 @@ enum { kStageFail = 0, kStageOk = 1, kStageStop = 2 };
 // keeps the rows it needs; the block holding tile 0 and the first rows of h writes the new
 // recurrent state and the shifted conv state.  Both states have two copies per layer: step i of
 // a launch reads copy i & 1 and writes the other, so that write never races the other blocks'
-// reads of the old state (their loads are issued before the barrier and may still be queued
-// behind weight loads after it).
+// reads of the old state (their loads are issued before their inputs are complete and may still
+// be queued behind weight loads).
 // text_modules.rs:134-162 (causal conv + state shift), :184-187 (l2norm), :365-443 (gated delta
 // rule), RMSNormGated: x = w[k % dv] * (o * rsqrt(mean_h(o^2) + eps)) * silu(z).
 //
@@ -490,7 +587,7 @@ Q35_DEV int gdn_channel(const StepArgs& a, int h, int t) {
   return 2 * a.key_dim + h * kDv + (t - 2 * kDk);
 }
 
-// Everything of the step that does not depend on the qkvz stage: issued before its barrier.
+// Everything of the step that does not depend on the qkvz stage: issued before its inputs.
 Q35_DEV void gdn_load(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g) {
   const int tid = tix(), j = tid % kDv, ig = tid / kDv;
   const int h = it.k0 / kDv;
@@ -510,7 +607,7 @@ Q35_DEV void gdn_load(const StepArgs& a, CLayer& L, const MvItem& it, int i, Gdn
   g.alog = ldg(L.a_log + h);
 }
 
-Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnPf& g, float* xs,
+Q35_DEV bool pro_gdn(const StepArgs& a, CLayer& L, const Tok& t, const MvItem& it, int i, GdnPf& g, float* xs,
                      float* scratch) {
   const int tid = tix(), lane = tid & 63;
   const int j = tid % kDv, ig = tid / kDv;
@@ -520,12 +617,23 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   float* part1 = part0 + kT;     // [kT]
   float* ov = part1 + kT;        // [dv] outputs of head h
   // qkvz-stage outputs: the thread's conv input, its z element and the two gate projections
+  const uint32_t e = (uint32_t)a.mv[SMV_QKVZ].nchunk;
   const int c = gdn_channel(a, h, min(tid, nch - 1));
-  const fx_t xr = ld_agent(&a.acc_proj[c]);
-  const fx_t zr = ld_agent(&a.acc_proj[a.conv_dim + it.k0 + min(tid, it.klen - 1)]);
-  const float bs = from_fx(ld_agent(&a.acc_ba[(size_t)h * kStepBaStride]));
-  const float as = from_fx(ld_agent(&a.acc_ba[(size_t)(a.nh + h) * kStepBaStride]));
-  const float x = from_fx(xr);
+  auto ad = [&](int q) -> const fx_t* {
+    const int tq = tix();
+    if (q == 0) return &t.acc[gdn_channel(a, h, min(tq, nch - 1))];
+    if (q == 1) return &t.acc[a.conv_dim + it.k0 + min(tq, it.klen - 1)];
+    return &t.acc[a.acc_ba_off + (size_t)(q == 2 ? h : a.nh + h) * kStepBaStride];
+  };
+  auto load_all = [&](fx_t (&r)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = ld_agent(ad(q));
+  };
+  fx_t in[4];
+  load_all(in);
+  const bool done = gather<4>(a, in, load_all, [&](int q) { return (const void*)ad(q); },
+                              [&](int, uint64_t w) { return fxc_ok((fx_t)w, e); });
+  const float x = fxc_val(in[0], e), zv = fxc_val(in[1], e), bs = fxc_val(in[2], e), as = fxc_val(in[3], e);
   if (tid < nch) qkv[tid] = silu_f(((g.cw[0] * g.cs[0] + g.cw[1] * g.cs[1]) + g.cw[2] * g.cs[2]) + g.cw[3] * x);
   const bool writer = it.tl == 0 && (it.k0 % kDv) == 0;  // uniform
   const GdnBuf b = gdn_buf(L, i);
@@ -569,9 +677,10 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
   // gated RMSNorm over the dv outputs of h, whose sum of squares every wave forms itself
   const float oa = ov[lane], ob = ov[lane + 64];
   const float rg = rsqrt_f(wave_sum(oa * oa + ob * ob) / (float)kDv + a.eps);
-  if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(from_fx(zr));
+  if (tid < it.klen) xs[tid] = (g.nw * (ov[it.k0 % kDv + tid] * rg)) * silu_f(zv);
   // Off the path to the out_proj multiply-adds: the writer's new state S'' (column j) and conv
-  // state [c] <- [s1, s2, x], stored while the multiply-adds run.
+  // state [c] <- [s1, s2, x], stored while the multiply-adds run.  Their completion is ordered
+  // before the writer's next contributions (the gate|up stage's), not before this stage's.
   if (writer) {
     const float dlk = dl * rk;
     float* Sw = b.S_w + (size_t)h * kDk * kDv;
@@ -585,6 +694,7 @@ Q35_DEV void pro_gdn(const StepArgs& a, CLayer& L, const MvItem& it, int i, GdnP
       st_agent(&cw[2], x);
     }
   }
+  return done;
 }
 
 Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
@@ -593,51 +703,67 @@ Q35_DEV void attn_chunking(const StepArgs& a, int T, int& chunk, int& nact) {
 }
 
 // o_proj input: merge the split-T partials of each touched query head (flash-decoding merge,
-// chunks in order) and apply the sigmoid output gate (text_modules.rs:936).
-Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, float* scratch) {
+// chunks in order) and apply the sigmoid output gate (text_modules.rs:936).  The partials carry
+// the attention stage's tag; the gate is a counted projection output.
+Q35_DEV bool pro_attn(const StepArgs& a, const Tok& t, int T, int k0, int klen, float* xs, float* scratch) {
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int rep = a.ah / a.kvh;
   int chunk, nact;
   attn_chunking(a, T, chunk, nact);
+  const uint32_t tag = att_tag(a, t.ti, t.l), eg = (uint32_t)a.mv[SMV_QKV].nchunk;
   float* wts = scratch;                         // [kMaxTouch][kMaxNmax] exp(m_c - M)
   float* pbuf = scratch + kMaxTouch * kMaxNmax; // [kT] per-part sums
   float* wl = pbuf + kT;                        // [kMaxTouch] L
-  const int h0 = k0 / kHd, h1 = (k0 + klen - 1) / kHd;
+  const int h0 = k0 / kHd, h1 = (k0 + klen - 1) / kHd;  // at most 3 heads (klen <= 512): waves 0..2
   // Thread (part, i): output element k0 + i, chunks part, part + parts, ...  The partial outputs
   // do not depend on the statistics, so the first batch is issued with them: one round trip.
   const int parts = klen <= 64 ? 8 : (klen <= 128 ? 4 : (klen <= 256 ? 2 : 1));
   const int span = kT / parts;
   const int i = tid % span, part = tid / span;
   const int kk = k0 + min(i, klen - 1), hk = kk / kHd;  // clamped; masked below
-  const float* og = a.att_o + ((size_t)(hk / rep) * a.att_nmax * kMaxRep + hk % rep) * kHd + kk % kHd;  // + c*kMaxRep*kHd
-  float v0[kMergeB];
-#pragma unroll
-  for (int j = 0; j < kMergeB; ++j) v0[j] = ld_agent(&og[(size_t)min(part + j * parts, nact - 1) * kMaxRep * kHd]);
-  // the thread's output gate (klen <= 512 = threads), loaded with the chunk statistics
-  const int kg = k0 + min(tid, klen - 1);
-  const fx_t graw = ld_agent(&a.acc_proj[(size_t)(kg / kHd) * 2 * kHd + kHd + kg % kHd]);
-  for (int hh = h0 + wid; hh <= h1; hh += kNW) {
-    const int g = hh / rep, hr = hh % rep;
-    const float* ml = a.att_ml + (size_t)g * a.att_nmax * 2 * kMaxRep;
-    float mv[kMaxNmax / 64], lv[kMaxNmax / 64];  // chunk c = lane + 64q (clamped; masked below)
-#pragma unroll
-    for (int q = 0; q < kMaxNmax / 64; ++q) {
-      const int c = min(lane + 64 * q, nact - 1);
-      mv[q] = ld_agent(&ml[c * 2 * kMaxRep + hr]);
-      lv[q] = ld_agent(&ml[c * 2 * kMaxRep + kMaxRep + hr]);
+  const uint64_t* og = a.att_o + ((size_t)(hk / rep) * a.att_nmax * kMaxRep + hk % rep) * kHd + kk % kHd;  // + c*kMaxRep*kHd
+  // the wave's head (wave w < h1 - h0 + 1 merges the statistics of head h0 + w)
+  const int hh = min(h0 + wid, h1);
+  constexpr int kQ = kMaxNmax / 64;
+  constexpr int kIn = kMergeB + 1 + 2 * kQ;
+  // input words: [0, kMergeB) first batch of partial outputs, kMergeB the gate (counted),
+  // then the chunk statistics m, l of chunks lane + 64q (clamped; masked below)
+  auto addr = [&](int q) -> const void* {
+    const int tq = tix(), iq = tq % span, pq = tq / span, kq = k0 + min(iq, klen - 1), hq = kq / kHd;
+    if (q < kMergeB)
+      return a.att_o + ((size_t)(hq / rep) * a.att_nmax * kMaxRep + hq % rep) * kHd + kq % kHd +
+             (size_t)min(pq + q * parts, nact - 1) * kMaxRep * kHd;
+    if (q == kMergeB) {
+      const int kg = k0 + min(tq, klen - 1);
+      return t.acc + (size_t)(kg / kHd) * 2 * kHd + kHd + kg % kHd;
     }
+    const int hw = min(h0 + (tq >> 6), h1);
+    const int qq = (q - kMergeB - 1) % kQ, ml_l = (q - kMergeB - 1) / kQ;
+    const int c = min((tq & 63) + 64 * qq, nact - 1);
+    return a.att_ml + (size_t)(hw / rep) * a.att_nmax * 2 * kMaxRep + (size_t)c * 2 * kMaxRep + ml_l * kMaxRep + hw % rep;
+  };
+  auto load_all = [&](uint64_t (&r)[kIn]) {
+#pragma unroll
+    for (int q = 0; q < kIn; ++q) r[q] = ld_agent64(static_cast<const uint64_t*>(addr(q)));
+  };
+  uint64_t in[kIn];
+  load_all(in);
+  bool done = gather<kIn>(a, in, load_all, addr, [&](int q, uint64_t w) {
+    return q == kMergeB ? fxc_ok((fx_t)w, eg) : tag_ok(w, tag);
+  });
+  if (wid <= h1 - h0) {
     float M = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < kMaxNmax / 64; ++q) M = fmaxf(M, (lane + 64 * q < nact) ? mv[q] : -INFINITY);
+    for (int q = 0; q < kQ; ++q) M = fmaxf(M, (lane + 64 * q < nact) ? tag_val(in[kMergeB + 1 + q]) : -INFINITY);
     M = wave_max(M);
     float Ls = 0.f;
 #pragma unroll
-    for (int q = 0; q < kMaxNmax / 64; ++q) {
+    for (int q = 0; q < kQ; ++q) {
       const int c = lane + 64 * q;
-      const float w = expf(mv[q] - M);
+      const float w = expf(tag_val(in[kMergeB + 1 + q]) - M);
       if (c < nact) {
         wts[(hh - h0) * kMaxNmax + c] = w;
-        Ls += lv[q] * w;
+        Ls += tag_val(in[kMergeB + 1 + kQ + q]) * w;
       }
     }
     Ls = wave_sum(Ls);
@@ -653,16 +779,25 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
 #pragma unroll
     for (int j = 0; j < kMergeB; ++j) wc[j] = w[min(part + j * parts, nact - 1)];
 #pragma unroll
-    for (int j = 0; j < kMergeB; ++j) o += (part + j * parts < nact) ? v0[j] * wc[j] : 0.f;
-    for (int c0 = part + kMergeB * parts; c0 < nact; c0 += kMergeB * parts) {
-      float v[kMergeB];  // all of a batch in flight at once (clamped; masked below)
+    for (int j = 0; j < kMergeB; ++j) o += (part + j * parts < nact) ? tag_val(in[j]) * wc[j] : 0.f;
+  }
+  // further batches (long contexts with more than kMergeB chunks per part)
+  for (int c0 = part + kMergeB * parts; c0 < nact; c0 += kMergeB * parts) {  // uniform per wave
+    uint64_t v[kMergeB];  // all of a batch in flight at once (clamped; masked below)
+    auto vaddr = [&](int j) -> const void* { return og + (size_t)min(c0 + j * parts, nact - 1) * kMaxRep * kHd; };
+    auto vload = [&](uint64_t (&r)[kMergeB]) {
 #pragma unroll
-      for (int j = 0; j < kMergeB; ++j) v[j] = ld_agent(&og[(size_t)min(c0 + j * parts, nact - 1) * kMaxRep * kHd]);
+      for (int j = 0; j < kMergeB; ++j) r[j] = ld_agent64(static_cast<const uint64_t*>(vaddr(j)));
+    };
+    vload(v);
+    done &= gather<kMergeB>(a, v, vload, vaddr, [&](int, uint64_t w) { return tag_ok(w, tag); });
+    if (i < klen) {
+      const float* w = wts + (hk - h0) * kMaxNmax;
       float wv[kMergeB];
 #pragma unroll
       for (int j = 0; j < kMergeB; ++j) wv[j] = w[min(c0 + j * parts, nact - 1)];
 #pragma unroll
-      for (int j = 0; j < kMergeB; ++j) o += (c0 + j * parts < nact) ? v[j] * wv[j] : 0.f;
+      for (int j = 0; j < kMergeB; ++j) o += (c0 + j * parts < nact) ? tag_val(v[j]) * wv[j] : 0.f;
     }
   }
   pbuf[part * span + i] = o;
@@ -670,45 +805,27 @@ Q35_DEV void pro_attn(const StepArgs& a, int T, int k0, int klen, float* xs, flo
   if (tid < klen) {
     float s = 0.f;
     for (int q = 0; q < parts; ++q) s += pbuf[q * span + tid];
-    const int hh = (k0 + tid) / kHd;
-    xs[tid] = (s * rcp_f(wl[hh - h0])) * sigmoid_f(from_fx(graw));
+    const int hq = (k0 + tid) / kHd;
+    xs[tid] = (s * rcp_f(wl[hq - h0])) * sigmoid_f(fxc_val((fx_t)in[kMergeB], eg));
   }
-}
-
-// Block bix()'s contiguous share of p[0, n) set to zero, one element per thread.
-Q35_DEV void zero_share(fx_t* p, int n) {
-  const int nb = (int)gridDim.x, per = (n + nb - 1) / nb, lo = bix() * per, hi = min(n, lo + per);
-  for (int i = lo + tix(); i < hi; i += kT) st_agent(&p[i], (fx_t)0);
-}
-
-// Side tasks of a stage (their inputs are final after its barrier, their outputs are not read
-// before the next one), spread evenly over the grid and issued behind the prologue's loads: a
-// block's loads would otherwise wait for its stores' acknowledgements (vmcnt counts both, in
-// order), and the few blocks holding all the stores arrived last.
-Q35_DEV void side_tasks(const StepArgs& a, int kind) {
-  if (kind == SMV_QKVZ || kind == SMV_QKV) {  // gate|up accumulator: last read by the previous down stage
-    zero_share(a.acc_gu, 2 * a.F);
-  } else if (kind == SMV_GU) {  // projection + gate accumulators: last read by the out / o stage
-    zero_share(a.acc_proj, (int)a.acc_zero_n);
-    if (bix() == gridDim.x - 1 && tix() < 2 * a.nh) st_agent(&a.acc_ba[tix() * kStepBaStride], (fx_t)0);
-  }
+  return done;
 }
 
 // One matvec stage.  The in_proj_b / in_proj_a gate projection (f32, [H][nh] each,
 // kernels.rs:174-247) rides on the qkvz stage: the item of tile t < 2*nh also forms the partial
 // dot product of its rows with column t of [W_b | W_a].  U: rows per lane the stage's items need;
 // KR: hidden-size elements per thread in the RMSNorm prologue (hidden <= 512 KR).
-// Returns kStageOk, kStageFail (barrier time-out) or, for the first stage of a step, kStageStop
+// Returns kStageOk, kStageFail (a wait failed) or, for the first stage of a step, kStageStop
 // (the step's input token is a stop id; *stop_tok receives it, nothing of the step has run).
 template <int U, int KR>
-Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int p, Bar& bar,
-                     const Shared& sh, int* stop_tok = nullptr) {
-  const Mv d = make_mv(a, L, kind);
+Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int pro, int i, int p, const Shared& sh,
+                     int* stop_tok = nullptr) {
+  const Mv d = make_mv(a, L, t, kind);
   const int nitems = d.t3 * d.nchunk;
   int item = bix();
   if (kind == SMV_GU) {
     // The out stage's state writers (out items with tile 0 and k0 % dv == 0, i.e. blocks b < nh cph
-    // with b % cph == 0) arrive last and so issue this stage's weights last: a permutation of
+    // with b % cph == 0) finish last and so issue this stage's weights last: a permutation of
     // [0, grid) gives them the last slots, which are idle when the stage has fewer items than blocks.
     const int cph = kDv / a.mv[SMV_OUT].kch, nw = a.nh, g = (int)gridDim.x, b = bix();
     if (nw * cph <= g) {
@@ -726,19 +843,34 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int
     mv_load(it, d.K, pf);
     if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
   }
-  if (!bar_wait(bar, sh.ok)) return kStageFail;
   int tok = 0;
   // Blocks with an item need the token for the embedding; with stop ids every block forms it,
-  // so that every block sees a stop (without them the idle blocks go straight to their side
-  // tasks, whose stores would otherwise wait behind the token's reduction).
+  // so that every block sees a stop.
   if (pro == PRO_EMBED_RMS && (item < nitems || a.n_stop > 0)) {
-    tok = select_token(a, i, p, sh);
+    if (!select_token(a, t, i, p, sh, tok)) return kStageFail;
     if (is_stop(a, p, tok)) {
       if (stop_tok) *stop_tok = tok;
       return kStageStop;
     }
   }
-  if (item >= nitems) side_tasks(a, kind);  // blocks with an item run them in the prologue
+  if (item >= nitems) {
+    // A block without an item still waits until the residual stream it would have read is
+    // complete (one word): a block that skipped the reads could otherwise run ahead far enough
+    // that a word's contribution count (modulo 256) repeats, and take an early value for a later
+    // one.  With this wait a block's reads of the stream are never more than two residual stages
+    // (at most 2 x 120 contributions) apart.
+    if (pro == PRO_RMS) {
+      bool ok = true;
+      if (tix() < 64) {
+        const uint64_t* w0 = reinterpret_cast<const uint64_t*>(t.h);
+        ok = wait_on(a, w0, [&](uint64_t w) { return fxc_ok((fx_t)w, t.hc); });
+      }
+      if (!ok) *sh.fail = 1;
+      __syncthreads();
+      if (*sh.fail) return kStageFail;
+    }
+    return kStageOk;
+  }
   float* xs = sh.smem + kXs;
   float* red = sh.smem + kRed;
   for (bool first = true; item < nitems; item += gridDim.x, first = false) {
@@ -747,40 +879,51 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int
       mv_load(it, d.K, pf);
       if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
     }
-    // the qkvz item's gate column (a 64-byte-strided gather) is issued behind the norm's inputs,
-    // not ahead of the barrier poll
+    // the qkvz item's gate column (a 64-byte-strided gather) is issued behind the norm's inputs
     auto aux_load = [&]() {
       if (kind == SMV_QKVZ && it.tile < naux && first) {  // row clamped; masked where it is used
         const float* W = it.tile < a.nh ? L.w_b : L.w_a;
         auxw = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
       }
-      if (first) side_tasks(a, kind);
     };
+    bool ok = true;
     switch (pro) {
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
-        const EmbLoad src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
-        pro_rms<KR, EmbRaw>(src, EmbConv{}, K, L.in_norm, a.eps, it.k0, it.klen, xs, sh.shs, aux_load);
-        if (bix() == 0 && first)  // the residual stream starts as the embedding row
-          for (int k = tix(); k < K; k += kT) st_agent(&a.h[k + (k & ~15)], to_fx(EmbConv{}(src(k))));
+        const EmbSrc src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
+        pro_rms<KR, EmbRaw>(a, src, K, L.in_norm, it.k0, it.klen, xs, sh.shs, aux_load);
+        if (bix() == 0 && first)  // the residual stream starts as the embedding row (one contribution)
+          for (int k = tix(); k < K; k += kT) fxc_add(a, &t.h[k + (k & ~15)], src.conv(src.load(k)));
       } break;
       case PRO_RMS:
-        pro_rms<KR, fx_t>(HLoad{a.h}, HConv{}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, a.eps, it.k0, it.klen,
-                          xs, sh.shs, aux_load);
+        ok = pro_rms<KR, fx_t>(a, HSrc{t.h, t.hc}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, it.k0, it.klen, xs,
+                               sh.shs, aux_load);
         break;
       case PRO_GDN:
-        pro_gdn(a, L, it, i, gp, xs, red);
+        ok = pro_gdn(a, L, t, it, i, gp, xs, red);
         break;
       case PRO_SWIGLU: {  // klen <= 512 = threads: one element per thread
         const int k = it.k0 + min(tix(), it.klen - 1);
-        const fx_t up = ld_agent(&a.acc_gu[a.F + k]), gate = ld_agent(&a.acc_gu[k]);
-        if (tix() < it.klen) xs[tix()] = from_fx(up) * silu_f(from_fx(gate));
+        const uint32_t e = (uint32_t)a.mv[SMV_GU].nchunk;
+        const fx_t* gu = t.acc + a.acc_gu_off;
+        auto ad = [&](int q) { return q == 0 ? &gu[a.F + k] : &gu[k]; };
+        auto load_all = [&](fx_t (&r)[2]) {
+          r[0] = ld_agent(ad(0));
+          r[1] = ld_agent(ad(1));
+        };
+        fx_t in[2];
+        load_all(in);
+        ok = gather<2>(a, in, load_all, [&](int q) { return (const void*)ad(q); },
+                       [&](int, uint64_t w) { return fxc_ok((fx_t)w, e); });
+        if (tix() < it.klen) xs[tix()] = fxc_val(in[0], e) * silu_f(fxc_val(in[1], e));
       } break;
       default:  // PRO_ATTN: merged attention output
-        pro_attn(a, p + 1, it.k0, it.klen, xs, red);
+        ok = pro_attn(a, t, p + 1, it.k0, it.klen, xs, red);
         break;
     }
+    if (!ok) *sh.fail = 1;
     __syncthreads();
+    if (*sh.fail) return kStageFail;
     // in_proj_b | in_proj_a column it.tile: each wave's part of the dot product goes into the
     // matvec reduction (further columns, when there are more than tiles, reduce on their own)
     float auxp = 0.f;
@@ -793,47 +936,50 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, int kind, int pro, int i, int
           w = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (o % a.nh)));
         }
         const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
+        fx_t* dst = t.acc + a.acc_ba_off + (size_t)o * kStepBaStride;
         if (o == it.tile) {
           auxp = wave_sum(v);
-          auxd = &a.acc_ba[(size_t)o * kStepBaStride];
+          auxd = dst;
         } else {
           const float s = block_sum(v, sh.shs);
-          if (tix() == 0) fx_add(&a.acc_ba[(size_t)o * kStepBaStride], s);
+          if (tix() == 0) fxc_add(a, dst, s);
         }
       }
     }
-    mv_compute(it, pf, xs, red, auxp, auxd);
+    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, auxp, auxd);
   }
-  bar_arrive(bar);
   return kStageOk;
 }
 
 // ------------------------------------------------------------------ attention partials
 // Item (kv head g, chunk c of `chunk` cached tokens) for the rep query heads of g
 // (text_modules.rs:842-944): q/k RMSNorm (1+w), partial RoPE (:739-774), KV append at p
-// (the item holding p), scores, chunk softmax statistics and P.V.
+// (the item holding p), scores, chunk softmax statistics and P.V, stored tagged.
 //
 // Nothing the qkv stage writes is needed to fetch the first item's cached K / V rows t < p
 // (written by earlier steps), the q / k norm weights and the thread's RoPE factors, so they are
-// loaded before the barrier: after it the stage has one memory round trip (its q, k, v inputs)
+// loaded before its inputs: the stage then has one memory round trip (its q, k, v inputs)
 // instead of four.  Wave w holds rows t0 + w + 8j, j < kAttnPf; rows beyond are loaded in-stage.
 constexpr int kAttnPf = 2;
-Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Shared& sh) {
+Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const Shared& sh) {
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int T = p + 1, rep = a.ah / a.kvh;
   int chunk, nact;
   attn_chunking(a, T, chunk, nact);
+  if ((int)bix() >= a.kvh * nact) return true;  // no item
   float4 kp[kAttnPf], vp[kAttnPf];
   {
-    const int it0 = min((int)bix(), a.kvh * nact - 1);
+    const int it0 = bix();
     const int g = it0 / nact, t0 = (it0 % nact) * chunk;
     const float* Kc = L.kc + (size_t)g * a.tmax * kHd;
     const float* Vc = L.vc + (size_t)g * a.tmax * kHd;
 #pragma unroll
     for (int j = 0; j < kAttnPf; ++j) {  // clamped to written rows; the row at p comes from LDS
-      const int t = max(0, min(t0 + wid + kNW * j, p - 1));
-      kp[j] = ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]);
-      vp[j] = ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]);
+      const int tt = max(0, min(t0 + wid + kNW * j, p - 1));
+      kp[j] = make_float4(ld_agent(&Kc[(size_t)tt * kHd + 4 * lane]), ld_agent(&Kc[(size_t)tt * kHd + 4 * lane + 1]),
+                          ld_agent(&Kc[(size_t)tt * kHd + 4 * lane + 2]), ld_agent(&Kc[(size_t)tt * kHd + 4 * lane + 3]));
+      vp[j] = make_float4(ld_agent(&Vc[(size_t)tt * kHd + 4 * lane]), ld_agent(&Vc[(size_t)tt * kHd + 4 * lane + 1]),
+                          ld_agent(&Vc[(size_t)tt * kHd + 4 * lane + 2]), ld_agent(&Vc[(size_t)tt * kHd + 4 * lane + 3]));
     }
   }
   const float4 qw = make_float4(ldg(L.q_norm + 4 * lane), ldg(L.q_norm + 4 * lane + 1), ldg(L.q_norm + 4 * lane + 2),
@@ -842,7 +988,6 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
                                 ldg(L.k_norm + 4 * lane + 3));
   const float csv = ldg(a.rope_cos + (size_t)p * a.rot + tid % a.rot);  // rot divides 512: the same
   const float snv = ldg(a.rope_sin + (size_t)p * a.rot + tid % a.rot);  // element in every round
-  if (!bar_wait(bar, sh.ok)) return false;
   float* qn = sh.smem;               // [kMaxRep][kHd]
   float* kn = qn + kMaxRep * kHd;    // [kHd]
   float* vn = kn + kHd;              // [kHd]
@@ -852,14 +997,29 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
   float* hm = ored + kNW * kMaxRep * kHd;  // [kMaxRep]
   float* hl = hm + kMaxRep;                // [kMaxRep]
   const int ldqg = a.ah * kHd * 2;
+  const uint32_t e = (uint32_t)a.mv[SMV_QKV].nchunk, tag = att_tag(a, t.ti, t.l);
   for (int item = bix(), first = 1; item < a.kvh * nact; item += gridDim.x, first = 0) {
     const int g = item / nact, c = item % nact;
     const int t0 = c * chunk, len = min(chunk, T - t0);
     const bool has_new = (c == nact - 1);
-    for (int w = wid; w < rep + (has_new ? 2 : 0); w += kNW) {
+    // wave w < rep: query head g*rep + w; w == rep: k of g; w == rep + 1: v of g (the item at p)
+    const int w = wid;
+    if (w < rep + (has_new ? 2 : 0)) {
       const int d = 4 * lane;
+      const fx_t* src = (w < rep)    ? t.acc + (size_t)(g * rep + w) * 2 * kHd + d
+                        : (w == rep) ? t.acc + ldqg + (size_t)g * kHd + d
+                                     : t.acc + ldqg + (size_t)(a.kvh + g) * kHd + d;
+      auto load_all = [&](fx_t (&r)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = ld_agent(src + q);
+      };
+      fx_t in[4];
+      load_all(in);
+      const bool done = gather<4>(a, in, load_all, [&](int q) { return (const void*)(src + q); },
+                                  [&](int, uint64_t x) { return fxc_ok((fx_t)x, e); });
+      if (!done) *sh.fail = 1;
+      const float4 v = make_float4(fxc_val(in[0], e), fxc_val(in[1], e), fxc_val(in[2], e), fxc_val(in[3], e));
       if (w < rep) {
-        const float4 v = ld4_fx(&a.acc_proj[(size_t)(g * rep + w) * 2 * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = rsqrt_f(ss / (float)kHd + a.eps);
         qn[w * kHd + d + 0] = (v.x * r) * (1.0f + qw.x);
@@ -867,7 +1027,6 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
         qn[w * kHd + d + 2] = (v.z * r) * (1.0f + qw.z);
         qn[w * kHd + d + 3] = (v.w * r) * (1.0f + qw.w);
       } else if (w == rep) {
-        const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)g * kHd + d]);
         const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
         const float r = rsqrt_f(ss / (float)kHd + a.eps);
         kn[d + 0] = (v.x * r) * (1.0f + kw.x);
@@ -875,23 +1034,23 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
         kn[d + 2] = (v.z * r) * (1.0f + kw.z);
         kn[d + 3] = (v.w * r) * (1.0f + kw.w);
       } else {
-        const float4 v = ld4_fx(&a.acc_proj[ldqg + (size_t)(a.kvh + g) * kHd + d]);
         *reinterpret_cast<float4*>(&vn[d]) = v;
       }
     }
     __syncthreads();
+    if (*sh.fail) return false;
     // RoPE on dims [0, rot): x' = x*cos + rotate_half(x)*sin
     const int half = a.rot / 2;
     const int nrot = rep + (has_new ? 1 : 0);
-    for (int e = tid; e < nrot * a.rot; e += kT) {
-      const int hh = e / a.rot, ii = e % a.rot;
+    for (int e2 = tid; e2 < nrot * a.rot; e2 += kT) {
+      const int hh = e2 / a.rot, ii = e2 % a.rot;
       const float* src = (hh < rep) ? qn + hh * kHd : kn;
       const float rh = (ii < half) ? -src[ii + half] : src[ii - half];
       rtmp[hh * kHd + ii] = src[ii] * csv + rh * snv;
     }
     __syncthreads();
-    for (int e = tid; e < nrot * a.rot; e += kT) {
-      const int hh = e / a.rot, ii = e % a.rot;
+    for (int e2 = tid; e2 < nrot * a.rot; e2 += kT) {
+      const int hh = e2 / a.rot, ii = e2 % a.rot;
       if (hh < rep) qn[hh * kHd + ii] = rtmp[hh * kHd + ii];
       else kn[ii] = rtmp[hh * kHd + ii];
     }
@@ -906,7 +1065,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) q4[h][e] = (h < rep) ? qn[h * kHd + 4 * lane + e] : 0.f;
+      for (int e2 = 0; e2 < 4; ++e2) q4[h][e2] = (h < rep) ? qn[h * kHd + 4 * lane + e2] : 0.f;
     auto score = [&](int tt, float4 kv) {
 #pragma unroll
       for (int h = 0; h < kMaxRep; ++h) {
@@ -916,18 +1075,21 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
         if (lane == 0) sc[h * kMaxChunk + tt] = dd * a.ascale;
       }
     };
+    auto ld4 = [&](const float* q) {
+      return make_float4(ld_agent(q), ld_agent(q + 1), ld_agent(q + 2), ld_agent(q + 3));
+    };
     const float4 kn4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
 #pragma unroll
-    for (int j = 0; j < kAttnPf; ++j) {  // rows held since before the barrier (first item)
+    for (int j = 0; j < kAttnPf; ++j) {  // rows held since before the inputs (first item)
       const int tt = wid + kNW * j;
       if (tt >= len) break;  // uniform
-      const int t = t0 + tt;
-      const float4 kv = (t == p) ? kn4 : (first ? kp[j] : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]));
+      const int tr = t0 + tt;
+      const float4 kv = (tr == p) ? kn4 : (first ? kp[j] : ld4(&Kc[(size_t)tr * kHd + 4 * lane]));
       score(tt, kv);
     }
     for (int tt = wid + kNW * kAttnPf; tt < len; tt += kNW) {
-      const int t = t0 + tt;
-      score(tt, (t == p) ? kn4 : ld4_agent(&Kc[(size_t)t * kHd + 4 * lane]));
+      const int tr = t0 + tt;
+      score(tt, (tr == p) ? kn4 : ld4(&Kc[(size_t)tr * kHd + 4 * lane]));
     }
     __syncthreads();
     for (int h = wid; h < rep; h += kNW) {
@@ -948,7 +1110,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+      for (int e2 = 0; e2 < 4; ++e2) acc[h][e2] = 0.f;
     auto pv = [&](int tt, float4 vv) {
 #pragma unroll
       for (int h = 0; h < kMaxRep; ++h) {
@@ -962,32 +1124,33 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
     for (int j = 0; j < kAttnPf; ++j) {
       const int tt = wid + kNW * j;
       if (tt >= len) break;  // uniform
-      const int t = t0 + tt;
-      pv(tt, (t == p) ? vn4 : (first ? vp[j] : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane])));
+      const int tr = t0 + tt;
+      pv(tt, (tr == p) ? vn4 : (first ? vp[j] : ld4(&Vc[(size_t)tr * kHd + 4 * lane])));
     }
     for (int tt = wid + kNW * kAttnPf; tt < len; tt += kNW) {
-      const int t = t0 + tt;
-      pv(tt, (t == p) ? vn4 : ld4_agent(&Vc[(size_t)t * kHd + 4 * lane]));
+      const int tr = t0 + tt;
+      pv(tt, (tr == p) ? vn4 : ld4(&Vc[(size_t)tr * kHd + 4 * lane]));
     }
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h)
       *reinterpret_cast<float4*>(&ored[(wid * kMaxRep + h) * kHd + 4 * lane]) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    // the KV row appended above completes before the partials that o_proj's readers observe
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const size_t pc = (size_t)g * a.att_nmax + c;
-    for (int e = tid; e < rep * kHd; e += kT) {
-      const int h = e / kHd, d = e % kHd;
+    for (int e2 = tid; e2 < rep * kHd; e2 += kT) {
+      const int h = e2 / kHd, d = e2 % kHd;
       float o = 0.f;
 #pragma unroll
-      for (int w = 0; w < kNW; ++w) o += ored[(w * kMaxRep + h) * kHd + d];
-      st_agent(&a.att_o[(pc * kMaxRep + h) * kHd + d], o);
+      for (int w2 = 0; w2 < kNW; ++w2) o += ored[(w2 * kMaxRep + h) * kHd + d];
+      st_agent64(&a.att_o[(pc * kMaxRep + h) * kHd + d], tagged(o, tag));
     }
     if (tid < rep) {
-      st_agent(&a.att_ml[pc * 2 * kMaxRep + tid], hm[tid]);
-      st_agent(&a.att_ml[pc * 2 * kMaxRep + kMaxRep + tid], hl[tid]);
+      st_agent64(&a.att_ml[pc * 2 * kMaxRep + tid], tagged(hm[tid], tag));
+      st_agent64(&a.att_ml[pc * 2 * kMaxRep + kMaxRep + tid], tagged(hl[tid], tag));
     }
     __syncthreads();
   }
-  bar_arrive(bar);
   return true;
 }
 
@@ -995,9 +1158,9 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, int p, Bar& bar, const Sha
 // Tied embedding [V][H] as lm_head (kernels.rs:251-291): wave w owns R rows per block step,
 // lane l reads the 16-byte chunks 16*(l + 64c), c < CPW, of each row; two steps of loads
 // (2 x 8 per lane, 128 KB per block) are kept in flight.  Block argmax (reference order,
-// ArgOrder) -> arg_v / arg_i.
+// ArgOrder) -> argp, tagged with the token.  Also clears the next token's accumulators.
 template <int CPW>
-Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
+Q35_DEV bool lm_stage(const StepArgs& a, const Tok& t, const Shared& sh) {
   constexpr int R = 8 / CPW;
   constexpr int RPB = kNW * R;
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
@@ -1033,8 +1196,8 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
       const float4* xp = reinterpret_cast<const float4*>(&xs[k]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float4 t = xp[q];
-        xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+        const float4 tq = xp[q];
+        xv[4 * q] = tq.x; xv[4 * q + 1] = tq.y; xv[4 * q + 2] = tq.z; xv[4 * q + 3] = tq.w;
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -1055,11 +1218,21 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
   };
   const int rb0 = bix(), gs = gridDim.x;
   if (rb0 < nrb) load(rb0, wa, sa);
-  if (!bar_wait(bar, sh.ok)) return false;
   // the second row block is issued behind the norm's inputs (rows clamped: always in the table)
-  pro_rms<2 * CPW, fx_t>(HLoad{a.h}, HConv{}, K, a.final_norm, a.eps, 0, K, xs, sh.shs,
-                         [&]() { load(rb0 + gs, wb, sb); });
+  const bool ok = pro_rms<2 * CPW, fx_t>(a, HSrc{t.h, t.hc}, K, a.final_norm, 0, K, xs, sh.shs,
+                                         [&]() { load(rb0 + gs, wb, sb); });
+  if (!ok) *sh.fail = 1;
   __syncthreads();
+  if (*sh.fail) return false;
+  {
+    // clear the other parity set (the next token's residual stream and accumulators): the last
+    // readers of it were the previous token's, and every block finished those before this token
+    const int64_t nh = 2 * (int64_t)a.H, na = (int64_t)a.n_layers * a.acc_stride, n = nh + na;
+    fx_t* hz = a.h + (size_t)((t.ti + 1) & 1) * nh;
+    fx_t* az = a.acc + (size_t)((t.ti + 1) & 1) * na;
+    const int64_t per = (n + gs - 1) / gs, lo = (int64_t)bix() * per, hi = min(n, lo + per);
+    for (int64_t q = lo + tid; q < hi; q += kT) st_agent(q < nh ? &hz[q] : &az[q - nh], (fx_t)0);
+  }
   for (int rb = rb0; rb < nrb; rb += 2 * gs) {
     if (rb != rb0 && rb + gs < nrb) load(rb + gs, wb, sb);
     compute(rb, wa, sa);
@@ -1068,8 +1241,10 @@ Q35_DEV bool lm_stage(const StepArgs& a, Bar& bar, const Shared& sh) {
     compute(rb + gs, wb, sb);
   }
   block_argmax(best_v, best_i, sh.shv, sh.shi, a.ord);
-  if (tid == 0) { st_agent(&a.arg_v[bix()], best_v); st_agent(&a.arg_i[bix()], best_i); }
-  bar_arrive(bar);
+  // the clearing stores complete before the partial that the next token's blocks wait for
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) st_agent64(&a.argp[(size_t)(t.ti & 1u) * gs + bix()], arg_pack(best_v, best_i, t.ti));
   return true;
 }
 
@@ -1095,7 +1270,7 @@ Q35_DEV void state_copy_back(const StepArgs& a) {
         if (!L.full) {
           const float* src = r < nr ? L.rec_alt + 4 * r : L.conv_alt + 4 * (r - nr);
           dst[u] = r < nr ? L.rec + 4 * r : L.conv_state + 4 * (r - nr);
-          v[u] = ld4_agent(src);
+          v[u] = make_float4(ld_agent(src), ld_agent(src + 1), ld_agent(src + 2), ld_agent(src + 3));
         }
       }
     }
@@ -1118,72 +1293,71 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   __shared__ __align__(16) float shs[kNW];
   __shared__ float shv[kNW];
   __shared__ int shi[kNW];
-  __shared__ int ok;
-  const Shared sh{smem, shs, shv, shi, &ok};
-  Bar bar{a.bar, a.err, a.bar_base};
+  __shared__ int fail;
+  const Shared sh{smem, shs, shv, shi, &fail};
   // a failed earlier launch left the model state invalid: do nothing until a reset
   if (ld_agent(a.err) != 0u) return;
+  if (tix() == 0) fail = 0;
+  __syncthreads();
   const int p0 = ldg(a.pos);
+  const uint32_t ts0 = ld_agent(a.tokseq);
   int executed = a.ntok, stop_tok = 0;
   for (int i = 0; i < a.ntok && executed == a.ntok; ++i) {
     const int p = p0 + i;
+    Tok t;
+    t.ti = ts0 + (uint32_t)i;
+    const int par = (int)(t.ti & 1u);
+    t.h = a.h + (size_t)par * 2 * a.H;
+    fx_t* acc0 = a.acc + (size_t)par * a.n_layers * a.acc_stride;
+    t.hc = 1;  // the embedding row
     for (int l = 0; l < a.n_layers; ++l) {
       CLayer& L = layer_at(a, l);
+      t.l = l;
+      t.acc = acc0 + (size_t)l * a.acc_stride;
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
       int r;
       if (!L.full) {
-        r = mv_stage<kU, KR>(a, L, SMV_QKVZ, pro0, i, p, bar, sh, &stop_tok);
+        r = mv_stage<kU, KR>(a, L, t, SMV_QKVZ, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
-        if (!mv_stage<kUOut, KR>(a, L, SMV_OUT, PRO_GDN, i, p, bar, sh)) return;
+        if (!mv_stage<kUOut, KR>(a, L, t, SMV_OUT, PRO_GDN, i, p, sh)) return;
+        t.hc += (uint32_t)a.mv[SMV_OUT].nchunk;
       } else {
-        r = mv_stage<kU, KR>(a, L, SMV_QKV, pro0, i, p, bar, sh, &stop_tok);
+        r = mv_stage<kU, KR>(a, L, t, SMV_QKV, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
-        if (!attn_stage(a, L, p, bar, sh)) return;
-        if (!mv_stage<kU, KR>(a, L, SMV_O, PRO_ATTN, i, p, bar, sh)) return;
+        if (!attn_stage(a, L, t, p, sh)) return;
+        if (!mv_stage<kU, KR>(a, L, t, SMV_O, PRO_ATTN, i, p, sh)) return;
+        t.hc += (uint32_t)a.mv[SMV_O].nchunk;
       }
-      if (!mv_stage<kU, KR>(a, L, SMV_GU, PRO_RMS, i, p, bar, sh)) return;
-      if (!mv_stage<kU, KR>(a, L, SMV_DOWN, PRO_SWIGLU, i, p, bar, sh)) return;
+      if (!mv_stage<kU, KR>(a, L, t, SMV_GU, PRO_RMS, i, p, sh)) return;
+      if (!mv_stage<kU, KR>(a, L, t, SMV_DOWN, PRO_SWIGLU, i, p, sh)) return;
+      t.hc += (uint32_t)a.mv[SMV_DOWN].nchunk;
     }
     if (executed != a.ntok) break;
-    if (!lm_stage<CPW>(a, bar, sh)) return;
+    if (!lm_stage<CPW>(a, t, sh)) return;
   }
-  if (executed != a.ntok) {
-    // Stopped before step `executed` ran (every block decided alike): arrive once for all the
-    // barriers the remaining steps would have passed, so the counters end where a full launch
-    // leaves them (the host counts barriers per launch).
-    const uint32_t final_epoch = a.bar_base + (uint32_t)a.ntok * (uint32_t)a.bar_per_token;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tix() == 0)
-      __hip_atomic_fetch_add((Q35_GLOBAL uint32_t*)&bar.ctr[(bix() % kGroups) * kCtrStride], final_epoch - bar.epoch,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bar.epoch = final_epoch;
-  }
-  // Every block has passed the last executed step's lm-stage barrier (a stop is decided after
-  // it), so all state writes are complete.
+  // Every block has read all argmax partials of the last executed step (or passed its lm stage),
+  // so all state writes of the launch are complete and ordered before this point.
   if (executed & 1) state_copy_back(a);
   // tail: block 0 turns the last step's block argmaxes into the token
   if (bix() != 0) return;
-  if (!bar_wait(bar, sh.ok)) return;
   if (executed != a.ntok) {  // the stop id stays the next token; hist already holds it
     if (tix() == 0) {
       stg(a.token, (int32_t)stop_tok);
       stg(a.pos, (int32_t)(p0 + executed));
+      st_agent((int32_t*)a.tokseq, (int32_t)(ts0 + (uint32_t)executed));
     }
     return;
   }
-  float v = -INFINITY;
-  int ix = INT_MAX;
-  if (tix() < (int)gridDim.x) { v = ld_agent(&a.arg_v[tix()]); ix = ld_agent(&a.arg_i[tix()]); }
-  block_argmax(v, ix, sh.shv, sh.shi, a.ord);
+  int tok = 0;
+  if (!reduce_argmax(a, ts0 + (uint32_t)a.ntok - 1u, sh, tok)) return;
   if (tix() == 0) {
-    const int tok = (ix == INT_MAX) ? 0 : ix;
     const int pl = p0 + a.ntok - 1;
     stg(a.hist + pl, (int32_t)tok);
     stg(a.token, (int32_t)tok);
     stg(a.pos, (int32_t)(pl + 1));
+    st_agent((int32_t*)a.tokseq, (int32_t)(ts0 + (uint32_t)a.ntok));
   }
 }
 
@@ -1218,6 +1392,7 @@ int step_validate(const q35_dims& d, int tmax, int grid) {
     return fail(Q35_E_SHAPE, "persistent step: attention needs head_dim 256 and <= 4 query heads per kv head");
   if (d.rot_dim < 2 || d.rot_dim > kHd || (d.rot_dim % 2) != 0 || (kT % d.rot_dim) != 0)
     return fail(Q35_E_SHAPE, "persistent step: rotary dims must be even, <= 256 and divide 512");
+  if (d.vocab >= (int)kArgNone) return fail(Q35_E_SHAPE, "persistent step: vocabulary must be < 2^18 - 1");
   if ((long long)tmax > (long long)kMaxChunk * step_att_nmax(grid, d.kv_heads))
     return fail(Q35_E_SHAPE, "persistent step: tmax too large for the attention split");
   return Q35_OK;
@@ -1239,13 +1414,15 @@ void step_plan(const q35_dims& d, int grid, StepMv* mv) {
       {SMV_DOWN, tiles(d.hidden), d.ffn},
   };
   for (const S& s : st) {
-    int nchunk = std::max(1, grid / s.tiles);
+    // at most 120 chunks: a residual word then gets < 128 contributions per stage, which keeps
+    // every reader's window of possible counts below the counter's 256 (see the kernel)
+    int nchunk = std::max(1, std::min(120, grid / s.tiles));
     int kch = (s.K + nchunk - 1) / nchunk;
     kch = (kch + 15) & ~15;
     if (kch > kKch) kch = kKch;
     if (s.kind == SMV_OUT) {
       int kc = d.lin_dv;
-      while (kc > kch && kc % 32 == 0) kc /= 2;
+      while (kc > kch && kc % 32 == 0 && (s.K + kc / 2 - 1) / (kc / 2) <= 120) kc /= 2;
       kch = kc;
     }
     nchunk = (s.K + kch - 1) / kch;
@@ -1253,15 +1430,9 @@ void step_plan(const q35_dims& d, int grid, StepMv* mv) {
   }
 }
 
-int step_barriers_per_token(const q35_dims& d) {
-  int n = 1;  // lm_head
-  for (int l = 0; l < d.n_layers; ++l) n += ((l + 1) % d.full_interval == 0) ? 5 : 4;
-  return n;
-}
-
 int step_launch(const StepArgs& a, int grid, hipStream_t st) {
   if (a.ntok < 1) return Q35_OK;
-  if (!a.bar || !a.err) return fail(Q35_E_ARG, "persistent step: null barrier or error word");
+  if (!a.err || !a.tokseq || !a.argp) return fail(Q35_E_ARG, "persistent step: null error word or token counter");
   StepArgs args = a;
   void* params[] = {&args};
   Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H), dim3(grid), dim3(kT), params, 0, st));

@@ -24,6 +24,7 @@ import oracle as O
 import q35
 from conftest import rel_l2
 from gpu_util import dev, host, normal, q8, q8_dev
+from q35._lib import Q35_E_SHAPE
 
 pytestmark = pytest.mark.gpu
 
@@ -336,6 +337,71 @@ def test_model_prefill_continuation_and_second_turn():
     g2, _ = m.generate(np.concatenate([[g1[-1]], p2]), 15, mode="persistent", prefill=True)
     m.check()
     np.testing.assert_array_equal(g2, r2)
+    m.close()
+
+
+def test_model_prefill_longer_than_one_pass():
+    """An 1100-token prompt in one prefill call runs as two passes over the same prompt-path
+    buffers (1024 + 76 tokens): the ids after it equal the oracle's token-by-token run, and the
+    recurrent / conv states and KV rows equal those of feeding the prompt one decode step at a
+    time."""
+    d = hybrid_dims()
+    seed, tmax, n = 3, 1200, 1100
+    prompt = np.random.default_rng(21).integers(0, d.vocab, n).astype(np.int32)
+    print(f"[long prefill] prompt={n} tmax={tmax}", flush=True)
+    rt, margins = oracle_model(d, seed, tmax).generate(prompt, 12)
+    a = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    toks, _ = a.generate(prompt, 12, mode="persistent", prefill=True)
+    a.check()
+    print("tokens", toks[:8], "min margin", margins.min(), flush=True)
+    np.testing.assert_array_equal(toks, rt)
+    a.reset()
+    a.prefill(prompt)
+    b = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
+    b.generate(prompt, 0, mode="persistent")
+    b.check()
+    assert a.position() == b.position() == n
+    for l in range(d.n_layers):
+        if (l + 1) % d.full_interval == 0:
+            for nm in ("k_cache", "v_cache"):
+                ta = a.tensor(f"layers.{l}.self_attn.{nm}", np.float32)
+                tb = b.tensor(f"layers.{l}.self_attn.{nm}", np.float32)
+                assert rel_l2(ta, tb) <= 1e-5, (l, nm)
+        else:
+            S_a = a.tensor(f"layers.{l}.linear_attn.recurrent_state", np.float32)
+            S_b = b.tensor(f"layers.{l}.linear_attn.recurrent_state", np.float32)
+            assert rel_l2(S_a, S_b) <= 1e-4, l
+            c_a = a.tensor(f"layers.{l}.linear_attn.conv_state", np.float32)
+            c_b = b.tensor(f"layers.{l}.linear_attn.conv_state", np.float32)
+            assert rel_l2(c_a, c_b) <= 1e-5, l
+    assert int(a.tensor("token", np.int32)[0]) == int(b.tensor("token", np.int32)[0])
+    a.close()
+    b.close()
+
+
+def test_prompt_path_rejects_unsupported_head_dims():
+    """The prompt path's chunked rule is built for 128 x 128 heads: with a value head of 64 the
+    model prefill and the batched prompt path report Q35_E_SHAPE before launching anything, and
+    the model still decodes token by token afterwards."""
+    d = q35.make_dims(hidden=512, ffn=1536, vocab=8192, n_layers=4, lin_heads=4, lin_dv=64, attn_heads=4, kv_heads=2)
+    prompt = np.random.default_rng(5).integers(0, d.vocab, 40).astype(np.int32)
+    m = q35.TextForCausalLM(d, seed=3, tmax=128)
+    with pytest.raises(q35.Q35Error) as e:
+        m.prefill(prompt)
+    assert e.value.code == Q35_E_SHAPE
+    with pytest.raises(q35.Q35Error) as e:
+        m.generate(prompt, 4, mode="graph", prefill=True)
+    assert e.value.code == Q35_E_SHAPE
+    b = q35.BatchDecoder(m, 2, tmax=128)
+    with pytest.raises(q35.Q35Error) as e:
+        b.generate([prompt, prompt[:17]], 4, prefill=True)
+    assert e.value.code == Q35_E_SHAPE
+    b.close()
+    m.reset()
+    rt, _ = oracle_model(d, 3, 128).generate(prompt, 6)
+    toks, _ = m.generate(prompt, 6, mode="graph")
+    m.check()
+    np.testing.assert_array_equal(toks, rt)
     m.close()
 
 
