@@ -232,7 +232,9 @@ Q35_DEV bool gather(const StepArgs& a, W (&w)[N], LoadAll load_all, Addr addr, T
       if (!test(j, (uint64_t)w[j])) jf = j;
     const uint64_t bad = __ballot(jf < N);
     if (bad == 0) return true;
-    const int lf = __ffsll((unsigned long long)bad) - 1;
+    const int sh = (bix() * 13 + (tix() >> 6) * 5) & 63;
+    const uint64_t rot = sh ? ((bad >> sh) | (bad << (64 - sh))) : bad;
+    const int lf = (__ffsll((unsigned long long)rot) - 1 + sh) & 63;
     const int jw = __builtin_amdgcn_readlane(jf, lf);
     const uint64_t* pw = static_cast<const uint64_t*>(readlane_ptr(addr(jw), lf));
     if (!wait_on(a, pw, [&](uint64_t x) { return test(jw, x); })) return false;
@@ -360,14 +362,14 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
   }
 }
 
-// y[tile cols] += sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.  aux_dst
+// y[tile cols] += scale * sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.  aux_dst
 // (optional): one more sum, of which each wave holds its part in aux, reduced with the columns.
 // wait_stores: every store the block issued before (cleared accumulators, KV rows, DeltaNet
 // states) completes before the first contribution is added, so whoever observes the
 // contributions can read what those stores wrote.
 template <int U>
 Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, const float* xs, float* red,
-                        bool wait_stores, float aux = 0.f, fx_t* aux_dst = nullptr) {
+                        bool wait_stores, float scale, float aux = 0.f, fx_t* aux_dst = nullptr) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
@@ -412,7 +414,7 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < kNW; ++w) s += red[kNW * kTile + w];
-    fxc_add(a, aux_dst, s);
+    fxc_add(a, aux_dst, s * scale);
   }
   if (tid < kTile) {
     // all kNW wave partials read before any is summed: one LDS round trip
@@ -424,7 +426,7 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
 #pragma unroll
     for (int i = 0; i < kNW; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
-    if (n < it.N) fxc_add(a, &it.acc[n + (n & it.spm)], v);
+    if (n < it.N) fxc_add(a, &it.acc[n + (n & it.spm)], v * scale);
   }
   __syncthreads();
 }
@@ -437,7 +439,11 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
 // ones (counted inputs), `src.conv` turns it into f32.  `post` (more weight loads of the caller)
 // is issued behind the prologue's loads and before their first use; scheduling barriers keep the
 // compiler from moving either group across it.  Returns false when a wait failed.
-template <int KR, class Raw, class Src, class Post>
+// DEFER: xs gets x * (1 + w) only, and each wave leaves its part of the sum of squares in shs;
+// the caller applies rsqrt(mean + eps) to the matvec's column sums (the scale is the same for
+// every row, so W^T (x r (1 + w)) = r W^T (x (1 + w))), which takes the block sum off the path to
+// the multiply-adds.
+template <int KR, bool DEFER, class Raw, class Src, class Post>
 Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, int K, const float* w, int k0, int klen, float* xs, float* shs,
                      Post post) {
   const int tid = tix();
@@ -459,6 +465,16 @@ Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, int K, const float* w, i
   for (int j = 0; j < KR; ++j) {
     v[j] = (tid + kT * j < K) ? src.conv(raw[j]) : 0.f;
     ss += v[j] * v[j];
+  }
+  if constexpr (DEFER) {
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) shs[tid >> 6] = ss;
+#pragma unroll
+    for (int j = 0; j < KR; ++j) {
+      const int k = tid + kT * j;
+      if (k >= k0 && k < k0 + klen) xs[k - k0] = v[j] * (1.0f + wn[j]);
+    }
+    return ok;
   }
   // every caller reaches here right after a workgroup barrier (the stage's start, or the
   // previous item's reduction), so the block sum needs no leading one
@@ -862,7 +878,7 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
     if (pro == PRO_RMS) {
       bool ok = true;
       if (tix() < 64) {
-        const uint64_t* w0 = reinterpret_cast<const uint64_t*>(t.h);
+        const uint64_t* w0 = reinterpret_cast<const uint64_t*>(HSrc{t.h, t.hc}.at((bix() * 67) % a.H));
         ok = wait_on(a, w0, [&](uint64_t w) { return fxc_ok((fx_t)w, t.hc); });
       }
       if (!ok) *sh.fail = 1;
@@ -891,12 +907,12 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
         const EmbSrc src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
-        pro_rms<KR, EmbRaw>(a, src, K, L.in_norm, it.k0, it.klen, xs, sh.shs, aux_load);
+        pro_rms<KR, true, EmbRaw>(a, src, K, L.in_norm, it.k0, it.klen, xs, sh.shs, aux_load);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row (one contribution)
           for (int k = tix(); k < K; k += kT) fxc_add(a, &t.h[k + (k & ~15)], src.conv(src.load(k)));
       } break;
       case PRO_RMS:
-        ok = pro_rms<KR, fx_t>(a, HSrc{t.h, t.hc}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, it.k0, it.klen, xs,
+        ok = pro_rms<KR, true, fx_t>(a, HSrc{t.h, t.hc}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, it.k0, it.klen, xs,
                                sh.shs, aux_load);
         break;
       case PRO_GDN:
@@ -924,6 +940,13 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
     if (!ok) *sh.fail = 1;
     __syncthreads();
     if (*sh.fail) return kStageFail;
+    // the RMSNorm scale deferred by the prologue (1 for the other prologues)
+    float rn = 1.f;
+    if (pro == PRO_RMS || pro == PRO_EMBED_RMS) {
+      const float4 s0 = *reinterpret_cast<const float4*>(sh.shs), s1 = *reinterpret_cast<const float4*>(sh.shs + 4);
+      const float ss = ((((((s0.x + s0.y) + s0.z) + s0.w) + s1.x) + s1.y) + s1.z) + s1.w;
+      rn = rsqrt_f(ss * rcp_f((float)d.K) + a.eps);
+    }
     // in_proj_b | in_proj_a column it.tile: each wave's part of the dot product goes into the
     // matvec reduction (further columns, when there are more than tiles, reduce on their own)
     float auxp = 0.f;
@@ -942,11 +965,11 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
           auxd = dst;
         } else {
           const float s = block_sum(v, sh.shs);
-          if (tix() == 0) fxc_add(a, dst, s);
+          if (tix() == 0) fxc_add(a, dst, s * rn);
         }
       }
     }
-    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, auxp, auxd);
+    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, rn, auxp, auxd);
   }
   return kStageOk;
 }
@@ -1219,7 +1242,7 @@ Q35_DEV bool lm_stage(const StepArgs& a, const Tok& t, const Shared& sh) {
   const int rb0 = bix(), gs = gridDim.x;
   if (rb0 < nrb) load(rb0, wa, sa);
   // the second row block is issued behind the norm's inputs (rows clamped: always in the table)
-  const bool ok = pro_rms<2 * CPW, fx_t>(a, HSrc{t.h, t.hc}, K, a.final_norm, 0, K, xs, sh.shs,
+  const bool ok = pro_rms<2 * CPW, false, fx_t>(a, HSrc{t.h, t.hc}, K, a.final_norm, 0, K, xs, sh.shs,
                                          [&]() { load(rb0 + gs, wb, sb); });
   if (!ok) *sh.fail = 1;
   __syncthreads();
