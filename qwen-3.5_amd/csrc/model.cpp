@@ -173,12 +173,14 @@ int setup_persistent(q35_model* m) {
   // per layer: projection outputs | gate|up | in_proj_b|a sums (each sum on its own cache line)
   const int64_t gu_off = ((int64_t)m->acc_proj_n + 15) / 16 * 16, ba_off = gu_off + 2 * (int64_t)d.ffn;
   const int64_t acc_stride = ba_off + 2 * (int64_t)nh * kStepBaStride;
+  const int64_t acc_par = (int64_t)d.n_layers * acc_stride;
+  const int64_t h_n = (int64_t)2 * d.n_layers * 2 * d.hidden;  // per parity: one copy per residual stage
   int rc;
   if ((rc = dev_alloc_t(m, "step_layers", hl.size(), &dl)) ||
       (rc = dev_alloc_t(m, "step_error", 1, &err)) ||
       (rc = dev_alloc_t(m, "step_tokseq", 1, &tokseq)) ||
-      (rc = dev_alloc_t(m, "step_acc", (size_t)2 * d.n_layers * acc_stride, &acc)) ||
-      (rc = dev_alloc_t(m, "step_h", (size_t)2 * 2 * d.hidden, &h_sp)) ||
+      (rc = dev_alloc_t(m, "step_acc", (size_t)2 * acc_par, &acc)) ||
+      (rc = dev_alloc_t(m, "step_h", (size_t)2 * h_n, &h_sp)) ||
       (rc = dev_alloc_t(m, "step_attn_partial_ml", (size_t)kvh * nmax * 8, &att_ml)) ||
       (rc = dev_alloc_t(m, "step_attn_partial_o", (size_t)kvh * nmax * 4 * 256, &att_o)) ||
       (rc = dev_alloc_t(m, "step_argmax_partial", (size_t)2 * grid, &argp)))
@@ -187,8 +189,8 @@ int setup_persistent(q35_model* m) {
   // counted accumulators, tags and the token counter start from zero (a model reset clears them again)
   Q35_HIP_TRY(hipMemset(err, 0, sizeof(uint32_t)));
   Q35_HIP_TRY(hipMemset(tokseq, 0, sizeof(uint32_t)));
-  Q35_HIP_TRY(hipMemset(acc, 0, (size_t)2 * d.n_layers * acc_stride * sizeof(fx_t)));
-  Q35_HIP_TRY(hipMemset(h_sp, 0, (size_t)4 * d.hidden * sizeof(fx_t)));
+  Q35_HIP_TRY(hipMemset(acc, 0, (size_t)2 * acc_par * sizeof(fx_t)));
+  Q35_HIP_TRY(hipMemset(h_sp, 0, (size_t)2 * h_n * sizeof(fx_t)));
   Q35_HIP_TRY(hipMemset(att_ml, 0, (size_t)kvh * nmax * 8 * sizeof(uint64_t)));
   Q35_HIP_TRY(hipMemset(att_o, 0, (size_t)kvh * nmax * 4 * 256 * sizeof(uint64_t)));
   Q35_HIP_TRY(hipMemset(argp, 0, (size_t)2 * grid * sizeof(uint64_t)));
@@ -203,10 +205,10 @@ int setup_persistent(q35_model* m) {
   step_plan(d, grid, a.mv);
   a.emb_q = m->embed.q; a.emb_s = m->embed.s; a.final_norm = m->final_norm;
   a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-  // The residual stream gets buffers of its own (one per token parity) with every 128-byte line
-  // on a 256-byte slot: each out / down / o stage adds 256 blocks' partials into it, and 16
-  // consecutive lines took those atomics about 1.8x as long as lines spread this way.
-  a.h = h_sp; a.acc = acc; a.acc_stride = acc_stride; a.acc_gu_off = gu_off; a.acc_ba_off = ba_off;
+  // The residual stream gets buffers of its own (a copy per residual stage and token parity) with
+  // every 128-byte line on a 256-byte slot: each out / down / o stage adds 256 blocks' partials
+  // into it, and 16 consecutive lines took those atomics about 1.8x as long as lines spread this way.
+  a.h = h_sp; a.n_res = 2 * d.n_layers; a.acc = acc; a.acc_stride = acc_stride; a.acc_gu_off = gu_off; a.acc_ba_off = ba_off; a.acc_par = acc_par;
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.argp = argp; a.tokseq = tokseq;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;

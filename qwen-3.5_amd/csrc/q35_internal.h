@@ -689,10 +689,13 @@ struct StepArgs {
   // Counted fixed-point accumulators (value * 2^32 plus one 2^56 per contribution; see step.hip),
   // one set per token parity: token t uses set t & 1, and the lm stage of token t clears the
   // other set for token t + 1.
-  fx_t* h;              // [2][2 * H] residual stream: value k at k + (k & ~15) (one 128-byte line per 256 bytes)
-  fx_t* acc;            // [2][n_layers][acc_stride] per layer: projections | gate|up | in_proj_b|a sums
+  fx_t* h;              // [2][n_res][2 * H] residual stream, one copy per residual stage (n_res = 2 n_layers):
+                        // value k at k + (k & ~15) (one 128-byte line per 256 bytes)
+  int32_t n_res;
+  fx_t* acc;            // [2][acc_par]: [n_layers][acc_stride] per layer: projections | gate|up | in_proj_b|a sums
   int64_t acc_stride;   // fx_t entries per layer
   int64_t acc_gu_off, acc_ba_off;  // offsets of the gate|up and the b|a sums inside a layer's entries
+  int64_t acc_par;      // fx_t entries per parity set (n_layers * acc_stride)
   // Attention partials, tagged: (tag << 32) | f32 bits, tag = a number unique to the token and layer
   uint64_t *att_ml, *att_o;
   int32_t att_nmax;     // attention chunks per kv head

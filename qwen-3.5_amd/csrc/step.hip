@@ -41,10 +41,15 @@
 // Ordering of the plain stores that are not tagged (KV rows, DeltaNet states, the clearing of
 // the next token's accumulators) follows from the data: a block waits for its stores to
 // complete before its next published contribution, and every later reader of them first
-// observes that contribution (or one that depends on it).  Accumulators are never re-used
-// within a token (one set per layer), and the lm stage of token t clears the set of token t + 1
-// (token parity); every block reads all argmax partials of token t before it starts token t + 1,
-// so the clearing is complete before any block adds into that set.
+// observes that contribution (or one that depends on it).  No counted word is ever added to
+// after its readers' count is reached: accumulators are not re-used within a token (one set per
+// layer), and the residual stream has a copy per residual stage, which receives the previous
+// copy once (the stage's first-chunk items add it with their contributions) and that stage's
+// contributions (a reader that falls behind would otherwise find its words already past its
+// count; the carry costs no extra atomic).  So a count never
+// exceeds 1 + 120 and never wraps.  The lm stage of token t clears the set of token t + 1 (token
+// parity); every block reads all argmax partials of token t before it starts token t + 1, so the
+// clearing is complete before any block adds into that set.
 // Every wait is bounded: on time-out a block sets the sticky error word and returns; other
 // blocks poll the word while they wait and return too, so the grid always drains; a later
 // launch that finds the word set returns at entry.  The launch is cooperative only so that all
@@ -165,13 +170,14 @@ Q35_DEV void raise_err(const StepArgs& a, uint32_t bit) {
 
 // One contribution v to a counted word (fire-and-forget agent-scope atomic).  A value that is not
 // finite or whose magnitude reaches 2^22 (the total must stay below 2^23) is not added: it sets
-// the range bit of the error word, which the host reports after the launch.
-Q35_DEV void fxc_add(const StepArgs& a, fx_t* p, float v) {
+// the range bit of the error word, which the host reports after the launch.  `base` (a fixed-point
+// value, exact) is added with it.
+Q35_DEV void fxc_add(const StepArgs& a, fx_t* p, float v, fx_t base = 0) {
   if (!(fabsf(v) < 4194304.0f)) {
     raise_err(a, kStepErrRange);
     v = 0.f;
   }
-  __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v) + (1ull << 56),
+  __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v) + (uint64_t)base + (1ull << 56),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -250,9 +256,10 @@ Q35_DEV CLayer& layer_at(const StepArgs& a, int l) { return *(CLayer*)(a.layers 
 
 // Per token and layer: where this token's counted accumulators are and what a complete word holds.
 struct Tok {
-  fx_t* h;       // residual stream of this token (parity set)
+  fx_t* h;       // the residual stream as the last residual stage left it (parity set)
+  fx_t* hn;      // the copy the next residual stage adds into (parity set)
   fx_t* acc;     // this layer's accumulators (parity set)
-  uint32_t hc;   // contributions a complete residual word holds at this point of the token
+  uint32_t hc;   // contributions a complete word of h holds
   uint32_t ti;   // tokens run since the last reset, this one included (minus 1)
   int l;         // layer
 };
@@ -285,7 +292,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, const Tok& t, int kind) {
       break;
     case SMV_OUT:
       d.K = a.vdim;
-      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.out_q; d.s0 = L.out_s; d.a0 = t.hn; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_QKV: {
@@ -298,7 +305,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, const Tok& t, int kind) {
     } break;
     case SMV_O:
       d.K = a.ah * a.hd;
-      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.o_q; d.s0 = L.o_s; d.a0 = t.hn; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
     case SMV_GU:
@@ -309,7 +316,7 @@ Q35_DEV Mv make_mv(const StepArgs& a, CLayer& L, const Tok& t, int kind) {
       break;
     default:  // SMV_DOWN
       d.K = a.F;
-      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = t.h; d.n0 = a.H; d.spm = ~15;
+      d.w0 = L.down_q; d.s0 = L.down_s; d.a0 = t.hn; d.n0 = a.H; d.spm = ~15;
       d.t1 = d.t2 = d.t3 = tiles_of(d.n0);
       break;
   }
@@ -367,9 +374,11 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
 // wait_stores: every store the block issued before (cleared accumulators, KV rows, DeltaNet
 // states) completes before the first contribution is added, so whoever observes the
 // contributions can read what those stores wrote.
+// The column sums are multiplied by `scale` (a deferred RMSNorm scale, else 1); thread n < kTile
+// adds `base` (fixed point) to its column's contribution.
 template <int U>
 Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, const float* xs, float* red,
-                        bool wait_stores, float scale, float aux = 0.f, fx_t* aux_dst = nullptr) {
+                        bool wait_stores, float scale, fx_t base, float aux = 0.f, fx_t* aux_dst = nullptr) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
@@ -426,7 +435,7 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
 #pragma unroll
     for (int i = 0; i < kNW; ++i) v += pr[i];
     const int n = it.tl * kTile + tid;
-    if (n < it.N) fxc_add(a, &it.acc[n + (n & it.spm)], v * scale);
+    if (n < it.N) fxc_add(a, &it.acc[n + (n & it.spm)], v * scale, base);
   }
   __syncthreads();
 }
@@ -439,15 +448,14 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
 // ones (counted inputs), `src.conv` turns it into f32.  `post` (more weight loads of the caller)
 // is issued behind the prologue's loads and before their first use; scheduling barriers keep the
 // compiler from moving either group across it.  Returns false when a wait failed.
-// DEFER: xs gets x * (1 + w) only, and each wave leaves its part of the sum of squares in shs;
-// the caller applies rsqrt(mean + eps) to the matvec's column sums (the scale is the same for
-// every row, so W^T (x r (1 + w)) = r W^T (x (1 + w))), which takes the block sum off the path to
-// the multiply-adds.
+// DEFER: xs gets x * (1 + w) only, and each wave leaves its part of the sum of squares in shs; the
+// caller applies rsqrt(mean + eps) to the matvec's column sums (the scale is the same for every
+// row: W^T (x r (1 + w)) = r W^T (x (1 + w))), which takes the block sum off the path to the
+// multiply-adds.
 template <int KR, bool DEFER, class Raw, class Src, class Post>
-Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, int K, const float* w, int k0, int klen, float* xs, float* shs,
-                     Post post) {
+Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, Raw (&raw)[KR], int K, const float* w, int k0, int klen, float* xs,
+                     float* shs, Post post) {
   const int tid = tix();
-  Raw raw[KR];
   float wn[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
@@ -458,7 +466,7 @@ Q35_DEV bool pro_rms(const StepArgs& a, const Src& src, int K, const float* w, i
   __builtin_amdgcn_sched_barrier(0);
   post();
   __builtin_amdgcn_sched_barrier(0);
-  const bool ok = src.template complete<KR>(a, raw, K);
+  const bool ok = src.template complete<KR>(a, raw, K, 0, K);
   float v[KR];
   float ss = 0.f;
 #pragma unroll
@@ -495,8 +503,9 @@ struct HSrc {
   Q35_DEV const fx_t* at(int k) const { return h + (k + (k & ~15)); }
   Q35_DEV fx_t load(int k) const { return ld_agent(at(k)); }
   Q35_DEV float conv(fx_t x) const { return fxc_val(x, e); }
+  // completes the thread's elements k in [lo, hi) (the others may stay incomplete)
   template <int KR>
-  Q35_DEV bool complete(const StepArgs& a, fx_t (&raw)[KR], int K) const {
+  Q35_DEV bool complete(const StepArgs& a, fx_t (&raw)[KR], int K, int lo, int hi) const {
     return gather<KR>(
         a, raw,
         [&](fx_t (&r)[KR]) {
@@ -504,7 +513,10 @@ struct HSrc {
           for (int j = 0; j < KR; ++j) r[j] = load(min(tix() + kT * j, K - 1));
         },
         [&](int j) { return (const void*)at(min(tix() + kT * j, K - 1)); },
-        [&](int, uint64_t w) { return fxc_ok((fx_t)w, e); });
+        [&](int j, uint64_t w) {
+          const int k = min(tix() + kT * j, K - 1);
+          return k < lo || k >= hi || fxc_ok((fx_t)w, e);
+        });
   }
 };
 // a row of the Q8F embedding table as pro_rms input: (byte, block scale) pairs
@@ -518,7 +530,7 @@ struct EmbSrc {
   Q35_DEV EmbRaw load(int k) const { return EmbRaw{ldg(q + k), ldg(s + (k >> 6))}; }
   Q35_DEV float conv(EmbRaw x) const { return (float)x.q * x.s; }
   template <int KR>
-  Q35_DEV bool complete(const StepArgs&, EmbRaw (&)[KR], int) const { return true; }
+  Q35_DEV bool complete(const StepArgs&, EmbRaw (&)[KR], int, int, int) const { return true; }
 };
 
 // The argmax of token ti from the per-block partials (the reference's order), once all carry
@@ -854,10 +866,20 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
   GdnPf gp;
   float auxw = 0.f;
   const int naux = 2 * a.nh;
+  // A residual stage adds into a fresh copy of the stream (t.hn); its first-chunk items carry the
+  // previous copy (t.h, complete: every block that reads this stage's inputs has seen it so) into
+  // it, each with its columns' words, loaded with the weights and checked after the prologue.
+  const bool carry = (kind == SMV_OUT || kind == SMV_O || kind == SMV_DOWN) && t.h != t.hn;
+  auto carry_at = [&]() {
+    const int n = min(it.tl * kTile + (tix() & (kTile - 1)), it.N - 1);
+    return &t.h[n + (n & ~15)];
+  };
+  fx_t hp[1] = {0};
   if (item < nitems) {
     it = mv_item(d, item);
     mv_load(it, d.K, pf);
     if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
+    if (carry && it.k0 == 0) hp[0] = ld_agent(carry_at());
   }
   int tok = 0;
   // Blocks with an item need the token for the embedding; with stop ids every block forms it,
@@ -869,24 +891,6 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       return kStageStop;
     }
   }
-  if (item >= nitems) {
-    // A block without an item still waits until the residual stream it would have read is
-    // complete (one word): a block that skipped the reads could otherwise run ahead far enough
-    // that a word's contribution count (modulo 256) repeats, and take an early value for a later
-    // one.  With this wait a block's reads of the stream are never more than two residual stages
-    // (at most 2 x 120 contributions) apart.
-    if (pro == PRO_RMS) {
-      bool ok = true;
-      if (tix() < 64) {
-        const uint64_t* w0 = reinterpret_cast<const uint64_t*>(HSrc{t.h, t.hc}.at((bix() * 67) % a.H));
-        ok = wait_on(a, w0, [&](uint64_t w) { return fxc_ok((fx_t)w, t.hc); });
-      }
-      if (!ok) *sh.fail = 1;
-      __syncthreads();
-      if (*sh.fail) return kStageFail;
-    }
-    return kStageOk;
-  }
   float* xs = sh.smem + kXs;
   float* red = sh.smem + kRed;
   for (bool first = true; item < nitems; item += gridDim.x, first = false) {
@@ -894,6 +898,7 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       it = mv_item(d, item);
       mv_load(it, d.K, pf);
       if (pro == PRO_GDN) gdn_load(a, L, it, i, gp);
+      if (carry && it.k0 == 0) hp[0] = ld_agent(carry_at());
     }
     // the qkvz item's gate column (a 64-byte-strided gather) is issued behind the norm's inputs
     auto aux_load = [&]() {
@@ -903,17 +908,20 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       }
     };
     bool ok = true;
+    const HSrc hsrc{t.h, t.hc};
+    fx_t hraw[KR];
     switch (pro) {
       case PRO_EMBED_RMS: {
         const int K = d.K, nbK = K >> 6;
         const EmbSrc src{a.emb_q + (size_t)tok * K, a.emb_s + (size_t)tok * nbK};
-        pro_rms<KR, true, EmbRaw>(a, src, K, L.in_norm, it.k0, it.klen, xs, sh.shs, aux_load);
+        EmbRaw eraw[KR];
+        pro_rms<KR, true, EmbRaw>(a, src, eraw, K, L.in_norm, it.k0, it.klen, xs, sh.shs, aux_load);
         if (bix() == 0 && first)  // the residual stream starts as the embedding row (one contribution)
-          for (int k = tix(); k < K; k += kT) fxc_add(a, &t.h[k + (k & ~15)], src.conv(src.load(k)));
+          for (int k = tix(); k < K; k += kT) fxc_add(a, &t.hn[k + (k & ~15)], src.conv(src.load(k)));
       } break;
       case PRO_RMS:
-        ok = pro_rms<KR, true, fx_t>(a, HSrc{t.h, t.hc}, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, it.k0, it.klen, xs,
-                               sh.shs, aux_load);
+        ok = pro_rms<KR, true, fx_t>(a, hsrc, hraw, d.K, kind == SMV_GU ? L.post_norm : L.in_norm, it.k0, it.klen, xs,
+                                     sh.shs, aux_load);
         break;
       case PRO_GDN:
         ok = pro_gdn(a, L, t, it, i, gp, xs, red);
@@ -937,6 +945,10 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
         ok = pro_attn(a, t, p + 1, it.k0, it.klen, xs, red);
         break;
     }
+    if (ok && carry && it.k0 == 0)
+      ok = gather<1>(
+          a, hp, [&](fx_t (&r)[1]) { r[0] = ld_agent(carry_at()); }, [&](int) { return (const void*)carry_at(); },
+          [&](int, uint64_t w) { return fxc_ok((fx_t)w, t.hc); });
     if (!ok) *sh.fail = 1;
     __syncthreads();
     if (*sh.fail) return kStageFail;
@@ -947,29 +959,22 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       const float ss = ((((((s0.x + s0.y) + s0.z) + s0.w) + s1.x) + s1.y) + s1.z) + s1.w;
       rn = rsqrt_f(ss * rcp_f((float)d.K) + a.eps);
     }
-    // in_proj_b | in_proj_a column it.tile: each wave's part of the dot product goes into the
-    // matvec reduction (further columns, when there are more than tiles, reduce on their own)
+    // in_proj_b | in_proj_a column it.tile (there are at least as many qkvz tiles, 1.5 nh + 0.5 nh
+    // rounded up, as the 2 nh columns): each wave's part of the dot product goes into the matvec
+    // reduction
     float auxp = 0.f;
     fx_t* auxd = nullptr;
-    if (kind == SMV_QKVZ) {
-      for (int o = it.tile; o < naux; o += d.t3) {
-        float w = auxw;
-        if (o != it.tile || !first) {
-          const float* W = o < a.nh ? L.w_b : L.w_a;
-          w = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (o % a.nh)));
-        }
-        const float v = (tix() < it.klen) ? xs[tix()] * w : 0.f;
-        fx_t* dst = t.acc + a.acc_ba_off + (size_t)o * kStepBaStride;
-        if (o == it.tile) {
-          auxp = wave_sum(v);
-          auxd = dst;
-        } else {
-          const float s = block_sum(v, sh.shs);
-          if (tix() == 0) fxc_add(a, dst, s * rn);
-        }
+    if (kind == SMV_QKVZ && it.tile < naux) {
+      float w = auxw;
+      if (!first) {
+        const float* W = it.tile < a.nh ? L.w_b : L.w_a;
+        w = ldg(W + ((size_t)(it.k0 + min(tix(), it.klen - 1)) * a.nh + (it.tile % a.nh)));
       }
+      auxp = wave_sum((tix() < it.klen) ? xs[tix()] * w : 0.f);
+      auxd = t.acc + a.acc_ba_off + (size_t)it.tile * kStepBaStride;
     }
-    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, rn, auxp, auxd);
+    const fx_t base = (carry && it.k0 == 0) ? (fx_t)((uint64_t)hp[0] - cnt_of(t.hc)) : 0;
+    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, rn, base, auxp, auxd);
   }
   return kStageOk;
 }
@@ -1242,7 +1247,8 @@ Q35_DEV bool lm_stage(const StepArgs& a, const Tok& t, const Shared& sh) {
   const int rb0 = bix(), gs = gridDim.x;
   if (rb0 < nrb) load(rb0, wa, sa);
   // the second row block is issued behind the norm's inputs (rows clamped: always in the table)
-  const bool ok = pro_rms<2 * CPW, false, fx_t>(a, HSrc{t.h, t.hc}, K, a.final_norm, 0, K, xs, sh.shs,
+  fx_t hraw[2 * CPW];
+  const bool ok = pro_rms<2 * CPW, false, fx_t>(a, HSrc{t.h, t.hc}, hraw, K, a.final_norm, 0, K, xs, sh.shs,
                                          [&]() { load(rb0 + gs, wb, sb); });
   if (!ok) *sh.fail = 1;
   __syncthreads();
@@ -1250,11 +1256,12 @@ Q35_DEV bool lm_stage(const StepArgs& a, const Tok& t, const Shared& sh) {
   {
     // clear the other parity set (the next token's residual stream and accumulators): the last
     // readers of it were the previous token's, and every block finished those before this token
-    const int64_t nh = 2 * (int64_t)a.H, na = (int64_t)a.n_layers * a.acc_stride, n = nh + na;
-    fx_t* hz = a.h + (size_t)((t.ti + 1) & 1) * nh;
+    // (of the stream copies only the words in use: 16 of every 32)
+    const int64_t nh = (int64_t)a.n_res * a.H, na = a.acc_par, n = nh + na;
+    fx_t* hz = a.h + (size_t)((t.ti + 1) & 1) * 2 * nh;
     fx_t* az = a.acc + (size_t)((t.ti + 1) & 1) * na;
     const int64_t per = (n + gs - 1) / gs, lo = (int64_t)bix() * per, hi = min(n, lo + per);
-    for (int64_t q = lo + tid; q < hi; q += kT) st_agent(q < nh ? &hz[q] : &az[q - nh], (fx_t)0);
+    for (int64_t q = lo + tid; q < hi; q += kT) st_agent(q < nh ? &hz[q + (q & ~15)] : &az[q - nh], (fx_t)0);
   }
   for (int rb = rb0; rb < nrb; rb += 2 * gs) {
     if (rb != rb0 && rb + gs < nrb) load(rb + gs, wb, sb);
@@ -1330,9 +1337,17 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
     Tok t;
     t.ti = ts0 + (uint32_t)i;
     const int par = (int)(t.ti & 1u);
-    t.h = a.h + (size_t)par * 2 * a.H;
-    fx_t* acc0 = a.acc + (size_t)par * a.n_layers * a.acc_stride;
-    t.hc = 1;  // the embedding row
+    t.hn = a.h + (size_t)par * a.n_res * 2 * a.H;  // the first copy: the embedding row + the first mixer
+    t.h = t.hn;
+    fx_t* acc0 = a.acc + (size_t)par * a.acc_par;
+    t.hc = 0;
+    // after a residual stage: its copy is the stream (a word holds the stage's chunk contributions,
+    // the first chunk's carrying the previous copy, and in the first copy the embedding row)
+    auto advance = [&](int kind, bool more) {
+      t.hc = (t.h == t.hn ? 1u : 0u) + (uint32_t)a.mv[kind].nchunk;
+      t.h = t.hn;
+      if (more) t.hn += 2 * a.H;
+    };
     for (int l = 0; l < a.n_layers; ++l) {
       CLayer& L = layer_at(a, l);
       t.l = l;
@@ -1344,18 +1359,18 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
         if (!mv_stage<kUOut, KR>(a, L, t, SMV_OUT, PRO_GDN, i, p, sh)) return;
-        t.hc += (uint32_t)a.mv[SMV_OUT].nchunk;
+        advance(SMV_OUT, true);
       } else {
         r = mv_stage<kU, KR>(a, L, t, SMV_QKV, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
         if (!attn_stage(a, L, t, p, sh)) return;
         if (!mv_stage<kU, KR>(a, L, t, SMV_O, PRO_ATTN, i, p, sh)) return;
-        t.hc += (uint32_t)a.mv[SMV_O].nchunk;
+        advance(SMV_O, true);
       }
       if (!mv_stage<kU, KR>(a, L, t, SMV_GU, PRO_RMS, i, p, sh)) return;
       if (!mv_stage<kU, KR>(a, L, t, SMV_DOWN, PRO_SWIGLU, i, p, sh)) return;
-      t.hc += (uint32_t)a.mv[SMV_DOWN].nchunk;
+      advance(SMV_DOWN, l + 1 < a.n_layers);  // the last copy is read by the lm stage
     }
     if (executed != a.ntok) break;
     if (!lm_stage<CPW>(a, t, sh)) return;
