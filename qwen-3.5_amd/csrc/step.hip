@@ -39,9 +39,10 @@
 // one memory round trip from the last producer's add to the consumer's data, where an arrive
 // (after the adds' acknowledgements), a barrier poll and a separate input read took three.
 // Ordering of the plain stores that are not tagged (KV rows, DeltaNet states, the clearing of
-// the next token's accumulators) follows from the data: a block waits for its stores to
-// complete before its next published contribution, and every later reader of them first
-// observes that contribution (or one that depends on it).  No counted word is ever added to
+// the next token's accumulators) follows from the data: none is read within the token that
+// wrote it, a block waits for all its stores to complete before it publishes its argmax partial
+// of the token, and every reader in a later token first observes all partials (or data made by
+// blocks that did).  No counted word is ever added to
 // after its readers' count is reached: accumulators are not re-used within a token (one set per
 // layer), and the residual stream has a copy per residual stage, which receives the previous
 // copy once (the stage's first-chunk items add it with their contributions) and that stage's
@@ -67,8 +68,8 @@ constexpr int kT = kStepThreads;  // 512
 constexpr int kNW = kT / 64;      // waves per block
 constexpr int kTile = 256;
 constexpr int kRG = kT / 16;      // matvec row groups (16 lanes cover a 256-byte tile row)
-constexpr int kU = 16;            // rows per lane per item
-constexpr int kKch = kRG * kU;    // rows per item, at most 512
+constexpr int kU = 13;            // rows per lane per item (the register budget)
+constexpr int kKch = kRG * kU;    // rows per item, at most 416
 constexpr int kRmsRegs = 8;       // RMSNorm prologue: K <= 8 * 512
 constexpr uint32_t kSpin = 1u << 21;  // polls before a wait gives up (seconds)
 constexpr int kHd = 256;          // attention head dim
@@ -371,14 +372,11 @@ Q35_DEV void mv_load(const MvItem& it, int K, MvPf<U>& pf) {
 
 // y[tile cols] += scale * sum over the item's rows of x[k] * dequant(W[k][cols]); x chunk in xs.  aux_dst
 // (optional): one more sum, of which each wave holds its part in aux, reduced with the columns.
-// wait_stores: every store the block issued before (cleared accumulators, KV rows, DeltaNet
-// states) completes before the first contribution is added, so whoever observes the
-// contributions can read what those stores wrote.
 // The column sums are multiplied by `scale` (a deferred RMSNorm scale, else 1); thread n < kTile
 // adds `base` (fixed point) to its column's contribution.
 template <int U>
 Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, const float* xs, float* red,
-                        bool wait_stores, float scale, fx_t base, float aux = 0.f, fx_t* aux_dst = nullptr) {
+                        float scale, fx_t base, float aux = 0.f, fx_t* aux_dst = nullptr) {
   const int tid = tix(), cg = tid & 15, rr = tid >> 4;
   float acc[16];
 #pragma unroll
@@ -417,7 +415,6 @@ Q35_DEV void mv_compute(const StepArgs& a, const MvItem& it, const MvPf<U>& pf, 
   }
   *reinterpret_cast<float4*>(&red[(rr >> 2) * kTile + cg * 16 + 4 * (rr & 3)]) = make_float4(t4[0], t4[1], t4[2], t4[3]);
   if (aux_dst && (tid & 63) == 0) red[kNW * kTile + (tid >> 6)] = aux;
-  if (wait_stores) __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (aux_dst && tid == 0) {
     float s = 0.f;
@@ -974,7 +971,7 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
       auxd = t.acc + a.acc_ba_off + (size_t)it.tile * kStepBaStride;
     }
     const fx_t base = (carry && it.k0 == 0) ? (fx_t)((uint64_t)hp[0] - cnt_of(t.hc)) : 0;
-    mv_compute(a, it, pf, xs, red, kind != SMV_OUT, rn, base, auxp, auxd);
+    mv_compute(a, it, pf, xs, red, rn, base, auxp, auxd);
   }
   return kStageOk;
 }
@@ -1162,8 +1159,6 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const
 #pragma unroll
     for (int h = 0; h < kMaxRep; ++h)
       *reinterpret_cast<float4*>(&ored[(wid * kMaxRep + h) * kHd + 4 * lane]) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-    // the KV row appended above completes before the partials that o_proj's readers observe
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const size_t pc = (size_t)g * a.att_nmax + c;
     for (int e2 = tid; e2 < rep * kHd; e2 += kT) {
@@ -1271,7 +1266,8 @@ Q35_DEV bool lm_stage(const StepArgs& a, const Tok& t, const Shared& sh) {
     compute(rb + gs, wb, sb);
   }
   block_argmax(best_v, best_i, sh.shv, sh.shi, a.ord);
-  // the clearing stores complete before the partial that the next token's blocks wait for
+  // every store of the block in this token (the clearing, KV rows, DeltaNet and conv states)
+  // completes before the partial that the next token's blocks wait for
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) st_agent64(&a.argp[(size_t)(t.ti & 1u) * gs + bix()], arg_pack(best_v, best_i, t.ti));
