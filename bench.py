@@ -344,6 +344,8 @@ def prefill_gemm_leg(torch, q35, st, d, T):
             "frac": round(2 * tf / MFMA_F16_PEAK_TFLOPS, 4),
             "unit": "TFLOP/s of f32-equivalent products (x @ dequant(W)); mfma_TFLOP/s counts both f16 MFMA "
                     "products (hi and lo halves of x * scale) against the f16 dense matrix-core peak",
+            "operands": "x * scale carried as f16 hi + lo: about 22 significant bits (the reference's f32 matmul "
+                        "has 24); the int8 weights are exact in f16; f32 accumulation",
             "vs_fp32_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
 
 
@@ -447,12 +449,17 @@ def copy_calibration():
     print("copied 3 x 1 GiB", flush=True)
 
 
-# HBM traffic of one step_kernel<2> launch of 64 decode steps at context 576-1088 of this workload:
-# FETCH_SIZE + WRITE_SIZE per dispatch from two rocprofv3 --pmc passes over
-# `bench.py --steps 512 --warmup 64 --no-cpu --no-sweep --no-layers`, each scaled by what the
-# counter reads for a 1 GiB copy (`bench.py --copy-calibration`).  A constant measured on the
-# kernel at the commit named in profiles/step_kernel_decode_2b_traffic.md, not in this run.
-STEP_TRAFFIC_PER_64 = 139.72e9
+# HBM traffic of one decode step of step_kernel<2> on this workload: FETCH_SIZE + WRITE_SIZE per
+# dispatch from two rocprofv3 --pmc passes over `bench.py --no-cpu --no-sweep --no-layers
+# --no-batch --no-readback --no-graph` (64-step launches at context 512-1040), each scaled by what
+# the counter reads for a 1 GiB copy (`bench.py --copy-calibration`), divided by the launch's
+# steps.  A constant measured on the kernel at the commit named in STEP_TRAFFIC_COMMIT (summary in
+# profiles/step_kernel_decode_2b_traffic.md), not in this run; a launch's traffic is this times its
+# steps (the weights, read once per step, are 95% of it).
+STEP_TRAFFIC_PER_STEP = 2.208e9
+STEP_TRAFFIC_COMMIT = "97823ca"
+GRAPH_STEPS = 64      # steps of the hipGraph-mode leg
+READBACK_STEPS = 64   # steps of the per-token readback leg
 
 
 # bench legs in the order main() runs them, each recognised by the first dispatch of its kernel
@@ -461,6 +468,8 @@ STEP_TRAFFIC_PER_64 = 139.72e9
 # (legs after the batched decode leg start after its last dispatch, whose kernels they share)
 TRACE_PHASES = (("model build + prompt prefill", None, False),
                 ("decode (persistent step kernel)", "step_kernel<", False),
+                ("hipGraph-mode decode leg", "mv_kn_kernel", False),
+                ("readback leg (one launch per token)", "step_kernel<", False),
                 ("prompt GEMM leg", "gemm_kernel", False), ("batched decode leg", "batch_embed", False),
                 ("matvec sweep", "mvp_kernel", True), ("gated delta rule decode leg", "gdn_step_kernel", False),
                 ("attention decode leg", "attn_chunk_kernel", False))
@@ -532,8 +541,9 @@ def main():
     ap.add_argument("--no-batch", action="store_true", help="skip the batched decode leg")
     ap.add_argument("--prefill-via-decode", action="store_true",
                     help="also time the prompt fed through the decode step (one token per step)")
-    ap.add_argument("--readback", action="store_true",
-                    help="also time one launch per token with a host readback each step (main.rs loop)")
+    ap.add_argument("--no-readback", action="store_true",
+                    help="skip the leg of one launch per token with a host readback each step (main.rs loop)")
+    ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph-captured step leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference point for FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -561,7 +571,7 @@ def main():
     d = q35.dims_2b()
     chunk = args.chunk
     n_pre, n_warm, n_timed = args.prompt, args.warmup, args.steps
-    tmax = n_pre + n_warm + n_timed + 8
+    tmax = n_pre + n_warm + n_timed + GRAPH_STEPS + READBACK_STEPS + 16
     log(f"building the 2B-shaped model (tmax {tmax})")
     t0 = time.time()
     m = q35.TextForCausalLM(d, seed=args.seed, tmax=tmax)
@@ -632,16 +642,33 @@ def main():
     achieved = sum(launch_bytes) / (sum(launch_ms) * 1e-3) / 1e9
     hist = m.tensor("hist", np.int32)[:ctx0 + n_timed]
     full = [i for i, n in enumerate(plan) if n == chunk]
-    traffic = None
-    if chunk == 64 and full:
-        traffic = STEP_TRAFFIC_PER_64
+    traffic = STEP_TRAFFIC_PER_STEP * plan[0]
 
+    # The same decode as a hipGraph-captured step (the whole step, about 120 kernels, one graph
+    # launch per token; the persistent kernel is the headline), continuing from the timed steps.
+    graph = None
+    if not args.no_graph:
+        c_g = ctx0 + n_timed
+        m.decode(2, mode="graph", stream=sh)  # capture, then one replay
+        m.check(stream=sh)
+        ge0, ge1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        tg = time.perf_counter()
+        ge0.record(st)
+        m.decode(GRAPH_STEPS, mode="graph", stream=sh)
+        ge1.record(st)
+        torch.cuda.synchronize()
+        g_wall = time.perf_counter() - tg
+        m.check(stream=sh)
+        graph = {"steps": GRAPH_STEPS, "ms_per_step": round(ge0.elapsed_time(ge1) / GRAPH_STEPS, 4),
+                 "tok_s": round(GRAPH_STEPS / g_wall, 2), "ctx_range": [c_g + 2, c_g + 2 + GRAPH_STEPS]}
+
+    # main.rs semantics (main.rs:100-107,149-155): one persistent launch per token, the token read
+    # back to the host (4 bytes) and the stream synchronised every step; the host-timed rate.
     toks_readback = None
-    if args.readback:  # main.rs semantics: one launch per token, token read back and synced each step
-        m.reset()
-        m.generate(prompt[:min(chunk, n_pre)], 0, mode="persistent", stream=sh)
-        _, dec_s = m.generate(prompt[:1], 64, mode="persistent", readback_each=True, stream=sh)
-        toks_readback = 64 / dec_s
+    if not args.no_readback:
+        _, dec_s = m.generate(prompt[:1], READBACK_STEPS, mode="persistent", readback_each=True, stream=sh)
+        toks_readback = READBACK_STEPS / dec_s
     m.close()
 
     log("prompt GEMM leg")
@@ -687,21 +714,29 @@ def main():
                    "launch": f"persistent step kernel, steps per launch {plan}, grid {grid}x512"},
         "roofline": {"kernel": "step_kernel<2>: persistent decode step",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_note": "FETCH_SIZE+WRITE_SIZE per 64-step launch, calibrated; a constant measured "
-                                     "at the commit in profiles/, not in this run" if traffic else None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": round(traffic),
+                     "traffic_note": f"HBM bytes per launch of {plan[0]} steps: calibrated FETCH_SIZE+WRITE_SIZE "
+                                     f"per step ({STEP_TRAFFIC_PER_STEP / 1e9:.3f} GB, rocprofv3 --pmc on the step "
+                                     f"kernel at commit {STEP_TRAFFIC_COMMIT}, not in this run) x steps",
                      "steps_per_launch": plan[0],
                      "bytes_per_launch": int(np.mean([launch_bytes[i] for i in full])) if full else int(launch_bytes[0]),
                      "avg_launch_us": round(1e3 * float(np.mean([launch_ms[i] for i in full])) if full
                                             else 1e3 * launch_ms[0], 1)},
         "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
         "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
+        "readback_note": None if toks_readback is None else
+            f"{READBACK_STEPS} steps, one persistent launch per token plus a 4-byte token readback and a stream "
+            "synchronise each step (the reference's loop), host-timed",
+        "graph_mode": graph,
+        "graph_mode_note": None if graph is None else
+            "the whole decode step (about 120 kernels) captured once in a hipGraph and replayed per token; "
+            "ms_per_step from HIP events, tok_s host-timed",
         "prefill": {"tokens": n_pre, "ms": round(prefill_ms, 3), "tok_s": round(n_pre / (prefill_ms * 1e-3), 1),
                     "timed_passes_ms": [round(x, 3) for x in prefill_pass_ms],
                     "wall_ms_incl_prompt_upload": round(prefill_wall_s * 1e3, 3),
-                    "path": "one forward at seq_len = prompt: Q8F GEMMs on the f16 matrix cores (f32-equivalent "
-                            "products), causal conv + chunked gated delta rule, causal attention; lm_head on the last "
-                            "row",
+                    "path": "one forward at seq_len = prompt: Q8F GEMMs on the f16 matrix cores (x * scale as f16 "
+                            "hi + lo, about 22 significant bits; f32 accumulation), causal conv + chunked gated delta "
+                            "rule, causal attention; lm_head on the last row",
                     "gemm_leg": pgemm},
         "batched_decode": batched,
         "batched_decode_note": None if batched is None else
