@@ -40,6 +40,11 @@ enum {
   Q35_E_ARG = 4,     /* NULL pointer or invalid enum */
   Q35_E_WS = 5,      /* workspace smaller than the *_ws_bytes() requirement */
   Q35_E_NOMEM = 6,   /* device or host allocation failed (model creation only) */
+  Q35_E_RANGE = 7,   /* a value bound for a fixed-point accumulator was not finite or out of
+                        range (|v| >= 2^31; 2^22 in the persistent step kernel): it was dropped and
+                        the results of the calls since the last check are invalid.  Where the
+                        reference's f32 sums would carry a NaN / Inf on, the split-K fixed-point
+                        sums cannot hold one, so the library reports it instead. */
 };
 
 /* Storage layouts of a Q8F matrix.
@@ -208,11 +213,16 @@ int q35_attention_core_decode(const q35_dims* d, const float* q_gate, const floa
 /* Workspace large enough for any of the layer calls above with these B / tmax. */
 size_t q35_layer_ws_bytes(const q35_dims* d, int32_t B, int32_t tmax);
 
-/* Device-side argument errors recorded in a layer workspace by earlier calls on `stream`
- * (synchronises it), then cleared.  Q35_E_SHAPE: an attention call met a position d_pos[b]
- * outside [0, tmax); that row's cache and output were left untouched.  No reference counterpart
- * (the reference panics on the host, text_modules.rs); it exists because the positions live in
- * device memory, where the host cannot check them without a synchronisation. */
+/* Device-side errors recorded in a layer workspace by earlier calls on `stream` (synchronises
+ * it), then cleared.  Q35_E_SHAPE: an attention call met a position d_pos[b] outside [0, tmax);
+ * that row's cache and output were left untouched.  Q35_E_RANGE: a projection or gate sum met a
+ * non-finite value or one of magnitude >= 2^31 (an input row holding NaN / Inf or overflowing
+ * values); it was dropped, so the outputs of the calls since the last check are invalid.  Both
+ * bits may be set; Q35_E_SHAPE is reported first.  Also reads the q35_q8_gemv workspace.  No
+ * reference counterpart (the reference panics on a bad position on the host, text_modules.rs, and
+ * carries a NaN through its f32 sums); it exists because the positions live in device memory,
+ * where the host cannot check them without a synchronisation, and because the fixed-point sums
+ * cannot hold a NaN. */
 int q35_workspace_status(void* ws, void* stream);
 
 /* Host: cos/sin tables [tmax][rot_dim] of TextRotaryEmbedding::forward for positions 0..tmax-1
@@ -329,11 +339,14 @@ int q35_model_step(q35_model* m, int32_t use_graph, void* stream);
  * Q35_LAUNCH_PERSISTENT mode all steps are one kernel launch. */
 int q35_model_decode(q35_model* m, int32_t n_steps, int32_t mode, void* stream);
 
-/* Synchronises the stream and reports a persistent-kernel failure (a grid barrier that timed
- * out; the kernel then exits early and its results are invalid).  Q35_OK otherwise.  The failure
- * is sticky: it is kept in device memory that no launch clears, every later persistent launch
- * returns at entry without touching the model state, and q35_model_step / _decode / _generate
- * refuse persistent mode once a check has seen it, until q35_model_reset. */
+/* Synchronises the stream and reports a failure of the launches since the last check:
+ * Q35_E_HIP for a persistent-kernel wait that timed out (the kernel then exits early and its
+ * results are invalid), Q35_E_RANGE for a non-finite or out-of-range value met by a fixed-point
+ * accumulator in any launch mode.  Q35_OK otherwise.  A persistent-kernel failure is sticky: it
+ * is kept in device memory that no launch clears, every later persistent launch returns at entry
+ * without touching the model state, and q35_model_step / _decode / _generate refuse persistent
+ * mode once a check has seen it, until q35_model_reset.  q35_model_generate / _generate_until /
+ * _decode_until run this check themselves. */
 int q35_model_check(q35_model* m, void* stream);
 
 /* Grid of the persistent step kernel (blocks, one per CU); returns an error code and message
@@ -423,7 +436,10 @@ int q35_batch_decode(q35_batch* b, int32_t n_steps, int32_t mode, void* stream);
  * q35_model_generate does for one.  Prompts are fed through the decode step (every row steps
  * max(len) + n_new times; a row with a shorter prompt generates past n_new, so tmax must allow
  * that) or, with Q35_PREFILL_GEMM in mode, through the prompt path one sequence at a time and
- * then n_new batched steps.  decode_seconds_host (optional): wall time of the batched steps. */
+ * then n_new batched steps.  decode_seconds_host (optional): wall time of the batched steps.
+ * Returns Q35_E_RANGE when a norm statistic or gate sum of this or an earlier q35_batch_step /
+ * _decode met a non-finite or out-of-range value (the batch state is then invalid until
+ * q35_batch_reset). */
 int q35_batch_generate(q35_batch* b, const int32_t* prompts_host, const int32_t* lens_host, int32_t n_new,
                        int32_t* out_tokens_host, int32_t mode, double* decode_seconds_host, void* stream);
 /* Host copy of the B positions. */

@@ -24,7 +24,7 @@
 namespace q35 {
 int batch_embed_f32_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
                            const int32_t* plen, const int32_t* pos, float* h, fx_t* ss, fx_t* zero_ptr, int64_t zero_n,
-                           int B, hipStream_t st);
+                           uint32_t* err, int B, hipStream_t st);
 int batch_argmax_groups(int V);
 int batch_argmax_launch(const float* logits, int V, int B, float* pv, int32_t* pi, int32_t* token, int32_t* pos,
                         int32_t* hist, int ldh, hipStream_t st);
@@ -105,11 +105,13 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
   std::vector<int32_t> gu_two((B + kRowGroup - 1) / kRowGroup, 0);  // gate|up left two partials
   // embedding rows + the first norm's statistic; clears every other statistic and gate sum
   if ((rc = batch_embed_f32_launch(m->embed.q, m->embed.s, H, bt->token, bt->prompt, bt->tmax, bt->plen, bt->pos, bt->h,
-                                   bt->ss, bt->ss + B, (int64_t)2 * NL * B + (int64_t)NL * B * kGateLd, B, st)))
+                                   bt->ss, bt->ss + B, (int64_t)2 * NL * B + (int64_t)NL * B * kGateLd,
+                                   ws_counters(bt->ws) + kWsErrWord, B, st)))
     return rc;
   auto base = [&](MbCall& c, int M) {
     c.M = M; c.eps = d.eps;
     c.part = bt->part; c.part_floats = bt->part_floats; c.ctr = bt->mb_ctr; c.nctr = kMbCounters;
+    c.err = ws_counters(bt->ws) + kWsErrWord;
   };
   for (int l = 0; l < NL; ++l) {
     const q35_model::Layer& L = m->layers[l];
@@ -311,6 +313,25 @@ SeqView row_view(q35_batch* b, int r) {
 }  // namespace
 }  // namespace q35
 
+namespace q35 {
+namespace {
+// Reads and clears the batch workspace's error word (after the stream is synchronised).
+int bcheck(q35_batch* b) {
+  uint32_t* word = ws_counters(b->ws) + kWsErrWord;
+  uint32_t v = 0;
+  Q35_HIP_TRY(hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost));
+  if (v == 0) return Q35_OK;
+  const uint32_t zero = 0;
+  Q35_HIP_TRY(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  if (v & kWsErrRange)
+    return fail(Q35_E_RANGE, "batch step: a value for a fixed-point sum (a norm statistic or gate sum) was not "
+                             "finite or |v| >= 2^31; the batch state is invalid until q35_batch_reset");
+  if (v & kWsErrPos) return fail(Q35_E_SHAPE, "batch step: an attention position was outside the cache");
+  return fail(Q35_E_HIP, "batch step: unknown error bits " + std::to_string(v));
+}
+}  // namespace
+}  // namespace q35
+
 using namespace q35;
 
 extern "C" {
@@ -396,6 +417,7 @@ int q35_batch_reset(q35_batch* b, void* stream) {
   hipStream_t st = bpick(b, stream);
   for (auto& kv : b->tensors)
     if (kv.first != "workspace") Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
+  Q35_HIP_TRY(hipMemsetAsync(ws_counters(b->ws) + kWsErrWord, 0, sizeof(uint32_t), st));
   std::fill(b->host_pos.begin(), b->host_pos.end(), 0);
   return Q35_OK;
 }
@@ -473,6 +495,7 @@ int q35_batch_generate(q35_batch* b, const int32_t* prompts_host, const int32_t*
     if ((rc = bstep(b, mode, st))) return rc;
   Q35_HIP_TRY(hipStreamSynchronize(st));
   const auto t1 = std::chrono::steady_clock::now();
+  if ((rc = bcheck(b))) return rc;
   if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
   for (int r = 0; r < B; ++r)
     Q35_HIP_TRY(hipMemcpy(out_tokens_host + (size_t)r * (n_new + 1), b->hist + (size_t)r * b->tmax + start[r] + lens_host[r] - 1,

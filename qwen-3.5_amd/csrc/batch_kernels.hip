@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kBT) void batch_embed_kernel(const int8_t* q, const
 __global__ __launch_bounds__(kBT) void batch_embed_f32_kernel(const int8_t* q, const float* s, int D,
                                                              const int32_t* token, const int32_t* prompt, int ldp,
                                                              const int32_t* plen, const int32_t* pos, float* h, fx_t* ss,
-                                                             fx_t* zero_ptr, int64_t zero_n) {
+                                                             fx_t* zero_ptr, int64_t zero_n, uint32_t* err) {
   __shared__ float sh[4];
   for (int64_t i = (int64_t)blockIdx.x * kBT + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * kBT) zero_ptr[i] = 0;
   const int b = blockIdx.x;
@@ -46,7 +46,10 @@ __global__ __launch_bounds__(kBT) void batch_embed_f32_kernel(const int8_t* q, c
     acc += e * e;
   }
   acc = block_sum256(acc, sh);
-  if (threadIdx.x == 0) ss[b] = to_fx(acc);
+  if (threadIdx.x == 0) {
+    if (!fx_addable(acc)) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)err, kWsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ss[b] = fx_addable(acc) ? to_fx(acc) : 0;
+  }
 }
 
 Q35_DEV void block_argmax256(float& v, int& i, float* shv, int* shi, const ArgOrder& o) {
@@ -107,9 +110,9 @@ __global__ __launch_bounds__(kBT) void batch_argmax_final_kernel(const float* pv
 
 int batch_embed_f32_launch(const int8_t* q, const float* s, int D, const int32_t* token, const int32_t* prompt, int ldp,
                            const int32_t* plen, const int32_t* pos, float* h, fx_t* ss, fx_t* zero_ptr, int64_t zero_n,
-                           int B, hipStream_t st) {
+                           uint32_t* err, int B, hipStream_t st) {
   hipLaunchKernelGGL(batch_embed_f32_kernel, dim3(B), dim3(kBT), 0, st, q, s, D, token, prompt, ldp, plen, pos, h, ss,
-                     zero_ptr, zero_n);
+                     zero_ptr, zero_n, err);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

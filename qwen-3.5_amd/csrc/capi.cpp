@@ -149,6 +149,7 @@ int q35_q8_gemv(const float* x, int32_t M, q35_q8f W, float* y, void* ws, size_t
     fx_t* acc = reinterpret_cast<fx_t*>(ws_scratch(ws));
     for (int m0 = 0; m0 < M; m0 += 8) {
       MvCall c;
+      c.err = ws_counters(ws) + kWsErrWord;
       c.K = K; c.M = std::min(8, M - m0); c.nseg = 1;
       c.seg[0] = seg_of(W, acc, N);
       c.pro = PRO_PLAIN; c.x = x + (size_t)m0 * K; c.ldx = K;
@@ -221,6 +222,9 @@ int q35_workspace_status(void* ws, void* stream) {
   Q35_HIP_TRY(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice));
   if (v & kWsErrPos)
     return fail(Q35_E_SHAPE, "attention: a row's position d_pos[b] was outside [0, tmax); that row was skipped");
+  if (v & kWsErrRange)
+    return fail(Q35_E_RANGE, "a value for a fixed-point sum was not finite or |v| >= 2^31 (NaN / Inf or overflowing "
+                             "inputs); it was dropped and the outputs are invalid");
   return fail(Q35_E_HIP, "workspace: unknown error bits " + std::to_string(v));
 }
 
@@ -256,6 +260,7 @@ int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const
   hipStream_t st = S(stream);
   for (int b0 = 0; b0 < B; b0 += 8) {  // in_proj_qkv | in_proj_z | in_proj_b,a (text_modules.rs:497-508,569-576)
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
     c.seg[0] = seg_of(w->in_proj_qkv, qkvz + (size_t)b0 * ldq, ldq);
     c.seg[1] = seg_of(w->in_proj_z, qkvz + (size_t)b0 * ldq + L.conv_dim, ldq);
@@ -271,6 +276,7 @@ int q35_gated_deltanet_decode(const q35_dims* d, const q35_gdn_weights* w, const
   if ((rc = gdn_step_launch(g, st))) return rc;
   for (int b0 = 0; b0 < B; b0 += 8) {  // gated RMSNorm + out_proj (:654-663); conv state advance
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = L.vdim; c.M = std::min(8, B - b0); c.nseg = 1;
     c.seg[0] = seg_of(w->out_proj, y + (size_t)b0 * L.H, L.H);
     c.pro = PRO_GATED; c.x = o + (size_t)b0 * L.vdim; c.ldx = L.vdim;
@@ -315,6 +321,7 @@ int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const flo
   hipStream_t st = S(stream);
   for (int b0 = 0; b0 < B; b0 += 8) {  // q_proj | k_proj | v_proj (text_modules.rs:855-893)
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 3;
     c.seg[0] = seg_of(w->q_proj, qkv + (size_t)b0 * LD, LD);
     c.seg[1] = seg_of(w->k_proj, qkv + (size_t)b0 * LD + ldqg, LD);
@@ -331,6 +338,7 @@ int q35_attention_decode(const q35_dims* d, const q35_attn_weights* w, const flo
   if ((rc = attn_launch_split(a, ws_counters(ws), ws_scratch(ws) + abytes, att_ws - kCounterBytes, st))) return rc;
   for (int b0 = 0; b0 < B; b0 += 8) {  // o_proj (:938-942)
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = ldo; c.M = std::min(8, B - b0); c.nseg = 1;
     c.seg[0] = seg_of(w->o_proj, y + (size_t)b0 * L.H, L.H);
     c.pro = PRO_PLAIN; c.x = att + (size_t)b0 * ldo; c.ldx = ldo;
@@ -360,6 +368,7 @@ int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, 
   hipStream_t st = S(stream);
   for (int b0 = 0; b0 < B; b0 += 8) {  // gate_proj | up_proj (text_modules.rs:1003-1004)
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = L.H; c.M = std::min(8, B - b0); c.nseg = 2;
     c.seg[0] = seg_of(w->gate_proj, gu + (size_t)b0 * 2 * L.F, 2 * L.F);
     c.seg[1] = seg_of(w->up_proj, gu + (size_t)b0 * 2 * L.F + L.F, 2 * L.F);
@@ -368,6 +377,7 @@ int q35_mlp_decode(const q35_dims* d, const q35_mlp_weights* w, const float* x, 
   }
   for (int b0 = 0; b0 < B; b0 += 8) {  // up * silu(gate) -> down_proj (:1005)
     MvCall c;
+    c.err = ws_counters(ws) + kWsErrWord;
     c.K = L.F; c.M = std::min(8, B - b0); c.nseg = 1;
     c.seg[0] = seg_of(w->down_proj, y + (size_t)b0 * L.H, L.H);
     c.pro = PRO_SWIGLU; c.xf = gu + (size_t)b0 * 2 * L.F; c.ldx = 2 * L.F; c.swiglu_off = L.F;

@@ -52,6 +52,7 @@ int launch_step(q35_model* m, hipStream_t st) {
   for (int l = 0; l < d.n_layers; ++l) {
     const q35_model::Layer& L = m->layers[l];
     MvCall c;
+    c.err = ws_counters(m->ws) + kWsErrWord;
     c.K = H; c.M = 1; c.xf = m->h; c.ldx = H; c.pw = L.in_norm; c.eps = d.eps;
     c.zero_ptr = m->acc_gu; c.zero_n = 2 * (int64_t)F;
     if (l == 0) {
@@ -73,6 +74,7 @@ int launch_step(q35_model* m, hipStream_t st) {
       g.ld_o = vdim; g.B = 1; g.nh = nh; g.dk = dk; g.dv = dv; g.conv_k = d.conv_k;
       if ((rc = gdn_step_launch(g, st))) return rc;
       MvCall c2;
+      c2.err = ws_counters(m->ws) + kWsErrWord;
       c2.K = vdim; c2.M = 1; c2.nseg = 1;
       c2.seg[0] = MvSeg{L.out.q, L.out.s, m->h, H, H, 1};
       c2.pro = PRO_GATED; c2.x = m->o_raw; c2.ldx = vdim; c2.x2f = m->acc_proj + conv_dim; c2.ldx2 = ldq;
@@ -93,12 +95,14 @@ int launch_step(q35_model* m, hipStream_t st) {
       a.out = m->attn; a.ld_out = ah * hd; a.B = 1; a.nh = ah; a.nkv = kvh; a.hd = hd;
       if ((rc = attn_launch(a, m->ws, m->ws_bytes, st))) return rc;
       MvCall c2;
+      c2.err = ws_counters(m->ws) + kWsErrWord;
       c2.K = ah * hd; c2.M = 1; c2.nseg = 1;
       c2.seg[0] = MvSeg{L.o.q, L.o.s, m->h, H, H, 1};
       c2.pro = PRO_PLAIN; c2.x = m->attn; c2.ldx = ah * hd;
       if ((rc = mv_kn_launch(c2, st))) return rc;
     }
     MvCall c3;
+    c3.err = ws_counters(m->ws) + kWsErrWord;
     c3.K = H; c3.M = 1; c3.nseg = 2;
     c3.seg[0] = MvSeg{L.gate.q, L.gate.s, m->acc_gu, F, 2 * F, 1};
     c3.seg[1] = MvSeg{L.up.q, L.up.s, m->acc_gu + F, F, 2 * F, 1};
@@ -106,6 +110,7 @@ int launch_step(q35_model* m, hipStream_t st) {
     c3.zero_ptr = m->acc_proj; c3.zero_n = m->acc_proj_n + 2 * nh;  // acc_ba follows acc_proj
     if ((rc = mv_kn_launch(c3, st))) return rc;
     MvCall c4;
+    c4.err = ws_counters(m->ws) + kWsErrWord;
     c4.K = F; c4.M = 1; c4.nseg = 1;
     c4.seg[0] = MvSeg{L.down.q, L.down.s, m->h, H, H, 1};
     c4.pro = PRO_SWIGLU; c4.xf = m->acc_gu; c4.ldx = 2 * F; c4.swiglu_off = F;
@@ -254,7 +259,7 @@ const char* kStepRange = "persistent step: a value to be accumulated in fixed po
 // caller then re-reads the device position (sync_pos).
 int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nullptr, int n_stop = 0) {
   if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
-  if (m->step_failed) return fail(Q35_E_HIP, m->step_fail_msg);
+  if (m->step_failed) return fail(m->step_fail_code, m->step_fail_msg);
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
   StepArgs a = m->step_args;
   a.ntok = n;
@@ -469,15 +474,35 @@ int prefill(q35_model* m, int n, hipStream_t st) {
 // Reads the persistent kernel's sticky error word (synchronises the stream).
 int check_persistent(q35_model* m, hipStream_t st) {
   if (m->step_rc != Q35_OK) return Q35_OK;
-  if (m->step_failed) return fail(Q35_E_HIP, m->step_fail_msg);
+  if (m->step_failed) return fail(m->step_fail_code, m->step_fail_msg);
   Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 8, m->step_args.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
   Q35_HIP_TRY(hipStreamSynchronize(st));
   if (m->pinned[8] != 0) {
     m->step_failed = true;
     m->step_fail_msg = (m->pinned[8] & kStepErrRange) ? kStepRange : kStepFailed;
-    return fail(Q35_E_HIP, m->step_fail_msg);
+    m->step_fail_code = (m->pinned[8] & kStepErrRange) ? Q35_E_RANGE : Q35_E_HIP;
+    return fail(m->step_fail_code, m->step_fail_msg);
   }
   return Q35_OK;
+}
+
+// Reads and clears the workspace error word of the stepwise launch modes (synchronises the
+// stream): kWsErrRange, a fixed-point accumulator met a non-finite or out-of-range value;
+// kWsErrPos, an attention position outside the cache.
+int check_numeric(q35_model* m, hipStream_t st) {
+  uint32_t* word = ws_counters(m->ws) + kWsErrWord;
+  Q35_HIP_TRY(hipMemcpyAsync(m->pinned + 9, word, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  const uint32_t v = (uint32_t)m->pinned[9];
+  if (v == 0) return Q35_OK;
+  m->pinned[9] = 0;
+  Q35_HIP_TRY(hipMemcpyAsync(word, m->pinned + 9, sizeof(uint32_t), hipMemcpyHostToDevice, st));
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  if (v & kWsErrRange)
+    return fail(Q35_E_RANGE, "decode step: a value for a fixed-point sum was not finite or |v| >= 2^31; it was "
+                             "dropped and the model state is invalid until q35_model_reset");
+  if (v & kWsErrPos) return fail(Q35_E_SHAPE, "decode step: an attention position was outside the cache");
+  return fail(Q35_E_HIP, "decode step: unknown error bits " + std::to_string(v));
 }
 
 int step(q35_model* m, int use_graph, hipStream_t st) {
@@ -689,6 +714,7 @@ int q35_model_reset(q35_model* m, void* stream) {
                        n == "step_attn_partial_o" || n == "step_error";
     if (state) Q35_HIP_TRY(hipMemsetAsync(kv.second.p, 0, kv.second.bytes, st));
   }
+  Q35_HIP_TRY(hipMemsetAsync(ws_counters(m->ws) + kWsErrWord, 0, sizeof(uint32_t), st));
   m->host_pos = 0;
   m->step_failed = false;
   return Q35_OK;
@@ -727,7 +753,9 @@ int q35_model_decode(q35_model* m, int32_t n_steps, int32_t mode, void* stream) 
 
 int q35_model_check(q35_model* m, void* stream) {
   if (!m) return fail(Q35_E_ARG, "model_check: null model");
-  return check_persistent(m, pick(m, stream));
+  hipStream_t st = pick(m, stream);
+  const int rc = check_persistent(m, st);
+  return rc ? rc : check_numeric(m, st);
 }
 
 int q35_model_persistent_info(q35_model* m, int32_t* grid_out) {
@@ -781,7 +809,7 @@ int q35_model_generate(q35_model* m, const int32_t* prompt_host, int32_t n_promp
   }
   Q35_HIP_TRY(hipStreamSynchronize(st));
   const auto t1 = std::chrono::steady_clock::now();
-  if (pers && (rc = check_persistent(m, st))) return rc;
+  if ((rc = pers ? check_persistent(m, st) : check_numeric(m, st))) return rc;
   if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
   Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + p0 + n_prompt - 1, sizeof(int32_t) * (n_new + 1), hipMemcpyDeviceToHost));
   return Q35_OK;
@@ -879,6 +907,7 @@ int decode_until(q35_model* m, int32_t pe, int32_t max_new, const int32_t* stop_
     Q35_HIP_TRY(hipStreamSynchronize(st));
   }
   const auto t1 = std::chrono::steady_clock::now();
+  if (!pers && (rc = check_numeric(m, st))) return rc;
   if (decode_seconds_host) *decode_seconds_host = std::chrono::duration<double>(t1 - t0).count();
   Q35_HIP_TRY(hipMemcpy(out_tokens_host, m->hist + pe - 1, sizeof(int32_t) * (produced + 1), hipMemcpyDeviceToHost));
   *n_out_host = produced;

@@ -48,6 +48,7 @@ struct q35_model {
   q35::StepArgs step_args{};
   bool step_failed = false;  // a check found the sticky error word set (cleared by reset)
   const char* step_fail_msg = "";
+  int step_fail_code = Q35_E_HIP;  // Q35_E_HIP (a wait timed out) or Q35_E_RANGE
   // prompt path (allocated on first use): up to pf_cap tokens per pass
   int pf_cap = 0, pf_ldy = 0, pf_lda = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_y = nullptr, *pf_a = nullptr, *pf_core = nullptr;

@@ -58,6 +58,7 @@ struct MvArgs {
   fx_t* zero_ptr; int64_t zero_n;
   float* cs_state; const fx_t* cs_x; int32_t cs_ch, cs_ldx, cs_B;
   float* y_out; int32_t ldy; uint32_t* tile_ctr;
+  uint32_t* err;
 };
 
 Q35_DEV float in1(const MvArgs& a, int m, int k) {
@@ -229,7 +230,7 @@ __device__ void mv_aux_block(const MvArgs& a, int ab, float* xs, float* red, flo
       if (tid < nout) {
         float s = 0.f;
         for (int g = 0; g < groups; ++g) s += red[g * nout + tid];
-        fx_add(&a.aux_acc[(size_t)m * a.aux_ldo + tid], s);
+        fx_add_chk(&a.aux_acc[(size_t)m * a.aux_ldo + tid], s, a.err);
       }
       __syncthreads();
     }
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void mv_kn_kernel(const MvArgs a) {
     float v = 0.f;
 #pragma unroll
     for (int i = 0; i < kRowsPerStep; ++i) v += red[i * kTile + tid];
-    if (m < a.M && n < seg.N) fx_add(&seg.acc[(size_t)m * seg.ldacc + n], v);
+    if (m < a.M && n < seg.N) fx_add_chk(&seg.acc[(size_t)m * seg.ldacc + n], v, a.err);
     __syncthreads();
   }
   // f32 output: the last block of the tile to finish (its adds and every earlier block's are
@@ -411,6 +412,7 @@ int mv_kn_launch(const MvCall& c, hipStream_t st) {
     if ((reinterpret_cast<uintptr_t>(g.w) & 15) != 0) return fail(Q35_E_ALIGN, "mv_kn: weights not 16-byte aligned");
   }
   if (c.nseg == 0 && c.aux_nh == 0) return fail(Q35_E_ARG, "mv_kn: nothing to compute");
+  if (!c.err) return fail(Q35_E_ARG, "mv_kn: null error word");
   if (c.aux_nh > 0) {
     if (!c.aux_wb || !c.aux_wa || !c.aux_acc) return fail(Q35_E_ARG, "mv_kn: null gate-projection pointer");
     if (2 * c.aux_nh > kThreads || (kThreads % (2 * c.aux_nh)) != 0)
@@ -446,6 +448,7 @@ int mv_kn_launch(const MvCall& c, hipStream_t st) {
   a.zero_ptr = c.zero_ptr; a.zero_n = c.zero_n;
   a.cs_state = c.cs_state; a.cs_x = c.cs_x; a.cs_ch = c.cs_ch; a.cs_ldx = c.cs_ldx; a.cs_B = c.cs_B;
   a.y_out = c.y_out; a.ldy = c.ldy; a.tile_ctr = c.tile_ctr;
+  a.err = c.err;
   if (c.y_out && (c.nseg != 1 || c.aux_nh > 0 || !c.tile_ctr || p.ntiles > kMaxCounters))
     return fail(Q35_E_ARG, "mv_kn: f32 output needs one segment, no gate blocks and a counter per tile");
 

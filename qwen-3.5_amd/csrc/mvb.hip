@@ -73,6 +73,7 @@ struct MbkArgs {
   int64_t xsstride;  // consumer of such partials (XS = 2): the second copy's offset
   const float* aux_wb; const float* aux_wa; int32_t aux_nh; fx_t* aux_acc; int32_t aux_ldo, naux;
   float* part; uint32_t* ctr;
+  uint32_t* err;
 };
 
 Q35_DEV f4 ld4(const float* p) { return *(const Q35_GLOBAL f4*)p; }
@@ -265,7 +266,7 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
       float v = 0.f;
 #pragma unroll
       for (int g = 0; g < 8; ++g) v += red[g * 32 + t];
-      fx_add(&a.aux_acc[(size_t)m * a.aux_ldo + t], v);
+      fx_add_chk(&a.aux_acc[(size_t)m * a.aux_ldo + t], v, a.err);
     }
     __syncthreads();
   }
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   }
   if (a.ss_out) {
     __syncthreads();
-    if (tid < a.M) fx_add(a.ss_out + tid, ((sq[0][tid] + sq[1][tid]) + sq[2][tid]) + sq[3][tid]);
+    if (tid < a.M) fx_add_chk(a.ss_out + tid, ((sq[0][tid] + sq[1][tid]) + sq[2][tid]) + sq[3][tid], a.err);
   }
 }
 
@@ -865,6 +866,8 @@ int mb_launch(const MbCall& c, hipStream_t st) {
   a.ss = c.pro == MB_PRO_RMS ? c.ss : reinterpret_cast<const fx_t*>(c.x);  // rows of x: >= 8 M bytes
   a.z = c.z; a.ldz = c.ldz; a.group = c.group; a.swiglu_off = c.swiglu_off;
   a.add = c.add; a.ss_out = c.ss_out;
+  if (!c.err) return fail(Q35_E_ARG, "mb_launch: null error word");
+  a.err = c.err;
   // two-split launches of up to 16 rows without a residual add may leave their partials to the
   // consumer (for 17..32 rows the consumer's doubled staging costs more than the hand-off saves)
   a.dstride = (c.defer_stride > 0 && a.nsplit == 2 && c.M <= 16 && !c.add && !c.ss_out) ? c.defer_stride : 0;

@@ -6,6 +6,7 @@
 #include <string>
 #include <type_traits>
 #include "../../include/q35.h"
+#include "fx_range.h"
 
 namespace q35 {
 
@@ -95,7 +96,8 @@ Q35_DEV void unpack16(const uint4 w, float* f) {
 // adds its partial sums with a fire-and-forget atomic; integer addition is associative, so the
 // total is identical whatever order the blocks arrive in (bit-reproducible), and the only
 // rounding is one f32 -> 2^-32 grid step per partial (|error| <= 2^-33 each).  The consumer
-// (a later kernel) converts the total back to f32.  Valid for |value| < 2^31.
+// (a later kernel) converts the total back to f32.  Valid for |value| < 2^31: contributions go
+// through fx_add_chk, which drops one that is not (fx_addable) and reports it.
 typedef long long fx_t;
 Q35_DEV fx_t to_fx(float v) { return __float2ll_rn(v * 4294967296.0f); }
 Q35_DEV float from_fx(fx_t a) { return (float)((double)a * (1.0 / 4294967296.0)); }
@@ -166,6 +168,10 @@ Q35_DEV void fx_add(fx_t* p, float v) {
   __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)p, (unsigned long long)to_fx(v), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
 }
+// fx_add of a value that is checked first: a non-finite one, or one whose magnitude would
+// overflow the fixed point, is not added; it ORs kWsErrRange into the error word *err instead
+// (where the reference's f32 sums would carry the NaN / Inf on, text_modules.rs:1080,1084).
+Q35_DEV void fx_add_chk(fx_t* p, float v, uint32_t* err);
 
 // Cross-block partial results are written and read with agent-scope relaxed atomics: on
 // gfx950 these are `global_store ... sc1` / `global_load ... sc1`, i.e. coherent at the device
@@ -318,9 +324,16 @@ constexpr size_t kCounterBytes = 65536;
 constexpr int kWsErrWord = (int)(kCounterBytes / 4) - 1;
 constexpr int kMaxCounters = kWsErrWord;
 inline uint32_t* ws_counters(void* ws) { return static_cast<uint32_t*>(ws); }
-enum : uint32_t { kWsErrPos = 1u };  // an attention position outside [0, tmax)
+enum : uint32_t {
+  kWsErrPos = 1u,    // an attention position outside [0, tmax)
+  kWsErrRange = 2u,  // a value for a fixed-point accumulator was not finite or |v| >= 2^31 (dropped)
+};
 Q35_DEV void ws_raise(uint32_t* counters, uint32_t bit) {
   __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)&counters[kWsErrWord], bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+Q35_DEV void fx_add_chk(fx_t* p, float v, uint32_t* err) {
+  if (fx_addable(v)) fx_add(p, v);
+  else __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)err, kWsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 inline char* ws_scratch(void* ws) { return static_cast<char*>(ws) + kCounterBytes; }
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -408,6 +421,8 @@ struct MvCall {
   float* y_out = nullptr;
   int32_t ldy = 0;
   uint32_t* tile_ctr = nullptr;
+  // the error word that receives kWsErrRange (required): a workspace's counters[kWsErrWord]
+  uint32_t* err = nullptr;
 };
 
 int mv_kn_launch(const MvCall& c, hipStream_t st);
@@ -588,6 +603,8 @@ struct MbCall {
   int64_t defer_stride = 0; int32_t* deferred_out = nullptr;
   // xsum = 2 (SwiGLU prologue, M <= 16): each input value is x[...] + x[... + xsstride], such partials
   int32_t xsum = 1; int64_t xsstride = 0;
+  // the error word that receives kWsErrRange (required)
+  uint32_t* err = nullptr;
 };
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).

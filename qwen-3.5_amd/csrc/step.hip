@@ -174,7 +174,7 @@ Q35_DEV void raise_err(const StepArgs& a, uint32_t bit) {
 // the range bit of the error word, which the host reports after the launch.  `base` (a fixed-point
 // value, exact) is added with it.
 Q35_DEV void fxc_add(const StepArgs& a, fx_t* p, float v, fx_t base = 0) {
-  if (!(fabsf(v) < 4194304.0f)) {
+  if (!fxc_addable(v)) {
     raise_err(a, kStepErrRange);
     v = 0.f;
   }

@@ -73,7 +73,10 @@ class MLP:
         self.t = dict(gate_proj=gate_proj, up_proj=up_proj, down_proj=down_proj)
         self.w = L.MlpWeights(gate_proj.desc(), up_proj.desc(), down_proj.desc())
 
-    def forward(self, x):
+    def forward(self, x, check=False):
+        """check=True synchronises and raises Q35Error (Q35_E_RANGE) if a row held a value that
+        the fixed-point sums cannot take (NaN / Inf, or products of magnitude >= 2^31), as
+        q35_workspace_status documents."""
         d = self.dims
         x2 = x.reshape(-1, d.hidden).contiguous()
         B = x2.shape[0]
@@ -81,6 +84,8 @@ class MLP:
         ws = workspace(L.lib().q35_layer_ws_bytes(ctypes.byref(d), B, 1), x2.device, ("mlp", B))
         L.check(L.lib().q35_mlp_decode(ctypes.byref(d), ctypes.byref(self.w), x2.data_ptr(), B, out.data_ptr(),
                                        ws.data_ptr(), ws.numel(), _stream()))
+        if check:
+            L.check(L.lib().q35_workspace_status(ws.data_ptr(), _stream()))
         return out
 
 

@@ -9,6 +9,7 @@ import oracle as O
 import q35
 from conftest import rel_l2
 from gpu_util import dev, host, normal, q8, q8_dev
+from q35._lib import Q35_E_RANGE
 
 pytestmark = pytest.mark.gpu
 
@@ -169,6 +170,27 @@ def test_mlp_module_tiled_weights(B):
     out = host(gpu.forward(dev(x)))
     exp = O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), x)
     assert rel_l2(out, exp) <= 1e-5
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, 1e12])
+def test_mlp_fixed_point_range_is_reported(bad):
+    """A row holding NaN / Inf, or a value whose products overflow the split-K fixed point
+    (1e12 x |w| ~ 1e10 > 2^31), is caught on the device: its contributions are dropped, every
+    kernel exits normally and the workspace reports Q35_E_RANGE; the word is then clear, so the
+    next good call passes and matches the oracle."""
+    print(f"[mlp range guard] bad={bad}", flush=True)
+    d = q35.dims_2b()
+    cfg = O.cfg_from_dims(d)
+    Wg, Wu, Wd = q8(100, d.hidden, d.ffn), q8(101, d.hidden, d.ffn), q8(102, d.ffn, d.hidden)
+    gpu = q35.MLP(d, q8_dev(Wg, q35.Q35_KN), q8_dev(Wu, q35.Q35_KN), q8_dev(Wd, q35.Q35_KN))
+    x = normal(103, (3, d.hidden))
+    x[1, 7] = bad
+    with pytest.raises(q35.Q35Error) as ei:
+        gpu.forward(dev(x), check=True)
+    assert ei.value.code == Q35_E_RANGE
+    good = normal(104, (2, d.hidden))
+    out = host(gpu.forward(dev(good), check=True))
+    assert rel_l2(out, O.mlp_decode(cfg, O.MlpLayer(Wg, Wu, Wd), good)) <= 1e-5
 
 
 def test_attention_position_outside_cache_is_reported():
