@@ -253,6 +253,28 @@ size_t q35_q8_gemm_ws_bytes(int32_t M, q35_q8f W);
 int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* The batched decode's projection (the kernel behind q35_batch_*) on its own: y[m][n] (+)=
+ * in[m][:] . dequant(W)[:, n] for M <= 32 rows on the f16 matrix cores (x * scale as f16 hi + lo,
+ * about 22 significant bits; f32 accumulation), W in Q35_KN_MB (rows = K, cols = N, both multiples
+ * of 128).  The prologue forms in[m] from the x row (ldx floats apart, 16-byte aligned):
+ *   Q35_MB_PLAIN   in = x;
+ *   Q35_MB_RMS     in = x * rsqrt(mean(x^2) + eps) * (1 + norm_w) (RMSNorm, text_modules.rs:801-809;
+ *                  the row statistic is formed here, the matrix's split factors too);
+ *   Q35_MB_GATED   in = RMSNormGated(x, z) over groups of `group` (a power of two, 16..128):
+ *                  x * rsqrt(mean_group(x^2) + eps) * norm_w * silu(z) (text_modules.rs:91-101),
+ *                  z rows ldz floats apart;
+ *   Q35_MB_SWIGLU  in[k] = x[K + k] * silu(x[k]) (x rows hold gate then up, ldx >= 2 K;
+ *                  text_modules.rs:1005).
+ * accumulate = 1 adds into y (a residual add).  Needs q35_q8_gemv_mb_ws_bytes(M, W) bytes of
+ * workspace; range errors are reported by q35_workspace_status.  No reference counterpart (the
+ * reference decodes one sequence): it is exposed for callers that batch rows themselves and for
+ * per-projection parity tests of the batched path. */
+enum { Q35_MB_PLAIN = 0, Q35_MB_RMS = 1, Q35_MB_GATED = 2, Q35_MB_SWIGLU = 3 };
+size_t q35_q8_gemv_mb_ws_bytes(int32_t M, q35_q8f W);
+int q35_q8_gemv_mb(const float* x, int32_t M, int32_t ldx, int32_t prologue, const float* norm_w, const float* z,
+                   int32_t ldz, int32_t group, float eps, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                   void* ws, size_t ws_bytes, void* stream);
+
 /* out[t] = [beta | g] for T prompt rows, as the prompt branch computes them
  * (text_modules.rs:578-595): beta = sigmoid(x.W_b), g = -exp(A_log) * softplus(x.W_a + dt_bias)
  * with softplus's identity branch taken when its INPUT exceeds 20 (decode, q35_gate_proj,

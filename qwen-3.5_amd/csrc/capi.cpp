@@ -487,6 +487,50 @@ int q35_q8_gemm_ws(const float* x, int32_t M, int32_t ldx, q35_q8f W, float* y, 
   return gemm_launch(c, S(stream));
 }
 
+size_t q35_q8_gemv_mb_ws_bytes(int32_t M, q35_q8f W) {
+  if (W.layout != Q35_KN_MB || M < 1 || M > 32 || W.rows < 128 || W.cols < 128) return 0;
+  const int K = W.rows, N = W.cols;
+  return kCounterBytes + align256(32 * sizeof(fx_t)) + align256((size_t)(N / 64) * sizeof(float)) +
+         align256(mb_part_floats(N / 64, K, M) * sizeof(float));
+}
+
+int q35_q8_gemv_mb(const float* x, int32_t M, int32_t ldx, int32_t prologue, const float* norm_w, const float* z,
+                   int32_t ldz, int32_t group, float eps, q35_q8f W, float* y, int32_t ldy, int32_t accumulate,
+                   void* ws, size_t ws_bytes, void* stream) {
+  if (W.layout != Q35_KN_MB) return fail(Q35_E_ARG, "q8_gemv_mb: W must be Q35_KN_MB");
+  if (!W.q || !W.scale || !x || !y) return fail(Q35_E_ARG, "q8_gemv_mb: null pointer");
+  const int K = W.rows, N = W.cols;
+  if (M < 1 || M > 32) return fail(Q35_E_SHAPE, "q8_gemv_mb: M must be in [1, 32]");
+  if (K < 128 || K % 128 || N < 128 || N % 128) return fail(Q35_E_SHAPE, "q8_gemv_mb: K and N must be multiples of 128");
+  if (prologue < Q35_MB_PLAIN || prologue > Q35_MB_SWIGLU) return fail(Q35_E_ARG, "q8_gemv_mb: bad prologue");
+  if ((prologue == Q35_MB_RMS || prologue == Q35_MB_GATED) && !norm_w) return fail(Q35_E_ARG, "q8_gemv_mb: null norm_w");
+  if (ldx < (prologue == Q35_MB_SWIGLU ? 2 * K : K) || ldy < N) return fail(Q35_E_SHAPE, "q8_gemv_mb: ldx / ldy too small");
+  if (!ws || ws_bytes < q35_q8_gemv_mb_ws_bytes(M, W)) return fail(Q35_E_WS, "q8_gemv_mb: workspace too small");
+  hipStream_t st = S(stream);
+  uint32_t* ctr = ws_counters(ws);
+  const size_t pf = mb_part_floats(N / 64, K, M);
+  Carver cv{ws_scratch(ws), ws_bytes - kCounterBytes};
+  fx_t* ss = cv.take<fx_t>(32);
+  float* f = cv.take<float>((size_t)(N / 64));
+  float* part = cv.take<float>(std::max<size_t>(pf, 1));
+  MbCall c;
+  c.M = M; c.K = K; c.x = x; c.ldx = ldx; c.pro = prologue; c.eps = eps; c.add = accumulate ? 1 : 0;
+  c.nseg = 1;
+  c.seg[0] = MbSeg{W.q, W.scale, y, N, ldy, nullptr};
+  c.part = part; c.part_floats = pf; c.ctr = ctr; c.nctr = kMaxCounters; c.err = ctr + kWsErrWord;
+  int rc;
+  if (prologue == Q35_MB_RMS) {
+    if ((rc = mb_row_ss_launch(x, ldx, K, M, ss, c.err, st)) || (rc = mb_split_factor_launch(W.scale, K, N, norm_w, f, st)))
+      return rc;
+    c.ss = ss; c.pw = norm_w; c.seg[0].f = f;
+  } else if (prologue == Q35_MB_GATED) {
+    c.z = z; c.ldz = ldz; c.group = group; c.pw = norm_w;
+  } else if (prologue == Q35_MB_SWIGLU) {
+    c.swiglu_off = K;
+  }
+  return mb_launch(c, st);
+}
+
 int q35_q8f_pack_mb(q35_q8f W, int8_t* q_mb, float* scale_mb, void* stream) {
   if (!W.q || !W.scale || !q_mb || !scale_mb) return fail(Q35_E_ARG, "q8f_pack_mb: null pointer");
   if (W.layout != Q35_KN && W.layout != Q35_KN_TILED) return fail(Q35_E_ARG, "q8f_pack_mb: W must be Q35_KN or Q35_KN_TILED");

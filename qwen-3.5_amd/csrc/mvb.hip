@@ -790,6 +790,32 @@ __global__ __launch_bounds__(1024) void scale_max_kernel(const float* s, int64_t
 }
 }  // namespace
 
+namespace {
+// ss[m] = fixed-point sum of squares of row m (one block per row), the RMS prologue's statistic
+__global__ __launch_bounds__(kT) void mb_row_ss_kernel(const float* x, int32_t ldx, int32_t K, fx_t* ss, uint32_t* err) {
+  __shared__ float sh[kT / 64];
+  const float* r = x + (size_t)blockIdx.x * ldx;
+  float a = 0.f;
+  for (int k = threadIdx.x; k < K; k += kT) a += r[k] * r[k];
+  a = wave_sum(a);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = a;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kT / 64; ++w) t += sh[w];
+    if (!fx_addable(t)) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)err, kWsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ss[blockIdx.x] = fx_addable(t) ? to_fx(t) : 0;
+  }
+}
+}  // namespace
+
+int mb_row_ss_launch(const float* x, int32_t ldx, int32_t K, int32_t M, fx_t* ss, uint32_t* err, hipStream_t st) {
+  if (!x || !ss || !err || M < 1 || K < 1) return fail(Q35_E_ARG, "mb_row_ss: bad arguments");
+  hipLaunchKernelGGL(mb_row_ss_kernel, dim3((unsigned)M), dim3(kT), 0, st, x, ldx, K, ss, err);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
 int mb_scale_max_launch(const float* s, int64_t n, float* out, hipStream_t st) {
   if (!s || !out || n < 1) return fail(Q35_E_ARG, "mb_scale_max: bad arguments");
   hipLaunchKernelGGL(scale_max_kernel, dim3(1), dim3(1024), 0, st, s, n, out);

@@ -609,6 +609,8 @@ struct MbCall {
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
 size_t mb_part_floats(int ncb, int K, int M);
+// ss[m] = fixed point of sum(x[m][k]^2, k < K) for M rows (the RMS prologue's row statistic)
+int mb_row_ss_launch(const float* x, int32_t ldx, int32_t K, int32_t M, fx_t* ss, uint32_t* err, hipStream_t st);
 // out[0] = max |s[i]| over n floats (one block).
 int mb_scale_max_launch(const float* s, int64_t n, float* out, hipStream_t st);
 // Split factors of an MB weight for RMS launches whose norm weights are norm_w.

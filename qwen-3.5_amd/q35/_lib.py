@@ -14,6 +14,7 @@ Q35_OK, Q35_E_SHAPE, Q35_E_ALIGN, Q35_E_HIP, Q35_E_ARG, Q35_E_WS, Q35_E_NOMEM, Q
 Q35_KN, Q35_NK, Q35_KN_TILED, Q35_KN_PANEL, Q35_KN_MB = 0, 1, 2, 3, 4
 Q35_LAUNCH_STREAM, Q35_LAUNCH_GRAPH, Q35_LAUNCH_PERSISTENT = 0, 1, 2
 Q35_PREFILL_GEMM = 0x100
+Q35_MB_PLAIN, Q35_MB_RMS, Q35_MB_GATED, Q35_MB_SWIGLU = 0, 1, 2, 3
 ERROR_NAMES = {1: "Q35_E_SHAPE", 2: "Q35_E_ALIGN", 3: "Q35_E_HIP", 4: "Q35_E_ARG", 5: "Q35_E_WS", 6: "Q35_E_NOMEM",
                7: "Q35_E_RANGE"}
 
@@ -75,6 +76,9 @@ PROTOTYPES = {
     "q35_rope_tables": (ctypes.c_int, [ctypes.POINTER(Dims), c_i32, c_vp, c_vp]),
     "q35_q8_gemm": (ctypes.c_int, [c_vp, c_i32, c_i32, Q8F, c_vp, c_i32, c_i32, c_vp]),
     "q35_q8_gemm_ws_bytes": (ctypes.c_size_t, [c_i32, Q8F]),
+    "q35_q8_gemv_mb_ws_bytes": (ctypes.c_size_t, [c_i32, Q8F]),
+    "q35_q8_gemv_mb": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, ctypes.c_float, Q8F, c_vp,
+                                      c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
     "q35_q8_gemm_ws": (ctypes.c_int, [c_vp, c_i32, c_i32, Q8F, c_vp, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
     "q35_gate_proj_prompt": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "q35_gated_delta_rule_prefill": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,

@@ -48,8 +48,9 @@ def test_batch_rows_match_independent_oracle_runs(B, mode, prefill):
 
 @pytest.mark.parametrize("B", [5, 20])
 def test_batch_logits_match_oracle(B):
-    """Every row's last-step logits against the oracle's for that sequence alone (rel-L2 <= 1e-4
-    after the prompt and 12 greedy steps), for a 16-row (B = 5) and a 32-row (B = 20) launch."""
+    """Every row's last-step logits against the oracle's for that sequence alone (rel-L2 <= 1e-5
+    after the prompt and 12 greedy steps; measured 5e-7 to 8e-7 with the 22-bit f16 hi + lo
+    operands), for a 16-row (B = 5) and a 32-row (B = 20) launch."""
     print(f"[batch logits] B={B}", flush=True)
     d = hybrid_dims()
     seed, n_new, plen = 4, 12, 9
@@ -68,7 +69,8 @@ def test_batch_logits_match_oracle(B):
             t, _, lg = ref.step(t, want_logits=(i == n_new - 1))
         np.testing.assert_array_equal(toks[r][-1], t, err_msg=f"row {r}")
         err = np.linalg.norm(logits[r] - lg) / np.linalg.norm(lg)
-        assert err <= 1e-4, f"row {r}: logits rel-L2 {err:.2e}"
+        print(f"row {r}: logits rel-L2 {err:.3e}", flush=True)
+        assert err <= 1e-5, f"row {r}: logits rel-L2 {err:.2e}"
     bt.close()
     m.close()
 
