@@ -30,6 +30,10 @@
  *     tap first (text_modules.rs:153).
  *   - f32 transcendentals (exp/log/sqrt/sin/cos) of Rust/ndarray to the last ulp: covered only
  *     by the tolerances of the parity tests.
+ *   - The token after a prompt: the reference picks it with Burn's generic logits.argmax(2)
+ *     (main.rs:92-95), not with kernels::argmax; no fixture pins Burn's tie rule.  orc_argmax
+ *     (the reference kernel's order, kernels.rs:298-371) is used for that token too, and so is
+ *     the product's prompt path; the two can differ only on exact ties of the maximum.
  */
 #ifndef Q35_ORACLE_H
 #define Q35_ORACLE_H

@@ -52,31 +52,45 @@ def word_tokenizer(vocab_size, im_end, im_start):
 class ScriptModel:
     """decode_until replays a scripted greedy sequence; records what the session fed."""
 
-    def __init__(self, script):
+    def __init__(self, script, tmax=1 << 20):
         self.script, self.i = list(script), 0
         self.prefills, self.forwarded, self.resets = [], [], 0
+        self.tmax, self.pos, self.max_asked = tmax, 0, 0
+
+    def position(self):
+        return self.pos
 
     def prefill(self, ids):
+        assert self.pos + len(ids) <= self.tmax, "prefill past tmax"
         self.prefills.append(list(ids))
+        self.pos += len(ids)
 
     def decode_until(self, n, stop_ids=(), mode=None):
+        # as q35_model_decode_until: refused unless position + n fits the cache
+        assert self.pos + n <= self.tmax, "decode_until past tmax"
+        self.max_asked = max(self.max_asked, n)
         out = []
         while len(out) < n:
             t = self.script[self.i]
             if t in stop_ids:
+                self.pos += len(out)
                 return out, t, 0.0
             out.append(t)
             self.i += 1
+        self.pos += len(out)
         return out, self.script[self.i], 0.0
 
     def set_token(self, t):
         self.forwarded.append(t)
 
     def step(self, mode=None):
+        assert self.pos < self.tmax, "step past tmax"
+        self.pos += 1
         self.i += 1 if self.forwarded and self.script[self.i] == self.forwarded[-1] else 0
 
     def reset(self):
         self.resets += 1
+        self.pos = 0
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 4, 32])
@@ -109,3 +123,24 @@ def test_session_max_output_tokens():
     r = s.send("hello")
     assert r.ids == list(range(200, 210)) and not r.stopped
     assert m.forwarded == [7]
+
+
+def test_session_stays_inside_the_cache():
+    """Near tmax the reply is cut so that the <|im_end|> forward still has a row (no call asks
+    for more rows than are left), and a turn that does not fit is reported as a full context
+    without touching the model; /reset makes room again."""
+    tok = word_tokenizer(1024, im_end=7, im_start=9)
+    turn_len = len(tok.encode(chatml_turn("hello world", True), add_special_tokens=False).ids)
+    tmax = turn_len + 10
+    m = ScriptModel(list(range(200, 260)) + [7], tmax=tmax)
+    s = ChatSession(m, tok, chunk=4)
+    r = s.send("hello world")
+    assert r.context_full and not r.stopped
+    assert r.ids == list(range(200, 209))  # 10 free rows: 9 reply ids, 1 row for <|im_end|>
+    assert m.forwarded == [7] and m.position() == tmax
+    r2 = s.send("again")
+    assert r2.context_full and r2.ids == [] and len(m.prefills) == 1
+    s.reset()
+    m.i = 0
+    r3 = s.send("hello world")
+    assert r3.ids == list(range(200, 209)) and len(m.prefills) == 2

@@ -149,18 +149,22 @@ def test_persistent_multi_step_launch_equals_single_steps():
     a.close()
 
 
-@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("mode", ["persistent", "graph", "prompt"])
 def test_fused_argmax_reference_tie_order(mode):
     """The lm_head's fused argmax resolves exact ties as the reference's two-stage argmax
     (kernels.rs:298-371).  The winning row of the tied embedding table is copied into rows that
     the reference's scan visits earlier and later, so those logits are bit-identical to the max;
-    the token picked must be the reference order's pick over the GPU's own logits."""
+    the token picked must be the reference order's pick over the GPU's own logits.  mode
+    "prompt": the token after a prompt through the prompt path, which picks it in the same order
+    (the reference picks that one with Burn's argmax(2), main.rs:92-95, whose tie rule no fixture
+    pins: parity unpinned for exact ties there)."""
     print(f"[model argmax ties] mode={mode}", flush=True)
     d = tiny_dims()
     c = d.vocab // 8
     prompt = (np.arange(12, dtype=np.int32) * 97 + 1000) % d.vocab
     m = q35.TextForCausalLM(d, seed=6, tmax=64)
-    toks, _ = m.generate(prompt, 0, mode=mode)
+    kw = dict(mode="persistent", prefill=True) if mode == "prompt" else dict(mode=mode)
+    toks, _ = m.generate(prompt, 0, **kw)
     m.check()
     w = int(toks[0])
     q = m.tensor("embed_tokens.q", np.int8).reshape(d.vocab, d.hidden).copy()
@@ -173,7 +177,7 @@ def test_fused_argmax_reference_tie_order(mode):
     m.set_tensor("embed_tokens.q", q)
     m.set_tensor("embed_tokens.scale", sc)
     m.reset()
-    toks2, _ = m.generate(prompt, 0, mode=mode)
+    toks2, _ = m.generate(prompt, 0, **kw)
     m.check()
     logits = m.tensor("logits", np.float32)
     tied = np.flatnonzero(logits == logits.max())
