@@ -494,12 +494,17 @@ def trace_summary(d):
     rows.sort()
     starts, i = [], 0
     batch_end = max((k for k in range(len(rows)) if "batch_argmax" in rows[k][1]), default=-1)
+    gemm0 = next((k for k in range(len(rows)) if "gemm_kernel" in rows[k][1] and k > 0 and any(
+        "step_kernel<" in r[1] for r in rows[:k])), len(rows))
+    graph_end = max((k for k in range(gemm0) if "mv_kn_kernel" in rows[k][1]), default=-1)
     for name, marker, runs in TRACE_PHASES:
         if marker is None:
             starts.append((name, 0, runs))
             continue
         if name != "batched decode leg" and starts and starts[-1][0] == "batched decode leg":
             i = batch_end + 1
+        if name.startswith("readback leg"):  # after the graph leg's last kernel
+            i = max(i, graph_end + 1)
         j = next((k for k in range(i, len(rows)) if marker in rows[k][1]), None)
         if j is not None:
             starts.append((name, j, runs))
