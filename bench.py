@@ -187,6 +187,25 @@ def matvec_sweep(torch, q35, st):
                     L.check(lib.q35_q8_gemv(x.data_ptr(), M, W, y.data_ptr(), None, 0, sh))
             row[f"M{M}"] = rate(q8_bytes(N, K, M), graph_per_call_us(torch, st, run, R))
             fits[M].append((q8_bytes(N, K, M), row[f"M{M}"]["us_per_call"]))
+        del copies
+        # the same shapes in the tiled layout (split-K over >= 256 blocks, fixed-point sums, the last
+        # block of each tile converting them; one launch per call with a workspace)
+        nt = (N + 255) // 256
+        copies = []
+        for _ in range(R):
+            q = torch.randint(-127, 128, (nt, K, 256), dtype=torch.int8, device="cuda")
+            s = torch.rand((nt, K, 4), device="cuda") * 1e-3
+            copies.append((q, s, L.Q8F(q.data_ptr(), s.data_ptr(), K, N, L.Q35_KN_TILED)))
+        for M in (1, 8):
+            x = torch.randn(M, K, device="cuda")
+            y = torch.empty(M, N, device="cuda")
+            nb = lib.q35_q8_gemv_ws_bytes(M, copies[0][2])
+            ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
+
+            def run_t():
+                for _, _, W in copies:
+                    L.check(lib.q35_q8_gemv(x.data_ptr(), M, W, y.data_ptr(), ws.data_ptr(), nb, sh))
+            row[f"tiled_M{M}"] = rate(q8_bytes(N, K, M), graph_per_call_us(torch, st, run_t, R))
         out[f"{label} [{N}x{K}]"] = row
         del copies
         torch.cuda.empty_cache()
