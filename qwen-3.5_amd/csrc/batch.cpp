@@ -41,11 +41,12 @@ struct q35_batch {
   float *proj = nullptr;   // q|k|v|z (linear) or q|k|v (full) projection rows [B][proj_n]
   float *gu = nullptr;     // gate | up rows [B][2 ffn], and a second copy for two split partials
   float *o_raw = nullptr, *attn = nullptr, *logits = nullptr, *pv = nullptr, *part = nullptr, *invf = nullptr;
+  float* words = nullptr;  // counted split-K words of the projections (zero between launches)
   _Float16* split16 = nullptr;  // the lm_head's split input rows (hi, lo) of one row group
   q35::fx_t* ss = nullptr;   // RMSNorm statistics [2 layers + 1][B]
   q35::fx_t* gates = nullptr;  // DeltaNet gate sums [layers][B][32] (follows ss)
   int64_t proj_n = 0;
-  size_t part_floats = 0;
+  size_t part_floats = 0, word_floats = 0;
   uint32_t *mb_ctr = nullptr, *gdn_ctr = nullptr;
   int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr, *pi = nullptr;
   int32_t* pinned = nullptr;
@@ -111,6 +112,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
   auto base = [&](MbCall& c, int M) {
     c.M = M; c.eps = d.eps;
     c.part = bt->part; c.part_floats = bt->part_floats; c.ctr = bt->mb_ctr; c.nctr = kMbCounters;
+    c.words = bt->words; c.word_floats = bt->word_floats;
     c.err = ws_counters(bt->ws) + kWsErrWord;
   };
   for (int l = 0; l < NL; ++l) {
@@ -377,7 +379,10 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
   // split-K partials: the largest any projection launch of this batch needs
   const int M0 = std::min(B, kRowGroup);
   const int shapes[6][2] = {{H, conv_dim + vdim}, {vdim, H}, {H, ah * hd * 2 + 2 * kvh * hd}, {ah * hd, H}, {H, 2 * F}, {F, H}};
-  for (const auto& kn : shapes) b->part_floats = std::max(b->part_floats, mb_part_floats(kn[1] / 64, kn[0], M0));
+  for (const auto& kn : shapes) {
+    b->part_floats = std::max(b->part_floats, mb_part_floats(kn[1] / 64, kn[0], M0));
+    b->word_floats = std::max(b->word_floats, mb_word_floats(kn[1] / 64, M0));
+  }
   fx_t* stats = nullptr;
   if ((rc = balloc_t(b, "norm_stats", (size_t)(2 * NL + 1) * B + (size_t)NL * B * kGateLd, &stats))) return bail(rc);
   b->ss = stats;
@@ -386,6 +391,7 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
       (rc = balloc_t(b, "gu", (size_t)2 * B * 2 * F, &b->gu)) || (rc = balloc_t(b, "lm_split16", (size_t)2 * kRowGroup * H, &b->split16)) ||
       (rc = balloc_t(b, "lm_invf", kRowGroup, &b->invf)) ||
       (rc = balloc_t(b, "partials", std::max<size_t>(b->part_floats, 64), &b->part)) ||
+      (rc = balloc_t(b, "split_words", std::max<size_t>(b->word_floats, 64), &b->words)) ||
       (rc = balloc_t(b, "mb_counters", kMbCounters, &b->mb_ctr)) ||
       (rc = balloc_t(b, "gdn_counters", (size_t)B * nh, &b->gdn_ctr)) ||
       (rc = balloc_t(b, "o_raw", (size_t)B * vdim, &b->o_raw)) || (rc = balloc_t(b, "attn", (size_t)B * ah * hd, &b->attn)) ||

@@ -491,7 +491,7 @@ size_t q35_q8_gemv_mb_ws_bytes(int32_t M, q35_q8f W) {
   if (W.layout != Q35_KN_MB || M < 1 || M > 32 || W.rows < 128 || W.cols < 128) return 0;
   const int K = W.rows, N = W.cols;
   return kCounterBytes + align256(32 * sizeof(fx_t)) + align256((size_t)(N / 64) * sizeof(float)) +
-         align256(mb_part_floats(N / 64, K, M) * sizeof(float));
+         align256(mb_part_floats(N / 64, K, M) * sizeof(float)) + align256(mb_word_floats(N / 64, M) * sizeof(float));
 }
 
 int q35_q8_gemv_mb(const float* x, int32_t M, int32_t ldx, int32_t prologue, const float* norm_w, const float* z,
@@ -513,11 +513,14 @@ int q35_q8_gemv_mb(const float* x, int32_t M, int32_t ldx, int32_t prologue, con
   fx_t* ss = cv.take<fx_t>(32);
   float* f = cv.take<float>((size_t)(N / 64));
   float* part = cv.take<float>(std::max<size_t>(pf, 1));
+  const size_t wf = mb_word_floats(N / 64, M);
+  float* words = cv.take<float>(wf);
   MbCall c;
   c.M = M; c.K = K; c.x = x; c.ldx = ldx; c.pro = prologue; c.eps = eps; c.add = accumulate ? 1 : 0;
   c.nseg = 1;
   c.seg[0] = MbSeg{W.q, W.scale, y, N, ldy, nullptr};
   c.part = part; c.part_floats = pf; c.ctr = ctr; c.nctr = kMaxCounters; c.err = ctr + kWsErrWord;
+  c.words = words; c.word_floats = wf;
   int rc;
   if (prologue == Q35_MB_RMS) {
     if ((rc = mb_row_ss_launch(x, ldx, K, M, ss, c.err, st)) || (rc = mb_split_factor_launch(W.scale, K, N, norm_w, f, st)))

@@ -25,9 +25,10 @@
 // weights with no further synchronisation: wave p takes the 32-row step p of every 128-row round,
 // its weights loaded 4 rounds ahead.  The 4 waves' accumulators are summed through LDS in a fixed
 // order.  A block with the whole K writes its outputs directly; with split-K the blocks of a
-// column block publish partials and the last to arrive sums them in split order (deterministic).
-// Residual projections add into the f32 residual rows and accumulate each row's sum of squares
-// for the next RMSNorm (fixed point, so the sum is order-independent).
+// column block add their partials to counted fixed-point words with returning atomics, and the
+// split that completes a word writes that output (exact sums, so deterministic).  Residual
+// projections add into the f32 residual rows and accumulate each row's sum of squares for the
+// next RMSNorm (fixed point, so the sum is order-independent).
 //
 // The lm_head (mbn_kernel) reads the tied [V][D] table directly: lane l = 16 g + c takes 16
 // consecutive bytes of vocab row c of a tile (k = 16 g .. 16 g + 15 of a 64-wide scale block),
@@ -50,6 +51,10 @@ constexpr int kNKmax = 2048;       // lm_head: largest hidden size (the whole x 
 constexpr int kNLd = kNKmax + 8;   // lm_head: padded LDS row of one plane (halves)
 constexpr int kAuxLd = kRound + 4; // f32 staging row of the gate side blocks (one 128-row chunk)
 constexpr int kDirectKR = 1024;    // rows of K per block on the RMS direct path
+// a counted split-K hand-off (mb_launch) costs one atomic per output and split: it is taken up
+// to kCountedMax of them, or up to kCountedMaxSplit with 5 or more splits (whose partials would
+// take longer to read back), measured on the decode projection shapes at 1-32 rows
+constexpr size_t kCountedMax = 150000, kCountedMaxSplit = 300000;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef q35_h2 h2;
@@ -72,7 +77,9 @@ struct MbkArgs {
   int64_t dstride;   // > 0 with nsplit == 2: split s writes its partial to y + s * dstride (no hand-off)
   int64_t xsstride;  // consumer of such partials (XS = 2): the second copy's offset
   const float* aux_wb; const float* aux_wa; int32_t aux_nh; fx_t* aux_acc; int32_t aux_ldo, naux;
-  float* part; uint32_t* ctr;
+  float* part; uint32_t* ctr;  // split-K partials [ncb][nsplit][Mp][64] and arrival counters
+  uint64_t* words;             // or counted fixed-point words [ncb][M][64], zero between launches
+  int32_t counted;
   uint32_t* err;
 };
 
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   __shared__ __align__(16) float pws[DIRECT ? 4 : X::KR];
   __shared__ __align__(16) float aux_red[256];
   __shared__ float invf[Mp];
-  __shared__ float sq[4][Mp];
+  __shared__ fx_t sq[4][Mp];
   __shared__ int last_flag;
 
   const int nmain = a.ncb * a.nsplit;
@@ -459,7 +466,14 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
     }
     return;
   }
-  if (a.nsplit > 1) {
+  // fin: this lane writes element (mt, i) (row < M; with split-K, only the split that completes
+  // the element's sum)
+  bool fin[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fin[mt][i] = 16 * mt + c < a.M;
+  if (a.nsplit > 1 && !a.counted) {
     float* pp = a.part + ((size_t)cb * a.nsplit + split) * Mp * 64;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -489,23 +503,65 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) out[mt] += pv[u][mt];
     }
+  } else if (a.nsplit > 1) {
+    // Split-K hand-off through counted fixed-point words, one per output [cb][m][64]: every
+    // split adds its partial (value * 2^32 plus 2^56, one count) with a returning atomic, and the
+    // split whose add brings the count to nsplit holds the exact total (order-independent, so
+    // deterministic), writes the output and clears the word for the next launch.  One round trip
+    // per block instead of three (partials stored, arrivals counted, partials read back), at
+    // the price of one atomic per output and split: the launcher picks it when those are few.
+    uint64_t* wb = a.words + (size_t)cb * a.M * 64 + 16 * p + 4 * g;
+    uint64_t add[MT][4], old[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = out[mt][i];
+        if (!fxc_addable(v)) {  // (counted anyway, as zero, so the word still completes)
+          if (fin[mt][i]) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)a.err, kWsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          v = 0.f;
+        }
+        add[mt][i] = (uint64_t)to_fx(v) + (1ull << 56);
+        old[mt][i] = fin[mt][i] ? __hip_atomic_fetch_add((Q35_GLOBAL uint64_t*)(wb + (size_t)(16 * mt + c) * 64 + i),
+                                                         add[mt][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : 0;
+      }
+    const uint64_t before = (uint64_t)(a.nsplit - 1) << 56;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // the word held nsplit - 1 contributions (|value| < 2^55 around its count)
+        fin[mt][i] = fin[mt][i] && (old[mt][i] - before + (1ull << 55)) < (1ull << 56);
+        if (fin[mt][i]) {
+          const uint64_t tot = old[mt][i] + add[mt][i] - ((uint64_t)a.nsplit << 56);
+          out[mt][i] = from_fx((fx_t)tot);
+          __hip_atomic_store((Q35_GLOBAL uint64_t*)(wb + (size_t)(16 * mt + c) * 64 + i), 0ull, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
   }
   // write (or add) the outputs of rows m < M; residual adds also sum the new rows' squares
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c;
-    float sqs = 0.f;
-    if (m < a.M) {
-      float* yr = sg.y + (size_t)m * sg.ldy + ncol0;
+    // the squares go to fixed point one by one, so the row's sum is exact whichever block
+    // completes which outputs
+    fx_t sqs = 0;
+    bool bad = false;
+    float* yr = sg.y + (size_t)min(m, a.M - 1) * sg.ldy + ncol0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
+      if (fin[mt][i]) {
         float v = out[mt][i];
         if (a.add) v += yold[mt][i];
         yr[i] = v;
-        sqs += v * v;
+        const float q = v * v;
+        if (fx_addable(q)) sqs += to_fx(q);
+        else bad = true;
       }
-    }
     if (a.ss_out) {
+      if (bad) __hip_atomic_fetch_or((Q35_GLOBAL uint32_t*)a.err, kWsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sqs += __shfl_xor(sqs, 16);
       sqs += __shfl_xor(sqs, 32);
       if (g == 0) sq[p][m] = sqs;
@@ -513,7 +569,13 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   }
   if (a.ss_out) {
     __syncthreads();
-    if (tid < a.M) fx_add_chk(a.ss_out + tid, ((sq[0][tid] + sq[1][tid]) + sq[2][tid]) + sq[3][tid], a.err);
+    // (with split-K, each block that completed some of the row's outputs adds their share)
+    if (tid < a.M) {
+      const fx_t v = ((sq[0][tid] + sq[1][tid]) + sq[2][tid]) + sq[3][tid];
+      if (!a.counted || v != 0)
+        __hip_atomic_fetch_add((Q35_GLOBAL unsigned long long*)(a.ss_out + tid), (unsigned long long)v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -853,6 +915,8 @@ size_t mb_part_floats(int ncb, int K, int M) {
   return n;
 }
 
+size_t mb_word_floats(int ncb, int M) { return (size_t)ncb * 64 * M * 2; }
+
 int mb_launch(const MbCall& c, hipStream_t st) {
   if (c.nseg < 1 || c.nseg > kMbMaxSeg) return fail(Q35_E_ARG, "mb_launch: 1..4 segments");
   if (c.M < 1 || c.M > 32) return fail(Q35_E_SHAPE, "mb_launch: M in [1, 32]");
@@ -911,10 +975,16 @@ int mb_launch(const MbCall& c, hipStream_t st) {
   if (c.aux_acc && (c.aux_nh < 1 || 2 * c.aux_nh > 32 || !c.aux_wb || !c.aux_wa))
     return fail(Q35_E_ARG, "mb_launch: gate side task needs 1..16 heads and both weights");
   if (a.nsplit > 1 && !a.dstride) {
-    const size_t need = (size_t)ncb * a.nsplit * (c.M <= 16 ? 16 : 32) * 64;
-    if (!c.part || c.part_floats < need || !c.ctr || c.nctr < ncb)
-      return fail(Q35_E_WS, "mb_launch: split-K partials / counters too small");
+    // the hand-off: counted words when the atomics they cost (one per output and split) are few
+    // or the splits many, else partials and an arrival counter
+    const size_t np = (size_t)ncb * a.nsplit * (c.M <= 16 ? 16 : 32) * 64, nw = mb_word_floats(ncb, c.M);
+    const size_t atomics = (size_t)ncb * 64 * c.M * a.nsplit;
+    a.counted = (atomics <= kCountedMax || (atomics <= kCountedMaxSplit && a.nsplit >= 5)) ? 1 : 0;
+    if (!c.part || c.part_floats < np || !c.ctr || c.nctr < ncb) return fail(Q35_E_WS, "mb_launch: split-K partials / counters too small");
+    if (!c.words || c.word_floats < nw || (reinterpret_cast<uintptr_t>(c.words) & 7))
+      return fail(Q35_E_WS, "mb_launch: split-K counted words too small");
     a.part = c.part; a.ctr = c.ctr;
+    a.words = reinterpret_cast<uint64_t*>(c.words);
   }
   const dim3 grid((unsigned)(ncb * a.nsplit + a.naux));
   if (xs == 2) {  // (staged SwiGLU prologue, <= 16 rows)

@@ -597,6 +597,7 @@ struct MbCall {
   fx_t* aux_acc = nullptr; int32_t aux_ldo = 0;
   // split-K partials and one counter per 64-column block (zero between launches)
   float* part = nullptr; size_t part_floats = 0; uint32_t* ctr = nullptr; int32_t nctr = 0;
+  float* words = nullptr; size_t word_floats = 0;  // counted split-K words (mb_word_floats), 8-byte aligned
   // defer_stride > 0 (no residual add, M <= 16): when the plan splits K in two, split s writes its
   // partial rows to seg.y + s * defer_stride and the launch ends without a hand-off;
   // *deferred_out tells.
@@ -609,6 +610,9 @@ struct MbCall {
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
 size_t mb_part_floats(int ncb, int K, int M);
+// Counted fixed-point split-K words of a launch of M rows over ncb column blocks (floats; a
+// region of its own, zero before the first launch and left zero by every launch).
+size_t mb_word_floats(int ncb, int M);
 // ss[m] = fixed point of sum(x[m][k]^2, k < K) for M rows (the RMS prologue's row statistic)
 int mb_row_ss_launch(const float* x, int32_t ldx, int32_t K, int32_t M, fx_t* ss, uint32_t* err, hipStream_t st);
 // out[0] = max |s[i]| over n floats (one block).

@@ -25,12 +25,14 @@ def silu(v):
     return (v / (1.0 + np.exp(-v))).astype(np.float32)
 
 
-def run(x, prologue, Wm, N, norm_w=None, z=None, group=0, y0=None):
-    """q35_q8_gemv_mb over the rows of x (device tensors; y0: rows to add into)."""
+def run(x, prologue, Wm, N, norm_w=None, z=None, group=0, y0=None, ws=None):
+    """q35_q8_gemv_mb over the rows of x (device tensors; y0: rows to add into; ws: a workspace
+    to reuse, else a fresh zeroed one)."""
     M = x.shape[0]
     y = y0.clone() if y0 is not None else torch.zeros((M, N), dtype=torch.float32, device="cuda")
     nb = L.lib().q35_q8_gemv_mb_ws_bytes(M, Wm.desc())
-    ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
+    if ws is None:
+        ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     L.check(L.lib().q35_q8_gemv_mb(x.data_ptr(), M, x.shape[1], prologue,
                                    norm_w.data_ptr() if norm_w is not None else None,
@@ -106,3 +108,22 @@ def test_batched_projection_plain(B):
         h0 = normal(s + 2, (B, N))
         out = run(dev(x), L.Q35_MB_PLAIN, Wm, N, y0=dev(h0) if add else None)
         check_rows(out, (h0 if add else 0) + O.gemv_kn(x, W))
+
+
+@pytest.mark.parametrize("K,N,B", [(2048, 2048, 8), (2048, 512, 8), (2048, 6144, 16), (6144, 2048, 32)])
+def test_batched_projection_workspace_reuse(K, N, B):
+    """Three calls in a row on one workspace give the same bits as a call on a fresh one: the
+    split-K hand-off leaves its counters and counted fixed-point words zero (out_proj and k/v at
+    B = 8 hand off through counted words, gate|up at B = 16 and down at B = 32 through partials
+    and an arrival counter)."""
+    print(f"[batched projection reuse] K={K} N={N} B={B}", flush=True)
+    W, Wm = mb_matrix(350 + B, K, N)
+    x = normal(351 + B, (B, K))
+    h0 = normal(352 + B, (B, N))
+    ref = run(dev(x), L.Q35_MB_PLAIN, Wm, N, y0=dev(h0))
+    check_rows(ref, h0 + O.gemv_kn(x, W))
+    nb = L.lib().q35_q8_gemv_mb_ws_bytes(B, Wm.desc())
+    ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
+    for i in range(3):
+        out = run(dev(x), L.Q35_MB_PLAIN, Wm, N, y0=dev(h0), ws=ws)
+        np.testing.assert_array_equal(out, ref, err_msg=f"call {i}")
