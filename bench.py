@@ -159,8 +159,10 @@ def rate(nbytes, us):
 def matvec_sweep(torch, q35, st):
     """Q8F matvec (q8_gemv / q8_gemv_partial_sum, kernels.rs:681-700) at every decode projection
     shape, M = 1 and 8, in the panel layout (one launch, no workspace), cycling through distinct
-    weight copies totalling >= 512 MB so every call streams from HBM; and the lm_head
-    (q8_lm_head, kernels.rs:724-731) over the tied [V][D] table."""
+    weight copies totalling >= 512 MB so every call streams from HBM; the same shapes in the tiled
+    layout (split K over >= 256 blocks) and, at M = 1, 8 and 16, in the f16 matrix-core layout of
+    the batched decode; and the lm_head (q8_lm_head, kernels.rs:724-731) over the tied [V][D]
+    table."""
     L = q35._lib
     lib = q35.lib()
     sh = st.cuda_stream
@@ -206,8 +208,28 @@ def matvec_sweep(torch, q35, st):
                 for _, _, W in copies:
                     L.check(lib.q35_q8_gemv(x.data_ptr(), M, W, y.data_ptr(), ws.data_ptr(), nb, sh))
             row[f"tiled_M{M}"] = rate(q8_bytes(N, K, M), graph_per_call_us(torch, st, run_t, R))
-        out[f"{label} [{N}x{K}]"] = row
         del copies
+        # and in the f16 matrix-core layout of the batched decode (q35_q8_gemv_mb, plain input:
+        # x * scale as f16 hi + lo, split K with the launcher's hand-off; rows padded to 16)
+        if N % 128 == 0:
+            copies = []
+            for _ in range(R):
+                q = torch.randint(-127, 128, (N // 64, K // 32, 2048), dtype=torch.int8, device="cuda")
+                s = torch.rand((N // 64, K), device="cuda") * 1e-3
+                copies.append((q, s, L.Q8F(q.data_ptr(), s.data_ptr(), K, N, L.Q35_KN_MB)))
+            for M in (1, 8, 16):
+                x = torch.randn(M, K, device="cuda")
+                y = torch.empty(M, N, device="cuda")
+                nb = lib.q35_q8_gemv_mb_ws_bytes(M, copies[0][2])
+                ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
+
+                def run_m():
+                    for _, _, W in copies:
+                        L.check(lib.q35_q8_gemv_mb(x.data_ptr(), M, K, L.Q35_MB_PLAIN, None, None, 0, 0, 1e-6, W,
+                                                   y.data_ptr(), N, 0, ws.data_ptr(), nb, sh))
+                row[f"mb_M{M}"] = rate(q8_bytes(N, K, M), graph_per_call_us(torch, st, run_m, R))
+            del copies
+        out[f"{label} [{N}x{K}]"] = row
         torch.cuda.empty_cache()
     V, D = 248320, 2048
     q = torch.randint(-127, 128, (V, D), dtype=torch.int8, device="cuda")
@@ -536,6 +558,8 @@ def trace_summary(d):
             key = (kname[:110], g)
             if runs and key != prev and "q35::" in kname:
                 run, prev = run + 1, key
+            elif runs and "distribution" in kname:
+                prev = None  # (torch's random fill of the next row count's inputs: a new run)
             key = (run if runs and "q35::" in kname else 0,) + key
             if key not in groups:
                 order.append(key)
@@ -548,6 +572,26 @@ def trace_summary(d):
             if runs and key[0] == 0:
                 continue  # library kernels between the runs (weight generation)
             print(f"{len(v):7d} {key[2]:9d} {sum(v) / len(v):10.3f} {v[len(v) // 2]:10.3f} {v[0]:10.3f}  {key[1]}")
+    # the batched decode leg per batch size: its timed steps (the last 64 embedding launches of
+    # each batch size, told apart by their grid), kernels per step
+    emb = [k for k in range(len(rows)) if "batch_embed_f32" in rows[k][1]]
+    for g in sorted({rows[k][2] for k in emb}):
+        idx = [k for k in emb if rows[k][2] == g][-64:]
+        if len(idx) < 64:
+            continue
+        k0 = idx[0]
+        k1 = max(k for k in range(idx[-1], min(len(rows), idx[-1] + 1000)) if "batch_argmax" in rows[k][1])
+        per = collections.defaultdict(list)
+        for _, kname, gg, us in rows[k0:k1 + 1]:
+            per[(kname[:110], gg)].append(us)
+        span = (rows[k1][0] - rows[k0][0]) / 1e3 + per[(rows[k1][1][:110], rows[k1][2])][-1]
+        busy = sum(sum(v) for v in per.values())
+        print(f"\n## batched decode, {g // 256} rows: 64 timed steps, {span / 64:.1f} us per step "
+              f"(kernels busy {busy / 64:.1f}), {sum(len(v) for v in per.values()) / 64:.1f} launches per step")
+        print(f"{'per step':>8} {'grid':>9} {'avg_us':>10} {'us/step':>10}  kernel")
+        for key in sorted(per, key=lambda k: -sum(per[k])):
+            v = per[key]
+            print(f"{len(v) / 64:8.1f} {key[1]:9d} {sum(v) / len(v):10.3f} {sum(v) / 64:10.1f}  {key[0]}")
 
 
 def main():
