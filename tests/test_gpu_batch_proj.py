@@ -3,7 +3,7 @@ as f16 hi + lo), row by row against the oracle's Q8F matvec (orc_q8_gemv_kn) at 
 at B = 8, 16 and 32 rows, for every prologue the batched step uses: RMSNorm (the qkvz / qkv and
 gate|up projections, through the direct path with split factors), the gated RMSNorm (out_proj),
 SwiGLU (down_proj) and the plain input (o_proj after the attention merge), with and without the
-residual add."""
+residual add; both split-K hand-offs on a reused workspace, and the counted one's range guard."""
 import ctypes
 
 import numpy as np
@@ -127,3 +127,28 @@ def test_batched_projection_workspace_reuse(K, N, B):
     for i in range(3):
         out = run(dev(x), L.Q35_MB_PLAIN, Wm, N, y0=dev(h0), ws=ws)
         np.testing.assert_array_equal(out, ref, err_msg=f"call {i}")
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, 1e12])
+def test_batched_projection_counted_range_is_reported(bad):
+    """out_proj at B = 8 (a counted split-K hand-off): a row holding NaN / Inf, or a value whose
+    partial sums leave the counted words' range (|partial| < 2^22, the persistent step kernel's
+    bound), is reported as Q35_E_RANGE through the workspace; the offending contributions count
+    as zero, so every word still completes and is cleared, and the next call on the same
+    workspace gives the same bits as a call on a fresh one."""
+    print(f"[batched projection range] bad={bad}", flush=True)
+    K, N, B = 2048, 2048, 8
+    W, Wm = mb_matrix(360, K, N)
+    x = normal(361, (B, K))
+    x[5, 9] = bad
+    nb = L.lib().q35_q8_gemv_mb_ws_bytes(B, Wm.desc())
+    ws = torch.zeros(nb // 4 + 64, dtype=torch.float32, device="cuda")
+    y = torch.zeros((B, N), dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    L.check(L.lib().q35_q8_gemv_mb(dev(x).data_ptr(), B, K, L.Q35_MB_PLAIN, None, None, 0, 0, ctypes.c_float(EPS),
+                                   Wm.desc(), y.data_ptr(), N, 0, ws.data_ptr(), ws.numel() * 4, st))
+    assert L.lib().q35_workspace_status(ws.data_ptr(), st) == L.Q35_E_RANGE
+    good = normal(362, (B, K))
+    fresh = run(dev(good), L.Q35_MB_PLAIN, Wm, N)
+    check_rows(fresh, O.gemv_kn(good, W))
+    np.testing.assert_array_equal(run(dev(good), L.Q35_MB_PLAIN, Wm, N, ws=ws), fresh)
