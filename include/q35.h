@@ -344,10 +344,12 @@ int q35_model_set_token(q35_model* m, int32_t token, void* stream);
  *   Q35_LAUNCH_STREAM      the step's ~120 fused kernels launched one by one on the stream;
  *   Q35_LAUNCH_GRAPH       the same kernels as a hipGraph captured on first use on this stream;
  *   Q35_LAUNCH_PERSISTENT  one cooperative launch of the persistent step kernel (one block per
- *                          CU, grid barriers between stages) that runs any number of
- *                          consecutive steps; fastest.  Needs hidden <= 4096, DeltaNet heads
- *                          of dk = dv = 128, attention head_dim 256 and the device to
- *                          co-schedule the grid (q35_model_persistent_info). */
+ *                          CU; stages hand data over through counted and tagged words, no grid
+ *                          barrier) that runs any number of consecutive steps; fastest.  Needs
+ *                          hidden <= 4096, DeltaNet heads of dk = dv = 128, attention head_dim
+ *                          256, tmax <= 2048 * min(256, CUs / kv_heads) (262144 for the 2B shape
+ *                          on 256 CUs) and the device to co-schedule the grid
+ *                          (q35_model_persistent_info). */
 enum { Q35_LAUNCH_STREAM = 0, Q35_LAUNCH_GRAPH = 1, Q35_LAUNCH_PERSISTENT = 2 };
 
 /* One decode step: reads the device token slot, runs embedding -> layers -> norm -> lm_head ->

@@ -74,7 +74,8 @@ constexpr int kRmsRegs = 8;       // RMSNorm prologue: K <= 8 * 512
 constexpr uint32_t kSpin = 1u << 21;  // polls before a wait gives up (seconds)
 constexpr int kHd = 256;          // attention head dim
 constexpr int kMaxRep = 4;        // query heads per kv head
-constexpr int kMaxChunk = 256;    // cached tokens per attention item
+constexpr int kMaxChunk = 256;    // cached tokens per attention item (x 128 chunks: 32768 tokens)
+constexpr int kMaxChunkLong = 2048;  // the long-context build of the kernel: 262144 tokens
 constexpr int kMinChunk = 8;
 constexpr int kMaxNmax = 256;     // attention chunks per kv head
 constexpr int kMaxTouch = 8;      // norm groups / heads one matvec item's rows can span
@@ -94,6 +95,11 @@ static_assert(kRed + kRG * kTile <= kSmem, "LDS");
 static_assert(512 + 2 * kT + kDv <= kRG * kTile, "DeltaNet scratch fits in kRed");
 static_assert(kKch <= kT, "one x element per thread in the gated / attention prologues");
 static_assert(kMaxTouch * kMaxNmax + kT + kMaxTouch <= kRG * kTile, "attention merge scratch fits in kRed");
+// LDS of the attention items of a build whose items hold up to mc cached tokens: q, k, v rows,
+// RoPE scratch, scores [kMaxRep][mc], the waves' outputs, m and l; the stage LDS of that build
+constexpr int attn_smem(int mc) { return (2 * kMaxRep + 3) * kHd + kMaxRep * mc + kNW * kMaxRep * kHd + 2 * kMaxRep; }
+constexpr int smem_for(int mc) { return attn_smem(mc) <= kSmem ? kSmem : (attn_smem(mc) + 255) / 256 * 256; }
+static_assert(attn_smem(kMaxChunk) <= kSmem, "attention item scratch fits in the stage LDS");
 
 // threadIdx.x / blockIdx.x read through an empty asm: every use is then loop-variant, so each
 // stage recomputes its per-thread address arithmetic instead of the compiler hoisting it out of
@@ -989,6 +995,7 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
 // loaded before its inputs: the stage then has one memory round trip (its q, k, v inputs)
 // instead of four.  Wave w holds rows t0 + w + 8j, j < kAttnPf; rows beyond are loaded in-stage.
 constexpr int kAttnPf = 2;
+template <int MC>
 Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const Shared& sh) {
   const int tid = tix(), lane = tid & 63, wid = tid >> 6;
   const int T = p + 1, rep = a.ah / a.kvh;
@@ -1020,8 +1027,8 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const
   float* kn = qn + kMaxRep * kHd;    // [kHd]
   float* vn = kn + kHd;              // [kHd]
   float* rtmp = vn + kHd;            // [kMaxRep + 1][kHd]
-  float* sc = rtmp + (kMaxRep + 1) * kHd;  // [kMaxRep][kMaxChunk]
-  float* ored = sc + kMaxRep * kMaxChunk;  // [kNW][kMaxRep][kHd]
+  float* sc = rtmp + (kMaxRep + 1) * kHd;  // [kMaxRep][MC]
+  float* ored = sc + kMaxRep * MC;  // [kNW][kMaxRep][kHd]
   float* hm = ored + kNW * kMaxRep * kHd;  // [kMaxRep]
   float* hl = hm + kMaxRep;                // [kMaxRep]
   const int ldqg = a.ah * kHd * 2;
@@ -1100,7 +1107,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const
         if (h >= rep) break;
         float dd = q4[h][0] * kv.x + q4[h][1] * kv.y + q4[h][2] * kv.z + q4[h][3] * kv.w;
         dd = wave_sum(dd);
-        if (lane == 0) sc[h * kMaxChunk + tt] = dd * a.ascale;
+        if (lane == 0) sc[h * MC + tt] = dd * a.ascale;
       }
     };
     auto ld4 = [&](const float* q) {
@@ -1122,12 +1129,12 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const
     __syncthreads();
     for (int h = wid; h < rep; h += kNW) {
       float mx = -INFINITY;
-      for (int tt = lane; tt < len; tt += 64) mx = fmaxf(mx, sc[h * kMaxChunk + tt]);
+      for (int tt = lane; tt < len; tt += 64) mx = fmaxf(mx, sc[h * MC + tt]);
       mx = wave_max(mx);
       float l = 0.f;
       for (int tt = lane; tt < len; tt += 64) {
-        const float pe = expf(sc[h * kMaxChunk + tt] - mx);
-        sc[h * kMaxChunk + tt] = pe;
+        const float pe = expf(sc[h * MC + tt] - mx);
+        sc[h * MC + tt] = pe;
         l += pe;
       }
       l = wave_sum(l);
@@ -1143,7 +1150,7 @@ Q35_DEV bool attn_stage(const StepArgs& a, CLayer& L, const Tok& t, int p, const
 #pragma unroll
       for (int h = 0; h < kMaxRep; ++h) {
         if (h >= rep) break;
-        const float pe = sc[h * kMaxChunk + tt];
+        const float pe = sc[h * MC + tt];
         acc[h][0] += pe * vv.x; acc[h][1] += pe * vv.y; acc[h][2] += pe * vv.z; acc[h][3] += pe * vv.w;
       }
     };
@@ -1315,10 +1322,10 @@ Q35_DEV void state_copy_back(const StepArgs& a) {
 }
 
 // ------------------------------------------------------------------ the kernel
-template <int CPW>
+template <int CPW, int MC>
 __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   constexpr int KR = 2 * CPW;  // hidden <= 256 CPW = 512 KR
-  __shared__ __align__(16) float smem[kSmem];
+  __shared__ __align__(16) float smem[smem_for(MC)];
   __shared__ __align__(16) float shs[kNW];
   __shared__ float shv[kNW];
   __shared__ int shi[kNW];
@@ -1363,7 +1370,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
         r = mv_stage<kU, KR>(a, L, t, SMV_QKV, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
-        if (!attn_stage(a, L, t, p, sh)) return;
+        if (!attn_stage<MC>(a, L, t, p, sh)) return;
         if (!mv_stage<kU, KR>(a, L, t, SMV_O, PRO_ATTN, i, p, sh)) return;
         advance(SMV_O, true);
       }
@@ -1398,10 +1405,18 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   }
 }
 
-const void* kernel_for(int hidden) {
-  if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1>);
-  if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2>);
-  return reinterpret_cast<const void*>(step_kernel<4>);
+// The build for contexts of up to kMaxChunk tokens per attention item, or the long-context one
+// (more LDS for the items' scores; kept apart because the larger allocation costs the common case
+// ~0.5% in register allocation).
+const void* kernel_for(int hidden, bool long_ctx) {
+  if (long_ctx) {
+    if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunkLong>);
+    if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunkLong>);
+    return reinterpret_cast<const void*>(step_kernel<4, kMaxChunkLong>);
+  }
+  if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunk>);
+  if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunk>);
+  return reinterpret_cast<const void*>(step_kernel<4, kMaxChunk>);
 }
 
 }  // namespace
@@ -1412,7 +1427,8 @@ int step_grid(int hidden) {
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(hidden), kT, 0) != hipSuccess || nb < 1) return 0;
+  for (const bool lc : {false, true})
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(hidden, lc), kT, 0) != hipSuccess || nb < 1) return 0;
   return std::min(ncu, kT);  // one block per CU; the argmax reduction reads one partial per thread
 }
 
@@ -1430,7 +1446,7 @@ int step_validate(const q35_dims& d, int tmax, int grid) {
   if (d.rot_dim < 2 || d.rot_dim > kHd || (d.rot_dim % 2) != 0 || (kT % d.rot_dim) != 0)
     return fail(Q35_E_SHAPE, "persistent step: rotary dims must be even, <= 256 and divide 512");
   if (d.vocab >= (int)kArgNone) return fail(Q35_E_SHAPE, "persistent step: vocabulary must be < 2^18 - 1");
-  if ((long long)tmax > (long long)kMaxChunk * step_att_nmax(grid, d.kv_heads))
+  if ((long long)tmax > (long long)kMaxChunkLong * step_att_nmax(grid, d.kv_heads))
     return fail(Q35_E_SHAPE, "persistent step: tmax too large for the attention split");
   return Q35_OK;
 }
@@ -1472,7 +1488,8 @@ int step_launch(const StepArgs& a, int grid, hipStream_t st) {
   if (!a.err || !a.tokseq || !a.argp) return fail(Q35_E_ARG, "persistent step: null error word or token counter");
   StepArgs args = a;
   void* params[] = {&args};
-  Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H), dim3(grid), dim3(kT), params, 0, st));
+  const bool long_ctx = (long long)a.tmax > (long long)kMaxChunk * a.att_nmax;
+  Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H, long_ctx), dim3(grid), dim3(kT), params, 0, st));
   return Q35_OK;
 }
 

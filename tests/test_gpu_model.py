@@ -267,6 +267,29 @@ def test_2b_persistent_matches_graph_long_context():
     m.close()
 
 
+def test_2b_persistent_matches_graph_beyond_32k():
+    """Full shapes over a 34,000-token context: attention items of 266 cached tokens each (more
+    than 256), the persistent kernel against the per-op graph step (whose attention is the
+    separate attn_chunk / attn_merge kernels): the same greedy ids and near-identical final
+    logits.  The prompt goes through the prompt path."""
+    print("[model 2b persistent vs graph, 34k context]", flush=True)
+    d = q35.dims_2b()
+    n_prompt, n_new = 34000, 6
+    tmax = n_prompt + n_new + 8
+    prompt = np.random.default_rng(7).integers(0, d.vocab, n_prompt).astype(np.int32)
+    m = q35.TextForCausalLM(d, seed=2, tmax=tmax)
+    tp, _ = m.generate(prompt, n_new, mode="persistent", prefill=True)
+    m.check()
+    lp = m.tensor("logits", np.float32).copy()
+    m.reset()
+    tg, _ = m.generate(prompt, n_new, mode="graph", prefill=True)
+    m.check()
+    lg = m.tensor("logits", np.float32)
+    np.testing.assert_array_equal(tp, tg)
+    assert rel_l2(lp, lg) <= 1e-4
+    m.close()
+
+
 def test_2b_persistent_matches_golden_512():
     """The benchmarked workload end to end: the 2B-shaped model (weights seed 0), a 512-token
     prompt and 512 greedy steps through the persistent kernel; all 513 greedy ids equal the
