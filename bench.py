@@ -610,7 +610,8 @@ def main():
     ap.add_argument("--prefill-via-decode", action="store_true",
                     help="also time the prompt fed through the decode step (one token per step)")
     ap.add_argument("--no-readback", action="store_true",
-                    help="skip the leg of one launch per token with a host readback each step (main.rs loop)")
+                    help="skip the legs that hand each token to the host: one launch per token with a readback "
+                         "each step (main.rs loop), and the streamed launch")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph-captured step leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference point for FETCH_SIZE / WRITE_SIZE)")
@@ -639,7 +640,7 @@ def main():
     d = q35.dims_2b()
     chunk = args.chunk
     n_pre, n_warm, n_timed = args.prompt, args.warmup, args.steps
-    tmax = n_pre + n_warm + n_timed + GRAPH_STEPS + READBACK_STEPS + 16
+    tmax = n_pre + n_warm + n_timed + GRAPH_STEPS + 2 * READBACK_STEPS + 16  # (readback and streamed legs)
     log(f"building the 2B-shaped model (tmax {tmax})")
     t0 = time.time()
     m = q35.TextForCausalLM(d, seed=args.seed, tmax=tmax)
@@ -737,6 +738,14 @@ def main():
     if not args.no_readback:
         _, dec_s = m.generate(prompt[:1], READBACK_STEPS, mode="persistent", readback_each=True, stream=sh)
         toks_readback = READBACK_STEPS / dec_s
+    # The same loop with the tokens streamed: one persistent launch for all the steps, the host
+    # reading each token from pinned memory as the kernel stores it (no per-step synchronisation).
+    toks_streamed = None
+    if not args.no_readback:
+        torch.cuda.synchronize()
+        t_s = time.perf_counter()
+        n_got = sum(1 for _ in m.decode_stream(READBACK_STEPS, stream=sh))
+        toks_streamed = n_got / (time.perf_counter() - t_s)
     m.close()
 
     log("prompt GEMM leg")
@@ -792,6 +801,10 @@ def main():
                                             else 1e3 * launch_ms[0], 1)},
         "greedy_ids_checksum": int(np.sum(hist.astype(np.int64) * (np.arange(hist.size) % 9973 + 1)) % 1000000007),
         "tok_s_with_readback": None if toks_readback is None else round(toks_readback, 2),
+        "tok_s_streamed": None if toks_streamed is None else round(toks_streamed, 2),
+        "streamed_note": None if toks_streamed is None else
+            f"{READBACK_STEPS} steps in one persistent launch, each token read by the host from pinned memory as "
+            "the kernel stores it (q35_model_decode_stream), host-timed from the call to the last token and the check",
         "readback_note": None if toks_readback is None else
             f"{READBACK_STEPS} steps, one persistent launch per token plus a 4-byte token readback and a stream "
             "synchronise each step (the reference's loop), host-timed",

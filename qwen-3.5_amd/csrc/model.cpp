@@ -17,6 +17,7 @@
 // captured graph is replayed unchanged for every prompt token and every generated token.
 #include "q35_host.h"
 
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -217,6 +218,7 @@ int setup_persistent(q35_model* m) {
   a.att_ml = att_ml; a.att_o = att_o; a.att_nmax = nmax;
   a.logits = m->logits; a.argp = argp; a.tokseq = tokseq;
   a.token = m->token; a.pos = m->pos; a.prompt = m->prompt; a.plen = m->plen; a.hist = m->hist;
+  a.tok_host = nullptr;
   a.ord = make_arg_order(d.vocab);
   a.err = err;
   a.ntok = 0;
@@ -231,6 +233,7 @@ void destroy(q35_model* m) {
   if (m->graph) (void)hipGraphDestroy(m->graph);
   for (void* p : m->allocs) (void)hipFree(p);
   if (m->pinned) (void)hipHostFree(m->pinned);
+  if (m->tok_stream) (void)hipHostFree(m->tok_stream);
   if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
   delete m;
 }
@@ -257,12 +260,14 @@ const char* kStepRange = "persistent step: a value to be accumulated in fixed po
 // launches as no-ops until a reset, so the base only has to be right while nothing failed.  With
 // stop ids the launch may end early (a stopped launch still settles its barrier counters); the
 // caller then re-reads the device position (sync_pos).
-int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nullptr, int n_stop = 0) {
+int persistent(q35_model* m, int n, hipStream_t st, const int32_t* stop_ids = nullptr, int n_stop = 0,
+               bool stream_tokens = false) {
   if (m->step_rc != Q35_OK) return fail(m->step_rc, m->step_msg);
   if (m->step_failed) return fail(m->step_fail_code, m->step_fail_msg);
   if ((int64_t)m->host_pos + n > m->tmax) return fail(Q35_E_SHAPE, "model_step: cache full (position == tmax)");
   StepArgs a = m->step_args;
   a.ntok = n;
+  a.tok_host = stream_tokens ? m->tok_stream_dev : nullptr;
   a.n_stop = n_stop;
   for (int j = 0; j < n_stop; ++j) a.stop_ids[j] = stop_ids[j];
   int rc = step_launch(a, m->step_grid, st);
@@ -654,6 +659,12 @@ int build_model(const q35_dims* dp, uint64_t seed, int32_t tmax, const ValuesFn&
   if ((rc = dev_alloc(m, "workspace", m->ws_bytes, &m->ws))) return bail(rc);
   if (hipHostMalloc(reinterpret_cast<void**>(&m->pinned), 64 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
     return bail(fail(Q35_E_NOMEM, "hipHostMalloc failed"));
+  if (hipHostMalloc(reinterpret_cast<void**>(&m->tok_stream), (size_t)tmax * sizeof(int32_t),
+                    hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+    return bail(fail(Q35_E_NOMEM, "hipHostMalloc (token stream) failed"));
+  for (int q = 0; q < tmax; ++q) m->tok_stream[q] = -1;
+  if (hipHostGetDevicePointer(reinterpret_cast<void**>(&m->tok_stream_dev), m->tok_stream, 0) != hipSuccess)
+    return bail(fail(Q35_E_HIP, "hipHostGetDevicePointer (token stream) failed"));
   if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(fail(Q35_E_HIP, "workspace clear"));
   if ((rc = setup_persistent(m))) return bail(rc);
   if ((rc = q35_model_reset(m, nullptr))) return bail(rc);
@@ -935,6 +946,21 @@ int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt
   Q35_HIP_TRY(hipStreamSynchronize(st));
   return prefill(m, n_prompt, st);
 }
+
+int q35_model_decode_stream(q35_model* m, int32_t n_steps, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_decode_stream: null model");
+  if (n_steps < 0) return fail(Q35_E_SHAPE, "model_decode_stream: n_steps must be >= 0");
+  if ((int64_t)m->host_pos + n_steps > m->tmax) return fail(Q35_E_SHAPE, "model_decode_stream: tmax too small");
+  if (n_steps == 0) return Q35_OK;
+  // the slots this launch writes start at -1 (host stores, before the launch is enqueued; an
+  // earlier launch still running writes only slots below host_pos)
+  volatile int32_t* slot = m->tok_stream;
+  for (int32_t q = m->host_pos; q < m->host_pos + n_steps; ++q) slot[q] = -1;
+  std::atomic_thread_fence(std::memory_order_seq_cst);
+  return persistent(m, n_steps, pick(m, stream), nullptr, 0, true);
+}
+
+const int32_t* q35_model_token_stream(q35_model* m) { return m ? m->tok_stream : nullptr; }
 
 int q35_model_position(q35_model* m, int32_t* pos_out) {
   if (!m || !pos_out) return fail(Q35_E_ARG, "model_position: null pointer");

@@ -36,6 +36,10 @@ struct q35_model {
   int64_t acc_proj_n = 0;
   int32_t *token = nullptr, *pos = nullptr, *prompt = nullptr, *plen = nullptr, *hist = nullptr;
   int32_t* pinned = nullptr;
+  // host token stream of the persistent decode: pinned, coherent host memory [tmax] and its
+  // device address (q35_model_decode_stream)
+  int32_t* tok_stream = nullptr;
+  int32_t* tok_stream_dev = nullptr;
   void* ws = nullptr;
   size_t ws_bytes = 0;
   hipStream_t own_stream = nullptr;

@@ -726,6 +726,10 @@ struct StepArgs {
   uint64_t* argp;       // per-block argmax partials [2][grid] (token parity): tag (14 bits) | index (18 bits) | f32 value
   uint32_t* tokseq;     // tokens the kernel has run since the last model reset (selects the parity set)
   int32_t *token, *pos, *prompt, *plen, *hist;
+  // Token stream (null: none): device address of pinned, coherent host memory [tmax]; a
+  // non-null pointer selects the streamed build, whose block 0 stores each token there, with one
+  // system-scope store, as it records it in hist
+  int32_t* tok_host;
   ArgOrder ord;         // the reference's argmax order over the vocabulary
   // Stop ids (main.rs:108-110): a generated step (position >= plen) whose input token is one of
   // them is not run; the launch ends there (pos = that position, token = the stop id).

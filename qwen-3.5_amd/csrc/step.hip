@@ -555,16 +555,30 @@ Q35_DEV bool reduce_argmax(const StepArgs& a, uint32_t ti, const Shared& sh, int
   return ok;
 }
 
+// The argmax after position q into hist[q], and in the streamed build (STREAM) into the host
+// token stream tok_host[q] as well: a plain system-scope store; each slot is written once per
+// launch and the host waits for it to leave the -1 it set before the launch.  A build of its own:
+// a runtime branch on the stream pointer cost the plain kernel 0.5% (code layout), and an
+// unconditional store (to hist when not streaming) 1%: stores and loads share the wave's memory
+// counter here, so block 0's next waits sat behind the slow system-scope store.
+template <bool STREAM>
+Q35_DEV void record_token(const StepArgs& a, int q, int tok) {
+  st_agent(&a.hist[q], tok);
+  if constexpr (STREAM)
+    __hip_atomic_store((Q35_GLOBAL int32_t*)(a.tok_host + q), tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Token of step i at position p: the prompt id while p < plen, else the argmax of the previous
 // step, or *token for the launch's first step.  Block 0 records the previous step's argmax in
 // hist.  Returns false when a wait failed.
+template <bool STREAM>
 Q35_DEV bool select_token(const StepArgs& a, const Tok& t, int i, int p, const Shared& sh, int& tok) {
   bool ok = true;
   if (i == 0) {
     tok = ld_agent(a.token);
   } else {
     ok = reduce_argmax(a, t.ti - 1, sh, tok);
-    if (bix() == 0 && tix() == 0) st_agent(&a.hist[p - 1], tok);
+    if (bix() == 0 && tix() == 0) record_token<STREAM>(a, p - 1, tok);
   }
   if (p < ldg(a.plen)) tok = ldg(a.prompt + p);
   return ok;
@@ -851,7 +865,7 @@ Q35_DEV bool pro_attn(const StepArgs& a, const Tok& t, int T, int k0, int klen, 
 // KR: hidden-size elements per thread in the RMSNorm prologue (hidden <= 512 KR).
 // Returns kStageOk, kStageFail (a wait failed) or, for the first stage of a step, kStageStop
 // (the step's input token is a stop id; *stop_tok receives it, nothing of the step has run).
-template <int U, int KR>
+template <int U, int KR, bool STREAM = false>
 Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int pro, int i, int p, const Shared& sh,
                      int* stop_tok = nullptr) {
   const Mv d = make_mv(a, L, t, kind);
@@ -891,7 +905,7 @@ Q35_DEV int mv_stage(const StepArgs& a, CLayer& L, const Tok& t, int kind, int p
   // Blocks with an item need the token for the embedding; with stop ids every block forms it,
   // so that every block sees a stop.
   if (pro == PRO_EMBED_RMS && (item < nitems || a.n_stop > 0)) {
-    if (!select_token(a, t, i, p, sh, tok)) return kStageFail;
+    if (!select_token<STREAM>(a, t, i, p, sh, tok)) return kStageFail;
     if (is_stop(a, p, tok)) {
       if (stop_tok) *stop_tok = tok;
       return kStageStop;
@@ -1322,7 +1336,7 @@ Q35_DEV void state_copy_back(const StepArgs& a) {
 }
 
 // ------------------------------------------------------------------ the kernel
-template <int CPW, int MC>
+template <int CPW, int MC, bool STREAM>
 __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   constexpr int KR = 2 * CPW;  // hidden <= 256 CPW = 512 KR
   __shared__ __align__(16) float smem[smem_for(MC)];
@@ -1361,13 +1375,13 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
       const int pro0 = (l == 0) ? PRO_EMBED_RMS : PRO_RMS;
       int r;
       if (!L.full) {
-        r = mv_stage<kU, KR>(a, L, t, SMV_QKVZ, pro0, i, p, sh, &stop_tok);
+        r = mv_stage<kU, KR, STREAM>(a, L, t, SMV_QKVZ, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
         if (!mv_stage<kUOut, KR>(a, L, t, SMV_OUT, PRO_GDN, i, p, sh)) return;
         advance(SMV_OUT, true);
       } else {
-        r = mv_stage<kU, KR>(a, L, t, SMV_QKV, pro0, i, p, sh, &stop_tok);
+        r = mv_stage<kU, KR, STREAM>(a, L, t, SMV_QKV, pro0, i, p, sh, &stop_tok);
         if (r == kStageStop) { executed = i; break; }
         if (r == kStageFail) return;
         if (!attn_stage<MC>(a, L, t, p, sh)) return;
@@ -1398,7 +1412,7 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
   if (!reduce_argmax(a, ts0 + (uint32_t)a.ntok - 1u, sh, tok)) return;
   if (tix() == 0) {
     const int pl = p0 + a.ntok - 1;
-    stg(a.hist + pl, (int32_t)tok);
+    record_token<STREAM>(a, pl, tok);
     stg(a.token, (int32_t)tok);
     stg(a.pos, (int32_t)(pl + 1));
     st_agent((int32_t*)a.tokseq, (int32_t)(ts0 + (uint32_t)a.ntok));
@@ -1407,16 +1421,20 @@ __global__ __launch_bounds__(kT) void step_kernel(const StepArgs a) {
 
 // The build for contexts of up to kMaxChunk tokens per attention item, or the long-context one
 // (more LDS for the items' scores; kept apart because the larger allocation costs the common case
-// ~0.5% in register allocation).
-const void* kernel_for(int hidden, bool long_ctx) {
+// ~0.5% in register allocation); each with and without the host token stream.
+template <bool STREAM>
+const void* kernel_for_t(int hidden, bool long_ctx) {
   if (long_ctx) {
-    if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunkLong>);
-    if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunkLong>);
-    return reinterpret_cast<const void*>(step_kernel<4, kMaxChunkLong>);
+    if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunkLong, STREAM>);
+    if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunkLong, STREAM>);
+    return reinterpret_cast<const void*>(step_kernel<4, kMaxChunkLong, STREAM>);
   }
-  if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunk>);
-  if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunk>);
-  return reinterpret_cast<const void*>(step_kernel<4, kMaxChunk>);
+  if (hidden <= 1024) return reinterpret_cast<const void*>(step_kernel<1, kMaxChunk, STREAM>);
+  if (hidden <= 2048) return reinterpret_cast<const void*>(step_kernel<2, kMaxChunk, STREAM>);
+  return reinterpret_cast<const void*>(step_kernel<4, kMaxChunk, STREAM>);
+}
+const void* kernel_for(int hidden, bool long_ctx, bool stream) {
+  return stream ? kernel_for_t<true>(hidden, long_ctx) : kernel_for_t<false>(hidden, long_ctx);
 }
 
 }  // namespace
@@ -1428,7 +1446,9 @@ int step_grid(int hidden) {
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return 0;
   for (const bool lc : {false, true})
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(hidden, lc), kT, 0) != hipSuccess || nb < 1) return 0;
+    for (const bool sm : {false, true})
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(hidden, lc, sm), kT, 0) != hipSuccess || nb < 1)
+        return 0;
   return std::min(ncu, kT);  // one block per CU; the argmax reduction reads one partial per thread
 }
 
@@ -1485,11 +1505,11 @@ void step_plan(const q35_dims& d, int grid, StepMv* mv) {
 
 int step_launch(const StepArgs& a, int grid, hipStream_t st) {
   if (a.ntok < 1) return Q35_OK;
-  if (!a.err || !a.tokseq || !a.argp) return fail(Q35_E_ARG, "persistent step: null error word or token counter");
+  if (!a.err || !a.tokseq || !a.argp || !a.hist) return fail(Q35_E_ARG, "persistent step: null error word, token counter or history");
   StepArgs args = a;
   void* params[] = {&args};
   const bool long_ctx = (long long)a.tmax > (long long)kMaxChunk * a.att_nmax;
-  Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H, long_ctx), dim3(grid), dim3(kT), params, 0, st));
+  Q35_HIP_TRY(hipLaunchCooperativeKernel(kernel_for(a.H, long_ctx, a.tok_host != nullptr), dim3(grid), dim3(kT), params, 0, st));
   return Q35_OK;
 }
 

@@ -92,6 +92,26 @@ class TextForCausalLM:
         """Synchronise and raise if a persistent launch failed."""
         L.check(L.lib().q35_model_check(self.h, stream))
 
+    def decode_stream(self, n_steps, stream=None, wait_s=30.0):
+        """n_steps decode steps as one persistent launch, yielding each token (the argmax after
+        each step) as the running kernel stores it into the model's pinned host token stream
+        (q35_model_decode_stream): the host sees every token as it is made, with no per-step
+        synchronisation.  The same tokens as decode() leaves in hist.  Checks the launch at the
+        end; a token that does not arrive within wait_s seconds ends in a check (which raises if
+        the launch failed) or an error."""
+        import time
+        p0 = self.position()
+        L.check(L.lib().q35_model_decode_stream(self.h, int(n_steps), stream))
+        slots = (ctypes.c_int32 * (p0 + int(n_steps))).from_address(L.lib().q35_model_token_stream(self.h))
+        for q in range(p0, p0 + int(n_steps)):
+            t0 = time.monotonic()
+            while slots[q] < 0:
+                if time.monotonic() - t0 > wait_s:
+                    self.check(stream)
+                    raise RuntimeError(f"decode_stream: no token for position {q} after {wait_s} s")
+            yield int(slots[q])
+        self.check(stream)
+
     def generate(self, prompt, n_new, use_graph=None, readback_each=False, mode=None, stream=None, prefill=False):
         """Returns (tokens[n_new+1], decode_seconds): the argmax after the last prompt token,
         then the argmax after each of n_new decode steps.  prefill=True feeds the prompt through

@@ -308,3 +308,22 @@ def test_2b_persistent_matches_golden_512():
         i = int(bad[0])
         pytest.fail(f"{bad.size} ids differ; first at step {i}: got {toks[i]}, oracle {want[i]} "
                     f"(oracle margin there {margins[i]:.3g})")
+
+
+def test_decode_stream_matches_decode():
+    """Streamed persistent decode (q35_model_decode_stream): the tokens the host reads from the
+    pinned token stream while the kernel runs equal the ids the synchronous persistent decode
+    records, over two consecutive streamed calls (positions continue) and after a reset; at the
+    2B shape (one 24-step launch) and the tiny hybrid model."""
+    print("[decode stream]", flush=True)
+    for d, seed, plen in ((q35.dims_2b(), 3, 40), (tiny_dims(), 4, 9)):
+        rng = np.random.default_rng(seed)
+        prompt = rng.integers(0, d.vocab, plen).astype(np.int32)
+        m = q35.TextForCausalLM(d, seed=seed, tmax=plen + 64)
+        want, _ = m.generate(prompt, 24, mode="persistent")
+        m.reset()
+        first, _ = m.generate(prompt, 0, mode="persistent")
+        got = [int(first[0])] + list(m.decode_stream(16)) + list(m.decode_stream(8))
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(m.tensor("hist", np.int32)[plen - 1:plen + 24], want)
+        m.close()
