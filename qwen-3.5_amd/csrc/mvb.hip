@@ -86,20 +86,24 @@ struct MbkArgs {
 Q35_DEV f4 ld4(const float* p) { return *(const Q35_GLOBAL f4*)p; }
 Q35_DEV f4 lds4(const float* p) { return *(const f4*)p; }
 
-// A block's input rows live in LDS for its whole K range: at most 1024 / MT rows of Mp = 16 MT
-// rows, as an f32 staging area (aux blocks) or as the hi / lo f16 planes, each row padded so that
-// the 16 rows a B-operand read touches start in different banks.
-template <int MT>
+// A block's input rows live in LDS for its whole K range: at most 1024 / MT rows of SR staged
+// rows (SR = Mp = 16 MT, or 8 when a launch has at most 8: the matrix cores still take 16 rows, the
+// reads of rows past SR repeat row SR - 1, whose outputs are never stored), as an f32 staging area
+// (aux blocks) or as the hi / lo f16 planes, each row padded so that the 16 rows a B-operand read
+// touches start in different banks.  Staging 8 rows puts 32 threads on each (half the loads and
+// arithmetic per thread) and halves the planes.
+template <int MT, int SR = 16 * MT>
 struct XBuf {
   static constexpr int Mp = 16 * MT;
+  static_assert(SR == Mp || (MT == 1 && SR == 8), "staged rows");
   static constexpr int KR = 1024 / MT;         // rows of K per block
   static constexpr int LDH = KR + 8;           // halves per row of one f16 plane
   static constexpr int NCH = KR / kRound;      // 128-row chunks
-  static constexpr int TPR = kT / Mp;          // staging threads per x row: 16 or 8
-  static constexpr int VPT = kRound / TPR;     // values per thread per chunk: 8 or 16
-  static constexpr int AUX = Mp * kAuxLd * 4;  // f32 staging of one chunk (gate side blocks)
+  static constexpr int TPR = kT / SR;          // staging threads per x row: 32, 16 or 8
+  static constexpr int VPT = kRound / TPR;     // values per thread per chunk: 4, 8 or 16
+  static constexpr int AUX = SR * kAuxLd * 4;  // f32 staging of one chunk (gate side blocks)
   static constexpr int RED = 4 * 16 * MT * 64 * 4;  // the 4 waves' accumulators
-  static constexpr int PLANES = 2 * Mp * LDH * 2;
+  static constexpr int PLANES = 2 * SR * LDH * 2;
   static constexpr int BYTES = PLANES > AUX ? (PLANES > RED ? PLANES : RED) : (AUX > RED ? AUX : RED);
   static constexpr int DBYTES = AUX > RED ? AUX : RED;  // direct path: no planes
 };
@@ -108,17 +112,17 @@ struct XBuf {
 // (x, the second operand, the norm weights, the row statistic) is issued first, so staging costs
 // one round trip.  Thread t covers row t / TPR of every chunk, columns (t % TPR) * VPT .. + VPT;
 // the rows of the chunk past M repeat row M - 1 (their outputs are never stored).
-//   SPLIT = false (klen = 128): x~ is written as f32 rows (xs, [Mp][kAuxLd]).
+//   SPLIT = false (klen = 128): x~ is written as f32 rows (xs, [SR][kAuxLd]).
 //   SPLIT = true: y = x~ * scale of the column block, split into hi / lo planes (xs: hi
-//   [Mp][LDH] then lo), with the row's inverse power of two in invf[row].
+//   [SR][LDH] then lo), with the row's inverse power of two in invf[row].
 // `issue` runs right after the staging loads are issued: the caller's weight prefetch goes
 // behind them, so the staging arithmetic waits only for its own loads (loads return in order).
 // XS = 2: the input rows are two split-K partials of the producer, xsstride floats apart (summed
 // here in split order, as the producer's own hand-off would have).
-template <int MT, bool SPLIT, int XS = 1, typename Issue>
+template <int MT, bool SPLIT, int XS = 1, int SR = 16 * MT, typename Issue>
 Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs, const float* scl, float* pws,
                      float* invf, Issue&& issue) {
-  using X = XBuf<MT>;
+  using X = XBuf<MT, SR>;
   const int t = threadIdx.x, mr = t / X::TPR, m = min(mr, a.M - 1), c0 = (t % X::TPR) * X::VPT;
   const int nch = klen / kRound;
   const bool rms = a.pro == MB_PRO_RMS, gated = a.pro == MB_PRO_GATED, two = gated || a.pro == MB_PRO_SWIGLU;
@@ -220,17 +224,26 @@ Q35_DEV void stage_x(const MbkArgs& a, int k0, int klen, char* xbuf, float* scs,
   split_scale(amax, f, inv);
   if ((t % X::TPR) == 0) invf[mr] = inv;
   _Float16* hp = reinterpret_cast<_Float16*>(xbuf) + mr * X::LDH + c0;
-  _Float16* lp = hp + X::Mp * X::LDH;
+  _Float16* lp = hp + SR * X::LDH;
 #pragma unroll
   for (int ci = 0; ci < X::NCH; ++ci)
     if (ci < nch) {
+      if constexpr (X::VPT % 8 == 0) {
 #pragma unroll
-      for (int i = 0; i < X::VPT; i += 8) {
-        uint32_t hi[4], lo[4];
+        for (int i = 0; i < X::VPT; i += 8) {
+          uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) split2(v[ci][i + 2 * j] * f, v[ci][i + 2 * j + 1] * f, hi[j], lo[j]);
-        *(q35_u32x4*)(hp + ci * kRound + i) = q35_u32x4{hi[0], hi[1], hi[2], hi[3]};
-        *(q35_u32x4*)(lp + ci * kRound + i) = q35_u32x4{lo[0], lo[1], lo[2], lo[3]};
+          for (int j = 0; j < 4; ++j) split2(v[ci][i + 2 * j] * f, v[ci][i + 2 * j + 1] * f, hi[j], lo[j]);
+          *(q35_u32x4*)(hp + ci * kRound + i) = q35_u32x4{hi[0], hi[1], hi[2], hi[3]};
+          *(q35_u32x4*)(lp + ci * kRound + i) = q35_u32x4{lo[0], lo[1], lo[2], lo[3]};
+        }
+      } else {  // 4 values per thread: one 8-byte store per plane
+        uint32_t hi[2], lo[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) split2(v[ci][2 * j] * f, v[ci][2 * j + 1] * f, hi[j], lo[j]);
+        typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+        *(u2*)(hp + ci * kRound) = u2{hi[0], hi[1]};
+        *(u2*)(lp + ci * kRound) = u2{lo[0], lo[1]};
       }
     }
 }
@@ -247,10 +260,10 @@ Q35_DEV MbkSeg seg_of(const MbkArgs& a, int cb) {
 // Gate projection side blocks (in_proj_b | in_proj_a, f32 [K][nh] each, kernels.rs:174-247):
 // block ab sums rows [128 ab, 128 ab + 128) of x~ . W for every row m and adds the raw sums to
 // aux_acc (fixed point); the DeltaNet step applies the gates' activations.
-template <int MT>
+template <int MT, int SR>
 Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
   const int t = threadIdx.x, kc = ab * kRound;
-  stage_x<MT, false>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr, nullptr, [] {});
+  stage_x<MT, false, 1, SR>(a, kc, kRound, xbuf, nullptr, nullptr, nullptr, nullptr, [] {});
   __syncthreads();
   const float* xs = reinterpret_cast<const float*>(xbuf);
   const int nh = a.aux_nh, no = 2 * nh;  // no <= 32
@@ -285,9 +298,9 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
 // |x * r| <= sqrt(K) for an RMS-normalised row, so sqrt(K) * max|1 + w| * max|s| bounds every |y|
 // of the block and f puts that bound in [2^13, 2^14)).  The bound is loose for most rows, which
 // costs nothing: hi / lo keep about 22 bits of each y down to 2^-17 of the bound.
-template <int MT, bool DIRECT, int XS = 1>
+template <int MT, bool DIRECT, int XS = 1, int SR = 16 * MT>
 __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
-  using X = XBuf<MT>;
+  using X = XBuf<MT, SR>;
   constexpr int Mp = X::Mp;
   constexpr int NCH = DIRECT ? kDirectKR / kRound : X::NCH;  // rounds per block at most
   // staged x~ (f32 or hi / lo planes); then the reduction
@@ -301,7 +314,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 
   const int nmain = a.ncb * a.nsplit;
   if ((int)blockIdx.x >= nmain) {
-    mbk_aux<MT>(a, (int)blockIdx.x - nmain, xbuf, aux_red);
+    mbk_aux<MT, SR>(a, (int)blockIdx.x - nmain, xbuf, aux_red);
     return;
   }
   const int tid = threadIdx.x, lane = tid & 63, p = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -358,13 +371,13 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) rrow[mt] = rsqrt_f(from_fx(ssv[mt]) * rcp_f((float)a.K) + a.eps);
   } else {
-    stage_x<MT, true, XS>(a, k0, klen, xbuf, scs, scl, pws, invf,
+    stage_x<MT, true, XS, SR>(a, k0, klen, xbuf, scs, scl, pws, invf,
                           [&] { static_for<kDepth>([&](auto d) { load_round(d, d); }); });
     __syncthreads();
   }
 
   const _Float16* xh = reinterpret_cast<const _Float16*>(xbuf);
-  const _Float16* xl = xh + Mp * X::LDH;
+  const _Float16* xl = xh + SR * X::LDH;
   f4 acc[4][MT];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
@@ -404,8 +417,9 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
       } else {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          bh[mt] = *(const h8*)(xh + (16 * mt + c) * X::LDH + kl);
-          bl[mt] = *(const h8*)(xl + (16 * mt + c) * X::LDH + kl);
+          const int row = min(16 * mt + c, SR - 1);  // (rows past SR: outputs never stored)
+          bh[mt] = *(const h8*)(xh + row * X::LDH + kl);
+          bl[mt] = *(const h8*)(xl + row * X::LDH + kl);
         }
       }
       const q35_u32x4 w0 = wr[d][0], w1 = wr[d][1];
@@ -925,7 +939,7 @@ int mb_launch(const MbCall& c, hipStream_t st) {
   if ((reinterpret_cast<uintptr_t>(c.x) & 15) || (c.ldx & 3)) return fail(Q35_E_ALIGN, "mb_launch: x rows 16-byte aligned");
   if (c.pro == MB_PRO_RMS && (!c.ss || !c.pw)) return fail(Q35_E_ARG, "mb_launch: RMS needs ss and w");
   if (c.pro == MB_PRO_GATED) {
-    const int vpt = c.M <= 16 ? 8 : 16;
+    const int vpt = c.M <= 8 ? 4 : c.M <= 16 ? 8 : 16;  // values per staging thread (XBuf)
     if (!c.z || !c.pw || c.group < vpt || c.group > kRound || (c.group & (c.group - 1)) || (c.ldz & 3) ||
         (reinterpret_cast<uintptr_t>(c.z) & 15))
       return fail(Q35_E_ARG, "mb_launch: gated prologue needs z (16-byte rows) and a power-of-two group in [vpt, 128]");
@@ -987,10 +1001,13 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     a.words = reinterpret_cast<uint64_t*>(c.words);
   }
   const dim3 grid((unsigned)(ncb * a.nsplit + a.naux));
+  // staged prologues of up to 8 rows stage 8 (XBuf)
   if (xs == 2) {  // (staged SwiGLU prologue, <= 16 rows)
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2>), grid, dim3(kT), 0, st, a);
+    if (c.M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2, 8>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2>), grid, dim3(kT), 0, st, a);
   } else if (c.M <= 16) {
     if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, true>), grid, dim3(kT), 0, st, a);
+    else if (c.M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 1, 8>), grid, dim3(kT), 0, st, a);
     else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false>), grid, dim3(kT), 0, st, a);
   } else {
     if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, true>), grid, dim3(kT), 0, st, a);
