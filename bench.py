@@ -490,7 +490,7 @@ def copy_calibration():
     print("copied 3 x 1 GiB", flush=True)
 
 
-# HBM traffic of one decode step of step_kernel<2> on this workload: FETCH_SIZE + WRITE_SIZE per
+# HBM traffic of one decode step of step_kernel<2, ...> on this workload: FETCH_SIZE + WRITE_SIZE per
 # dispatch from two rocprofv3 --pmc passes over `bench.py --no-cpu --no-sweep --no-layers
 # --no-batch --no-readback --no-graph` (64-step launches at context 512-1040), each scaled by what
 # the counter reads for a 1 GiB copy (`bench.py --copy-calibration`), divided by the launch's
@@ -498,7 +498,7 @@ def copy_calibration():
 # profiles/step_kernel_decode_2b_traffic.md), not in this run; a launch's traffic is this times its
 # steps (the weights, read once per step, are 95% of it).
 STEP_TRAFFIC_PER_STEP = 2.208e9
-STEP_TRAFFIC_COMMIT = "97823ca"
+STEP_TRAFFIC_COMMIT = "6de3763"
 GRAPH_STEPS = 64      # steps of the hipGraph-mode leg
 READBACK_STEPS = 64   # steps of the per-token readback leg
 
@@ -789,7 +789,7 @@ def main():
                    "batch": 1, "prompt_len": n_pre, "ctx_range": [ctx0, ctx0 + n_timed],
                    "weights": "int8 Q8F per-64 f32 scales",
                    "launch": f"persistent step kernel, steps per launch {plan}, grid {grid}x512"},
-        "roofline": {"kernel": "step_kernel<2>: persistent decode step",
+        "roofline": {"kernel": "step_kernel<2, 256, false>: persistent decode step",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": round(traffic),
                      "traffic_note": f"HBM bytes per launch of {plan[0]} steps: calibrated FETCH_SIZE+WRITE_SIZE "
