@@ -426,15 +426,24 @@ int q35_model_decode_until(q35_model* m, int32_t max_new, const int32_t* stop_id
                            int32_t* out_tokens_host, int32_t* n_out_host, int32_t use_graph,
                            double* decode_seconds_host, void* stream);
 
-/* Streamed decode: n_steps steps as one persistent launch (Q35_LAUNCH_PERSISTENT only), returning
- * once the launch is enqueued.  The token each step produces — the argmax after position q,
- * q = position before the call .. + n_steps - 1, the same values as hist[q] — is stored by the
- * running kernel into slot q of q35_model_token_stream() as soon as the device knows it; the
- * call first sets those slots to -1, so a host thread reads each token by waiting for its slot
- * to become >= 0, while the device runs on (main.rs:100-107 prints each token as it is made; here
- * without a per-step synchronisation).  Call q35_model_check after the last token.  The tokens
- * are identical to q35_model_decode's. */
-int q35_model_decode_stream(q35_model* m, int32_t n_steps, void* stream);
+/* Streamed decode: up to max_steps steps as one persistent launch (Q35_LAUNCH_PERSISTENT only),
+ * returning once the launch is enqueued.  The token each step produces — the argmax after
+ * position q, q = position before the call .. + max_steps - 1, the same values as hist[q] — is
+ * stored by the running kernel into slot q of q35_model_token_stream() as soon as the device
+ * knows it; the call first sets those slots to -1, so a host thread reads each token by waiting
+ * for its slot to become >= 0, while the device runs on (main.rs:100-107 prints each token as it
+ * is made; here without a per-step synchronisation).  With stop ids (0..4, main.rs:105-110) the
+ * launch ends before a step whose input token is one of them, so the last slot written holds that
+ * stop id and the later ones stay -1: stop reading there.  Then call q35_model_stream_end before
+ * any other call on the model.  The tokens are identical to q35_model_decode's (_decode_until's
+ * with stop ids). */
+int q35_model_decode_stream(q35_model* m, int32_t max_steps, const int32_t* stop_ids_host, int32_t n_stop,
+                            void* stream);
+
+/* Ends a streamed decode: synchronises, reports a failed launch as q35_model_check does, sets the
+ * model's position to where the launch ended and writes the steps it ran to *n_steps_out
+ * (optional). */
+int q35_model_stream_end(q35_model* m, int32_t* n_steps_out, void* stream);
 
 /* The model's host token stream: pinned, coherent host memory of tmax slots written by
  * q35_model_decode_stream launches (read them as volatile); valid until q35_model_destroy. */

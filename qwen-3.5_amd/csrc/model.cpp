@@ -947,17 +947,49 @@ int q35_model_prefill(q35_model* m, const int32_t* prompt_host, int32_t n_prompt
   return prefill(m, n_prompt, st);
 }
 
-int q35_model_decode_stream(q35_model* m, int32_t n_steps, void* stream) {
+int q35_model_decode_stream(q35_model* m, int32_t max_steps, const int32_t* stop_ids_host, int32_t n_stop, void* stream) {
   if (!m) return fail(Q35_E_ARG, "model_decode_stream: null model");
-  if (n_steps < 0) return fail(Q35_E_SHAPE, "model_decode_stream: n_steps must be >= 0");
-  if ((int64_t)m->host_pos + n_steps > m->tmax) return fail(Q35_E_SHAPE, "model_decode_stream: tmax too small");
-  if (n_steps == 0) return Q35_OK;
+  if (n_stop < 0 || n_stop > Q35_MAX_STOP_IDS || (n_stop > 0 && !stop_ids_host))
+    return fail(Q35_E_ARG, "model_decode_stream: between 0 and 4 stop ids");
+  if (max_steps < 0) return fail(Q35_E_SHAPE, "model_decode_stream: max_steps must be >= 0");
+  if ((int64_t)m->host_pos + max_steps > m->tmax) return fail(Q35_E_SHAPE, "model_decode_stream: tmax too small");
+  if (n_stop > 0 && m->host_pos < 1) return fail(Q35_E_SHAPE, "model_decode_stream: nothing decoded yet (feed a prompt first)");
+  hipStream_t st = pick(m, stream);
+  m->stream_p0 = m->host_pos;
+  m->stream_max = max_steps;
+  if (max_steps == 0) return Q35_OK;
+  if (n_stop > 0) {  // generated steps from here on: a stop id among their input tokens ends the launch
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+    m->pinned[0] = m->host_pos;
+    Q35_HIP_TRY(hipMemcpyAsync(m->plen, m->pinned, sizeof(int32_t), hipMemcpyHostToDevice, st));
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+  }
   // the slots this launch writes start at -1 (host stores, before the launch is enqueued; an
   // earlier launch still running writes only slots below host_pos)
   volatile int32_t* slot = m->tok_stream;
-  for (int32_t q = m->host_pos; q < m->host_pos + n_steps; ++q) slot[q] = -1;
+  for (int32_t q = m->host_pos; q < m->host_pos + max_steps; ++q) slot[q] = -1;
   std::atomic_thread_fence(std::memory_order_seq_cst);
-  return persistent(m, n_steps, pick(m, stream), nullptr, 0, true);
+  return persistent(m, max_steps, st, stop_ids_host, n_stop, true);
+}
+
+int q35_model_stream_end(q35_model* m, int32_t* n_steps_out, void* stream) {
+  if (!m) return fail(Q35_E_ARG, "model_stream_end: null model");
+  hipStream_t st = pick(m, stream);
+  int rc;
+  if (m->stream_max > 0) {
+    Q35_HIP_TRY(hipMemcpyAsync(m->pinned, m->pos, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+    if ((rc = check_persistent(m, st))) return rc;
+    const int32_t dpos = m->pinned[0];
+    if (dpos < m->stream_p0 || dpos > m->stream_p0 + m->stream_max)
+      return fail(Q35_E_HIP, "model_stream_end: device position out of range");
+    m->host_pos = dpos;  // (a launch that met a stop id ran fewer steps than it was given)
+  } else {
+    Q35_HIP_TRY(hipStreamSynchronize(st));
+  }
+  if (n_steps_out) *n_steps_out = m->host_pos - m->stream_p0;
+  m->stream_max = 0;
+  return Q35_OK;
 }
 
 const int32_t* q35_model_token_stream(q35_model* m) { return m ? m->tok_stream : nullptr; }

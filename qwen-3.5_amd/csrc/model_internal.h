@@ -40,6 +40,7 @@ struct q35_model {
   // device address (q35_model_decode_stream)
   int32_t* tok_stream = nullptr;
   int32_t* tok_stream_dev = nullptr;
+  int32_t stream_p0 = 0, stream_max = 0;  // the last streamed launch: start position, steps given
   void* ws = nullptr;
   size_t ws_bytes = 0;
   hipStream_t own_stream = nullptr;

@@ -105,7 +105,8 @@ PROTOTYPES = {
     "q35_model_decode_until": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_vp, ctypes.POINTER(c_i32), c_i32,
                                               ctypes.POINTER(ctypes.c_double), c_vp]),
     "q35_model_position": (ctypes.c_int, [c_vp, ctypes.POINTER(c_i32)]),
-    "q35_model_decode_stream": (ctypes.c_int, [c_vp, c_i32, c_vp]),
+    "q35_model_decode_stream": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "q35_model_stream_end": (ctypes.c_int, [c_vp, ctypes.POINTER(c_i32), c_vp]),
     "q35_model_token_stream": (c_vp, [c_vp]),
     "q35_model_tensor": (ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_vp), ctypes.POINTER(c_sz)]),
     "q35_batch_create": (ctypes.c_int, [c_vp, c_i32, c_i32, ctypes.POINTER(c_vp)]),

@@ -92,25 +92,40 @@ class TextForCausalLM:
         """Synchronise and raise if a persistent launch failed."""
         L.check(L.lib().q35_model_check(self.h, stream))
 
-    def decode_stream(self, n_steps, stream=None, wait_s=30.0):
-        """n_steps decode steps as one persistent launch, yielding each token (the argmax after
-        each step) as the running kernel stores it into the model's pinned host token stream
+    def decode_stream(self, max_steps, stop_ids=(), stream=None, wait_s=30.0):
+        """Up to max_steps decode steps as one persistent launch, yielding each token (the argmax
+        after each step) as the running kernel stores it into the model's pinned host token stream
         (q35_model_decode_stream): the host sees every token as it is made, with no per-step
-        synchronisation.  The same tokens as decode() leaves in hist.  Checks the launch at the
-        end; a token that does not arrive within wait_s seconds ends in a check (which raises if
-        the launch failed) or an error."""
+        synchronisation.  The same tokens as decode() leaves in hist.  With stop ids the launch
+        ends before a step whose input token is one of them: the stop id is the last token
+        yielded (none, if the current token already is one).  The launch is checked and the
+        position updated (q35_model_stream_end) when the generator finishes or is closed; a token
+        that does not arrive within wait_s seconds raises."""
         import time
+        stops = [int(v) for v in stop_ids]
+        s = np.ascontiguousarray(np.asarray(stops, dtype=np.int32))
+        if stops:
+            self.check(stream)
+            if int(self.tensor("token", np.int32)[0]) in stops:
+                return
         p0 = self.position()
-        L.check(L.lib().q35_model_decode_stream(self.h, int(n_steps), stream))
-        slots = (ctypes.c_int32 * (p0 + int(n_steps))).from_address(L.lib().q35_model_token_stream(self.h))
-        for q in range(p0, p0 + int(n_steps)):
-            t0 = time.monotonic()
-            while slots[q] < 0:
-                if time.monotonic() - t0 > wait_s:
-                    self.check(stream)
-                    raise RuntimeError(f"decode_stream: no token for position {q} after {wait_s} s")
-            yield int(slots[q])
-        self.check(stream)
+        L.check(L.lib().q35_model_decode_stream(self.h, int(max_steps), s.ctypes.data if s.size else None, s.size,
+                                                stream))
+        try:
+            if max_steps > 0:
+                slots = (ctypes.c_int32 * (p0 + int(max_steps))).from_address(L.lib().q35_model_token_stream(self.h))
+            for q in range(p0, p0 + int(max_steps)):
+                t0 = time.monotonic()
+                while slots[q] < 0:
+                    if time.monotonic() - t0 > wait_s:
+                        raise RuntimeError(f"decode_stream: no token for position {q} after {wait_s} s")
+                tok = int(slots[q])
+                yield tok
+                if tok in stops:
+                    break
+        finally:
+            n = ctypes.c_int32(0)
+            L.check(L.lib().q35_model_stream_end(self.h, ctypes.byref(n), stream))
 
     def generate(self, prompt, n_new, use_graph=None, readback_each=False, mode=None, stream=None, prefill=False):
         """Returns (tokens[n_new+1], decode_seconds): the argmax after the last prompt token,
@@ -156,6 +171,12 @@ class TextForCausalLM:
         after its last token is left in the token slot.  Asynchronous after the upload."""
         p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
         L.check(L.lib().q35_model_prefill(self.h, p.ctypes.data, p.size, stream))
+
+    def current_token(self, stream=None):
+        """The token slot: the input of the next decode step (the argmax after the last one, or
+        after the prompt).  Synchronises."""
+        self.check(stream)
+        return int(self.tensor("token", np.int32)[0])
 
     def position(self):
         v = ctypes.c_int32(0)

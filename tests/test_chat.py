@@ -93,11 +93,34 @@ class ScriptModel:
         self.pos = 0
 
 
+class StreamScriptModel(ScriptModel):
+    """The same script through current_token / decode_stream (the streamed reply path)."""
+
+    def current_token(self):
+        return self.script[self.i]
+
+    def decode_stream(self, n, stop_ids=()):
+        # as q35_model_decode_stream: refused unless position + n fits the cache; the launch
+        # ends before a step whose input token is a stop id; each step yields its argmax
+        assert self.pos + n <= self.tmax, "decode_stream past tmax"
+        self.max_asked = max(self.max_asked, n)
+        for _ in range(n):
+            if self.script[self.i] in stop_ids:
+                return
+            self.i += 1
+            self.pos += 1
+            yield self.script[self.i]
+
+
+FAKES = {"chunked": ScriptModel, "streamed": StreamScriptModel}
+
+
+@pytest.mark.parametrize("fake", ["chunked", "streamed"])
 @pytest.mark.parametrize("chunk", [1, 3, 4, 32])
-def test_session_stops_and_forwards_im_end(chunk):
+def test_session_stops_and_forwards_im_end(chunk, fake):
     tok = word_tokenizer(1024, im_end=7, im_start=9)
     reply1 = [500, 501, 502, 503]  # 4 ids, then <|im_end|> (a chunk boundary when chunk is 4)
-    m = ScriptModel(reply1 + [7] + [600, 601, EOS_ID])
+    m = FAKES[fake](reply1 + [7] + [600, 601, EOS_ID])
     s = ChatSession(m, tok, chunk=chunk)
     r = s.send("hello world")
     assert r.ids == reply1 and r.stopped
@@ -116,23 +139,25 @@ def test_session_stops_and_forwards_im_end(chunk):
     assert m.prefills[2][:3] == m.prefills[0][:3]  # the system prompt again
 
 
-def test_session_max_output_tokens():
+@pytest.mark.parametrize("fake", ["chunked", "streamed"])
+def test_session_max_output_tokens(fake):
     tok = word_tokenizer(1024, im_end=7, im_start=9)
-    m = ScriptModel(list(range(200, 260)) + [7])
+    m = FAKES[fake](list(range(200, 260)) + [7])
     s = ChatSession(m, tok, max_output_tokens=10, chunk=4)
     r = s.send("hello")
     assert r.ids == list(range(200, 210)) and not r.stopped
     assert m.forwarded == [7]
 
 
-def test_session_stays_inside_the_cache():
+@pytest.mark.parametrize("fake", ["chunked", "streamed"])
+def test_session_stays_inside_the_cache(fake):
     """Near tmax the reply is cut so that the <|im_end|> forward still has a row (no call asks
     for more rows than are left), and a turn that does not fit is reported as a full context
     without touching the model; /reset makes room again."""
     tok = word_tokenizer(1024, im_end=7, im_start=9)
     turn_len = len(tok.encode(chatml_turn("hello world", True), add_special_tokens=False).ids)
     tmax = turn_len + 10
-    m = ScriptModel(list(range(200, 260)) + [7], tmax=tmax)
+    m = FAKES[fake](list(range(200, 260)) + [7], tmax=tmax)
     s = ChatSession(m, tok, chunk=4)
     r = s.send("hello world")
     assert r.context_full and not r.stopped

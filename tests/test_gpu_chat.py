@@ -21,9 +21,10 @@ def oracle(d, seed, tmax):
     return O.Model(O.cfg_from_dims(d), lambda name, n: q35.synth_model_tensor(d, seed, name, n), tmax)
 
 
-@pytest.mark.parametrize("chunk", [4, 32])
-def test_chat_session_matches_oracle_conversation(chunk):
-    print(f"[chat] chunk={chunk}", flush=True)
+@pytest.mark.parametrize("chunk,stream", [(4, False), (32, False), (32, True)])
+def test_chat_session_matches_oracle_conversation(chunk, stream):
+    """Two turns against the oracle, the reply in launches of `chunk` steps or streamed."""
+    print(f"[chat] chunk={chunk} stream={stream}", flush=True)
     d, seed, tmax = hybrid_dims(), 3, 256
     im_end = 7
     tok = word_tokenizer(d.vocab, im_end=im_end, im_start=9)
@@ -32,7 +33,7 @@ def test_chat_session_matches_oracle_conversation(chunk):
     k = next(j for j in range(3, 40) if rt[j] not in set(rt[:j].tolist()) and rt[j] != im_end)
     eos = int(rt[k])
     m = q35.TextForCausalLM(d, seed=seed, tmax=tmax)
-    chat = ChatSession(m, tok, max_output_tokens=30, eos_id=eos, chunk=chunk)
+    chat = ChatSession(m, tok, max_output_tokens=30, eos_id=eos, chunk=chunk, stream=stream)
     r1 = chat.send("hello world")
     assert r1.stopped and r1.ids == [int(t) for t in rt[:k]]
     assert r1.text == tok.decode(r1.ids, skip_special_tokens=True)

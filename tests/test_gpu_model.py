@@ -327,3 +327,30 @@ def test_decode_stream_matches_decode():
         np.testing.assert_array_equal(got, want)
         np.testing.assert_array_equal(m.tensor("hist", np.int32)[plen - 1:plen + 24], want)
         m.close()
+
+
+def test_decode_stream_with_stop_ids_matches_decode_until():
+    """Streamed decode with stop ids ends where decode_until does: the tokens it yields are
+    decode_until's produced ids (its step inputs) shifted by one plus the stop id, and the model
+    is left at the same position with the same token slot (tiny hybrid model; the stop id is the
+    10th generated token, then one that never comes)."""
+    print("[decode stream stop ids]", flush=True)
+    d = tiny_dims()
+    prompt = np.random.default_rng(11).integers(0, d.vocab, 9).astype(np.int32)
+    m = q35.TextForCausalLM(d, seed=5, tmax=96)
+    ref, _ = m.generate(prompt, 40, mode="persistent")
+    for stop, expect_stop in ((int(ref[10]), True), (d.vocab - 1 if d.vocab - 1 not in ref else 0, False)):
+        m.reset()
+        m.generate(prompt, 0, mode="persistent")
+        got, last, _ = m.decode_until(30, stop_ids=[stop], mode="persistent")
+        pos_u, tok_u = m.position(), m.current_token()
+        m.reset()
+        m.generate(prompt, 0, mode="persistent")
+        cur = m.current_token()
+        streamed = list(m.decode_stream(30, stop_ids=[stop]))
+        assert cur == got[0]
+        np.testing.assert_array_equal(streamed[:-1], got[1:])
+        assert streamed[-1] == last
+        assert (last == stop) == expect_stop
+        assert m.position() == pos_u and m.current_token() == tok_u
+    m.close()
