@@ -31,9 +31,13 @@ struct GdnArgs {
   float qscale;
 };
 
+// QF: the mixed qkv rows are fixed-point accumulator words (else f32).  A compile-time choice:
+// a load inside a runtime branch is joined by a wait for every load in flight (the state slice).
+template <bool QF>
 Q35_DEV float qkv_at(const GdnCall& c, int b, int ch) {
   const size_t i = (size_t)b * c.ld_qkv + ch;
-  return c.qkv_f ? from_fx(c.qkv_f[i]) : c.qkv[i];
+  if constexpr (QF) return from_fx(c.qkv_f[i]);
+  else return c.qkv[i];
 }
 
 Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
@@ -41,7 +45,24 @@ Q35_DEV float conv4_silu(float xin, const float* st, const float* w) {
   return silu_f(acc);
 }
 
-template <int CS>
+// One channel's conv inputs in registers (loaded ahead of any use), and the same conv + SiLU.
+struct ConvIn {
+  float x, s[3], w[4];
+};
+template <bool QF>
+Q35_DEV ConvIn conv_in(const GdnCall& a, const float* cs, int b, int c) {
+  ConvIn r;
+  r.x = qkv_at<QF>(a, b, c);
+  const float* st = cs + (size_t)c * 3;
+  const float* w = a.conv_w + (size_t)c * 4;
+  r.s[0] = st[0]; r.s[1] = st[1]; r.s[2] = st[2];
+  r.w[0] = w[0]; r.w[1] = w[1]; r.w[2] = w[2]; r.w[3] = w[3];
+  return r;
+}
+Q35_DEV float conv4_silu(const ConvIn& r) { return conv4_silu(r.x, r.s, r.w); }
+
+// BF: the gates arrive as raw fixed-point projections (else activated f32 [beta | g]).
+template <int CS, bool QF, bool BF>
 __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   constexpr int VW = CS / 32;  // value columns per thread (4: one float4)
   const GdnCall& a = A.c;
@@ -75,14 +96,29 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
     }
   }
 
-  {  // q (tid < 128) and k (tid >= 128) channels of head h
-    const int c = (tid < kDk) ? h * kDk + tid : A.key_dim + h * kDk + (tid - kDk);
-    qk[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
+  // the gate inputs too (independent of everything above: one round trip for all; kept raw
+  // until used, so that no wait for them sits before the conv loads)
+  fx_t g_bx = 0, g_ax = 0;
+  float g_b = 0.f, g_a = 0.f, g_dt = 0.f, g_al = 0.f;
+  if constexpr (BF) {
+    g_bx = a.ba_f[(size_t)b * a.ld_bg + h];
+    g_ax = a.ba_f[(size_t)b * a.ld_bg + a.nh + h];
+    g_dt = a.dt_bias[h];
+    g_al = a.a_log[h];
+  } else {
+    g_b = a.bg[(size_t)b * a.ld_bg + h];
+    g_a = a.bg[(size_t)b * a.ld_bg + a.nh + h];
   }
-  if (tid < CS) {
-    const int c = 2 * A.key_dim + h * a.dv + slice * CS + tid;
-    vv[tid] = conv4_silu(qkv_at(a, b, c), cs + (size_t)c * 3, a.conv_w + (size_t)c * 4);
-  }
+
+  // the conv inputs of the thread's q (tid < 128) or k channel of head h and of the slice's v
+  // channel (clamped: every thread loads, the first CS use it), all issued before any is used,
+  // so the state slice, the gates and the conv inputs take one round trip; no divergent branch
+  // around a load (its join would wait for every load in flight)
+  const ConvIn in_qk = conv_in<QF>(a, cs, b, (tid < kDk) ? h * kDk + tid : A.key_dim + h * kDk + (tid - kDk));
+  const ConvIn in_v = conv_in<QF>(a, cs, b, 2 * A.key_dim + h * a.dv + slice * CS + min(tid, CS - 1));
+  __builtin_amdgcn_sched_barrier(0);  // (the scheduler would interleave the conv math and its waits)
+  qk[tid] = conv4_silu(in_qk);
+  if (tid < CS) vv[tid] = conv4_silu(in_v);
   __syncthreads();
   {
     const float v = qk[tid];
@@ -96,16 +132,14 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
   else kh[tid - kDk] = qk[tid] * rk;
 
   float beta, g;
-  if (a.ba_f) {  // raw projections: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias)
-    const float bs = from_fx(a.ba_f[(size_t)b * a.ld_bg + h]);
-    const float as = from_fx(a.ba_f[(size_t)b * a.ld_bg + a.nh + h]);
-    beta = sigmoid_f(bs);
-    const float xg = as + a.dt_bias[h];
+  if constexpr (BF) {  // raw projections: beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias)
+    beta = sigmoid_f(from_fx(g_bx));
+    const float xg = from_fx(g_ax) + g_dt;
     const float pre = logf(expf(xg) + 1.0f);
-    g = -expf(a.a_log[h]) * (pre > 20.0f ? xg : pre);
+    g = -expf(g_al) * (pre > 20.0f ? xg : pre);
   } else {
-    beta = a.bg[(size_t)b * a.ld_bg + h];
-    g = a.bg[(size_t)b * a.ld_bg + a.nh + h];
+    beta = g_b;
+    g = g_a;
   }
   const float decay = expf(g);
   __syncthreads();
@@ -158,16 +192,18 @@ __global__ __launch_bounds__(kThreads) void gdn_step_kernel(const GdnArgs A) {
     a.o[(size_t)b * a.ld_o + h * a.dv + slice * CS + tid] = o;
   }
   if (!a.head_ctr) return;
-  // the last slice of (b, h) to get here advances the head's conv state: [s1, s2, x]
-  if (!arrive_last(&a.head_ctr[b * a.nh + h], (uint32_t)A.nslice, &last_flag)) return;
+  // conv state advance, [s0, s1, s2] <- [s1, s2, x], from the registers loaded above: each slice
+  // owns its CS v channels and advances them now; the q/k channels are read by every slice of
+  // (b, h), so the last slice to get here advances them
   float* cw = a.conv_state + (size_t)b * A.conv_dim * 3;
-  for (int e = tid; e < 2 * kDk + a.dv; e += kThreads) {
-    const int c = e < kDk ? h * kDk + e : (e < 2 * kDk ? A.key_dim + h * kDk + (e - kDk) : 2 * A.key_dim + h * a.dv + (e - 2 * kDk));
-    float* st = cw + (size_t)c * 3;
-    const float s1 = st[1], s2 = st[2];
-    st[0] = s1;
-    st[1] = s2;
-    st[2] = qkv_at(a, b, c);
+  if (tid < CS) {
+    float* st = cw + (size_t)(2 * A.key_dim + h * a.dv + slice * CS + tid) * 3;
+    st[0] = in_v.s[1]; st[1] = in_v.s[2]; st[2] = in_v.x;
+  }
+  if (!arrive_last(&a.head_ctr[b * a.nh + h], (uint32_t)A.nslice, &last_flag)) return;
+  {
+    float* st = cw + (size_t)((tid < kDk) ? h * kDk + tid : A.key_dim + h * kDk + (tid - kDk)) * 3;
+    st[0] = in_qk.s[1]; st[1] = in_qk.s[2]; st[2] = in_qk.x;
   }
 }
 
@@ -245,8 +281,15 @@ int gdn_step_launch(const GdnCall& c, hipStream_t st) {
                     (reinterpret_cast<uintptr_t>(c.S) & 15) == 0 && (c.dv % 4) == 0;
   a.nslice = c.dv / (wide ? 128 : 32);
   const int grid = c.B * c.nh * a.nslice;
-  if (wide) hipLaunchKernelGGL(gdn_step_kernel<128>, dim3(grid), dim3(kThreads), 0, st, a);
-  else hipLaunchKernelGGL(gdn_step_kernel<32>, dim3(grid), dim3(kThreads), 0, st, a);
+  const void* k;
+  if (c.qkv_f)
+    k = c.ba_f ? (wide ? (const void*)gdn_step_kernel<128, true, true> : (const void*)gdn_step_kernel<32, true, true>)
+               : (wide ? (const void*)gdn_step_kernel<128, true, false> : (const void*)gdn_step_kernel<32, true, false>);
+  else
+    k = c.ba_f ? (wide ? (const void*)gdn_step_kernel<128, false, true> : (const void*)gdn_step_kernel<32, false, true>)
+               : (wide ? (const void*)gdn_step_kernel<128, false, false> : (const void*)gdn_step_kernel<32, false, false>);
+  void* params[] = {&a};
+  Q35_HIP_TRY(hipLaunchKernel(k, dim3(grid), dim3(kThreads), params, 0, st));
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }
