@@ -200,7 +200,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
   }
   // final RMSNorm and the tied lm_head (model.rs:113-129) for every row
   for (int r0 = 0; r0 < B; r0 += kRowGroup)
-    if ((rc = mb_lm_head_launch(m->embed.q, m->embed_scale_t, d.vocab, H, bt->h + (size_t)r0 * H, H, m->final_norm, d.eps,
+    if ((rc = mb_lm_head_launch(m->embed_lm, m->embed_scale_t, d.vocab, H, bt->h + (size_t)r0 * H, H, m->final_norm, d.eps,
                                 std::min(kRowGroup, B - r0), bt->split16, bt->invf, bt->logits + (size_t)r0 * d.vocab,
                                 d.vocab, st)))
       return rc;
@@ -282,12 +282,16 @@ int ensure_mb(q35_model* m, hipStream_t st) {
       return rc;
   }
   float* sT = nullptr;
+  int8_t* lm = nullptr;
   if ((rc = dev_alloc_t(m, "mb.embed_scale_t", (size_t)m->d.vocab * (m->d.hidden / 64), &sT)) ||
-      (rc = mb_scale_transpose_launch(m->embed.s, m->d.vocab, m->d.hidden, sT, st)))
+      (rc = mb_scale_transpose_launch(m->embed.s, m->d.vocab, m->d.hidden, sT, st)) ||
+      (rc = dev_alloc_t(m, "mb.embed_lm", mb_lm_table_bytes(m->d.vocab, m->d.hidden), &lm)) ||
+      (rc = mb_lm_table_launch(m->embed.q, m->d.vocab, m->d.hidden, lm, st)))
     return rc;
   Q35_HIP_TRY(hipStreamSynchronize(st));
   m->mb = std::move(mb);
   m->embed_scale_t = sT;
+  m->embed_lm = lm;
   return Q35_OK;
 }
 

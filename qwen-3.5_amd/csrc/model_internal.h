@@ -72,6 +72,7 @@ struct q35_model {
   struct MbLayer { Mb qkv, z, out, q, k, v, o, gate, up, down, gu; };
   std::vector<MbLayer> mb;
   const float* embed_scale_t = nullptr;  // the embedding table's scales transposed [hidden/64][vocab]
+  const int8_t* embed_lm = nullptr;      // the embedding table in the batched lm_head's load order
 };
 
 namespace q35 {

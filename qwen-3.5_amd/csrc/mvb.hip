@@ -30,11 +30,14 @@
 // projections add into the f32 residual rows and accumulate each row's sum of squares for the
 // next RMSNorm (fixed point, so the sum is order-independent).
 //
-// The lm_head (mbn_kernel) reads the tied [V][D] table directly: lane l = 16 g + c takes 16
-// consecutive bytes of vocab row c of a tile (k = 16 g .. 16 g + 15 of a 64-wide scale block),
-// its A operands for two MFMAs; the block scale depends on the output row there, so each 64-k
-// block is accumulated separately and added with the rows' scales (read from a transposed copy of
-// the scale table).  Its input rows arrive already normalised and split (rms_rows_split_kernel).
+// The lm_head (mbn_kernel) reads a copy of the tied [V][D] table in its load order (built once,
+// mb_lm_table_launch): lane l = 16 g + c takes 16 consecutive bytes of vocab row c of a tile
+// (k = 16 g .. 16 g + 15 of a 64-wide scale block), its A operands for two MFMAs, and the copy
+// puts the 64 lanes' bytes of one load instruction side by side, so each instruction reads 1 KB
+// contiguous (from the table itself it would touch 16 rows, 64 bytes each).  The block scale
+// depends on the output row there, so each 64-k block is accumulated separately and added with
+// the rows' scales (read from a transposed copy of the scale table).  Its input rows arrive
+// already normalised and split (rms_rows_split_kernel).
 #include "q35_internal.h"
 
 #include <algorithm>
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
 
 // ------------------------------------------------------------------ lm_head over the NK table
 struct MbnArgs {
-  const int8_t* q;   // [V][K]
+  const int8_t* q;   // the table in load order (mb_lm_table_launch)
   const float* sT;   // scales transposed, [K/64][V]
   int32_t V, K, M;
   const _Float16* xh; const _Float16* xl; int32_t ld16;  // split rows [M][ld16] (hi, lo)
@@ -625,10 +628,9 @@ __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
     const _Float16* src = (pl ? a.xl : a.xh) + (size_t)min(m, a.M - 1) * a.ld16 + k + 8 * lane;
     dma16(src, &xs[pl][m * kNLd + k]);
   }
-  // lane's rows n = nbase + 16 nt + c (clamped for the loads; not stored past V)
-  const int8_t* rowp[4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) rowp[nt] = a.q + (size_t)min(nbase + 16 * nt + c, a.V - 1) * a.K + 16 * g;
+  // lane's rows n = nbase + 16 nt + c (not stored past V); the wave's 64-row tile in the copy
+  // (clamped: a block's waves past the table read its last tile)
+  const int8_t* tile = a.q + (size_t)min(nbase / 64, (a.V + 63) / 64 - 1) * 64 * a.K;
   // the output rows' scales: rows nbase + 16 nt + 4 g .. + 3 of block kb (clamped)
   const int srow = nbase + 4 * g;
   // (rounds past K load the first round again: every round issues the same loads, so the
@@ -641,7 +643,7 @@ __global__ __launch_bounds__(kT, 1) void mbn_kernel(const MbnArgs a) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
-        wv[kb][nt] = ldg16v_nt(rowp[nt] + rr * kRound + 64 * kb);
+        wv[kb][nt] = ldg16v_nt(tile + (size_t)rr * (64 * kRound) + (kb * 4 + nt) * 1024 + 16 * lane);
         sv[kb][nt] = ld4(a.sT + (size_t)(2 * rr + kb) * a.V + min(srow + 16 * nt, a.V - 4));
       }
   };
@@ -783,6 +785,22 @@ __global__ void mb_convert_kernel(const int8_t* qt, const float* st, int K, int 
     const int cb = (int)(i / K), k = (int)(i % K);
     sb[i] = tiled ? st[((size_t)(cb >> 2) * K + k) * 4 + (cb & 3)] : st[(size_t)k * (N / 64) + cb];
   }
+}
+
+// The lm_head's table in load order: 16-byte chunk i = ((t * K/128 + r) * 8 + 4 kb + nt) * 64 + l
+// holds row 64 t + 16 nt + (l & 15) (the last tile's rows past V repeat row V - 1), bytes
+// k = 128 r + 64 kb + 16 (l >> 4) .. + 15.
+__global__ void lm_table_kernel(const int8_t* q, int V, int K, int8_t* p, size_t nchunk) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nchunk) return;
+  const int l = (int)(i & 63), q8 = (int)((i >> 6) & 7);
+  const size_t rest = i >> 9;
+  const int nr = K / kRound, r = (int)(rest % nr);
+  const size_t t = rest / nr;
+  const int kb = q8 >> 2, nt = q8 & 3;
+  const int row = (int)min((size_t)V - 1, 64 * t + 16 * nt + (l & 15));
+  const int k = kRound * r + 64 * kb + 16 * (l >> 4);
+  *(uint4*)(p + i * 16) = *(const uint4*)(q + (size_t)row * K + k);
 }
 
 // sT[kb][n] = s[n][kb] (the lm_head scales by 64-k block)
@@ -1013,6 +1031,19 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, true>), grid, dim3(kT), 0, st, a);
     else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, false>), grid, dim3(kT), 0, st, a);
   }
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
+
+size_t mb_lm_table_bytes(int32_t V, int32_t K) { return (size_t)((V + 63) / 64) * 64 * (size_t)K; }
+
+int mb_lm_table_launch(const int8_t* q, int32_t V, int32_t K, int8_t* p, hipStream_t st) {
+  if (!q || !p) return fail(Q35_E_ARG, "mb_lm_table: null pointer");
+  if (K < kRound || K % kRound || V < 1) return fail(Q35_E_SHAPE, "mb_lm_table: K must be a multiple of 128");
+  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(p) & 15))
+    return fail(Q35_E_ALIGN, "mb_lm_table: 16-byte aligned tables");
+  const size_t nchunk = mb_lm_table_bytes(V, K) / 16;
+  hipLaunchKernelGGL(lm_table_kernel, dim3((unsigned)((nchunk + 255) / 256)), dim3(256), 0, st, q, V, K, p, nchunk);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -623,9 +623,13 @@ int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float*
 // -> MB layout.
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
                       hipStream_t st, int tiled = 1);
-// logits[m][n] = RMSNorm(h[m]) . dequant(E[n]) over the tied NK table (scales transposed,
-// sT[K/64][V]), M <= 32 rows, K a multiple of 512 up to 2048; split16 holds 2 * M * K halves and
-// invf M floats of scratch.
+// The lm_head's copy of the tied NK table q[V][K] in its load order (mb_lm_table_bytes bytes; K a
+// multiple of 128).
+size_t mb_lm_table_bytes(int32_t V, int32_t K);
+int mb_lm_table_launch(const int8_t* q, int32_t V, int32_t K, int8_t* p, hipStream_t st);
+// logits[m][n] = RMSNorm(h[m]) . dequant(E[n]) over the tied NK table (q: its copy in load order,
+// mb_lm_table_launch; scales transposed, sT[K/64][V]), M <= 32 rows, K a multiple of 512 up to
+// 2048; split16 holds 2 * M * K halves and invf M floats of scratch.
 int mb_lm_head_launch(const int8_t* q, const float* sT, int32_t V, int32_t K, const float* h, int32_t ldh,
                       const float* norm_w, float eps, int32_t M, _Float16* split16, float* invf, float* y, int32_t ldy,
                       hipStream_t st);
