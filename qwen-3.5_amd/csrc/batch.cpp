@@ -114,6 +114,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
     c.part = bt->part; c.part_floats = bt->part_floats; c.ctr = bt->mb_ctr; c.nctr = kMbCounters;
     c.words = bt->words; c.word_floats = bt->word_floats;
     c.err = ws_counters(bt->ws) + kWsErrWord;
+    c.stream_order = true;  // the .qs copies
   };
   for (int l = 0; l < NL; ++l) {
     const q35_model::Layer& L = m->layers[l];
@@ -129,14 +130,14 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       float* pr = bt->proj + (size_t)r0 * ldq;
       if (!L.full) {
         c.nseg = 2;
-        c.seg[0] = MbSeg{W.qkv.q, W.qkv.s, pr, conv_dim, ldq, W.qkv.f};
-        c.seg[1] = MbSeg{W.z.q, W.z.s, pr + conv_dim, vdim, ldq, W.z.f};
+        c.seg[0] = MbSeg{W.qkv.qs, W.qkv.s, pr, conv_dim, ldq, W.qkv.f};
+        c.seg[1] = MbSeg{W.z.qs, W.z.s, pr + conv_dim, vdim, ldq, W.z.f};
         c.aux_wb = L.w_b; c.aux_wa = L.w_a; c.aux_nh = nh; c.aux_acc = gates + (size_t)r0 * kGateLd; c.aux_ldo = kGateLd;
       } else {
         c.nseg = 3;
-        c.seg[0] = MbSeg{W.q.q, W.q.s, pr, ldqg, ldq, W.q.f};
-        c.seg[1] = MbSeg{W.k.q, W.k.s, pr + ldqg, kvw, ldq, W.k.f};
-        c.seg[2] = MbSeg{W.v.q, W.v.s, pr + ldqg + kvw, kvw, ldq, W.v.f};
+        c.seg[0] = MbSeg{W.q.qs, W.q.s, pr, ldqg, ldq, W.q.f};
+        c.seg[1] = MbSeg{W.k.qs, W.k.s, pr + ldqg, kvw, ldq, W.k.f};
+        c.seg[2] = MbSeg{W.v.qs, W.v.s, pr + ldqg + kvw, kvw, ldq, W.v.f};
       }
       if ((rc = mb_launch(c, st))) return rc;
     }
@@ -151,7 +152,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
         base(c, std::min(kRowGroup, B - r0));
         c.K = vdim; c.x = bt->o_raw + (size_t)r0 * vdim; c.ldx = vdim; c.pro = MB_PRO_GATED;
         c.z = bt->proj + (size_t)r0 * ldq + conv_dim; c.ldz = ldq; c.group = dv; c.pw = L.norm_w;
-        c.nseg = 1; c.seg[0] = MbSeg{W.out.q, W.out.s, bt->h + (size_t)r0 * H, H, H};
+        c.nseg = 1; c.seg[0] = MbSeg{W.out.qs, W.out.s, bt->h + (size_t)r0 * H, H, H};
         c.add = 1; c.ss_out = ss_mid + r0;
         if ((rc = mb_launch(c, st))) return rc;
       }
@@ -167,7 +168,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
         MbCall c;
         base(c, std::min(kRowGroup, B - r0));
         c.K = ah * hd; c.x = bt->attn + (size_t)r0 * ah * hd; c.ldx = ah * hd; c.pro = MB_PRO_PLAIN;
-        c.nseg = 1; c.seg[0] = MbSeg{W.o.q, W.o.s, bt->h + (size_t)r0 * H, H, H};
+        c.nseg = 1; c.seg[0] = MbSeg{W.o.qs, W.o.s, bt->h + (size_t)r0 * H, H, H};
         c.add = 1; c.ss_out = ss_mid + r0;
         if ((rc = mb_launch(c, st))) return rc;
       }
@@ -178,8 +179,8 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
       c.K = H; c.x = bt->h + (size_t)r0 * H; c.ldx = H; c.pro = MB_PRO_RMS; c.pw = L.post_norm; c.ss = ss_mid + r0;
       float* gu = bt->gu + (size_t)r0 * 2 * F;
       c.nseg = 2;
-      c.seg[0] = MbSeg{W.gate.q, W.gate.s, gu, F, 2 * F, W.gate.f};
-      c.seg[1] = MbSeg{W.up.q, W.up.s, gu + F, F, 2 * F, W.up.f};
+      c.seg[0] = MbSeg{W.gate.qs, W.gate.s, gu, F, 2 * F, W.gate.f};
+      c.seg[1] = MbSeg{W.up.qs, W.up.s, gu + F, F, 2 * F, W.up.f};
       // with two K splits the down projection sums the two partial copies itself (no hand-off)
       c.defer_stride = (int64_t)B * 2 * F;
       c.deferred_out = &gu_two[r0 / kRowGroup];
@@ -193,7 +194,7 @@ int batch_step_launch(q35_batch* bt, hipStream_t st) {
         c.xsum = 2;
         c.xsstride = (int64_t)B * 2 * F;
       }
-      c.nseg = 1; c.seg[0] = MbSeg{W.down.q, W.down.s, bt->h + (size_t)r0 * H, H, H};
+      c.nseg = 1; c.seg[0] = MbSeg{W.down.qs, W.down.s, bt->h + (size_t)r0 * H, H, H};
       c.add = 1; c.ss_out = ss_next + r0;
       if ((rc = mb_launch(c, st))) return rc;
     }
@@ -295,6 +296,32 @@ int ensure_mb(q35_model* m, hipStream_t st) {
   return Q35_OK;
 }
 
+// The batched decode's copies of the projection weights in stream order (the prompt GEMMs keep
+// reading the MB order): the bytes only; scales and split factors are shared with the MB copies.
+int ensure_mb_stream(q35_model* m, hipStream_t st) {
+  int rc;
+  if ((rc = ensure_mb(m, st))) return rc;
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const q35_model::Layer& L = m->layers[l];
+    q35_model::MbLayer& o = m->mb[l];
+    const std::string p = "mb.layers." + std::to_string(l) + ".";
+    const std::pair<const q35_model::Q8*, q35_model::Mb*> ws[] = {
+        {&L.qkv, &o.qkv}, {&L.z, &o.z}, {&L.out, &o.out}, {&L.q, &o.q}, {&L.k, &o.k},
+        {&L.v, &o.v}, {&L.o, &o.o}, {&L.gate, &o.gate}, {&L.up, &o.up}, {&L.down, &o.down}};
+    for (int i = 0; i < 10; ++i) {
+      q35_model::Mb& mw = *ws[i].second;
+      if (!mw.q || mw.qs) continue;
+      const size_t nb = (size_t)ws[i].first->rows * ws[i].first->cols;
+      int8_t* qs = nullptr;
+      if ((rc = dev_alloc_t(m, p + std::to_string(i) + ".stream", nb, &qs)) || (rc = mb_stream_launch(mw.q, nb, qs, st)))
+        return rc;
+      mw.qs = qs;
+    }
+  }
+  Q35_HIP_TRY(hipStreamSynchronize(st));
+  return Q35_OK;
+}
+
 namespace {
 
 // The prompt-path view of row r's state.
@@ -362,7 +389,7 @@ int q35_batch_create(q35_model* m, int32_t B, int32_t tmax, q35_batch** out) {
                                   "the DeltaNet value width and the attention width multiples of 128, value heads of <= "
                                   "128 and <= 16 DeltaNet heads"));
   int rc;
-  if ((rc = ensure_mb(m, b->own_stream))) return bail(rc);
+  if ((rc = ensure_mb_stream(m, b->own_stream))) return bail(rc);
   for (int l = 0; l < d.n_layers; ++l) {
     const std::string p = "layers." + std::to_string(l) + ".";
     float *cs = nullptr, *rs = nullptr, *k = nullptr, *v = nullptr;

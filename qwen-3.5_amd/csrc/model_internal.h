@@ -63,6 +63,7 @@ struct q35_model {
   // matrix-core batch kernels (q[N/64][K/16][64][16], scale[N/64][K])
   struct Mb {
     const int8_t* q = nullptr;
+    const int8_t* qs = nullptr;   // the same bytes in stream order (batched decode; mb_stream_launch)
     const float* s = nullptr;
     const float* f = nullptr;     // batched RMS launches: split factor per column block
     const float* smax = nullptr;  // max |scale| (prompt GEMMs)

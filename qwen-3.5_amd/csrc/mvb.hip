@@ -15,7 +15,10 @@
 // 32-row step ks, 2 KB in which lane l = 16 g + c of a wave finds, as two 16-byte loads, the bytes
 // u = q + 128 of q[32 ks + 8 g + j][64 cb + 16 nt + c] (j = 0..7) for each of the 4 column tiles
 // nt: exactly its A operands (row c of tile nt, k slot g) of one MFMA, with the k order permuted
-// inside the step (the sum is unchanged).  u converts to f16 as the bit pattern 0x6400 | u
+// inside the step (the sum is unchanged).  The batched decode reads a copy in stream order
+// (mb_stream_launch): lane l's two 16-byte loads at 16 l and 1024 + 16 l instead of 32 l and
+// 32 l + 16, so each load instruction reads 1 KB contiguous rather than half of each of 16 lines
+// (the prompt GEMMs, which re-read every weight from L2, run faster on the MB order).  u converts to f16 as the bit pattern 0x6400 | u
 // (= 1024 + u) minus 1152.  Scales are stored per column block, scale[cb][K].
 //
 // Block = 4 waves = one column block (64 outputs) x the block's K range (at most 1024 / MT rows).
@@ -301,7 +304,10 @@ Q35_DEV void mbk_aux(const MbkArgs& a, int ab, char* xbuf, float* red) {
 // |x * r| <= sqrt(K) for an RMS-normalised row, so sqrt(K) * max|1 + w| * max|s| bounds every |y|
 // of the block and f puts that bound in [2^13, 2^14)).  The bound is loose for most rows, which
 // costs nothing: hi / lo keep about 22 bits of each y down to 2^-17 of the bound.
-template <int MT, bool DIRECT, int XS = 1, int SR = 16 * MT>
+// SO: the weights are in stream order (lane l's bytes at 16 l and 1024 + 16 l of each 2 KB record;
+// else the MB order's 32 l and 32 l + 16).  A compile-time choice, so both loads keep immediate
+// offsets from one address.
+template <int MT, bool DIRECT, int XS = 1, int SR = 16 * MT, bool SO = false>
 __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   using X = XBuf<MT, SR>;
   constexpr int Mp = X::Mp;
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   const int nround = klen / kRound;
   const int nks = a.K >> 5;
   // wave p's 32-row step in round r: 4 r + p, relative to k0
-  const int8_t* wq = sg.q + ((size_t)lcb * nks + (k0 >> 5) + p) * 2048 + lane * 32;
+  const int8_t* wq = sg.q + ((size_t)lcb * nks + (k0 >> 5) + p) * 2048 + lane * (SO ? 16 : 32);
 
   // Rounds past the block's range load 32 bytes per lane of its (cached) scale row instead (inside
   // the row: K >= 128), so every round issues the same loads and the compiler's waits count them
@@ -342,9 +348,10 @@ __global__ __launch_bounds__(kT, 2) void mbk_kernel(const MbkArgs a) {
   float rrow[MT];
   const int kl0 = k0 + 32 * p + 8 * g;  // the lane's first k (round 0)
   auto load_round = [&](int r, int d) {
-    const int8_t* src = r < nround ? wq + (size_t)r * 4 * 2048 : dummy;
+    const bool in = r < nround;
+    const int8_t* src = in ? wq + (size_t)r * 4 * 2048 : dummy;
     wr[d][0] = ldg16v_nt(src);
-    wr[d][1] = ldg16v_nt(src + 16);
+    wr[d][1] = ldg16v_nt(src + (in ? (SO ? 1024 : 16) : 16));
     if constexpr (DIRECT) {  // rounds past the range reload the last one (cached)
       const int kk = kl0 + min(r, nround - 1) * kRound;
       sr[d][0] = ld4(scl + kk);
@@ -803,6 +810,16 @@ __global__ void lm_table_kernel(const int8_t* q, int V, int K, int8_t* p, size_t
   *(uint4*)(p + i * 16) = *(const uint4*)(q + (size_t)row * K + k);
 }
 
+// MB order -> stream order: 16-byte chunk (record b, lane l, half h) from b * 2048 + 32 l + 16 h
+// to b * 2048 + 1024 h + 16 l.
+__global__ void mb_stream_kernel(const int8_t* in, int8_t* out, size_t nchunk) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nchunk) return;
+  const size_t b = i >> 7;
+  const int l = (int)(i & 63), h = (int)((i >> 6) & 1);
+  *(uint4*)(out + b * 2048 + 1024 * h + 16 * l) = *(const uint4*)(in + b * 2048 + 32 * l + 16 * h);
+}
+
 // sT[kb][n] = s[n][kb] (the lm_head scales by 64-k block)
 __global__ void scale_transpose_kernel(const float* s, int V, int nkb, float* sT) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -813,6 +830,17 @@ __global__ void scale_transpose_kernel(const float* s, int V, int nkb, float* sT
 }
 
 }  // namespace
+
+int mb_stream_launch(const int8_t* q_mb, size_t nbytes, int8_t* q_stream, hipStream_t st) {
+  if (!q_mb || !q_stream) return fail(Q35_E_ARG, "mb_stream: null pointer");
+  if (nbytes % 2048) return fail(Q35_E_SHAPE, "mb_stream: the MB copy is whole 2 KB records");
+  if ((reinterpret_cast<uintptr_t>(q_mb) & 15) || (reinterpret_cast<uintptr_t>(q_stream) & 15))
+    return fail(Q35_E_ALIGN, "mb_stream: 16-byte aligned copies");
+  const size_t nchunk = nbytes / 16;
+  hipLaunchKernelGGL(mb_stream_kernel, dim3((unsigned)((nchunk + 255) / 256)), dim3(256), 0, st, q_mb, q_stream, nchunk);
+  Q35_HIP_TRY(hipGetLastError());
+  return Q35_OK;
+}
 
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
                       hipStream_t st, int tiled) {
@@ -949,6 +977,24 @@ size_t mb_part_floats(int ncb, int K, int M) {
 
 size_t mb_word_floats(int ncb, int M) { return (size_t)ncb * 64 * M * 2; }
 
+namespace {
+// staged prologues of up to 8 rows stage 8 (XBuf)
+template <bool SO>
+void mbk_dispatch(const MbkArgs& a, int M, int xs, bool direct, dim3 grid, hipStream_t st) {
+  if (xs == 2) {  // (staged SwiGLU prologue, <= 16 rows)
+    if (M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2, 8, SO>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2, 16, SO>), grid, dim3(kT), 0, st, a);
+  } else if (M <= 16) {
+    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, true, 1, 16, SO>), grid, dim3(kT), 0, st, a);
+    else if (M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 1, 8, SO>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 1, 16, SO>), grid, dim3(kT), 0, st, a);
+  } else {
+    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, true, 1, 32, SO>), grid, dim3(kT), 0, st, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, false, 1, 32, SO>), grid, dim3(kT), 0, st, a);
+  }
+}
+}  // namespace
+
 int mb_launch(const MbCall& c, hipStream_t st) {
   if (c.nseg < 1 || c.nseg > kMbMaxSeg) return fail(Q35_E_ARG, "mb_launch: 1..4 segments");
   if (c.M < 1 || c.M > 32) return fail(Q35_E_SHAPE, "mb_launch: M in [1, 32]");
@@ -1019,18 +1065,8 @@ int mb_launch(const MbCall& c, hipStream_t st) {
     a.words = reinterpret_cast<uint64_t*>(c.words);
   }
   const dim3 grid((unsigned)(ncb * a.nsplit + a.naux));
-  // staged prologues of up to 8 rows stage 8 (XBuf)
-  if (xs == 2) {  // (staged SwiGLU prologue, <= 16 rows)
-    if (c.M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2, 8>), grid, dim3(kT), 0, st, a);
-    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 2>), grid, dim3(kT), 0, st, a);
-  } else if (c.M <= 16) {
-    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, true>), grid, dim3(kT), 0, st, a);
-    else if (c.M <= 8) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false, 1, 8>), grid, dim3(kT), 0, st, a);
-    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<1, false>), grid, dim3(kT), 0, st, a);
-  } else {
-    if (direct) hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, true>), grid, dim3(kT), 0, st, a);
-    else hipLaunchKernelGGL(HIP_KERNEL_NAME(mbk_kernel<2, false>), grid, dim3(kT), 0, st, a);
-  }
+  if (c.stream_order) mbk_dispatch<true>(a, c.M, xs, direct, grid, st);
+  else mbk_dispatch<false>(a, c.M, xs, direct, grid, st);
   Q35_HIP_TRY(hipGetLastError());
   return Q35_OK;
 }

@@ -606,6 +606,8 @@ struct MbCall {
   int32_t xsum = 1; int64_t xsstride = 0;
   // the error word that receives kWsErrRange (required)
   uint32_t* err = nullptr;
+  // the weights are in stream order (mb_stream_launch) rather than the MB order
+  bool stream_order = false;
 };
 int mb_launch(const MbCall& c, hipStream_t st);
 // Partial-sum floats a launch over ncb column blocks needs (0 without split-K).
@@ -619,6 +621,11 @@ int mb_row_ss_launch(const float* x, int32_t ldx, int32_t K, int32_t M, fx_t* ss
 int mb_scale_max_launch(const float* s, int64_t n, float* out, hipStream_t st);
 // Split factors of an MB weight for RMS launches whose norm weights are norm_w.
 int mb_split_factor_launch(const float* s_mb, int32_t K, int32_t N, const float* norm_w, float* f, hipStream_t st);
+// MB weights in stream order: each 2 KB record (64 lanes x 32 bytes) as two 1 KB halves, lane l's
+// first 16 bytes at 16 l and its second at 1024 + 16 l, so that each wave load instruction of the
+// batched projections reads 1 KB contiguous (a pass that streams the weights once; the prompt
+// GEMMs, which re-read them, keep the MB order).  nbytes: the MB copy's size (K * N).
+int mb_stream_launch(const int8_t* q_mb, size_t nbytes, int8_t* q_stream, hipStream_t st);
 // Tile-major projection weights (q[t][K][256], scale[t][K][4]; or, tiled = 0, row-major KN)
 // -> MB layout.
 int mb_convert_launch(const int8_t* q_tiled, const float* s_tiled, int32_t K, int32_t N, int8_t* q_mb, float* s_mb,
