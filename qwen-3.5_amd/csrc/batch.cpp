@@ -305,17 +305,18 @@ int ensure_mb_stream(q35_model* m, hipStream_t st) {
     const q35_model::Layer& L = m->layers[l];
     q35_model::MbLayer& o = m->mb[l];
     const std::string p = "mb.layers." + std::to_string(l) + ".";
-    const std::pair<const q35_model::Q8*, q35_model::Mb*> ws[] = {
-        {&L.qkv, &o.qkv}, {&L.z, &o.z}, {&L.out, &o.out}, {&L.q, &o.q}, {&L.k, &o.k},
-        {&L.v, &o.v}, {&L.o, &o.o}, {&L.gate, &o.gate}, {&L.up, &o.up}, {&L.down, &o.down}};
-    for (int i = 0; i < 10; ++i) {
-      q35_model::Mb& mw = *ws[i].second;
-      if (!mw.q || mw.qs) continue;
-      const size_t nb = (size_t)ws[i].first->rows * ws[i].first->cols;
+    struct W { const q35_model::Q8* w; q35_model::Mb* mb; const char* name; };
+    const W ws[] = {{&L.qkv, &o.qkv, "in_proj_qkv"}, {&L.z, &o.z, "in_proj_z"}, {&L.out, &o.out, "out_proj"},
+                    {&L.q, &o.q, "q_proj"},         {&L.k, &o.k, "k_proj"},     {&L.v, &o.v, "v_proj"},
+                    {&L.o, &o.o, "o_proj"},         {&L.gate, &o.gate, "gate_proj"}, {&L.up, &o.up, "up_proj"},
+                    {&L.down, &o.down, "down_proj"}};
+    for (const W& x : ws) {  // named as the MB copy (mb.layers.<l>.<proj>) + ".stream"
+      if (!x.mb->q || x.mb->qs) continue;
+      const size_t nb = (size_t)x.w->rows * x.w->cols;
       int8_t* qs = nullptr;
-      if ((rc = dev_alloc_t(m, p + std::to_string(i) + ".stream", nb, &qs)) || (rc = mb_stream_launch(mw.q, nb, qs, st)))
+      if ((rc = dev_alloc_t(m, p + x.name + ".stream", nb, &qs)) || (rc = mb_stream_launch(x.mb->q, nb, qs, st)))
         return rc;
-      mw.qs = qs;
+      x.mb->qs = qs;
     }
   }
   Q35_HIP_TRY(hipStreamSynchronize(st));

@@ -115,3 +115,31 @@ def test_batch_2b_rows_match_single_sequence_decode():
         np.testing.assert_array_equal(toks[r], want, err_msg=f"row {r}")
     bt.close()
     m.close()
+
+
+def test_batch_weight_copies_match_their_layouts():
+    """The copies a batch decoder reads, bit for bit against their definitions: each projection's
+    stream-order copy is its MB copy with every 2 KB record's 64 lane records of 32 bytes split in
+    two 1 KB halves (lane l's bytes 0-15 at 16 l, bytes 16-31 at 1024 + 16 l); the lm_head's copy
+    of the tied [V][H] table is in load order (per 64-row tile t, 128-k round r and (kb, nt) pair,
+    lane l = 16 g + c holds row 64 t + 16 nt + c, k = 128 r + 64 kb + 16 g .. + 15; rows past V
+    repeat row V - 1: vocab 8100 leaves a partial last tile)."""
+    d = q35.make_dims(hidden=512, ffn=1536, vocab=8100, n_layers=4, lin_heads=4, attn_heads=4, kv_heads=2)
+    m = q35.TextForCausalLM(d, seed=5, tmax=64)
+    bt = q35.BatchDecoder(m, 2, 64)
+    try:
+        for l, proj in [(0, "in_proj_qkv"), (0, "in_proj_z"), (0, "out_proj"), (3, "q_proj"), (3, "o_proj"),
+                        (3, "down_proj")]:
+            name = f"mb.layers.{l}.{proj}"
+            mb = m.tensor(name, np.uint8).reshape(-1, 64, 2, 16)      # [record][lane][half][16]
+            st = m.tensor(name + ".stream", np.uint8).reshape(-1, 2, 64, 16)
+            np.testing.assert_array_equal(st, mb.transpose(0, 2, 1, 3), err_msg=name)
+        V, H = d.vocab, d.hidden
+        q = m.tensor("embed_tokens.q", np.int8).reshape(V, H)
+        nt = (V + 63) // 64
+        E = q[np.minimum(np.arange(nt * 64), V - 1)].reshape(nt, 4, 16, H // 128, 2, 4, 16)  # [t][nt][c][r][kb][g][b]
+        exp = E.transpose(0, 3, 4, 1, 5, 2, 6).reshape(-1)                                  # [t][r][kb][nt][g][c][b]
+        np.testing.assert_array_equal(m.tensor("mb.embed_lm", np.int8), exp)
+    finally:
+        bt.close()
+        m.close()
